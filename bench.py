@@ -1,0 +1,223 @@
+#!/usr/bin/env python3
+"""Decode throughput of RAMforge's hot path on one MI355X.
+
+Workload (BASELINE.json metric): random-init Llama-3-8B-shape model (32
+layers, d 4096, 32/8 heads, FFN 14336, vocab 128256), Q8_0 weights resident in
+HBM, greedy decode.  One step = one token: output norm + logits matvec,
+on-device argmax, embedding of the chosen token, 32 transformer layers.  The
+prompt (32 random token ids) is forwarded before the timed region.
+
+Prints one JSON line with the decode tok/s, the roofline of the dominant
+kernel (ffn RMSNorm + gate/up Q8_0 matvec + SiLU*up, timed with HIP events on
+the stream it runs on), the Q8_0 4096x4096 matvec HBM GB/s
+and the CPU baseline: the oracle restatement of the reference CPU path
+(reference threading policy: Q8_0 matvecs single-threaded) timed on this
+host on a bounded sample of the same workload.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_HBM_GBS = 8000.0
+METRIC = "decode tok/s (8B-shape Q8_0, 1 GPU); matvec achieved HBM GB/s vs peak"
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def cpu_model_name() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def matvec_q8_0_gbs(ctx, rf, syn, iters: int = 120):
+    """Q8_0 4096x4096 matvec; weights rotate through ~1 GiB
+    of distinct copies so the 256 MiB Infinity Cache cannot serve them."""
+    out_dim = in_dim = 4096
+    nblk = out_dim * in_dim // 32
+    wbytes = nblk * 34
+    copies = max(2, (1 << 30) // wbytes + 1)
+    ws = []
+    for i in range(copies):
+        w = ctx.empty((wbytes,), "uint8", charge=f"bench:q8_0_4096:{i}")
+        ctx.synth_blocks(syn.Q8_0, 1001, 0, nblk, 0.02 / 127, w)
+        ws.append(w)
+    import numpy as np
+
+    x = ctx.array(np.random.default_rng(1).normal(0, 1, in_dim).astype(np.float32), "bench:q8_0_4096:x")
+    y = ctx.empty((out_dim,), charge="bench:q8_0_4096:y")
+    for i in range(copies):
+        rf.matvec(ctx, syn.Q8_0, ws[i], (out_dim, in_dim), x, y)
+    ctx.synchronize()
+    e0, e1 = ctx.event(), ctx.event()
+    ctx.record(e0, ctx.compute_stream)
+    for i in range(iters):
+        rf.matvec(ctx, syn.Q8_0, ws[i % copies], (out_dim, in_dim), x, y, stream=ctx.compute_stream)
+    ctx.record(e1, ctx.compute_stream)
+    ms = ctx.elapsed_ms(e0, e1) / iters
+    alg = wbytes + 4 * in_dim + 4 * out_dim
+    for a in ws + [x, y]:
+        a.free()
+    return {"config": "Q8_0 4096x4096 y=Wx, weights rotated over %d copies (%.2f GiB)" % (copies,
+                                                                                      copies * wbytes / 2 ** 30),
+            "us_per_call": round(ms * 1e3, 3), "algorithmic_bytes": alg,
+            "achieved_GBs": round(alg / (ms * 1e-3) / 1e9, 1), "frac_of_peak": round(alg / (ms * 1e-3) / 1e9 /
+                                                                                      PEAK_HBM_GBS, 4)}
+
+
+def cpu_baseline(cfg, specs, tokens: int):
+    """Time the oracle (reference CPU path restated in C, reference threading
+    policy) on `tokens` decode steps of the same model at positions 0..tokens-1."""
+    import numpy as np
+
+    import oracle as orc
+
+    t0 = time.perf_counter()
+    T = orc.model_tensors(specs)
+    gen_s = time.perf_counter() - t0
+    m = orc.Model(cfg, T, kv_capacity=tokens + 1, threads=os.cpu_count() or 1, use_simd=True)
+    per = []
+    tok = 1
+    for pos in range(tokens):
+        t0 = time.perf_counter()
+        h = m.forward(tok, pos)
+        logits = m.logits(h)
+        tok = orc.argmax(logits)
+        per.append(time.perf_counter() - t0)
+        log(f"cpu token {pos}: {per[-1]:.2f} s")
+    m.close()
+    med = statistics.median(per)
+    return {"value": round(1.0 / med, 5), "unit": "tok/s", "cores": 1, "kind": "port",
+            "sample": (f"{tokens} decode steps of the same 8B-shape Q8_0 model at positions 0..{tokens - 1}, "
+                       f"median; oracle restatement of the reference CPU path (Q8_0 matvecs single-threaded "
+                       f"as in compute_dispatch.rs:219-254), host {cpu_model_name()}; weights generated in "
+                       f"{gen_s:.1f} s, untimed"),
+            "seconds_per_token": [round(p, 3) for p in per]}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=64)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--prompt", type=int, default=32)
+    ap.add_argument("--no-graph", action="store_true", help="eager launches instead of hipGraph replay")
+    ap.add_argument("--cpu-tokens", type=int, default=3)
+    ap.add_argument("--skip-cpu", action="store_true")
+    ap.add_argument("--kernel-reps", type=int, default=4)
+    ap.add_argument("--tile-bytes", type=int, default=0, help="matvec LDS tile bytes (tuning)")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures the decode hot path on ONE GPU only: this build has no multi-GPU path "
+              "(no collectives or sharding); run with --gpus 1.", file=sys.stderr)
+        return 2
+
+    import numpy as np
+
+    import ramforge_amd as rf
+    from ramforge_amd import synthetic as syn
+
+    if args.tile_bytes:
+        rf.tune_matvec_tile_bytes(args.tile_bytes)
+    cfg = syn.CONFIG_8B
+    specs = syn.llama_specs(cfg, syn.Q8_0, seed=8)
+    wbytes = syn.weight_bytes(specs)
+    cap = args.prompt + args.warmup + args.steps + 8
+    ctx = rf.Context(0)
+    name, cus = ctx.device_info()
+    log(f"device {name}, {cus} CUs; building 8B-shape Q8_0 model ({wbytes / 1e9:.2f} GB) in HBM")
+    m = syn.build_device_model(ctx, cfg, specs, cap)
+    prompt = [int(t) for t in np.random.default_rng(8).integers(0, cfg["vocab_size"], args.prompt)]
+    t0 = time.perf_counter()
+    for p, t in enumerate(prompt):
+        m.forward(t, p)
+    log(f"prompt of {args.prompt} tokens forwarded in {time.perf_counter() - t0:.3f} s")
+    m.use_graph(not args.no_graph)
+    m.decode_steps(args.warmup)
+    ctx.synchronize()
+
+    t0 = time.perf_counter()
+    m.decode_steps(args.steps)
+    ctx.synchronize()
+    wall = time.perf_counter() - t0
+    toks = m.read_tokens(args.steps)
+    tok_s = args.steps / wall
+    ms_step = wall * 1e3 / args.steps
+    log(f"decode: {args.steps} steps in {wall * 1e3:.1f} ms -> {tok_s:.1f} tok/s ({ms_step:.3f} ms/step)")
+
+    # live per-group kernel times (HIP events on the compute stream)
+    m.use_graph(False)
+    per_token_bytes = 0
+    breakdown = {}
+    for kind in ("qkv", "attention", "oproj", "gateup", "down", "logits"):
+        ms, b, n = m.time_kernel(kind, args.kernel_reps)
+        per_tok = 1 if kind == "logits" else cfg["block_count"]
+        breakdown[kind] = {"us_per_launch": round(ms * 1e3, 3), "launches_per_token": per_tok,
+                           "bytes_per_launch": b, "GBs": round(b / (ms * 1e-3) / 1e9, 1)}
+        per_token_bytes += b * per_tok
+    kernel_ms = sum(v["us_per_launch"] * v["launches_per_token"] for v in breakdown.values()) / 1e3
+    dom = max(breakdown, key=lambda k: breakdown[k]["us_per_launch"] * breakdown[k]["launches_per_token"])
+    d = breakdown[dom]
+    achieved = d["bytes_per_launch"] / (d["us_per_launch"] * 1e-6) / 1e9
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "gateup_q8_0_8b_traffic.json")
+    if dom == "gateup" and os.path.exists(tpath):
+        try:
+            traffic = json.load(open(tpath)).get("bytes_per_launch")
+        except (OSError, ValueError):
+            traffic = None
+    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": traffic,
+                "kernel": "matvec_tiled<Q8_0, EPI_SWIGLU> (ffn RMSNorm + gate/up + SiLU*up)" if dom == "gateup"
+                else dom}
+    log(f"dominant group {dom}: {d['us_per_launch']} us/launch, {achieved:.0f} GB/s "
+        f"({achieved / PEAK_HBM_GBS:.1%} of peak); kernel time per token {kernel_ms:.3f} ms")
+    mv = matvec_q8_0_gbs(ctx, rf, syn)
+    log(f"Q8_0 4096x4096 matvec: {mv['achieved_GBs']} GB/s")
+    m.close()
+    ctx.close()
+
+    cpu = None
+    if not args.skip_cpu:
+        log(f"CPU baseline: {args.cpu_tokens} tokens of the oracle restatement")
+        cpu = cpu_baseline(cfg, specs, args.cpu_tokens)
+
+    line = {
+        "metric": METRIC, "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms_step, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": "greedy decode, 1 token per step, llama 8B shape, Q8_0 weights resident in HBM",
+                   "layers": cfg["block_count"], "d_model": cfg["embedding_length"],
+                   "heads": [cfg["head_count"], cfg["head_count_kv"]], "ffn": cfg["feed_forward_length"],
+                   "vocab": cfg["vocab_size"], "prompt_tokens": args.prompt,
+                   "weights_bytes_per_token": wbytes, "hip_graph": not args.no_graph},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "roofline_tok_s_at_peak": round(PEAK_HBM_GBS * 1e9 / per_token_bytes, 1),
+        "kernel_ms_per_token": round(kernel_ms, 4),
+        "breakdown": breakdown,
+        "matvec_q8_0_4096x4096": mv,
+        "tokens_head": toks[:8],
+        "device": name,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,282 @@
+/*
+ * ramforge_hip.h — C ABI of the MI355X (gfx950) decode-step tier for RAMforge.
+ *
+ * The library replaces RAMforge's legacy CPU decode hot path: the GGUF block
+ * matvec and single-query GQA attention, the per-layer composition around them
+ * and the device-memory side of the layer-lifetime contract.  The signatures
+ * are plain C (pointers, sizes, status codes) so a Rust `extern "C"` block can
+ * bind them one-to-one.  Reference paths are relative to
+ * crates/ramforge-{core,runtime}/src of RAMforge.
+ *
+ * Conventions (mirroring the reference's Rust API):
+ *   - Every call returns int32_t: RF_OK (0) or an RF_ERR_* code.  The message
+ *     of the last failure on the calling thread is read with rf_last_error();
+ *     messages keep the reference's wording ("row truncated", "not divisible",
+ *     "arity mismatch", "exceeds out_dim", "insufficient memory", ...).
+ *   - Arguments are validated before anything is written or launched: on
+ *     error the outputs are untouched (quant.rs:1718-1730, 1788-1806).
+ *   - Tensors passed to compute calls are DEVICE pointers; shapes use the
+ *     reference's conventions (matvec kernels take out_dim/in_dim as quant.rs
+ *     does; the weight bytes are the raw GGUF payload, row-major [out][in]).
+ *   - `stream` is a hipStream_t; NULL selects the context's compute stream.
+ *     Compute calls are asynchronous with respect to the host.
+ *   - No compute call allocates device memory: the context owns grown
+ *     workspaces (created on the first call that needs them and kept).
+ */
+#ifndef RAMFORGE_HIP_H
+#define RAMFORGE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define RF_OK 0
+#define RF_ERR_INVALID 1     /* shape / argument error (reference: Err(String)) */
+#define RF_ERR_BUDGET 2      /* VRAM ledger refused a charge (MemoryError)     */
+#define RF_ERR_HIP 3         /* HIP runtime failure                            */
+#define RF_ERR_UNSUPPORTED 4 /* type or shape outside what the kernels cover   */
+
+/* ggml type ids: core/src/types.rs:238-292 (GgmlType::from_u32). */
+#define RF_TYPE_F32 0u
+#define RF_TYPE_F16 1u
+#define RF_TYPE_Q4_0 2u
+#define RF_TYPE_Q5_0 6u
+#define RF_TYPE_Q8_0 8u
+#define RF_TYPE_Q2_K 10u
+#define RF_TYPE_Q3_K 11u
+#define RF_TYPE_Q4_K 12u
+#define RF_TYPE_Q5_K 13u
+#define RF_TYPE_Q6_K 14u
+#define RF_TYPE_Q8_K 15u
+#define RF_TYPE_BF16 30u
+
+/* matvec row_count value meaning "all rows from row_start" (Rust `None`). */
+#define RF_ALL_ROWS UINT64_MAX
+
+typedef struct rf_ctx rf_ctx;
+typedef struct rf_model rf_model;
+typedef void *rf_stream_t; /* hipStream_t */
+
+/* ------------------------------------------------------------------ errors */
+
+/* Copies the calling thread's last error message (NUL-terminated, truncated
+ * to cap) and returns its full length. */
+size_t rf_last_error(char *buf, size_t cap);
+/* Library version string. */
+const char *rf_version(void);
+
+/* --------------------------------------------------------------- context */
+
+/* Creates a context on HIP device `device` with a device-memory ledger of
+ * `vram_budget_bytes` (0 = the device's total memory).  The ledger is the
+ * device-domain MemoryBudget (core/src/memory.rs:30-384) that the GPU
+ * residency tier charges; the context also owns one compute stream and one
+ * copy stream at default priority.  Replaces CpuBackend::new
+ * (runtime/src/backend.rs:72-84) as the compute backend handle. */
+int32_t rf_ctx_create(int32_t device, uint64_t vram_budget_bytes, rf_ctx **out);
+void rf_ctx_destroy(rf_ctx *ctx);
+int32_t rf_ctx_synchronize(rf_ctx *ctx);
+rf_stream_t rf_ctx_compute_stream(rf_ctx *ctx);
+rf_stream_t rf_ctx_copy_stream(rf_ctx *ctx);
+/* Device name and compute-unit count (for reports). */
+int32_t rf_ctx_device_info(rf_ctx *ctx, char *name, size_t cap, int32_t *compute_units);
+
+/* ------------------------------------------------- VRAM ledger + buffers */
+
+/* MemoryBudget::allocate (memory.rs:93-122) followed by hipMalloc: the charge
+ * is reserved before the allocation and rolled back if hipMalloc fails.
+ * Errors: zero size, duplicate name, insufficient budget. */
+int32_t rf_vram_alloc(rf_ctx *ctx, const char *charge, uint64_t bytes, void **out);
+/* hipFree of the buffer registered under `charge`, then MemoryBudget::release
+ * (memory.rs:133-152): the physical free precedes the logical release. */
+int32_t rf_vram_release(rf_ctx *ctx, const char *charge);
+/* memory.rs:286-325: renames every charge starting with old_prefix. */
+int32_t rf_vram_rename_prefix(rf_ctx *ctx, const char *old_prefix, const char *new_prefix);
+/* Charge size (RF_ERR_INVALID if absent), used / total / peak bytes. */
+int32_t rf_vram_charge(rf_ctx *ctx, const char *charge, uint64_t *bytes);
+uint64_t rf_vram_used(rf_ctx *ctx);
+uint64_t rf_vram_total(rf_ctx *ctx);
+uint64_t rf_vram_peak(rf_ctx *ctx);
+
+/* Pinned host staging buffers (hipHostMalloc). */
+int32_t rf_pinned_alloc(rf_ctx *ctx, uint64_t bytes, void **out);
+int32_t rf_pinned_free(rf_ctx *ctx, void *ptr);
+
+/* Copies.  rf_upload_async is hipMemcpyAsync host->device on `stream`
+ * (pinned sources overlap with compute when issued on the copy stream). */
+int32_t rf_upload_async(rf_ctx *ctx, void *dst, const void *src, uint64_t bytes, rf_stream_t stream);
+int32_t rf_upload(rf_ctx *ctx, void *dst, const void *src, uint64_t bytes);
+int32_t rf_download(rf_ctx *ctx, void *dst, const void *src, uint64_t bytes);
+int32_t rf_memset(rf_ctx *ctx, void *dst, int32_t value, uint64_t bytes);
+
+/* Events for stream ordering and timing. */
+int32_t rf_event_create(rf_ctx *ctx, void **event);
+int32_t rf_event_destroy(rf_ctx *ctx, void *event);
+int32_t rf_event_record(rf_ctx *ctx, void *event, rf_stream_t stream);
+int32_t rf_stream_wait_event(rf_ctx *ctx, rf_stream_t stream, void *event);
+int32_t rf_event_elapsed_ms(rf_ctx *ctx, void *start, void *stop, float *ms);
+int32_t rf_event_synchronize(rf_ctx *ctx, void *event);
+
+/* --------------------------------------------------------------- matvec */
+
+/* y = W x for one GGUF tensor, kernel shape [out_dim, in_dim].
+ * Replaces quant::matvec_<fmt> / matvec_<fmt>_row_range (core/src/quant.rs:
+ * 898-1489) and, for RF_TYPE_F32, CpuBackend::matvec (runtime/src/backend.rs:
+ * 173-218), i.e. everything compute_dispatch::matvec_backend routes to
+ * (runtime/src/compute_dispatch.rs:40-58).  Rows [row_start, row_start +
+ * row_count) are computed into the LOCAL y (y[0] <-> row_start,
+ * quant.rs:907-912); row_count = RF_ALL_ROWS means through out_dim.
+ * w_bytes is the size of the buffer behind w (validated like the
+ * reference's w_bytes.len()).  x has in_dim floats, y has row_count floats. */
+int32_t rf_matvec(rf_ctx *ctx, uint32_t ggml_type, const void *w, uint64_t w_bytes, uint64_t out_dim,
+                  uint64_t in_dim, const float *x, float *y, uint64_t row_start, uint64_t row_count,
+                  rf_stream_t stream);
+
+/* Bit-exact row decode: rows [row_start, row_start + row_count) of a
+ * [rows, in_dim] GGUF tensor into out[row_count][in_dim].  Replaces
+ * dequantize_row_<fmt> (quant.rs:615-868) and decode_row_to_f32
+ * (core/src/tensor.rs:801-866, incl. F32/F16/BF16). */
+int32_t rf_dequantize_rows(rf_ctx *ctx, uint32_t ggml_type, const void *w, uint64_t w_bytes,
+                           uint64_t in_dim, uint64_t row_start, uint64_t row_count, float *out,
+                           rf_stream_t stream);
+
+/* ------------------------------------------------------------ attention */
+
+/* Single-token causal GQA attention: out[q_heads][head_dim].  Replaces
+ * ops::attention_checked (runtime/src/ops.rs:49-69) ->
+ * compute::attention_reference (core/src/compute.rs:461-547).  k_hist/v_hist
+ * hold hist_len positions in [pos][kv_heads][head_dim] layout (KvCache,
+ * runtime/src/kv_cache.rs:452-481); k_cur/v_cur are [kv_heads][head_dim];
+ * q and k_cur are already rotated (RoPE is a separate call, as in
+ * model_executor.rs:196-204).  Unlike the reference the output is written to
+ * a caller-owned buffer instead of a fresh Vec. */
+int32_t rf_attention_decode(rf_ctx *ctx, const float *q, const float *k_hist, const float *v_hist,
+                            const float *k_cur, const float *v_cur, uint32_t hist_len, uint32_t q_heads,
+                            uint32_t kv_heads, uint32_t head_dim, float *out, rf_stream_t stream);
+
+/* ---------------------------------------------------------- elementwise */
+
+/* ops::apply_rope -> compute::rope_reference (runtime/src/ops.rs:9-20,
+ * core/src/compute.rs:389-456): half-split RoPE in place on q[q_heads][hd]
+ * and k[kv_heads][hd].  cos/sin are computed on the host with the
+ * reference's f32 expression and libm. */
+int32_t rf_rope(rf_ctx *ctx, float *q, float *k, uint64_t position, uint32_t head_dim, uint32_t q_heads,
+                uint32_t kv_heads, float theta, rf_stream_t stream);
+/* compute::rms_norm_reference (compute.rs:291-319); ComputeBackend::rmsnorm. */
+int32_t rf_rmsnorm(rf_ctx *ctx, const float *x, const float *weight, uint64_t n, float eps, float *out,
+                   rf_stream_t stream);
+/* add_reference / mul_reference / silu_reference / swiglu_reference
+ * (compute.rs:321-361). */
+int32_t rf_add(rf_ctx *ctx, const float *a, const float *b, uint64_t n, float *out, rf_stream_t stream);
+int32_t rf_mul(rf_ctx *ctx, const float *a, const float *b, uint64_t n, float *out, rf_stream_t stream);
+int32_t rf_silu(rf_ctx *ctx, const float *x, uint64_t n, float *out, rf_stream_t stream);
+int32_t rf_swiglu(rf_ctx *ctx, const float *gate, const float *up, uint64_t n, float *out, rf_stream_t stream);
+/* softmax_reference in place (compute.rs:363-384). */
+int32_t rf_softmax(rf_ctx *ctx, float *values, uint64_t n, rf_stream_t stream);
+/* Greedy Sampler::sample_checked (runtime/src/sampling.rs:45-57): the first
+ * maximum wins; the index is written to DEVICE memory out_index. */
+int32_t rf_argmax(rf_ctx *ctx, const float *logits, uint64_t n, uint32_t *out_index, rf_stream_t stream);
+
+/* ------------------------------------------------- synthetic payloads */
+
+/* Writes n_blocks GGUF blocks of ggml_type (F32: n_blocks floats) generated
+ * from `seed` starting at global block index first_block, on the device.
+ * Scale fields are f16(|n| * scale_mul) with n an Irwin-Hall(12) normal;
+ * Q8_0 codes are uniform in [-127, 127]; the other codes are uniform bytes.
+ * Bench and test input generator; it has no counterpart in the reference. */
+int32_t rf_synth_blocks(rf_ctx *ctx, uint32_t ggml_type, uint64_t seed, uint64_t first_block, uint64_t n_blocks,
+                        double scale_mul, void *dst, rf_stream_t stream);
+
+/* ---------------------------------------------------------------- model */
+
+/* LlamaConfig (runtime/src/model.rs:26-37). */
+typedef struct {
+    uint64_t vocab_size;
+    uint64_t context_length;
+    uint64_t embedding_length;
+    uint64_t block_count;
+    uint64_t feed_forward_length;
+    uint64_t head_count;
+    uint64_t head_count_kv;
+    uint64_t head_dim;
+    float rms_eps;
+    float rope_freq_base;
+} rf_model_config;
+
+/* A dense llama/qwen2 decoder whose weights live in VRAM (charges
+ * "layer:{i}:{tensor}", "persistent:{tensor}", "kv_cache", "tmp:forward"),
+ * executing StreamingLlamaModel::forward_single_streaming
+ * (streaming_model.rs:909-1305) with ModelExecutor::execute_layer
+ * (model_executor.rs:102-236) per layer, compute_logits
+ * (streaming_model.rs:1334-1370) and the greedy loop of
+ * InferenceEngine::generate_impl (inference.rs:445-759).  kv_capacity is the
+ * KV cache capacity in tokens (<= context_length). */
+int32_t rf_model_create(rf_ctx *ctx, const rf_model_config *cfg, uint64_t kv_capacity, rf_model **out);
+void rf_model_destroy(rf_model *model);
+
+/* Installs tensor `name` (GGUF names: token_embd.weight, output_norm.weight,
+ * output.weight, blk.{i}.{attn_norm,attn_q,attn_k,attn_v,attn_output,
+ * ffn_norm,ffn_gate,ffn_up,ffn_down}.weight, blk.{i}.attn_{q,k,v}.bias) of
+ * ggml shape [ne0 = in, ne1 = out] from host bytes (uploaded through a
+ * pinned staging buffer on the copy stream). */
+int32_t rf_model_set_tensor(rf_model *model, const char *name, uint32_t ggml_type, uint64_t ne0, uint64_t ne1,
+                            const void *host_data, uint64_t nbytes);
+/* Same, generating the payload on the device with rf_synth_blocks(seed,
+ * scale_mul); F32 tensors may instead be a constant (constant != NaN). */
+int32_t rf_model_synth_tensor(rf_model *model, const char *name, uint32_t ggml_type, uint64_t ne0, uint64_t ne1,
+                              uint64_t seed, double scale_mul, float constant);
+/* Resets the KV cache (seq_len = 0). */
+int32_t rf_model_reset(rf_model *model);
+uint64_t rf_model_seq_len(rf_model *model);
+
+/* One forward pass for `token` at `pos` (must equal seq_len); optionally
+ * copies the output-normed hidden state to host final_hidden[embedding]. */
+int32_t rf_model_forward(rf_model *model, uint32_t token, uint64_t pos, float *final_hidden);
+/* Logits of the last forward to host logits[vocab]. */
+int32_t rf_model_logits(rf_model *model, float *logits);
+/* Greedy generation: prompt tokens forwarded one at a time, then up to
+ * max_tokens greedy tokens with the reference's stop rules (EOS when eos >= 0,
+ * max tokens without a terminal forward, context length). */
+int32_t rf_model_generate(rf_model *model, const uint32_t *prompt, uint64_t prompt_len, uint64_t max_tokens,
+                          int64_t eos, uint32_t *out_tokens, uint64_t *n_out);
+/* One decode step on the device (logits -> argmax -> embedding of the chosen
+ * token -> forward), without host synchronisation: the token id stays in
+ * device memory.  Used by the throughput benchmark after the prompt. */
+int32_t rf_model_decode_steps(rf_model *model, uint64_t steps);
+/* Copies the last `n` greedy tokens produced by rf_model_decode_steps. */
+int32_t rf_model_read_tokens(rf_model *model, uint32_t *out, uint64_t n);
+/* Enables capture of one decode step into a hipGraph that is replayed by
+ * rf_model_decode_steps (1) or eager launches (0, default). */
+int32_t rf_model_use_graph(rf_model *model, int32_t enable);
+
+/* Launch groups of one decode step (see rf_model_time_kernel). */
+#define RF_KERNEL_QKV 1       /* attn RMSNorm + Q/K/V matvec (+ bias)      */
+#define RF_KERNEL_ATTENTION 2 /* RoPE + split-K attention + K/V commit     */
+#define RF_KERNEL_OPROJ 3     /* attn_output matvec + residual             */
+#define RF_KERNEL_GATEUP 4    /* ffn RMSNorm + gate/up matvec + SiLU*up    */
+#define RF_KERNEL_DOWN 5      /* ffn_down matvec + residual                */
+#define RF_KERNEL_LOGITS 6    /* output RMSNorm + output projection        */
+
+/* Times one launch group exactly as a decode step launches it: for every
+ * layer in order (RF_KERNEL_LOGITS: the output projection), `reps` times,
+ * back-to-back on the compute stream between two HIP events.  Returns the
+ * average milliseconds per launch, the average algorithmic HBM bytes per
+ * launch (weights + vectors read + written; attention: the K/V history at the
+ * current position) and the number of launches.  Activations are overwritten
+ * with meaningless values: call rf_model_reset before decoding again.  Used
+ * for the profiler's per-event times (runtime/src/profile.rs:7-23). */
+int32_t rf_model_time_kernel(rf_model *model, uint32_t kind, uint32_t reps, float *avg_ms,
+                             uint64_t *bytes_per_launch, uint64_t *launches);
+
+/* ------------------------------------------------------------- tuning */
+
+/* LDS bytes per matvec tile (4096..61440); returns the value in effect. */
+uint32_t rf_tune_matvec_tile_bytes(uint32_t bytes);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

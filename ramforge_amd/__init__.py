@@ -1,0 +1,447 @@
+"""ramforge_amd — MI355X (gfx950) decode-step tier for RAMforge.
+
+Python host mirror of RAMforge's compute interface for the decode hot path,
+over the C ABI of ``libramforge_hip.so`` (include/ramforge_hip.h).  Reference
+paths are relative to crates/ramforge-{core,runtime}/src of RAMforge.
+
+* :class:`Context`     — compute backend handle + device-memory ledger
+                          (CpuBackend::new, backend.rs:72-84; MemoryBudget,
+                          memory.rs:30-384, on the device domain)
+* :func:`matvec`       — quant::matvec_<fmt>[_row_range] (quant.rs:898-1489)
+* :class:`GpuBackend`  — ComputeBackend (backend.rs:27-52) for device buffers
+* :func:`matvec_backend` — compute_dispatch::matvec_backend (compute_dispatch.rs:40-58)
+* :func:`attention_checked` — ops::attention_checked (ops.rs:49-69)
+* :class:`GpuLlamaModel` — forward_single_streaming / compute_logits /
+                          generate_impl (streaming_model.rs:909-1370,
+                          inference.rs:445-759) on VRAM-resident weights.
+
+All compute runs in the HIP library; this module only moves host arrays and
+passes device pointers.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass
+from typing import Optional, Sequence
+
+import numpy as np
+
+from . import _lib
+from ._lib import RF_ALL_ROWS, ModelConfig, RamforgeError
+
+__all__ = [
+    "GGML", "BLOCK_GEOMETRY", "Context", "DeviceArray", "RamforgeError", "ModelConfig",
+    "matvec", "dequantize_rows", "attention_checked", "apply_rope", "rmsnorm", "add", "mul",
+    "silu", "swiglu", "softmax", "argmax", "GpuBackend", "GpuTensor", "matvec_backend",
+    "GpuLlamaModel", "row_bytes",
+]
+
+
+class GGML:
+    """ggml type ids (core/src/types.rs:238-292)."""
+
+    F32 = 0
+    F16 = 1
+    Q4_0 = 2
+    Q5_0 = 6
+    Q8_0 = 8
+    Q2_K = 10
+    Q3_K = 11
+    Q4_K = 12
+    Q5_K = 13
+    Q6_K = 14
+    Q8_K = 15
+    BF16 = 30
+
+    NAMES = {0: "F32", 1: "F16", 2: "Q4_0", 6: "Q5_0", 8: "Q8_0", 10: "Q2_K", 11: "Q3_K",
+             12: "Q4_K", 13: "Q5_K", 14: "Q6_K", 15: "Q8_K", 30: "BF16"}
+
+
+# (elements per block, bytes per block): core/src/quant.rs:24-37
+BLOCK_GEOMETRY = {
+    GGML.F32: (1, 4), GGML.F16: (1, 2), GGML.BF16: (1, 2),
+    GGML.Q4_0: (32, 18), GGML.Q5_0: (32, 22), GGML.Q8_0: (32, 34),
+    GGML.Q2_K: (256, 84), GGML.Q3_K: (256, 110), GGML.Q4_K: (256, 144),
+    GGML.Q5_K: (256, 176), GGML.Q6_K: (256, 210), GGML.Q8_K: (256, 292),
+}
+
+
+def row_bytes(ggml_type: int, in_dim: int) -> int:
+    qk, bs = BLOCK_GEOMETRY[ggml_type]
+    if in_dim % qk:
+        raise ValueError(f"{GGML.NAMES[ggml_type]} in_dim {in_dim} not divisible by {qk}")
+    return in_dim // qk * bs
+
+
+def _ptr(a) -> Optional[int]:
+    if a is None:
+        return None
+    if isinstance(a, DeviceArray):
+        return a.ptr
+    if isinstance(a, int):
+        return a
+    raise TypeError(f"expected a DeviceArray or device address, got {type(a).__name__}")
+
+
+class DeviceArray:
+    """A ledger-charged device buffer with a numpy view of its shape/dtype."""
+
+    def __init__(self, ctx: "Context", ptr: int, nbytes: int, shape, dtype, charge: str):
+        self.ctx = ctx
+        self.ptr = ptr
+        self.nbytes = nbytes
+        self.shape = tuple(shape)
+        self.dtype = np.dtype(dtype)
+        self.charge = charge
+
+    def upload(self, host: np.ndarray) -> "DeviceArray":
+        h = np.ascontiguousarray(host)
+        if h.nbytes > self.nbytes:
+            raise ValueError(f"upload of {h.nbytes} bytes into a {self.nbytes}-byte buffer")
+        _lib.check(self.ctx.lib.rf_upload(self.ctx.handle, self.ptr, h.ctypes.data, h.nbytes))
+        return self
+
+    def numpy(self) -> np.ndarray:
+        out = np.empty(self.shape, dtype=self.dtype)
+        _lib.check(self.ctx.lib.rf_download(self.ctx.handle, out.ctypes.data, self.ptr, out.nbytes))
+        return out
+
+    def free(self) -> None:
+        if self.ptr:
+            _lib.check(self.ctx.lib.rf_vram_release(self.ctx.handle, self.charge.encode()))
+            self.ptr = 0
+
+
+class Context:
+    """Device context: compute + copy streams and the VRAM ledger."""
+
+    _serial = 0
+
+    def __init__(self, device: int = 0, vram_budget_bytes: int = 0):
+        self.lib = _lib.load()
+        h = C.c_void_p()
+        _lib.check(self.lib.rf_ctx_create(device, vram_budget_bytes, C.byref(h)))
+        self.handle = h
+
+    # lifecycle
+    def close(self) -> None:
+        if self.handle:
+            self.lib.rf_ctx_destroy(self.handle)
+            self.handle = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def synchronize(self) -> None:
+        _lib.check(self.lib.rf_ctx_synchronize(self.handle))
+
+    @property
+    def compute_stream(self) -> int:
+        return self.lib.rf_ctx_compute_stream(self.handle)
+
+    @property
+    def copy_stream(self) -> int:
+        return self.lib.rf_ctx_copy_stream(self.handle)
+
+    def device_info(self):
+        name = C.create_string_buffer(256)
+        cus = C.c_int32()
+        _lib.check(self.lib.rf_ctx_device_info(self.handle, name, 256, C.byref(cus)))
+        return name.value.decode(), cus.value
+
+    # ledger (MemoryBudget on the device domain)
+    @property
+    def vram_used(self) -> int:
+        return self.lib.rf_vram_used(self.handle)
+
+    @property
+    def vram_total(self) -> int:
+        return self.lib.rf_vram_total(self.handle)
+
+    @property
+    def vram_peak(self) -> int:
+        return self.lib.rf_vram_peak(self.handle)
+
+    def charge(self, name: str) -> Optional[int]:
+        v = C.c_uint64()
+        rc = self.lib.rf_vram_charge(self.handle, name.encode(), C.byref(v))
+        return v.value if rc == _lib.RF_OK else None
+
+    def rename_prefix(self, old: str, new: str) -> None:
+        _lib.check(self.lib.rf_vram_rename_prefix(self.handle, old.encode(), new.encode()))
+
+    # buffers
+    def alloc(self, nbytes: int, charge: Optional[str] = None, shape=None, dtype=np.uint8) -> DeviceArray:
+        if charge is None:
+            Context._serial += 1
+            charge = f"tmp:array:{Context._serial}"
+        p = C.c_void_p()
+        _lib.check(self.lib.rf_vram_alloc(self.handle, charge.encode(), int(nbytes), C.byref(p)))
+        if shape is None:
+            shape = (nbytes // np.dtype(dtype).itemsize,)
+        return DeviceArray(self, p.value, int(nbytes), shape, dtype, charge)
+
+    def empty(self, shape, dtype=np.float32, charge: Optional[str] = None) -> DeviceArray:
+        shape = tuple(int(s) for s in (shape if isinstance(shape, (tuple, list)) else (shape,)))
+        n = int(np.prod(shape)) * np.dtype(dtype).itemsize
+        return self.alloc(max(n, 1), charge, shape, dtype)
+
+    def array(self, host: np.ndarray, charge: Optional[str] = None) -> DeviceArray:
+        h = np.ascontiguousarray(host)
+        d = self.alloc(max(h.nbytes, 1), charge, h.shape, h.dtype)
+        if h.nbytes:
+            d.upload(h)
+        return d
+
+    # synthetic payloads (bench / test inputs)
+    def synth_blocks(self, ggml_type: int, seed: int, first_block: int, n_blocks: int, scale_mul: float,
+                     dst: DeviceArray, stream=None) -> None:
+        _lib.check(self.lib.rf_synth_blocks(self.handle, ggml_type, seed, first_block, n_blocks, scale_mul,
+                                            _ptr(dst), stream))
+
+    # events
+    def event(self):
+        e = C.c_void_p()
+        _lib.check(self.lib.rf_event_create(self.handle, C.byref(e)))
+        return e.value
+
+    def record(self, ev, stream=None) -> None:
+        _lib.check(self.lib.rf_event_record(self.handle, ev, stream))
+
+    def elapsed_ms(self, a, b) -> float:
+        ms = C.c_float()
+        _lib.check(self.lib.rf_event_synchronize(self.handle, b))
+        _lib.check(self.lib.rf_event_elapsed_ms(self.handle, a, b, C.byref(ms)))
+        return ms.value
+
+    def destroy_event(self, ev) -> None:
+        _lib.check(self.lib.rf_event_destroy(self.handle, ev))
+
+
+# --------------------------------------------------------------------- ops
+
+def matvec(ctx: Context, ggml_type: int, w, w_shape: Sequence[int], x, y, row_start: int = 0,
+           row_count: Optional[int] = None, w_bytes: Optional[int] = None, stream=None) -> None:
+    """quant::matvec_<fmt>_row_range (quant.rs:913-975): kernel shape
+    ``w_shape = [out_dim, in_dim]``; y is local to ``row_start``."""
+    if len(w_shape) != 2:
+        raise RamforgeError(_lib.RF_ERR_INVALID, f"{GGML.NAMES.get(ggml_type, ggml_type)} matvec expects 2D weight")
+    out_dim, in_dim = (int(v) for v in w_shape)
+    wb = w.nbytes if (w_bytes is None and isinstance(w, DeviceArray)) else int(w_bytes or 0)
+    rc = ctx.lib.rf_matvec(ctx.handle, ggml_type, _ptr(w), wb, out_dim, in_dim, _ptr(x), _ptr(y), row_start,
+                           RF_ALL_ROWS if row_count is None else row_count, stream)
+    _lib.check(rc)
+
+
+def dequantize_rows(ctx: Context, ggml_type: int, w, in_dim: int, row_start: int, row_count: int, out,
+                    w_bytes: Optional[int] = None, stream=None) -> None:
+    """dequantize_row_<fmt> (quant.rs:615-868) for a row range, bit-exact."""
+    wb = w.nbytes if (w_bytes is None and isinstance(w, DeviceArray)) else int(w_bytes or 0)
+    _lib.check(ctx.lib.rf_dequantize_rows(ctx.handle, ggml_type, _ptr(w), wb, in_dim, row_start, row_count,
+                                          _ptr(out), stream))
+
+
+def attention_checked(ctx: Context, q, k_hist, v_hist, k_new, v_new, hist_len: int, n_heads: int,
+                      n_kv_heads: int, head_dim: int, out: Optional[DeviceArray] = None, stream=None) -> DeviceArray:
+    """ops::attention_checked (ops.rs:49-69) -> compute::attention_reference."""
+    if out is None:
+        out = ctx.empty((n_heads * head_dim,))
+    _lib.check(ctx.lib.rf_attention_decode(ctx.handle, _ptr(q), _ptr(k_hist), _ptr(v_hist), _ptr(k_new),
+                                           _ptr(v_new), hist_len, n_heads, n_kv_heads, head_dim, _ptr(out), stream))
+    return out
+
+
+def apply_rope(ctx: Context, q, k, pos: int, head_dim: int, n_heads: int, n_kv_heads: int, freq_base: float,
+               stream=None) -> None:
+    """ops::apply_rope (ops.rs:9-20): half-split RoPE in place."""
+    _lib.check(ctx.lib.rf_rope(ctx.handle, _ptr(q), _ptr(k), pos, head_dim, n_heads, n_kv_heads, freq_base, stream))
+
+
+def rmsnorm(ctx: Context, x, weight, n: int, eps: float, out, stream=None) -> None:
+    _lib.check(ctx.lib.rf_rmsnorm(ctx.handle, _ptr(x), _ptr(weight), n, eps, _ptr(out), stream))
+
+
+def add(ctx: Context, a, b, n: int, out, stream=None) -> None:
+    _lib.check(ctx.lib.rf_add(ctx.handle, _ptr(a), _ptr(b), n, _ptr(out), stream))
+
+
+def mul(ctx: Context, a, b, n: int, out, stream=None) -> None:
+    _lib.check(ctx.lib.rf_mul(ctx.handle, _ptr(a), _ptr(b), n, _ptr(out), stream))
+
+
+def silu(ctx: Context, x, n: int, out, stream=None) -> None:
+    _lib.check(ctx.lib.rf_silu(ctx.handle, _ptr(x), n, _ptr(out), stream))
+
+
+def swiglu(ctx: Context, gate, up, n: int, out, stream=None) -> None:
+    _lib.check(ctx.lib.rf_swiglu(ctx.handle, _ptr(gate), _ptr(up), n, _ptr(out), stream))
+
+
+def softmax(ctx: Context, values, n: int, stream=None) -> None:
+    _lib.check(ctx.lib.rf_softmax(ctx.handle, _ptr(values), n, stream))
+
+
+def argmax(ctx: Context, logits, n: int, out_index, stream=None) -> None:
+    """Greedy Sampler::sample_checked (sampling.rs:45-57) into device memory."""
+    _lib.check(ctx.lib.rf_argmax(ctx.handle, _ptr(logits), n, _ptr(out_index), stream))
+
+
+# ------------------------------------------------- backend / dispatch mirror
+
+@dataclass
+class GpuTensor:
+    """A TensorData held in VRAM (core/src/tensor.rs:328-343): raw GGUF
+    payload with ggml shape ``[in, out]``."""
+
+    ggml_type: int
+    shape: tuple
+    data: DeviceArray
+
+
+class GpuBackend:
+    """ComputeBackend (runtime/src/backend.rs:27-52) over device buffers."""
+
+    def __init__(self, ctx: Context):
+        self.ctx = ctx
+
+    def name(self) -> str:
+        return "HIP-gfx950"
+
+    def num_threads(self) -> int:
+        return 1  # parallelism is inside the kernels; calls come from one thread
+
+    def matvec(self, w: DeviceArray, w_shape: Sequence[int], x: DeviceArray, y: DeviceArray) -> None:
+        """F32 matvec with ``w_shape = [in, out]`` (ggml layout)."""
+        if len(w_shape) != 2:
+            raise RamforgeError(_lib.RF_ERR_INVALID,
+                                f"backend matvec expects 2D w_shape [in, out] (ggml layout), got {list(w_shape)}")
+        in_dim, out_dim = int(w_shape[0]), int(w_shape[1])
+        if x.shape[0] != in_dim or y.shape[0] != out_dim or w.nbytes < 4 * in_dim * out_dim:
+            raise RamforgeError(
+                _lib.RF_ERR_INVALID,
+                f"backend matvec arity mismatch (ggml layout [in, out]): shape {list(w_shape)} implies in={in_dim}, "
+                f"out={out_dim}, but got w bytes={w.nbytes}, x.len()={x.shape[0]}, y.len()={y.shape[0]}")
+        matvec(self.ctx, GGML.F32, w, (out_dim, in_dim), x, y)
+
+    def rmsnorm(self, x, weight, eps: float, y) -> None:
+        rmsnorm(self.ctx, x, weight, x.shape[0], eps, y)
+
+    def add(self, a, b, out) -> None:
+        add(self.ctx, a, b, a.shape[0], out)
+
+    def mul(self, a, b, out) -> None:
+        mul(self.ctx, a, b, a.shape[0], out)
+
+    def silu(self, x, out) -> None:
+        silu(self.ctx, x, x.shape[0], out)
+
+    def softmax(self, x) -> None:
+        softmax(self.ctx, x, x.shape[0])
+
+
+def matvec_backend(backend: GpuBackend, td: GpuTensor, x: DeviceArray, y: DeviceArray) -> None:
+    """compute_dispatch::matvec_backend (compute_dispatch.rs:40-58): F32 goes
+    through the backend matvec, quantized tensors through the block kernels
+    after the ``[in, out] -> [out, in]`` flip (compute_dispatch.rs:109-110)."""
+    if len(td.shape) != 2:
+        raise RamforgeError(_lib.RF_ERR_INVALID,
+                            f"{GGML.NAMES.get(td.ggml_type)} matvec expects 2D tensor shape, got {list(td.shape)}")
+    if td.ggml_type == GGML.F32:
+        backend.matvec(td.data, td.shape, x, y)
+        return
+    in_dim, out_dim = td.shape
+    if x.shape[0] != in_dim or y.shape[0] != out_dim:
+        raise RamforgeError(_lib.RF_ERR_INVALID,
+                            f"matvec shape mismatch: W {[out_dim, in_dim]}, x {x.shape[0]}, y {y.shape[0]}")
+    matvec(backend.ctx, td.ggml_type, td.data, (out_dim, in_dim), x, y)
+
+
+# ------------------------------------------------------------------- model
+
+class GpuLlamaModel:
+    """VRAM-resident dense llama decoder (rf_model_* in the C ABI)."""
+
+    def __init__(self, ctx: Context, cfg: dict, kv_capacity: Optional[int] = None):
+        self.ctx = ctx
+        self.cfg = dict(cfg)
+        c = ModelConfig(**{k: self.cfg[k] for k, _ in ModelConfig._fields_})
+        self._c = c
+        h = C.c_void_p()
+        cap = int(kv_capacity if kv_capacity is not None else cfg["context_length"])
+        _lib.check(ctx.lib.rf_model_create(ctx.handle, C.byref(c), cap, C.byref(h)))
+        self.handle = h
+        self.kv_capacity = cap
+
+    def close(self) -> None:
+        if self.handle:
+            self.ctx.lib.rf_model_destroy(self.handle)
+            self.handle = None
+
+    def set_tensor(self, name: str, ggml_type: int, ne0: int, ne1: int, data: np.ndarray) -> None:
+        h = np.ascontiguousarray(data)
+        _lib.check(self.ctx.lib.rf_model_set_tensor(self.handle, name.encode(), ggml_type, ne0, ne1,
+                                                    h.ctypes.data, h.nbytes))
+
+    def synth_tensor(self, name: str, ggml_type: int, ne0: int, ne1: int, seed: int, scale_mul: float,
+                     constant: float = float("nan")) -> None:
+        _lib.check(self.ctx.lib.rf_model_synth_tensor(self.handle, name.encode(), ggml_type, ne0, ne1, seed,
+                                                      scale_mul, constant))
+
+    def reset(self) -> None:
+        _lib.check(self.ctx.lib.rf_model_reset(self.handle))
+
+    @property
+    def seq_len(self) -> int:
+        return self.ctx.lib.rf_model_seq_len(self.handle)
+
+    def forward(self, token: int, pos: int, want_hidden: bool = False) -> Optional[np.ndarray]:
+        hidden = np.empty(self.cfg["embedding_length"], np.float32) if want_hidden else None
+        _lib.check(self.ctx.lib.rf_model_forward(self.handle, token, pos,
+                                                 hidden.ctypes.data if hidden is not None else None))
+        return hidden
+
+    def logits(self) -> np.ndarray:
+        out = np.empty(self.cfg["vocab_size"], np.float32)
+        _lib.check(self.ctx.lib.rf_model_logits(self.handle, out.ctypes.data))
+        return out
+
+    def generate(self, prompt: Sequence[int], max_tokens: int, eos: int = -1) -> list:
+        p = np.ascontiguousarray(np.asarray(prompt, dtype=np.uint32))
+        out = np.zeros(max(max_tokens, 1), np.uint32)
+        n = C.c_uint64()
+        _lib.check(self.ctx.lib.rf_model_generate(self.handle, p.ctypes.data, len(p), max_tokens, eos,
+                                                  out.ctypes.data, C.byref(n)))
+        return [int(t) for t in out[: n.value]]
+
+    def use_graph(self, enable: bool) -> None:
+        _lib.check(self.ctx.lib.rf_model_use_graph(self.handle, 1 if enable else 0))
+
+    def decode_steps(self, steps: int) -> None:
+        _lib.check(self.ctx.lib.rf_model_decode_steps(self.handle, steps))
+
+    KERNELS = {"qkv": 1, "attention": 2, "oproj": 3, "gateup": 4, "down": 5, "logits": 6}
+
+    def time_kernel(self, kind: str, reps: int = 1):
+        """(avg ms per launch, algorithmic bytes per launch, launches) of one
+        decode-step launch group, timed with HIP events on the compute stream."""
+        ms, b, n = C.c_float(), C.c_uint64(), C.c_uint64()
+        _lib.check(self.ctx.lib.rf_model_time_kernel(self.handle, self.KERNELS[kind], reps, C.byref(ms), C.byref(b),
+                                                     C.byref(n)))
+        return ms.value, b.value, n.value
+
+    def read_tokens(self, n: int) -> list:
+        out = np.zeros(max(n, 1), np.uint32)
+        _lib.check(self.ctx.lib.rf_model_read_tokens(self.handle, out.ctypes.data, n))
+        return [int(t) for t in out[:n]]
+
+
+def tune_matvec_tile_bytes(nbytes: int = 0) -> int:
+    """Set (nbytes > 0) and return the LDS bytes per matvec tile."""
+    return _lib.load().rf_tune_matvec_tile_bytes(nbytes)
+
+
+# Fail loudly at import if the HIP library was not built.
+_lib.load()

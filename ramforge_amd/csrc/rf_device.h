@@ -1,0 +1,74 @@
+// rf_device.h — device helpers shared by the gfx950 kernels.
+//
+// All kernels are compiled with -ffp-contract=off: a multiply followed by an
+// add stays two roundings unless fmaf() is written explicitly.  Dequantisation
+// relies on that to stay bit-identical with the reference decoders, which never
+// fuse (Rust does not contract floating-point expressions).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define RF_WAVE 64
+
+// GGUF half -> float exactly as core/src/quant.rs:40-65 decodes it.  Normal,
+// infinite and NaN halves decode to their IEEE value (NaN payload kept, not
+// quieted).  The reference's subnormal branch normalises with a test-then-shift
+// loop that counts one shift too many, so a subnormal half with fraction f
+// decodes to f * 2^-25 — half its IEEE value.  f * 2^-25 is computed exactly
+// here (f < 1024 is exact in binary32 and the scale is a power of two), which
+// yields the same bits as the reference.
+__device__ __forceinline__ float rf_half_to_float(uint32_t h) {
+  const uint32_t sign = (h & 0x8000u) << 16;
+  const uint32_t exp = (h >> 10) & 0x1Fu;
+  const uint32_t frac = h & 0x3FFu;
+  if (exp == 0u) {
+    const float v = (float)frac * 0x1p-25f;
+    return __uint_as_float(__float_as_uint(v) | sign);
+  }
+  const uint32_t e32 = (exp == 0x1Fu) ? 0xFFu : exp + 112u;
+  return __uint_as_float(sign | (e32 << 23) | (frac << 13));
+}
+
+__device__ __forceinline__ float rf_bf16_to_float(uint32_t h) { return __uint_as_float(h << 16); }
+
+// Unaligned little-endian loads from a byte pointer (any alignment), byte-wise.
+__device__ __forceinline__ uint32_t rf_ld_u16(const uint8_t* p) {
+  return (uint32_t)p[0] | ((uint32_t)p[1] << 8);
+}
+
+// 32-bit word at byte offset `off` of an LDS buffer whose base is 4-byte
+// aligned; `off` may have any alignment.  Reads the two aligned words that
+// cover it and shifts with v_alignbyte.  The LDS buffer must be readable for 4
+// bytes past the last byte requested.
+__device__ __forceinline__ uint32_t rf_lds_u32(const uint8_t* lds, uint32_t off) {
+  const uint32_t* w = reinterpret_cast<const uint32_t*>(lds + (off & ~3u));
+  return __builtin_amdgcn_alignbyte(w[1], w[0], off & 3u);
+}
+
+// N consecutive 32-bit words starting at byte offset `off` (any alignment).
+template <int N>
+__device__ __forceinline__ void rf_lds_words(const uint8_t* lds, uint32_t off, uint32_t (&out)[N]) {
+  const uint32_t* w = reinterpret_cast<const uint32_t*>(lds + (off & ~3u));
+  const uint32_t sh = off & 3u;
+  uint32_t raw[N + 1];
+#pragma unroll
+  for (int i = 0; i < N + 1; ++i) raw[i] = w[i];
+#pragma unroll
+  for (int i = 0; i < N; ++i) out[i] = __builtin_amdgcn_alignbyte(raw[i + 1], raw[i], sh);
+}
+
+__device__ __forceinline__ float rf_wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, RF_WAVE);
+  return v;
+}
+
+__device__ __forceinline__ float rf_wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, RF_WAVE));
+  return v;
+}
+
+// Unsigned byte k of a word converted to float (v_cvt_f32_ubyte{k}).
+__device__ __forceinline__ float rf_ub(uint32_t w, int k) { return (float)((w >> (8 * k)) & 0xFFu); }

@@ -1,0 +1,104 @@
+// rf_kernels.h — kernel argument structs and host-side launchers (internal).
+#pragma once
+
+#include "rf_formats.h"
+
+namespace rf {
+
+enum { EPI_STORE = 0, EPI_RESIDUAL = 1, EPI_SWIGLU = 2 };
+
+struct MvSeg {
+  const uint8_t* w;
+  float* y;
+  const float* res;
+  uint32_t rows;
+  uint32_t tile_begin;
+};
+
+struct MvArgs {
+  MvSeg seg[3];
+  uint32_t nseg;
+  const float* x;
+  const float* norm_w;
+  float eps;
+  uint32_t in_dim, units, rg, rows_per_tile, row_bytes, tile_stride;
+  const uint8_t* w_up;
+};
+
+struct MvPlan {
+  bool tiled;
+  uint32_t units, rg, rows_per_tile, threads, row_bytes, tile_stride, lds_bytes;
+};
+
+// One output segment of a (possibly multi-matrix) matvec launch.  All
+// segments of one launch share the input vector, in_dim and ggml type.
+struct MvSegDesc {
+  const void* w;      // first byte of the segment's first row
+  const void* w_up;   // EPI_SWIGLU: the paired "up" matrix (same rows)
+  float* y;
+  const float* res;   // EPI_RESIDUAL: y = res + W x
+  uint64_t rows;
+};
+
+bool type_geometry(uint32_t t, uint64_t* qk, uint64_t* bs);
+MvPlan plan_matvec(uint32_t t, uint64_t in_dim, bool dual);
+void set_matvec_tile_bytes(uint32_t bytes);
+uint32_t matvec_tile_bytes();
+hipError_t launch_matvec_segments(uint32_t t, const MvSegDesc* segs, int nseg, const float* x,
+                                  const float* norm_w, float eps, uint64_t in_dim, int epi,
+                                  hipStream_t st);
+
+// Bit-exact row decode: rows [0, rows) of `w` (row_bytes each) -> out[rows][in_dim].
+// If token_index != nullptr the single row *token_index is decoded instead.
+hipError_t launch_dequant_rows(uint32_t t, const void* w, uint64_t in_dim, uint64_t rows,
+                               float* out, const uint32_t* token_index, uint64_t token_rows,
+                               hipStream_t st);
+
+// Split-K single-query attention (see rf_attention.hip).
+struct AttnArgs {
+  const float* q;        // [qh][hd]
+  const float* k_hist;   // [hist][kvh][hd] (or the model's cache base)
+  const float* v_hist;
+  const float* k_cur;    // [kvh][hd]
+  const float* v_cur;
+  float* out;            // [qh][hd]
+  float* ws;             // [nsplit][qh][hd + 2]
+  const float* rope;     // model mode: [cap][hd/2][2] cos/sin table, else null
+  float* k_store;        // model mode: cache slot base (k_cache), else null
+  float* v_store;
+  const int32_t* d_pos;  // model mode: device position (== hist), else null
+  uint32_t hist;         // API mode history length
+  uint32_t qh, kvh, hd, nsplit;
+  float denom;           // sqrt(hd) as the reference computes it
+};
+hipError_t launch_attention(const AttnArgs& a, hipStream_t st);
+// Any-shape kernel; its workspace is [qh][hist + 1] floats.
+hipError_t launch_attention_naive(const AttnArgs& a, hipStream_t st);
+uint32_t attention_splits(uint32_t total_positions, uint32_t kvh);
+bool attention_supported(uint32_t qh, uint32_t kvh, uint32_t hd);
+
+// Elementwise (rf_elementwise.hip).
+hipError_t launch_rmsnorm(const float* x, const float* w, uint64_t n, float eps, float* y, hipStream_t st);
+hipError_t launch_binary(int op, const float* a, const float* b, uint64_t n, float* out, hipStream_t st);
+hipError_t launch_silu(const float* x, uint64_t n, float* y, hipStream_t st);
+hipError_t launch_softmax(float* v, uint64_t n, hipStream_t st);
+// cos/sin pairs of one position passed by value (hd <= 512).
+struct RopeCS {
+  float cs[512];
+};
+hipError_t launch_rope_pair(float* q, float* k, const RopeCS& cs, uint32_t hd, uint32_t qh, uint32_t kvh, hipStream_t st);
+hipError_t launch_bias_add(float* v, const float* b, uint64_t n, hipStream_t st);
+// Writes the index to *out and, if ring != null, also to ring[*d_pos].
+hipError_t launch_argmax(const float* logits, uint64_t n, uint32_t* out, float* ws_val, uint32_t* ws_idx,
+                         uint32_t* ring, const int32_t* d_pos, hipStream_t st);
+uint32_t argmax_partials(uint64_t n);
+hipError_t launch_synth(uint32_t t, uint64_t seed, uint64_t first_block, uint64_t n_blocks, double mul,
+                        void* dst, hipStream_t st);
+hipError_t launch_advance_pos(int32_t* d_pos, hipStream_t st);
+hipError_t launch_set_u32(uint32_t* p, uint32_t v, hipStream_t st);
+hipError_t launch_set_i32(int32_t* p, int32_t v, hipStream_t st);
+hipError_t launch_fill(float* p, float v, uint64_t n, hipStream_t st);
+
+enum { BIN_ADD = 0, BIN_MUL = 1, BIN_SWIGLU = 2 };
+
+}  // namespace rf

@@ -1,0 +1,682 @@
+// rf_model.hip — device-resident dense llama/qwen2 decode (host executor).
+//
+// Mirrors the reference's composition with the device kernels:
+//   forward  = StreamingLlamaModel::forward_single_streaming
+//              (runtime/src/streaming_model.rs:909-1305)
+//   layer    = ModelExecutor::execute_layer (runtime/src/model_executor.rs:102-236)
+//   logits   = compute_logits (streaming_model.rs:1334-1370)
+//   generate = InferenceEngine::generate_impl's greedy loop (inference.rs:580-707)
+//
+// Per layer the op order is the reference's (RMSNorm -> Q/K/V -> bias -> RoPE
+// -> attention -> o-proj -> residual -> RMSNorm -> gate/up -> SiLU*up -> down
+// -> residual) with these launch-level fusions:
+//   1. attn RMSNorm + Q/K/V projections: one matvec launch over three segments
+//   2. RoPE + attention + K/V cache commit: the split-K attention kernel
+//   3. o-proj + residual add: matvec epilogue
+//   4. ffn RMSNorm + gate/up + SiLU(gate)*up: dual-tile matvec
+//   5. down + residual add: matvec epilogue
+// K/V of the token is written to slot `pos` of each layer's own cache while
+// that layer runs; every layer reads only slots < pos, so this is equivalent
+// to the reference's stage-then-commit after the last layer
+// (streaming_model.rs:1049-1070, 1288-1295).
+//
+// Device state (current position, current token, generated-token ring) lives
+// in VRAM so a decode step needs no host round-trip and can be captured once
+// into a hipGraph and replayed.
+#include <cmath>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "rf_runtime.h"
+
+namespace rf {
+
+struct DevTensor {
+  uint32_t type = 0;
+  uint64_t ne0 = 0, ne1 = 0, nbytes = 0;
+  void* d = nullptr;
+  std::string charge;
+  bool present() const { return d != nullptr; }
+};
+
+struct Layer {
+  DevTensor attn_norm, q, k, v, o, ffn_norm, gate, up, down, bq, bk, bv;
+};
+
+}  // namespace rf
+
+using namespace rf;
+
+struct rf_model {
+  rf_ctx* ctx = nullptr;
+  rf_model_config cfg{};
+  uint64_t kv_cap = 0;
+  DevTensor token_embd, output_norm, output;
+  std::vector<Layer> layers;
+  float* k_cache = nullptr;  // [layer][cap][kvh][hd]
+  float* v_cache = nullptr;
+  float* rope = nullptr;     // [cap][hd/2][2]
+  float *hidden = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attn_out = nullptr, *act = nullptr;
+  float *logits = nullptr, *final_hidden = nullptr, *attn_ws = nullptr, *up_tmp = nullptr;
+  float* amax_val = nullptr;
+  uint32_t* amax_idx = nullptr;
+  int32_t* d_pos = nullptr;
+  uint32_t* d_token = nullptr;
+  uint32_t* d_ring = nullptr;  // token chosen for position p is stored at ring[p]
+  uint32_t nsplit = 1;
+  uint64_t seq_len = 0;
+  bool use_graph = false;
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t graph_exec = nullptr;
+  std::vector<std::string> charges;
+};
+
+namespace {
+
+int32_t charge_alloc(rf_model* m, const std::string& name, uint64_t bytes, void** out) {
+  int32_t rc = vram_alloc(m->ctx, name, bytes, out);
+  if (rc == RF_OK) m->charges.push_back(name);
+  return rc;
+}
+
+int32_t drop_tensor(rf_model* m, DevTensor& t) {
+  if (!t.present()) return RF_OK;
+  int32_t rc = vram_release(m->ctx, t.charge);
+  for (size_t i = 0; i < m->charges.size(); ++i)
+    if (m->charges[i] == t.charge) { m->charges.erase(m->charges.begin() + i); break; }
+  t = DevTensor{};
+  return rc;
+}
+
+void reset_graph(rf_model* m) {
+  if (m->graph_exec) hipGraphExecDestroy(m->graph_exec);
+  if (m->graph) hipGraphDestroy(m->graph);
+  m->graph_exec = nullptr;
+  m->graph = nullptr;
+}
+
+// Resolve a GGUF tensor name to its slot and expected shape [ne0, ne1].
+int32_t resolve(rf_model* m, const std::string& name, DevTensor** slot, uint64_t* e0, uint64_t* e1,
+                std::string* charge) {
+  const rf_model_config& c = m->cfg;
+  const uint64_t d = c.embedding_length, qd = c.head_count * c.head_dim, kvd = c.head_count_kv * c.head_dim;
+  const uint64_t f = c.feed_forward_length;
+  if (name == "token_embd.weight") { *slot = &m->token_embd; *e0 = d; *e1 = c.vocab_size; *charge = "persistent:" + name; return RF_OK; }
+  if (name == "output_norm.weight") { *slot = &m->output_norm; *e0 = d; *e1 = 1; *charge = "persistent:" + name; return RF_OK; }
+  if (name == "output.weight") { *slot = &m->output; *e0 = d; *e1 = c.vocab_size; *charge = "persistent:" + name; return RF_OK; }
+  unsigned li = 0;
+  char rest[128];
+  if (sscanf(name.c_str(), "blk.%u.%127s", &li, rest) == 2 && li < m->layers.size()) {
+    Layer& L = m->layers[li];
+    const std::string r(rest);
+    *charge = "layer:" + std::to_string(li) + ":" + r;
+    struct E { const char* n; DevTensor* t; uint64_t a, b; } tab[] = {
+        {"attn_norm.weight", &L.attn_norm, d, 1}, {"attn_q.weight", &L.q, d, qd},
+        {"attn_k.weight", &L.k, d, kvd},          {"attn_v.weight", &L.v, d, kvd},
+        {"attn_output.weight", &L.o, qd, d},      {"ffn_norm.weight", &L.ffn_norm, d, 1},
+        {"ffn_gate.weight", &L.gate, d, f},       {"ffn_up.weight", &L.up, d, f},
+        {"ffn_down.weight", &L.down, f, d},       {"attn_q.bias", &L.bq, qd, 1},
+        {"attn_k.bias", &L.bk, kvd, 1},           {"attn_v.bias", &L.bv, kvd, 1}};
+    for (auto& e : tab)
+      if (r == e.n) { *slot = e.t; *e0 = e.a; *e1 = e.b; return RF_OK; }
+  }
+  return set_error(RF_ERR_INVALID, "unknown tensor '%s' for a %llu-layer llama model", name.c_str(),
+                   (unsigned long long)c.block_count);
+}
+
+bool is_vector_slot(const std::string& name) {
+  return name.find("_norm.weight") != std::string::npos || name.find(".bias") != std::string::npos;
+}
+
+int32_t check_tensor_shape(rf_model* m, const std::string& name, uint32_t t, uint64_t ne0, uint64_t ne1,
+                           uint64_t e0, uint64_t e1, uint64_t* bytes) {
+  if (ne0 != e0 || ne1 != e1)
+    return set_error(RF_ERR_INVALID, "tensor '%s' has shape [%llu, %llu], expected [%llu, %llu]", name.c_str(),
+                     (unsigned long long)ne0, (unsigned long long)ne1, (unsigned long long)e0,
+                     (unsigned long long)e1);
+  uint64_t qk = 1, bs = 0;
+  if (t == T_F32) bs = 4;
+  else if (t == T_F16 || t == T_BF16) bs = 2;
+  else if (!type_geometry(t, &qk, &bs))
+    return set_error(RF_ERR_UNSUPPORTED, "tensor '%s' has unsupported type %s", name.c_str(), type_name(t));
+  if (ne0 % qk != 0)
+    return set_error(RF_ERR_INVALID, "%s row size %llu not divisible by block size %llu", type_name(t),
+                     (unsigned long long)ne0, (unsigned long long)qk);
+  if (is_vector_slot(name) && t != T_F32 && t != T_F16 && t != T_BF16)
+    return set_error(RF_ERR_UNSUPPORTED, "tensor '%s' must be F32/F16/BF16, got %s", name.c_str(), type_name(t));
+  *bytes = ne0 / qk * bs * ne1;
+  (void)m;
+  return RF_OK;
+}
+
+// Upload (or synthesize) one tensor.  F16/BF16 payloads are decoded to F32 on
+// the device, as TensorData decodes them at load (core/src/tensor.rs:460-521).
+int32_t install(rf_model* m, const char* cname, uint32_t t, uint64_t ne0, uint64_t ne1, const void* host,
+                uint64_t nbytes, bool synth, uint64_t seed, double mul, float constant) {
+  if (!m || !cname) return set_error(RF_ERR_INVALID, "null model or tensor name");
+  const std::string name(cname);
+  DevTensor* slot = nullptr;
+  uint64_t e0 = 0, e1 = 0, bytes = 0;
+  std::string charge;
+  int32_t rc = resolve(m, name, &slot, &e0, &e1, &charge);
+  if (rc) return rc;
+  rc = check_tensor_shape(m, name, t, ne0, ne1, e0, e1, &bytes);
+  if (rc) return rc;
+  if (!synth && nbytes < bytes)
+    return set_error(RF_ERR_INVALID, "tensor '%s' truncated: expected %llu bytes, got %llu", name.c_str(),
+                     (unsigned long long)bytes, (unsigned long long)nbytes);
+  if (synth && (t == T_F16 || t == T_BF16))
+    return set_error(RF_ERR_UNSUPPORTED, "synthetic generator does not emit %s", type_name(t));
+  rf_ctx* ctx = m->ctx;
+  reset_graph(m);
+  hipError_t e = hipStreamSynchronize(ctx->compute);
+  if (e != hipSuccess) return hip_error(e, "hipStreamSynchronize");
+  rc = drop_tensor(m, *slot);
+  if (rc) return rc;
+  const bool widen = (t == T_F16 || t == T_BF16);
+  const uint64_t final_bytes = widen ? ne0 * ne1 * 4 : bytes;
+  void* d = nullptr;
+  rc = charge_alloc(m, charge, final_bytes, &d);
+  if (rc) return rc;
+  if (synth) {
+    uint64_t qk = 1, bs = 4;
+    type_geometry(t, &qk, &bs);
+    const uint64_t nblk = t == T_F32 ? ne0 * ne1 : ne0 / qk * ne1;
+    if (t == T_F32 && !std::isnan(constant)) e = launch_fill(static_cast<float*>(d), constant, ne0 * ne1, ctx->compute);
+    else e = launch_synth(t, seed, 0, nblk, mul, d, ctx->compute);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->compute);
+    if (e != hipSuccess) return hip_error(e, "tensor synthesis");
+  } else if (widen) {
+    void* tmp = nullptr;
+    rc = vram_alloc(ctx, "tmp:load:" + name, bytes, &tmp);
+    if (rc) return rc;
+    rc = staged_upload(ctx, tmp, host, bytes);
+    if (rc == RF_OK) {
+      e = launch_dequant_rows(t, tmp, ne0, ne1, static_cast<float*>(d), nullptr, 0, ctx->compute);
+      if (e == hipSuccess) e = hipStreamSynchronize(ctx->compute);
+      if (e != hipSuccess) rc = hip_error(e, "F16/BF16 widen");
+    }
+    const int32_t rc2 = vram_release(ctx, "tmp:load:" + name);
+    if (rc) return rc;
+    if (rc2) return rc2;
+  } else {
+    rc = staged_upload(ctx, d, host, bytes);
+    if (rc) return rc;
+  }
+  slot->type = widen ? T_F32 : t;
+  slot->ne0 = ne0;
+  slot->ne1 = ne1;
+  slot->nbytes = final_bytes;
+  slot->d = d;
+  slot->charge = charge;
+  return RF_OK;
+}
+
+int32_t check_ready(rf_model* m) {
+  if (!m->token_embd.present()) return set_error(RF_ERR_INVALID, "model tensor 'token_embd.weight' not loaded");
+  if (!m->output_norm.present()) return set_error(RF_ERR_INVALID, "model tensor 'output_norm.weight' not loaded");
+  for (size_t i = 0; i < m->layers.size(); ++i) {
+    Layer& L = m->layers[i];
+    const DevTensor* req[] = {&L.attn_norm, &L.q, &L.k, &L.v, &L.o, &L.ffn_norm, &L.gate, &L.up, &L.down};
+    for (const DevTensor* t : req)
+      if (!t->present()) return set_error(RF_ERR_INVALID, "layer %zu is missing a required tensor", i);
+    const int nb = L.bq.present() + L.bk.present() + L.bv.present();
+    if (nb != 0 && nb != 3)
+      return set_error(RF_ERR_INVALID, "internal error: incomplete Q/K/V bias set survived load of layer %zu", i);
+  }
+  return RF_OK;
+}
+
+#define RF_LAUNCH(expr, what)                               \
+  do {                                                      \
+    hipError_t _e = (expr);                                 \
+    if (_e != hipSuccess) return hip_error(_e, what);       \
+  } while (0)
+
+// The five launch groups of one transformer block (model_executor.rs:102-236).
+// 1. attention RMSNorm + Q/K/V projections (+ bias), segments grouped by type.
+int32_t enqueue_qkv(rf_model* m, size_t li) {
+  const rf_model_config& c = m->cfg;
+  Layer& L = m->layers[li];
+  hipStream_t st = m->ctx->compute;
+  const uint64_t d = c.embedding_length, hd = c.head_dim, qd = c.head_count * hd, kvd = c.head_count_kv * hd;
+  const float* attn_norm = static_cast<const float*>(L.attn_norm.d);
+  const DevTensor* qkv[3] = {&L.q, &L.k, &L.v};
+  float* outs[3] = {m->q, m->k, m->v};
+  const uint64_t rows[3] = {qd, kvd, kvd};
+  int i = 0;
+  while (i < 3) {
+    MvSegDesc segs[3];
+    int n = 0;
+    const uint32_t t = qkv[i]->type;
+    while (i < 3 && qkv[i]->type == t) {
+      segs[n++] = MvSegDesc{qkv[i]->d, nullptr, outs[i], nullptr, rows[i]};
+      ++i;
+    }
+    RF_LAUNCH(launch_matvec_segments(t, segs, n, m->hidden, attn_norm, c.rms_eps, d, EPI_STORE, st), "qkv matvec");
+  }
+  if (L.bq.present()) {
+    RF_LAUNCH(launch_bias_add(m->q, static_cast<const float*>(L.bq.d), qd, st), "bias");
+    RF_LAUNCH(launch_bias_add(m->k, static_cast<const float*>(L.bk.d), kvd, st), "bias");
+    RF_LAUNCH(launch_bias_add(m->v, static_cast<const float*>(L.bv.d), kvd, st), "bias");
+  }
+  return RF_OK;
+}
+
+// 2. RoPE + attention + K/V cache write.
+int32_t enqueue_attention(rf_model* m, size_t li) {
+  const rf_model_config& c = m->cfg;
+  hipStream_t st = m->ctx->compute;
+  const uint64_t hd = c.head_dim, kvd = c.head_count_kv * hd;
+  float* kc = m->k_cache + li * m->kv_cap * kvd;
+  float* vc = m->v_cache + li * m->kv_cap * kvd;
+  AttnArgs a{};
+  a.q = m->q; a.k_hist = kc; a.v_hist = vc; a.k_cur = m->k; a.v_cur = m->v; a.out = m->attn_out;
+  a.ws = m->attn_ws; a.rope = m->rope; a.k_store = kc; a.v_store = vc; a.d_pos = m->d_pos;
+  a.qh = (uint32_t)c.head_count; a.kvh = (uint32_t)c.head_count_kv; a.hd = (uint32_t)hd;
+  a.nsplit = m->nsplit;
+  a.denom = sqrtf((float)hd);
+  RF_LAUNCH(launch_attention(a, st), "attention");
+  return RF_OK;
+}
+
+// 3. o-proj + residual.
+int32_t enqueue_oproj(rf_model* m, size_t li) {
+  const rf_model_config& c = m->cfg;
+  Layer& L = m->layers[li];
+  const uint64_t d = c.embedding_length, qd = c.head_count * c.head_dim;
+  MvSegDesc s{L.o.d, nullptr, m->hidden, m->hidden, d};
+  RF_LAUNCH(launch_matvec_segments(L.o.type, &s, 1, m->attn_out, nullptr, 0.f, qd, EPI_RESIDUAL, m->ctx->compute),
+            "o-proj");
+  return RF_OK;
+}
+
+// 4. ffn RMSNorm + gate/up + SiLU(gate) * up.
+int32_t enqueue_gateup(rf_model* m, size_t li) {
+  const rf_model_config& c = m->cfg;
+  Layer& L = m->layers[li];
+  hipStream_t st = m->ctx->compute;
+  const uint64_t d = c.embedding_length, f = c.feed_forward_length;
+  const float* ffn_norm = static_cast<const float*>(L.ffn_norm.d);
+  if (L.gate.type == L.up.type) {
+    MvSegDesc s{L.gate.d, L.up.d, m->act, nullptr, f};
+    RF_LAUNCH(launch_matvec_segments(L.gate.type, &s, 1, m->hidden, ffn_norm, c.rms_eps, d, EPI_SWIGLU, st),
+              "gate/up");
+  } else {
+    float* up_tmp = m->up_tmp;
+    MvSegDesc sg{L.gate.d, nullptr, m->act, nullptr, f};
+    MvSegDesc su{L.up.d, nullptr, up_tmp, nullptr, f};
+    RF_LAUNCH(launch_matvec_segments(L.gate.type, &sg, 1, m->hidden, ffn_norm, c.rms_eps, d, EPI_STORE, st), "gate");
+    RF_LAUNCH(launch_matvec_segments(L.up.type, &su, 1, m->hidden, ffn_norm, c.rms_eps, d, EPI_STORE, st), "up");
+    RF_LAUNCH(launch_binary(BIN_SWIGLU, m->act, up_tmp, f, m->act, st), "swiglu");
+  }
+  return RF_OK;
+}
+
+// 5. down + residual.
+int32_t enqueue_down(rf_model* m, size_t li) {
+  const rf_model_config& c = m->cfg;
+  Layer& L = m->layers[li];
+  const uint64_t d = c.embedding_length, f = c.feed_forward_length;
+  MvSegDesc s{L.down.d, nullptr, m->hidden, m->hidden, d};
+  RF_LAUNCH(launch_matvec_segments(L.down.type, &s, 1, m->act, nullptr, 0.f, f, EPI_RESIDUAL, m->ctx->compute),
+            "down");
+  return RF_OK;
+}
+
+int32_t enqueue_layer(rf_model* m, size_t li) {
+  int32_t rc;
+  if ((rc = enqueue_qkv(m, li))) return rc;
+  if ((rc = enqueue_attention(m, li))) return rc;
+  if ((rc = enqueue_oproj(m, li))) return rc;
+  if ((rc = enqueue_gateup(m, li))) return rc;
+  return enqueue_down(m, li);
+}
+
+// Algorithmic HBM bytes of one launch group of layer li (weights + vectors read
+// + vectors written); attention counts the K/V history it reads at `hist`.
+uint64_t part_bytes(rf_model* m, int kind, size_t li, uint64_t hist) {
+  const rf_model_config& c = m->cfg;
+  const uint64_t d = c.embedding_length, hd = c.head_dim, qd = c.head_count * hd, kvd = c.head_count_kv * hd;
+  const uint64_t f = c.feed_forward_length, V = c.vocab_size;
+  if (kind == RF_KERNEL_LOGITS) {
+    const DevTensor& w = m->output.present() ? m->output : m->token_embd;
+    return w.nbytes + 4 * (d + d + V);
+  }
+  Layer& L = m->layers[li];
+  switch (kind) {
+    case RF_KERNEL_QKV: return L.q.nbytes + L.k.nbytes + L.v.nbytes + 4 * (d + d + qd + 2 * kvd);
+    case RF_KERNEL_ATTENTION: return 4 * (2 * hist * kvd + 2 * qd + 2 * kvd) + 2 * 4 * kvd;
+    case RF_KERNEL_OPROJ: return L.o.nbytes + 4 * (qd + 2 * d);
+    case RF_KERNEL_GATEUP: return L.gate.nbytes + L.up.nbytes + 4 * (2 * d + f);
+    case RF_KERNEL_DOWN: return L.down.nbytes + 4 * (f + 2 * d);
+    default: return 0;
+  }
+}
+
+// Embedding of *d_token, all layers, position advance.
+int32_t enqueue_forward(rf_model* m) {
+  hipStream_t st = m->ctx->compute;
+  const rf_model_config& c = m->cfg;
+  RF_LAUNCH(launch_dequant_rows(m->token_embd.type, m->token_embd.d, c.embedding_length, 1, m->hidden, m->d_token,
+                                c.vocab_size, st),
+            "embedding");
+  for (size_t li = 0; li < m->layers.size(); ++li) {
+    int32_t rc = enqueue_layer(m, li);
+    if (rc) return rc;
+  }
+  RF_LAUNCH(launch_advance_pos(m->d_pos, st), "advance position");
+  return RF_OK;
+}
+
+// Output norm + output projection (or tied embedding) into m->logits.
+int32_t enqueue_logits(rf_model* m) {
+  const rf_model_config& c = m->cfg;
+  const DevTensor& w = m->output.present() ? m->output : m->token_embd;
+  MvSegDesc s{w.d, nullptr, m->logits, nullptr, c.vocab_size};
+  RF_LAUNCH(launch_matvec_segments(w.type, &s, 1, m->hidden, static_cast<const float*>(m->output_norm.d), c.rms_eps,
+                                   c.embedding_length, EPI_STORE, m->ctx->compute),
+            "logits");
+  return RF_OK;
+}
+
+// One decode step: logits -> argmax (token stored at ring[pos]) -> forward.
+int32_t enqueue_decode_step(rf_model* m) {
+  int32_t rc = enqueue_logits(m);
+  if (rc) return rc;
+  RF_LAUNCH(launch_argmax(m->logits, m->cfg.vocab_size, m->d_token, m->amax_val, m->amax_idx, m->d_ring, m->d_pos,
+                          m->ctx->compute),
+            "argmax");
+  return enqueue_forward(m);
+}
+
+int32_t sync(rf_model* m) {
+  hipError_t e = hipStreamSynchronize(m->ctx->compute);
+  return e == hipSuccess ? RF_OK : hip_error(e, "hipStreamSynchronize");
+}
+
+int32_t forward_token(rf_model* m, uint32_t token, uint64_t pos) {
+  if (pos != m->seq_len)
+    return set_error(RF_ERR_INVALID, "KV position/history mismatch: position %llu requires cache history %llu, got %llu",
+                     (unsigned long long)pos, (unsigned long long)pos, (unsigned long long)m->seq_len);
+  if (m->seq_len >= m->kv_cap) return set_error(RF_ERR_INVALID, "KV cache full");
+  if (token >= m->cfg.vocab_size)
+    return set_error(RF_ERR_INVALID, "token_id %u out of bounds for embedding with %llu rows", token,
+                     (unsigned long long)m->cfg.vocab_size);
+  int32_t rc = check_ready(m);
+  if (rc) return rc;
+  RF_LAUNCH(launch_set_u32(m->d_token, token, m->ctx->compute), "set token");
+  rc = enqueue_forward(m);
+  if (rc) return rc;
+  m->seq_len += 1;
+  return RF_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int32_t rf_model_create(rf_ctx* ctx, const rf_model_config* cfg, uint64_t kv_cap, rf_model** out) {
+  if (!ctx || !cfg || !out) return set_error(RF_ERR_INVALID, "null argument to rf_model_create");
+  const rf_model_config& c = *cfg;
+  if (c.embedding_length == 0 || c.head_count == 0 || c.head_count_kv == 0 || c.head_dim == 0 || c.vocab_size == 0 ||
+      c.block_count == 0 || c.feed_forward_length == 0)
+    return set_error(RF_ERR_INVALID, "model dimensions must be non-zero");
+  if (c.head_count % c.head_count_kv != 0)
+    return set_error(RF_ERR_INVALID, "GQA requires query_heads %llu to be divisible by kv_heads %llu",
+                     (unsigned long long)c.head_count, (unsigned long long)c.head_count_kv);
+  if (c.head_dim % 2 != 0 || c.head_dim > 512)
+    return set_error(RF_ERR_INVALID, "RoPE head dimension must be non-zero and even (<= 512)");
+  if (kv_cap == 0 || kv_cap > c.context_length)
+    return set_error(RF_ERR_INVALID, "KV capacity %llu must be in 1..=context_length %llu",
+                     (unsigned long long)kv_cap, (unsigned long long)c.context_length);
+  if (c.vocab_size > 0xFFFFFFFFull) return set_error(RF_ERR_UNSUPPORTED, "vocabulary exceeds 2^32 entries");
+  rf_model* m = new rf_model();
+  m->ctx = ctx;
+  m->cfg = c;
+  m->kv_cap = kv_cap;
+  m->layers.resize(c.block_count);
+  const uint64_t d = c.embedding_length, qd = c.head_count * c.head_dim, kvd = c.head_count_kv * c.head_dim;
+  const uint64_t f = c.feed_forward_length;
+  const uint64_t kv_bytes = c.block_count * kv_cap * kvd * 4;
+  void* p = nullptr;
+  int32_t rc = charge_alloc(m, "kv_cache:k", kv_bytes, &p);
+  if (rc) { rf_model_destroy(m); return rc; }
+  m->k_cache = static_cast<float*>(p);
+  rc = charge_alloc(m, "kv_cache:v", kv_bytes, &p);
+  if (rc) { rf_model_destroy(m); return rc; }
+  m->v_cache = static_cast<float*>(p);
+  // activations: hidden, q, k, v, attn_out, act, up scratch, logits, final hidden
+  const uint64_t act_floats = d + qd + kvd + kvd + qd + f + f + c.vocab_size + d + 9 * 16;
+  rc = charge_alloc(m, "tmp:forward", act_floats * 4 + 64 * 8, &p);
+  if (rc) { rf_model_destroy(m); return rc; }
+  float* base = static_cast<float*>(p);
+  auto take = [&](uint64_t n) { float* r = base; base += (n + 15) / 16 * 16; return r; };
+  m->hidden = take(d); m->q = take(qd); m->k = take(kvd); m->v = take(kvd); m->attn_out = take(qd);
+  m->act = take(f); m->up_tmp = take(f); m->logits = take(c.vocab_size); m->final_hidden = take(d);
+  // attention workspace: fixed split count for the capacity (graph-friendly)
+  const bool fast = attention_supported((uint32_t)c.head_count, (uint32_t)c.head_count_kv, (uint32_t)c.head_dim);
+  m->nsplit = fast ? attention_splits((uint32_t)kv_cap, (uint32_t)c.head_count_kv) : 1;
+  const uint64_t ws_floats = fast ? (uint64_t)m->nsplit * c.head_count * (c.head_dim + 2) : c.head_count * kv_cap;
+  rc = charge_alloc(m, "workspace:model_attention", ws_floats * 4, &p);
+  if (rc) { rf_model_destroy(m); return rc; }
+  m->attn_ws = static_cast<float*>(p);
+  rc = charge_alloc(m, "workspace:model_state", 256 * 8 + 64 + kv_cap * 4 + 64, &p);
+  if (rc) { rf_model_destroy(m); return rc; }
+  m->amax_val = static_cast<float*>(p);
+  m->amax_idx = reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(p) + 256 * 4);
+  m->d_pos = reinterpret_cast<int32_t*>(static_cast<uint8_t*>(p) + 256 * 8);
+  m->d_token = reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(p) + 256 * 8 + 16);
+  m->d_ring = reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(p) + 256 * 8 + 64);
+  // RoPE table for every position of the cache (host libm, reference expression)
+  const uint64_t rope_floats = kv_cap * c.head_dim;
+  rc = charge_alloc(m, "persistent:rope_table", rope_floats * 4, &p);
+  if (rc) { rf_model_destroy(m); return rc; }
+  m->rope = static_cast<float*>(p);
+  std::vector<float> tab(rope_floats);
+  rope_table_host(tab.data(), 0, kv_cap, (uint32_t)c.head_dim, c.rope_freq_base);
+  rc = staged_upload(ctx, m->rope, tab.data(), rope_floats * 4);
+  if (rc) { rf_model_destroy(m); return rc; }
+  hipError_t e = launch_set_i32(m->d_pos, 0, ctx->compute);
+  if (e == hipSuccess) e = hipStreamSynchronize(ctx->compute);
+  if (e != hipSuccess) { rf_model_destroy(m); return hip_error(e, "model init"); }
+  *out = m;
+  return RF_OK;
+}
+
+void rf_model_destroy(rf_model* m) {
+  if (!m) return;
+  reset_graph(m);
+  hipStreamSynchronize(m->ctx->compute);
+  for (auto it = m->charges.rbegin(); it != m->charges.rend(); ++it) vram_release(m->ctx, *it);
+  delete m;
+}
+
+int32_t rf_model_set_tensor(rf_model* m, const char* name, uint32_t t, uint64_t ne0, uint64_t ne1, const void* host,
+                            uint64_t nbytes) {
+  if (!host) return set_error(RF_ERR_INVALID, "null tensor data");
+  return install(m, name, t, ne0, ne1, host, nbytes, false, 0, 0.0, NAN);
+}
+
+int32_t rf_model_synth_tensor(rf_model* m, const char* name, uint32_t t, uint64_t ne0, uint64_t ne1, uint64_t seed,
+                              double mul, float constant) {
+  return install(m, name, t, ne0, ne1, nullptr, 0, true, seed, mul, constant);
+}
+
+int32_t rf_model_reset(rf_model* m) {
+  if (!m) return set_error(RF_ERR_INVALID, "null model");
+  m->seq_len = 0;
+  hipError_t e = launch_set_i32(m->d_pos, 0, m->ctx->compute);
+  if (e != hipSuccess) return hip_error(e, "reset");
+  return sync(m);
+}
+
+uint64_t rf_model_seq_len(rf_model* m) { return m ? m->seq_len : 0; }
+
+int32_t rf_model_forward(rf_model* m, uint32_t token, uint64_t pos, float* final_hidden) {
+  if (!m) return set_error(RF_ERR_INVALID, "null model");
+  int32_t rc = forward_token(m, token, pos);
+  if (rc) return rc;
+  if (final_hidden) {
+    // output_norm of the last hidden state (streaming_model.rs:1297-1301)
+    RF_LAUNCH(launch_rmsnorm(m->hidden, static_cast<const float*>(m->output_norm.d), m->cfg.embedding_length,
+                             m->cfg.rms_eps, m->final_hidden, m->ctx->compute),
+              "output norm");
+    RF_LAUNCH(hipMemcpyAsync(final_hidden, m->final_hidden, m->cfg.embedding_length * 4, hipMemcpyDeviceToHost,
+                             m->ctx->compute),
+              "download hidden");
+  }
+  return sync(m);
+}
+
+int32_t rf_model_logits(rf_model* m, float* logits) {
+  if (!m || !logits) return set_error(RF_ERR_INVALID, "null argument");
+  if (m->seq_len == 0) return set_error(RF_ERR_INVALID, "logits requested before any forward pass");
+  int32_t rc = enqueue_logits(m);
+  if (rc) return rc;
+  RF_LAUNCH(hipMemcpyAsync(logits, m->logits, m->cfg.vocab_size * 4, hipMemcpyDeviceToHost, m->ctx->compute),
+            "download logits");
+  return sync(m);
+}
+
+int32_t rf_model_generate(rf_model* m, const uint32_t* prompt, uint64_t plen, uint64_t max_tokens, int64_t eos,
+                          uint32_t* out, uint64_t* n_out) {
+  if (!m || (plen && !prompt) || (max_tokens && !out) || !n_out) return set_error(RF_ERR_INVALID, "null argument");
+  *n_out = 0;
+  const uint64_t ctx_len = m->cfg.context_length;
+  // inference.rs:465-476: the request must fit the context.
+  if (plen + max_tokens > ctx_len)
+    return set_error(RF_ERR_INVALID, "prompt (%llu tokens) plus max_tokens (%llu) exceeds context length %llu",
+                     (unsigned long long)plen, (unsigned long long)max_tokens, (unsigned long long)ctx_len);
+  for (uint64_t p = 0; p < plen; ++p) {
+    int32_t rc = forward_token(m, prompt[p], m->seq_len);
+    if (rc) return rc;
+  }
+  uint64_t cur = m->seq_len;
+  uint64_t n = 0;
+  for (uint64_t gi = 0; gi < max_tokens; ++gi) {
+    if (m->seq_len == 0) return set_error(RF_ERR_INVALID, "generation requires a non-empty prompt");
+    int32_t rc = enqueue_logits(m);
+    if (rc) return rc;
+    RF_LAUNCH(launch_argmax(m->logits, m->cfg.vocab_size, m->d_token, m->amax_val, m->amax_idx, nullptr, nullptr,
+                            m->ctx->compute),
+              "argmax");
+    uint32_t next = 0;
+    RF_LAUNCH(hipMemcpyAsync(&next, m->d_token, 4, hipMemcpyDeviceToHost, m->ctx->compute), "download token");
+    rc = sync(m);
+    if (rc) return rc;
+    if (eos >= 0 && (int64_t)next == eos) break;
+    out[n++] = next;
+    *n_out = n;
+    const uint64_t next_pos = cur + 1;
+    if (gi + 1 >= max_tokens) break;        // terminal forward skipped (inference.rs:643-653)
+    if (next_pos >= ctx_len) break;
+    rc = forward_token(m, next, cur);
+    if (rc) return rc;
+    cur = next_pos;
+    if (cur >= ctx_len) break;
+  }
+  return sync(m);
+}
+
+int32_t rf_model_use_graph(rf_model* m, int32_t enable) {
+  if (!m) return set_error(RF_ERR_INVALID, "null model");
+  m->use_graph = enable != 0;
+  if (!m->use_graph) reset_graph(m);
+  return RF_OK;
+}
+
+int32_t rf_model_decode_steps(rf_model* m, uint64_t steps) {
+  if (!m) return set_error(RF_ERR_INVALID, "null model");
+  if (m->seq_len == 0) return set_error(RF_ERR_INVALID, "decode requires a forwarded prompt");
+  if (m->seq_len + steps > m->kv_cap) return set_error(RF_ERR_INVALID, "KV cache full");
+  int32_t rc = check_ready(m);
+  if (rc) return rc;
+  hipStream_t st = m->ctx->compute;
+  if (m->use_graph && !m->graph_exec) {
+    RF_LAUNCH(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal), "begin capture");
+    rc = enqueue_decode_step(m);
+    hipGraph_t g = nullptr;
+    hipError_t e = hipStreamEndCapture(st, &g);
+    if (rc) { if (g) hipGraphDestroy(g); return rc; }
+    if (e != hipSuccess) return hip_error(e, "end capture");
+    m->graph = g;
+    e = hipGraphInstantiate(&m->graph_exec, g, nullptr, nullptr, 0);
+    if (e != hipSuccess) { reset_graph(m); return hip_error(e, "graph instantiate"); }
+  }
+  for (uint64_t s = 0; s < steps; ++s) {
+    if (m->graph_exec) {
+      RF_LAUNCH(hipGraphLaunch(m->graph_exec, st), "graph launch");
+    } else {
+      rc = enqueue_decode_step(m);
+      if (rc) return rc;
+    }
+    m->seq_len += 1;
+  }
+  return RF_OK;
+}
+
+int32_t rf_model_time_kernel(rf_model* m, uint32_t kind, uint32_t reps, float* avg_ms, uint64_t* bytes_per_launch,
+                             uint64_t* launches) {
+  if (!m || !avg_ms || !bytes_per_launch || !launches || reps == 0) return set_error(RF_ERR_INVALID, "null argument");
+  if (kind < RF_KERNEL_QKV || kind > RF_KERNEL_LOGITS)
+    return set_error(RF_ERR_INVALID, "unknown kernel group %u", kind);
+  int32_t rc = check_ready(m);
+  if (rc) return rc;
+  if (kind == RF_KERNEL_ATTENTION && m->seq_len == 0)
+    return set_error(RF_ERR_INVALID, "attention timing needs a forwarded prompt");
+  hipStream_t st = m->ctx->compute;
+  hipEvent_t e0, e1;
+  RF_LAUNCH(hipEventCreate(&e0), "hipEventCreate");
+  RF_LAUNCH(hipEventCreate(&e1), "hipEventCreate");
+  // Attention is timed at the current position (the kernel only reads d_pos).
+  const uint64_t hist = m->seq_len;
+  uint64_t n = 0, bytes = 0;
+  hipError_t e = hipEventRecord(e0, st);
+  for (uint32_t r = 0; r < reps && e == hipSuccess && rc == RF_OK; ++r) {
+    if (kind == RF_KERNEL_LOGITS) {
+      rc = enqueue_logits(m);
+      bytes += part_bytes(m, kind, 0, hist);
+      ++n;
+      continue;
+    }
+    for (size_t li = 0; li < m->layers.size() && rc == RF_OK; ++li) {
+      switch (kind) {
+        case RF_KERNEL_QKV: rc = enqueue_qkv(m, li); break;
+        case RF_KERNEL_ATTENTION: rc = enqueue_attention(m, li); break;
+        case RF_KERNEL_OPROJ: rc = enqueue_oproj(m, li); break;
+        case RF_KERNEL_GATEUP: rc = enqueue_gateup(m, li); break;
+        case RF_KERNEL_DOWN: rc = enqueue_down(m, li); break;
+      }
+      bytes += part_bytes(m, kind, li, hist);
+      ++n;
+    }
+  }
+  if (e == hipSuccess) e = hipEventRecord(e1, st);
+  if (e == hipSuccess) e = hipEventSynchronize(e1);
+  float ms = 0.f;
+  if (e == hipSuccess) e = hipEventElapsedTime(&ms, e0, e1);
+  hipEventDestroy(e0);
+  hipEventDestroy(e1);
+  if (rc) return rc;
+  if (e != hipSuccess) return hip_error(e, "kernel timing");
+  // The attention kernel wrote K/V into slot `hist` of every layer; that slot is
+  // rewritten by the next forward, so the cache contents stay consistent.
+  *avg_ms = ms / (float)n;
+  *bytes_per_launch = bytes / n;
+  *launches = n;
+  return RF_OK;
+}
+
+int32_t rf_model_read_tokens(rf_model* m, uint32_t* out, uint64_t n) {
+  if (!m || (n && !out)) return set_error(RF_ERR_INVALID, "null argument");
+  if (n > m->seq_len) return set_error(RF_ERR_INVALID, "only %llu positions exist", (unsigned long long)m->seq_len);
+  int32_t rc = sync(m);
+  if (rc) return rc;
+  // the token forwarded at position p was chosen from position p-1's logits
+  RF_LAUNCH(hipMemcpy(out, m->d_ring + (m->seq_len - n), n * 4, hipMemcpyDeviceToHost), "download tokens");
+  return RF_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,79 @@
+// rf_runtime.h — host-side runtime internals (context, ledger, errors).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <map>
+#include <mutex>
+#include <string>
+
+#include "../../include/ramforge_hip.h"
+#include "rf_kernels.h"
+
+namespace rf {
+
+// Thread-local last-error message; returns `code` for tail calls.
+int32_t set_error(int32_t code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int32_t hip_error(hipError_t e, const char* what);
+
+// Device-domain MemoryBudget (core/src/memory.rs:30-384): named charges,
+// reserve before allocating, release after the physical free.
+class Ledger {
+ public:
+  explicit Ledger(uint64_t total) : total_(total) {}
+  int32_t allocate(const std::string& name, uint64_t bytes);
+  int32_t release(const std::string& name, uint64_t* released = nullptr);
+  int32_t resize(const std::string& name, uint64_t bytes);
+  int32_t rename_prefix(const std::string& old_prefix, const std::string& new_prefix);
+  bool get(const std::string& name, uint64_t* bytes) const;
+  uint64_t used() const { return used_; }
+  uint64_t total() const { return total_; }
+  uint64_t peak() const { return peak_; }
+
+ private:
+  uint64_t total_;
+  uint64_t used_ = 0;
+  uint64_t peak_ = 0;
+  std::map<std::string, uint64_t> allocs_;
+};
+
+struct Workspace {
+  void* ptr = nullptr;
+  uint64_t bytes = 0;
+};
+
+}  // namespace rf
+
+struct rf_ctx {
+  int device = 0;
+  hipStream_t compute = nullptr;
+  hipStream_t copy = nullptr;
+  rf::Ledger ledger{0};
+  std::mutex mu;
+  std::map<std::string, void*> buffers;  // charge name -> device pointer
+  rf::Workspace attn_ws, scratch_ws;
+  float* amax_val = nullptr;
+  uint32_t* amax_idx = nullptr;
+  void* pinned_stage[2] = {nullptr, nullptr};
+  hipEvent_t stage_ev[2] = {nullptr, nullptr};
+  uint64_t stage_bytes = 0;
+};
+
+namespace rf {
+// Grow a context-owned workspace (charged as `charge`); synchronises the
+// device before releasing a smaller previous buffer.
+int32_t ensure_workspace(rf_ctx* ctx, Workspace& ws, const char* charge, uint64_t bytes);
+// Allocate / free a ledger-charged device buffer.
+int32_t vram_alloc(rf_ctx* ctx, const std::string& charge, uint64_t bytes, void** out);
+int32_t vram_release(rf_ctx* ctx, const std::string& charge);
+// Upload host bytes through the pinned staging buffers on the copy stream.
+int32_t staged_upload(rf_ctx* ctx, void* dst, const void* src, uint64_t bytes);
+inline hipStream_t pick_stream(rf_ctx* ctx, rf_stream_t s) {
+  return s ? static_cast<hipStream_t>(s) : ctx->compute;
+}
+const char* type_name(uint32_t t);
+// Host cos/sin table for RoPE: out[p][i][2] for positions [p0, p0 + np),
+// i < hd/2, with the reference's f32 expression (compute.rs:446-456).
+void rope_table_host(float* out, uint64_t p0, uint64_t np, uint32_t hd, float theta);
+}  // namespace rf

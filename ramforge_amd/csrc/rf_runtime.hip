@@ -1,0 +1,611 @@
+// rf_runtime.hip — context, device-memory ledger and the op entry points of
+// the C ABI (include/ramforge_hip.h).  Host code; kernels live in the other
+// translation units.
+#include "rf_runtime.h"
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <vector>
+
+namespace rf {
+
+static thread_local std::string g_err;
+
+int32_t set_error(int32_t code, const char* fmt, ...) {
+  char buf[1024];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+int32_t hip_error(hipError_t e, const char* what) {
+  return set_error(RF_ERR_HIP, "%s failed: %s (%d)", what, hipGetErrorString(e), (int)e);
+}
+
+const char* type_name(uint32_t t) {
+  switch (t) {
+    case T_F32: return "F32"; case T_F16: return "F16"; case T_BF16: return "BF16";
+    case T_Q4_0: return "Q4_0"; case T_Q5_0: return "Q5_0"; case T_Q8_0: return "Q8_0";
+    case T_Q2_K: return "Q2_K"; case T_Q3_K: return "Q3_K"; case T_Q4_K: return "Q4_K";
+    case T_Q5_K: return "Q5_K"; case T_Q6_K: return "Q6_K"; case T_Q8_K: return "Q8_K";
+    default: return "unknown";
+  }
+}
+
+// ------------------------------------------------------------------ Ledger
+// Messages follow MemoryError (core/src/error.rs:62-90).
+int32_t Ledger::allocate(const std::string& name, uint64_t bytes) {
+  if (bytes == 0) return set_error(RF_ERR_BUDGET, "invalid allocation size: 0 (must be > 0)");
+  if (allocs_.count(name)) return set_error(RF_ERR_BUDGET, "allocation '%s' already exists", name.c_str());
+  const uint64_t avail = total_ - used_;
+  if (bytes > avail)
+    return set_error(RF_ERR_BUDGET,
+                     "insufficient memory: requested %llu bytes for '%s', but only %llu bytes available (total %llu, used %llu)",
+                     (unsigned long long)bytes, name.c_str(), (unsigned long long)avail, (unsigned long long)total_,
+                     (unsigned long long)used_);
+  allocs_[name] = bytes;
+  used_ += bytes;
+  if (used_ > peak_) peak_ = used_;
+  return RF_OK;
+}
+
+int32_t Ledger::release(const std::string& name, uint64_t* released) {
+  auto it = allocs_.find(name);
+  if (it == allocs_.end()) return set_error(RF_ERR_BUDGET, "allocation '%s' not found", name.c_str());
+  if (it->second > used_)
+    return set_error(RF_ERR_BUDGET, "memory accounting underflow while releasing %llu bytes for '%s' (used %llu)",
+                     (unsigned long long)it->second, name.c_str(), (unsigned long long)used_);
+  used_ -= it->second;
+  if (released) *released = it->second;
+  allocs_.erase(it);
+  return RF_OK;
+}
+
+int32_t Ledger::resize(const std::string& name, uint64_t bytes) {
+  if (bytes == 0) return set_error(RF_ERR_BUDGET, "invalid allocation size: 0 (must be > 0)");
+  auto it = allocs_.find(name);
+  if (it == allocs_.end()) return set_error(RF_ERR_BUDGET, "allocation '%s' not found", name.c_str());
+  const uint64_t old = it->second;
+  if (bytes > old) {
+    const uint64_t add = bytes - old, avail = total_ - used_;
+    if (add > avail)
+      return set_error(RF_ERR_BUDGET,
+                       "insufficient memory: requested %llu bytes for '%s', but only %llu bytes available (total %llu, used %llu)",
+                       (unsigned long long)add, name.c_str(), (unsigned long long)avail,
+                       (unsigned long long)total_, (unsigned long long)used_);
+    used_ += add;
+  } else {
+    used_ -= old - bytes;
+  }
+  it->second = bytes;
+  if (used_ > peak_) peak_ = used_;
+  return RF_OK;
+}
+
+int32_t Ledger::rename_prefix(const std::string& op, const std::string& np) {
+  std::vector<std::pair<std::string, std::string>> ren;
+  for (auto& kv : allocs_)
+    if (kv.first.compare(0, op.size(), op) == 0) ren.emplace_back(kv.first, np + kv.first.substr(op.size()));
+  if (ren.empty()) return set_error(RF_ERR_BUDGET, "allocation '%s' not found", op.c_str());
+  for (auto& r : ren)
+    if (allocs_.count(r.second)) return set_error(RF_ERR_BUDGET, "allocation '%s' already exists", r.second.c_str());
+  for (auto& r : ren) {
+    const uint64_t b = allocs_[r.first];
+    allocs_.erase(r.first);
+    allocs_[r.second] = b;
+  }
+  return RF_OK;
+}
+
+bool Ledger::get(const std::string& name, uint64_t* bytes) const {
+  auto it = allocs_.find(name);
+  if (it == allocs_.end()) return false;
+  if (bytes) *bytes = it->second;
+  return true;
+}
+
+// ------------------------------------------------------------ buffers
+int32_t vram_alloc(rf_ctx* ctx, const std::string& charge, uint64_t bytes, void** out) {
+  std::lock_guard<std::mutex> lk(ctx->mu);
+  int32_t rc = ctx->ledger.allocate(charge, bytes);
+  if (rc) return rc;
+  void* p = nullptr;
+  hipError_t e = hipMalloc(&p, bytes);
+  if (e != hipSuccess) {
+    ctx->ledger.release(charge);  // roll back the reservation
+    return hip_error(e, "hipMalloc");
+  }
+  ctx->buffers[charge] = p;
+  *out = p;
+  return RF_OK;
+}
+
+int32_t vram_release(rf_ctx* ctx, const std::string& charge) {
+  std::lock_guard<std::mutex> lk(ctx->mu);
+  auto it = ctx->buffers.find(charge);
+  if (it == ctx->buffers.end()) return set_error(RF_ERR_BUDGET, "allocation '%s' not found", charge.c_str());
+  hipError_t e = hipFree(it->second);  // physical free first (memory.rs:9-15)
+  ctx->buffers.erase(it);
+  const int32_t rc = ctx->ledger.release(charge);
+  if (e != hipSuccess) return hip_error(e, "hipFree");
+  return rc;
+}
+
+int32_t ensure_workspace(rf_ctx* ctx, Workspace& ws, const char* charge, uint64_t bytes) {
+  if (ws.bytes >= bytes) return RF_OK;
+  uint64_t want = bytes < 65536 ? 65536 : bytes;
+  if (ws.ptr) {
+    hipError_t e = hipDeviceSynchronize();  // the old buffer may still be read by queued kernels
+    if (e != hipSuccess) return hip_error(e, "hipDeviceSynchronize");
+    int32_t rc = vram_release(ctx, charge);
+    ws.ptr = nullptr;
+    ws.bytes = 0;
+    if (rc) return rc;
+  }
+  void* p = nullptr;
+  int32_t rc = vram_alloc(ctx, charge, want, &p);
+  if (rc) return rc;
+  ws.ptr = p;
+  ws.bytes = want;
+  return RF_OK;
+}
+
+int32_t staged_upload(rf_ctx* ctx, void* dst, const void* src, uint64_t bytes) {
+  constexpr uint64_t kStage = 64ull << 20;
+  if (!ctx->pinned_stage[0]) {
+    for (int i = 0; i < 2; ++i) {
+      hipError_t e = hipHostMalloc(&ctx->pinned_stage[i], kStage, hipHostMallocDefault);
+      if (e != hipSuccess) return hip_error(e, "hipHostMalloc");
+      e = hipEventCreateWithFlags(&ctx->stage_ev[i], hipEventDisableTiming);
+      if (e != hipSuccess) return hip_error(e, "hipEventCreate");
+    }
+    ctx->stage_bytes = kStage;
+  }
+  const uint8_t* s = static_cast<const uint8_t*>(src);
+  uint8_t* d = static_cast<uint8_t*>(dst);
+  int buf = 0;
+  bool used[2] = {false, false};
+  for (uint64_t off = 0; off < bytes; off += kStage) {
+    const uint64_t n = bytes - off < kStage ? bytes - off : kStage;
+    if (used[buf]) {
+      hipError_t e = hipEventSynchronize(ctx->stage_ev[buf]);
+      if (e != hipSuccess) return hip_error(e, "hipEventSynchronize");
+    }
+    std::memcpy(ctx->pinned_stage[buf], s + off, n);
+    hipError_t e = hipMemcpyAsync(d + off, ctx->pinned_stage[buf], n, hipMemcpyHostToDevice, ctx->copy);
+    if (e != hipSuccess) return hip_error(e, "hipMemcpyAsync");
+    e = hipEventRecord(ctx->stage_ev[buf], ctx->copy);
+    if (e != hipSuccess) return hip_error(e, "hipEventRecord");
+    used[buf] = true;
+    buf ^= 1;
+  }
+  hipError_t e = hipStreamSynchronize(ctx->copy);
+  if (e != hipSuccess) return hip_error(e, "hipStreamSynchronize");
+  return RF_OK;
+}
+
+// RoPE angle table with the reference's expression: angle =
+// theta.powf(-2.0 * i / hd) * pos in f32, then cos / sin (compute.rs:446-456).
+void rope_table_host(float* out, uint64_t p0, uint64_t np, uint32_t hd, float theta) {
+  const uint32_t half = hd / 2;
+  for (uint64_t p = 0; p < np; ++p) {
+    const float pos = (float)(p0 + p);
+    for (uint32_t i = 0; i < half; ++i) {
+      const float angle = powf(theta, -2.0f * (float)i / (float)hd) * pos;
+      out[(p * half + i) * 2] = cosf(angle);
+      out[(p * half + i) * 2 + 1] = sinf(angle);
+    }
+  }
+}
+
+}  // namespace rf
+
+using namespace rf;
+
+#define RF_CHECK_CTX(ctx) \
+  if (!(ctx)) return set_error(RF_ERR_INVALID, "null context")
+#define RF_HIP(call, what)                          \
+  do {                                              \
+    hipError_t _e = (call);                         \
+    if (_e != hipSuccess) return hip_error(_e, what); \
+  } while (0)
+
+extern "C" {
+
+size_t rf_last_error(char* buf, size_t cap) {
+  if (buf && cap) {
+    const size_t n = g_err.size() < cap - 1 ? g_err.size() : cap - 1;
+    std::memcpy(buf, g_err.data(), n);
+    buf[n] = 0;
+  }
+  return g_err.size();
+}
+
+const char* rf_version(void) { return "ramforge_hip 0.1.0 (gfx950)"; }
+
+int32_t rf_ctx_create(int32_t device, uint64_t budget, rf_ctx** out) {
+  if (!out) return set_error(RF_ERR_INVALID, "null output pointer");
+  int n = 0;
+  RF_HIP(hipGetDeviceCount(&n), "hipGetDeviceCount");
+  if (device < 0 || device >= n) return set_error(RF_ERR_INVALID, "HIP device %d out of range (%d devices)", device, n);
+  RF_HIP(hipSetDevice(device), "hipSetDevice");
+  size_t free_b = 0, total_b = 0;
+  RF_HIP(hipMemGetInfo(&free_b, &total_b), "hipMemGetInfo");
+  rf_ctx* c = new rf_ctx();
+  c->device = device;
+  c->ledger = Ledger(budget ? budget : (uint64_t)total_b);
+  hipError_t e = hipStreamCreateWithFlags(&c->compute, hipStreamNonBlocking);
+  if (e == hipSuccess) e = hipStreamCreateWithFlags(&c->copy, hipStreamNonBlocking);
+  if (e != hipSuccess) {
+    delete c;
+    return hip_error(e, "hipStreamCreate");
+  }
+  void* p = nullptr;
+  int32_t rc = vram_alloc(c, "workspace:argmax", 256 * 8 + 64, &p);
+  if (rc) {
+    rf_ctx_destroy(c);
+    return rc;
+  }
+  c->amax_val = static_cast<float*>(p);
+  c->amax_idx = reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(p) + 256 * 4);
+  *out = c;
+  return RF_OK;
+}
+
+void rf_ctx_destroy(rf_ctx* ctx) {
+  if (!ctx) return;
+  hipSetDevice(ctx->device);
+  hipDeviceSynchronize();
+  for (auto& kv : ctx->buffers) hipFree(kv.second);
+  ctx->buffers.clear();
+  for (int i = 0; i < 2; ++i) {
+    if (ctx->pinned_stage[i]) hipHostFree(ctx->pinned_stage[i]);
+    if (ctx->stage_ev[i]) hipEventDestroy(ctx->stage_ev[i]);
+  }
+  if (ctx->compute) hipStreamDestroy(ctx->compute);
+  if (ctx->copy) hipStreamDestroy(ctx->copy);
+  delete ctx;
+}
+
+int32_t rf_ctx_synchronize(rf_ctx* ctx) {
+  RF_CHECK_CTX(ctx);
+  RF_HIP(hipStreamSynchronize(ctx->compute), "hipStreamSynchronize");
+  RF_HIP(hipStreamSynchronize(ctx->copy), "hipStreamSynchronize");
+  return RF_OK;
+}
+
+rf_stream_t rf_ctx_compute_stream(rf_ctx* ctx) { return ctx ? ctx->compute : nullptr; }
+rf_stream_t rf_ctx_copy_stream(rf_ctx* ctx) { return ctx ? ctx->copy : nullptr; }
+
+int32_t rf_ctx_device_info(rf_ctx* ctx, char* name, size_t cap, int32_t* cus) {
+  RF_CHECK_CTX(ctx);
+  hipDeviceProp_t prop;
+  RF_HIP(hipGetDeviceProperties(&prop, ctx->device), "hipGetDeviceProperties");
+  if (name && cap) {
+    snprintf(name, cap, "%s (%s)", prop.name, prop.gcnArchName);
+  }
+  if (cus) *cus = prop.multiProcessorCount;
+  return RF_OK;
+}
+
+int32_t rf_vram_alloc(rf_ctx* ctx, const char* charge, uint64_t bytes, void** out) {
+  RF_CHECK_CTX(ctx);
+  if (!charge || !out) return set_error(RF_ERR_INVALID, "null charge name or output pointer");
+  return vram_alloc(ctx, charge, bytes, out);
+}
+
+int32_t rf_vram_release(rf_ctx* ctx, const char* charge) {
+  RF_CHECK_CTX(ctx);
+  if (!charge) return set_error(RF_ERR_INVALID, "null charge name");
+  return vram_release(ctx, charge);
+}
+
+int32_t rf_vram_rename_prefix(rf_ctx* ctx, const char* op, const char* np) {
+  RF_CHECK_CTX(ctx);
+  if (!op || !np) return set_error(RF_ERR_INVALID, "null prefix");
+  std::lock_guard<std::mutex> lk(ctx->mu);
+  const std::string o(op), n(np);
+  int32_t rc = ctx->ledger.rename_prefix(o, n);
+  if (rc) return rc;
+  std::map<std::string, void*> nb;
+  for (auto& kv : ctx->buffers) {
+    if (kv.first.compare(0, o.size(), o) == 0) nb[n + kv.first.substr(o.size())] = kv.second;
+    else nb[kv.first] = kv.second;
+  }
+  ctx->buffers.swap(nb);
+  return RF_OK;
+}
+
+int32_t rf_vram_charge(rf_ctx* ctx, const char* charge, uint64_t* bytes) {
+  RF_CHECK_CTX(ctx);
+  std::lock_guard<std::mutex> lk(ctx->mu);
+  if (!charge || !ctx->ledger.get(charge, bytes))
+    return set_error(RF_ERR_INVALID, "allocation '%s' not found", charge ? charge : "(null)");
+  return RF_OK;
+}
+
+uint64_t rf_vram_used(rf_ctx* ctx) { return ctx ? ctx->ledger.used() : 0; }
+uint64_t rf_vram_total(rf_ctx* ctx) { return ctx ? ctx->ledger.total() : 0; }
+uint64_t rf_vram_peak(rf_ctx* ctx) { return ctx ? ctx->ledger.peak() : 0; }
+
+int32_t rf_pinned_alloc(rf_ctx* ctx, uint64_t bytes, void** out) {
+  RF_CHECK_CTX(ctx);
+  if (!out || bytes == 0) return set_error(RF_ERR_INVALID, "invalid pinned allocation");
+  RF_HIP(hipHostMalloc(out, bytes, hipHostMallocDefault), "hipHostMalloc");
+  return RF_OK;
+}
+
+int32_t rf_pinned_free(rf_ctx* ctx, void* p) {
+  RF_CHECK_CTX(ctx);
+  if (p) RF_HIP(hipHostFree(p), "hipHostFree");
+  return RF_OK;
+}
+
+int32_t rf_upload_async(rf_ctx* ctx, void* dst, const void* src, uint64_t bytes, rf_stream_t s) {
+  RF_CHECK_CTX(ctx);
+  if (bytes == 0) return RF_OK;
+  if (!dst || !src) return set_error(RF_ERR_INVALID, "null copy pointer");
+  RF_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, pick_stream(ctx, s)), "hipMemcpyAsync");
+  return RF_OK;
+}
+
+int32_t rf_upload(rf_ctx* ctx, void* dst, const void* src, uint64_t bytes) {
+  RF_CHECK_CTX(ctx);
+  if (bytes == 0) return RF_OK;
+  if (!dst || !src) return set_error(RF_ERR_INVALID, "null copy pointer");
+  RF_HIP(hipStreamSynchronize(ctx->compute), "hipStreamSynchronize");
+  RF_HIP(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice), "hipMemcpy");
+  return RF_OK;
+}
+
+int32_t rf_download(rf_ctx* ctx, void* dst, const void* src, uint64_t bytes) {
+  RF_CHECK_CTX(ctx);
+  if (bytes == 0) return RF_OK;
+  if (!dst || !src) return set_error(RF_ERR_INVALID, "null copy pointer");
+  RF_HIP(hipStreamSynchronize(ctx->compute), "hipStreamSynchronize");
+  RF_HIP(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost), "hipMemcpy");
+  return RF_OK;
+}
+
+int32_t rf_memset(rf_ctx* ctx, void* dst, int32_t value, uint64_t bytes) {
+  RF_CHECK_CTX(ctx);
+  if (bytes == 0) return RF_OK;
+  RF_HIP(hipMemsetAsync(dst, value, bytes, ctx->compute), "hipMemsetAsync");
+  RF_HIP(hipStreamSynchronize(ctx->compute), "hipStreamSynchronize");
+  return RF_OK;
+}
+
+int32_t rf_event_create(rf_ctx* ctx, void** ev) {
+  RF_CHECK_CTX(ctx);
+  hipEvent_t e;
+  RF_HIP(hipEventCreate(&e), "hipEventCreate");
+  *ev = e;
+  return RF_OK;
+}
+
+int32_t rf_event_destroy(rf_ctx* ctx, void* ev) {
+  RF_CHECK_CTX(ctx);
+  if (ev) RF_HIP(hipEventDestroy(static_cast<hipEvent_t>(ev)), "hipEventDestroy");
+  return RF_OK;
+}
+
+int32_t rf_event_record(rf_ctx* ctx, void* ev, rf_stream_t s) {
+  RF_CHECK_CTX(ctx);
+  RF_HIP(hipEventRecord(static_cast<hipEvent_t>(ev), pick_stream(ctx, s)), "hipEventRecord");
+  return RF_OK;
+}
+
+int32_t rf_stream_wait_event(rf_ctx* ctx, rf_stream_t s, void* ev) {
+  RF_CHECK_CTX(ctx);
+  RF_HIP(hipStreamWaitEvent(pick_stream(ctx, s), static_cast<hipEvent_t>(ev), 0), "hipStreamWaitEvent");
+  return RF_OK;
+}
+
+int32_t rf_event_elapsed_ms(rf_ctx* ctx, void* a, void* b, float* ms) {
+  RF_CHECK_CTX(ctx);
+  RF_HIP(hipEventElapsedTime(ms, static_cast<hipEvent_t>(a), static_cast<hipEvent_t>(b)), "hipEventElapsedTime");
+  return RF_OK;
+}
+
+int32_t rf_event_synchronize(rf_ctx* ctx, void* ev) {
+  RF_CHECK_CTX(ctx);
+  RF_HIP(hipEventSynchronize(static_cast<hipEvent_t>(ev)), "hipEventSynchronize");
+  return RF_OK;
+}
+
+// ------------------------------------------------------------------ matvec
+int32_t rf_matvec(rf_ctx* ctx, uint32_t t, const void* w, uint64_t w_bytes, uint64_t out_dim, uint64_t in_dim,
+                  const float* x, float* y, uint64_t row_start, uint64_t row_count, rf_stream_t s) {
+  RF_CHECK_CTX(ctx);
+  uint64_t qk = 0, bs = 0;
+  if (!type_geometry(t, &qk, &bs))
+    return set_error(RF_ERR_UNSUPPORTED, "matvec does not support tensor type %s (%u)", type_name(t), t);
+  const char* nm = type_name(t);
+  if (!w || !x || !y) return set_error(RF_ERR_INVALID, "%s matvec received a null pointer", nm);
+  if (in_dim % qk != 0)
+    return set_error(RF_ERR_INVALID, "%s in_dim %llu not divisible by %llu", nm, (unsigned long long)in_dim,
+                     (unsigned long long)qk);
+  if (row_start > out_dim)
+    return set_error(RF_ERR_INVALID, "%s row start %llu exceeds out_dim %llu", nm, (unsigned long long)row_start,
+                     (unsigned long long)out_dim);
+  const uint64_t count = row_count == RF_ALL_ROWS ? out_dim - row_start : row_count;
+  if (row_start + count < row_start) return set_error(RF_ERR_INVALID, "%s row range overflow", nm);
+  if (row_start + count > out_dim)
+    return set_error(RF_ERR_INVALID, "%s row range %llu..%llu exceeds out_dim %llu", nm,
+                     (unsigned long long)row_start, (unsigned long long)(row_start + count),
+                     (unsigned long long)out_dim);
+  const uint64_t rb = in_dim / qk * bs;
+  if (w_bytes < out_dim * rb) {
+    if (t == T_F32)
+      return set_error(RF_ERR_INVALID,
+                       "backend matvec arity mismatch (ggml layout [in, out]): shape [%llu, %llu] requires %llu weight bytes, got %llu",
+                       (unsigned long long)in_dim, (unsigned long long)out_dim, (unsigned long long)(out_dim * rb),
+                       (unsigned long long)w_bytes);
+    return set_error(RF_ERR_INVALID, "%s weight truncated: expected %llu bytes, got %llu", nm,
+                     (unsigned long long)(out_dim * rb), (unsigned long long)w_bytes);
+  }
+  if (count == 0) return RF_OK;
+  if (in_dim == 0) {
+    hipError_t e = launch_fill(y, 0.f, count, pick_stream(ctx, s));
+    return e == hipSuccess ? RF_OK : hip_error(e, "fill");
+  }
+  if (count > 0xFFFFFFFFull || rb > 0xFFFFFFFFull)
+    return set_error(RF_ERR_UNSUPPORTED, "%s matvec shape exceeds 32-bit row indexing", nm);
+  MvSegDesc seg{static_cast<const uint8_t*>(w) + row_start * rb, nullptr, y, nullptr, count};
+  hipError_t e = launch_matvec_segments(t, &seg, 1, x, nullptr, 0.f, in_dim, EPI_STORE, pick_stream(ctx, s));
+  if (e != hipSuccess) return hip_error(e, "matvec launch");
+  return RF_OK;
+}
+
+int32_t rf_dequantize_rows(rf_ctx* ctx, uint32_t t, const void* w, uint64_t w_bytes, uint64_t in_dim,
+                           uint64_t row_start, uint64_t row_count, float* out, rf_stream_t s) {
+  RF_CHECK_CTX(ctx);
+  uint64_t qk = 1, bs = 0;
+  if (t == T_F32) bs = 4;
+  else if (t == T_F16 || t == T_BF16) bs = 2;
+  else if (!type_geometry(t, &qk, &bs))
+    return set_error(RF_ERR_UNSUPPORTED, "decode_row_to_f32: unsupported tensor type %s", type_name(t));
+  const char* nm = type_name(t);
+  if (!w || !out) return set_error(RF_ERR_INVALID, "%s row decode received a null pointer", nm);
+  if (in_dim % qk != 0)
+    return set_error(RF_ERR_INVALID, "%s row size %llu not divisible by block size %llu", nm,
+                     (unsigned long long)in_dim, (unsigned long long)qk);
+  const uint64_t rb = in_dim / qk * bs;
+  const uint64_t need = (row_start + row_count) * rb;
+  if (w_bytes < need)
+    return set_error(RF_ERR_INVALID, "%s row truncated: expected %llu bytes, got %llu", nm,
+                     (unsigned long long)need, (unsigned long long)w_bytes);
+  hipError_t e = launch_dequant_rows(t, static_cast<const uint8_t*>(w) + row_start * rb, in_dim, row_count, out,
+                                     nullptr, 0, pick_stream(ctx, s));
+  if (e != hipSuccess) return hip_error(e, "dequant launch");
+  return RF_OK;
+}
+
+// --------------------------------------------------------------- attention
+int32_t rf_attention_decode(rf_ctx* ctx, const float* q, const float* kh, const float* vh, const float* kc,
+                            const float* vc, uint32_t hist, uint32_t qh, uint32_t kvh, uint32_t hd, float* out,
+                            rf_stream_t s) {
+  RF_CHECK_CTX(ctx);
+  if (qh == 0 || kvh == 0 || hd == 0)
+    return set_error(RF_ERR_INVALID, "attention requires non-zero query heads, KV heads, and head dimension");
+  if (qh % kvh != 0)
+    return set_error(RF_ERR_INVALID, "GQA requires query_heads %u to be divisible by kv_heads %u", qh, kvh);
+  if (!q || !kc || !vc || !out || (hist > 0 && (!kh || !vh)))
+    return set_error(RF_ERR_INVALID, "attention tensor shape mismatch");
+  const uint32_t total = hist + 1;
+  AttnArgs a{};
+  a.q = q; a.k_hist = kh; a.v_hist = vh; a.k_cur = kc; a.v_cur = vc; a.out = out;
+  a.hist = hist; a.qh = qh; a.kvh = kvh; a.hd = hd;
+  a.denom = sqrtf((float)hd);
+  auto aligned = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
+  const bool fast = attention_supported(qh, kvh, hd) && aligned(q) && aligned(kh) && aligned(vh) &&
+                    aligned(kc) && aligned(vc);
+  uint64_t ws_bytes;
+  if (fast) {
+    a.nsplit = attention_splits(total, kvh);
+    ws_bytes = (uint64_t)a.nsplit * qh * (hd + 2) * 4;
+  } else {
+    a.nsplit = 1;
+    ws_bytes = (uint64_t)qh * total * 4;
+  }
+  int32_t rc = ensure_workspace(ctx, ctx->attn_ws, "workspace:attention", ws_bytes);
+  if (rc) return rc;
+  a.ws = static_cast<float*>(ctx->attn_ws.ptr);
+  const hipError_t e = fast ? launch_attention(a, pick_stream(ctx, s)) : launch_attention_naive(a, pick_stream(ctx, s));
+  if (e != hipSuccess) return hip_error(e, "attention launch");
+  return RF_OK;
+}
+
+// --------------------------------------------------------------- elementwise
+int32_t rf_rope(rf_ctx* ctx, float* q, float* k, uint64_t pos, uint32_t hd, uint32_t qh, uint32_t kvh, float theta,
+                rf_stream_t s) {
+  RF_CHECK_CTX(ctx);
+  if (hd == 0 || hd % 2 != 0) return set_error(RF_ERR_INVALID, "RoPE head dimension must be non-zero and even");
+  if (qh == 0 || kvh == 0) return set_error(RF_ERR_INVALID, "RoPE requires non-zero query and KV head counts");
+  if (!std::isfinite(theta) || theta <= 0.f)
+    return set_error(RF_ERR_INVALID, "RoPE frequency base must be finite and positive");
+  if (hd > 512) return set_error(RF_ERR_UNSUPPORTED, "RoPE head dimension %u exceeds 512", hd);
+  if (!q || !k) return set_error(RF_ERR_INVALID, "RoPE shape mismatch: null q or k");
+  RopeCS cs{};
+  rope_table_host(cs.cs, pos, 1, hd, theta);
+  hipError_t e = launch_rope_pair(q, k, cs, hd, qh, kvh, pick_stream(ctx, s));
+  if (e != hipSuccess) return hip_error(e, "rope launch");
+  return RF_OK;
+}
+
+int32_t rf_rmsnorm(rf_ctx* ctx, const float* x, const float* w, uint64_t n, float eps, float* y, rf_stream_t s) {
+  RF_CHECK_CTX(ctx);
+  if (n == 0 || !x || !w || !y)
+    return set_error(RF_ERR_INVALID, "RMSNorm shape mismatch: input %llu, weight %llu, output %llu",
+                     (unsigned long long)n, (unsigned long long)n, (unsigned long long)n);
+  if (!std::isfinite(eps) || eps < 0.f)
+    return set_error(RF_ERR_INVALID, "RMSNorm epsilon must be finite and non-negative");
+  hipError_t e = launch_rmsnorm(x, w, n, eps, y, pick_stream(ctx, s));
+  return e == hipSuccess ? RF_OK : hip_error(e, "rmsnorm launch");
+}
+
+static int32_t binop(rf_ctx* ctx, int op, const float* a, const float* b, uint64_t n, float* out, rf_stream_t s) {
+  RF_CHECK_CTX(ctx);
+  if (n && (!a || !b || !out)) return set_error(RF_ERR_INVALID, "elementwise shape mismatch: null operand");
+  hipError_t e = launch_binary(op, a, b, n, out, pick_stream(ctx, s));
+  return e == hipSuccess ? RF_OK : hip_error(e, "elementwise launch");
+}
+
+int32_t rf_add(rf_ctx* ctx, const float* a, const float* b, uint64_t n, float* out, rf_stream_t s) {
+  return binop(ctx, BIN_ADD, a, b, n, out, s);
+}
+int32_t rf_mul(rf_ctx* ctx, const float* a, const float* b, uint64_t n, float* out, rf_stream_t s) {
+  return binop(ctx, BIN_MUL, a, b, n, out, s);
+}
+int32_t rf_swiglu(rf_ctx* ctx, const float* g, const float* u, uint64_t n, float* out, rf_stream_t s) {
+  return binop(ctx, BIN_SWIGLU, g, u, n, out, s);
+}
+
+int32_t rf_silu(rf_ctx* ctx, const float* x, uint64_t n, float* out, rf_stream_t s) {
+  RF_CHECK_CTX(ctx);
+  if (n && (!x || !out)) return set_error(RF_ERR_INVALID, "SiLU shape mismatch: null operand");
+  hipError_t e = launch_silu(x, n, out, pick_stream(ctx, s));
+  return e == hipSuccess ? RF_OK : hip_error(e, "silu launch");
+}
+
+int32_t rf_softmax(rf_ctx* ctx, float* v, uint64_t n, rf_stream_t s) {
+  RF_CHECK_CTX(ctx);
+  if (n == 0 || !v) return set_error(RF_ERR_INVALID, "softmax requires a non-empty vector");
+  hipError_t e = launch_softmax(v, n, pick_stream(ctx, s));
+  return e == hipSuccess ? RF_OK : hip_error(e, "softmax launch");
+}
+
+int32_t rf_argmax(rf_ctx* ctx, const float* logits, uint64_t n, uint32_t* out, rf_stream_t s) {
+  RF_CHECK_CTX(ctx);
+  if (!out) return set_error(RF_ERR_INVALID, "argmax output is null");
+  if (n == 0) {
+    hipError_t e = launch_set_u32(out, 0, pick_stream(ctx, s));  // sampling.rs:41-43
+    return e == hipSuccess ? RF_OK : hip_error(e, "argmax launch");
+  }
+  if (!logits) return set_error(RF_ERR_INVALID, "argmax logits are null");
+  if (n > 0xFFFFFFFFull) return set_error(RF_ERR_UNSUPPORTED, "argmax over more than 2^32 logits");
+  hipError_t e = launch_argmax(logits, n, out, ctx->amax_val, ctx->amax_idx, nullptr, nullptr, pick_stream(ctx, s));
+  return e == hipSuccess ? RF_OK : hip_error(e, "argmax launch");
+}
+
+int32_t rf_synth_blocks(rf_ctx* ctx, uint32_t t, uint64_t seed, uint64_t first, uint64_t n, double mul, void* dst,
+                        rf_stream_t s) {
+  RF_CHECK_CTX(ctx);
+  if (!type_geometry(t, nullptr, nullptr))
+    return set_error(RF_ERR_UNSUPPORTED, "synthetic generator does not emit %s", type_name(t));
+  if (n && !dst) return set_error(RF_ERR_INVALID, "null synthetic destination");
+  hipError_t e = launch_synth(t, seed, first, n, mul, dst, pick_stream(ctx, s));
+  return e == hipSuccess ? RF_OK : hip_error(e, "synth launch");
+}
+
+uint32_t rf_tune_matvec_tile_bytes(uint32_t bytes) {
+  if (bytes) set_matvec_tile_bytes(bytes);
+  return matvec_tile_bytes();
+}
+
+}  // extern "C"

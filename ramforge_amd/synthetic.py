@@ -1,0 +1,97 @@
+"""Random-init llama models and matvec inputs for the benchmark configurations.
+
+The payloads come from the seeded counter generator (rf_synth_blocks on the
+device; the CPU oracle carries a byte-identical copy), so a model can be built
+directly in VRAM in milliseconds and rebuilt bit-for-bit on the host for the
+CPU baseline and the parity tests.
+
+Scale fields are f16(|n| * scale_mul) with n ~ Irwin-Hall(12) (a normal
+approximation that is exact in binary64 on both sides).
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+# ggml type ids (core/src/types.rs:238-292)
+F32, Q4_0, Q8_0, Q4_K, Q6_K = 0, 2, 8, 12, 14
+
+# Per-format scale multipliers that give weights of roughly N(0, 0.02)
+# magnitude: Q8_0 d = |N(0,0.02)|/127; Q4_0 d = |N(0,0.02)|/8;
+# K-quants scale sub-block factors of up to 63 * 15 or 63 * 32.
+SCALE_MUL = {Q8_0: 0.02 / 127.0, Q4_0: 0.02 / 8.0, Q4_K: 0.02 / (63.0 * 15.0), Q6_K: 0.02 / (127.0 * 32.0),
+             F32: 0.02}
+
+# BASELINE.json configurations
+CONFIG_4 = dict(vocab_size=32000, context_length=4096, embedding_length=2048, block_count=16,
+                feed_forward_length=8192, head_count=32, head_count_kv=8, head_dim=64, rms_eps=1e-5,
+                rope_freq_base=10000.0)
+CONFIG_8B = dict(vocab_size=128256, context_length=8192, embedding_length=4096, block_count=32,
+                 feed_forward_length=14336, head_count=32, head_count_kv=8, head_dim=128, rms_eps=1e-5,
+                 rope_freq_base=10000.0)
+
+
+@dataclass
+class TensorSpec:
+    name: str
+    ggml_type: int
+    ne0: int          # ggml [in, out]
+    ne1: int
+    seed: int
+    scale_mul: float
+    constant: float = float("nan")  # F32 constant fill (norm weights)
+
+
+def llama_specs(cfg: dict, body_type: int = Q8_0, output_type: int | None = None, embd_type: int | None = None,
+                seed: int = 1234) -> list[TensorSpec]:
+    """GGUF tensor list of a random-init llama model."""
+    out_t = body_type if output_type is None else output_type
+    emb_t = body_type if embd_type is None else embd_type
+    d, f, V = cfg["embedding_length"], cfg["feed_forward_length"], cfg["vocab_size"]
+    qd = cfg["head_count"] * cfg["head_dim"]
+    kvd = cfg["head_count_kv"] * cfg["head_dim"]
+    specs = []
+    k = 0
+
+    def add(name, t, ne0, ne1, const=float("nan")):
+        nonlocal k
+        k += 1
+        specs.append(TensorSpec(name, t, ne0, ne1, seed * 1000003 + k, SCALE_MUL.get(t, 0.02), const))
+
+    add("token_embd.weight", emb_t, d, V)
+    add("output_norm.weight", F32, d, 1, 1.0)
+    add("output.weight", out_t, d, V)
+    for i in range(cfg["block_count"]):
+        add(f"blk.{i}.attn_norm.weight", F32, d, 1, 1.0)
+        add(f"blk.{i}.attn_q.weight", body_type, d, qd)
+        add(f"blk.{i}.attn_k.weight", body_type, d, kvd)
+        add(f"blk.{i}.attn_v.weight", body_type, d, kvd)
+        add(f"blk.{i}.attn_output.weight", body_type, qd, d)
+        add(f"blk.{i}.ffn_norm.weight", F32, d, 1, 1.0)
+        add(f"blk.{i}.ffn_gate.weight", body_type, d, f)
+        add(f"blk.{i}.ffn_up.weight", body_type, d, f)
+        add(f"blk.{i}.ffn_down.weight", body_type, f, d)
+    return specs
+
+
+def n_blocks(spec: TensorSpec) -> int:
+    qk = 1 if spec.ggml_type == F32 else (32 if spec.ggml_type in (Q4_0, Q8_0, 6) else 256)
+    return spec.ne0 // qk * spec.ne1
+
+
+def weight_bytes(specs: list[TensorSpec]) -> int:
+    geo = {F32: (1, 4), Q4_0: (32, 18), Q8_0: (32, 34), Q4_K: (256, 144), Q6_K: (256, 210)}
+    tot = 0
+    for s in specs:
+        qk, bs = geo[s.ggml_type]
+        tot += s.ne0 // qk * bs * s.ne1
+    return tot
+
+
+def build_device_model(ctx, cfg: dict, specs: list[TensorSpec], kv_capacity: int):
+    """A GpuLlamaModel with every tensor generated in VRAM."""
+    from . import GpuLlamaModel
+
+    m = GpuLlamaModel(ctx, cfg, kv_capacity)
+    for s in specs:
+        m.synth_tensor(s.name, s.ggml_type, s.ne0, s.ne1, s.seed, s.scale_mul, s.constant)
+    return m

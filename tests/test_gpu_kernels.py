@@ -1,0 +1,358 @@
+"""GPU parity of the HIP kernels against the CPU oracle (through the C ABI).
+
+Bars: dequantisation, RoPE and the synthetic generator are bit-exact; matvec,
+attention and the elementwise ops are within 1e-4 max relative error per
+element (relative to max(|ref|, 1e-3 * max|ref|), see helpers.rel_err) and
+inside the float64 accumulation bound.
+"""
+import numpy as np
+import pytest
+
+from helpers import (F32, Q2_K, Q3_K, Q4_0, Q4_K, Q5_0, Q5_K, Q6_K, Q8_0, Q8_K, QUANT_TYPES, GEOM, NAMES,
+                     assert_close, random_matrix, row_bytes)
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-4
+
+
+def _rf():
+    import ramforge_amd as rf
+
+    return rf
+
+
+def _with_subnormal_scales(t, raw, rng):
+    """Force some f16 scale fields into the subnormal range (the reference
+    decodes them at half their IEEE value)."""
+    qk, bs = GEOM[t]
+    blocks = raw.reshape(-1, bs)
+    offs = {Q8_0: [0], Q4_0: [0], Q5_0: [0], Q4_K: [0, 2], Q5_K: [0, 2], Q6_K: [208], Q2_K: [80, 82],
+            Q3_K: [108]}.get(t, [])
+    for o in offs:
+        sel = rng.random(len(blocks)) < 0.3
+        sub = rng.integers(1, 1024, size=sel.sum()).astype(np.uint16)
+        blocks[sel, o:o + 2] = sub.view(np.uint8).reshape(-1, 2)
+    return blocks.reshape(-1)
+
+
+# ------------------------------------------------------------- dequant
+
+@pytest.mark.parametrize("t", QUANT_TYPES + [F32])
+def test_dequant_rows_bit_exact(ctx, orc, t):
+    rf = _rf()
+    rng = np.random.default_rng(100 + t)
+    in_dim = 512 if GEOM[t][0] == 256 else 96
+    rows = 9
+    raw = _with_subnormal_scales(t, random_matrix(t, rows, in_dim, rng), rng)
+    w = ctx.array(raw)
+    out = ctx.empty((rows, in_dim))
+    rf.dequantize_rows(ctx, t, w, in_dim, 0, rows, out)
+    got = out.numpy()
+    if t == F32:
+        ref = raw.view(np.float32).reshape(rows, in_dim)
+    else:
+        ref = orc.dequantize_rows(t, raw, in_dim, rows)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), NAMES[t]
+    # a row range decodes the same rows
+    out2 = ctx.empty((3, in_dim))
+    rf.dequantize_rows(ctx, t, w, in_dim, 4, 3, out2)
+    assert np.array_equal(out2.numpy().view(np.uint32), ref[4:7].view(np.uint32))
+    for a in (w, out, out2):
+        a.free()
+
+
+def test_dequant_f16_bf16_rows(ctx, orc):
+    rf = _rf()
+    bits = np.arange(65536, dtype=np.uint16)
+    for t in (1, 30):
+        w = ctx.array(bits.view(np.uint8))
+        out = ctx.empty((65536,))
+        rf.dequantize_rows(ctx, t, w, 65536, 0, 1, out)
+        ref = orc.dequantize_row(t, bits.view(np.uint8), 65536)
+        assert np.array_equal(out.numpy().view(np.uint32), ref.view(np.uint32))
+        w.free()
+        out.free()
+
+
+def test_dequant_validation(ctx):
+    rf = _rf()
+    w = ctx.array(np.zeros(34, np.uint8))
+    out = ctx.empty((64,))
+    with pytest.raises(rf.RamforgeError, match="row truncated"):
+        rf.dequantize_rows(ctx, Q8_0, w, 64, 0, 1, out)
+    with pytest.raises(rf.RamforgeError, match="not divisible"):
+        rf.dequantize_rows(ctx, Q8_0, w, 31, 0, 1, out)
+    w.free()
+    out.free()
+
+
+# -------------------------------------------------------------- matvec
+
+def _check_matvec(ctx, orc, t, out_dim, in_dim, seed, row_start=0, row_count=None, threads=16):
+    rf = _rf()
+    rng = np.random.default_rng(seed)
+    raw = random_matrix(t, out_dim, in_dim, rng)
+    x = rng.normal(0, 1, in_dim).astype(np.float32)
+    print(f"  matvec {NAMES[t]} out={out_dim} in={in_dim} rows={row_start}+{row_count} seed={seed}", flush=True)
+    w, xd = ctx.array(raw), ctx.array(x)
+    n = out_dim - row_start if row_count is None else row_count
+    y = ctx.empty((n,))
+    rf.matvec(ctx, t, w, (out_dim, in_dim), xd, y, row_start, row_count)
+    got = y.numpy()
+    if t == F32:
+        ref = orc.backend_matvec_f32(raw.view(np.float32), in_dim, out_dim, x, threads, True)
+        wdec = raw.view(np.float32).reshape(out_dim, in_dim)
+    else:
+        ref = orc.dispatch_matvec(t, raw, in_dim, out_dim, x, threads)
+        wdec = None
+    ref = ref[row_start:row_start + n]
+    err = assert_close(got, ref, TOL, what=f"{NAMES[t]} {out_dim}x{in_dim}")
+    if wdec is None and out_dim * in_dim <= 1 << 22:
+        wdec = orc.dequantize_rows(t, raw, in_dim, out_dim)
+    if wdec is not None:
+        w64 = wdec[row_start:row_start + n].astype(np.float64)
+        ref64 = w64 @ x.astype(np.float64)
+        bound = (np.abs(w64) @ np.abs(x.astype(np.float64))) * 64 * 2.0 ** -24
+        assert np.all(np.abs(got - ref64) <= bound), NAMES[t]
+    for a in (w, xd, y):
+        a.free()
+    return err
+
+
+@pytest.mark.parametrize("t", QUANT_TYPES + [F32])
+def test_matvec_small_shapes(ctx, orc, t):
+    qk = GEOM[t][0]
+    shapes = [(67, 512), (1, 256), (130, 1024)] if qk == 256 else [(67, 96), (3, 32), (130, 1024), (33, 4096)]
+    for i, (o, n) in enumerate(shapes):
+        _check_matvec(ctx, orc, t, o, n, 200 + 10 * t + i)
+
+
+@pytest.mark.parametrize("t", [Q4_0, Q6_K, Q8_0, F32])
+def test_matvec_row_range_is_local(ctx, orc, t):
+    in_dim = 512
+    _check_matvec(ctx, orc, t, 300, in_dim, 300 + t, row_start=128, row_count=77)
+    _check_matvec(ctx, orc, t, 300, in_dim, 310 + t, row_start=299, row_count=None)
+
+
+def test_matvec_f32_any_length_and_wide_rows(ctx, orc):
+    _check_matvec(ctx, orc, F32, 5, 100, 401)     # in_dim not a multiple of 32: rowwise kernel
+    _check_matvec(ctx, orc, Q8_0, 40, 40960, 402)  # > 1024 units per row: rowwise kernel
+    _check_matvec(ctx, orc, Q4_K, 20, 33792, 403)
+
+
+BASELINE_SHAPES = [(Q8_0, 4096, 4096), (Q4_0, 14336, 4096), (Q4_0, 4096, 14336), (Q4_K, 14336, 4096),
+                   (Q4_K, 4096, 14336), (Q6_K, 14336, 4096), (Q6_K, 4096, 14336), (F32, 4096, 4096),
+                   (Q8_0, 14336, 4096), (Q8_0, 4096, 14336)]
+
+
+@pytest.mark.parametrize("t,out_dim,in_dim", BASELINE_SHAPES)
+def test_matvec_baseline_shapes(ctx, orc, t, out_dim, in_dim):
+    _check_matvec(ctx, orc, t, out_dim, in_dim, 500 + t + out_dim % 97)
+
+
+def test_matvec_kats(ctx):
+    """quant.rs:1914-2175 matvec known answers through the HIP path."""
+    rf = _rf()
+    from helpers import h16, q4_0_block, q8_0_block
+
+    cases = [(Q4_0, q4_0_block(0x3C00, [0x99] * 16) * 2, 32, 1.0, 32.0),
+             (Q8_0, q8_0_block(0x3C00, [1] * 32) * 2, 32, 2.0, 64.0),
+             (Q4_K, (h16(0x3C00) + h16(0) + bytes([1] * 12) + bytes([0x11] * 128)) * 2, 256, 1.0, 256.0),
+             (Q5_K, (h16(0x3C00) + h16(0) + bytes([1] * 12) + bytes(32) + bytes([0x11] * 128)) * 2, 256, 1.0,
+              256.0),
+             (Q8_K, (np.float32(1).tobytes() + bytes([1] * 256) + bytes(32)) * 2, 256, 1.0, 256.0)]
+    for t, raw, n, xv, expect in cases:
+        w = ctx.array(np.frombuffer(raw, np.uint8))
+        x = ctx.array(np.full(n, xv, np.float32))
+        y = ctx.empty((2,))
+        rf.matvec(ctx, t, w, (2, n), x, y)
+        assert np.allclose(y.numpy(), expect, atol=1e-3), NAMES[t]
+        for a in (w, x, y):
+            a.free()
+
+
+def test_matvec_validation_keeps_destination(ctx):
+    rf = _rf()
+    w = ctx.array(np.zeros(3 * 34, np.uint8))
+    x = ctx.array(np.ones(32, np.float32))
+    y = ctx.array(np.full(3, 7.0, np.float32))
+    with pytest.raises(rf.RamforgeError, match="not divisible"):
+        rf.matvec(ctx, Q8_0, w, (3, 31), x, y)
+    with pytest.raises(rf.RamforgeError, match="weight truncated"):
+        rf.matvec(ctx, Q8_0, w, (4, 32), x, y)
+    with pytest.raises(rf.RamforgeError, match="exceeds out_dim"):
+        rf.matvec(ctx, Q8_0, w, (3, 32), x, y, row_start=4)
+    with pytest.raises(rf.RamforgeError, match="exceeds out_dim"):
+        rf.matvec(ctx, Q8_0, w, (3, 32), x, y, row_start=2, row_count=2)
+    with pytest.raises(rf.RamforgeError, match="does not support"):
+        rf.matvec(ctx, 3, w, (3, 32), x, y)
+    wf = ctx.array(np.zeros(6, np.float32))
+    with pytest.raises(rf.RamforgeError, match="arity mismatch"):
+        rf.GpuBackend(ctx).matvec(wf, [3, 2], ctx.array(np.ones(2, np.float32)), ctx.array(np.ones(3, np.float32)))
+    assert np.all(y.numpy() == 7.0)
+
+
+def test_matvec_backend_dispatch(ctx, orc):
+    """compute_dispatch::matvec_backend: ggml [in, out] tensors."""
+    rf = _rf()
+    rng = np.random.default_rng(77)
+    backend = rf.GpuBackend(ctx)
+    for t in (Q4_0, Q6_K, Q8_0, F32):
+        in_dim, out_dim = 512, 129
+        raw = random_matrix(t, out_dim, in_dim, rng)
+        x = rng.normal(0, 1, in_dim).astype(np.float32)
+        td = rf.GpuTensor(t, (in_dim, out_dim), ctx.array(raw))
+        y = ctx.empty((out_dim,))
+        rf.matvec_backend(backend, td, ctx.array(x), y)
+        ref = orc.dispatch_matvec(t, raw.view(np.float32) if t == F32 else raw, in_dim, out_dim, x, 4)
+        assert_close(y.numpy(), ref, TOL)
+
+
+# ----------------------------------------------------------- attention
+
+def _attention_case(ctx, orc, hist, qh, kvh, hd, seed, rope_pos=None):
+    rf = _rf()
+    rng = np.random.default_rng(seed)
+    q = rng.normal(0, 1, qh * hd).astype(np.float32)
+    kh = rng.normal(0, 1, max(hist, 1) * kvh * hd).astype(np.float32)[: hist * kvh * hd]
+    vh = rng.normal(0, 1, max(hist, 1) * kvh * hd).astype(np.float32)[: hist * kvh * hd]
+    kc = rng.normal(0, 1, kvh * hd).astype(np.float32)
+    vc = rng.normal(0, 1, kvh * hd).astype(np.float32)
+    print(f"  attention hist={hist} qh={qh} kvh={kvh} hd={hd} rope={rope_pos} seed={seed}", flush=True)
+    dq, dkc = ctx.array(q), ctx.array(kc)
+    if rope_pos is not None:
+        rf.apply_rope(ctx, dq, dkc, rope_pos, hd, qh, kvh, 10000.0)
+        q, kc = orc.rope(q, kc, rope_pos, hd, qh, kvh, 10000.0)
+        assert np.array_equal(dq.numpy().view(np.uint32), q.view(np.uint32)), "RoPE not bit-exact"
+        assert np.array_equal(dkc.numpy().view(np.uint32), kc.view(np.uint32)), "RoPE not bit-exact"
+    dkh = ctx.array(kh if hist else np.zeros(1, np.float32))
+    dvh = ctx.array(vh if hist else np.zeros(1, np.float32))
+    dvc = ctx.array(vc)
+    out = rf.attention_checked(ctx, dq, dkh, dvh, dkc, dvc, hist, qh, kvh, hd)
+    got = out.numpy()
+    ref = orc.attention(q, kh, vh, kc, vc, hist, qh, kvh, hd)
+    assert_close(got, ref, TOL, what=f"attention hist={hist}")
+    for a in (dq, dkc, dkh, dvh, dvc, out):
+        a.free()
+
+
+def test_attention_gqa_kat(ctx):
+    rf = _rf()
+    q = ctx.array(np.array([1.0, 0.0, 0.0, 1.0], np.float32))
+    kc = ctx.array(np.array([1.0, 0.0], np.float32))
+    vc = ctx.array(np.array([2.0, 3.0], np.float32))
+    z = ctx.array(np.zeros(1, np.float32))
+    out = rf.attention_checked(ctx, q, z, z, kc, vc, 0, 2, 1, 2)
+    assert out.numpy().tolist() == [2.0, 3.0, 2.0, 3.0]
+
+
+@pytest.mark.parametrize("hist,qh,kvh,hd", [(0, 4, 2, 8), (7, 6, 3, 10), (0, 32, 8, 128), (1, 32, 8, 128),
+                                            (100, 32, 8, 128), (300, 32, 8, 64), (77, 8, 8, 128),
+                                            (64, 16, 2, 128), (33, 4, 1, 256)])
+def test_attention_shapes(ctx, orc, hist, qh, kvh, hd):
+    _attention_case(ctx, orc, hist, qh, kvh, hd, 600 + hist + qh + hd)
+
+
+@pytest.mark.parametrize("ctx_len", [512, 2048, 8192])
+def test_attention_baseline_config(ctx, orc, ctx_len):
+    """32 q heads, 8 KV heads, hd 128, RoPE theta 1e4 at
+    position hist = L - 1, so L positions are attended."""
+    _attention_case(ctx, orc, ctx_len - 1, 32, 8, 128, 700 + ctx_len, rope_pos=ctx_len - 1)
+
+
+def test_attention_validation(ctx):
+    rf = _rf()
+    z = ctx.array(np.zeros(64, np.float32))
+    with pytest.raises(rf.RamforgeError, match="divisible"):
+        rf.attention_checked(ctx, z, z, z, z, z, 0, 3, 2, 8)
+    with pytest.raises(rf.RamforgeError, match="non-zero"):
+        rf.attention_checked(ctx, z, z, z, z, z, 0, 0, 1, 8)
+
+
+# --------------------------------------------------------- elementwise
+
+def test_rope_bit_exact(ctx, orc):
+    rf = _rf()
+    rng = np.random.default_rng(801)
+    for hd, qh, kvh in ((128, 32, 8), (64, 4, 4), (2, 1, 1)):
+        for pos in (0, 1, 255, 8191):
+            q = rng.normal(0, 1, qh * hd).astype(np.float32)
+            k = rng.normal(0, 1, kvh * hd).astype(np.float32)
+            dq, dk = ctx.array(q), ctx.array(k)
+            rf.apply_rope(ctx, dq, dk, pos, hd, qh, kvh, 10000.0)
+            rq, rk = orc.rope(q, k, pos, hd, qh, kvh, 10000.0)
+            assert np.array_equal(dq.numpy().view(np.uint32), rq.view(np.uint32)), (hd, pos)
+            assert np.array_equal(dk.numpy().view(np.uint32), rk.view(np.uint32)), (hd, pos)
+            dq.free()
+            dk.free()
+
+
+def test_elementwise_ops(ctx, orc):
+    rf = _rf()
+    rng = np.random.default_rng(802)
+    for n in (2, 4096, 14336):
+        a = rng.normal(0, 2, n).astype(np.float32)
+        b = rng.normal(1, 0.5, n).astype(np.float32)
+        da, db, do = ctx.array(a), ctx.array(b), ctx.empty((n,))
+        rf.rmsnorm(ctx, da, db, n, 1e-5, do)
+        assert_close(do.numpy(), orc.rms_norm(a, b, 1e-5), 1e-5)
+        rf.add(ctx, da, db, n, do)
+        assert np.array_equal(do.numpy(), orc.add(a, b))
+        rf.mul(ctx, da, db, n, do)
+        assert np.array_equal(do.numpy(), orc.mul(a, b))
+        rf.silu(ctx, da, n, do)
+        assert_close(do.numpy(), orc.silu(a), 1e-6)
+        rf.swiglu(ctx, da, db, n, do)
+        assert_close(do.numpy(), orc.swiglu(a, b), 1e-6)
+        rf.softmax(ctx, da, n)
+        assert_close(da.numpy(), orc.softmax(a), 1e-5)
+        for x in (da, db, do):
+            x.free()
+
+
+def test_argmax_rules(ctx, orc):
+    rf = _rf()
+    rng = np.random.default_rng(803)
+    big = rng.normal(0, 1, 128256).astype(np.float32)
+    big[[5000, 90000]] = 10.0
+    cases = [[1.0, 3.0, 3.0, 2.0], [float("nan"), 5.0, 6.0], [1.0, float("nan"), 6.0, 6.0], [float("-inf")] * 4,
+             big, rng.normal(0, 1, 32000).astype(np.float32)]
+    out = ctx.empty((1,), np.uint32)
+    for c in cases:
+        x = ctx.array(np.asarray(c, np.float32))
+        rf.argmax(ctx, x, len(c), out)
+        assert int(out.numpy()[0]) == orc.argmax(c)
+        x.free()
+
+
+@pytest.mark.parametrize("t", QUANT_TYPES + [F32])
+def test_synth_matches_host_generator(ctx, orc, t):
+    rf = _rf()
+    bs = GEOM[t][1]
+    for first, n, mul in ((0, 1000, 0.02 / 127), (123456, 777, 0.02)):
+        d = ctx.empty((n * bs,), np.uint8)
+        ctx.synth_blocks(t, 99 + t, first, n, mul, d)
+        assert np.array_equal(d.numpy(), orc.synth_blocks(t, 99 + t, first, n, mul)), NAMES[t]
+        d.free()
+
+
+# --------------------------------------------------------------- ledger
+
+def test_vram_ledger_semantics(ctx):
+    rf = _rf()
+    with rf.Context(0, vram_budget_bytes=1 << 20) as c:
+        base = c.vram_used
+        a = c.alloc(1000, "layer:0:attn_q.weight")
+        assert c.charge("layer:0:attn_q.weight") == 1000 and c.vram_used == base + 1000
+        with pytest.raises(rf.RamforgeError, match="already exists"):
+            c.alloc(10, "layer:0:attn_q.weight")
+        with pytest.raises(rf.RamforgeError, match="insufficient memory"):
+            c.alloc(1 << 20, "layer:1:ffn_up.weight")
+        assert c.vram_used == base + 1000  # the refused charge was rolled back
+        c.rename_prefix("layer:0:", "cache:layer:0:")
+        assert c.charge("cache:layer:0:attn_q.weight") == 1000 and c.charge("layer:0:attn_q.weight") is None
+        a.charge = "cache:layer:0:attn_q.weight"
+        a.free()
+        assert c.vram_used == base and c.vram_peak >= base + 1000
+        with pytest.raises(rf.RamforgeError, match="not found"):
+            rf._lib.check(c.lib.rf_vram_release(c.handle, b"layer:9:nothing"))
