@@ -188,7 +188,7 @@ int32_t rf_argmax(rf_ctx *ctx, const float *logits, uint64_t n, uint32_t *out_in
  * Q8_0 codes are uniform in [-127, 127]; the other codes are uniform bytes.
  * Bench and test input generator; it has no counterpart in the reference. */
 int32_t rf_synth_blocks(rf_ctx *ctx, uint32_t ggml_type, uint64_t seed, uint64_t first_block, uint64_t n_blocks,
-                        double scale_mul, void *dst, rf_stream_t stream);
+                        double scale_mul, void *dst, uint64_t dst_bytes, rf_stream_t stream);
 
 /* ---------------------------------------------------------------- model */
 
@@ -273,8 +273,12 @@ int32_t rf_model_time_kernel(rf_model *model, uint32_t kind, uint32_t reps, floa
 
 /* ------------------------------------------------------------- tuning */
 
-/* LDS bytes per matvec tile (4096..61440); returns the value in effect. */
+/* LDS bytes per one-shot matvec tile (4096..61440); returns the value in effect. */
 uint32_t rf_tune_matvec_tile_bytes(uint32_t bytes);
+/* Matvec kernel family: 1 = persistent streaming kernel where rows and bases
+ * are 16-byte aligned (default), 0 = one-shot tile kernel everywhere, other
+ * values only query.  Returns the mode in effect (process-wide). */
+int32_t rf_tune_matvec_kernel(int32_t mode);
 
 #ifdef __cplusplus
 }

@@ -200,7 +200,7 @@ class Context:
     def synth_blocks(self, ggml_type: int, seed: int, first_block: int, n_blocks: int, scale_mul: float,
                      dst: DeviceArray, stream=None) -> None:
         _lib.check(self.lib.rf_synth_blocks(self.handle, ggml_type, seed, first_block, n_blocks, scale_mul,
-                                            _ptr(dst), stream))
+                                            _ptr(dst), dst.nbytes, stream))
 
     # events
     def event(self):
@@ -439,8 +439,14 @@ class GpuLlamaModel:
 
 
 def tune_matvec_tile_bytes(nbytes: int = 0) -> int:
-    """Set (nbytes > 0) and return the LDS bytes per matvec tile."""
+    """Set (nbytes > 0) and return the LDS bytes per one-shot matvec tile."""
     return _lib.load().rf_tune_matvec_tile_bytes(nbytes)
+
+
+def tune_matvec_kernel(mode: int = -1) -> int:
+    """1: persistent streaming matvec (default), 0: one-shot tile kernel;
+    -1 queries.  Returns the mode in effect."""
+    return _lib.load().rf_tune_matvec_kernel(mode)
 
 
 # Fail loudly at import if the HIP library was not built.

@@ -23,11 +23,16 @@ struct MvArgs {
   float eps;
   uint32_t in_dim, units, rg, rows_per_tile, row_bytes, tile_stride;
   const uint8_t* w_up;
+  uint32_t ntiles;      // persistent kernel: tiles over all segments
+  uint32_t red_offset;  // persistent kernel: LDS byte offset of the reduction area
 };
 
 struct MvPlan {
   bool tiled;
   uint32_t units, rg, rows_per_tile, threads, row_bytes, tile_stride, lds_bytes;
+  // persistent streaming kernel (chosen when rows and bases are 16-byte aligned)
+  bool stream;
+  uint32_t s_rows_per_tile, s_threads, s_lds_bytes, s_red_offset, s_wgs_per_cu;
 };
 
 // One output segment of a (possibly multi-matrix) matvec launch.  All
@@ -44,6 +49,8 @@ bool type_geometry(uint32_t t, uint64_t* qk, uint64_t* bs);
 MvPlan plan_matvec(uint32_t t, uint64_t in_dim, bool dual);
 void set_matvec_tile_bytes(uint32_t bytes);
 uint32_t matvec_tile_bytes();
+void set_matvec_stream(bool on);
+bool matvec_stream();
 hipError_t launch_matvec_segments(uint32_t t, const MvSegDesc* segs, int nseg, const float* x,
                                   const float* norm_w, float eps, uint64_t in_dim, int epi,
                                   hipStream_t st);

@@ -22,6 +22,8 @@
 //     a dual gate/up tile with a SiLU(gate)*up epilogue.
 #include "rf_kernels.h"
 
+#include <mutex>
+
 namespace rf {
 
 // Copy `bytes` from global `src` to LDS `dst` (16-byte aligned), all threads.
@@ -33,12 +35,12 @@ __device__ __forceinline__ void copy_tile(uint8_t* __restrict__ dst, const uint8
     const u32x4* s4 = reinterpret_cast<const u32x4*>(src);
     u32x4* d4 = reinterpret_cast<u32x4*>(dst);
     constexpr int UNR = 8;
-    for (uint32_t base = 0; base < n16; base += nth * UNR) {
+    for (uint32_t base = 0; n16 && base < n16; base += nth * UNR) {
       u32x4 r[UNR];
 #pragma unroll
-      for (int j = 0; j < UNR; ++j) {
-        const uint32_t i = base + j * nth + tid;
-        if (i < n16) r[j] = __builtin_nontemporal_load(s4 + i);
+      for (int j = 0; j < UNR; ++j) {  // unconditional (clamped) loads keep them all in flight
+        const uint32_t i = min(base + j * nth + tid, n16 - 1u);
+        r[j] = __builtin_nontemporal_load(s4 + i);
       }
 #pragma unroll
       for (int j = 0; j < UNR; ++j) {
@@ -58,22 +60,44 @@ __device__ __forceinline__ void copy_tile(uint8_t* __restrict__ dst, const uint8
   }
 }
 
-__device__ __forceinline__ void load_xunit(XUnit& xu, const float* __restrict__ x, uint32_t u, bool active) {
-  if (!active) {
+// x[32u .. 32u+31] with eight unconditional 16-byte loads (u < units always
+// holds, so every thread reads in bounds).  The host guarantees 16-byte
+// aligned x and norm weights for the tiled kernels: a data-dependent branch
+// around these loads makes the compiler drain the memory counter behind the
+// in-flight tile loads, which costs more than the whole decode.
+__device__ __forceinline__ void load_xunit(XUnit& xu, const float* __restrict__ x, uint32_t u) {
+  const float4* p = reinterpret_cast<const float4*>(x + 32u * u);
 #pragma unroll
-    for (int i = 0; i < 32; ++i) xu.v[i] = 0.f;
-    return;
+  for (int i = 0; i < 8; ++i) {
+    const float4 v = p[i];
+    xu.v[4 * i] = v.x; xu.v[4 * i + 1] = v.y; xu.v[4 * i + 2] = v.z; xu.v[4 * i + 3] = v.w;
   }
-  const float* p = x + 32u * u;
-  if ((reinterpret_cast<uintptr_t>(p) & 15u) == 0) {
+}
+
+// RMSNorm prologue (core/src/compute.rs:291-319: x / sqrt(mean(x^2) + eps) * w),
+// with the reciprocal of the rms.  Threads of row group 0 hold every unit of x
+// exactly once, so sum(x^2) is a workgroup reduction of register values.
+__device__ __forceinline__ void norm_xunit(XUnit& xu, const float* __restrict__ nw, uint32_t u, bool first_group,
+                                           uint32_t in_dim, float eps, float* wsum, uint32_t tid, uint32_t nth) {
+  float ss = 0.f;
+  if (first_group) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const float4 v = reinterpret_cast<const float4*>(p)[i];
-      xu.v[4 * i] = v.x; xu.v[4 * i + 1] = v.y; xu.v[4 * i + 2] = v.z; xu.v[4 * i + 3] = v.w;
-    }
-  } else {
+    for (int i = 0; i < 32; ++i) ss = fmaf(xu.v[i], xu.v[i], ss);
+  }
+  ss = rf_wave_sum(ss);
+  if ((tid & 63u) == 0) wsum[tid >> 6] = ss;
+  __syncthreads();
+  float tot = 0.f;
+  for (uint32_t i = 0; i < (nth >> 6); ++i) tot += wsum[i];
+  const float inv = 1.0f / sqrtf(tot / (float)in_dim + eps);
+  const float4* w4 = reinterpret_cast<const float4*>(nw + 32u * u);
 #pragma unroll
-    for (int i = 0; i < 32; ++i) xu.v[i] = p[i];
+  for (int i = 0; i < 8; ++i) {
+    const float4 w = w4[i];
+    xu.v[4 * i] = xu.v[4 * i] * inv * w.x;
+    xu.v[4 * i + 1] = xu.v[4 * i + 1] * inv * w.y;
+    xu.v[4 * i + 2] = xu.v[4 * i + 2] * inv * w.z;
+    xu.v[4 * i + 3] = xu.v[4 * i + 3] * inv * w.w;
   }
 }
 
@@ -112,30 +136,9 @@ __global__ __launch_bounds__(1024) void matvec_tiled(MvArgs a) {
   const uint32_t u = tid % units, g = tid / units;
   const bool active = g < a.rg;
   XUnit xu;
-  load_xunit(xu, a.x, u, active);
-
-  if (a.norm_w != nullptr) {
-    // RMSNorm prologue (core/src/compute.rs:291-319: x / sqrt(mean(x^2) + eps) * w).
-    float ss = 0.f;
-    if (active && g == 0) {
-#pragma unroll
-      for (int i = 0; i < 32; ++i) ss = fmaf(xu.v[i], xu.v[i], ss);
-    }
-    ss = rf_wave_sum(ss);
-    if ((tid & 63u) == 0) wsum[tid >> 6] = ss;
-    __syncthreads();
-    float tot = 0.f;
-    for (uint32_t i = 0; i < (nth >> 6); ++i) tot += wsum[i];
-    const float rms = sqrtf(tot / (float)a.in_dim + a.eps);
-    const float inv = 1.0f / rms;
-    if (active) {
-      const float* nw = a.norm_w + 32u * u;
-#pragma unroll
-      for (int i = 0; i < 32; ++i) xu.v[i] = xu.v[i] * inv * nw[i];
-    }
-  } else {
-    __syncthreads();
-  }
+  load_xunit(xu, a.x, u);
+  if (a.norm_w != nullptr) norm_xunit(xu, a.norm_w, u, active && g == 0, a.in_dim, a.eps, wsum, tid, nth);
+  else __syncthreads();
   finish_xunit(xu);
 
   const uint32_t blk = (u / UPB) * Fmt<T>::BS, sub = u % UPB;
@@ -181,6 +184,138 @@ __global__ __launch_bounds__(1024) void matvec_tiled(MvArgs a) {
         // silu_reference then mul_reference (compute.rs:337-350, 329-335)
         const float sg = v / (1.0f + expf(-v));
         y[o] = sg * v2;
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Persistent streaming variant (the decode hot path).  A grid of about
+// (CUs x workgroups-per-CU) workgroups walks the tiles of all segments; each
+// workgroup loads its x slice (and applies the fused RMSNorm) once, and keeps
+// the next tile's 16-byte words in registers while it decodes the current
+// tile from LDS, so every workgroup always has one tile of HBM reads in
+// flight.  Requires 16-byte aligned rows (row_bytes % 16 == 0) and weight
+// bases; the dual (gate/up) tile is the gate rows followed by the up rows.
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+constexpr int PF = 8;  // prefetch words (16 B) per thread per tile
+
+struct TileRef {
+  const u32x4* p0;  // first range (gate / plain rows)
+  const u32x4* p1;  // second range (up rows) or null
+  uint32_t n0, n;   // words in the first range, total words
+  uint32_t r0, nrows;
+  int seg;
+};
+
+__device__ __forceinline__ TileRef tile_ref(const MvArgs& a, uint32_t tile, bool dual) {
+  TileRef t;
+  t.seg = (a.nseg > 2 && tile >= a.seg[2].tile_begin) ? 2 : ((a.nseg > 1 && tile >= a.seg[1].tile_begin) ? 1 : 0);
+  const uint8_t* w = t.seg == 0 ? a.seg[0].w : (t.seg == 1 ? a.seg[1].w : a.seg[2].w);
+  const uint32_t rows = t.seg == 0 ? a.seg[0].rows : (t.seg == 1 ? a.seg[1].rows : a.seg[2].rows);
+  const uint32_t tb = t.seg == 0 ? a.seg[0].tile_begin : (t.seg == 1 ? a.seg[1].tile_begin : a.seg[2].tile_begin);
+  t.r0 = (tile - tb) * a.rows_per_tile;
+  t.nrows = min(a.rows_per_tile, rows - t.r0);
+  const uint32_t words = t.nrows * a.row_bytes / 16u;
+  t.p0 = reinterpret_cast<const u32x4*>(w + (size_t)t.r0 * a.row_bytes);
+  t.n0 = words;
+  t.p1 = dual ? reinterpret_cast<const u32x4*>(a.w_up + (size_t)t.r0 * a.row_bytes) : nullptr;
+  t.n = dual ? 2 * words : words;
+  return t;
+}
+
+// Branch-free on purpose: every slot issues one load (indices past the tile
+// are clamped to its last word and never stored).  A guarded load, or an
+// if/else between the gate and up ranges, makes the compiler drain the memory
+// counter before each load and serialises the prefetch.
+__device__ __forceinline__ void tile_prefetch(u32x4 (&r)[PF], const TileRef& t, uint32_t tid, uint32_t nth) {
+#pragma unroll
+  for (int j = 0; j < PF; ++j) {
+    const uint32_t i = min(j * nth + tid, t.n - 1u);
+    const u32x4* src = i < t.n0 ? t.p0 + i : t.p1 + (i - t.n0);
+    r[j] = __builtin_nontemporal_load(src);
+  }
+}
+
+__device__ __forceinline__ void tile_store(const u32x4 (&r)[PF], uint8_t* lds, uint32_t n, uint32_t tid,
+                                           uint32_t nth) {
+  u32x4* d = reinterpret_cast<u32x4*>(lds);
+#pragma unroll
+  for (int j = 0; j < PF; ++j) {
+    const uint32_t i = j * nth + tid;
+    if (i < n) d[i] = r[j];
+  }
+}
+
+template <uint32_t T, int EPI>
+__global__ __launch_bounds__(512) void matvec_stream(MvArgs a) {
+  extern __shared__ __align__(16) uint8_t lds[];
+  __shared__ float wsum[8];
+  constexpr bool DUAL = EPI == EPI_SWIGLU;
+  constexpr uint32_t UPB = Fmt<T>::QK / 32u;
+  const uint32_t tid = threadIdx.x, nth = blockDim.x;
+  const uint32_t ntiles = a.ntiles;
+  uint32_t tile = blockIdx.x;
+  u32x4 pf[PF];
+  TileRef cur{};
+  if (tile < ntiles) {
+    cur = tile_ref(a, tile, DUAL);
+    tile_prefetch(pf, cur, tid, nth);
+  }
+
+  const uint32_t units = a.units;
+  const uint32_t u = tid % units, g = tid / units;
+  const bool active = g < a.rg;
+  XUnit xu;
+  load_xunit(xu, a.x, u);
+  if (a.norm_w != nullptr) norm_xunit(xu, a.norm_w, u, active && g == 0, a.in_dim, a.eps, wsum, tid, nth);
+  finish_xunit(xu);
+
+  const uint32_t row_bytes = a.row_bytes;
+  const uint32_t blk = (u / UPB) * Fmt<T>::BS, sub = u % UPB;
+  float* red = reinterpret_cast<float*>(lds + a.red_offset);
+  const uint32_t lane = tid & 63u, wave = tid >> 6, nwaves = nth >> 6;
+  constexpr int MAXR = 8;
+
+  for (; tile < ntiles; tile += gridDim.x) {
+    tile_store(pf, lds, cur.n, tid, nth);
+    __syncthreads();
+    const TileRef t = cur;
+    const uint32_t next = tile + gridDim.x;
+    if (next < ntiles) {
+      cur = tile_ref(a, next, DUAL);
+      tile_prefetch(pf, cur, tid, nth);
+    }
+    const uint32_t nrows = t.nrows;
+#pragma unroll
+    for (int k = 0; k < MAXR; ++k) {
+      const uint32_t r = g + k * a.rg;
+      if (active && r < nrows) {
+        red[r * units + u] = Fmt<T>::dot(lds, r * row_bytes + blk, sub, xu);
+        if (DUAL) red[(nrows + r) * units + u] = Fmt<T>::dot(lds + nrows * row_bytes, r * row_bytes + blk, sub, xu);
+      }
+    }
+    __syncthreads();
+    float* y = t.seg == 0 ? a.seg[0].y : (t.seg == 1 ? a.seg[1].y : a.seg[2].y);
+    const float* res = t.seg == 0 ? a.seg[0].res : (t.seg == 1 ? a.seg[1].res : a.seg[2].res);
+    for (uint32_t r = wave; r < nrows; r += nwaves) {
+      float v = 0.f, v2 = 0.f;
+      for (uint32_t i = lane; i < units; i += 64u) {
+        v += red[r * units + i];
+        if (DUAL) v2 += red[(nrows + r) * units + i];
+      }
+      v = rf_wave_sum(v);
+      if (DUAL) v2 = rf_wave_sum(v2);
+      if (lane == 0) {
+        const uint32_t o = t.r0 + r;
+        if (EPI == EPI_STORE) {
+          y[o] = v;
+        } else if (EPI == EPI_RESIDUAL) {
+          y[o] = res[o] + v;
+        } else {
+          const float sg = v / (1.0f + expf(-v));
+          y[o] = sg * v2;
+        }
       }
     }
   }
@@ -252,9 +387,12 @@ bool type_geometry(uint32_t t, uint64_t* qk, uint64_t* bs) {
   return true;
 }
 
-static uint32_t g_tile_target = 32768;  // LDS bytes per matvec tile (tunable)
+static uint32_t g_tile_target = 32768;  // LDS bytes per one-shot matvec tile (tunable)
+static bool g_stream_enabled = true;    // persistent streaming kernel where eligible
 void set_matvec_tile_bytes(uint32_t bytes) { g_tile_target = bytes < 4096 ? 4096 : (bytes > 61440 ? 61440 : bytes); }
 uint32_t matvec_tile_bytes() { return g_tile_target; }
+void set_matvec_stream(bool on) { g_stream_enabled = on; }
+bool matvec_stream() { return g_stream_enabled; }
 
 MvPlan plan_matvec(uint32_t t, uint64_t in_dim, bool dual) {
   MvPlan p{};
@@ -267,19 +405,73 @@ MvPlan plan_matvec(uint32_t t, uint64_t in_dim, bool dual) {
   }
   p.tiled = true;
   p.units = (uint32_t)units;
-  p.rg = units >= 256 ? 1u : (uint32_t)(256 / units);
   const uint64_t per_matrix = dual ? g_tile_target / 2 : g_tile_target;
-  uint64_t rpt = per_matrix / (p.rg * rb);
-  if (rpt < 1) rpt = 1;
-  if (rpt > 8) rpt = 8;
+  uint64_t max_rows = per_matrix / rb;
+  if (max_rows < 1) max_rows = 1;
+  uint64_t rg = units >= 256 ? 1 : 256 / units;
+  uint64_t rpt;
+  if (rg > max_rows) {  // short rows but a small tile budget: fewer row groups
+    rg = max_rows;
+    rpt = 1;
+  } else {
+    rpt = max_rows / rg;
+    if (rpt > 8) rpt = 8;
+  }
+  p.rg = (uint32_t)rg;
   p.rows_per_tile = (uint32_t)(p.rg * rpt);
   p.threads = (uint32_t)(((units * p.rg) + 63) / 64 * 64);
   p.tile_stride = (uint32_t)((p.rows_per_tile * rb + 15) / 16 * 16);
   const uint64_t tile = (uint64_t)p.tile_stride * (dual ? 2 : 1);
   const uint64_t red = (uint64_t)p.rows_per_tile * units * 4 * (dual ? 2 : 1);
-  p.lds_bytes = (uint32_t)((tile > red ? tile : red) + 16);
+  const uint64_t lds = (tile > red ? tile : red) + 16;
+  if (lds > 65536 - 512) {  // with the static LDS it would not fit 64 KiB: rowwise kernel
+    p.tiled = false;
+    return p;
+  }
+  p.lds_bytes = (uint32_t)lds;
+
+  // Persistent streaming plan: one prefetch of PF 16-byte words per thread
+  // bounds the tile; aim for >= 2 workgroups per CU (160 KiB LDS per CU).
+  p.stream = false;
+  const uint64_t sthreads = (units * rg + 63) / 64 * 64;
+  if (rb % 16 == 0 && sthreads <= 512) {
+    uint64_t tile_cap = 16ull * PF * sthreads;
+    if (tile_cap > 57344) tile_cap = 57344;
+    const uint64_t per_row = rb * (dual ? 2 : 1);
+    uint64_t rows = tile_cap / per_row;
+    if (rows > rg * 8) rows = rg * 8;
+    if (rows >= 1) {
+      const uint64_t tile_bytes = rows * per_row;
+      const uint64_t red_off = (tile_bytes + 16 + 15) / 16 * 16;
+      const uint64_t s_lds = red_off + rows * units * 4 * (dual ? 2 : 1);
+      if (s_lds <= 65536 - 512) {
+        p.stream = true;
+        p.s_rows_per_tile = (uint32_t)rows;
+        p.s_threads = (uint32_t)sthreads;
+        p.s_red_offset = (uint32_t)red_off;
+        p.s_lds_bytes = (uint32_t)s_lds;
+        uint64_t by_lds = 163840 / (s_lds + 256);
+        uint64_t by_waves = 16 / (sthreads / 64);  // ~4 waves per SIMD at ~120 VGPRs
+        uint64_t w = by_lds < by_waves ? by_lds : by_waves;
+        p.s_wgs_per_cu = (uint32_t)(w < 1 ? 1 : w);
+      }
+    }
+  }
   return p;
 }
+
+static int cu_count() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cached[dev]) {
+    hipDeviceProp_t prop;
+    cached[dev] = hipGetDeviceProperties(&prop, dev) == hipSuccess ? prop.multiProcessorCount : 256;
+  }
+  return cached[dev];
+}
+
+static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 template <uint32_t T, int EPI>
 static hipError_t launch_tiled_t(const MvArgs& a, uint32_t grid, const MvPlan& p, hipStream_t st) {
@@ -287,21 +479,50 @@ static hipError_t launch_tiled_t(const MvArgs& a, uint32_t grid, const MvPlan& p
   return hipGetLastError();
 }
 
+// Resident workgroups per CU of one persistent kernel instance (registers,
+// LDS and waves all counted by the runtime), cached per shape.
+template <uint32_t T, int EPI>
+static uint32_t stream_occupancy(uint32_t threads, uint32_t lds) {
+  static std::mutex mu;
+  std::lock_guard<std::mutex> lock(mu);
+  static uint32_t cache_threads[8] = {0}, cache_lds[8] = {0}, cache_val[8] = {0};
+  for (int i = 0; i < 8; ++i)
+    if (cache_threads[i] == threads && cache_lds[i] == lds) return cache_val[i];
+  int n = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, matvec_stream<T, EPI>, (int)threads, (size_t)lds) !=
+          hipSuccess || n < 1)
+    n = 1;
+  for (int i = 0; i < 8; ++i)
+    if (cache_threads[i] == 0) {
+      cache_threads[i] = threads;
+      cache_lds[i] = lds;
+      cache_val[i] = (uint32_t)n;
+      break;
+    }
+  return (uint32_t)n;
+}
+
+template <uint32_t T, int EPI>
+static hipError_t launch_stream_t(const MvArgs& a, uint32_t tiles, const MvPlan& p, hipStream_t st) {
+  // balanced persistent grid: every workgroup walks k tiles
+  const uint64_t max_grid = (uint64_t)cu_count() * stream_occupancy<T, EPI>(p.s_threads, p.s_lds_bytes);
+  const uint64_t k = (tiles + max_grid - 1) / max_grid;
+  const uint32_t grid = (uint32_t)((tiles + k - 1) / k);
+  hipLaunchKernelGGL((matvec_stream<T, EPI>), dim3(grid), dim3(p.s_threads), p.s_lds_bytes, st, a);
+  return hipGetLastError();
+}
+
 template <int EPI>
-static hipError_t launch_tiled_e(uint32_t t, const MvArgs& a, uint32_t grid, const MvPlan& p, hipStream_t st) {
+static hipError_t launch_tiled_e(uint32_t t, const MvArgs& a, uint32_t grid, const MvPlan& p, hipStream_t st,
+                                 bool stream) {
+#define RF_MV(TT) \
+  case TT: return stream ? launch_stream_t<TT, EPI>(a, grid, p, st) : launch_tiled_t<TT, EPI>(a, grid, p, st);
   switch (t) {
-    case T_Q8_0: return launch_tiled_t<T_Q8_0, EPI>(a, grid, p, st);
-    case T_Q4_0: return launch_tiled_t<T_Q4_0, EPI>(a, grid, p, st);
-    case T_Q5_0: return launch_tiled_t<T_Q5_0, EPI>(a, grid, p, st);
-    case T_Q4_K: return launch_tiled_t<T_Q4_K, EPI>(a, grid, p, st);
-    case T_Q5_K: return launch_tiled_t<T_Q5_K, EPI>(a, grid, p, st);
-    case T_Q6_K: return launch_tiled_t<T_Q6_K, EPI>(a, grid, p, st);
-    case T_Q2_K: return launch_tiled_t<T_Q2_K, EPI>(a, grid, p, st);
-    case T_Q3_K: return launch_tiled_t<T_Q3_K, EPI>(a, grid, p, st);
-    case T_Q8_K: return launch_tiled_t<T_Q8_K, EPI>(a, grid, p, st);
-    case T_F32: return launch_tiled_t<T_F32, EPI>(a, grid, p, st);
+    RF_MV(T_Q8_0) RF_MV(T_Q4_0) RF_MV(T_Q5_0) RF_MV(T_Q4_K) RF_MV(T_Q5_K) RF_MV(T_Q6_K) RF_MV(T_Q2_K)
+    RF_MV(T_Q3_K) RF_MV(T_Q8_K) RF_MV(T_F32)
     default: return hipErrorInvalidValue;
   }
+#undef RF_MV
 }
 
 hipError_t launch_matvec_segments(uint32_t t, const MvSegDesc* segs, int nseg, const float* x,
@@ -310,7 +531,10 @@ hipError_t launch_matvec_segments(uint32_t t, const MvSegDesc* segs, int nseg, c
   if (nseg < 1 || nseg > 3) return hipErrorInvalidValue;
   const bool dual = epi == EPI_SWIGLU;
   MvPlan p = plan_matvec(t, in_dim, dual);
-  if (!p.tiled) {
+  // The tiled kernels read x and the norm weights as 16-byte vectors; other
+  // pointers take the rowwise kernel (plain store epilogue only).
+  const bool x_vec = aligned16(x) && (norm_w == nullptr || aligned16(norm_w));
+  if (!p.tiled || !x_vec) {
     if (norm_w != nullptr || epi != EPI_STORE) return hipErrorInvalidValue;
     for (int i = 0; i < nseg; ++i) {
       const uint32_t rows = (uint32_t)segs[i].rows;
@@ -328,6 +552,10 @@ hipError_t launch_matvec_segments(uint32_t t, const MvSegDesc* segs, int nseg, c
     }
     return hipSuccess;
   }
+  bool stream = p.stream && g_stream_enabled;
+  for (int i = 0; i < nseg && stream; ++i)
+    stream = aligned16(segs[i].w) && (!dual || aligned16(segs[i].w_up));
+  const uint32_t rpt = stream ? p.s_rows_per_tile : p.rows_per_tile;
   MvArgs a{};
   uint32_t tiles = 0;
   for (int i = 0; i < nseg; ++i) {
@@ -336,7 +564,7 @@ hipError_t launch_matvec_segments(uint32_t t, const MvSegDesc* segs, int nseg, c
     a.seg[i].res = segs[i].res;
     a.seg[i].rows = (uint32_t)segs[i].rows;
     a.seg[i].tile_begin = tiles;
-    tiles += (uint32_t)((segs[i].rows + p.rows_per_tile - 1) / p.rows_per_tile);
+    tiles += (uint32_t)((segs[i].rows + rpt - 1) / rpt);
   }
   if (tiles == 0) return hipSuccess;
   a.nseg = (uint32_t)nseg;
@@ -350,10 +578,16 @@ hipError_t launch_matvec_segments(uint32_t t, const MvSegDesc* segs, int nseg, c
   a.row_bytes = p.row_bytes;
   a.tile_stride = p.tile_stride;
   a.w_up = dual ? static_cast<const uint8_t*>(segs[0].w_up) : nullptr;
+  const uint32_t grid = tiles;  // one-shot kernel: one workgroup per tile
+  if (stream) {
+    a.rows_per_tile = rpt;
+    a.ntiles = tiles;
+    a.red_offset = p.s_red_offset;
+  }
   switch (epi) {
-    case EPI_STORE: return launch_tiled_e<EPI_STORE>(t, a, tiles, p, st);
-    case EPI_RESIDUAL: return launch_tiled_e<EPI_RESIDUAL>(t, a, tiles, p, st);
-    case EPI_SWIGLU: return launch_tiled_e<EPI_SWIGLU>(t, a, tiles, p, st);
+    case EPI_STORE: return launch_tiled_e<EPI_STORE>(t, a, grid, p, st, stream);
+    case EPI_RESIDUAL: return launch_tiled_e<EPI_RESIDUAL>(t, a, grid, p, st, stream);
+    case EPI_SWIGLU: return launch_tiled_e<EPI_SWIGLU>(t, a, grid, p, st, stream);
     default: return hipErrorInvalidValue;
   }
 }

@@ -23,6 +23,7 @@
 // Device state (current position, current token, generated-token ring) lives
 // in VRAM so a decode step needs no host round-trip and can be captured once
 // into a hipGraph and replayed.
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 #include <string>
@@ -59,6 +60,7 @@ struct rf_model {
   float* rope = nullptr;     // [cap][hd/2][2]
   float *hidden = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attn_out = nullptr, *act = nullptr;
   float *logits = nullptr, *final_hidden = nullptr, *attn_ws = nullptr, *up_tmp = nullptr;
+  float *xnorm = nullptr, *mvtmp = nullptr;  // scratch of the unfused fallback
   float* amax_val = nullptr;
   uint32_t* amax_idx = nullptr;
   int32_t* d_pos = nullptr;
@@ -234,6 +236,40 @@ int32_t check_ready(rf_model* m) {
     if (_e != hipSuccess) return hip_error(_e, what);       \
   } while (0)
 
+// A fused matvec launch, or — when a row does not fit the LDS tile (very wide
+// F32 rows) — the same computation as separate kernels: RMSNorm into xnorm,
+// rowwise matvec, then the residual / SiLU*up epilogue.
+hipError_t fused_matvec(rf_model* m, uint32_t t, const MvSegDesc* segs, int nseg, const float* x,
+                        const float* norm_w, uint64_t in_dim, int epi) {
+  hipStream_t st = m->ctx->compute;
+  const bool x_vec = (reinterpret_cast<uintptr_t>(x) & 15u) == 0 && (reinterpret_cast<uintptr_t>(norm_w) & 15u) == 0;
+  if (plan_matvec(t, in_dim, epi == EPI_SWIGLU).tiled && x_vec)
+    return launch_matvec_segments(t, segs, nseg, x, norm_w, m->cfg.rms_eps, in_dim, epi, st);
+  hipError_t e = hipSuccess;
+  const float* xe = x;
+  if (norm_w) {
+    e = launch_rmsnorm(x, norm_w, in_dim, m->cfg.rms_eps, m->xnorm, st);
+    if (e != hipSuccess) return e;
+    xe = m->xnorm;
+  }
+  for (int i = 0; i < nseg && e == hipSuccess; ++i) {
+    const MvSegDesc& s = segs[i];
+    if (epi == EPI_STORE) {
+      e = launch_matvec_segments(t, &s, 1, xe, nullptr, 0.f, in_dim, EPI_STORE, st);
+    } else if (epi == EPI_RESIDUAL) {
+      MvSegDesc tmp{s.w, nullptr, m->mvtmp, nullptr, s.rows};
+      e = launch_matvec_segments(t, &tmp, 1, xe, nullptr, 0.f, in_dim, EPI_STORE, st);
+      if (e == hipSuccess) e = launch_binary(BIN_ADD, s.res, m->mvtmp, s.rows, s.y, st);
+    } else {
+      MvSegDesc g{s.w, nullptr, s.y, nullptr, s.rows}, u{s.w_up, nullptr, m->mvtmp, nullptr, s.rows};
+      e = launch_matvec_segments(t, &g, 1, xe, nullptr, 0.f, in_dim, EPI_STORE, st);
+      if (e == hipSuccess) e = launch_matvec_segments(t, &u, 1, xe, nullptr, 0.f, in_dim, EPI_STORE, st);
+      if (e == hipSuccess) e = launch_binary(BIN_SWIGLU, s.y, m->mvtmp, s.rows, s.y, st);
+    }
+  }
+  return e;
+}
+
 // The five launch groups of one transformer block (model_executor.rs:102-236).
 // 1. attention RMSNorm + Q/K/V projections (+ bias), segments grouped by type.
 int32_t enqueue_qkv(rf_model* m, size_t li) {
@@ -254,7 +290,7 @@ int32_t enqueue_qkv(rf_model* m, size_t li) {
       segs[n++] = MvSegDesc{qkv[i]->d, nullptr, outs[i], nullptr, rows[i]};
       ++i;
     }
-    RF_LAUNCH(launch_matvec_segments(t, segs, n, m->hidden, attn_norm, c.rms_eps, d, EPI_STORE, st), "qkv matvec");
+    RF_LAUNCH(fused_matvec(m, t, segs, n, m->hidden, attn_norm, d, EPI_STORE), "qkv matvec");
   }
   if (L.bq.present()) {
     RF_LAUNCH(launch_bias_add(m->q, static_cast<const float*>(L.bq.d), qd, st), "bias");
@@ -287,7 +323,7 @@ int32_t enqueue_oproj(rf_model* m, size_t li) {
   Layer& L = m->layers[li];
   const uint64_t d = c.embedding_length, qd = c.head_count * c.head_dim;
   MvSegDesc s{L.o.d, nullptr, m->hidden, m->hidden, d};
-  RF_LAUNCH(launch_matvec_segments(L.o.type, &s, 1, m->attn_out, nullptr, 0.f, qd, EPI_RESIDUAL, m->ctx->compute),
+  RF_LAUNCH(fused_matvec(m, L.o.type, &s, 1, m->attn_out, nullptr, qd, EPI_RESIDUAL),
             "o-proj");
   return RF_OK;
 }
@@ -301,14 +337,14 @@ int32_t enqueue_gateup(rf_model* m, size_t li) {
   const float* ffn_norm = static_cast<const float*>(L.ffn_norm.d);
   if (L.gate.type == L.up.type) {
     MvSegDesc s{L.gate.d, L.up.d, m->act, nullptr, f};
-    RF_LAUNCH(launch_matvec_segments(L.gate.type, &s, 1, m->hidden, ffn_norm, c.rms_eps, d, EPI_SWIGLU, st),
+    RF_LAUNCH(fused_matvec(m, L.gate.type, &s, 1, m->hidden, ffn_norm, d, EPI_SWIGLU),
               "gate/up");
   } else {
     float* up_tmp = m->up_tmp;
     MvSegDesc sg{L.gate.d, nullptr, m->act, nullptr, f};
     MvSegDesc su{L.up.d, nullptr, up_tmp, nullptr, f};
-    RF_LAUNCH(launch_matvec_segments(L.gate.type, &sg, 1, m->hidden, ffn_norm, c.rms_eps, d, EPI_STORE, st), "gate");
-    RF_LAUNCH(launch_matvec_segments(L.up.type, &su, 1, m->hidden, ffn_norm, c.rms_eps, d, EPI_STORE, st), "up");
+    RF_LAUNCH(fused_matvec(m, L.gate.type, &sg, 1, m->hidden, ffn_norm, d, EPI_STORE), "gate");
+    RF_LAUNCH(fused_matvec(m, L.up.type, &su, 1, m->hidden, ffn_norm, d, EPI_STORE), "up");
     RF_LAUNCH(launch_binary(BIN_SWIGLU, m->act, up_tmp, f, m->act, st), "swiglu");
   }
   return RF_OK;
@@ -320,7 +356,7 @@ int32_t enqueue_down(rf_model* m, size_t li) {
   Layer& L = m->layers[li];
   const uint64_t d = c.embedding_length, f = c.feed_forward_length;
   MvSegDesc s{L.down.d, nullptr, m->hidden, m->hidden, d};
-  RF_LAUNCH(launch_matvec_segments(L.down.type, &s, 1, m->act, nullptr, 0.f, f, EPI_RESIDUAL, m->ctx->compute),
+  RF_LAUNCH(fused_matvec(m, L.down.type, &s, 1, m->act, nullptr, f, EPI_RESIDUAL),
             "down");
   return RF_OK;
 }
@@ -375,8 +411,8 @@ int32_t enqueue_logits(rf_model* m) {
   const rf_model_config& c = m->cfg;
   const DevTensor& w = m->output.present() ? m->output : m->token_embd;
   MvSegDesc s{w.d, nullptr, m->logits, nullptr, c.vocab_size};
-  RF_LAUNCH(launch_matvec_segments(w.type, &s, 1, m->hidden, static_cast<const float*>(m->output_norm.d), c.rms_eps,
-                                   c.embedding_length, EPI_STORE, m->ctx->compute),
+  RF_LAUNCH(fused_matvec(m, w.type, &s, 1, m->hidden, static_cast<const float*>(m->output_norm.d),
+                         c.embedding_length, EPI_STORE),
             "logits");
   return RF_OK;
 }
@@ -448,13 +484,15 @@ int32_t rf_model_create(rf_ctx* ctx, const rf_model_config* cfg, uint64_t kv_cap
   if (rc) { rf_model_destroy(m); return rc; }
   m->v_cache = static_cast<float*>(p);
   // activations: hidden, q, k, v, attn_out, act, up scratch, logits, final hidden
-  const uint64_t act_floats = d + qd + kvd + kvd + qd + f + f + c.vocab_size + d + 9 * 16;
+  const uint64_t wide = std::max(std::max(d, qd), f), widest = std::max(wide, (uint64_t)c.vocab_size);
+  const uint64_t act_floats = d + qd + kvd + kvd + qd + f + f + c.vocab_size + d + wide + widest + 11 * 16;
   rc = charge_alloc(m, "tmp:forward", act_floats * 4 + 64 * 8, &p);
   if (rc) { rf_model_destroy(m); return rc; }
   float* base = static_cast<float*>(p);
   auto take = [&](uint64_t n) { float* r = base; base += (n + 15) / 16 * 16; return r; };
   m->hidden = take(d); m->q = take(qd); m->k = take(kvd); m->v = take(kvd); m->attn_out = take(qd);
   m->act = take(f); m->up_tmp = take(f); m->logits = take(c.vocab_size); m->final_hidden = take(d);
+  m->xnorm = take(wide); m->mvtmp = take(widest);
   // attention workspace: fixed split count for the capacity (graph-friendly)
   const bool fast = attention_supported((uint32_t)c.head_count, (uint32_t)c.head_count_kv, (uint32_t)c.head_dim);
   m->nsplit = fast ? attention_splits((uint32_t)kv_cap, (uint32_t)c.head_count_kv) : 1;
@@ -626,6 +664,9 @@ int32_t rf_model_time_kernel(rf_model* m, uint32_t kind, uint32_t reps, float* a
   if (rc) return rc;
   if (kind == RF_KERNEL_ATTENTION && m->seq_len == 0)
     return set_error(RF_ERR_INVALID, "attention timing needs a forwarded prompt");
+  if (kind == RF_KERNEL_ATTENTION && m->seq_len >= m->kv_cap)
+    return set_error(RF_ERR_INVALID, "attention timing writes K/V slot %llu but the cache holds %llu",
+                     (unsigned long long)m->seq_len, (unsigned long long)m->kv_cap);
   hipStream_t st = m->ctx->compute;
   hipEvent_t e0, e1;
   RF_LAUNCH(hipEventCreate(&e0), "hipEventCreate");

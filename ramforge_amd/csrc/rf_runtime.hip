@@ -594,11 +594,15 @@ int32_t rf_argmax(rf_ctx* ctx, const float* logits, uint64_t n, uint32_t* out, r
 }
 
 int32_t rf_synth_blocks(rf_ctx* ctx, uint32_t t, uint64_t seed, uint64_t first, uint64_t n, double mul, void* dst,
-                        rf_stream_t s) {
+                        uint64_t dst_bytes, rf_stream_t s) {
   RF_CHECK_CTX(ctx);
-  if (!type_geometry(t, nullptr, nullptr))
+  uint64_t qk = 0, bs = 0;
+  if (!type_geometry(t, &qk, &bs))
     return set_error(RF_ERR_UNSUPPORTED, "synthetic generator does not emit %s", type_name(t));
   if (n && !dst) return set_error(RF_ERR_INVALID, "null synthetic destination");
+  if (n > dst_bytes / bs)
+    return set_error(RF_ERR_INVALID, "%llu %s blocks need %llu bytes, destination holds %llu", (unsigned long long)n,
+                     type_name(t), (unsigned long long)(n * bs), (unsigned long long)dst_bytes);
   hipError_t e = launch_synth(t, seed, first, n, mul, dst, pick_stream(ctx, s));
   return e == hipSuccess ? RF_OK : hip_error(e, "synth launch");
 }
@@ -606,6 +610,11 @@ int32_t rf_synth_blocks(rf_ctx* ctx, uint32_t t, uint64_t seed, uint64_t first, 
 uint32_t rf_tune_matvec_tile_bytes(uint32_t bytes) {
   if (bytes) set_matvec_tile_bytes(bytes);
   return matvec_tile_bytes();
+}
+
+int32_t rf_tune_matvec_kernel(int32_t mode) {
+  if (mode == 0 || mode == 1) set_matvec_stream(mode == 1);
+  return matvec_stream() ? 1 : 0;
 }
 
 }  // extern "C"

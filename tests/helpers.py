@@ -85,3 +85,23 @@ def assert_close(y, ref, tol: float = 1e-4, floor_frac: float = 1e-3, what: str 
     e = rel_err(np.asarray(y), np.asarray(ref), floor_frac)
     assert e <= tol, f"{what}: max relative error {e:.3e} > {tol:.1e}"
     return e
+
+
+def scaled_err(y, ref, scale, floor: float = 1e-2) -> float:
+    """Max per-element error |y - ref| / max(|ref|, floor * scale).
+
+    ``scale`` is each element's term magnitude (sum_j |w_ij x_j| for a matvec,
+    sum_p p_p |v_p| for attention).  Well-conditioned elements get the plain
+    relative error; an element that cancels to near zero is measured against
+    1% of its terms, which is where any two f32 summation orders (the
+    reference's sequential one included) legitimately differ."""
+    ref = np.asarray(ref, np.float64)
+    d = np.abs(np.asarray(y, np.float64) - ref)
+    den = np.maximum(np.abs(ref), floor * np.asarray(scale, np.float64))
+    return float(np.max(d / np.maximum(den, 1e-30))) if ref.size else 0.0
+
+
+def assert_close_scaled(y, ref, scale, tol: float = 1e-4, what: str = ""):
+    e = scaled_err(y, ref, scale)
+    assert e <= tol, f"{what}: max scaled relative error {e:.3e} > {tol:.1e}"
+    return e

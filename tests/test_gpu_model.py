@@ -63,8 +63,10 @@ MIXED = dict(embd=Q4_K, out=Q6_K, q=Q4_K, k=Q4_K, v=Q6_K, o=Q4_K, gate=Q4_K, up=
 ALL_F32 = dict(embd=F32, out=F32, q=F32, k=F32, v=F32, o=F32, gate=F32, up=F32, down=F32)
 
 
+@pytest.mark.parametrize("mode", [1, 0], ids=["stream", "oneshot"])
 @pytest.mark.parametrize("kind,bias", [("q8", False), ("mixed", True), ("f32", True)])
-def test_tiny_model_forward_and_generate(ctx, orc, kind, bias):
+def test_tiny_model_forward_and_generate(ctx, orc, kind, bias, mode):
+    _rf().tune_matvec_kernel(mode)
     cfg = dict(TINY)
     types = {"q8": ALL_Q8, "mixed": MIXED, "f32": ALL_F32}[kind]
     if kind == "mixed":
@@ -89,6 +91,7 @@ def test_tiny_model_forward_and_generate(ctx, orc, kind, bias):
     assert gm.seq_len == 4 + 19
     gm.close()
     om.close()
+    _rf().tune_matvec_kernel(1)
 
 
 def test_generate_stop_rules(ctx, orc):
