@@ -6,31 +6,51 @@
 // [pos][kvh][hd], position hist is the current K/V; score = dot / sqrt(hd);
 // softmax over hist+1 positions; out = sum_p softmax_p * V_p.
 //
-// Flash-decoding on gfx950: the positions are split into `nsplit` chunks per
-// KV head.  A workgroup (4 wavefronts) owns one (chunk, KV head) pair and all
-// G = qh/kvh query heads that share it, so each K/V row is read from HBM once
-// for the whole group.  Sixteen lanes cooperate on one position (each holds
-// hd/16 consecutive dims: 512 contiguous bytes per position for hd = 128), so
-// a wavefront streams four positions per step.  Scores go to LDS, the chunk's
-// max and exp-sum are workgroup reductions, then V is accumulated with the
-// same lane mapping.  Each chunk writes (o, m, l); a combine kernel merges
-// the chunks with the usual max-rescaling.
+// Flash-decoding on gfx950, one launch per call:
+//   * The positions are cut into chunks of at least 64 (one chunk per
+//     workgroup and KV head).  A workgroup (4 wavefronts) owns one
+//     (chunk, KV head) pair and all G = qh/kvh query heads that share it, so
+//     every K/V row is read from HBM once for the whole group.
+//   * Sixteen lanes cooperate on one position (hd/16 consecutive dims each:
+//     512 contiguous bytes per position for hd = 128); a wavefront covers four
+//     positions per step and every lane issues the loads of four steps before
+//     it uses any of them, so a 64-position chunk is one round trip per pass.
+//   * The G partial dot products of a position are summed over the 16 lanes
+//     with a transposing butterfly (log2(G) exchange steps that halve the
+//     heads each lane holds, then plain steps): 5 shuffles for G = 4 instead
+//     of 16.
+//   * Scores go to LDS; the chunk max and exp-sum are per-head wavefront
+//     reductions.  For V each lane owns hd/64 dims and each wavefront 16 of
+//     every 64 positions, so the weighted sum needs no cross-lane step; the
+//     four wavefronts are summed through LDS.
+//   * Each chunk writes (o, m, l) of its G heads; a second kernel merges
+//     the chunks with the usual max-rescaling.  (Merging inside the split
+//     kernel through arrival counters needs device-scope release fences,
+//     which write back the per-XCD L2 on gfx950 and cost far more than the
+//     second launch.)
 //
 // Model mode (d_pos != null) fuses the decode-step glue: RoPE (half-split,
 // core/src/compute.rs:446-456) is applied to q and the current k from a
 // host-built cos/sin table, and the rotated k and the raw v are written into
 // the cache slot `hist` (kv_cache.rs:381-412).  No workgroup of the launch
-// reads that slot, so the write does not race with the reads.
+// reads that slot from memory (the current position is taken from LDS), so
+// the write does not race with the reads.
 #include "rf_kernels.h"
 
 namespace rf {
 
 constexpr int ATT_THREADS = 256;
-constexpr int ATT_MAX_CHUNK = 1024;
+constexpr uint32_t ATT_MAX_CHUNK = 1024;  // positions of one chunk (LDS score rows)
+constexpr uint32_t ATT_MIN_CHUNK = 64;    // 16 position slots x 4 loads in flight
+constexpr int ATT_UNROLL = 4;
+constexpr uint32_t ATT_MAX_SPLITS = 256;
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ uint32_t att_chunk(uint32_t total, uint32_t nsplit) {
   uint32_t c = (total + nsplit - 1) / nsplit;
-  return (c + 15u) & ~15u;
+  c = (c + 15u) & ~15u;
+  return c < ATT_MIN_CHUNK ? ATT_MIN_CHUNK : c;
 }
 
 // Rotated element d of a head vector v (half-split RoPE, cs = [half][2] cos/sin).
@@ -45,11 +65,63 @@ __device__ __forceinline__ float rope_elem(const float* v, const float* cs, uint
   return v[i] * s + v[d] * c;
 }
 
+// Sum of s[h] over the 16 lanes of a position group (one DPP row) for every
+// h < N.  Each exchange level hands half of the heads a lane holds to its
+// partner across bit OFF and keeps the other half; after log2(N) levels a
+// lane holds one head, summed by plain exchanges over the remaining bits.
+// `head` accumulates which head the lane ends with; lanes with
+// (lane & (16/N - 1)) == 0 hold distinct heads.
+template <int N, int OFF>
+__device__ __forceinline__ float head_reduce16(float* s, uint32_t lane, uint32_t& head) {
+  if constexpr (N > 1) {
+    constexpr int half = N / 2;
+    const bool hi = (lane & OFF) != 0;
+#pragma unroll
+    for (int i = 0; i < half; ++i) {
+      const float send = hi ? s[i] : s[i + half];
+      const float keep = hi ? s[i + half] : s[i];
+      s[i] = keep + rf_xchg16<OFF>(send);
+    }
+    if (hi) head += half;
+    return head_reduce16<half, OFF / 2>(s, lane, head);
+  } else if constexpr (OFF >= 1) {
+    s[0] += rf_xchg16<OFF>(s[0]);
+    return head_reduce16<1, OFF / 2>(s, lane, head);
+  } else {
+    return s[0];
+  }
+}
+
+template <int N>
+__device__ __forceinline__ void load_few(float* dst, const float* src) {
+  if constexpr (N == 1) {
+    dst[0] = __builtin_nontemporal_load(src);
+  } else {
+    typedef float vec __attribute__((ext_vector_type(N)));
+    const vec v = __builtin_nontemporal_load(reinterpret_cast<const vec*>(src));
+#pragma unroll
+    for (int i = 0; i < N; ++i) dst[i] = v[i];
+  }
+}
+
+__device__ __forceinline__ void load_dims(float* dst, const float* src, int n) {
+  const f32x4* p = reinterpret_cast<const f32x4*>(src);
+#pragma unroll
+  for (int i = 0; i < n / 4; ++i) {
+    const f32x4 v = __builtin_nontemporal_load(p + i);
+    dst[4 * i] = v.x; dst[4 * i + 1] = v.y; dst[4 * i + 2] = v.z; dst[4 * i + 3] = v.w;
+  }
+}
+
 template <int G, int DPL>
 __global__ __launch_bounds__(ATT_THREADS) void attn_split(AttnArgs a) {
   constexpr int HD = DPL * 16;
+  constexpr int U = DPL <= 8 ? ATT_UNROLL : ATT_UNROLL / 2;  // register budget for hd = 256
+  constexpr uint32_t WMASK = 16u / G - 1u;
   __shared__ __align__(16) float sc[G][ATT_MAX_CHUNK];
+  __shared__ __align__(16) float qs[G][HD];
   __shared__ __align__(16) float kcur[HD];
+  __shared__ __align__(16) float vcur[HD];
   __shared__ float mh[G], lh[G];
   __shared__ __align__(16) float ored[4][G][HD];
 
@@ -62,51 +134,116 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_split(AttnArgs a) {
   if (p0 >= total) return;
   const uint32_t p1 = min(total, p0 + chunk);
   const uint32_t npos = p1 - p0;
-  const uint32_t nsplit_used = (total + chunk - 1) / chunk;
+  const uint32_t nmain = min(p1, hist) - p0;  // positions read from the cache
+  const bool has_cur = p1 == total;           // the current position is the last one
+  const uint32_t ns = (total + chunk - 1) / chunk;
   const uint32_t kvw = a.kvh * HD;
   const float* cs = a.rope ? a.rope + (size_t)hist * HD : nullptr;  // [half][2] for this position
+  const uint32_t sl = lane & 15u, slot = wave * 4u + (lane >> 4);
+  const uint32_t d0 = sl * DPL;
+  const float* kb = a.k_hist + (size_t)p0 * kvw + g * HD + d0;
+  // Pass 2 maps lanes to dims instead: lane l owns dims [l*DPW, (l+1)*DPW) of
+  // every V row and wavefront w the rows w*16 .. w*16+15 of each 64-row batch,
+  // so the weighted V sum needs no cross-lane reduction.
+  constexpr int DPW = HD / 64;
+  const float* vb = a.v_hist + (size_t)p0 * kvw + g * HD + lane * DPW;
 
-  // Current k of this KV head (rotated in model mode), and the cache write.
-  for (uint32_t d = tid; d < (uint32_t)HD; d += ATT_THREADS) {
-    const float* kc = a.k_cur + g * HD;
-    const float kv = cs ? rope_elem(kc, cs, d, HD) : kc[d];
-    kcur[d] = kv;
-    if (a.k_store && sp == 0) {
-      a.k_store[(size_t)hist * kvw + g * HD + d] = kv;
-      a.v_store[(size_t)hist * kvw + g * HD + d] = a.v_cur[g * HD + d];
+  // The first batch of K and V rows is requested before anything else, so the
+  // prologue's loads and both passes of a 64-position chunk share one memory
+  // round trip.  Indices are clamped: every load is in bounds.
+  float kv[U][DPL], vv[16][DPW];
+  if (nmain > 0) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const uint32_t j = min(slot + 16u * u, nmain - 1u);
+      load_dims(kv[u], kb + (size_t)j * kvw, DPL);
+    }
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      const uint32_t j = min(wave * 16u + k, nmain - 1u);
+      load_few<DPW>(vv[k], vb + (size_t)j * kvw);
     }
   }
 
-  const uint32_t sl = lane & 15u, slot = wave * 4u + (lane >> 4);
-  const uint32_t d0 = sl * DPL;
-  float qr[G][DPL];
+  // Rotated q of the G heads, the current k (rotated) and v, and the slot
+  // write.  Element t of [q heads..., k, v] is handled by thread t % 256; all
+  // loads are issued before any is used (clamped indices, in bounds).
+  {
+    constexpr uint32_t NE = (G + 2) * HD, NP = (NE + ATT_THREADS - 1) / ATT_THREADS, HALF = HD / 2;
+    float va[NP], vp[NP], c0[NP], c1[NP];
 #pragma unroll
-  for (int h = 0; h < G; ++h) {
-    const float* qv = a.q + (size_t)(g * G + h) * HD;
+    for (uint32_t i = 0; i < NP; ++i) {
+      const uint32_t t = min(tid + i * ATT_THREADS, NE - 1u), r = t / HD, d = t % HD;
+      const float* src = r < (uint32_t)G ? a.q + (size_t)(g * G + r) * HD : (r == (uint32_t)G ? a.k_cur : a.v_cur) + g * HD;
+      const uint32_t ci = d < HALF ? d : d - HALF;
+      va[i] = src[d];
+      vp[i] = src[d < HALF ? d + HALF : d - HALF];
+      c0[i] = cs ? cs[2 * ci] : 1.f;
+      c1[i] = cs ? cs[2 * ci + 1] : 0.f;
+    }
 #pragma unroll
-    for (int i = 0; i < DPL; ++i) qr[h][i] = cs ? rope_elem(qv, cs, d0 + i, HD) : qv[d0 + i];
+    for (uint32_t i = 0; i < NP; ++i) {
+      const uint32_t t = tid + i * ATT_THREADS, r = t / HD, d = t % HD;
+      if (t >= NE) break;
+      // half-split rotation in the RoPE kernel's operation order
+      const float rot = d < HALF ? va[i] * c0[i] - vp[i] * c1[i] : vp[i] * c1[i] + va[i] * c0[i];
+      if (r < (uint32_t)G) {
+        qs[r][d] = cs ? rot : va[i];
+      } else if (r == (uint32_t)G) {
+        const float kv = cs ? rot : va[i];
+        kcur[d] = kv;
+        if (a.k_store && sp == 0) a.k_store[(size_t)hist * kvw + g * HD + d] = kv;
+      } else {
+        vcur[d] = va[i];
+        if (a.v_store && sp == 0) a.v_store[(size_t)hist * kvw + g * HD + d] = va[i];
+      }
+    }
   }
   __syncthreads();
 
-  // Pass 1: scores.
-  for (uint32_t j = slot; j < npos; j += 16u) {
-    const uint32_t p = p0 + j;
-    const float* kp = (p < hist) ? a.k_hist + (size_t)p * kvw + g * HD + d0 : kcur + d0;
-    float kv[DPL];
+  float qr[G][DPL];
 #pragma unroll
-    for (int i = 0; i < DPL; i += 4) {
-      const float4 v4 = *reinterpret_cast<const float4*>(kp + i);
-      kv[i] = v4.x; kv[i + 1] = v4.y; kv[i + 2] = v4.z; kv[i + 3] = v4.w;
+  for (int h = 0; h < G; ++h)
+#pragma unroll
+    for (int i = 0; i < DPL; ++i) qr[h][i] = qs[h][d0 + i];
+
+  // Pass 1: scores.
+  for (uint32_t j0 = 0; j0 < nmain; j0 += 16u * U) {
+    if (j0 > 0) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const uint32_t j = min(j0 + slot + 16u * u, nmain - 1u);
+        load_dims(kv[u], kb + (size_t)j * kvw, DPL);
+      }
     }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      float s[G];
+#pragma unroll
+      for (int h = 0; h < G; ++h) {
+        float acc = 0.f;
+#pragma unroll
+        for (int i = 0; i < DPL; ++i) acc = fmaf(qr[h][i], kv[u][i], acc);
+        s[h] = acc;
+      }
+      uint32_t hh = 0;
+      const float r = head_reduce16<G, 8>(s, lane, hh);
+      const uint32_t j = j0 + slot + 16u * u;
+      if (j < nmain && (lane & WMASK) == 0) sc[hh][j] = r / a.denom;
+    }
+  }
+  if (has_cur && wave == 0) {
+    float s[G];
 #pragma unroll
     for (int h = 0; h < G; ++h) {
-      float s = 0.f;
+      float acc = 0.f;
 #pragma unroll
-      for (int i = 0; i < DPL; ++i) s = fmaf(qr[h][i], kv[i], s);
-#pragma unroll
-      for (int o = 8; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
-      if (sl == 0) sc[h][j] = s / a.denom;
+      for (int i = 0; i < DPL; ++i) acc = fmaf(qr[h][i], kcur[d0 + i], acc);
+      s[h] = acc;
     }
+    uint32_t hh = 0;
+    const float r = head_reduce16<G, 8>(s, lane, hh);
+    if (slot == 0 && (lane & WMASK) == 0) sc[hh][nmain] = r / a.denom;
   }
   __syncthreads();
 
@@ -126,50 +263,58 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_split(AttnArgs a) {
   }
   __syncthreads();
 
-  // Pass 2: o[h] = sum_p e[h][p] * V_p.
-  float o[G][DPL];
+  // Pass 2: o[h] = sum_p e[h][p] * V_p, 64 rows per batch.
+  float o[G][DPW];
 #pragma unroll
   for (int h = 0; h < G; ++h)
 #pragma unroll
-    for (int i = 0; i < DPL; ++i) o[h][i] = 0.f;
-  for (uint32_t j = slot; j < npos; j += 16u) {
-    const uint32_t p = p0 + j;
-    const float* vp = (p < hist) ? a.v_hist + (size_t)p * kvw + g * HD + d0 : a.v_cur + g * HD + d0;
-    float vv[DPL];
+    for (int i = 0; i < DPW; ++i) o[h][i] = 0.f;
+  for (uint32_t j0 = 0; j0 < nmain; j0 += 64u) {
+    if (j0 > 0) {
 #pragma unroll
-    for (int i = 0; i < DPL; i += 4) {
-      const float4 v4 = *reinterpret_cast<const float4*>(vp + i);
-      vv[i] = v4.x; vv[i + 1] = v4.y; vv[i + 2] = v4.z; vv[i + 3] = v4.w;
+      for (int k = 0; k < 16; ++k) {
+        const uint32_t j = min(j0 + wave * 16u + k, nmain - 1u);
+        load_few<DPW>(vv[k], vb + (size_t)j * kvw);
+      }
     }
-#pragma unroll
-    for (int h = 0; h < G; ++h) {
-      const float e = sc[h][j];
-#pragma unroll
-      for (int i = 0; i < DPL; ++i) o[h][i] = fmaf(e, vv[i], o[h][i]);
-    }
-  }
-  // Reduce the four 16-lane groups of each wavefront, then the four wavefronts.
-#pragma unroll
-  for (int h = 0; h < G; ++h)
-#pragma unroll
-    for (int i = 0; i < DPL; ++i) {
-      float v = o[h][i];
-      v += __shfl_xor(v, 16, 64);
-      v += __shfl_xor(v, 32, 64);
-      o[h][i] = v;
-    }
-  if (lane < 16u) {
+    // weights of this wavefront's 16 rows, 16-byte LDS reads (j0 + 16w is a
+    // multiple of 16 and below ATT_MAX_CHUNK since j0 < nmain <= chunk)
+    float e[G][16];
 #pragma unroll
     for (int h = 0; h < G; ++h)
 #pragma unroll
-      for (int i = 0; i < DPL; ++i) ored[wave][h][d0 + i] = o[h][i];
+      for (int q4 = 0; q4 < 4; ++q4) {
+        const float4 w4 = *reinterpret_cast<const float4*>(&sc[h][j0 + wave * 16u + 4u * q4]);
+        e[h][4 * q4] = w4.x; e[h][4 * q4 + 1] = w4.y; e[h][4 * q4 + 2] = w4.z; e[h][4 * q4 + 3] = w4.w;
+      }
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      const bool use = j0 + wave * 16u + k < nmain;
+#pragma unroll
+      for (int h = 0; h < G; ++h)
+#pragma unroll
+        for (int i = 0; i < DPW; ++i) o[h][i] = use ? fmaf(e[h][k], vv[k][i], o[h][i]) : o[h][i];
+    }
   }
+  if (has_cur && wave == 0) {
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      const float e = sc[h][nmain];
+#pragma unroll
+      for (int i = 0; i < DPW; ++i) o[h][i] = fmaf(e, vcur[lane * DPW + i], o[h][i]);
+    }
+  }
+  // Sum the four wavefronts.
+#pragma unroll
+  for (int h = 0; h < G; ++h)
+#pragma unroll
+    for (int i = 0; i < DPW; ++i) ored[wave][h][lane * DPW + i] = o[h][i];
   __syncthreads();
   for (uint32_t t = tid; t < (uint32_t)(G * HD); t += ATT_THREADS) {
     const uint32_t h = t / HD, d = t % HD;
     const float v = ored[0][h][d] + ored[1][h][d] + ored[2][h][d] + ored[3][h][d];
     const uint32_t qhead = g * G + h;
-    if (nsplit_used == 1) {
+    if (ns == 1) {
       a.out[(size_t)qhead * HD + d] = v / lh[h];
     } else {
       float* w = a.ws + ((size_t)sp * a.qh + qhead) * (HD + 2);
@@ -179,30 +324,58 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_split(AttnArgs a) {
   }
 }
 
-// Merge the per-chunk (o, m, l) of every query head.  One workgroup per head.
+// Merge the chunk records (o, m, l) of one query head and 32 of its dims:
+// the factors exp(m_s - M) are computed once per workgroup in parallel over
+// the chunks, then 8 groups of 32 lanes sum disjoint chunk subsets.
 __global__ __launch_bounds__(256) void attn_combine(AttnArgs a) {
-  const uint32_t qhead = blockIdx.x, hd = a.hd;
+  __shared__ float fac[ATT_MAX_SPLITS];
+  __shared__ float red[8][32];
+  __shared__ float wm[4], wl[4];
+  const uint32_t qhead = blockIdx.x, hd = a.hd, tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
   const uint32_t hist = a.d_pos ? (uint32_t)(*a.d_pos) : a.hist;
   const uint32_t total = hist + 1;
   const uint32_t chunk = att_chunk(total, a.nsplit);
   const uint32_t ns = (total + chunk - 1) / chunk;
   if (ns == 1) return;
-  float m = -INFINITY;
-  for (uint32_t s = 0; s < ns; ++s) m = fmaxf(m, a.ws[((size_t)s * a.qh + qhead) * (hd + 2) + hd]);
-  float l = 0.f;
-  for (uint32_t s = 0; s < ns; ++s) {
-    const float* w = a.ws + ((size_t)s * a.qh + qhead) * (hd + 2);
-    l = fmaf(w[hd + 1], expf(w[hd] - m), l);
+  const size_t rec = hd + 2, stride = (size_t)a.qh * rec;
+  const float* base = a.ws + (size_t)qhead * rec;
+  const uint32_t dl = tid & 31u, grp = tid >> 5, d = blockIdx.y * 32u + dl;
+  // the first four records of this lane's chunk subset, requested up front
+  float pre[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t s = grp + 8u * i;
+    pre[i] = (s < ns && d < hd) ? base[s * stride + d] : 0.f;
   }
-  for (uint32_t d = threadIdx.x; d < hd; d += blockDim.x) {
-    float acc = 0.f;
-    for (uint32_t s = 0; s < ns; ++s) {
-      const float* w = a.ws + ((size_t)s * a.qh + qhead) * (hd + 2);
-      acc = fmaf(w[d], expf(w[hd] - m), acc);
-    }
-    a.out[(size_t)qhead * hd + d] = acc / l;
+  const float m_s = tid < ns ? base[tid * stride + hd] : -INFINITY;  // ns <= 256
+  float m = rf_wave_max(m_s);
+  if (lane == 0) wm[wave] = m;
+  __syncthreads();
+  m = fmaxf(fmaxf(wm[0], wm[1]), fmaxf(wm[2], wm[3]));
+  const float f = tid < ns ? expf(m_s - m) : 0.f;
+  fac[tid] = f;
+  float l = rf_wave_sum(tid < ns ? base[tid * stride + hd + 1] * f : 0.f);
+  if (lane == 0) wl[wave] = l;
+  __syncthreads();
+  l = wl[0] + wl[1] + wl[2] + wl[3];
+  float acc = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t s = grp + 8u * i;
+    if (s < ns) acc = fmaf(fac[s], pre[i], acc);
+  }
+  if (d < hd)
+    for (uint32_t s = grp + 32u; s < ns; s += 8u) acc = fmaf(fac[s], base[s * stride + d], acc);
+  red[grp][dl] = acc;
+  __syncthreads();
+  if (grp == 0 && d < hd) {
+    float v = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v += red[i][dl];
+    a.out[(size_t)qhead * hd + d] = v / l;
   }
 }
+
 
 // Any-shape fallback (tiny heads, large GQA groups): one workgroup per query
 // head, scores in the workspace ([qh][total]), plain loops.
@@ -270,21 +443,31 @@ __global__ __launch_bounds__(256) void attn_naive(AttnArgs a) {
   }
 }
 
-bool attention_supported(uint32_t qh, uint32_t kvh, uint32_t hd) {
+bool attention_supported(uint32_t qh, uint32_t kvh, uint32_t hd, uint64_t total) {
   if (kvh == 0 || qh % kvh != 0) return false;
+  if (total > (uint64_t)ATT_MAX_SPLITS * ATT_MAX_CHUNK) return false;
   const uint32_t G = qh / kvh;
   const bool g_ok = G == 1 || G == 2 || G == 4 || G == 8;
   const bool hd_ok = hd == 64 || hd == 128 || hd == 256;
   return g_ok && hd_ok && G * (hd / 16) <= 64;
 }
 
+// Chunks per KV head: 64 positions each while that keeps the launch within
+// about 1024 workgroups, longer chunks beyond (at most ATT_MAX_SPLITS chunks
+// of at most ATT_MAX_CHUNK positions).
 uint32_t attention_splits(uint32_t total, uint32_t kvh) {
-  const uint32_t by_len = (total + 63) / 64;
-  const uint32_t want = (512 + kvh - 1) / kvh;
-  const uint32_t min_for_lds = (total + ATT_MAX_CHUNK - 1) / ATT_MAX_CHUNK;
-  uint32_t n = by_len < want ? by_len : want;
-  if (n < min_for_lds) n = min_for_lds;
+  uint32_t n = (total + ATT_MIN_CHUNK - 1) / ATT_MIN_CHUNK;
+  uint32_t cap = 1024u / (kvh ? kvh : 1u);
+  if (cap > ATT_MAX_SPLITS) cap = ATT_MAX_SPLITS;
+  if (cap < 1) cap = 1;
+  if (n > cap) n = cap;
+  const uint32_t lo = (total + ATT_MAX_CHUNK - 1) / ATT_MAX_CHUNK;
+  if (n < lo) n = lo;
   return n < 1 ? 1 : n;
+}
+
+uint64_t attention_ws_floats(uint32_t nsplit, uint32_t qh, uint32_t hd) {
+  return (uint64_t)nsplit * qh * (hd + 2);
 }
 
 template <int G, int DPL>
@@ -298,19 +481,19 @@ hipError_t launch_attention_naive(const AttnArgs& a, hipStream_t st) {
 }
 
 hipError_t launch_attention(const AttnArgs& a, hipStream_t st) {
-  if (!attention_supported(a.qh, a.kvh, a.hd)) return launch_attention_naive(a, st);
+  if (a.nsplit < 1 || a.nsplit > ATT_MAX_SPLITS) return hipErrorInvalidValue;
   const uint32_t G = a.qh / a.kvh, dpl = a.hd / 16;
-#define RF_ATT(GG, DD) if (G == GG && dpl == DD) launch_split_t<GG, DD>(a, st);
+  bool done = false;
+#define RF_ATT(GG, DD) \
+  if (!done && G == GG && dpl == DD) { launch_split_t<GG, DD>(a, st); done = true; }
   RF_ATT(1, 4) RF_ATT(1, 8) RF_ATT(1, 16) RF_ATT(2, 4) RF_ATT(2, 8) RF_ATT(2, 16)
   RF_ATT(4, 4) RF_ATT(4, 8) RF_ATT(4, 16) RF_ATT(8, 4) RF_ATT(8, 8)
 #undef RF_ATT
+  if (!done) return hipErrorInvalidValue;
   hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  if (a.nsplit > 1) {
-    hipLaunchKernelGGL(attn_combine, dim3(a.qh), dim3(a.hd < 256 ? a.hd : 256), 0, st, a);
-    e = hipGetLastError();
-  }
-  return e;
+  if (e != hipSuccess || a.nsplit == 1) return e;
+  hipLaunchKernelGGL(attn_combine, dim3(a.qh, (a.hd + 31) / 32), dim3(256), 0, st, a);
+  return hipGetLastError();
 }
 
 }  // namespace rf

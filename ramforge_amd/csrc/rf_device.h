@@ -58,16 +58,49 @@ __device__ __forceinline__ void rf_lds_words(const uint8_t* lds, uint32_t off, u
   for (int i = 0; i < N; ++i) out[i] = __builtin_amdgcn_alignbyte(raw[i + 1], raw[i], sh);
 }
 
-__device__ __forceinline__ float rf_wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, RF_WAVE);
+// Cross-lane data movement inside a 16-lane row with DPP (a VALU operand
+// modifier: no LDS round trip, unlike ds_bpermute behind __shfl_xor).
+// rf_xchg16<OFF>(v) returns v of a partner lane whose index differs from
+// this lane's in bit OFF: quad permutations for OFF = 1, 2 (lane ^ 1,
+// lane ^ 2), the half-row mirror (lane ^ 7) for OFF = 4 and the row mirror
+// (lane ^ 15) for OFF = 8.  Every lane of the wavefront must be active.
+template <int OFF>
+__device__ __forceinline__ float rf_xchg16(float v) {
+  static_assert(OFF == 1 || OFF == 2 || OFF == 4 || OFF == 8, "DPP partner bit");
+  constexpr int ctrl = OFF == 1 ? 0xB1 : OFF == 2 ? 0x4E : OFF == 4 ? 0x141 : 0x140;
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), ctrl, 0xF, 0xF, true));
+}
+
+// Sum (max) over the 16 lanes of each row; every lane gets its row's value.
+__device__ __forceinline__ float rf_row16_sum(float v) {
+  v += rf_xchg16<1>(v);
+  v += rf_xchg16<2>(v);
+  v += rf_xchg16<4>(v);
+  v += rf_xchg16<8>(v);
   return v;
 }
 
-__device__ __forceinline__ float rf_wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, RF_WAVE));
+__device__ __forceinline__ float rf_row16_max(float v) {
+  v = fmaxf(v, rf_xchg16<1>(v));
+  v = fmaxf(v, rf_xchg16<2>(v));
+  v = fmaxf(v, rf_xchg16<4>(v));
+  v = fmaxf(v, rf_xchg16<8>(v));
   return v;
+}
+
+__device__ __forceinline__ float rf_lane(float v, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+
+// Wavefront sum / max (all 64 lanes active); the result is uniform.
+__device__ __forceinline__ float rf_wave_sum(float v) {
+  v = rf_row16_sum(v);
+  return (rf_lane(v, 0) + rf_lane(v, 16)) + (rf_lane(v, 32) + rf_lane(v, 48));
+}
+
+__device__ __forceinline__ float rf_wave_max(float v) {
+  v = rf_row16_max(v);
+  return fmaxf(fmaxf(rf_lane(v, 0), rf_lane(v, 16)), fmaxf(rf_lane(v, 32), rf_lane(v, 48)));
 }
 
 // Unsigned byte k of a word converted to float (v_cvt_f32_ubyte{k}).

@@ -69,7 +69,7 @@ struct AttnArgs {
   const float* k_cur;    // [kvh][hd]
   const float* v_cur;
   float* out;            // [qh][hd]
-  float* ws;             // [nsplit][qh][hd + 2]
+  float* ws;             // chunk records [nsplit][qh][hd + 2]
   const float* rope;     // model mode: [cap][hd/2][2] cos/sin table, else null
   float* k_store;        // model mode: cache slot base (k_cache), else null
   float* v_store;
@@ -82,7 +82,9 @@ hipError_t launch_attention(const AttnArgs& a, hipStream_t st);
 // Any-shape kernel; its workspace is [qh][hist + 1] floats.
 hipError_t launch_attention_naive(const AttnArgs& a, hipStream_t st);
 uint32_t attention_splits(uint32_t total_positions, uint32_t kvh);
-bool attention_supported(uint32_t qh, uint32_t kvh, uint32_t hd);
+uint64_t attention_ws_floats(uint32_t nsplit, uint32_t qh, uint32_t hd);
+// The split kernel handles this shape for up to `total_positions` positions.
+bool attention_supported(uint32_t qh, uint32_t kvh, uint32_t hd, uint64_t total_positions);
 
 // Elementwise (rf_elementwise.hip).
 hipError_t launch_rmsnorm(const float* x, const float* w, uint64_t n, float eps, float* y, hipStream_t st);

@@ -60,6 +60,7 @@ struct rf_model {
   float* rope = nullptr;     // [cap][hd/2][2]
   float *hidden = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attn_out = nullptr, *act = nullptr;
   float *logits = nullptr, *final_hidden = nullptr, *attn_ws = nullptr, *up_tmp = nullptr;
+  bool attn_fast = false;  // split kernel (else the any-shape kernel)
   float *xnorm = nullptr, *mvtmp = nullptr;  // scratch of the unfused fallback
   float* amax_val = nullptr;
   uint32_t* amax_idx = nullptr;
@@ -313,7 +314,7 @@ int32_t enqueue_attention(rf_model* m, size_t li) {
   a.qh = (uint32_t)c.head_count; a.kvh = (uint32_t)c.head_count_kv; a.hd = (uint32_t)hd;
   a.nsplit = m->nsplit;
   a.denom = sqrtf((float)hd);
-  RF_LAUNCH(launch_attention(a, st), "attention");
+  RF_LAUNCH(m->attn_fast ? launch_attention(a, st) : launch_attention_naive(a, st), "attention");
   return RF_OK;
 }
 
@@ -494,9 +495,12 @@ int32_t rf_model_create(rf_ctx* ctx, const rf_model_config* cfg, uint64_t kv_cap
   m->act = take(f); m->up_tmp = take(f); m->logits = take(c.vocab_size); m->final_hidden = take(d);
   m->xnorm = take(wide); m->mvtmp = take(widest);
   // attention workspace: fixed split count for the capacity (graph-friendly)
-  const bool fast = attention_supported((uint32_t)c.head_count, (uint32_t)c.head_count_kv, (uint32_t)c.head_dim);
+  const bool fast = attention_supported((uint32_t)c.head_count, (uint32_t)c.head_count_kv, (uint32_t)c.head_dim,
+                                        kv_cap);
+  m->attn_fast = fast;
   m->nsplit = fast ? attention_splits((uint32_t)kv_cap, (uint32_t)c.head_count_kv) : 1;
-  const uint64_t ws_floats = fast ? (uint64_t)m->nsplit * c.head_count * (c.head_dim + 2) : c.head_count * kv_cap;
+  const uint64_t ws_floats = fast ? attention_ws_floats(m->nsplit, (uint32_t)c.head_count, (uint32_t)c.head_dim)
+                                  : c.head_count * kv_cap;
   rc = charge_alloc(m, "workspace:model_attention", ws_floats * 4, &p);
   if (rc) { rf_model_destroy(m); return rc; }
   m->attn_ws = static_cast<float*>(p);

@@ -503,12 +503,12 @@ int32_t rf_attention_decode(rf_ctx* ctx, const float* q, const float* kh, const 
   a.hist = hist; a.qh = qh; a.kvh = kvh; a.hd = hd;
   a.denom = sqrtf((float)hd);
   auto aligned = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
-  const bool fast = attention_supported(qh, kvh, hd) && aligned(q) && aligned(kh) && aligned(vh) &&
+  const bool fast = attention_supported(qh, kvh, hd, total) && aligned(q) && (hist == 0 || (aligned(kh) && aligned(vh))) &&
                     aligned(kc) && aligned(vc);
   uint64_t ws_bytes;
   if (fast) {
     a.nsplit = attention_splits(total, kvh);
-    ws_bytes = (uint64_t)a.nsplit * qh * (hd + 2) * 4;
+    ws_bytes = attention_ws_floats(a.nsplit, qh, hd) * 4;
   } else {
     a.nsplit = 1;
     ws_bytes = (uint64_t)qh * total * 4;

@@ -288,6 +288,26 @@ def test_attention_shapes(ctx, orc, hist, qh, kvh, hd):
     _attention_case(ctx, orc, hist, qh, kvh, hd, 600 + hist + qh + hd)
 
 
+@pytest.mark.parametrize("hist,qh,kvh", [(63, 32, 8), (64, 32, 8), (127, 32, 8), (1023, 32, 8), (1087, 32, 8),
+                                         (1100, 64, 8), (20000, 32, 8), (5000, 8, 1)])
+def test_attention_chunk_tree(ctx, orc, hist, qh, kvh):
+    """Chunk counts around the in-kernel merge tree: one chunk (direct
+    output), up to 16 (one merge level), more (two levels, partly filled last
+    group).  Each case runs twice: the arrival counters must be back at zero."""
+    rf = _rf()
+    _attention_case(ctx, orc, hist, qh, kvh, 128, 900 + hist + qh)
+    rng = np.random.default_rng(hist)
+    hd = 128
+    arrs = [rng.normal(0, 1, n).astype(np.float32) for n in (qh * hd, max(hist, 1) * kvh * hd,
+                                                           max(hist, 1) * kvh * hd, kvh * hd, kvh * hd)]
+    dev = [ctx.array(x) for x in arrs]
+    first = rf.attention_checked(ctx, *dev, hist, qh, kvh, hd).numpy()
+    second = rf.attention_checked(ctx, *dev, hist, qh, kvh, hd).numpy()
+    assert np.array_equal(first.view(np.uint32), second.view(np.uint32))
+    for a in dev:
+        a.free()
+
+
 @pytest.mark.parametrize("ctx_len", [512, 2048, 8192])
 def test_attention_baseline_config(ctx, orc, ctx_len):
     """32 q heads, 8 KV heads, hd 128, RoPE theta 1e4 at
