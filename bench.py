@@ -109,6 +109,31 @@ def cpu_baseline(cfg, specs, tokens: int):
             "seconds_per_token": [round(p, 3) for p in per]}
 
 
+DOMINANT_KERNEL = "matvec_stream<Q8_0, EPI_SWIGLU> (ffn RMSNorm + gate/up + SiLU*up)"
+COPY_BYTES = 256 << 20
+
+
+def traffic_probe(ctx, m, cfg) -> int:
+    """Launch only what the HBM-traffic counters are read for: one forward
+    (so activations are defined), then the gate/up group of every layer once,
+    then four plain device copies of COPY_BYTES (the calibration kernel)."""
+    m.forward(1, 0)
+    ctx.synchronize()
+    ms, b, n = m.time_kernel("gateup", 1)
+    src = ctx.empty((COPY_BYTES,), "uint8", charge="probe:copy:src")
+    dst = ctx.empty((COPY_BYTES,), "uint8", charge="probe:copy:dst")
+    for _ in range(4):
+        ctx.copy(dst, src, COPY_BYTES)
+    ctx.synchronize()
+    print(json.dumps({"probe": "gateup", "kernel": DOMINANT_KERNEL, "launches": n, "algorithmic_bytes": b,
+                      "copy_bytes": COPY_BYTES, "copies": 4, "layers": cfg["block_count"]}), flush=True)
+    src.free()
+    dst.free()
+    m.close()
+    ctx.close()
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -120,6 +145,9 @@ def main() -> int:
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--kernel-reps", type=int, default=4)
     ap.add_argument("--tile-bytes", type=int, default=0, help="matvec LDS tile bytes (tuning)")
+    ap.add_argument("--traffic-probe", action="store_true",
+                    help="only launch the dominant kernel (32 gate/up launches) and a 256 MiB device copy, "
+                         "for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -142,6 +170,8 @@ def main() -> int:
     name, cus = ctx.device_info()
     log(f"device {name}, {cus} CUs; building 8B-shape Q8_0 model ({wbytes / 1e9:.2f} GB) in HBM")
     m = syn.build_device_model(ctx, cfg, specs, cap)
+    if args.traffic_probe:
+        return traffic_probe(ctx, m, cfg)
     prompt = [int(t) for t in np.random.default_rng(8).integers(0, cfg["vocab_size"], args.prompt)]
     t0 = time.perf_counter()
     for p, t in enumerate(prompt):
@@ -183,8 +213,7 @@ def main() -> int:
             traffic = None
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                 "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": traffic,
-                "kernel": "matvec_tiled<Q8_0, EPI_SWIGLU> (ffn RMSNorm + gate/up + SiLU*up)" if dom == "gateup"
-                else dom}
+                "kernel": DOMINANT_KERNEL if dom == "gateup" else dom}
     log(f"dominant group {dom}: {d['us_per_launch']} us/launch, {achieved:.0f} GB/s "
         f"({achieved / PEAK_HBM_GBS:.1%} of peak); kernel time per token {kernel_ms:.3f} ms")
     mv = matvec_q8_0_gbs(ctx, rf, syn)

@@ -111,6 +111,9 @@ int32_t rf_upload_async(rf_ctx *ctx, void *dst, const void *src, uint64_t bytes,
 int32_t rf_upload(rf_ctx *ctx, void *dst, const void *src, uint64_t bytes);
 int32_t rf_download(rf_ctx *ctx, void *dst, const void *src, uint64_t bytes);
 int32_t rf_memset(rf_ctx *ctx, void *dst, int32_t value, uint64_t bytes);
+/* Device -> device copy on `stream` (hipMemcpyAsync); no reference
+ * counterpart (the reference moves layer bytes host-side only). */
+int32_t rf_copy_async(rf_ctx *ctx, void *dst, const void *src, uint64_t bytes, rf_stream_t stream);
 
 /* Events for stream ordering and timing. */
 int32_t rf_event_create(rf_ctx *ctx, void **event);

@@ -203,6 +203,10 @@ class Context:
                                             _ptr(dst), dst.nbytes, stream))
 
     # events
+    def copy(self, dst, src, nbytes: int, stream=None) -> None:
+        """Device-to-device copy (hipMemcpyAsync on `stream`, default the compute stream)."""
+        _lib.check(self.lib.rf_copy_async(self.handle, _ptr(dst), _ptr(src), nbytes, stream))
+
     def event(self):
         e = C.c_void_p()
         _lib.check(self.lib.rf_event_create(self.handle, C.byref(e)))

@@ -75,6 +75,7 @@ SIGNATURES = {
     "rf_upload": (_i32, [_vp, _vp, _vp, _u64]),
     "rf_download": (_i32, [_vp, _vp, _vp, _u64]),
     "rf_memset": (_i32, [_vp, _vp, _i32, _u64]),
+    "rf_copy_async": (_i32, [_vp, _vp, _vp, _u64, _vp]),
     "rf_event_create": (_i32, [_vp, C.POINTER(_vp)]),
     "rf_event_destroy": (_i32, [_vp, _vp]),
     "rf_event_record": (_i32, [_vp, _vp, _vp]),

@@ -48,6 +48,7 @@ struct MvSegDesc {
 bool type_geometry(uint32_t t, uint64_t* qk, uint64_t* bs);
 MvPlan plan_matvec(uint32_t t, uint64_t in_dim, bool dual);
 void set_matvec_tile_bytes(uint32_t bytes);
+void set_matvec_stream_tile(uint32_t bytes);
 uint32_t matvec_tile_bytes();
 void set_matvec_stream(bool on);
 bool matvec_stream();

@@ -74,11 +74,22 @@ __device__ __forceinline__ void load_xunit(XUnit& xu, const float* __restrict__ 
   }
 }
 
+// Norm weights of unit u (same addressing as load_xunit).
+__device__ __forceinline__ void load_nwunit(float (&nw)[32], const float* __restrict__ w, uint32_t u) {
+  const float4* p = reinterpret_cast<const float4*>(w + 32u * u);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float4 v = p[i];
+    nw[4 * i] = v.x; nw[4 * i + 1] = v.y; nw[4 * i + 2] = v.z; nw[4 * i + 3] = v.w;
+  }
+}
+
 // RMSNorm prologue (core/src/compute.rs:291-319: x / sqrt(mean(x^2) + eps) * w),
 // with the reciprocal of the rms.  Threads of row group 0 hold every unit of x
-// exactly once, so sum(x^2) is a workgroup reduction of register values.
-__device__ __forceinline__ void norm_xunit(XUnit& xu, const float* __restrict__ nw, uint32_t u, bool first_group,
-                                           uint32_t in_dim, float eps, float* wsum, uint32_t tid, uint32_t nth) {
+// exactly once, so sum(x^2) is a workgroup reduction of register values.  The
+// weights arrive in registers (loaded with x, ahead of the weight tiles).
+__device__ __forceinline__ void norm_xunit(XUnit& xu, const float (&nw)[32], bool first_group, uint32_t in_dim,
+                                           float eps, float* wsum, uint32_t tid, uint32_t nth) {
   float ss = 0.f;
   if (first_group) {
 #pragma unroll
@@ -90,15 +101,8 @@ __device__ __forceinline__ void norm_xunit(XUnit& xu, const float* __restrict__ 
   float tot = 0.f;
   for (uint32_t i = 0; i < (nth >> 6); ++i) tot += wsum[i];
   const float inv = 1.0f / sqrtf(tot / (float)in_dim + eps);
-  const float4* w4 = reinterpret_cast<const float4*>(nw + 32u * u);
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const float4 w = w4[i];
-    xu.v[4 * i] = xu.v[4 * i] * inv * w.x;
-    xu.v[4 * i + 1] = xu.v[4 * i + 1] * inv * w.y;
-    xu.v[4 * i + 2] = xu.v[4 * i + 2] * inv * w.z;
-    xu.v[4 * i + 3] = xu.v[4 * i + 3] * inv * w.w;
-  }
+  for (int i = 0; i < 32; ++i) xu.v[i] = xu.v[i] * inv * nw[i];
 }
 
 __device__ __forceinline__ void finish_xunit(XUnit& xu) {
@@ -137,8 +141,13 @@ __global__ __launch_bounds__(1024) void matvec_tiled(MvArgs a) {
   const bool active = g < a.rg;
   XUnit xu;
   load_xunit(xu, a.x, u);
-  if (a.norm_w != nullptr) norm_xunit(xu, a.norm_w, u, active && g == 0, a.in_dim, a.eps, wsum, tid, nth);
-  else __syncthreads();
+  if (a.norm_w != nullptr) {
+    float nw[32];
+    load_nwunit(nw, a.norm_w, u);
+    norm_xunit(xu, nw, active && g == 0, a.in_dim, a.eps, wsum, tid, nth);
+  } else {
+    __syncthreads();
+  }
   finish_xunit(xu);
 
   const uint32_t blk = (u / UPB) * Fmt<T>::BS, sub = u % UPB;
@@ -256,19 +265,24 @@ __global__ __launch_bounds__(512) void matvec_stream(MvArgs a) {
   const uint32_t tid = threadIdx.x, nth = blockDim.x;
   const uint32_t ntiles = a.ntiles;
   uint32_t tile = blockIdx.x;
+  const uint32_t units = a.units;
+  const uint32_t u = tid % units, g = tid / units;
+  const bool active = g < a.rg;
+  // x and the norm weights are requested first (L2-resident, they return
+  // before the weight tile), so the RMSNorm prologue overlaps the tile fetch.
+  // Without a norm the x slice is loaded twice instead of branching around
+  // the loads.
+  XUnit xu;
+  load_xunit(xu, a.x, u);
+  float nw[32];
+  load_nwunit(nw, a.norm_w != nullptr ? a.norm_w : a.x, u);
   u32x4 pf[PF];
   TileRef cur{};
   if (tile < ntiles) {
     cur = tile_ref(a, tile, DUAL);
     tile_prefetch(pf, cur, tid, nth);
   }
-
-  const uint32_t units = a.units;
-  const uint32_t u = tid % units, g = tid / units;
-  const bool active = g < a.rg;
-  XUnit xu;
-  load_xunit(xu, a.x, u);
-  if (a.norm_w != nullptr) norm_xunit(xu, a.norm_w, u, active && g == 0, a.in_dim, a.eps, wsum, tid, nth);
+  if (a.norm_w != nullptr) norm_xunit(xu, nw, active && g == 0, a.in_dim, a.eps, wsum, tid, nth);
   finish_xunit(xu);
 
   const uint32_t row_bytes = a.row_bytes;
@@ -389,6 +403,8 @@ bool type_geometry(uint32_t t, uint64_t* qk, uint64_t* bs) {
 
 static uint32_t g_tile_target = 32768;  // LDS bytes per one-shot matvec tile (tunable)
 static bool g_stream_enabled = true;    // persistent streaming kernel where eligible
+static uint32_t g_stream_tile_cap = 57344;  // bytes of one streaming tile (tunable)
+void set_matvec_stream_tile(uint32_t bytes) { g_stream_tile_cap = bytes < 2048 ? 2048 : (bytes > 57344 ? 57344 : bytes); }
 void set_matvec_tile_bytes(uint32_t bytes) { g_tile_target = bytes < 4096 ? 4096 : (bytes > 61440 ? 61440 : bytes); }
 uint32_t matvec_tile_bytes() { return g_tile_target; }
 void set_matvec_stream(bool on) { g_stream_enabled = on; }
@@ -436,7 +452,7 @@ MvPlan plan_matvec(uint32_t t, uint64_t in_dim, bool dual) {
   const uint64_t sthreads = (units * rg + 63) / 64 * 64;
   if (rb % 16 == 0 && sthreads <= 512) {
     uint64_t tile_cap = 16ull * PF * sthreads;
-    if (tile_cap > 57344) tile_cap = 57344;
+    if (tile_cap > g_stream_tile_cap) tile_cap = g_stream_tile_cap;
     const uint64_t per_row = rb * (dual ? 2 : 1);
     uint64_t rows = tile_cap / per_row;
     if (rows > rg * 8) rows = rg * 8;

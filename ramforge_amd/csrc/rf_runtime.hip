@@ -380,6 +380,14 @@ int32_t rf_memset(rf_ctx* ctx, void* dst, int32_t value, uint64_t bytes) {
   return RF_OK;
 }
 
+int32_t rf_copy_async(rf_ctx* ctx, void* dst, const void* src, uint64_t bytes, rf_stream_t s) {
+  RF_CHECK_CTX(ctx);
+  if (bytes == 0) return RF_OK;
+  if (!dst || !src) return set_error(RF_ERR_INVALID, "null copy pointer");
+  RF_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, pick_stream(ctx, s)), "hipMemcpyAsync");
+  return RF_OK;
+}
+
 int32_t rf_event_create(rf_ctx* ctx, void** ev) {
   RF_CHECK_CTX(ctx);
   hipEvent_t e;
