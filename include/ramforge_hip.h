@@ -138,6 +138,25 @@ int32_t rf_matvec(rf_ctx *ctx, uint32_t ggml_type, const void *w, uint64_t w_byt
                   uint64_t in_dim, const float *x, float *y, uint64_t row_start, uint64_t row_count,
                   rf_stream_t stream);
 
+/* Device-native ("packed") layout of Q8_0 and Q4_0 tensors, used by the
+ * model for its weights.  No counterpart in the reference, which reads GGUF
+ * blocks as stored; the arithmetic of rf_matvec_packed is that of
+ * quant::matvec_q8_0 / matvec_q4_0 (quant.rs:913-1029).  Layout of a
+ * [rows][in_dim] tensor, same byte count as the GGUF payload: the code bytes
+ * of all rows (in_dim bytes per row for Q8_0, in_dim/2 for Q4_0, each block's
+ * 16 Q4_0 bytes in GGUF order), then the f16 block scales of all rows
+ * (in_dim/32 per row).  rf_pack_weights converts a GGUF payload (raw and
+ * packed must not overlap); rf_packed_supported(type, in_dim) is 1 when the
+ * packed kernel covers the shape (Q8_0/Q4_0, in_dim % 32 == 0, in_dim <= 16384). */
+int32_t rf_packed_supported(uint32_t ggml_type, uint64_t in_dim);
+int32_t rf_pack_weights(rf_ctx *ctx, uint32_t ggml_type, const void *raw, uint64_t raw_bytes, uint64_t rows,
+                        uint64_t in_dim, void *packed, uint64_t packed_bytes, rf_stream_t stream);
+/* rf_matvec on a packed tensor: same arguments, validation, row-range and
+ * error rules (packed_bytes plays the role of w_bytes). */
+int32_t rf_matvec_packed(rf_ctx *ctx, uint32_t ggml_type, const void *packed, uint64_t packed_bytes,
+                         uint64_t out_dim, uint64_t in_dim, const float *x, float *y, uint64_t row_start,
+                         uint64_t row_count, rf_stream_t stream);
+
 /* Bit-exact row decode: rows [row_start, row_start + row_count) of a
  * [rows, in_dim] GGUF tensor into out[row_count][in_dim].  Replaces
  * dequantize_row_<fmt> (quant.rs:615-868) and decode_row_to_f32
@@ -282,6 +301,11 @@ uint32_t rf_tune_matvec_tile_bytes(uint32_t bytes);
  * are 16-byte aligned (default), 0 = one-shot tile kernel everywhere, other
  * values only query.  Returns the mode in effect (process-wide). */
 int32_t rf_tune_matvec_kernel(int32_t mode);
+/* Weight layout of models created afterwards: 1 = Q8_0 / Q4_0 projection
+ * weights are repacked at install into the device-native layout (default),
+ * 0 = kept as GGUF bytes; other values only query.  Applies to tensors
+ * installed after the call.  Returns the mode in effect (process-wide). */
+int32_t rf_tune_packed_weights(int32_t mode);
 
 #ifdef __cplusplus
 }

@@ -240,6 +240,32 @@ def matvec(ctx: Context, ggml_type: int, w, w_shape: Sequence[int], x, y, row_st
     _lib.check(rc)
 
 
+def packed_supported(ggml_type: int, in_dim: int) -> bool:
+    """Whether the packed (device-native) layout and kernel cover (type, in_dim)."""
+    return bool(_lib.load().rf_packed_supported(ggml_type, in_dim))
+
+
+def pack_weights(ctx: Context, ggml_type: int, raw, rows: int, in_dim: int, packed, raw_bytes: Optional[int] = None,
+                 stream=None) -> None:
+    """GGUF Q8_0 / Q4_0 payload [rows][in_dim] -> packed layout (codes of all
+    rows, then the f16 scales of all rows; same byte count)."""
+    rb = raw.nbytes if (raw_bytes is None and isinstance(raw, DeviceArray)) else int(raw_bytes or 0)
+    pb = packed.nbytes if isinstance(packed, DeviceArray) else rb
+    _lib.check(ctx.lib.rf_pack_weights(ctx.handle, ggml_type, _ptr(raw), rb, rows, in_dim, _ptr(packed), pb, stream))
+
+
+def matvec_packed(ctx: Context, ggml_type: int, w, w_shape: Sequence[int], x, y, row_start: int = 0,
+                  row_count: Optional[int] = None, w_bytes: Optional[int] = None, stream=None) -> None:
+    """matvec() on a packed tensor (see pack_weights)."""
+    if len(w_shape) != 2:
+        raise RamforgeError(_lib.RF_ERR_INVALID, f"{GGML.NAMES.get(ggml_type, ggml_type)} matvec expects 2D weight")
+    out_dim, in_dim = (int(v) for v in w_shape)
+    wb = w.nbytes if (w_bytes is None and isinstance(w, DeviceArray)) else int(w_bytes or 0)
+    rc = ctx.lib.rf_matvec_packed(ctx.handle, ggml_type, _ptr(w), wb, out_dim, in_dim, _ptr(x), _ptr(y), row_start,
+                                  RF_ALL_ROWS if row_count is None else row_count, stream)
+    _lib.check(rc)
+
+
 def dequantize_rows(ctx: Context, ggml_type: int, w, in_dim: int, row_start: int, row_count: int, out,
                     w_bytes: Optional[int] = None, stream=None) -> None:
     """dequantize_row_<fmt> (quant.rs:615-868) for a row range, bit-exact."""
@@ -451,6 +477,13 @@ def tune_matvec_kernel(mode: int = -1) -> int:
     """1: persistent streaming matvec (default), 0: one-shot tile kernel;
     -1 queries.  Returns the mode in effect."""
     return _lib.load().rf_tune_matvec_kernel(mode)
+
+
+def tune_packed_weights(mode: int = -1) -> int:
+    """1: Q8_0 / Q4_0 projection weights of models are repacked into the
+    device-native layout at install (default), 0: kept as GGUF bytes; -1
+    queries.  Returns the mode in effect."""
+    return _lib.load().rf_tune_packed_weights(mode)
 
 
 # Fail loudly at import if the HIP library was not built.

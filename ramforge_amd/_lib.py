@@ -76,6 +76,9 @@ SIGNATURES = {
     "rf_download": (_i32, [_vp, _vp, _vp, _u64]),
     "rf_memset": (_i32, [_vp, _vp, _i32, _u64]),
     "rf_copy_async": (_i32, [_vp, _vp, _vp, _u64, _vp]),
+    "rf_packed_supported": (_i32, [_u32, _u64]),
+    "rf_pack_weights": (_i32, [_vp, _u32, _vp, _u64, _u64, _u64, _vp, _u64, _vp]),
+    "rf_matvec_packed": (_i32, [_vp, _u32, _vp, _u64, _u64, _u64, _fp, _fp, _u64, _u64, _vp]),
     "rf_event_create": (_i32, [_vp, C.POINTER(_vp)]),
     "rf_event_destroy": (_i32, [_vp, _vp]),
     "rf_event_record": (_i32, [_vp, _vp, _vp]),
@@ -109,6 +112,7 @@ SIGNATURES = {
     "rf_model_time_kernel": (_i32, [_vp, _u32, _u32, C.POINTER(_f32), C.POINTER(_u64), C.POINTER(_u64)]),
     "rf_tune_matvec_tile_bytes": (_u32, [_u32]),
     "rf_tune_matvec_kernel": (_i32, [_i32]),
+    "rf_tune_packed_weights": (_i32, [_i32]),
 }
 
 _LIB = None

@@ -56,6 +56,46 @@ hipError_t launch_matvec_segments(uint32_t t, const MvSegDesc* segs, int nseg, c
                                   const float* norm_w, float eps, uint64_t in_dim, int epi,
                                   hipStream_t st);
 
+// Matvec on the packed layout of Q8_0 / Q4_0 (rf_matvec_packed.hip): codes of
+// all rows (row-major, in or in/2 bytes per row), then the f16 block scales of
+// all rows.  Same byte count as the GGUF payload.
+struct PkSeg {
+  const uint8_t* codes;      // first code byte of the segment's first row
+  const uint16_t* scales;    // its first scale
+  const uint8_t* codes_up;   // EPI_SWIGLU: the "up" matrix
+  const uint16_t* scales_up;
+  float* y;
+  const float* res;
+  uint32_t row_begin;        // first row of the segment among all segments
+};
+struct PkArgs {
+  PkSeg seg[3];
+  uint32_t nseg, rows_total;
+  const float* x;
+  const float* norm_w;
+  float eps;
+  uint32_t in_dim, kw;
+};
+struct PkPlan {
+  bool ok;
+  uint32_t lpw, kw;
+};
+struct PkSegDesc {
+  const void* packed;     // packed matrix base (codes of row 0)
+  const void* packed_up;  // EPI_SWIGLU: packed "up" matrix, same shape
+  uint64_t matrix_rows;   // rows of the whole packed matrix (locates the scales)
+  uint64_t row_start;     // first row of this segment within the matrix
+  uint64_t rows;
+  float* y;
+  const float* res;
+};
+bool packed_type(uint32_t t);
+PkPlan plan_packed(uint32_t t, uint64_t in_dim);
+hipError_t launch_matvec_packed(uint32_t t, const PkSegDesc* segs, int nseg, const float* x, const float* norm_w,
+                                float eps, uint64_t in_dim, int epi, hipStream_t st);
+// GGUF payload [rows][in_dim] -> packed layout (distinct buffers).
+hipError_t launch_pack(uint32_t t, const void* raw, void* packed, uint64_t rows, uint64_t in_dim, hipStream_t st);
+
 // Bit-exact row decode: rows [0, rows) of `w` (row_bytes each) -> out[rows][in_dim].
 // If token_index != nullptr the single row *token_index is decoded instead.
 hipError_t launch_dequant_rows(uint32_t t, const void* w, uint64_t in_dim, uint64_t rows,

@@ -38,8 +38,13 @@ struct DevTensor {
   uint64_t ne0 = 0, ne1 = 0, nbytes = 0;
   void* d = nullptr;
   std::string charge;
+  bool packed = false;  // device-native layout (rf_matvec_packed.hip), else GGUF bytes
   bool present() const { return d != nullptr; }
 };
+
+// Projection weights in Q8_0 / Q4_0 are repacked at install unless disabled
+// (rf_tune_packed_weights); the embedding stays in GGUF layout for its row gather.
+static int g_pack_weights = 1;
 
 struct Layer {
   DevTensor attn_norm, q, k, v, o, ffn_norm, gate, up, down, bq, bk, bv;
@@ -155,6 +160,20 @@ int32_t check_tensor_shape(rf_model* m, const std::string& name, uint32_t t, uin
 
 // Upload (or synthesize) one tensor.  F16/BF16 payloads are decoded to F32 on
 // the device, as TensorData decodes them at load (core/src/tensor.rs:460-521).
+// The matrices the decode step multiplies (everything but the embedding, the
+// norms and the biases).
+bool is_projection(const std::string& name) {
+  if (name == "output.weight") return true;
+  static const char* sfx[] = {".attn_q.weight", ".attn_k.weight", ".attn_v.weight", ".attn_output.weight",
+                              ".ffn_gate.weight", ".ffn_up.weight", ".ffn_down.weight"};
+  if (name.rfind("blk.", 0) != 0) return false;
+  for (const char* x : sfx) {
+    const size_t n = strlen(x);
+    if (name.size() > n && name.compare(name.size() - n, n, x) == 0) return true;
+  }
+  return false;
+}
+
 int32_t install(rf_model* m, const char* cname, uint32_t t, uint64_t ne0, uint64_t ne1, const void* host,
                 uint64_t nbytes, bool synth, uint64_t seed, double mul, float constant) {
   if (!m || !cname) return set_error(RF_ERR_INVALID, "null model or tensor name");
@@ -207,12 +226,27 @@ int32_t install(rf_model* m, const char* cname, uint32_t t, uint64_t ne0, uint64
     rc = staged_upload(ctx, d, host, bytes);
     if (rc) return rc;
   }
+  bool packed = false;
+  if (g_pack_weights && is_projection(name) && plan_packed(t, ne0).ok) {
+    // GGUF -> packed through a temporary copy (install time only)
+    void* tmp = nullptr;
+    rc = vram_alloc(ctx, "tmp:pack:" + name, bytes, &tmp);
+    if (rc) return rc;
+    e = launch_pack(t, d, tmp, ne1, ne0, ctx->compute);
+    if (e == hipSuccess) e = hipMemcpyAsync(d, tmp, bytes, hipMemcpyDeviceToDevice, ctx->compute);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->compute);
+    const int32_t rc2 = vram_release(ctx, "tmp:pack:" + name);
+    if (e != hipSuccess) return hip_error(e, "weight packing");
+    if (rc2) return rc2;
+    packed = true;
+  }
   slot->type = widen ? T_F32 : t;
   slot->ne0 = ne0;
   slot->ne1 = ne1;
   slot->nbytes = final_bytes;
   slot->d = d;
   slot->charge = charge;
+  slot->packed = packed;
   return RF_OK;
 }
 
@@ -237,12 +271,35 @@ int32_t check_ready(rf_model* m) {
     if (_e != hipSuccess) return hip_error(_e, what);       \
   } while (0)
 
-// A fused matvec launch, or — when a row does not fit the LDS tile (very wide
-// F32 rows) — the same computation as separate kernels: RMSNorm into xnorm,
-// rowwise matvec, then the residual / SiLU*up epilogue.
-hipError_t fused_matvec(rf_model* m, uint32_t t, const MvSegDesc* segs, int nseg, const float* x,
-                        const float* norm_w, uint64_t in_dim, int epi) {
+// One output segment of a model matvec: a weight tensor (and its "up" pair
+// for SiLU(gate)*up), the output and the residual input.
+struct MSeg {
+  const DevTensor* w;
+  const DevTensor* w_up;
+  float* y;
+  const float* res;
+  uint64_t rows;
+};
+
+// A fused matvec launch over segments of one type and layout: the packed
+// kernel for packed tensors; else the GGUF-layout kernels, or — when a row
+// does not fit the LDS tile (very wide F32 rows) — the same computation as
+// separate kernels: RMSNorm into xnorm, rowwise matvec, then the residual /
+// SiLU*up epilogue.
+hipError_t fused_matvec(rf_model* m, const MSeg* ms, int nseg, const float* x, const float* norm_w, uint64_t in_dim,
+                        int epi) {
   hipStream_t st = m->ctx->compute;
+  const uint32_t t = ms[0].w->type;
+  if (ms[0].w->packed) {
+    PkSegDesc ps[3];
+    for (int i = 0; i < nseg; ++i)
+      ps[i] = PkSegDesc{ms[i].w->d, ms[i].w_up ? ms[i].w_up->d : nullptr, ms[i].w->ne1, 0, ms[i].rows, ms[i].y,
+                        ms[i].res};
+    return launch_matvec_packed(t, ps, nseg, x, norm_w, m->cfg.rms_eps, in_dim, epi, st);
+  }
+  MvSegDesc segs[3];
+  for (int i = 0; i < nseg; ++i)
+    segs[i] = MvSegDesc{ms[i].w->d, ms[i].w_up ? ms[i].w_up->d : nullptr, ms[i].y, ms[i].res, ms[i].rows};
   const bool x_vec = (reinterpret_cast<uintptr_t>(x) & 15u) == 0 && (reinterpret_cast<uintptr_t>(norm_w) & 15u) == 0;
   if (plan_matvec(t, in_dim, epi == EPI_SWIGLU).tiled && x_vec)
     return launch_matvec_segments(t, segs, nseg, x, norm_w, m->cfg.rms_eps, in_dim, epi, st);
@@ -283,15 +340,16 @@ int32_t enqueue_qkv(rf_model* m, size_t li) {
   float* outs[3] = {m->q, m->k, m->v};
   const uint64_t rows[3] = {qd, kvd, kvd};
   int i = 0;
-  while (i < 3) {
-    MvSegDesc segs[3];
+  while (i < 3) {  // consecutive projections of one type and layout share a launch
+    MSeg segs[3];
     int n = 0;
     const uint32_t t = qkv[i]->type;
-    while (i < 3 && qkv[i]->type == t) {
-      segs[n++] = MvSegDesc{qkv[i]->d, nullptr, outs[i], nullptr, rows[i]};
+    const bool pk = qkv[i]->packed;
+    while (i < 3 && qkv[i]->type == t && qkv[i]->packed == pk) {
+      segs[n++] = MSeg{qkv[i], nullptr, outs[i], nullptr, rows[i]};
       ++i;
     }
-    RF_LAUNCH(fused_matvec(m, t, segs, n, m->hidden, attn_norm, d, EPI_STORE), "qkv matvec");
+    RF_LAUNCH(fused_matvec(m, segs, n, m->hidden, attn_norm, d, EPI_STORE), "qkv matvec");
   }
   if (L.bq.present()) {
     RF_LAUNCH(launch_bias_add(m->q, static_cast<const float*>(L.bq.d), qd, st), "bias");
@@ -323,9 +381,8 @@ int32_t enqueue_oproj(rf_model* m, size_t li) {
   const rf_model_config& c = m->cfg;
   Layer& L = m->layers[li];
   const uint64_t d = c.embedding_length, qd = c.head_count * c.head_dim;
-  MvSegDesc s{L.o.d, nullptr, m->hidden, m->hidden, d};
-  RF_LAUNCH(fused_matvec(m, L.o.type, &s, 1, m->attn_out, nullptr, qd, EPI_RESIDUAL),
-            "o-proj");
+  MSeg s{&L.o, nullptr, m->hidden, m->hidden, d};
+  RF_LAUNCH(fused_matvec(m, &s, 1, m->attn_out, nullptr, qd, EPI_RESIDUAL), "o-proj");
   return RF_OK;
 }
 
@@ -336,16 +393,15 @@ int32_t enqueue_gateup(rf_model* m, size_t li) {
   hipStream_t st = m->ctx->compute;
   const uint64_t d = c.embedding_length, f = c.feed_forward_length;
   const float* ffn_norm = static_cast<const float*>(L.ffn_norm.d);
-  if (L.gate.type == L.up.type) {
-    MvSegDesc s{L.gate.d, L.up.d, m->act, nullptr, f};
-    RF_LAUNCH(fused_matvec(m, L.gate.type, &s, 1, m->hidden, ffn_norm, d, EPI_SWIGLU),
-              "gate/up");
+  if (L.gate.type == L.up.type && L.gate.packed == L.up.packed) {
+    MSeg s{&L.gate, &L.up, m->act, nullptr, f};
+    RF_LAUNCH(fused_matvec(m, &s, 1, m->hidden, ffn_norm, d, EPI_SWIGLU), "gate/up");
   } else {
     float* up_tmp = m->up_tmp;
-    MvSegDesc sg{L.gate.d, nullptr, m->act, nullptr, f};
-    MvSegDesc su{L.up.d, nullptr, up_tmp, nullptr, f};
-    RF_LAUNCH(fused_matvec(m, L.gate.type, &sg, 1, m->hidden, ffn_norm, d, EPI_STORE), "gate");
-    RF_LAUNCH(fused_matvec(m, L.up.type, &su, 1, m->hidden, ffn_norm, d, EPI_STORE), "up");
+    MSeg sg{&L.gate, nullptr, m->act, nullptr, f};
+    MSeg su{&L.up, nullptr, up_tmp, nullptr, f};
+    RF_LAUNCH(fused_matvec(m, &sg, 1, m->hidden, ffn_norm, d, EPI_STORE), "gate");
+    RF_LAUNCH(fused_matvec(m, &su, 1, m->hidden, ffn_norm, d, EPI_STORE), "up");
     RF_LAUNCH(launch_binary(BIN_SWIGLU, m->act, up_tmp, f, m->act, st), "swiglu");
   }
   return RF_OK;
@@ -356,9 +412,8 @@ int32_t enqueue_down(rf_model* m, size_t li) {
   const rf_model_config& c = m->cfg;
   Layer& L = m->layers[li];
   const uint64_t d = c.embedding_length, f = c.feed_forward_length;
-  MvSegDesc s{L.down.d, nullptr, m->hidden, m->hidden, d};
-  RF_LAUNCH(fused_matvec(m, L.down.type, &s, 1, m->act, nullptr, f, EPI_RESIDUAL),
-            "down");
+  MSeg s{&L.down, nullptr, m->hidden, m->hidden, d};
+  RF_LAUNCH(fused_matvec(m, &s, 1, m->act, nullptr, f, EPI_RESIDUAL), "down");
   return RF_OK;
 }
 
@@ -411,9 +466,9 @@ int32_t enqueue_forward(rf_model* m) {
 int32_t enqueue_logits(rf_model* m) {
   const rf_model_config& c = m->cfg;
   const DevTensor& w = m->output.present() ? m->output : m->token_embd;
-  MvSegDesc s{w.d, nullptr, m->logits, nullptr, c.vocab_size};
-  RF_LAUNCH(fused_matvec(m, w.type, &s, 1, m->hidden, static_cast<const float*>(m->output_norm.d),
-                         c.embedding_length, EPI_STORE),
+  MSeg s{&w, nullptr, m->logits, nullptr, c.vocab_size};
+  RF_LAUNCH(fused_matvec(m, &s, 1, m->hidden, static_cast<const float*>(m->output_norm.d), c.embedding_length,
+                         EPI_STORE),
             "logits");
   return RF_OK;
 }
@@ -712,6 +767,11 @@ int32_t rf_model_time_kernel(rf_model* m, uint32_t kind, uint32_t reps, float* a
   *bytes_per_launch = bytes / n;
   *launches = n;
   return RF_OK;
+}
+
+int32_t rf_tune_packed_weights(int32_t mode) {
+  if (mode == 0 || mode == 1) g_pack_weights = mode;
+  return g_pack_weights;
 }
 
 int32_t rf_model_read_tokens(rf_model* m, uint32_t* out, uint64_t n) {

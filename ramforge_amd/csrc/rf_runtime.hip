@@ -427,9 +427,14 @@ int32_t rf_event_synchronize(rf_ctx* ctx, void* ev) {
 }
 
 // ------------------------------------------------------------------ matvec
-int32_t rf_matvec(rf_ctx* ctx, uint32_t t, const void* w, uint64_t w_bytes, uint64_t out_dim, uint64_t in_dim,
-                  const float* x, float* y, uint64_t row_start, uint64_t row_count, rf_stream_t s) {
-  RF_CHECK_CTX(ctx);
+// Shared argument validation of the matvec entry points, in the reference's
+// order and wording (quant.rs:907-975, backend.rs:173-199).  On success
+// *count is the number of rows to compute and *rb the bytes per row; a zero
+// count or in_dim has already been handled (*done = true).
+static int32_t validate_matvec(rf_ctx* ctx, uint32_t t, const void* w, uint64_t w_bytes, uint64_t out_dim,
+                               uint64_t in_dim, const float* x, float* y, uint64_t row_start, uint64_t row_count,
+                               rf_stream_t s, uint64_t* count_out, uint64_t* rb_out, bool* done) {
+  *done = false;
   uint64_t qk = 0, bs = 0;
   if (!type_geometry(t, &qk, &bs))
     return set_error(RF_ERR_UNSUPPORTED, "matvec does not support tensor type %s (%u)", type_name(t), t);
@@ -457,16 +462,88 @@ int32_t rf_matvec(rf_ctx* ctx, uint32_t t, const void* w, uint64_t w_bytes, uint
     return set_error(RF_ERR_INVALID, "%s weight truncated: expected %llu bytes, got %llu", nm,
                      (unsigned long long)(out_dim * rb), (unsigned long long)w_bytes);
   }
-  if (count == 0) return RF_OK;
+  *count_out = count;
+  *rb_out = rb;
+  if (count == 0) {
+    *done = true;
+    return RF_OK;
+  }
   if (in_dim == 0) {
+    *done = true;
     hipError_t e = launch_fill(y, 0.f, count, pick_stream(ctx, s));
     return e == hipSuccess ? RF_OK : hip_error(e, "fill");
   }
   if (count > 0xFFFFFFFFull || rb > 0xFFFFFFFFull)
     return set_error(RF_ERR_UNSUPPORTED, "%s matvec shape exceeds 32-bit row indexing", nm);
+  return RF_OK;
+}
+
+int32_t rf_matvec(rf_ctx* ctx, uint32_t t, const void* w, uint64_t w_bytes, uint64_t out_dim, uint64_t in_dim,
+                  const float* x, float* y, uint64_t row_start, uint64_t row_count, rf_stream_t s) {
+  RF_CHECK_CTX(ctx);
+  uint64_t count = 0, rb = 0;
+  bool done = false;
+  int32_t rc = validate_matvec(ctx, t, w, w_bytes, out_dim, in_dim, x, y, row_start, row_count, s, &count, &rb,
+                               &done);
+  if (rc || done) return rc;
   MvSegDesc seg{static_cast<const uint8_t*>(w) + row_start * rb, nullptr, y, nullptr, count};
   hipError_t e = launch_matvec_segments(t, &seg, 1, x, nullptr, 0.f, in_dim, EPI_STORE, pick_stream(ctx, s));
   if (e != hipSuccess) return hip_error(e, "matvec launch");
+  return RF_OK;
+}
+
+int32_t rf_packed_supported(uint32_t t, uint64_t in_dim) { return plan_packed(t, in_dim).ok ? 1 : 0; }
+
+int32_t rf_pack_weights(rf_ctx* ctx, uint32_t t, const void* raw, uint64_t raw_bytes, uint64_t rows, uint64_t in_dim,
+                        void* packed, uint64_t packed_bytes, rf_stream_t s) {
+  RF_CHECK_CTX(ctx);
+  if (!packed_type(t))
+    return set_error(RF_ERR_UNSUPPORTED, "packed layout does not support tensor type %s (%u)", type_name(t), t);
+  const char* nm = type_name(t);
+  if (!raw || !packed) return set_error(RF_ERR_INVALID, "%s pack received a null pointer", nm);
+  if (in_dim % 32 != 0)
+    return set_error(RF_ERR_INVALID, "%s in_dim %llu not divisible by 32", nm, (unsigned long long)in_dim);
+  const uint64_t need = rows * (in_dim / 32) * (t == T_Q8_0 ? 34 : 18);
+  if (raw_bytes < need)
+    return set_error(RF_ERR_INVALID, "%s weight truncated: expected %llu bytes, got %llu", nm,
+                     (unsigned long long)need, (unsigned long long)raw_bytes);
+  if (packed_bytes < need)
+    return set_error(RF_ERR_INVALID, "%s packed buffer holds %llu bytes, %llu needed", nm,
+                     (unsigned long long)packed_bytes, (unsigned long long)need);
+  const uint8_t* r8 = static_cast<const uint8_t*>(raw);
+  const uint8_t* p8 = static_cast<const uint8_t*>(packed);
+  if (p8 < r8 + need && r8 < p8 + need) return set_error(RF_ERR_INVALID, "%s pack buffers overlap", nm);
+  hipError_t e = launch_pack(t, raw, packed, rows, in_dim, pick_stream(ctx, s));
+  if (e != hipSuccess) return hip_error(e, "pack launch");
+  return RF_OK;
+}
+
+int32_t rf_matvec_packed(rf_ctx* ctx, uint32_t t, const void* packed, uint64_t packed_bytes, uint64_t out_dim,
+                         uint64_t in_dim, const float* x, float* y, uint64_t row_start, uint64_t row_count,
+                         rf_stream_t s) {
+  RF_CHECK_CTX(ctx);
+  if (!packed_type(t))
+    return set_error(RF_ERR_UNSUPPORTED, "packed matvec does not support tensor type %s (%u)", type_name(t), t);
+  uint64_t count = 0, rb = 0;
+  bool done = false;
+  int32_t rc = validate_matvec(ctx, t, packed, packed_bytes, out_dim, in_dim, x, y, row_start, row_count, s, &count,
+                               &rb, &done);
+  if (rc || done) return rc;
+  if (!plan_packed(t, in_dim).ok)
+    return set_error(RF_ERR_UNSUPPORTED, "packed %s matvec supports in_dim up to 16384, got %llu", type_name(t),
+                     (unsigned long long)in_dim);
+  hipStream_t st = pick_stream(ctx, s);
+  const float* xa = x;
+  if ((reinterpret_cast<uintptr_t>(x) & 15u) != 0) {
+    // the kernel reads x with 16-byte loads: stage a misaligned x in the context scratch
+    rc = ensure_workspace(ctx, ctx->scratch_ws, "workspace:scratch", in_dim * 4);
+    if (rc) return rc;
+    RF_HIP(hipMemcpyAsync(ctx->scratch_ws.ptr, x, in_dim * 4, hipMemcpyDeviceToDevice, st), "hipMemcpyAsync");
+    xa = static_cast<const float*>(ctx->scratch_ws.ptr);
+  }
+  PkSegDesc seg{packed, nullptr, out_dim, row_start, count, y, nullptr};
+  hipError_t e = launch_matvec_packed(t, &seg, 1, xa, nullptr, 0.f, in_dim, EPI_STORE, st);
+  if (e != hipSuccess) return hip_error(e, "packed matvec launch");
   return RF_OK;
 }
 

@@ -157,6 +157,84 @@ def test_matvec_unaligned_pointers(ctx, orc, t, kernel_mode):
     _check_matvec(ctx, orc, t, 70, 512, 370 + t, x_off=8, w_off=6, row_start=5, row_count=40)
 
 
+def _pack_host(t, raw, rows, in_dim):
+    """Packed layout built on the host from the GGUF bytes (codes of all rows,
+    then the f16 scale bits of all rows)."""
+    qk, bs = GEOM[t]
+    blocks = raw.reshape(rows * in_dim // 32, bs)
+    return np.concatenate([blocks[:, 2:].reshape(-1), blocks[:, :2].reshape(-1)])
+
+
+@pytest.mark.parametrize("t", [Q8_0, Q4_0])
+def test_pack_weights_layout_is_exact(ctx, t):
+    rf = _rf()
+    rng = np.random.default_rng(40 + t)
+    for rows, in_dim in ((3, 32), (17, 4096), (5, 14336)):
+        raw = random_matrix(t, rows, in_dim, rng)
+        w = ctx.array(raw)
+        p = ctx.empty((raw.nbytes,), np.uint8)
+        rf.pack_weights(ctx, t, w, rows, in_dim, p)
+        assert np.array_equal(p.numpy(), _pack_host(t, raw, rows, in_dim)), (NAMES[t], rows, in_dim)
+        w.free()
+        p.free()
+
+
+def _check_matvec_packed(ctx, orc, t, out_dim, in_dim, seed, row_start=0, row_count=None, x_off=0):
+    rf = _rf()
+    rng = np.random.default_rng(seed)
+    raw = random_matrix(t, out_dim, in_dim, rng)
+    x = rng.normal(0, 1, in_dim).astype(np.float32)
+    print(f"  packed matvec {NAMES[t]} out={out_dim} in={in_dim} rows={row_start}+{row_count} seed={seed} "
+          f"x_off={x_off}", flush=True)
+    w = ctx.array(_pack_host(t, raw, out_dim, in_dim))
+    xd = ctx.array(np.concatenate([np.zeros(x_off, np.uint8), x.view(np.uint8)]))
+    n = out_dim - row_start if row_count is None else row_count
+    y = ctx.empty((n,))
+    rf.matvec_packed(ctx, t, w, (out_dim, in_dim), xd.ptr + x_off, y, row_start, row_count)
+    got = y.numpy()
+    ref = orc.dispatch_matvec(t, raw, in_dim, out_dim, x, 16)[row_start:row_start + n]
+    wdec = orc.dequantize_rows(t, raw, in_dim, out_dim)[row_start:row_start + n].astype(np.float64)
+    scale = np.abs(wdec) @ np.abs(x.astype(np.float64))
+    err = assert_close_scaled(got, ref, scale, TOL, what=f"packed {NAMES[t]} {out_dim}x{in_dim}")
+    assert np.all(np.abs(got - wdec @ x.astype(np.float64)) <= scale * 64 * 2.0 ** -24), NAMES[t]
+    print(f"    scaled rel err vs oracle {err:.2e}", flush=True)
+    for a in (w, xd, y):
+        a.free()
+
+
+@pytest.mark.parametrize("t", [Q8_0, Q4_0])
+@pytest.mark.parametrize("out_dim,in_dim", [(1, 32), (67, 96), (130, 1024), (33, 2048), (70, 3072), (257, 4096),
+                                            (1000, 5120), (4096, 4096), (14336, 4096), (4096, 14336), (9, 16384)])
+def test_matvec_packed_shapes(ctx, orc, t, out_dim, in_dim):
+    _check_matvec_packed(ctx, orc, t, out_dim, in_dim, 1200 + t + in_dim % 977 + out_dim)
+
+
+@pytest.mark.parametrize("t", [Q8_0, Q4_0])
+def test_matvec_packed_row_range_and_unaligned_x(ctx, orc, t):
+    _check_matvec_packed(ctx, orc, t, 300, 4096, 1300 + t, row_start=128, row_count=77)
+    _check_matvec_packed(ctx, orc, t, 300, 4096, 1310 + t, row_start=299)
+    _check_matvec_packed(ctx, orc, t, 50, 2048, 1320 + t, x_off=4)
+
+
+def test_matvec_packed_validation(ctx):
+    rf = _rf()
+    w = ctx.array(np.zeros(34 * 4, np.uint8))
+    x = ctx.array(np.zeros(128, np.float32))
+    y = ctx.array(np.full(2, 7.0, np.float32))
+    with pytest.raises(rf.RamforgeError, match="truncated"):
+        rf.matvec_packed(ctx, Q8_0, w, (2, 128), x, y)
+    with pytest.raises(rf.RamforgeError, match="not divisible"):
+        rf.matvec_packed(ctx, Q8_0, w, (2, 100), x, y)
+    with pytest.raises(rf.RamforgeError, match="exceeds out_dim"):
+        rf.matvec_packed(ctx, Q8_0, w, (1, 128), x, y, 2)
+    with pytest.raises(rf.RamforgeError, match="does not support"):
+        rf.matvec_packed(ctx, Q4_K, w, (1, 256), x, y)
+    assert y.numpy().tolist() == [7.0, 7.0]  # destination untouched
+    assert not rf.packed_supported(Q8_0, 32768) and rf.packed_supported(Q4_0, 14336)
+    for a in (w, x, y):
+        a.free()
+
+
 def test_matvec_f32_any_length_and_wide_rows(ctx, orc):
     _check_matvec(ctx, orc, F32, 5, 100, 401)     # in_dim not a multiple of 32: rowwise kernel
     _check_matvec(ctx, orc, Q8_0, 40, 40960, 402)  # > 1024 units per row: rowwise kernel

@@ -61,14 +61,26 @@ def _load_gpu(ctx, cfg, T, cap):
 ALL_Q8 = dict(embd=Q8_0, out=Q8_0, q=Q8_0, k=Q8_0, v=Q8_0, o=Q8_0, gate=Q8_0, up=Q8_0, down=Q8_0)
 MIXED = dict(embd=Q4_K, out=Q6_K, q=Q4_K, k=Q4_K, v=Q6_K, o=Q4_K, gate=Q4_K, up=Q6_K, down=Q4_0)
 ALL_F32 = dict(embd=F32, out=F32, q=F32, k=F32, v=F32, o=F32, gate=F32, up=F32, down=F32)
+ALL_Q4 = dict(embd=Q8_0, out=Q4_0, q=Q4_0, k=Q4_0, v=Q4_0, o=Q4_0, gate=Q4_0, up=Q4_0, down=Q4_0)
 
 
-@pytest.mark.parametrize("mode", [1, 0], ids=["stream", "oneshot"])
-@pytest.mark.parametrize("kind,bias", [("q8", False), ("mixed", True), ("f32", True)])
-def test_tiny_model_forward_and_generate(ctx, orc, kind, bias, mode):
-    _rf().tune_matvec_kernel(mode)
+@pytest.fixture(params=["packed", "stream", "oneshot"])
+def layout_mode(request):
+    """packed: Q8_0/Q4_0 projections in the device-native layout (default);
+    stream / oneshot: GGUF layout with the persistent or one-shot kernel."""
+    rf = _rf()
+    old_k, old_p = rf.tune_matvec_kernel(-1), rf.tune_packed_weights(-1)
+    rf.tune_matvec_kernel(0 if request.param == "oneshot" else 1)
+    rf.tune_packed_weights(1 if request.param == "packed" else 0)
+    yield request.param
+    rf.tune_matvec_kernel(old_k)
+    rf.tune_packed_weights(old_p)
+
+
+@pytest.mark.parametrize("kind,bias", [("q8", False), ("q4", False), ("mixed", True), ("f32", True)])
+def test_tiny_model_forward_and_generate(ctx, orc, kind, bias, layout_mode):
     cfg = dict(TINY)
-    types = {"q8": ALL_Q8, "mixed": MIXED, "f32": ALL_F32}[kind]
+    types = {"q8": ALL_Q8, "q4": ALL_Q4, "mixed": MIXED, "f32": ALL_F32}[kind]
     if kind == "mixed":
         cfg.update(embedding_length=256, feed_forward_length=512, head_dim=64)
     rng = np.random.default_rng(900 + len(kind))
