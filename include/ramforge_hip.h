@@ -274,6 +274,32 @@ int32_t rf_model_read_tokens(rf_model *model, uint32_t *out, uint64_t n);
  * rf_model_decode_steps (1) or eager launches (0, default). */
 int32_t rf_model_use_graph(rf_model *model, int32_t enable);
 
+/* VRAM residency tier with layer streaming (device side of load_layer,
+ * release_layer and LayerCache: streaming_model.rs:555-873,
+ * layer_cache.rs:74-268).  Must be called before any blk.* tensor is
+ * installed.  Afterwards every block tensor is kept in pinned host memory (in
+ * the device layout) and a forward pass uploads each layer it needs on the
+ * copy stream: charges "layer:{i}:{tensor}" are made before the buffers are
+ * allocated (all released again if one fails), the next layer's upload
+ * overlaps the current layer's kernels, and a computed layer enters an LRU
+ * cache of at most layer_cache_bytes (charges renamed "cache:layer:{i}:*",
+ * least recently used layers evicted first; buffers are freed before their
+ * charges are released).  A layer that cannot be cached is released after
+ * the pass.  Loads evict cached layers until the context's VRAM budget holds
+ * them; when even an empty cache leaves too little, the pass fails with
+ * RF_ERR_BUDGET ("insufficient memory").  Graph replay and kernel timing are
+ * unavailable in this mode. */
+int32_t rf_model_enable_streaming(rf_model *model, uint64_t layer_cache_bytes);
+/* Layer cache eviction policy: 0 = least recently used (LayerCache, the
+ * default); 1 = the layer needed furthest in the future of the layer cycle
+ * (optimal for decoding's in-order scan; a just-computed layer that would be
+ * needed later than every cached one is released instead of cached).  No
+ * counterpart in the reference for policy 1. */
+int32_t rf_model_set_cache_policy(rf_model *model, int32_t policy);
+/* out[6]: cache hits, misses (layer uploads), evictions, bytes uploaded,
+ * bytes and layers currently cached. */
+int32_t rf_model_residency_stats(rf_model *model, uint64_t *out);
+
 /* Launch groups of one decode step (see rf_model_time_kernel). */
 #define RF_KERNEL_QKV 1       /* attn RMSNorm + Q/K/V matvec (+ bias)      */
 #define RF_KERNEL_ATTENTION 2 /* RoPE + split-K attention + K/V commit     */
@@ -292,6 +318,19 @@ int32_t rf_model_use_graph(rf_model *model, int32_t enable);
  * for the profiler's per-event times (runtime/src/profile.rs:7-23). */
 int32_t rf_model_time_kernel(rf_model *model, uint32_t kind, uint32_t reps, float *avg_ms,
                              uint64_t *bytes_per_launch, uint64_t *launches);
+
+/* ------------------------------------------------------- graph capture */
+
+/* Records the calls the caller enqueues on the context's compute stream
+ * between rf_capture_begin and rf_capture_end into a hipGraph (thread-local
+ * capture: other threads are unaffected), and replays it.  No counterpart in
+ * the reference; used to time kernels without host launch overhead.
+ * rf_graph_replay launches the graph `reps` times on the compute stream and
+ * reports the mean milliseconds per replay (HIP events). */
+int32_t rf_capture_begin(rf_ctx *ctx);
+int32_t rf_capture_end(rf_ctx *ctx, void **graph);
+int32_t rf_graph_replay(rf_ctx *ctx, void *graph, uint32_t reps, float *ms_per_replay);
+int32_t rf_graph_destroy(rf_ctx *ctx, void *graph);
 
 /* ------------------------------------------------------------- tuning */
 

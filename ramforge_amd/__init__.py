@@ -112,6 +112,43 @@ class DeviceArray:
             self.ptr = 0
 
 
+class CapturedGraph:
+    """A hipGraph recorded from the compute stream (rf_capture_begin/end)."""
+
+    def __init__(self, ctx: "Context", handle: int):
+        self.ctx = ctx
+        self.handle = handle
+
+    def replay(self, reps: int = 1) -> float:
+        """Launch the graph `reps` times; returns the mean ms per replay."""
+        ms = C.c_float(0.0)
+        _lib.check(self.ctx.lib.rf_graph_replay(self.ctx.handle, self.handle, reps, C.byref(ms)))
+        return ms.value
+
+    def close(self) -> None:
+        if self.handle:
+            _lib.check(self.ctx.lib.rf_graph_destroy(self.ctx.handle, self.handle))
+            self.handle = None
+
+
+class _Capture:
+    def __init__(self, ctx: "Context"):
+        self.ctx = ctx
+        self.graph: Optional[CapturedGraph] = None
+
+    def __enter__(self) -> "_Capture":
+        _lib.check(self.ctx.lib.rf_capture_begin(self.ctx.handle))
+        return self
+
+    def __exit__(self, exc_type, exc, tb):
+        h = C.c_void_p()
+        rc = self.ctx.lib.rf_capture_end(self.ctx.handle, C.byref(h))
+        if exc_type is None:
+            _lib.check(rc)
+            self.graph = CapturedGraph(self.ctx, h.value)
+        return False
+
+
 class Context:
     """Device context: compute + copy streams and the VRAM ledger."""
 
@@ -206,6 +243,11 @@ class Context:
     def copy(self, dst, src, nbytes: int, stream=None) -> None:
         """Device-to-device copy (hipMemcpyAsync on `stream`, default the compute stream)."""
         _lib.check(self.lib.rf_copy_async(self.handle, _ptr(dst), _ptr(src), nbytes, stream))
+
+    def capture(self):
+        """Context manager: the calls enqueued on the compute stream inside the
+        block are recorded into a graph (CapturedGraph) instead of running."""
+        return _Capture(self)
 
     def event(self):
         e = C.c_void_p()
@@ -409,6 +451,21 @@ class GpuLlamaModel:
         if self.handle:
             self.ctx.lib.rf_model_destroy(self.handle)
             self.handle = None
+
+    def enable_streaming(self, layer_cache_bytes: int) -> None:
+        """Keep block tensors in pinned host memory and stream layers into an
+        LRU device cache of at most layer_cache_bytes (call before loading)."""
+        _lib.check(self.ctx.lib.rf_model_enable_streaming(self.handle, int(layer_cache_bytes)))
+
+    def set_cache_policy(self, policy: int) -> None:
+        """0: least recently used (reference LayerCache); 1: next use in the layer cycle."""
+        _lib.check(self.ctx.lib.rf_model_set_cache_policy(self.handle, policy))
+
+    def residency_stats(self) -> dict:
+        out = (C.c_uint64 * 6)()
+        _lib.check(self.ctx.lib.rf_model_residency_stats(self.handle, out))
+        keys = ("hits", "misses", "evictions", "uploaded_bytes", "cached_bytes", "cached_layers")
+        return dict(zip(keys, (int(v) for v in out)))
 
     def set_tensor(self, name: str, ggml_type: int, ne0: int, ne1: int, data: np.ndarray) -> None:
         h = np.ascontiguousarray(data)

@@ -103,5 +103,14 @@ __device__ __forceinline__ float rf_wave_max(float v) {
   return fmaxf(fmaxf(rf_lane(v, 0), rf_lane(v, 16)), fmaxf(rf_lane(v, 32), rf_lane(v, 48)));
 }
 
+// Hides a value from the optimiser (empty asm, value stays in a VGPR).  A
+// packed-nibble word w & 0x0F0F0F0F passed through it keeps its four bytes
+// in one register, so each element costs one v_cvt_f32_ubyte{k}; without it
+// the mask is folded into a per-element bit-field extract plus a convert.
+__device__ __forceinline__ uint32_t rf_opaque(uint32_t v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
+
 // Unsigned byte k of a word converted to float (v_cvt_f32_ubyte{k}).
 __device__ __forceinline__ float rf_ub(uint32_t w, int k) { return (float)((w >> (8 * k)) & 0xFFu); }

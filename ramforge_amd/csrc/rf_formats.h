@@ -70,7 +70,7 @@ template <> struct Fmt<T_Q4_0> {
     float acc = 0.f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const uint32_t lo = w[i] & 0x0F0F0F0Fu, hi = (w[i] >> 4) & 0x0F0F0F0Fu;
+      const uint32_t lo = rf_opaque(w[i] & 0x0F0F0F0Fu), hi = rf_opaque((w[i] >> 4) & 0x0F0F0F0Fu);
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
         acc = fmaf(rf_ub(lo, k), x.v[4 * i + k], acc);
@@ -101,7 +101,7 @@ template <> struct Fmt<T_Q5_0> {
     float acc = 0.f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const uint32_t lo = w[i] & 0x0F0F0F0Fu, hi = (w[i] >> 4) & 0x0F0F0F0Fu;
+      const uint32_t lo = rf_opaque(w[i] & 0x0F0F0F0Fu), hi = rf_opaque((w[i] >> 4) & 0x0F0F0F0Fu);
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
         const int e = 4 * i + k;
@@ -158,7 +158,7 @@ template <> struct Fmt<T_Q4_K> {
     float acc = 0.f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const uint32_t n = (w[i] >> sh) & 0x0F0F0F0Fu;
+      const uint32_t n = rf_opaque((w[i] >> sh) & 0x0F0F0F0Fu);
 #pragma unroll
       for (int k = 0; k < 4; ++k) acc = fmaf(rf_ub(n, k), x.v[4 * i + k], acc);
     }
@@ -198,7 +198,7 @@ template <> struct Fmt<T_Q5_K> {
     float acc = 0.f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const uint32_t n = (w[i] >> sh) & 0x0F0F0F0Fu;
+      const uint32_t n = rf_opaque((w[i] >> sh) & 0x0F0F0F0Fu);
       // element l = 4i + k reads byte l/8 = i/2 of qh, bit s
       const uint32_t hb = (qh >> (8 * (i >> 1) + s)) & 1u;
       const uint32_t nh = n | (hb * 0x10101010u);
@@ -244,7 +244,7 @@ template <> struct Fmt<T_Q6_K> {
     float acc_lo = 0.f, acc_hi = 0.f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const uint32_t q = ((ql[i] >> nsh) & 0x0F0F0F0Fu) | (((qh[i] >> hsh) & 0x03030303u) << 4);
+      const uint32_t q = rf_opaque(((ql[i] >> nsh) & 0x0F0F0F0Fu) | (((qh[i] >> hsh) & 0x03030303u) << 4));
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk) {
         if (i < 4) acc_lo = fmaf(rf_ub(q, kk), x.v[4 * i + kk], acc_lo);

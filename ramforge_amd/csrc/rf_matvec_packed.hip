@@ -55,7 +55,7 @@ template <> struct Pk<T_Q4_0> {
     float s = 0.f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const uint32_t lo = q[i] & 0x0F0F0F0Fu, hi = (q[i] >> 4) & 0x0F0F0F0Fu;
+      const uint32_t lo = rf_opaque(q[i] & 0x0F0F0F0Fu), hi = rf_opaque((q[i] >> 4) & 0x0F0F0F0Fu);
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
         s = fmaf(rf_ub(lo, k), x[4 * i + k], s);

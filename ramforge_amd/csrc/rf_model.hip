@@ -24,6 +24,7 @@
 // in VRAM so a decode step needs no host round-trip and can be captured once
 // into a hipGraph and replayed.
 #include <algorithm>
+#include <list>
 #include <cmath>
 #include <cstring>
 #include <string>
@@ -39,7 +40,19 @@ struct DevTensor {
   void* d = nullptr;
   std::string charge;
   bool packed = false;  // device-native layout (rf_matvec_packed.hip), else GGUF bytes
-  bool present() const { return d != nullptr; }
+  void* host = nullptr;  // streamed layers: pinned host copy in device layout (d set while resident)
+  bool present() const { return d != nullptr || host != nullptr; }
+};
+
+// Residency of one streamed layer (device side of load_layer / LayerCache,
+// streaming_model.rs:581-873, layer_cache.rs:74-268).
+enum { LAYER_HOST = 0, LAYER_ACTIVE = 1, LAYER_CACHED = 2, LAYER_RETIRED = 3 };
+struct LayerRes {
+  int state = LAYER_HOST;         // ACTIVE: charged "layer:{i}:*"; CACHED: "cache:layer:{i}:*";
+                                  // RETIRED: computed, not cacheable, released once its kernels end
+  uint64_t bytes = 0;             // device bytes of the layer (sum of its tensors)
+  hipEvent_t uploaded = nullptr;  // copy stream: the layer's uploads finished
+  hipEvent_t used = nullptr;      // compute stream: the last kernel reading the layer finished
 };
 
 // Projection weights in Q8_0 / Q4_0 are repacked at install unless disabled
@@ -78,6 +91,16 @@ struct rf_model {
   hipGraph_t graph = nullptr;
   hipGraphExec_t graph_exec = nullptr;
   std::vector<std::string> charges;
+  // Layer streaming: every block tensor lives in pinned host memory and is
+  // uploaded on demand; an LRU cache of at most cache_cap device bytes keeps
+  // layers between tokens.
+  bool streaming = false;
+  uint64_t cache_cap = 0, cache_used = 0;
+  std::vector<LayerRes> res;
+  std::list<uint32_t> lru;  // cached layers, most recently used first
+  uint64_t st_hits = 0, st_misses = 0, st_evictions = 0, st_uploaded = 0;
+  int cache_policy = 0;    // 0: LRU (LayerCache); 1: next use within the layer cycle
+  uint32_t cur_layer = 0;  // layer the forward pass is at (policy 1)
 };
 
 namespace {
@@ -102,6 +125,244 @@ void reset_graph(rf_model* m) {
   if (m->graph) hipGraphDestroy(m->graph);
   m->graph_exec = nullptr;
   m->graph = nullptr;
+}
+
+// ------------------------------------------------------- layer streaming
+
+// Host copies of the decode rules the device uses at install (F16/BF16 are
+// widened to F32; quant.rs:40-65 incl. its subnormal rule, tensor.rs:1044-1047).
+float host_half_to_float(uint32_t h) {
+  const uint32_t sign = (h & 0x8000u) << 16, exp = (h >> 10) & 0x1Fu, frac = h & 0x3FFu;
+  uint32_t bits;
+  if (exp == 0u) {
+    float v = (float)frac * 0x1p-25f;
+    memcpy(&bits, &v, 4);
+    bits |= sign;
+  } else {
+    bits = sign | (((exp == 0x1Fu) ? 0xFFu : exp + 112u) << 23) | (frac << 13);
+  }
+  float f;
+  memcpy(&f, &bits, 4);
+  return f;
+}
+
+// GGUF Q8_0 / Q4_0 payload -> packed layout (same rules as pack_blocks).
+void host_pack(uint32_t t, const uint8_t* raw, uint64_t rows, uint64_t in, uint8_t* out) {
+  const uint64_t nb = in / 32, bs = t == T_Q8_0 ? 34 : 18, cb = bs - 2;
+  uint8_t* scales = out + rows * nb * cb;
+  for (uint64_t i = 0; i < rows * nb; ++i) {
+    const uint8_t* b = raw + i * bs;
+    memcpy(scales + 2 * i, b, 2);
+    memcpy(out + i * cb, b + 2, cb);
+  }
+}
+
+void layer_slots(Layer& L, DevTensor* out[12]) {
+  DevTensor* t[12] = {&L.attn_norm, &L.q, &L.k, &L.v, &L.o, &L.ffn_norm, &L.gate, &L.up, &L.down, &L.bq, &L.bk, &L.bv};
+  for (int i = 0; i < 12; ++i) out[i] = t[i];
+}
+
+const char* slot_name(int i) {
+  static const char* n[12] = {"attn_norm.weight", "attn_q.weight", "attn_k.weight", "attn_v.weight",
+                              "attn_output.weight", "ffn_norm.weight", "ffn_gate.weight", "ffn_up.weight",
+                              "ffn_down.weight", "attn_q.bias", "attn_k.bias", "attn_v.bias"};
+  return n[i];
+}
+
+void update_layer_bytes(rf_model* m, uint32_t li) {
+  DevTensor* t[12];
+  layer_slots(m->layers[li], t);
+  uint64_t b = 0;
+  for (DevTensor* x : t)
+    if (x->host) b += x->nbytes;
+  m->res[li].bytes = b;
+}
+
+// Physical free of a resident layer's buffers, then release of its charges
+// (memory.rs:9-15): waits until the last kernel that read the layer ended.
+int32_t layer_free(rf_model* m, uint32_t li) {
+  LayerRes& R = m->res[li];
+  if (R.state == LAYER_HOST) return RF_OK;
+  hipError_t e = hipEventSynchronize(R.used);
+  if (e == hipSuccess) e = hipEventSynchronize(R.uploaded);
+  if (e != hipSuccess) return hip_error(e, "layer release");
+  DevTensor* t[12];
+  layer_slots(m->layers[li], t);
+  int32_t rc = RF_OK;
+  for (DevTensor* x : t) {
+    if (!x->d) continue;
+    const int32_t r = vram_release(m->ctx, x->charge);
+    if (r && !rc) rc = r;
+    x->d = nullptr;
+    x->charge.clear();
+  }
+  if (R.state == LAYER_CACHED) {
+    m->lru.remove(li);
+    m->cache_used -= R.bytes;
+  }
+  R.state = LAYER_HOST;
+  return rc;
+}
+
+// Steps until layer j is needed again by the pass that is at cur_layer
+// (every pass visits the layers in order; the current layer counts as a
+// full cycle away once computed).
+uint32_t next_use(const rf_model* m, uint32_t j) {
+  const uint32_t n = (uint32_t)m->layers.size();
+  const uint32_t d = (j + n - m->cur_layer) % n;
+  return d == 0 ? n : d;
+}
+
+// The cached layer to drop: LayerCache::evict_lru's least recently used one
+// (policy 0), or the one needed furthest in the future (policy 1, the
+// optimal choice for the cyclic layer scan of decoding).
+uint32_t pick_victim(const rf_model* m) {
+  if (m->cache_policy == 0) return m->lru.back();
+  uint32_t best = m->lru.back(), bd = 0;
+  for (uint32_t j : m->lru)
+    if (next_use(m, j) > bd) { bd = next_use(m, j); best = j; }
+  return best;
+}
+
+bool evict_lru(rf_model* m, int32_t* rc) {
+  if (m->lru.empty()) return false;
+  const uint32_t victim = pick_victim(m);
+  *rc = layer_free(m, victim);
+  m->st_evictions += 1;
+  return true;
+}
+
+// Release every layer that was computed but is not cacheable.
+int32_t release_retired(rf_model* m) {
+  for (uint32_t li = 0; li < m->res.size(); ++li)
+    if (m->res[li].state == LAYER_RETIRED) {
+      const int32_t rc = layer_free(m, li);
+      if (rc) return rc;
+    }
+  return RF_OK;
+}
+
+// Make room for `bytes`: retired layers first, then LRU cached layers
+// (ensure_layer_cache_headroom, streaming_model.rs:555-572).
+int32_t make_headroom(rf_model* m, uint64_t bytes) {
+  if (vram_can_allocate(m->ctx, bytes)) return RF_OK;
+  int32_t rc = release_retired(m);
+  if (rc) return rc;
+  while (!vram_can_allocate(m->ctx, bytes)) {
+    if (!evict_lru(m, &rc)) return RF_ERR_BUDGET;
+    if (rc) return rc;
+  }
+  return RF_OK;
+}
+
+// load_layer (streaming_model.rs:581-847) on the device: every tensor is
+// charged "layer:{i}:{name}" before its buffer is allocated, then uploaded
+// from the pinned host copy on the copy stream.  On failure every charge made
+// for the layer is released and the layer stays host-only.
+int32_t load_layer(rf_model* m, uint32_t li) {
+  LayerRes& R = m->res[li];
+  int32_t rc = make_headroom(m, R.bytes);
+  if (rc == RF_ERR_BUDGET)
+    return set_error(RF_ERR_BUDGET,
+                     "insufficient memory: layer %u needs %llu bytes, %llu of %llu in use after evicting every cached "
+                     "layer",
+                     li, (unsigned long long)R.bytes, (unsigned long long)m->ctx->ledger.used(),
+                     (unsigned long long)m->ctx->ledger.total());
+  if (rc) return rc;
+  DevTensor* t[12];
+  layer_slots(m->layers[li], t);
+  hipStream_t cs = m->ctx->copy;
+  for (int i = 0; i < 12; ++i) {
+    DevTensor* x = t[i];
+    if (!x->host) continue;
+    const std::string charge = "layer:" + std::to_string(li) + ":" + slot_name(i);
+    void* d = nullptr;
+    rc = vram_alloc(m->ctx, charge, x->nbytes, &d);
+    hipError_t e = hipSuccess;
+    if (rc == RF_OK) {
+      x->d = d;
+      x->charge = charge;
+      e = hipMemcpyAsync(d, x->host, x->nbytes, hipMemcpyHostToDevice, cs);
+      if (e != hipSuccess) rc = hip_error(e, "layer upload");
+    }
+    if (rc) {  // roll back every charge of this layer
+      hipStreamSynchronize(cs);
+      for (DevTensor* y : t)
+        if (y->d) {
+          vram_release(m->ctx, y->charge);
+          y->d = nullptr;
+          y->charge.clear();
+        }
+      return rc;
+    }
+    m->st_uploaded += x->nbytes;
+  }
+  hipError_t e = hipEventRecord(R.uploaded, cs);
+  if (e == hipSuccess) e = hipEventRecord(R.used, m->ctx->compute);  // not in use yet
+  if (e != hipSuccess) return hip_error(e, "hipEventRecord");
+  R.state = LAYER_ACTIVE;
+  return RF_OK;
+}
+
+// A layer about to be computed: a cached one returns to "layer:{i}:" (hit),
+// a host-only one is loaded (miss).  With `prefetch` a miss that does not fit
+// is skipped instead of failing.
+int32_t acquire_layer(rf_model* m, uint32_t li, bool prefetch) {
+  LayerRes& R = m->res[li];
+  if (R.state == LAYER_ACTIVE || R.state == LAYER_RETIRED) {
+    R.state = LAYER_ACTIVE;
+    return RF_OK;
+  }
+  if (R.state == LAYER_CACHED) {
+    int32_t rc = vram_rename_prefix(m->ctx, "cache:layer:" + std::to_string(li) + ":",
+                                    "layer:" + std::to_string(li) + ":");
+    if (rc) return rc;
+    DevTensor* t[12];
+    layer_slots(m->layers[li], t);
+    for (DevTensor* x : t)
+      if (x->d) x->charge = "layer:" + x->charge.substr(std::string("cache:layer:").size());
+    m->lru.remove(li);
+    m->cache_used -= R.bytes;
+    R.state = LAYER_ACTIVE;
+    m->st_hits += 1;
+    return RF_OK;
+  }
+  if (prefetch && !vram_can_allocate(m->ctx, R.bytes) && m->lru.empty()) return RF_OK;
+  int32_t rc = load_layer(m, li);
+  if (prefetch && rc == RF_ERR_BUDGET) return RF_OK;
+  if (rc == RF_OK) m->st_misses += 1;
+  return rc;
+}
+
+// After the layer's kernels: LayerCache::insert_loaded (rename "layer:{i}:"
+// -> "cache:layer:{i}:", evicting LRU layers while over capacity), or, when
+// the layer cannot be cached, retire it for release once its kernels end.
+int32_t settle_layer(rf_model* m, uint32_t li) {
+  LayerRes& R = m->res[li];
+  hipError_t e = hipEventRecord(R.used, m->ctx->compute);
+  if (e != hipSuccess) return hip_error(e, "hipEventRecord");
+  if (R.bytes == 0 || R.bytes > m->cache_cap) {
+    R.state = LAYER_RETIRED;
+    return RF_OK;
+  }
+  if (m->cache_policy == 1 && m->cache_used + R.bytes > m->cache_cap && !m->lru.empty() &&
+      next_use(m, li) >= next_use(m, pick_victim(m))) {
+    R.state = LAYER_RETIRED;  // needed later than every cached layer: not worth an eviction
+    return RF_OK;
+  }
+  int32_t rc = RF_OK;
+  while (m->cache_used + R.bytes > m->cache_cap)
+    if (!evict_lru(m, &rc) || rc) return rc;
+  rc = vram_rename_prefix(m->ctx, "layer:" + std::to_string(li) + ":", "cache:layer:" + std::to_string(li) + ":");
+  if (rc) return rc;
+  DevTensor* t[12];
+  layer_slots(m->layers[li], t);
+  for (DevTensor* x : t)
+    if (x->d) x->charge = "cache:" + x->charge;
+  R.state = LAYER_CACHED;
+  m->lru.push_front(li);
+  m->cache_used += R.bytes;
+  return RF_OK;
 }
 
 // Resolve a GGUF tensor name to its slot and expected shape [ne0, ne1].
@@ -174,6 +435,75 @@ bool is_projection(const std::string& name) {
   return false;
 }
 
+// A block tensor of a streaming model: its device-layout bytes go to pinned
+// host memory (packed / widened as on the device path); the layer is uploaded
+// when a forward pass needs it.
+int32_t install_streamed(rf_model* m, const std::string& name, DevTensor* slot, uint32_t t, uint64_t ne0,
+                         uint64_t ne1, uint64_t bytes, const void* host, bool synth, uint64_t seed, double mul,
+                         float constant) {
+  unsigned li = 0;
+  if (sscanf(name.c_str(), "blk.%u.", &li) != 1 || li >= m->layers.size())
+    return set_error(RF_ERR_INVALID, "unknown tensor '%s'", name.c_str());
+  rf_ctx* ctx = m->ctx;
+  reset_graph(m);
+  int32_t rc = layer_free(m, li);  // a resident copy of the layer is stale now
+  if (rc) return rc;
+  const bool widen = (t == T_F16 || t == T_BF16);
+  const bool pack = g_pack_weights && is_projection(name) && plan_packed(t, ne0).ok;
+  const uint64_t fbytes = widen ? ne0 * ne1 * 4 : bytes;
+  void* pin = nullptr;
+  hipError_t e = hipHostMalloc(&pin, fbytes, hipHostMallocDefault);
+  if (e != hipSuccess) return hip_error(e, "hipHostMalloc");
+  if (synth) {
+    void *tmp = nullptr, *tmp2 = nullptr;
+    rc = vram_alloc(ctx, "tmp:synth:" + name, bytes, &tmp);
+    if (rc == RF_OK && pack) rc = vram_alloc(ctx, "tmp:pack:" + name, bytes, &tmp2);
+    if (rc == RF_OK) {
+      uint64_t qk = 1, bs = 4;
+      type_geometry(t, &qk, &bs);
+      const uint64_t nblk = t == T_F32 ? ne0 * ne1 : ne0 / qk * ne1;
+      if (t == T_F32 && !std::isnan(constant)) e = launch_fill(static_cast<float*>(tmp), constant, ne0 * ne1, ctx->compute);
+      else e = launch_synth(t, seed, 0, nblk, mul, tmp, ctx->compute);
+      if (e == hipSuccess && pack) e = launch_pack(t, tmp, tmp2, ne1, ne0, ctx->compute);
+      if (e == hipSuccess) e = hipMemcpyAsync(pin, pack ? tmp2 : tmp, fbytes, hipMemcpyDeviceToHost, ctx->compute);
+      if (e == hipSuccess) e = hipStreamSynchronize(ctx->compute);
+      if (e != hipSuccess) rc = hip_error(e, "tensor synthesis");
+    }
+    if (tmp2) vram_release(ctx, "tmp:pack:" + name);
+    if (tmp) vram_release(ctx, "tmp:synth:" + name);
+  } else if (widen) {
+    const uint16_t* h = static_cast<const uint16_t*>(host);
+    float* o = static_cast<float*>(pin);
+    for (uint64_t i = 0; i < ne0 * ne1; ++i) {
+      if (t == T_F16) {
+        o[i] = host_half_to_float(h[i]);
+      } else {
+        const uint32_t b = (uint32_t)h[i] << 16;
+        memcpy(&o[i], &b, 4);
+      }
+    }
+  } else if (pack) {
+    host_pack(t, static_cast<const uint8_t*>(host), ne1, ne0, static_cast<uint8_t*>(pin));
+  } else {
+    memcpy(pin, host, bytes);
+  }
+  if (rc) {
+    hipHostFree(pin);
+    return rc;
+  }
+  if (slot->host) hipHostFree(slot->host);
+  slot->type = widen ? T_F32 : t;
+  slot->ne0 = ne0;
+  slot->ne1 = ne1;
+  slot->nbytes = fbytes;
+  slot->d = nullptr;
+  slot->charge.clear();
+  slot->packed = pack;
+  slot->host = pin;
+  update_layer_bytes(m, li);
+  return RF_OK;
+}
+
 int32_t install(rf_model* m, const char* cname, uint32_t t, uint64_t ne0, uint64_t ne1, const void* host,
                 uint64_t nbytes, bool synth, uint64_t seed, double mul, float constant) {
   if (!m || !cname) return set_error(RF_ERR_INVALID, "null model or tensor name");
@@ -190,6 +520,8 @@ int32_t install(rf_model* m, const char* cname, uint32_t t, uint64_t ne0, uint64
                      (unsigned long long)bytes, (unsigned long long)nbytes);
   if (synth && (t == T_F16 || t == T_BF16))
     return set_error(RF_ERR_UNSUPPORTED, "synthetic generator does not emit %s", type_name(t));
+  if (m->streaming && name.rfind("blk.", 0) == 0)
+    return install_streamed(m, name, slot, t, ne0, ne1, bytes, host, synth, seed, mul, constant);
   rf_ctx* ctx = m->ctx;
   reset_graph(m);
   hipError_t e = hipStreamSynchronize(ctx->compute);
@@ -454,8 +786,22 @@ int32_t enqueue_forward(rf_model* m) {
   RF_LAUNCH(launch_dequant_rows(m->token_embd.type, m->token_embd.d, c.embedding_length, 1, m->hidden, m->d_token,
                                 c.vocab_size, st),
             "embedding");
-  for (size_t li = 0; li < m->layers.size(); ++li) {
-    int32_t rc = enqueue_layer(m, li);
+  const uint32_t nl = (uint32_t)m->layers.size();
+  for (uint32_t li = 0; li < nl; ++li) {
+    int32_t rc;
+    m->cur_layer = li;
+    if (m->streaming) {
+      // this layer resident (hit or load), the next one's upload started so it
+      // overlaps this layer's kernels, then the kernels wait for the upload
+      if ((rc = acquire_layer(m, li, false))) return rc;
+      if (li + 1 < nl && (rc = acquire_layer(m, li + 1, true))) return rc;
+      RF_LAUNCH(hipStreamWaitEvent(st, m->res[li].uploaded, 0), "wait for layer upload");
+    }
+    if ((rc = enqueue_layer(m, li))) return rc;
+    if (m->streaming && (rc = settle_layer(m, li))) return rc;
+  }
+  if (m->streaming) {
+    int32_t rc = release_retired(m);  // release_layer for layers the cache did not take
     if (rc) return rc;
   }
   RF_LAUNCH(launch_advance_pos(m->d_pos, st), "advance position");
@@ -586,6 +932,16 @@ void rf_model_destroy(rf_model* m) {
   if (!m) return;
   reset_graph(m);
   hipStreamSynchronize(m->ctx->compute);
+  hipStreamSynchronize(m->ctx->copy);
+  for (uint32_t li = 0; li < m->res.size(); ++li) {
+    layer_free(m, li);
+    DevTensor* t[12];
+    layer_slots(m->layers[li], t);
+    for (DevTensor* x : t)
+      if (x->host) hipHostFree(x->host);
+    if (m->res[li].uploaded) hipEventDestroy(m->res[li].uploaded);
+    if (m->res[li].used) hipEventDestroy(m->res[li].used);
+  }
   for (auto it = m->charges.rbegin(); it != m->charges.rend(); ++it) vram_release(m->ctx, *it);
   delete m;
 }
@@ -679,6 +1035,8 @@ int32_t rf_model_generate(rf_model* m, const uint32_t* prompt, uint64_t plen, ui
 
 int32_t rf_model_use_graph(rf_model* m, int32_t enable) {
   if (!m) return set_error(RF_ERR_INVALID, "null model");
+  if (enable && m->streaming)
+    return set_error(RF_ERR_UNSUPPORTED, "graph replay needs every layer resident; this model streams its layers");
   m->use_graph = enable != 0;
   if (!m->use_graph) reset_graph(m);
   return RF_OK;
@@ -721,6 +1079,7 @@ int32_t rf_model_time_kernel(rf_model* m, uint32_t kind, uint32_t reps, float* a
     return set_error(RF_ERR_INVALID, "unknown kernel group %u", kind);
   int32_t rc = check_ready(m);
   if (rc) return rc;
+  if (m->streaming) return set_error(RF_ERR_UNSUPPORTED, "kernel timing needs every layer resident");
   if (kind == RF_KERNEL_ATTENTION && m->seq_len == 0)
     return set_error(RF_ERR_INVALID, "attention timing needs a forwarded prompt");
   if (kind == RF_KERNEL_ATTENTION && m->seq_len >= m->kv_cap)
@@ -766,6 +1125,49 @@ int32_t rf_model_time_kernel(rf_model* m, uint32_t kind, uint32_t reps, float* a
   *avg_ms = ms / (float)n;
   *bytes_per_launch = bytes / n;
   *launches = n;
+  return RF_OK;
+}
+
+int32_t rf_model_enable_streaming(rf_model* m, uint64_t layer_cache_bytes) {
+  if (!m) return set_error(RF_ERR_INVALID, "null model");
+  if (m->streaming) {
+    m->cache_cap = layer_cache_bytes;
+    return RF_OK;
+  }
+  for (Layer& L : m->layers) {
+    DevTensor* t[12];
+    layer_slots(L, t);
+    for (DevTensor* x : t)
+      if (x->present()) return set_error(RF_ERR_INVALID, "layer streaming must be enabled before block tensors load");
+  }
+  m->res.resize(m->layers.size());
+  for (LayerRes& R : m->res) {
+    hipError_t e = hipEventCreateWithFlags(&R.uploaded, hipEventDisableTiming);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&R.used, hipEventDisableTiming);
+    if (e != hipSuccess) return hip_error(e, "hipEventCreate");
+  }
+  m->streaming = true;
+  m->cache_cap = layer_cache_bytes;
+  m->use_graph = false;
+  reset_graph(m);
+  return RF_OK;
+}
+
+int32_t rf_model_set_cache_policy(rf_model* m, int32_t policy) {
+  if (!m) return set_error(RF_ERR_INVALID, "null model");
+  if (policy != 0 && policy != 1) return set_error(RF_ERR_INVALID, "unknown layer cache policy %d", policy);
+  m->cache_policy = policy;
+  return RF_OK;
+}
+
+int32_t rf_model_residency_stats(rf_model* m, uint64_t* out) {
+  if (!m || !out) return set_error(RF_ERR_INVALID, "null argument");
+  out[0] = m->st_hits;
+  out[1] = m->st_misses;
+  out[2] = m->st_evictions;
+  out[3] = m->st_uploaded;
+  out[4] = m->cache_used;
+  out[5] = m->lru.size();
   return RF_OK;
 }
 

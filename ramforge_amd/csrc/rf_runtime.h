@@ -67,6 +67,10 @@ int32_t ensure_workspace(rf_ctx* ctx, Workspace& ws, const char* charge, uint64_
 // Allocate / free a ledger-charged device buffer.
 int32_t vram_alloc(rf_ctx* ctx, const std::string& charge, uint64_t bytes, void** out);
 int32_t vram_release(rf_ctx* ctx, const std::string& charge);
+// Rename every charge (and its buffer record) that starts with old_prefix.
+int32_t vram_rename_prefix(rf_ctx* ctx, const std::string& old_prefix, const std::string& new_prefix);
+// MemoryBudget::can_allocate: whether `bytes` more fit under the budget.
+bool vram_can_allocate(rf_ctx* ctx, uint64_t bytes);
 // Upload host bytes through the pinned staging buffers on the copy stream.
 int32_t staged_upload(rf_ctx* ctx, void* dst, const void* src, uint64_t bytes);
 inline hipStream_t pick_stream(rf_ctx* ctx, rf_stream_t s) {

@@ -136,6 +136,24 @@ int32_t vram_release(rf_ctx* ctx, const std::string& charge) {
   return rc;
 }
 
+int32_t vram_rename_prefix(rf_ctx* ctx, const std::string& o, const std::string& n) {
+  std::lock_guard<std::mutex> lk(ctx->mu);
+  int32_t rc = ctx->ledger.rename_prefix(o, n);
+  if (rc) return rc;
+  std::map<std::string, void*> nb;
+  for (auto& kv : ctx->buffers) {
+    if (kv.first.compare(0, o.size(), o) == 0) nb[n + kv.first.substr(o.size())] = kv.second;
+    else nb[kv.first] = kv.second;
+  }
+  ctx->buffers.swap(nb);
+  return RF_OK;
+}
+
+bool vram_can_allocate(rf_ctx* ctx, uint64_t bytes) {
+  std::lock_guard<std::mutex> lk(ctx->mu);
+  return ctx->ledger.used() + bytes >= ctx->ledger.used() && ctx->ledger.used() + bytes <= ctx->ledger.total();
+}
+
 int32_t ensure_workspace(rf_ctx* ctx, Workspace& ws, const char* charge, uint64_t bytes) {
   if (ws.bytes >= bytes) return RF_OK;
   uint64_t want = bytes < 65536 ? 65536 : bytes;
@@ -308,17 +326,7 @@ int32_t rf_vram_release(rf_ctx* ctx, const char* charge) {
 int32_t rf_vram_rename_prefix(rf_ctx* ctx, const char* op, const char* np) {
   RF_CHECK_CTX(ctx);
   if (!op || !np) return set_error(RF_ERR_INVALID, "null prefix");
-  std::lock_guard<std::mutex> lk(ctx->mu);
-  const std::string o(op), n(np);
-  int32_t rc = ctx->ledger.rename_prefix(o, n);
-  if (rc) return rc;
-  std::map<std::string, void*> nb;
-  for (auto& kv : ctx->buffers) {
-    if (kv.first.compare(0, o.size(), o) == 0) nb[n + kv.first.substr(o.size())] = kv.second;
-    else nb[kv.first] = kv.second;
-  }
-  ctx->buffers.swap(nb);
-  return RF_OK;
+  return vram_rename_prefix(ctx, op, np);
 }
 
 int32_t rf_vram_charge(rf_ctx* ctx, const char* charge, uint64_t* bytes) {
@@ -690,6 +698,66 @@ int32_t rf_synth_blocks(rf_ctx* ctx, uint32_t t, uint64_t seed, uint64_t first, 
                      type_name(t), (unsigned long long)(n * bs), (unsigned long long)dst_bytes);
   hipError_t e = launch_synth(t, seed, first, n, mul, dst, pick_stream(ctx, s));
   return e == hipSuccess ? RF_OK : hip_error(e, "synth launch");
+}
+
+struct rf_graph_h {
+  hipGraph_t g = nullptr;
+  hipGraphExec_t x = nullptr;
+};
+
+int32_t rf_capture_begin(rf_ctx* ctx) {
+  RF_CHECK_CTX(ctx);
+  RF_HIP(hipStreamBeginCapture(ctx->compute, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+  return RF_OK;
+}
+
+int32_t rf_capture_end(rf_ctx* ctx, void** graph) {
+  RF_CHECK_CTX(ctx);
+  if (!graph) return set_error(RF_ERR_INVALID, "null graph output");
+  hipGraph_t g = nullptr;
+  RF_HIP(hipStreamEndCapture(ctx->compute, &g), "hipStreamEndCapture");
+  hipGraphExec_t x = nullptr;
+  const hipError_t e = hipGraphInstantiate(&x, g, nullptr, nullptr, 0);
+  if (e != hipSuccess) {
+    hipGraphDestroy(g);
+    return hip_error(e, "hipGraphInstantiate");
+  }
+  rf_graph_h* h = new rf_graph_h;
+  h->g = g;
+  h->x = x;
+  *graph = h;
+  return RF_OK;
+}
+
+int32_t rf_graph_replay(rf_ctx* ctx, void* graph, uint32_t reps, float* ms_per_replay) {
+  RF_CHECK_CTX(ctx);
+  if (!graph || reps == 0) return set_error(RF_ERR_INVALID, "null graph or zero repetitions");
+  rf_graph_h* h = static_cast<rf_graph_h*>(graph);
+  hipEvent_t a = nullptr, b = nullptr;
+  RF_HIP(hipEventCreate(&a), "hipEventCreate");
+  hipError_t e = hipEventCreate(&b);
+  if (e == hipSuccess) e = hipEventRecord(a, ctx->compute);
+  for (uint32_t i = 0; i < reps && e == hipSuccess; ++i) e = hipGraphLaunch(h->x, ctx->compute);
+  if (e == hipSuccess) e = hipEventRecord(b, ctx->compute);
+  if (e == hipSuccess) e = hipEventSynchronize(b);
+  float ms = 0.f;
+  if (e == hipSuccess) e = hipEventElapsedTime(&ms, a, b);
+  hipEventDestroy(a);
+  if (b) hipEventDestroy(b);
+  if (e != hipSuccess) return hip_error(e, "graph replay");
+  if (ms_per_replay) *ms_per_replay = ms / (float)reps;
+  return RF_OK;
+}
+
+int32_t rf_graph_destroy(rf_ctx* ctx, void* graph) {
+  RF_CHECK_CTX(ctx);
+  if (!graph) return RF_OK;
+  rf_graph_h* h = static_cast<rf_graph_h*>(graph);
+  hipError_t e = hipStreamSynchronize(ctx->compute);
+  if (h->x) hipGraphExecDestroy(h->x);
+  if (h->g) hipGraphDestroy(h->g);
+  delete h;
+  return e == hipSuccess ? RF_OK : hip_error(e, "hipStreamSynchronize");
 }
 
 uint32_t rf_tune_matvec_tile_bytes(uint32_t bytes) {

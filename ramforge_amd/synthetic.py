@@ -87,11 +87,17 @@ def weight_bytes(specs: list[TensorSpec]) -> int:
     return tot
 
 
-def build_device_model(ctx, cfg: dict, specs: list[TensorSpec], kv_capacity: int):
-    """A GpuLlamaModel with every tensor generated in VRAM."""
+def build_device_model(ctx, cfg: dict, specs: list[TensorSpec], kv_capacity: int,
+                       stream_cache_bytes: int | None = None, cache_policy: int = 0):
+    """A GpuLlamaModel with every tensor generated on the device.  With
+    stream_cache_bytes the block tensors go to pinned host memory and layers
+    stream through a device LRU cache of that many bytes."""
     from . import GpuLlamaModel
 
     m = GpuLlamaModel(ctx, cfg, kv_capacity)
+    if stream_cache_bytes is not None:
+        m.enable_streaming(stream_cache_bytes)
+        m.set_cache_policy(cache_policy)
     for s in specs:
         m.synth_tensor(s.name, s.ggml_type, s.ne0, s.ne1, s.seed, s.scale_mul, s.constant)
     return m

@@ -235,6 +235,36 @@ def test_matvec_packed_validation(ctx):
         a.free()
 
 
+def test_capture_replay_matches_eager(ctx):
+    """rf_capture_begin/end + rf_graph_replay: the recorded launches replay to
+    the eager result; replays interleave with eager work."""
+    rf = _rf()
+    rng = np.random.default_rng(77)
+    raw = random_matrix(Q8_0, 257, 4096, rng)
+    w, p = ctx.array(raw), ctx.empty((raw.nbytes,), np.uint8)
+    rf.pack_weights(ctx, Q8_0, w, 257, 4096, p)
+    x = ctx.array(rng.normal(0, 1, 4096).astype(np.float32))
+    y1, y2 = ctx.empty((257,)), ctx.empty((257,))
+    rf.matvec(ctx, Q8_0, w, (257, 4096), x, y1)
+    rf.matvec_packed(ctx, Q8_0, p, (257, 4096), x, y2)
+    e1, e2 = y1.numpy(), y2.numpy()
+    y1.upload(np.zeros(257, np.float32))
+    y2.upload(np.zeros(257, np.float32))
+    with ctx.capture() as cap:
+        rf.matvec(ctx, Q8_0, w, (257, 4096), x, y1)
+        rf.matvec_packed(ctx, Q8_0, p, (257, 4096), x, y2)
+    g = cap.graph
+    for _ in range(3):
+        ms = g.replay(2)
+        assert ms > 0
+        assert np.array_equal(y1.numpy(), e1) and np.array_equal(y2.numpy(), e2)
+        y1.upload(np.zeros(257, np.float32))
+        rf.matvec(ctx, Q8_0, w, (257, 4096), x, y1)  # eager work between replays
+    g.close()
+    for a in (w, p, x, y1, y2):
+        a.free()
+
+
 def test_matvec_f32_any_length_and_wide_rows(ctx, orc):
     _check_matvec(ctx, orc, F32, 5, 100, 401)     # in_dim not a multiple of 32: rowwise kernel
     _check_matvec(ctx, orc, Q8_0, 40, 40960, 402)  # > 1024 units per row: rowwise kernel

@@ -182,3 +182,141 @@ def test_config4_greedy_tokens_identical(ctx, orc):
         orc.set_parity_threads(0)
         om.close()
         gm.close()
+
+
+# ------------------------------------------------- residency tier (streaming)
+
+STREAM_CFG = dict(TINY, block_count=4, embedding_length=256, feed_forward_length=512, head_dim=64)
+STREAM_TYPES = dict(embd=Q8_0, out=Q6_K, q=Q8_0, k=Q4_K, v=Q4_0, o=Q8_0, gate=Q4_0, up=Q4_0, down=Q6_K)
+
+
+def _layer_bytes(T, li):
+    return sum(arr.nbytes for name, (t, ne0, ne1, arr) in T.items() if name.startswith(f"blk.{li}."))
+
+
+def _streaming_model(cfg, T, budget, cache_bytes, cap=40):
+    rf = _rf()
+    ctx = rf.Context(0, budget)
+    ctx.base_used = ctx.vram_used  # the context's own buffers
+    m = rf.GpuLlamaModel(ctx, cfg, cap)
+    m.enable_streaming(cache_bytes)
+    for name, (t, ne0, ne1, arr) in T.items():
+        m.set_tensor(name, t, ne0, ne1, arr)
+    return ctx, m
+
+
+def _resident_reference(ctx, cfg, T, prompt, n):
+    gm = _load_gpu(ctx, cfg, T, 40)
+    logits = []
+    for p, tok in enumerate(prompt):
+        gm.forward(tok, p)
+        logits.append(gm.logits())
+    gm.reset()
+    toks = gm.generate(prompt, n)
+    gm.close()
+    return logits, toks
+
+
+def test_streamed_layers_match_resident_model(ctx):
+    """Layers streamed from pinned host memory through an LRU cache that holds
+    one of four layers give bit-identical logits and tokens; charges follow
+    load_layer / LayerCache naming; the ledger never exceeds the budget."""
+    rng = np.random.default_rng(1234)
+    T = _tiny_tensors(rng, STREAM_CFG, STREAM_TYPES, bias=True)
+    prompt = [3, 14, 15, 92]
+    ref_logits, ref_toks = _resident_reference(ctx, STREAM_CFG, T, prompt, 10)
+    lb = max(_layer_bytes(T, i) for i in range(4))
+    # persistent tensors, KV, activations and workspaces of this model, measured
+    probe_ctx, probe = _streaming_model(STREAM_CFG, T, 0, 0)
+    base = probe_ctx.vram_used
+    probe.close()
+    probe_ctx.close()
+    budget = base + 2 * lb + 4096  # two layers in flight at once, at most
+    sctx, sm = _streaming_model(STREAM_CFG, T, budget, lb)
+    for p, tok in enumerate(prompt):
+        sm.forward(tok, p)
+        got = sm.logits()
+        assert np.array_equal(got.view(np.uint32), ref_logits[p].view(np.uint32)), p
+        cached = [i for i in range(4) if sctx.charge(f"cache:layer:{i}:attn_q.weight") is not None]
+        active = [i for i in range(4) if sctx.charge(f"layer:{i}:attn_q.weight") is not None]
+        assert len(cached) <= 1 and not active, (cached, active)
+    sm.reset()
+    assert sm.generate(prompt, 10) == ref_toks
+    st = sm.residency_stats()
+    passes = len(prompt) + len(prompt) + 9  # forwards before the reset, then generate (terminal forward skipped)
+    assert st["hits"] + st["misses"] == 4 * passes
+    assert st["evictions"] > 0 and st["uploaded_bytes"] >= st["misses"] * min(_layer_bytes(T, i) for i in range(4))
+    assert sctx.vram_peak <= budget
+    sm.close()
+    assert sctx.vram_used == sctx.base_used
+    sctx.close()
+
+
+def test_next_use_policy_keeps_what_fits(ctx):
+    """Policy 1 on the in-order layer scan: once the cache is full, the layers
+    in it stay (hits every pass) and only the rest are re-uploaded; outputs
+    are identical to the resident model."""
+    rng = np.random.default_rng(1238)
+    T = _tiny_tensors(rng, STREAM_CFG, STREAM_TYPES)
+    prompt = [9, 8, 7]
+    _, ref_toks = _resident_reference(ctx, STREAM_CFG, T, prompt, 8)
+    lb = max(_layer_bytes(T, i) for i in range(4))
+    sctx, sm = _streaming_model(STREAM_CFG, T, 0, 2 * lb)
+    sm.set_cache_policy(1)
+    assert sm.generate(prompt, 8) == ref_toks
+    st = sm.residency_stats()
+    passes = len(prompt) + 7
+    assert st["cached_layers"] == 2
+    assert st["misses"] == 4 + 2 * (passes - 1)  # first pass loads all, then two streamed layers per pass
+    assert st["hits"] == 2 * (passes - 1)
+    sm.close()
+    sctx.close()
+
+
+def test_streaming_without_cache_releases_every_layer(ctx):
+    rng = np.random.default_rng(1235)
+    T = _tiny_tensors(rng, STREAM_CFG, STREAM_TYPES)
+    sctx, sm = _streaming_model(STREAM_CFG, T, 0, 0)
+    before = sctx.vram_used
+    sm.forward(7, 0)
+    assert sctx.vram_used == before  # release_layer after the pass: no layer or cache charge left
+    for i in range(4):
+        assert sctx.charge(f"layer:{i}:attn_q.weight") is None
+        assert sctx.charge(f"cache:layer:{i}:attn_q.weight") is None
+    assert sm.residency_stats()["misses"] == 4 and sm.residency_stats()["cached_layers"] == 0
+    sm.close()
+    sctx.close()
+
+
+def test_streaming_budget_too_small_rolls_back(ctx):
+    rf = _rf()
+    rng = np.random.default_rng(1236)
+    T = _tiny_tensors(rng, STREAM_CFG, STREAM_TYPES)
+    probe_ctx, probe = _streaming_model(STREAM_CFG, T, 0, 0)
+    base = probe_ctx.vram_used
+    probe.close()
+    probe_ctx.close()
+    lb = min(_layer_bytes(T, i) for i in range(4))
+    sctx, sm = _streaming_model(STREAM_CFG, T, base + lb // 2, 10 ** 9)
+    used = sctx.vram_used
+    with pytest.raises(rf.RamforgeError, match="insufficient memory"):
+        sm.forward(7, 0)
+    assert sctx.vram_used == used  # every charge of the failed load released
+    assert sm.seq_len == 0
+    sm.close()
+    sctx.close()
+
+
+def test_streaming_refuses_graph_and_late_enable(ctx):
+    rf = _rf()
+    rng = np.random.default_rng(1237)
+    T = _tiny_tensors(rng, STREAM_CFG, STREAM_TYPES)
+    gm = _load_gpu(ctx, STREAM_CFG, T, 40)
+    with pytest.raises(rf.RamforgeError, match="before block tensors"):
+        gm.enable_streaming(1 << 20)
+    gm.close()
+    sctx, sm = _streaming_model(STREAM_CFG, T, 0, 1 << 30)
+    with pytest.raises(rf.RamforgeError, match="resident"):
+        sm.use_graph(True)
+    sm.close()
+    sctx.close()
