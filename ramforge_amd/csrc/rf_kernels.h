@@ -74,11 +74,11 @@ struct PkArgs {
   const float* x;
   const float* norm_w;
   float eps;
-  uint32_t in_dim, kw;
+  uint32_t in_dim;
 };
 struct PkPlan {
   bool ok;
-  uint32_t lpw, kw;
+  uint32_t lds_bytes;  // x and its slice sums staged in LDS
 };
 struct PkSegDesc {
   const void* packed;     // packed matrix base (codes of row 0)

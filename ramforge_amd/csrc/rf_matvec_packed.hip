@@ -12,18 +12,19 @@
 // GGUF interleaves a 2-byte scale with every 32 (Q8_0) or 16 (Q4_0) code
 // bytes, so its blocks are never 16-byte aligned.  Split apart, the code
 // bytes of a row are one aligned stream that a wavefront reads with 16-byte
-// loads straight into registers (1 KiB per load instruction): no LDS staging,
-// no barrier in the main loop.
+// loads straight into registers.
 //
 // Work decomposition: lane l of a wavefront owns bytes [1024c + 16l, +16) of
-// "chunk" c of every row (16 Q8_0 codes or 32 Q4_0 codes = one block) and
-// keeps the matching x elements in registers.  A wavefront covers LPW chunks;
-// `kw` wavefronts cover a row (kw in {1, 2, 4}); a 256-thread workgroup holds
-// 4/kw row groups.  Each row group takes U rows per step; the next step's
-// codes are requested before the current step is decoded (two register
-// buffers).  Row sums are DPP row reductions plus readlane; with kw > 1 the
-// wavefront partials meet in LDS.  Fusions as in rf_matvec.hip: RMSNorm
-// prologue, residual or SiLU(gate)*up epilogue, up to three output segments.
+// "chunk" c of a row (16 Q8_0 codes or 32 Q4_0 codes); one 16-byte load per
+// lane moves 1 KiB per instruction.  x (normalised when the RMSNorm prologue
+// is fused) and the sum of each lane's x slice of each chunk are staged in
+// LDS once per workgroup, so no register holds x between steps.  A wavefront
+// owns U whole rows (every chunk), so no partial sum crosses wavefronts and
+// the main loop has no barrier; a step is U rows x LPW chunks and the next
+// step's codes are requested before the current one is decoded (two register
+// buffers).  Row sums are DPP row reductions plus readlane.  Fusions as in
+// rf_matvec.hip: RMSNorm prologue, residual or SiLU(gate)*up epilogue, up to
+// three output segments.
 #include "rf_kernels.h"
 
 #include <mutex>
@@ -36,208 +37,204 @@ template <uint32_t T> struct Pk;
 template <> struct Pk<T_Q8_0> {
   static constexpr uint32_t CB = 32;   // code bytes per 32 elements
   static constexpr uint32_t EPL = 16;  // elements per 16-byte lane load
-  __device__ static float dot(const nv_u32x4& q, const float* x, float xsum) {
-    float s = 0.f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint32_t b = q[i] ^ 0x80808080u;  // q + 128 as unsigned bytes
-#pragma unroll
-      for (int k = 0; k < 4; ++k) s = fmaf(rf_ub(b, k), x[4 * i + k], s);
-    }
-    return fmaf(-128.f, xsum, s);
-  }
 };
 template <> struct Pk<T_Q4_0> {
   static constexpr uint32_t CB = 16;
   static constexpr uint32_t EPL = 32;
-  // byte j: low nibble -> element j, high nibble -> element j + 16 (quant.rs:84-113)
-  __device__ static float dot(const nv_u32x4& q, const float* x, float xsum) {
-    float s = 0.f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint32_t lo = rf_opaque(q[i] & 0x0F0F0F0Fu), hi = rf_opaque((q[i] >> 4) & 0x0F0F0F0Fu);
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        s = fmaf(rf_ub(lo, k), x[4 * i + k], s);
-        s = fmaf(rf_ub(hi, k), x[16 + 4 * i + k], s);
-      }
-    }
-    return fmaf(-8.f, xsum, s);
-  }
 };
 
-template <uint32_t T, int EPI, bool NORM, int LPW, int U>
-__global__ __launch_bounds__(256) void matvec_packed(PkArgs a) {
+// The workgroup stages x while its first step's codes are in flight.  x sits
+// in LDS permuted so that the 16-byte reads of a step are consecutive across
+// lanes (no bank conflicts): element 4i + k of lane l's slice of chunk c (EPL
+// elements per slice) is stored at c * 64 * EPL + 256 i + 4 l + k.
+template <uint32_t T, int EPI, bool NORM, int U, int LPW, int NT>
+__global__ __launch_bounds__(NT) void matvec_packed(PkArgs a) {
   constexpr bool DUAL = EPI == EPI_SWIGLU;
-  constexpr uint32_t EPL = Pk<T>::EPL;
-  __shared__ float part[2][4][2 * U];
-  __shared__ float ssq[4];
-  const uint32_t lane = threadIdx.x & 63u, w = threadIdx.x >> 6;
-  const uint32_t kw = a.kw, kwi = w % kw, rgi = w / kw, nrg = 4u / kw;
-  const uint32_t in = a.in_dim, nb = in / 32u;
+  constexpr uint32_t EPL = Pk<T>::EPL, EPB = 32u / Pk<T>::CB, NW = NT / 64;
+  extern __shared__ __align__(16) float xl[];  // [nchunk * 64 * EPL] x, then [nchunk * 64] slice sums
+  __shared__ float wsum[NW];
+  const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+  const uint32_t in = a.in_dim, nb = in / 32u, crb = in / EPB;
+  const uint32_t nchunk = (crb + 1023u) / 1024u, nstep = (nchunk + LPW - 1) / LPW;
+  float* xsum_l = xl + nchunk * 64u * EPL;
 
-  // This lane's code bytes and x elements in each of its LPW chunks.
-  uint32_t boff[LPW], eoff[LPW];
-  bool ok[LPW];
-#pragma unroll
-  for (int l = 0; l < LPW; ++l) {
-    const uint32_t b = (kwi * LPW + l) * 1024u + 16u * lane;
-    const uint32_t e = b * (32u / Pk<T>::CB);
-    ok[l] = e < in;
-    eoff[l] = ok[l] ? e : in - EPL;  // clamped: every load stays in bounds
-    boff[l] = eoff[l] / (32u / Pk<T>::CB);
-  }
-
-  // Row v of all segments -> its segment, chosen with selects (a dynamic
-  // index into the kernel-argument array would be copied to scratch).
   auto seg_of = [&](uint32_t v) -> PkSeg {
     return (a.nseg > 2 && v >= a.seg[2].row_begin) ? a.seg[2]
                                                    : ((a.nseg > 1 && v >= a.seg[1].row_begin) ? a.seg[1] : a.seg[0]);
   };
-  const uint32_t crb = in * Pk<T>::CB / 32u;
+
+  const uint32_t ntask = (a.rows_total + U - 1) / U;
+  const uint32_t gstride = gridDim.x * NW;
 
   nv_u32x4 qa[U][LPW], qb[U][LPW], q2a[U][LPW], q2b[U][LPW];
   uint32_t sa[U][LPW], sb[U][LPW], s2a[U][LPW], s2b[U][LPW];
-  auto fetch = [&](nv_u32x4 (&q)[U][LPW], uint32_t (&sc)[U][LPW], nv_u32x4 (&q2)[U][LPW],
-                   uint32_t (&sc2)[U][LPW], uint32_t v0) {
+  auto fetch = [&](nv_u32x4 (&q)[U][LPW], uint32_t (&sc)[U][LPW], nv_u32x4 (&q2)[U][LPW], uint32_t (&sc2)[U][LPW],
+                   uint32_t t, uint32_t st) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const uint32_t v = min(v0 + u, a.rows_total - 1u);
+      const uint32_t v = min(t * U + u, a.rows_total - 1u);
       const PkSeg g = seg_of(v);
       const uint32_t r = v - g.row_begin;
 #pragma unroll
       for (int l = 0; l < LPW; ++l) {
-        q[u][l] = __builtin_nontemporal_load(reinterpret_cast<const nv_u32x4*>(g.codes + (size_t)r * crb + boff[l]));
-        sc[u][l] = g.scales[(size_t)r * nb + eoff[l] / 32u];
+        const uint32_t b0 = (st * LPW + l) * 1024u + 16u * lane;
+        const uint32_t b = b0 < crb ? b0 : crb - 16u;  // clamped: every load stays in bounds
+        q[u][l] = __builtin_nontemporal_load(reinterpret_cast<const nv_u32x4*>(g.codes + (size_t)r * crb + b));
+        sc[u][l] = g.scales[(size_t)r * nb + b * EPB / 32u];
         if (DUAL) {
-          q2[u][l] = __builtin_nontemporal_load(
-              reinterpret_cast<const nv_u32x4*>(g.codes_up + (size_t)r * crb + boff[l]));
-          sc2[u][l] = g.scales_up[(size_t)r * nb + eoff[l] / 32u];
+          q2[u][l] = __builtin_nontemporal_load(reinterpret_cast<const nv_u32x4*>(g.codes_up + (size_t)r * crb + b));
+          sc2[u][l] = g.scales_up[(size_t)r * nb + b * EPB / 32u];
         }
       }
     }
   };
 
-  // Loop over workgroup batches of nrg * U rows: every wavefront of the
-  // workgroup runs the same number of iterations (barriers below).
-  const uint32_t step = gridDim.x * nrg * U;
-  uint32_t wb = blockIdx.x * nrg * U;
-  const uint32_t off = rgi * U;
-  if (wb < a.rows_total) fetch(qa, sa, q2a, s2a, wb + off);  // weights first, then x
+  uint32_t t = blockIdx.x * NW + wave, st = 0;
+  if (t < ntask) fetch(qa, sa, q2a, s2a, t, 0);  // the first step's codes before the prologue
 
-  float xs[LPW][EPL], xsum[LPW];
-#pragma unroll
-  for (int l = 0; l < LPW; ++l) {
-    const float4* xp = reinterpret_cast<const float4*>(a.x + eoff[l]);
-#pragma unroll
-    for (int i = 0; i < (int)EPL / 4; ++i) {
-      const float4 v = xp[i];
-      xs[l][4 * i] = v.x; xs[l][4 * i + 1] = v.y; xs[l][4 * i + 2] = v.z; xs[l][4 * i + 3] = v.w;
-    }
-  }
+  // Prologue.  rms_norm_reference (core/src/compute.rs:291-319) when NORM:
+  // x / sqrt(mean(x^2) + eps) * w.
+  float inv = 1.f;
   if (NORM) {
-    // rms_norm_reference (core/src/compute.rs:291-319): x / sqrt(mean(x^2) + eps) * w
-    float nwr[LPW][EPL];
+    float ss = 0.f;
+    for (uint32_t i = tid * 4u; i < in; i += NT * 4u) {
+      const float4 v = *reinterpret_cast<const float4*>(a.x + i);
+      ss = fmaf(v.x, v.x, ss); ss = fmaf(v.y, v.y, ss); ss = fmaf(v.z, v.z, ss); ss = fmaf(v.w, v.w, ss);
+    }
+    ss = rf_wave_sum(ss);
+    if (lane == 0) wsum[wave] = ss;
+    __syncthreads();
+    float tot = 0.f;
+#pragma unroll
+    for (uint32_t i = 0; i < NW; ++i) tot += wsum[i];
+    inv = 1.0f / sqrtf(tot / (float)in + a.eps);
+  }
+  for (uint32_t i = tid * 4u; i < in; i += NT * 4u) {
+    float4 v = *reinterpret_cast<const float4*>(a.x + i);
+    if (NORM) {
+      const float4 w = *reinterpret_cast<const float4*>(a.norm_w + i);
+      v.x = v.x * inv * w.x; v.y = v.y * inv * w.y; v.z = v.z * inv * w.z; v.w = v.w * inv * w.w;
+    }
+    const uint32_t c = i / (64u * EPL), r = i % (64u * EPL), l = r / EPL, k4 = (r % EPL) / 4u;
+    *reinterpret_cast<float4*>(xl + c * 64u * EPL + k4 * 256u + 4u * l) = v;
+  }
+  __syncthreads();
+  for (uint32_t j = tid; j < nchunk * 64u; j += NT) {
+    const uint32_t c = j >> 6, l = j & 63u;
+    float s = 0.f;
+    if ((c * 1024u + 16u * l) * EPB < in)
+#pragma unroll
+      for (uint32_t k4 = 0; k4 < EPL / 4u; ++k4) {
+        const float4 v = *reinterpret_cast<const float4*>(xl + c * 64u * EPL + k4 * 256u + 4u * l);
+        s += v.x; s += v.y; s += v.z; s += v.w;
+      }
+    xsum_l[j] = s;
+  }
+  __syncthreads();
+
+  float acc[U], acc2[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) { acc[u] = 0.f; acc2[u] = 0.f; }
+
+  auto consume = [&](const nv_u32x4 (&q)[U][LPW], const uint32_t (&sc)[U][LPW], const nv_u32x4 (&q2)[U][LPW],
+                     const uint32_t (&sc2)[U][LPW], uint32_t tt, uint32_t ss) {
 #pragma unroll
     for (int l = 0; l < LPW; ++l) {
-      const float4* np = reinterpret_cast<const float4*>(a.norm_w + eoff[l]);
+      const uint32_t c = ss * LPW + l;
+      if ((c * 1024u + 16u * lane) * EPB >= in) continue;
+      const float* xp = xl + c * 64u * EPL + 4u * lane;
+      float s[U], s2[U];
 #pragma unroll
-      for (int i = 0; i < (int)EPL / 4; ++i) {
-        const float4 v = np[i];
-        nwr[l][4 * i] = v.x; nwr[l][4 * i + 1] = v.y; nwr[l][4 * i + 2] = v.z; nwr[l][4 * i + 3] = v.w;
-      }
-    }
-    float ss = 0.f;
+      for (int u = 0; u < U; ++u) { s[u] = 0.f; s2[u] = 0.f; }
 #pragma unroll
-    for (int l = 0; l < LPW; ++l)
-      if (ok[l])
+      for (int i = 0; i < 4; ++i) {
+        if (T == T_Q8_0) {
+          const float4 xv = *reinterpret_cast<const float4*>(xp + 256 * i);
+          const float xe[4] = {xv.x, xv.y, xv.z, xv.w};
 #pragma unroll
-        for (int i = 0; i < (int)EPL; ++i) ss = fmaf(xs[l][i], xs[l][i], ss);
-    ss = rf_wave_sum(ss);
-    if (kw > 1) {
-      if (lane == 0) ssq[w] = ss;
-      __syncthreads();
-      ss = 0.f;
-      for (uint32_t k = 0; k < kw; ++k) ss += ssq[rgi * kw + k];
-    }
-    const float inv = 1.0f / sqrtf(ss / (float)in + a.eps);
+          for (int u = 0; u < U; ++u) {
+            const uint32_t w = q[u][l][i] ^ 0x80808080u;  // q + 128 as unsigned bytes
 #pragma unroll
-    for (int l = 0; l < LPW; ++l)
+            for (int k = 0; k < 4; ++k) s[u] = fmaf(rf_ub(w, k), xe[k], s[u]);
+            if (DUAL) {
+              const uint32_t w2 = q2[u][l][i] ^ 0x80808080u;
 #pragma unroll
-      for (int i = 0; i < (int)EPL; ++i) xs[l][i] = xs[l][i] * inv * nwr[l][i];
-  }
+              for (int k = 0; k < 4; ++k) s2[u] = fmaf(rf_ub(w2, k), xe[k], s2[u]);
+            }
+          }
+        } else {
+          // byte j: low nibble -> element j, high nibble -> element j + 16 (quant.rs:84-113)
+          const float4 xv = *reinterpret_cast<const float4*>(xp + 256 * i);
+          const float4 xw = *reinterpret_cast<const float4*>(xp + 256 * (i + 4));
+          const float xe[4] = {xv.x, xv.y, xv.z, xv.w}, xh[4] = {xw.x, xw.y, xw.z, xw.w};
 #pragma unroll
-  for (int l = 0; l < LPW; ++l) {
-    float s = 0.f;
+          for (int u = 0; u < U; ++u) {
+            const uint32_t lo = rf_opaque(q[u][l][i] & 0x0F0F0F0Fu), hi = rf_opaque((q[u][l][i] >> 4) & 0x0F0F0F0Fu);
 #pragma unroll
-    for (int i = 0; i < (int)EPL; ++i) s += xs[l][i];
-    xsum[l] = s;
-  }
-
-  int buf = 0;
-  auto consume = [&](const nv_u32x4 (&q)[U][LPW], const uint32_t (&sc)[U][LPW], const nv_u32x4 (&q2)[U][LPW],
-                     const uint32_t (&sc2)[U][LPW], uint32_t v0) {
-    float v[U], v2[U];
+            for (int k = 0; k < 4; ++k) {
+              s[u] = fmaf(rf_ub(lo, k), xe[k], s[u]);
+              s[u] = fmaf(rf_ub(hi, k), xh[k], s[u]);
+            }
+            if (DUAL) {
+              const uint32_t lo2 = rf_opaque(q2[u][l][i] & 0x0F0F0F0Fu),
+                             hi2 = rf_opaque((q2[u][l][i] >> 4) & 0x0F0F0F0Fu);
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      float acc = 0.f, acc2 = 0.f;
-#pragma unroll
-      for (int l = 0; l < LPW; ++l) {
-        if (!ok[l]) continue;
-        acc = fmaf(rf_half_to_float(sc[u][l]), Pk<T>::dot(q[u][l], xs[l], xsum[l]), acc);
-        if (DUAL) acc2 = fmaf(rf_half_to_float(sc2[u][l]), Pk<T>::dot(q2[u][l], xs[l], xsum[l]), acc2);
-      }
-      v[u] = rf_wave_sum(acc);
-      v2[u] = DUAL ? rf_wave_sum(acc2) : 0.f;
-    }
-    if (kw > 1) {
-      if (lane == 0)
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-          part[buf][w][u] = v[u];
-          if (DUAL) part[buf][w][U + u] = v2[u];
+              for (int k = 0; k < 4; ++k) {
+                s2[u] = fmaf(rf_ub(lo2, k), xe[k], s2[u]);
+                s2[u] = fmaf(rf_ub(hi2, k), xh[k], s2[u]);
+              }
+            }
+          }
         }
-      __syncthreads();
+      }
+      const float xs = xsum_l[c * 64u + lane];
+      constexpr float bias = T == T_Q8_0 ? -128.f : -8.f;
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        float t = 0.f, t2 = 0.f;
-        for (uint32_t k = 0; k < kw; ++k) {
-          t += part[buf][rgi * kw + k][u];
-          if (DUAL) t2 += part[buf][rgi * kw + k][U + u];
-        }
-        v[u] = t;
-        v2[u] = t2;
+        acc[u] = fmaf(rf_half_to_float(sc[u][l]), fmaf(bias, xs, s[u]), acc[u]);
+        if (DUAL) acc2[u] = fmaf(rf_half_to_float(sc2[u][l]), fmaf(bias, xs, s2[u]), acc2[u]);
       }
-      buf ^= 1;  // the other buffer is written next step: no second barrier
     }
-    if (kwi == 0 && lane < (uint32_t)U) {
-      float mine = 0.f, mine2 = 0.f;
+    if (ss + 1u == nstep) {  // the task's rows are complete
+      float v[U], v2[U];
 #pragma unroll
-      for (int u = 0; u < U; ++u)
-        if (lane == (uint32_t)u) { mine = v[u]; mine2 = v2[u]; }
-      const uint32_t vr = v0 + lane;
-      if (vr < a.rows_total) {
-        const PkSeg g = seg_of(vr);
-        const uint32_t o = vr - g.row_begin;
-        if (EPI == EPI_STORE) {
-          g.y[o] = mine;
-        } else if (EPI == EPI_RESIDUAL) {
-          g.y[o] = g.res[o] + mine;  // add_reference (compute.rs:321-327)
-        } else {
-          g.y[o] = mine / (1.0f + expf(-mine)) * mine2;  // silu_reference * up (compute.rs:337-350)
+      for (int u = 0; u < U; ++u) {
+        v[u] = rf_wave_sum(acc[u]);
+        v2[u] = DUAL ? rf_wave_sum(acc2[u]) : 0.f;
+        acc[u] = 0.f;
+        acc2[u] = 0.f;
+      }
+      if (lane < (uint32_t)U) {
+        float mine = 0.f, mine2 = 0.f;
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+          if (lane == (uint32_t)u) { mine = v[u]; mine2 = v2[u]; }
+        const uint32_t vr = tt * U + lane;
+        if (vr < a.rows_total) {
+          const PkSeg g = seg_of(vr);
+          const uint32_t o = vr - g.row_begin;
+          if (EPI == EPI_STORE) g.y[o] = mine;
+          else if (EPI == EPI_RESIDUAL) g.y[o] = g.res[o] + mine;  // add_reference (compute.rs:321-327)
+          else g.y[o] = mine / (1.0f + expf(-mine)) * mine2;  // silu_reference * up (compute.rs:337-350)
         }
       }
     }
   };
-  while (wb < a.rows_total) {
-    const uint32_t w1 = wb + step;
-    if (w1 < a.rows_total) fetch(qb, sb, q2b, s2b, w1 + off);
-    consume(qa, sa, q2a, s2a, wb + off);
-    if (w1 >= a.rows_total) break;
-    const uint32_t w2 = w1 + step;
-    if (w2 < a.rows_total) fetch(qa, sa, q2a, s2a, w2 + off);
-    consume(qb, sb, q2b, s2b, w1 + off);
-    wb = w2;
+  auto advance = [&](uint32_t& tt, uint32_t& ss) {
+    if (++ss == nstep) { ss = 0; tt += gstride; }
+  };
+  while (t < ntask) {
+    uint32_t t1 = t, s1 = st;
+    advance(t1, s1);
+    if (t1 < ntask) fetch(qb, sb, q2b, s2b, t1, s1);
+    consume(qa, sa, q2a, s2a, t, st);
+    if (t1 >= ntask) break;
+    uint32_t t2 = t1, s2 = s1;
+    advance(t2, s2);
+    if (t2 < ntask) fetch(qa, sa, q2a, s2a, t2, s2);
+    consume(qb, sb, q2b, s2b, t1, s1);
+    t = t2;
+    st = s2;
   }
 }
 
@@ -260,23 +257,32 @@ __global__ __launch_bounds__(256) void pack_blocks(const uint8_t* __restrict__ r
 
 bool packed_type(uint32_t t) { return t == T_Q8_0 || t == T_Q4_0; }
 
+static uint32_t pk_lds_limit() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 65536;
+  if (!cached[dev]) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess || n < 65536)
+      n = 65536;
+    cached[dev] = n;
+  }
+  return (uint32_t)cached[dev];
+}
+
+static uint64_t pk_nchunk(uint32_t t, uint64_t in_dim) {
+  const uint64_t crb = in_dim * (t == T_Q8_0 ? 32u : 16u) / 32u;
+  return (crb + 1023) / 1024;
+}
+
 PkPlan plan_packed(uint32_t t, uint64_t in_dim) {
   PkPlan p{};
   if (!packed_type(t) || in_dim == 0 || in_dim % 32 != 0 || in_dim > (1u << 24)) return p;
-  const uint32_t cb = t == T_Q8_0 ? 32u : 16u;
-  const uint64_t crb = in_dim * cb / 32;
-  const uint32_t nchunk = (uint32_t)((crb + 1023) / 1024);
-  uint32_t lpw, kw;
-  if (nchunk <= 1) { lpw = 1; kw = 1; }
-  else if (nchunk <= 2) { lpw = 2; kw = 1; }
-  else if (nchunk <= 8) { lpw = 2; kw = (nchunk + 1) / 2; }
-  else { lpw = 4; kw = (nchunk + 3) / 4; }
-  if (t == T_Q4_0 && lpw == 4) { lpw = 2; kw = (nchunk + 1) / 2; }  // 32 x floats per chunk: keep 64
-  if (kw == 3) kw = 4;
-  if (kw > 4) return p;
+  const uint64_t nchunk = pk_nchunk(t, in_dim), epl = t == T_Q8_0 ? 16 : 32;
+  const uint64_t lds = (nchunk * 64 * epl + nchunk * 64) * 4 + 64;  // + the static reduction slots
+  if (lds > pk_lds_limit()) return p;
   p.ok = true;
-  p.lpw = lpw;
-  p.kw = kw;
+  p.lds_bytes = (uint32_t)(lds - 64);
   return p;
 }
 
@@ -292,63 +298,80 @@ static int pk_cu_count() {
   return cached[dev];
 }
 
-template <uint32_t T, int EPI, bool NORM, int LPW, int U>
-static hipError_t launch_pk(const PkArgs& a, hipStream_t st) {
-  static std::mutex mu;
-  static int occ_cache = 0;
-  int occ;
-  {
-    std::lock_guard<std::mutex> lock(mu);
-    if (!occ_cache) {
-      int n = 0;
-      if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, matvec_packed<T, EPI, NORM, LPW, U>, 256, 0) !=
-              hipSuccess || n < 1)
-        n = 1;
-      occ_cache = n;
-    }
-    occ = occ_cache;
+// Resident workgroups per CU of one kernel at one LDS size; the caller keeps
+// one cache per kernel (a few distinct sizes per model).
+struct PkOccCache {
+  std::mutex mu;
+  uint32_t keys[16];
+  int vals[16];
+  int n = 0;
+  bool attr_set = false;
+};
+static int pk_occupancy(PkOccCache& c, const void* kern, int nt, uint32_t lds) {
+  std::lock_guard<std::mutex> lock(c.mu);
+  for (int i = 0; i < c.n; ++i)
+    if (c.keys[i] == lds) return c.vals[i];
+  if (lds > 65536 && !c.attr_set) {
+    if (hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)pk_lds_limit()) != hipSuccess)
+      return 0;
+    c.attr_set = true;
   }
-  const uint32_t nrg = 4u / a.kw;
-  const uint64_t batches = (a.rows_total + (uint64_t)nrg * U - 1) / ((uint64_t)nrg * U);
-  const uint64_t cap = (uint64_t)pk_cu_count() * occ;
-  const uint32_t grid = (uint32_t)(batches < cap ? batches : cap);
-  hipLaunchKernelGGL((matvec_packed<T, EPI, NORM, LPW, U>), dim3(grid), dim3(256), 0, st, a);
+  int occ = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kern, nt, lds) != hipSuccess || occ < 1) occ = 1;
+  if (c.n < 16) {
+    c.keys[c.n] = lds;
+    c.vals[c.n] = occ;
+    ++c.n;
+  }
+  return occ;
+}
+
+template <uint32_t T, int EPI, bool NORM, int LPW, int NT>
+static hipError_t launch_pk(const PkArgs& a, uint32_t lds, hipStream_t st) {
+  constexpr int U = 1;
+  static PkOccCache cache;
+  auto kern = matvec_packed<T, EPI, NORM, U, LPW, NT>;
+  const int occ = pk_occupancy(cache, reinterpret_cast<const void*>(kern), NT, lds);
+  if (occ < 1) return hipErrorInvalidConfiguration;
+  const uint64_t tasks = (a.rows_total + U - 1) / U, nw = NT / 64;
+  const uint64_t want = (tasks + nw - 1) / nw, cap = (uint64_t)pk_cu_count() * occ;
+  const uint32_t grid = (uint32_t)(want < cap ? want : cap);
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(NT), lds, st, a);
   return hipGetLastError();
 }
 
-// Rows per step U against chunks per lane LPW: two register buffers of
-// U x LPW x (16 B codes, twice for gate/up) plus LPW x EPL x floats stay
-// within about 190 VGPRs (chosen by timing the 8B projections: the spread
-// between the candidates was within 15%).
-template <uint32_t T, int EPI, int LPW>
-constexpr int pk_rows_per_step() {
-  constexpr bool dual = EPI == EPI_SWIGLU;
-  if (LPW >= 4) return dual ? 1 : 2;
-  if (LPW == 2) return (T == T_Q4_0 && dual) ? 1 : 2;
-  return dual ? 2 : 4;
-}
-
+// Launch shape, from timing the 8B projections (Q8_0 and Q4_0; 4096 and
+// 14336 inputs): one row per wavefront; LPW = chunks per step, up to 4 (2 for
+// gate/up, whose step loads two matrices); 1024-thread workgroups when x fills
+// more than 40 KB of LDS (two resident workgroups then still give 32
+// wavefronts per CU), else 512.
 template <uint32_t T, int EPI, bool NORM>
-static hipError_t launch_pk_l(const PkArgs& a, uint32_t lpw, hipStream_t st) {
-  switch (lpw) {
-    case 1: return launch_pk<T, EPI, NORM, 1, pk_rows_per_step<T, EPI, 1>()>(a, st);
-    case 2: return launch_pk<T, EPI, NORM, 2, pk_rows_per_step<T, EPI, 2>()>(a, st);
-    case 4:
-      if constexpr (T == T_Q8_0) return launch_pk<T, EPI, NORM, 4, pk_rows_per_step<T, EPI, 4>()>(a, st);
-      return hipErrorInvalidValue;
+static hipError_t launch_pk_l(const PkArgs& a, uint32_t lds, hipStream_t st) {
+  const uint64_t nchunk = pk_nchunk(T, a.in_dim);
+  const uint32_t pref = EPI == EPI_SWIGLU ? 2 : 4;
+  uint32_t lpw = 1;
+  while (lpw * 2 <= pref && lpw * 2 <= nchunk) lpw *= 2;
+  const bool big = lds > 40960;
+  switch (lpw * 2 + (big ? 1 : 0)) {
+    case 2: return launch_pk<T, EPI, NORM, 1, 512>(a, lds, st);
+    case 3: return launch_pk<T, EPI, NORM, 1, 1024>(a, lds, st);
+    case 4: return launch_pk<T, EPI, NORM, 2, 512>(a, lds, st);
+    case 5: return launch_pk<T, EPI, NORM, 2, 1024>(a, lds, st);
+    case 8: return launch_pk<T, EPI, NORM, 4, 512>(a, lds, st);
+    case 9: return launch_pk<T, EPI, NORM, 4, 1024>(a, lds, st);
     default: return hipErrorInvalidValue;
   }
 }
 
 template <uint32_t T>
-static hipError_t launch_pk_t(const PkArgs& a, uint32_t lpw, int epi, bool norm, hipStream_t st) {
+static hipError_t launch_pk_t(const PkArgs& a, uint32_t lds, int epi, bool norm, hipStream_t st) {
   switch (epi * 2 + (norm ? 1 : 0)) {
-    case EPI_STORE * 2: return launch_pk_l<T, EPI_STORE, false>(a, lpw, st);
-    case EPI_STORE * 2 + 1: return launch_pk_l<T, EPI_STORE, true>(a, lpw, st);
-    case EPI_RESIDUAL * 2: return launch_pk_l<T, EPI_RESIDUAL, false>(a, lpw, st);
-    case EPI_RESIDUAL * 2 + 1: return launch_pk_l<T, EPI_RESIDUAL, true>(a, lpw, st);
-    case EPI_SWIGLU * 2: return launch_pk_l<T, EPI_SWIGLU, false>(a, lpw, st);
-    case EPI_SWIGLU * 2 + 1: return launch_pk_l<T, EPI_SWIGLU, true>(a, lpw, st);
+    case EPI_STORE * 2: return launch_pk_l<T, EPI_STORE, false>(a, lds, st);
+    case EPI_STORE * 2 + 1: return launch_pk_l<T, EPI_STORE, true>(a, lds, st);
+    case EPI_RESIDUAL * 2: return launch_pk_l<T, EPI_RESIDUAL, false>(a, lds, st);
+    case EPI_RESIDUAL * 2 + 1: return launch_pk_l<T, EPI_RESIDUAL, true>(a, lds, st);
+    case EPI_SWIGLU * 2: return launch_pk_l<T, EPI_SWIGLU, false>(a, lds, st);
+    case EPI_SWIGLU * 2 + 1: return launch_pk_l<T, EPI_SWIGLU, true>(a, lds, st);
     default: return hipErrorInvalidValue;
   }
 }
@@ -390,10 +413,9 @@ hipError_t launch_matvec_packed(uint32_t t, const PkSegDesc* segs, int nseg, con
   a.norm_w = norm_w;
   a.eps = eps;
   a.in_dim = (uint32_t)in_dim;
-  a.kw = p.kw;
   switch (t) {
-    case T_Q8_0: return launch_pk_t<T_Q8_0>(a, p.lpw, epi, norm_w != nullptr, st);
-    case T_Q4_0: return launch_pk_t<T_Q4_0>(a, p.lpw, epi, norm_w != nullptr, st);
+    case T_Q8_0: return launch_pk_t<T_Q8_0>(a, p.lds_bytes, epi, norm_w != nullptr, st);
+    case T_Q4_0: return launch_pk_t<T_Q4_0>(a, p.lds_bytes, epi, norm_w != nullptr, st);
     default: return hipErrorInvalidValue;
   }
 }

@@ -204,8 +204,12 @@ def _check_matvec_packed(ctx, orc, t, out_dim, in_dim, seed, row_start=0, row_co
 
 @pytest.mark.parametrize("t", [Q8_0, Q4_0])
 @pytest.mark.parametrize("out_dim,in_dim", [(1, 32), (67, 96), (130, 1024), (33, 2048), (70, 3072), (257, 4096),
-                                            (1000, 5120), (4096, 4096), (14336, 4096), (4096, 14336), (9, 16384)])
+                                            (1000, 5120), (4096, 4096), (14336, 4096), (4096, 14336), (9, 16384),
+                                            (5, 28672)])
 def test_matvec_packed_shapes(ctx, orc, t, out_dim, in_dim):
+    if not _rf().packed_supported(t, in_dim):
+        # x of a row must fit the workgroup's LDS (64 KiB, or what the device allows)
+        pytest.skip(f"in_dim {in_dim} exceeds this device's LDS for {NAMES[t]}")
     _check_matvec_packed(ctx, orc, t, out_dim, in_dim, 1200 + t + in_dim % 977 + out_dim)
 
 
@@ -230,7 +234,8 @@ def test_matvec_packed_validation(ctx):
     with pytest.raises(rf.RamforgeError, match="does not support"):
         rf.matvec_packed(ctx, Q4_K, w, (1, 256), x, y)
     assert y.numpy().tolist() == [7.0, 7.0]  # destination untouched
-    assert not rf.packed_supported(Q8_0, 32768) and rf.packed_supported(Q4_0, 14336)
+    assert not rf.packed_supported(Q8_0, 1 << 16) and rf.packed_supported(Q4_0, 14336)
+    assert rf.packed_supported(Q8_0, 14336) and not rf.packed_supported(Q8_0, 100)
     for a in (w, x, y):
         a.free()
 
