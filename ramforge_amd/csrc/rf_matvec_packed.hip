@@ -16,9 +16,9 @@
 //
 // Work decomposition: lane l of a wavefront owns bytes [1024c + 16l, +16) of
 // "chunk" c of a row (16 Q8_0 codes or 32 Q4_0 codes); one 16-byte load per
-// lane moves 1 KiB per instruction.  x (normalised when the RMSNorm prologue
-// is fused) and the sum of each lane's x slice of each chunk are staged in
-// LDS once per workgroup, so no register holds x between steps.  A wavefront
+// lane moves 1 KiB per instruction.  x (times the norm weights when the
+// RMSNorm prologue is fused) and the sums of its 16-element units are staged
+// in LDS once per workgroup, so no register holds x between steps.  A wavefront
 // owns U whole rows (every chunk), so no partial sum crosses wavefronts and
 // the main loop has no barrier; a step is U rows x LPW chunks and the next
 // step's codes are requested before the current one is decoded (two register
@@ -51,7 +51,7 @@ template <uint32_t T, int EPI, bool NORM, int U, int LPW, int NT>
 __global__ __launch_bounds__(NT) void matvec_packed(PkArgs a) {
   constexpr bool DUAL = EPI == EPI_SWIGLU;
   constexpr uint32_t EPL = Pk<T>::EPL, EPB = 32u / Pk<T>::CB, NW = NT / 64;
-  extern __shared__ __align__(16) float xl[];  // [nchunk * 64 * EPL] x, then [nchunk * 64] slice sums
+  extern __shared__ __align__(16) float xl[];  // [nchunk * 64 * EPL] x, then [nchunk * 64 * EPL / 16] unit sums
   __shared__ float wsum[NW];
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
   const uint32_t in = a.in_dim, nb = in / 32u, crb = in / EPB;
@@ -92,45 +92,57 @@ __global__ __launch_bounds__(NT) void matvec_packed(PkArgs a) {
   uint32_t t = blockIdx.x * NW + wave, st = 0;
   if (t < ntask) fetch(qa, sa, q2a, s2a, t, 0);  // the first step's codes before the prologue
 
-  // Prologue.  rms_norm_reference (core/src/compute.rs:291-319) when NORM:
-  // x / sqrt(mean(x^2) + eps) * w.
+  // Prologue, one round of loads and one barrier.  Thread j (then j + NT, ...)
+  // owns unit j: 16 consecutive elements, one lane slice of a Q8_0 chunk or
+  // half of a Q4_0 one.  It writes the unit into LDS and the unit's sum.
+  // With NORM, rms_norm_reference (core/src/compute.rs:291-319) is
+  // x / sqrt(mean(x^2) + eps) * w; LDS holds x * w and every row sum is
+  // scaled by 1 / sqrt(mean(x^2) + eps) in the epilogue (the same value up to
+  // rounding), so the mean's reduction shares the prologue's barrier.
+  constexpr uint32_t UPS = EPL / 16u;  // units per lane slice
+  const uint32_t nunit = nchunk * 64u * UPS;
+  {
+    const float4* x4 = reinterpret_cast<const float4*>(a.x);
+    const float4* w4 = reinterpret_cast<const float4*>(a.norm_w);
+    float ss = 0.f;
+    for (uint32_t j = tid; j < nunit; j += NT) {
+      const uint32_t js = j / UPS, h = j % UPS;
+      const uint32_t e = ((js >> 6) * 1024u + 16u * (js & 63u)) * EPB + 16u * h;
+      float s = 0.f;
+      if (e < in) {
+        float4 v[4], w[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          v[k] = x4[e / 4u + k];
+          if (NORM) w[k] = w4[e / 4u + k];
+        }
+        float* dst = xl + (js >> 6) * 64u * EPL + 4u * h * 256u + 4u * (js & 63u);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          if (NORM) {
+            ss = fmaf(v[k].x, v[k].x, ss); ss = fmaf(v[k].y, v[k].y, ss);
+            ss = fmaf(v[k].z, v[k].z, ss); ss = fmaf(v[k].w, v[k].w, ss);
+            v[k].x *= w[k].x; v[k].y *= w[k].y; v[k].z *= w[k].z; v[k].w *= w[k].w;
+          }
+          *reinterpret_cast<float4*>(dst + 256 * k) = v[k];
+          s += v[k].x; s += v[k].y; s += v[k].z; s += v[k].w;
+        }
+      }
+      xsum_l[j] = s;
+    }
+    if (NORM) {
+      ss = rf_wave_sum(ss);
+      if (lane == 0) wsum[wave] = ss;
+    }
+  }
+  __syncthreads();
   float inv = 1.f;
   if (NORM) {
-    float ss = 0.f;
-    for (uint32_t i = tid * 4u; i < in; i += NT * 4u) {
-      const float4 v = *reinterpret_cast<const float4*>(a.x + i);
-      ss = fmaf(v.x, v.x, ss); ss = fmaf(v.y, v.y, ss); ss = fmaf(v.z, v.z, ss); ss = fmaf(v.w, v.w, ss);
-    }
-    ss = rf_wave_sum(ss);
-    if (lane == 0) wsum[wave] = ss;
-    __syncthreads();
     float tot = 0.f;
 #pragma unroll
     for (uint32_t i = 0; i < NW; ++i) tot += wsum[i];
     inv = 1.0f / sqrtf(tot / (float)in + a.eps);
   }
-  for (uint32_t i = tid * 4u; i < in; i += NT * 4u) {
-    float4 v = *reinterpret_cast<const float4*>(a.x + i);
-    if (NORM) {
-      const float4 w = *reinterpret_cast<const float4*>(a.norm_w + i);
-      v.x = v.x * inv * w.x; v.y = v.y * inv * w.y; v.z = v.z * inv * w.z; v.w = v.w * inv * w.w;
-    }
-    const uint32_t c = i / (64u * EPL), r = i % (64u * EPL), l = r / EPL, k4 = (r % EPL) / 4u;
-    *reinterpret_cast<float4*>(xl + c * 64u * EPL + k4 * 256u + 4u * l) = v;
-  }
-  __syncthreads();
-  for (uint32_t j = tid; j < nchunk * 64u; j += NT) {
-    const uint32_t c = j >> 6, l = j & 63u;
-    float s = 0.f;
-    if ((c * 1024u + 16u * l) * EPB < in)
-#pragma unroll
-      for (uint32_t k4 = 0; k4 < EPL / 4u; ++k4) {
-        const float4 v = *reinterpret_cast<const float4*>(xl + c * 64u * EPL + k4 * 256u + 4u * l);
-        s += v.x; s += v.y; s += v.z; s += v.w;
-      }
-    xsum_l[j] = s;
-  }
-  __syncthreads();
 
   float acc[U], acc2[U];
 #pragma unroll
@@ -187,7 +199,8 @@ __global__ __launch_bounds__(NT) void matvec_packed(PkArgs a) {
           }
         }
       }
-      const float xs = xsum_l[c * 64u + lane];
+      const float xs = UPS == 1 ? xsum_l[c * 64u + lane]
+                                : xsum_l[(c * 64u + lane) * 2u] + xsum_l[(c * 64u + lane) * 2u + 1u];
       constexpr float bias = T == T_Q8_0 ? -128.f : -8.f;
 #pragma unroll
       for (int u = 0; u < U; ++u) {
@@ -199,8 +212,8 @@ __global__ __launch_bounds__(NT) void matvec_packed(PkArgs a) {
       float v[U], v2[U];
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        v[u] = rf_wave_sum(acc[u]);
-        v2[u] = DUAL ? rf_wave_sum(acc2[u]) : 0.f;
+        v[u] = rf_wave_sum(acc[u]) * inv;
+        v2[u] = DUAL ? rf_wave_sum(acc2[u]) * inv : 0.f;
         acc[u] = 0.f;
         acc2[u] = 0.f;
       }
@@ -279,7 +292,7 @@ PkPlan plan_packed(uint32_t t, uint64_t in_dim) {
   PkPlan p{};
   if (!packed_type(t) || in_dim == 0 || in_dim % 32 != 0 || in_dim > (1u << 24)) return p;
   const uint64_t nchunk = pk_nchunk(t, in_dim), epl = t == T_Q8_0 ? 16 : 32;
-  const uint64_t lds = (nchunk * 64 * epl + nchunk * 64) * 4 + 64;  // + the static reduction slots
+  const uint64_t lds = (nchunk * 64 * epl + nchunk * 64 * (epl / 16)) * 4 + 64;  // + the static reduction slots
   if (lds > pk_lds_limit()) return p;
   p.ok = true;
   p.lds_bytes = (uint32_t)(lds - 64);

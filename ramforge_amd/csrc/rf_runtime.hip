@@ -538,8 +538,9 @@ int32_t rf_matvec_packed(rf_ctx* ctx, uint32_t t, const void* packed, uint64_t p
                                &rb, &done);
   if (rc || done) return rc;
   if (!plan_packed(t, in_dim).ok)
-    return set_error(RF_ERR_UNSUPPORTED, "packed %s matvec supports in_dim up to 16384, got %llu", type_name(t),
-                     (unsigned long long)in_dim);
+    return set_error(RF_ERR_UNSUPPORTED,
+                     "packed %s matvec stages x in LDS: in_dim %llu exceeds this device's workgroup LDS",
+                     type_name(t), (unsigned long long)in_dim);
   hipStream_t st = pick_stream(ctx, s);
   const float* xa = x;
   if ((reinterpret_cast<uintptr_t>(x) & 15u) != 0) {
