@@ -453,11 +453,15 @@ bool attention_supported(uint32_t qh, uint32_t kvh, uint32_t hd, uint64_t total)
 }
 
 // Chunks per KV head: 64 positions each while that keeps the launch within
-// about 1024 workgroups, longer chunks beyond (at most ATT_MAX_SPLITS chunks
-// of at most ATT_MAX_CHUNK positions).
+// about 256 workgroups (one per CU), longer chunks beyond (at most
+// ATT_MAX_SPLITS chunks of at most ATT_MAX_CHUNK positions).  Timed on
+// 32 q / 8 KV heads, hd 128, split + merge per layer: 256 workgroups beat
+// 1024 at every length from 256 to 8192 positions (9.3 vs 13.2 us at 512,
+// 20.5 vs 24.5 us at 8192); workgroups of chunks past the end still cost
+// their dispatch.
 uint32_t attention_splits(uint32_t total, uint32_t kvh) {
   uint32_t n = (total + ATT_MIN_CHUNK - 1) / ATT_MIN_CHUNK;
-  uint32_t cap = 1024u / (kvh ? kvh : 1u);
+  uint32_t cap = 256u / (kvh ? kvh : 1u);
   if (cap > ATT_MAX_SPLITS) cap = ATT_MAX_SPLITS;
   if (cap < 1) cap = 1;
   if (n > cap) n = cap;

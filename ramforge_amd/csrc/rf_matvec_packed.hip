@@ -47,7 +47,16 @@ template <> struct Pk<T_Q4_0> {
 // in LDS permuted so that the 16-byte reads of a step are consecutive across
 // lanes (no bank conflicts): element 4i + k of lane l's slice of chunk c (EPL
 // elements per slice) is stored at c * 64 * EPL + 256 i + 4 l + k.
-template <uint32_t T, int EPI, bool NORM, int U, int LPW, int NT>
+// Codes and scales of one step: U rows x LPW chunks (twice with the "up" matrix).
+template <int U, int LPW, bool DUAL>
+struct PkStep {
+  nv_u32x4 q[U][LPW], q2[DUAL ? U : 1][LPW];
+  uint32_t s[U][LPW], s2[DUAL ? U : 1][LPW];
+};
+
+// NB step buffers per wavefront: NB - 1 steps are in flight while one is
+// decoded.
+template <uint32_t T, int EPI, bool NORM, int U, int LPW, int NB, int NT>
 __global__ __launch_bounds__(NT) void matvec_packed(PkArgs a) {
   constexpr bool DUAL = EPI == EPI_SWIGLU;
   constexpr uint32_t EPL = Pk<T>::EPL, EPB = 32u / Pk<T>::CB, NW = NT / 64;
@@ -66,10 +75,9 @@ __global__ __launch_bounds__(NT) void matvec_packed(PkArgs a) {
   const uint32_t ntask = (a.rows_total + U - 1) / U;
   const uint32_t gstride = gridDim.x * NW;
 
-  nv_u32x4 qa[U][LPW], qb[U][LPW], q2a[U][LPW], q2b[U][LPW];
-  uint32_t sa[U][LPW], sb[U][LPW], s2a[U][LPW], s2b[U][LPW];
-  auto fetch = [&](nv_u32x4 (&q)[U][LPW], uint32_t (&sc)[U][LPW], nv_u32x4 (&q2)[U][LPW], uint32_t (&sc2)[U][LPW],
-                   uint32_t t, uint32_t st) {
+  typedef PkStep<U, LPW, DUAL> Step;
+  Step buf[NB];
+  auto fetch = [&](Step& B, uint32_t t, uint32_t st) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const uint32_t v = min(t * U + u, a.rows_total - 1u);
@@ -79,18 +87,26 @@ __global__ __launch_bounds__(NT) void matvec_packed(PkArgs a) {
       for (int l = 0; l < LPW; ++l) {
         const uint32_t b0 = (st * LPW + l) * 1024u + 16u * lane;
         const uint32_t b = b0 < crb ? b0 : crb - 16u;  // clamped: every load stays in bounds
-        q[u][l] = __builtin_nontemporal_load(reinterpret_cast<const nv_u32x4*>(g.codes + (size_t)r * crb + b));
-        sc[u][l] = g.scales[(size_t)r * nb + b * EPB / 32u];
-        if (DUAL) {
-          q2[u][l] = __builtin_nontemporal_load(reinterpret_cast<const nv_u32x4*>(g.codes_up + (size_t)r * crb + b));
-          sc2[u][l] = g.scales_up[(size_t)r * nb + b * EPB / 32u];
+        B.q[u][l] = __builtin_nontemporal_load(reinterpret_cast<const nv_u32x4*>(g.codes + (size_t)r * crb + b));
+        B.s[u][l] = g.scales[(size_t)r * nb + b * EPB / 32u];
+        if constexpr (DUAL) {
+          B.q2[u][l] = __builtin_nontemporal_load(reinterpret_cast<const nv_u32x4*>(g.codes_up + (size_t)r * crb + b));
+          B.s2[u][l] = g.scales_up[(size_t)r * nb + b * EPB / 32u];
         }
       }
     }
   };
 
-  uint32_t t = blockIdx.x * NW + wave, st = 0;
-  if (t < ntask) fetch(qa, sa, q2a, s2a, t, 0);  // the first step's codes before the prologue
+  auto advance = [&](uint32_t& tt, uint32_t& ss) {
+    if (++ss == nstep) { ss = 0; tt += gstride; }
+  };
+  // The first NB - 1 steps are requested before the prologue.
+  uint32_t ct = blockIdx.x * NW + wave, cs = 0, ft = ct, fs = 0;
+#pragma unroll
+  for (int b = 0; b < NB - 1; ++b) {
+    if (ft < ntask) fetch(buf[b], ft, fs);
+    advance(ft, fs);
+  }
 
   // Prologue, one round of loads and one barrier.  Thread j (then j + NT, ...)
   // owns unit j: 16 consecutive elements, one lane slice of a Q8_0 chunk or
@@ -148,8 +164,7 @@ __global__ __launch_bounds__(NT) void matvec_packed(PkArgs a) {
 #pragma unroll
   for (int u = 0; u < U; ++u) { acc[u] = 0.f; acc2[u] = 0.f; }
 
-  auto consume = [&](const nv_u32x4 (&q)[U][LPW], const uint32_t (&sc)[U][LPW], const nv_u32x4 (&q2)[U][LPW],
-                     const uint32_t (&sc2)[U][LPW], uint32_t tt, uint32_t ss) {
+  auto consume = [&](const Step& B, uint32_t tt, uint32_t ss) {
 #pragma unroll
     for (int l = 0; l < LPW; ++l) {
       const uint32_t c = ss * LPW + l;
@@ -165,11 +180,11 @@ __global__ __launch_bounds__(NT) void matvec_packed(PkArgs a) {
           const float xe[4] = {xv.x, xv.y, xv.z, xv.w};
 #pragma unroll
           for (int u = 0; u < U; ++u) {
-            const uint32_t w = q[u][l][i] ^ 0x80808080u;  // q + 128 as unsigned bytes
+            const uint32_t w = B.q[u][l][i] ^ 0x80808080u;  // q + 128 as unsigned bytes
 #pragma unroll
             for (int k = 0; k < 4; ++k) s[u] = fmaf(rf_ub(w, k), xe[k], s[u]);
-            if (DUAL) {
-              const uint32_t w2 = q2[u][l][i] ^ 0x80808080u;
+            if constexpr (DUAL) {
+              const uint32_t w2 = B.q2[u][l][i] ^ 0x80808080u;
 #pragma unroll
               for (int k = 0; k < 4; ++k) s2[u] = fmaf(rf_ub(w2, k), xe[k], s2[u]);
             }
@@ -181,15 +196,15 @@ __global__ __launch_bounds__(NT) void matvec_packed(PkArgs a) {
           const float xe[4] = {xv.x, xv.y, xv.z, xv.w}, xh[4] = {xw.x, xw.y, xw.z, xw.w};
 #pragma unroll
           for (int u = 0; u < U; ++u) {
-            const uint32_t lo = rf_opaque(q[u][l][i] & 0x0F0F0F0Fu), hi = rf_opaque((q[u][l][i] >> 4) & 0x0F0F0F0Fu);
+            const uint32_t lo = rf_opaque(B.q[u][l][i] & 0x0F0F0F0Fu), hi = rf_opaque((B.q[u][l][i] >> 4) & 0x0F0F0F0Fu);
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
               s[u] = fmaf(rf_ub(lo, k), xe[k], s[u]);
               s[u] = fmaf(rf_ub(hi, k), xh[k], s[u]);
             }
-            if (DUAL) {
-              const uint32_t lo2 = rf_opaque(q2[u][l][i] & 0x0F0F0F0Fu),
-                             hi2 = rf_opaque((q2[u][l][i] >> 4) & 0x0F0F0F0Fu);
+            if constexpr (DUAL) {
+              const uint32_t lo2 = rf_opaque(B.q2[u][l][i] & 0x0F0F0F0Fu),
+                             hi2 = rf_opaque((B.q2[u][l][i] >> 4) & 0x0F0F0F0Fu);
 #pragma unroll
               for (int k = 0; k < 4; ++k) {
                 s2[u] = fmaf(rf_ub(lo2, k), xe[k], s2[u]);
@@ -204,8 +219,8 @@ __global__ __launch_bounds__(NT) void matvec_packed(PkArgs a) {
       constexpr float bias = T == T_Q8_0 ? -128.f : -8.f;
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        acc[u] = fmaf(rf_half_to_float(sc[u][l]), fmaf(bias, xs, s[u]), acc[u]);
-        if (DUAL) acc2[u] = fmaf(rf_half_to_float(sc2[u][l]), fmaf(bias, xs, s2[u]), acc2[u]);
+        acc[u] = fmaf(rf_half_to_float(B.s[u][l]), fmaf(bias, xs, s[u]), acc[u]);
+        if constexpr (DUAL) acc2[u] = fmaf(rf_half_to_float(B.s2[u][l]), fmaf(bias, xs, s2[u]), acc2[u]);
       }
     }
     if (ss + 1u == nstep) {  // the task's rows are complete
@@ -233,21 +248,18 @@ __global__ __launch_bounds__(NT) void matvec_packed(PkArgs a) {
       }
     }
   };
-  auto advance = [&](uint32_t& tt, uint32_t& ss) {
-    if (++ss == nstep) { ss = 0; tt += gstride; }
-  };
-  while (t < ntask) {
-    uint32_t t1 = t, s1 = st;
-    advance(t1, s1);
-    if (t1 < ntask) fetch(qb, sb, q2b, s2b, t1, s1);
-    consume(qa, sa, q2a, s2a, t, st);
-    if (t1 >= ntask) break;
-    uint32_t t2 = t1, s2 = s1;
-    advance(t2, s2);
-    if (t2 < ntask) fetch(qa, sa, q2a, s2a, t2, s2);
-    consume(qb, sb, q2b, s2b, t1, s1);
-    t = t2;
-    st = s2;
+  // Buffer b holds step k with k % NB == b: the step NB - 1 ahead goes into
+  // the buffer freed by the previous step.
+  while (ct < ntask) {
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      if (ct < ntask) {
+        if (ft < ntask) fetch(buf[(b + NB - 1) % NB], ft, fs);
+        advance(ft, fs);
+        consume(buf[b], ct, cs);
+        advance(ct, cs);
+      }
+    }
   }
 }
 
@@ -339,11 +351,11 @@ static int pk_occupancy(PkOccCache& c, const void* kern, int nt, uint32_t lds) {
   return occ;
 }
 
-template <uint32_t T, int EPI, bool NORM, int LPW, int NT>
+template <uint32_t T, int EPI, bool NORM, int LPW, int NB, int NT>
 static hipError_t launch_pk(const PkArgs& a, uint32_t lds, hipStream_t st) {
   constexpr int U = 1;
   static PkOccCache cache;
-  auto kern = matvec_packed<T, EPI, NORM, U, LPW, NT>;
+  auto kern = matvec_packed<T, EPI, NORM, U, LPW, NB, NT>;
   const int occ = pk_occupancy(cache, reinterpret_cast<const void*>(kern), NT, lds);
   if (occ < 1) return hipErrorInvalidConfiguration;
   const uint64_t tasks = (a.rows_total + U - 1) / U, nw = NT / 64;
@@ -366,12 +378,12 @@ static hipError_t launch_pk_l(const PkArgs& a, uint32_t lds, hipStream_t st) {
   while (lpw * 2 <= pref && lpw * 2 <= nchunk) lpw *= 2;
   const bool big = lds > 40960;
   switch (lpw * 2 + (big ? 1 : 0)) {
-    case 2: return launch_pk<T, EPI, NORM, 1, 512>(a, lds, st);
-    case 3: return launch_pk<T, EPI, NORM, 1, 1024>(a, lds, st);
-    case 4: return launch_pk<T, EPI, NORM, 2, 512>(a, lds, st);
-    case 5: return launch_pk<T, EPI, NORM, 2, 1024>(a, lds, st);
-    case 8: return launch_pk<T, EPI, NORM, 4, 512>(a, lds, st);
-    case 9: return launch_pk<T, EPI, NORM, 4, 1024>(a, lds, st);
+    case 2: return launch_pk<T, EPI, NORM, 1, 2, 512>(a, lds, st);
+    case 3: return launch_pk<T, EPI, NORM, 1, 2, 1024>(a, lds, st);
+    case 4: return launch_pk<T, EPI, NORM, 2, 2, 512>(a, lds, st);
+    case 5: return launch_pk<T, EPI, NORM, 2, 2, 1024>(a, lds, st);
+    case 8: return launch_pk<T, EPI, NORM, 4, 2, 512>(a, lds, st);
+    case 9: return launch_pk<T, EPI, NORM, 4, 2, 1024>(a, lds, st);
     default: return hipErrorInvalidValue;
   }
 }

@@ -85,11 +85,12 @@ struct rf_model {
   int32_t* d_pos = nullptr;
   uint32_t* d_token = nullptr;
   uint32_t* d_ring = nullptr;  // token chosen for position p is stored at ring[p]
-  uint32_t nsplit = 1;
+  uint32_t nsplit = 1;  // attention chunks per KV head past ATT_SINGLE_CHUNK positions
   uint64_t seq_len = 0;
   bool use_graph = false;
-  hipGraph_t graph = nullptr;
-  hipGraphExec_t graph_exec = nullptr;
+  // one decode-step graph per attention regime: [0] single chunk, [1] nsplit chunks + merge
+  hipGraph_t graph[2] = {nullptr, nullptr};
+  hipGraphExec_t graph_exec[2] = {nullptr, nullptr};
   std::vector<std::string> charges;
   // Layer streaming: every block tensor lives in pinned host memory and is
   // uploaded on demand; an LRU cache of at most cache_cap device bytes keeps
@@ -121,10 +122,12 @@ int32_t drop_tensor(rf_model* m, DevTensor& t) {
 }
 
 void reset_graph(rf_model* m) {
-  if (m->graph_exec) hipGraphExecDestroy(m->graph_exec);
-  if (m->graph) hipGraphDestroy(m->graph);
-  m->graph_exec = nullptr;
-  m->graph = nullptr;
+  for (int r = 0; r < 2; ++r) {
+    if (m->graph_exec[r]) hipGraphExecDestroy(m->graph_exec[r]);
+    if (m->graph[r]) hipGraphDestroy(m->graph[r]);
+    m->graph_exec[r] = nullptr;
+    m->graph[r] = nullptr;
+  }
 }
 
 // ------------------------------------------------------- layer streaming
@@ -691,6 +694,15 @@ int32_t enqueue_qkv(rf_model* m, size_t li) {
   return RF_OK;
 }
 
+// Attention chunks for the step at position pos.  Up to ATT_SINGLE_CHUNK
+// positions one chunk per KV head covers the context and no merge kernel runs;
+// beyond, the capacity's split count (fixed, so one graph serves the regime).
+constexpr uint64_t ATT_SINGLE_CHUNK = 64;
+uint32_t attn_nsplit_at(const rf_model* m, uint64_t pos) {
+  return (m->attn_fast && pos + 1 <= ATT_SINGLE_CHUNK) ? 1u : m->nsplit;
+}
+int attn_regime(const rf_model* m, uint64_t pos) { return attn_nsplit_at(m, pos) == m->nsplit ? 1 : 0; }
+
 // 2. RoPE + attention + K/V cache write.
 int32_t enqueue_attention(rf_model* m, size_t li) {
   const rf_model_config& c = m->cfg;
@@ -702,7 +714,7 @@ int32_t enqueue_attention(rf_model* m, size_t li) {
   a.q = m->q; a.k_hist = kc; a.v_hist = vc; a.k_cur = m->k; a.v_cur = m->v; a.out = m->attn_out;
   a.ws = m->attn_ws; a.rope = m->rope; a.k_store = kc; a.v_store = vc; a.d_pos = m->d_pos;
   a.qh = (uint32_t)c.head_count; a.kvh = (uint32_t)c.head_count_kv; a.hd = (uint32_t)hd;
-  a.nsplit = m->nsplit;
+  a.nsplit = attn_nsplit_at(m, m->seq_len);  // the position this step processes
   a.denom = sqrtf((float)hd);
   RF_LAUNCH(m->attn_fast ? launch_attention(a, st) : launch_attention_naive(a, st), "attention");
   return RF_OK;
@@ -1049,20 +1061,22 @@ int32_t rf_model_decode_steps(rf_model* m, uint64_t steps) {
   int32_t rc = check_ready(m);
   if (rc) return rc;
   hipStream_t st = m->ctx->compute;
-  if (m->use_graph && !m->graph_exec) {
-    RF_LAUNCH(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal), "begin capture");
-    rc = enqueue_decode_step(m);
-    hipGraph_t g = nullptr;
-    hipError_t e = hipStreamEndCapture(st, &g);
-    if (rc) { if (g) hipGraphDestroy(g); return rc; }
-    if (e != hipSuccess) return hip_error(e, "end capture");
-    m->graph = g;
-    e = hipGraphInstantiate(&m->graph_exec, g, nullptr, nullptr, 0);
-    if (e != hipSuccess) { reset_graph(m); return hip_error(e, "graph instantiate"); }
-  }
   for (uint64_t s = 0; s < steps; ++s) {
-    if (m->graph_exec) {
-      RF_LAUNCH(hipGraphLaunch(m->graph_exec, st), "graph launch");
+    const int r = attn_regime(m, m->seq_len);
+    if (m->use_graph && !m->graph_exec[r]) {
+      // captured at the first step of its regime; replays read the position from d_pos
+      RF_LAUNCH(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal), "begin capture");
+      rc = enqueue_decode_step(m);
+      hipGraph_t g = nullptr;
+      hipError_t e = hipStreamEndCapture(st, &g);
+      if (rc) { if (g) hipGraphDestroy(g); return rc; }
+      if (e != hipSuccess) return hip_error(e, "end capture");
+      m->graph[r] = g;
+      e = hipGraphInstantiate(&m->graph_exec[r], g, nullptr, nullptr, 0);
+      if (e != hipSuccess) { reset_graph(m); return hip_error(e, "graph instantiate"); }
+    }
+    if (m->use_graph) {
+      RF_LAUNCH(hipGraphLaunch(m->graph_exec[r], st), "graph launch");
     } else {
       rc = enqueue_decode_step(m);
       if (rc) return rc;

@@ -148,6 +148,39 @@ def test_device_decode_steps_graph_replay_matches_eager(ctx):
     gm.close()
 
 
+REGIME_CFG = dict(TINY, context_length=256, embedding_length=256, feed_forward_length=512, head_dim=64)
+
+
+def test_decode_graphs_cross_the_attention_regimes(ctx, orc):
+    """Decode from position 5 to 154 with graph replay: positions up to 63 run
+    the single-chunk attention graph, later ones the split + merge graph (both
+    captured lazily).  Tokens equal the eager loop's and the oracle's."""
+    rng = np.random.default_rng(961)
+    T = _tiny_tensors(rng, REGIME_CFG, ALL_Q8)
+    prompt = [3, 1, 4, 1, 5]
+    gm = _load_gpu(ctx, REGIME_CFG, T, 160)
+    om = orc.Model(REGIME_CFG, T, kv_capacity=160, threads=4)
+    try:
+        ref = gm.generate(prompt, 150)
+        oref, margin = om.generate(prompt, 150)
+        first = next((i for i, (a, b) in enumerate(zip(ref, oref)) if a != b), None)
+        assert ref == oref, f"eager vs oracle: first divergence at {first}, margin {margin[first]:.3g}"
+        gm.reset()
+        for p, t in enumerate(prompt):
+            gm.forward(t, p)
+        gm.use_graph(True)
+        got = []
+        for n in (30, 40, 80):  # 5..34, 35..74 (crosses 64), 75..154
+            gm.decode_steps(n)
+            got += gm.read_tokens(n)
+            ctx.synchronize()
+        assert got == ref[:150]
+        gm.use_graph(False)
+    finally:
+        om.close()
+        gm.close()
+
+
 def test_config4_greedy_tokens_identical(ctx, orc):
     """random-init llama, 16 layers, d 2048, 32/8 heads,
     FFN 8192, vocab 32000, Q8_0 everywhere; 32-token random prompt, 128 greedy
