@@ -150,7 +150,7 @@ int32_t rf_matvec(rf_ctx *ctx, uint32_t ggml_type, const void *w, uint64_t w_byt
  * packed kernel covers the shape (Q8_0/Q4_0, in_dim % 32 == 0, and the row's
  * x staged in one workgroup's LDS: about 4 bytes per element of in_dim, up to
  * the current device's limit, 160 KiB on gfx950, so in_dim <= 37888 for Q8_0
- * and <= 36864 for Q4_0 there, 15360 / 14336 on a 64 KiB device). */
+ * and <= 36864 for Q4_0 there, 14336 for both on a 64 KiB device). */
 int32_t rf_packed_supported(uint32_t ggml_type, uint64_t in_dim);
 int32_t rf_pack_weights(rf_ctx *ctx, uint32_t ggml_type, const void *raw, uint64_t raw_bytes, uint64_t rows,
                         uint64_t in_dim, void *packed, uint64_t packed_bytes, rf_stream_t stream);

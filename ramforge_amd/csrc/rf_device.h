@@ -30,6 +30,15 @@ __device__ __forceinline__ float rf_half_to_float(uint32_t h) {
   return __uint_as_float(sign | (e32 << 23) | (frac << 13));
 }
 
+// rf_half_to_float through the hardware conversion: the same value for every
+// non-NaN input (a subnormal converts exactly to f * 2^-24 and is halved; a
+// NaN keeps its payload but comes back quiet).  For hot loops that decode a
+// block scale per lane.
+__device__ __forceinline__ float rf_half_to_float_fast(uint32_t h) {
+  const float f = (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+  return (h & 0x7C00u) ? f : f * 0.5f;
+}
+
 __device__ __forceinline__ float rf_bf16_to_float(uint32_t h) { return __uint_as_float(h << 16); }
 
 // Unaligned little-endian loads from a byte pointer (any alignment), byte-wise.

@@ -33,6 +33,16 @@ namespace rf {
 
 typedef uint32_t nv_u32x4 __attribute__((ext_vector_type(4)));
 
+// Tasks (row groups) per wavefront whose residual is staged in LDS.
+constexpr uint32_t PK_RES_SLOTS = 8;
+// Word 3 of a raw (untyped, stride 0) buffer resource on gfx9-family parts,
+// and the cache-policy operand of a streaming (nt) load.
+constexpr int PK_RSRC_WORD3 = 0x00020000;
+constexpr int PK_AUX_NT = 2;
+// Upper bound of the kernel's static LDS (norm partials and staged
+// residuals: 16 + 16 * PK_RES_SLOTS floats at 1024 threads).
+constexpr uint64_t PK_STATIC_LDS = 1024;
+
 template <uint32_t T> struct Pk;
 template <> struct Pk<T_Q8_0> {
   static constexpr uint32_t CB = 32;   // code bytes per 32 elements
@@ -62,7 +72,12 @@ __global__ __launch_bounds__(NT) void matvec_packed(PkArgs a) {
   constexpr uint32_t EPL = Pk<T>::EPL, EPB = 32u / Pk<T>::CB, NW = NT / 64;
   extern __shared__ __align__(16) float xl[];  // [nchunk * 64 * EPL] x, then [nchunk * 64 * EPL / 16] unit sums
   __shared__ float wsum[NW];
-  const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+  __shared__ float resl[EPI == EPI_RESIDUAL ? NW : 1][PK_RES_SLOTS][U];
+  static_assert(sizeof(wsum) + sizeof(resl) <= PK_STATIC_LDS, "static LDS above the planner's reservation");
+  // The wavefront index through readfirstlane: rows, segments and their
+  // pointers are then scalar values, so no vector load (whose wait would also
+  // wait for the codes in flight) is spent on them.
+  const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const uint32_t in = a.in_dim, nb = in / 32u, crb = in / EPB;
   const uint32_t nchunk = (crb + 1023u) / 1024u, nstep = (nchunk + LPW - 1) / LPW;
   float* xsum_l = xl + nchunk * 64u * EPL;
@@ -77,21 +92,35 @@ __global__ __launch_bounds__(NT) void matvec_packed(PkArgs a) {
 
   typedef PkStep<U, LPW, DUAL> Step;
   Step buf[NB];
+  // Codes and scales through raw buffer loads: one resource per row (scalar
+  // base, range = the row's bytes), the lane's byte offset in a VGPR.  Offsets
+  // past the row (the tail of a partial chunk) and every load of a fetch past
+  // the last task (range 0) return zeros without touching memory, so fetches
+  // are issued unconditionally and the compiler's wait counts stay exact: a
+  // consume waits for its own step only, never for the prefetch behind it.
   auto fetch = [&](Step& B, uint32_t t, uint32_t st) {
+    const bool live = t < ntask;  // wave-uniform
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const uint32_t v = min(t * U + u, a.rows_total - 1u);
       const PkSeg g = seg_of(v);
       const uint32_t r = v - g.row_begin;
+      const int32_t nc = live ? (int32_t)crb : 0, ns2 = live ? (int32_t)(nb * 2u) : 0;
+      const auto rc = __builtin_amdgcn_make_buffer_rsrc((void*)(g.codes + (size_t)r * crb), 0, nc, PK_RSRC_WORD3);
+      const auto rs = __builtin_amdgcn_make_buffer_rsrc((void*)(g.scales + (size_t)r * nb), 0, ns2, PK_RSRC_WORD3);
+      __amdgpu_buffer_rsrc_t rc2, rs2;
+      if constexpr (DUAL) {
+        rc2 = __builtin_amdgcn_make_buffer_rsrc((void*)(g.codes_up + (size_t)r * crb), 0, nc, PK_RSRC_WORD3);
+        rs2 = __builtin_amdgcn_make_buffer_rsrc((void*)(g.scales_up + (size_t)r * nb), 0, ns2, PK_RSRC_WORD3);
+      }
 #pragma unroll
       for (int l = 0; l < LPW; ++l) {
-        const uint32_t b0 = (st * LPW + l) * 1024u + 16u * lane;
-        const uint32_t b = b0 < crb ? b0 : crb - 16u;  // clamped: every load stays in bounds
-        B.q[u][l] = __builtin_nontemporal_load(reinterpret_cast<const nv_u32x4*>(g.codes + (size_t)r * crb + b));
-        B.s[u][l] = g.scales[(size_t)r * nb + b * EPB / 32u];
+        const uint32_t b = (st * LPW + l) * 1024u + 16u * lane, sb = (b * EPB / 32u) * 2u;
+        B.q[u][l] = __builtin_amdgcn_raw_buffer_load_b128(rc, b, 0, PK_AUX_NT);
+        B.s[u][l] = __builtin_amdgcn_raw_buffer_load_b16(rs, sb, 0, 0);
         if constexpr (DUAL) {
-          B.q2[u][l] = __builtin_nontemporal_load(reinterpret_cast<const nv_u32x4*>(g.codes_up + (size_t)r * crb + b));
-          B.s2[u][l] = g.scales_up[(size_t)r * nb + b * EPB / 32u];
+          B.q2[u][l] = __builtin_amdgcn_raw_buffer_load_b128(rc2, b, 0, PK_AUX_NT);
+          B.s2[u][l] = __builtin_amdgcn_raw_buffer_load_b16(rs2, sb, 0, 0);
         }
       }
     }
@@ -104,7 +133,7 @@ __global__ __launch_bounds__(NT) void matvec_packed(PkArgs a) {
   uint32_t ct = blockIdx.x * NW + wave, cs = 0, ft = ct, fs = 0;
 #pragma unroll
   for (int b = 0; b < NB - 1; ++b) {
-    if (ft < ntask) fetch(buf[b], ft, fs);
+    fetch(buf[b], ft, fs);
     advance(ft, fs);
   }
 
@@ -150,6 +179,24 @@ __global__ __launch_bounds__(NT) void matvec_packed(PkArgs a) {
       ss = rf_wave_sum(ss);
       if (lane == 0) wsum[wave] = ss;
     }
+    // EPI_RESIDUAL: the residual of every row this wavefront will finish
+    // (at most PK_RES_SLOTS tasks; the launch sizes the grid for that), so
+    // the epilogue reads LDS instead of waiting on a load queued behind codes.
+    if constexpr (EPI == EPI_RESIDUAL) {
+      for (uint32_t k = 0; k < PK_RES_SLOTS; ++k) {
+        const uint32_t t = ct + k * gstride;
+        if (t >= ntask) break;
+        if (lane < (uint32_t)U) {
+          const uint32_t vr = t * U + lane;
+          float r = 0.f;
+          if (vr < a.rows_total) {
+            const PkSeg g = seg_of(vr);
+            r = g.res[vr - g.row_begin];
+          }
+          resl[wave][k][lane] = r;
+        }
+      }
+    }
   }
   __syncthreads();
   float inv = 1.f;
@@ -163,13 +210,17 @@ __global__ __launch_bounds__(NT) void matvec_packed(PkArgs a) {
   float acc[U], acc2[U];
 #pragma unroll
   for (int u = 0; u < U; ++u) { acc[u] = 0.f; acc2[u] = 0.f; }
+  uint32_t done = 0;  // tasks this wavefront has finished
 
   auto consume = [&](const Step& B, uint32_t tt, uint32_t ss) {
 #pragma unroll
     for (int l = 0; l < LPW; ++l) {
-      const uint32_t c = ss * LPW + l;
-      if ((c * 1024u + 16u * lane) * EPB >= in) continue;
-      const float* xp = xl + c * 64u * EPL + 4u * lane;
+      // Lanes past the end of the row (a partial last chunk, or a chunk past
+      // nchunk when LPW does not divide it) decode zeros against a clamped,
+      // in-bounds slice of x and keep their sums by a select.
+      const uint32_t c = ss * LPW + l, cx = c < nchunk ? c : nchunk - 1u;
+      const bool valid = c * 1024u + 16u * lane < crb;
+      const float* xp = xl + cx * 64u * EPL + 4u * lane;
       float s[U], s2[U];
 #pragma unroll
       for (int u = 0; u < U; ++u) { s[u] = 0.f; s2[u] = 0.f; }
@@ -214,51 +265,55 @@ __global__ __launch_bounds__(NT) void matvec_packed(PkArgs a) {
           }
         }
       }
-      const float xs = UPS == 1 ? xsum_l[c * 64u + lane]
-                                : xsum_l[(c * 64u + lane) * 2u] + xsum_l[(c * 64u + lane) * 2u + 1u];
+      const float xs = UPS == 1 ? xsum_l[cx * 64u + lane]
+                                : xsum_l[(cx * 64u + lane) * 2u] + xsum_l[(cx * 64u + lane) * 2u + 1u];
       constexpr float bias = T == T_Q8_0 ? -128.f : -8.f;
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        acc[u] = fmaf(rf_half_to_float(B.s[u][l]), fmaf(bias, xs, s[u]), acc[u]);
-        if constexpr (DUAL) acc2[u] = fmaf(rf_half_to_float(B.s2[u][l]), fmaf(bias, xs, s2[u]), acc2[u]);
+        const float t = fmaf(rf_half_to_float_fast(B.s[u][l]), fmaf(bias, xs, s[u]), acc[u]);
+        acc[u] = valid ? t : acc[u];
+        if constexpr (DUAL) {
+          const float t2 = fmaf(rf_half_to_float_fast(B.s2[u][l]), fmaf(bias, xs, s2[u]), acc2[u]);
+          acc2[u] = valid ? t2 : acc2[u];
+        }
       }
     }
     if (ss + 1u == nstep) {  // the task's rows are complete
-      float v[U], v2[U];
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        v[u] = rf_wave_sum(acc[u]) * inv;
-        v2[u] = DUAL ? rf_wave_sum(acc2[u]) * inv : 0.f;
+        const float v = rf_wave_sum(acc[u]) * inv;
+        const float v2 = DUAL ? rf_wave_sum(acc2[u]) * inv : 0.f;
         acc[u] = 0.f;
         acc2[u] = 0.f;
-      }
-      if (lane < (uint32_t)U) {
-        float mine = 0.f, mine2 = 0.f;
-#pragma unroll
-        for (int u = 0; u < U; ++u)
-          if (lane == (uint32_t)u) { mine = v[u]; mine2 = v2[u]; }
-        const uint32_t vr = tt * U + lane;
-        if (vr < a.rows_total) {
+        const uint32_t vr = tt * U + u;  // wave-uniform
+        if (lane == (uint32_t)u && vr < a.rows_total) {
           const PkSeg g = seg_of(vr);
           const uint32_t o = vr - g.row_begin;
-          if (EPI == EPI_STORE) g.y[o] = mine;
-          else if (EPI == EPI_RESIDUAL) g.y[o] = g.res[o] + mine;  // add_reference (compute.rs:321-327)
-          else g.y[o] = mine / (1.0f + expf(-mine)) * mine2;  // silu_reference * up (compute.rs:337-350)
+          if (EPI == EPI_STORE) {
+            g.y[o] = v;
+          } else if (EPI == EPI_RESIDUAL) {
+            // add_reference (compute.rs:321-327); the launch keeps done < PK_RES_SLOTS
+            g.y[o] = (done < PK_RES_SLOTS ? resl[wave][done][u] : g.res[o]) + v;
+          } else {
+            g.y[o] = v / (1.0f + expf(-v)) * v2;  // silu_reference * up (compute.rs:337-350)
+          }
         }
       }
+      ++done;
     }
   };
   // Buffer b holds step k with k % NB == b: the step NB - 1 ahead goes into
   // the buffer freed by the previous step.
-  while (ct < ntask) {
+  // The only exit is the uniform check at the top of each step, so every
+  // buffer is consumed (its loads waited for) before it is refilled.
+  for (;;) {
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
-      if (ct < ntask) {
-        if (ft < ntask) fetch(buf[(b + NB - 1) % NB], ft, fs);
-        advance(ft, fs);
-        consume(buf[b], ct, cs);
-        advance(ct, cs);
-      }
+      if (ct >= ntask) return;
+      fetch(buf[(b + NB - 1) % NB], ft, fs);
+      advance(ft, fs);
+      consume(buf[b], ct, cs);
+      advance(ct, cs);
     }
   }
 }
@@ -304,10 +359,10 @@ PkPlan plan_packed(uint32_t t, uint64_t in_dim) {
   PkPlan p{};
   if (!packed_type(t) || in_dim == 0 || in_dim % 32 != 0 || in_dim > (1u << 24)) return p;
   const uint64_t nchunk = pk_nchunk(t, in_dim), epl = t == T_Q8_0 ? 16 : 32;
-  const uint64_t lds = (nchunk * 64 * epl + nchunk * 64 * (epl / 16)) * 4 + 64;  // + the static reduction slots
-  if (lds > pk_lds_limit()) return p;
+  const uint64_t lds = (nchunk * 64 * epl + nchunk * 64 * (epl / 16)) * 4;
+  if (lds + PK_STATIC_LDS > pk_lds_limit()) return p;
   p.ok = true;
-  p.lds_bytes = (uint32_t)(lds - 64);
+  p.lds_bytes = (uint32_t)lds;
   return p;
 }
 
@@ -330,16 +385,15 @@ struct PkOccCache {
   uint32_t keys[16];
   int vals[16];
   int n = 0;
-  bool attr_set = false;
+  uint32_t attr = 0;  // dynamic LDS the kernel has been opened up to (above 64 KiB)
 };
 static int pk_occupancy(PkOccCache& c, const void* kern, int nt, uint32_t lds) {
   std::lock_guard<std::mutex> lock(c.mu);
   for (int i = 0; i < c.n; ++i)
     if (c.keys[i] == lds) return c.vals[i];
-  if (lds > 65536 && !c.attr_set) {
-    if (hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)pk_lds_limit()) != hipSuccess)
-      return 0;
-    c.attr_set = true;
+  if (lds > 65536 && lds > c.attr) {
+    if (hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) return 0;
+    c.attr = lds;
   }
   int occ = 0;
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kern, nt, lds) != hipSuccess || occ < 1) occ = 1;
@@ -360,8 +414,12 @@ static hipError_t launch_pk(const PkArgs& a, uint32_t lds, hipStream_t st) {
   if (occ < 1) return hipErrorInvalidConfiguration;
   const uint64_t tasks = (a.rows_total + U - 1) / U, nw = NT / 64;
   const uint64_t want = (tasks + nw - 1) / nw, cap = (uint64_t)pk_cu_count() * occ;
-  const uint32_t grid = (uint32_t)(want < cap ? want : cap);
-  hipLaunchKernelGGL(kern, dim3(grid), dim3(NT), lds, st, a);
+  uint64_t grid = want < cap ? want : cap;
+  if (EPI == EPI_RESIDUAL) {  // at most PK_RES_SLOTS tasks per wavefront (residuals staged in LDS)
+    const uint64_t need = (tasks + nw * PK_RES_SLOTS - 1) / (nw * PK_RES_SLOTS);
+    if (grid < need) grid = need;
+  }
+  hipLaunchKernelGGL(kern, dim3((uint32_t)grid), dim3(NT), lds, st, a);
   return hipGetLastError();
 }
 
