@@ -179,10 +179,12 @@ def test_pack_weights_layout_is_exact(ctx, t):
         p.free()
 
 
-def _check_matvec_packed(ctx, orc, t, out_dim, in_dim, seed, row_start=0, row_count=None, x_off=0):
+def _check_matvec_packed(ctx, orc, t, out_dim, in_dim, seed, row_start=0, row_count=None, x_off=0, patch=None):
     rf = _rf()
     rng = np.random.default_rng(seed)
     raw = random_matrix(t, out_dim, in_dim, rng)
+    if patch is not None:
+        raw = patch(raw.copy(), rng)
     x = rng.normal(0, 1, in_dim).astype(np.float32)
     print(f"  packed matvec {NAMES[t]} out={out_dim} in={in_dim} rows={row_start}+{row_count} seed={seed} "
           f"x_off={x_off}", flush=True)
@@ -218,6 +220,25 @@ def test_matvec_packed_row_range_and_unaligned_x(ctx, orc, t):
     _check_matvec_packed(ctx, orc, t, 300, 4096, 1300 + t, row_start=128, row_count=77)
     _check_matvec_packed(ctx, orc, t, 300, 4096, 1310 + t, row_start=299)
     _check_matvec_packed(ctx, orc, t, 50, 2048, 1320 + t, x_off=4)
+
+
+@pytest.mark.parametrize("t", [Q8_0, Q4_0])
+def test_matvec_packed_subnormal_and_signed_scales(ctx, orc, t):
+    """Every block scale an f16 subnormal (the reference decodes frac * 2^-25,
+    half the IEEE value), +-0 or negative: the packed kernel's hardware f16
+    conversion plus its subnormal rule against the oracle.  With no normal
+    scale in the matrix, a scale off by 2x would show at full size."""
+    def patch(raw, rng):
+        bs = GEOM[t][1]
+        blocks = raw.reshape(-1, bs)
+        sc = rng.integers(1, 0x400, len(blocks)).astype(np.uint16)
+        sc[::3] |= 0x8000
+        sc[1::7] = 0
+        sc[2::11] = 0x8000
+        blocks[:, 0:2] = sc.view(np.uint8).reshape(-1, 2)
+        return raw
+
+    _check_matvec_packed(ctx, orc, t, 96, 3072, 1400 + t, patch=patch)
 
 
 def test_matvec_packed_validation(ctx):
