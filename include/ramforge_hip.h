@@ -138,19 +138,24 @@ int32_t rf_matvec(rf_ctx *ctx, uint32_t ggml_type, const void *w, uint64_t w_byt
                   uint64_t in_dim, const float *x, float *y, uint64_t row_start, uint64_t row_count,
                   rf_stream_t stream);
 
-/* Device-native ("packed") layout of Q8_0 and Q4_0 tensors, used by the
- * model for its weights.  No counterpart in the reference, which reads GGUF
- * blocks as stored; the arithmetic of rf_matvec_packed is that of
- * quant::matvec_q8_0 / matvec_q4_0 (quant.rs:913-1029).  Layout of a
- * [rows][in_dim] tensor, same byte count as the GGUF payload: the code bytes
- * of all rows (in_dim bytes per row for Q8_0, in_dim/2 for Q4_0, each block's
- * 16 Q4_0 bytes in GGUF order), then the f16 block scales of all rows
- * (in_dim/32 per row).  rf_pack_weights converts a GGUF payload (raw and
- * packed must not overlap); rf_packed_supported(type, in_dim) is 1 when the
- * packed kernel covers the shape (Q8_0/Q4_0, in_dim % 32 == 0, and the row's
- * x staged in one workgroup's LDS: about 4 bytes per element of in_dim, up to
- * the current device's limit, 160 KiB on gfx950, so in_dim <= 37888 for Q8_0
- * and <= 36864 for Q4_0 there, 14336 for both on a 64 KiB device). */
+/* Device-native ("packed") layout of Q8_0, Q4_0, Q4_K and Q6_K tensors, used
+ * by the model for its weights.  No counterpart in the reference, which reads
+ * GGUF blocks as stored; the arithmetic of rf_matvec_packed is that of
+ * quant::matvec_q8_0 / matvec_q4_0 / matvec_q4_k / matvec_q6_k
+ * (quant.rs:898-1327).  Layout of a [rows][in_dim] tensor, same byte count as
+ * the GGUF payload: each block is cut into byte ranges ("regions") and every
+ * region is stored for all blocks of all rows, row-major, one region after
+ * the other:
+ *   Q8_0: codes (bytes 2-33), f16 scale (0-1)
+ *   Q4_0: codes (bytes 2-17, GGUF nibble order), f16 scale (0-1)
+ *   Q4_K: qs (bytes 16-143), header d, dmin, scales[12] (0-15)
+ *   Q6_K: ql (0-127), qh (128-191), scales (192-207), d (208-209)
+ * rf_pack_weights converts a GGUF payload (raw and packed must not overlap);
+ * rf_packed_supported(type, in_dim) is 1 when the packed kernel covers the
+ * shape (in_dim a whole number of blocks, and the row's x staged in one
+ * workgroup's LDS: about 4 bytes per element of in_dim, up to the current
+ * device's limit, 160 KiB on gfx950, so in_dim <= 37888 for Q8_0 and <= 36864
+ * for the others there, 14336 for all on a 64 KiB device). */
 int32_t rf_packed_supported(uint32_t ggml_type, uint64_t in_dim);
 int32_t rf_pack_weights(rf_ctx *ctx, uint32_t ggml_type, const void *raw, uint64_t raw_bytes, uint64_t rows,
                         uint64_t in_dim, void *packed, uint64_t packed_bytes, rf_stream_t stream);

@@ -289,8 +289,10 @@ def packed_supported(ggml_type: int, in_dim: int) -> bool:
 
 def pack_weights(ctx: Context, ggml_type: int, raw, rows: int, in_dim: int, packed, raw_bytes: Optional[int] = None,
                  stream=None) -> None:
-    """GGUF Q8_0 / Q4_0 payload [rows][in_dim] -> packed layout (codes of all
-    rows, then the f16 scales of all rows; same byte count)."""
+    """GGUF Q8_0 / Q4_0 / Q4_K / Q6_K payload [rows][in_dim] -> packed layout:
+    the byte ranges of each block split into regions stored for all rows
+    (Q8_0 / Q4_0: codes, f16 scales; Q4_K: codes, 16-byte headers; Q6_K: ql,
+    qh, scales, d); same byte count."""
     rb = raw.nbytes if (raw_bytes is None and isinstance(raw, DeviceArray)) else int(raw_bytes or 0)
     pb = packed.nbytes if isinstance(packed, DeviceArray) else rb
     _lib.check(ctx.lib.rf_pack_weights(ctx.handle, ggml_type, _ptr(raw), rb, rows, in_dim, _ptr(packed), pb, stream))

@@ -56,17 +56,18 @@ hipError_t launch_matvec_segments(uint32_t t, const MvSegDesc* segs, int nseg, c
                                   const float* norm_w, float eps, uint64_t in_dim, int epi,
                                   hipStream_t st);
 
-// Matvec on the packed layout of Q8_0 / Q4_0 (rf_matvec_packed.hip): codes of
-// all rows (row-major, in or in/2 bytes per row), then the f16 block scales of
-// all rows.  Same byte count as the GGUF payload.
+// Matvec on the packed (device-native) layout of Q8_0, Q4_0, Q4_K and Q6_K
+// (rf_matvec_packed.hip): the bytes of each block are split into regions,
+// each stored for all rows, row-major: Q8_0 / Q4_0 codes, f16 scales; Q4_K
+// codes, 16-byte headers (d, dmin, 12 scale bytes); Q6_K low bits (ql), high
+// bits (qh), 16 int8 scales, f16 d.  Same byte count as the GGUF payload.
+constexpr int PK_MAX_REGIONS = 4;
 struct PkSeg {
-  const uint8_t* codes;      // first code byte of the segment's first row
-  const uint16_t* scales;    // its first scale
-  const uint8_t* codes_up;   // EPI_SWIGLU: the "up" matrix
-  const uint16_t* scales_up;
+  const uint8_t* reg[PK_MAX_REGIONS];     // each region at the segment's first row (codes first)
+  const uint8_t* reg_up[PK_MAX_REGIONS];  // EPI_SWIGLU: the "up" matrix
   float* y;
   const float* res;
-  uint32_t row_begin;        // first row of the segment among all segments
+  uint32_t row_begin;  // first row of the segment among all segments
 };
 struct PkArgs {
   PkSeg seg[3];

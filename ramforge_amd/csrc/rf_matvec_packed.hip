@@ -1,30 +1,37 @@
 // rf_matvec_packed.hip — batch-1 matvec on the device-native ("packed")
-// layout of Q8_0 and Q4_0 matrices (gfx950).
+// layout of Q8_0, Q4_0, Q4_K and Q6_K matrices (gfx950).
 //
-// Same arithmetic as quant::matvec_q8_0 / matvec_q4_0 (core/src/quant.rs:
-// 913-1029): y[o] = sum over blocks of d_b * sum_i q_i x_i with the
-// reference's codes and f16 scales; only the memory layout differs.
+// Same arithmetic as quant::matvec_q8_0 / matvec_q4_0 / matvec_q4_k /
+// matvec_q6_k (core/src/quant.rs:898-1327): y[o] = sum over blocks of the
+// block's decoded weights times x, with the reference's codes and scales;
+// only the memory layout differs.
 //
-// Packed layout of a [rows][in] matrix (same byte count as the GGUF payload):
-//   codes : rows x CRB bytes, row-major (CRB = in for Q8_0, in/2 for Q4_0;
-//           Q4_0 keeps the GGUF nibble order of each block's 16 bytes)
-//   scales: rows x (in/32) f16 scale bits, row-major, after all codes.
-// GGUF interleaves a 2-byte scale with every 32 (Q8_0) or 16 (Q4_0) code
-// bytes, so its blocks are never 16-byte aligned.  Split apart, the code
-// bytes of a row are one aligned stream that a wavefront reads with 16-byte
-// loads straight into registers.
+// Packed layout of a [rows][in] matrix: the bytes of every block are split
+// into regions, each stored for all rows, row-major (same byte count as the
+// GGUF payload):
+//   Q8_0 / Q4_0: codes (32 / 16 bytes per block; Q4_0 keeps the GGUF nibble
+//                order), f16 scales (2 bytes per block)
+//   Q4_K:        codes (qs, 128 bytes per block), header (d, dmin, the 12
+//                6-bit scale/min bytes: 16 bytes per block)
+//   Q6_K:        ql (128), qh (64), int8 scales (16), f16 d (2 per block)
+// GGUF interleaves these, so its blocks are never 16-byte aligned.  Split
+// apart, the code bytes of a row are one aligned stream that a wavefront reads
+// with 16-byte loads straight into registers.
 //
 // Work decomposition: lane l of a wavefront owns bytes [1024c + 16l, +16) of
-// "chunk" c of a row (16 Q8_0 codes or 32 Q4_0 codes); one 16-byte load per
-// lane moves 1 KiB per instruction.  x (times the norm weights when the
-// RMSNorm prologue is fused) and the sums of its 16-element units are staged
-// in LDS once per workgroup, so no register holds x between steps.  A wavefront
-// owns U whole rows (every chunk), so no partial sum crosses wavefronts and
-// the main loop has no barrier; a step is U rows x LPW chunks and the next
-// step's codes are requested before the current one is decoded (two register
-// buffers).  Row sums are DPP row reductions plus readlane.  Fusions as in
-// rf_matvec.hip: RMSNorm prologue, residual or SiLU(gate)*up epilogue, up to
-// three output segments.
+// "chunk" c of a row's codes (16 Q8_0 codes, or 32 codes of the 4-/6-bit
+// formats); one 16-byte load per lane moves 1 KiB per instruction.  The 16
+// or 32 weights of a lane meet one or two 16-element "units" of x: Q4_0's low
+// nibbles are elements j, its high nibbles j + 16; Q4_K's are 32 apart (two
+// sub-blocks of a 64-element group); Q6_K's 64 apart.  x (times the norm
+// weights when the RMSNorm prologue is fused) and the sum of every unit are
+// staged in LDS once per workgroup, so no register holds x between steps.  A
+// wavefront owns U whole rows (every chunk), so no partial sum crosses
+// wavefronts and the main loop has no barrier; a step is U rows x LPW chunks
+// and the next step's codes are requested before the current one is decoded
+// (NB register buffers).  Row sums are DPP row reductions plus readlane.
+// Fusions as in rf_matvec.hip: RMSNorm prologue, residual or SiLU(gate)*up
+// epilogue, up to three output segments.
 #include "rf_kernels.h"
 
 #include <mutex>
@@ -43,34 +50,195 @@ constexpr int PK_AUX_NT = 2;
 // residuals: 16 + 16 * PK_RES_SLOTS floats at 1024 threads).
 constexpr uint64_t PK_STATIC_LDS = 1024;
 
-template <uint32_t T> struct Pk;
-template <> struct Pk<T_Q8_0> {
-  static constexpr uint32_t CB = 32;   // code bytes per 32 elements
-  static constexpr uint32_t EPL = 16;  // elements per 16-byte lane load
-};
-template <> struct Pk<T_Q4_0> {
-  static constexpr uint32_t CB = 16;
-  static constexpr uint32_t EPL = 32;
+typedef __amdgpu_buffer_rsrc_t PkRsrc;
+
+// ---------------------------------------------------------------- formats
+//
+// PkFmt<T>:
+//   QK, EPB      block elements, elements per byte of the code region
+//   NREG         regions; row_bytes(k, in) = bytes of region k per row
+//   Meta         what a lane loads besides its 16 code bytes
+//   fetch        loads of one lane at code byte b of the row
+//   unit_elem    first element of unit h of the lane whose codes start at b
+//   word         decode code word i against x words (units 0 and 1)
+//   finish       scale the unit sums into the chunk's contribution
+// Lane constants (which sub-block / half a lane's 16 bytes fall in) depend
+// only on b % 128 = 16 (lane % 8), because every chunk starts at a multiple of
+// 1024 bytes.
+
+template <uint32_t T> struct PkFmt;
+
+template <> struct PkFmt<T_Q8_0> {
+  static constexpr uint32_t QK = 32, EPB = 1, NREG = 2;
+  __host__ __device__ static uint64_t row_bytes(int k, uint64_t in) { return k == 0 ? in : in / 32 * 2; }
+  typedef uint32_t Meta;  // f16 scale bits
+  struct Lane {
+    __device__ explicit Lane(uint32_t) {}
+  };
+  __device__ static void fetch(nv_u32x4& q, Meta& m, const PkRsrc* r, uint32_t b) {
+    q = __builtin_amdgcn_raw_buffer_load_b128(r[0], b, 0, PK_AUX_NT);
+    m = __builtin_amdgcn_raw_buffer_load_b16(r[1], (b >> 5) << 1, 0, 0);  // block b/32, 2 bytes each
+  }
+  __device__ static uint32_t unit_elem(uint32_t b, uint32_t) { return b; }
+  // q + 128 as unsigned bytes (XOR 0x80); the 128 * sum(x) is taken off in finish
+  __device__ static void word(const Lane&, uint32_t q, const Meta&, int, const float4& xv, const float4&,
+                              float& s0, float&) {
+    const uint32_t w = q ^ 0x80808080u;
+    s0 = fmaf(rf_ub(w, 0), xv.x, s0); s0 = fmaf(rf_ub(w, 1), xv.y, s0);
+    s0 = fmaf(rf_ub(w, 2), xv.z, s0); s0 = fmaf(rf_ub(w, 3), xv.w, s0);
+  }
+  __device__ static float finish(const Lane&, const Meta& m, float s0, float, float xs0, float) {
+    return rf_half_to_float_fast(m) * fmaf(-128.f, xs0, s0);
+  }
 };
 
-// The workgroup stages x while its first step's codes are in flight.  x sits
-// in LDS permuted so that the 16-byte reads of a step are consecutive across
-// lanes (no bank conflicts): element 4i + k of lane l's slice of chunk c (EPL
-// elements per slice) is stored at c * 64 * EPL + 256 i + 4 l + k.
-// Codes and scales of one step: U rows x LPW chunks (twice with the "up" matrix).
-template <int U, int LPW, bool DUAL>
+template <> struct PkFmt<T_Q4_0> {
+  static constexpr uint32_t QK = 32, EPB = 2, NREG = 2;
+  __host__ __device__ static uint64_t row_bytes(int k, uint64_t in) { return k == 0 ? in / 2 : in / 32 * 2; }
+  typedef uint32_t Meta;
+  struct Lane {
+    __device__ explicit Lane(uint32_t) {}
+  };
+  __device__ static void fetch(nv_u32x4& q, Meta& m, const PkRsrc* r, uint32_t b) {
+    q = __builtin_amdgcn_raw_buffer_load_b128(r[0], b, 0, PK_AUX_NT);
+    m = __builtin_amdgcn_raw_buffer_load_b16(r[1], (b >> 4) << 1, 0, 0);  // block b/16
+  }
+  // byte j: low nibble -> element j, high nibble -> element j + 16 (quant.rs:84-113)
+  __device__ static uint32_t unit_elem(uint32_t b, uint32_t h) { return 2u * b + 16u * h; }
+  __device__ static void word(const Lane&, uint32_t q, const Meta&, int, const float4& xv, const float4& xw,
+                              float& s0, float& s1) {
+    const uint32_t lo = rf_opaque(q & 0x0F0F0F0Fu), hi = rf_opaque((q >> 4) & 0x0F0F0F0Fu);
+    s0 = fmaf(rf_ub(lo, 0), xv.x, s0); s0 = fmaf(rf_ub(lo, 1), xv.y, s0);
+    s0 = fmaf(rf_ub(lo, 2), xv.z, s0); s0 = fmaf(rf_ub(lo, 3), xv.w, s0);
+    s1 = fmaf(rf_ub(hi, 0), xw.x, s1); s1 = fmaf(rf_ub(hi, 1), xw.y, s1);
+    s1 = fmaf(rf_ub(hi, 2), xw.z, s1); s1 = fmaf(rf_ub(hi, 3), xw.w, s1);
+  }
+  __device__ static float finish(const Lane&, const Meta& m, float s0, float s1, float xs0, float xs1) {
+    return rf_half_to_float_fast(m) * fmaf(-8.f, xs0 + xs1, s0 + s1);
+  }
+};
+
+// Q4_K (quant.rs:186-255): a 256-element block is 4 groups of 64; byte l of
+// group g holds element 64g + l (low nibble, sub-block 2g) and 64g + 32 + l
+// (high nibble, sub-block 2g + 1).  A lane's 16 bytes are half hh of group g
+// (g = (lane % 8) / 2, hh = lane % 2).  Sub-block j has 6-bit scale and min
+// per get_scale_min (quant.rs:216-226); value d*sc*q - dmin*m.
+template <> struct PkFmt<T_Q4_K> {
+  static constexpr uint32_t QK = 256, EPB = 2, NREG = 2;
+  __host__ __device__ static uint64_t row_bytes(int k, uint64_t in) { return k == 0 ? in / 2 : in / 256 * 16; }
+  typedef nv_u32x4 Meta;  // d | dmin << 16, then scale bytes 0-3, 4-7, 8-11
+  struct Lane {
+    uint32_t sh;  // bit offset of sub-block 2g's byte in its scale word
+    bool hi;      // g >= 2: the 4+2-bit form
+    __device__ explicit Lane(uint32_t lane) {
+      const uint32_t g = (lane & 7u) >> 1;
+      sh = 16u * (g & 1u);
+      hi = g >= 2u;
+    }
+  };
+  __device__ static void fetch(nv_u32x4& q, Meta& m, const PkRsrc* r, uint32_t b) {
+    q = __builtin_amdgcn_raw_buffer_load_b128(r[0], b, 0, PK_AUX_NT);
+    m = __builtin_amdgcn_raw_buffer_load_b128(r[1], (b >> 7) << 4, 0, 0);
+  }
+  __device__ static uint32_t unit_elem(uint32_t b, uint32_t h) {
+    const uint32_t o = b & 127u;
+    return (b >> 7) * 256u + 64u * (o >> 5) + 16u * ((o >> 4) & 1u) + 32u * h;
+  }
+  __device__ static void word(const Lane& L, uint32_t q, const Meta& m, int i, const float4& xv, const float4& xw,
+                              float& s0, float& s1) {
+    PkFmt<T_Q4_0>::word(PkFmt<T_Q4_0>::Lane(0), q, 0u, i, xv, xw, s0, s1);
+  }
+  __device__ static float finish(const Lane& L, const Meta& m, float s0, float s1, float xs0, float xs1) {
+    // sub-blocks j = 2g (+0) and 2g + 1 (+8 bits): for j < 4 sc = S[j] & 63,
+    // m = S[j+4] & 63; else sc = (S[j+4] & 15) | (S[j-4] >> 6) << 4,
+    // m = (S[j+4] >> 4) | (S[j] >> 6) << 4  (S = the 12 scale bytes)
+    uint32_t sc[2], mn[2];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const uint32_t s = L.sh + 8u * k;
+      const uint32_t a = (m.y >> s) & 0xFFu, c = (m.z >> s) & 0xFFu, e = (m.w >> s) & 0xFFu;
+      sc[k] = L.hi ? ((e & 15u) | ((a >> 6) << 4)) : (a & 63u);
+      mn[k] = L.hi ? ((e >> 4) | ((c >> 6) << 4)) : (c & 63u);
+    }
+    const float d = rf_half_to_float_fast(m.x & 0xFFFFu), dmin = rf_half_to_float_fast(m.x >> 16);
+    const float r0 = fmaf(d * (float)sc[0], s0, -(dmin * (float)mn[0]) * xs0);
+    return fmaf(d * (float)sc[1], s1, fmaf(-(dmin * (float)mn[1]), xs1, r0));
+  }
+};
+
+// Q6_K (quant.rs:347-407): per 128-element half hf, byte r < 64 of ql holds
+// element 128hf + r (low nibble) and 128hf + 64 + r (high nibble); their two
+// high bits are bits 2k and 2k + 4 of qh[32hf + r % 32], k = r / 32; scales
+// sc[8hf + 2k + (r % 32) / 16] and the same + 4; value d*sc*(q - 32).  A
+// lane's 16 bytes sit at r = 16 (lane % 4) of half hf = (lane % 8) / 4.
+template <> struct PkFmt<T_Q6_K> {
+  static constexpr uint32_t QK = 256, EPB = 2, NREG = 4;
+  __host__ __device__ static uint64_t row_bytes(int k, uint64_t in) {
+    return k == 0 ? in / 2 : k == 1 ? in / 4 : k == 2 ? in / 256 * 16 : in / 256 * 2;
+  }
+  struct Meta {
+    nv_u32x4 qh, sc;
+    uint32_t d;
+  };
+  struct Lane {
+    uint32_t qsh;  // 2k: shift of the low unit's high bits
+    uint32_t bsh;  // bit offset of the low unit's scale byte in its word
+    bool hf;       // half 1: scale words 2 and 3 instead of 0 and 1
+    __device__ explicit Lane(uint32_t lane) {
+      qsh = 2u * ((lane & 3u) >> 1);
+      bsh = 8u * (qsh + (lane & 1u));
+      hf = (lane & 4u) != 0;
+    }
+  };
+  __device__ static void fetch(nv_u32x4& q, Meta& m, const PkRsrc* r, uint32_t b) {
+    const uint32_t blk = b >> 7, o = b & 127u;
+    q = __builtin_amdgcn_raw_buffer_load_b128(r[0], b, 0, PK_AUX_NT);
+    m.qh = __builtin_amdgcn_raw_buffer_load_b128(r[1], blk * 64u + 32u * (o >> 6) + (o & 31u), 0, PK_AUX_NT);
+    m.sc = __builtin_amdgcn_raw_buffer_load_b128(r[2], blk * 16u, 0, 0);
+    m.d = __builtin_amdgcn_raw_buffer_load_b16(r[3], blk * 2u, 0, 0);
+  }
+  __device__ static uint32_t unit_elem(uint32_t b, uint32_t h) {
+    const uint32_t o = b & 127u;
+    return (b >> 7) * 256u + 128u * (o >> 6) + (o & 63u) + 64u * h;
+  }
+  __device__ static void word(const Lane& L, uint32_t q, const Meta& m, int i, const float4& xv, const float4& xw,
+                              float& s0, float& s1) {
+    const uint32_t h = m.qh[i];
+    const uint32_t lo = rf_opaque((q & 0x0F0F0F0Fu) | (((h >> L.qsh) & 0x03030303u) << 4));
+    const uint32_t hi = rf_opaque(((q >> 4) & 0x0F0F0F0Fu) | (((h >> (L.qsh + 4u)) & 0x03030303u) << 4));
+    s0 = fmaf(rf_ub(lo, 0), xv.x, s0); s0 = fmaf(rf_ub(lo, 1), xv.y, s0);
+    s0 = fmaf(rf_ub(lo, 2), xv.z, s0); s0 = fmaf(rf_ub(lo, 3), xv.w, s0);
+    s1 = fmaf(rf_ub(hi, 0), xw.x, s1); s1 = fmaf(rf_ub(hi, 1), xw.y, s1);
+    s1 = fmaf(rf_ub(hi, 2), xw.z, s1); s1 = fmaf(rf_ub(hi, 3), xw.w, s1);
+  }
+  __device__ static float finish(const Lane& L, const Meta& m, float s0, float s1, float xs0, float xs1) {
+    const uint32_t w0 = L.hf ? m.sc.z : m.sc.x, w1 = L.hf ? m.sc.w : m.sc.y;
+    const float sc0 = (float)(int32_t)(int8_t)((w0 >> L.bsh) & 0xFFu);
+    const float sc1 = (float)(int32_t)(int8_t)((w1 >> L.bsh) & 0xFFu);
+    const float d = rf_half_to_float_fast(m.d);
+    return d * fmaf(sc0, fmaf(-32.f, xs0, s0), sc1 * fmaf(-32.f, xs1, s1));
+  }
+};
+
+// Codes and metadata of one step: U rows x LPW chunks (twice with the "up" matrix).
+template <uint32_t T, int U, int LPW, bool DUAL>
 struct PkStep {
   nv_u32x4 q[U][LPW], q2[DUAL ? U : 1][LPW];
-  uint32_t s[U][LPW], s2[DUAL ? U : 1][LPW];
+  typename PkFmt<T>::Meta m[U][LPW], m2[DUAL ? U : 1][LPW];
 };
 
-// NB step buffers per wavefront: NB - 1 steps are in flight while one is
-// decoded.
+// The workgroup stages x while its first steps' codes are in flight.  x sits
+// in LDS permuted so that the 16-byte reads of a step are consecutive across
+// lanes (no bank conflicts): element 4i + k of unit h of lane l's slice of
+// chunk c (EPL = 16 or 32 elements per slice) is stored at
+// c * 64 * EPL + 256 (4h + i) + 4 l + k.  NB step buffers per wavefront: NB - 1
+// steps are in flight while one is decoded.
 template <uint32_t T, int EPI, bool NORM, int U, int LPW, int NB, int NT>
 __global__ __launch_bounds__(NT) void matvec_packed(PkArgs a) {
+  typedef PkFmt<T> F;
   constexpr bool DUAL = EPI == EPI_SWIGLU;
-  constexpr uint32_t EPL = Pk<T>::EPL, EPB = 32u / Pk<T>::CB, NW = NT / 64;
-  extern __shared__ __align__(16) float xl[];  // [nchunk * 64 * EPL] x, then [nchunk * 64 * EPL / 16] unit sums
+  constexpr uint32_t EPB = F::EPB, UPS = EPB, EPL = 16u * UPS, NW = NT / 64;
+  extern __shared__ __align__(16) float xl[];  // [nchunk * 64 * EPL] x, then [nchunk * 64 * UPS] unit sums
   __shared__ float wsum[NW];
   __shared__ float resl[EPI == EPI_RESIDUAL ? NW : 1][PK_RES_SLOTS][U];
   static_assert(sizeof(wsum) + sizeof(resl) <= PK_STATIC_LDS, "static LDS above the planner's reservation");
@@ -78,9 +246,10 @@ __global__ __launch_bounds__(NT) void matvec_packed(PkArgs a) {
   // pointers are then scalar values, so no vector load (whose wait would also
   // wait for the codes in flight) is spent on them.
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const uint32_t in = a.in_dim, nb = in / 32u, crb = in / EPB;
+  const uint32_t in = a.in_dim, crb = in / EPB;
   const uint32_t nchunk = (crb + 1023u) / 1024u, nstep = (nchunk + LPW - 1) / LPW;
   float* xsum_l = xl + nchunk * 64u * EPL;
+  const typename F::Lane LC(lane);
 
   auto seg_of = [&](uint32_t v) -> PkSeg {
     return (a.nseg > 2 && v >= a.seg[2].row_begin) ? a.seg[2]
@@ -90,14 +259,14 @@ __global__ __launch_bounds__(NT) void matvec_packed(PkArgs a) {
   const uint32_t ntask = (a.rows_total + U - 1) / U;
   const uint32_t gstride = gridDim.x * NW;
 
-  typedef PkStep<U, LPW, DUAL> Step;
+  typedef PkStep<T, U, LPW, DUAL> Step;
   Step buf[NB];
-  // Codes and scales through raw buffer loads: one resource per row (scalar
-  // base, range = the row's bytes), the lane's byte offset in a VGPR.  Offsets
-  // past the row (the tail of a partial chunk) and every load of a fetch past
-  // the last task (range 0) return zeros without touching memory, so fetches
-  // are issued unconditionally and the compiler's wait counts stay exact: a
-  // consume waits for its own step only, never for the prefetch behind it.
+  // Raw buffer loads: one resource per row and region (scalar base, range =
+  // the row's bytes), the lane's byte offset in a VGPR.  Offsets past the row
+  // (the tail of a partial chunk) and every load of a fetch past the last task
+  // (range 0) return zeros without touching memory, so fetches are issued
+  // unconditionally and the compiler's wait counts stay exact: a consume waits
+  // for its own step only, never for the prefetch behind it.
   auto fetch = [&](Step& B, uint32_t t, uint32_t st) {
     const bool live = t < ntask;  // wave-uniform
 #pragma unroll
@@ -105,23 +274,20 @@ __global__ __launch_bounds__(NT) void matvec_packed(PkArgs a) {
       const uint32_t v = min(t * U + u, a.rows_total - 1u);
       const PkSeg g = seg_of(v);
       const uint32_t r = v - g.row_begin;
-      const int32_t nc = live ? (int32_t)crb : 0, ns2 = live ? (int32_t)(nb * 2u) : 0;
-      const auto rc = __builtin_amdgcn_make_buffer_rsrc((void*)(g.codes + (size_t)r * crb), 0, nc, PK_RSRC_WORD3);
-      const auto rs = __builtin_amdgcn_make_buffer_rsrc((void*)(g.scales + (size_t)r * nb), 0, ns2, PK_RSRC_WORD3);
-      __amdgpu_buffer_rsrc_t rc2, rs2;
-      if constexpr (DUAL) {
-        rc2 = __builtin_amdgcn_make_buffer_rsrc((void*)(g.codes_up + (size_t)r * crb), 0, nc, PK_RSRC_WORD3);
-        rs2 = __builtin_amdgcn_make_buffer_rsrc((void*)(g.scales_up + (size_t)r * nb), 0, ns2, PK_RSRC_WORD3);
+      PkRsrc rr[F::NREG], rr2[F::NREG];
+#pragma unroll
+      for (int k = 0; k < (int)F::NREG; ++k) {
+        const uint32_t rb = (uint32_t)F::row_bytes(k, in);
+        const int32_t n = live ? (int32_t)rb : 0;
+        rr[k] = __builtin_amdgcn_make_buffer_rsrc((void*)(g.reg[k] + (size_t)r * rb), 0, n, PK_RSRC_WORD3);
+        if constexpr (DUAL)
+          rr2[k] = __builtin_amdgcn_make_buffer_rsrc((void*)(g.reg_up[k] + (size_t)r * rb), 0, n, PK_RSRC_WORD3);
       }
 #pragma unroll
       for (int l = 0; l < LPW; ++l) {
-        const uint32_t b = (st * LPW + l) * 1024u + 16u * lane, sb = (b * EPB / 32u) * 2u;
-        B.q[u][l] = __builtin_amdgcn_raw_buffer_load_b128(rc, b, 0, PK_AUX_NT);
-        B.s[u][l] = __builtin_amdgcn_raw_buffer_load_b16(rs, sb, 0, 0);
-        if constexpr (DUAL) {
-          B.q2[u][l] = __builtin_amdgcn_raw_buffer_load_b128(rc2, b, 0, PK_AUX_NT);
-          B.s2[u][l] = __builtin_amdgcn_raw_buffer_load_b16(rs2, sb, 0, 0);
-        }
+        const uint32_t b = (st * LPW + l) * 1024u + 16u * lane;
+        F::fetch(B.q[u][l], B.m[u][l], rr, b);
+        if constexpr (DUAL) F::fetch(B.q2[u][l], B.m2[u][l], rr2, b);
       }
     }
   };
@@ -138,13 +304,12 @@ __global__ __launch_bounds__(NT) void matvec_packed(PkArgs a) {
   }
 
   // Prologue, one round of loads and one barrier.  Thread j (then j + NT, ...)
-  // owns unit j: 16 consecutive elements, one lane slice of a Q8_0 chunk or
-  // half of a Q4_0 one.  It writes the unit into LDS and the unit's sum.
-  // With NORM, rms_norm_reference (core/src/compute.rs:291-319) is
+  // owns unit j: 16 consecutive elements of x, unit j % UPS of lane slice
+  // j / UPS.  It writes the unit into LDS and the unit's sum.  With NORM,
+  // rms_norm_reference (core/src/compute.rs:291-319) is
   // x / sqrt(mean(x^2) + eps) * w; LDS holds x * w and every row sum is
   // scaled by 1 / sqrt(mean(x^2) + eps) in the epilogue (the same value up to
   // rounding), so the mean's reduction shares the prologue's barrier.
-  constexpr uint32_t UPS = EPL / 16u;  // units per lane slice
   const uint32_t nunit = nchunk * 64u * UPS;
   {
     const float4* x4 = reinterpret_cast<const float4*>(a.x);
@@ -152,9 +317,10 @@ __global__ __launch_bounds__(NT) void matvec_packed(PkArgs a) {
     float ss = 0.f;
     for (uint32_t j = tid; j < nunit; j += NT) {
       const uint32_t js = j / UPS, h = j % UPS;
-      const uint32_t e = ((js >> 6) * 1024u + 16u * (js & 63u)) * EPB + 16u * h;
+      const uint32_t b = (js >> 6) * 1024u + 16u * (js & 63u);
       float s = 0.f;
-      if (e < in) {
+      if (b < crb) {
+        const uint32_t e = F::unit_elem(b, h);
         float4 v[4], w[4];
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
@@ -221,60 +387,29 @@ __global__ __launch_bounds__(NT) void matvec_packed(PkArgs a) {
       const uint32_t c = ss * LPW + l, cx = c < nchunk ? c : nchunk - 1u;
       const bool valid = c * 1024u + 16u * lane < crb;
       const float* xp = xl + cx * 64u * EPL + 4u * lane;
-      float s[U], s2[U];
+      float s0[U], s1[U], t0[U], t1[U];
 #pragma unroll
-      for (int u = 0; u < U; ++u) { s[u] = 0.f; s2[u] = 0.f; }
+      for (int u = 0; u < U; ++u) { s0[u] = 0.f; s1[u] = 0.f; t0[u] = 0.f; t1[u] = 0.f; }
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        if (T == T_Q8_0) {
-          const float4 xv = *reinterpret_cast<const float4*>(xp + 256 * i);
-          const float xe[4] = {xv.x, xv.y, xv.z, xv.w};
+        const float4 xv = *reinterpret_cast<const float4*>(xp + 256 * i);
+        float4 xw = xv;
+        if (UPS == 2) xw = *reinterpret_cast<const float4*>(xp + 256 * (i + 4));
 #pragma unroll
-          for (int u = 0; u < U; ++u) {
-            const uint32_t w = B.q[u][l][i] ^ 0x80808080u;  // q + 128 as unsigned bytes
-#pragma unroll
-            for (int k = 0; k < 4; ++k) s[u] = fmaf(rf_ub(w, k), xe[k], s[u]);
-            if constexpr (DUAL) {
-              const uint32_t w2 = B.q2[u][l][i] ^ 0x80808080u;
-#pragma unroll
-              for (int k = 0; k < 4; ++k) s2[u] = fmaf(rf_ub(w2, k), xe[k], s2[u]);
-            }
-          }
-        } else {
-          // byte j: low nibble -> element j, high nibble -> element j + 16 (quant.rs:84-113)
-          const float4 xv = *reinterpret_cast<const float4*>(xp + 256 * i);
-          const float4 xw = *reinterpret_cast<const float4*>(xp + 256 * (i + 4));
-          const float xe[4] = {xv.x, xv.y, xv.z, xv.w}, xh[4] = {xw.x, xw.y, xw.z, xw.w};
-#pragma unroll
-          for (int u = 0; u < U; ++u) {
-            const uint32_t lo = rf_opaque(B.q[u][l][i] & 0x0F0F0F0Fu), hi = rf_opaque((B.q[u][l][i] >> 4) & 0x0F0F0F0Fu);
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-              s[u] = fmaf(rf_ub(lo, k), xe[k], s[u]);
-              s[u] = fmaf(rf_ub(hi, k), xh[k], s[u]);
-            }
-            if constexpr (DUAL) {
-              const uint32_t lo2 = rf_opaque(B.q2[u][l][i] & 0x0F0F0F0Fu),
-                             hi2 = rf_opaque((B.q2[u][l][i] >> 4) & 0x0F0F0F0Fu);
-#pragma unroll
-              for (int k = 0; k < 4; ++k) {
-                s2[u] = fmaf(rf_ub(lo2, k), xe[k], s2[u]);
-                s2[u] = fmaf(rf_ub(hi2, k), xh[k], s2[u]);
-              }
-            }
-          }
+        for (int u = 0; u < U; ++u) {
+          F::word(LC, B.q[u][l][i], B.m[u][l], i, xv, xw, s0[u], s1[u]);
+          if constexpr (DUAL) F::word(LC, B.q2[u][l][i], B.m2[u][l], i, xv, xw, t0[u], t1[u]);
         }
       }
-      const float xs = UPS == 1 ? xsum_l[cx * 64u + lane]
-                                : xsum_l[(cx * 64u + lane) * 2u] + xsum_l[(cx * 64u + lane) * 2u + 1u];
-      constexpr float bias = T == T_Q8_0 ? -128.f : -8.f;
+      const uint32_t ui = (cx * 64u + lane) * UPS;
+      const float xs0 = xsum_l[ui], xs1 = UPS == 2 ? xsum_l[ui + 1u] : 0.f;
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        const float t = fmaf(rf_half_to_float_fast(B.s[u][l]), fmaf(bias, xs, s[u]), acc[u]);
-        acc[u] = valid ? t : acc[u];
+        const float f = F::finish(LC, B.m[u][l], s0[u], s1[u], xs0, xs1);
+        acc[u] = valid ? acc[u] + f : acc[u];
         if constexpr (DUAL) {
-          const float t2 = fmaf(rf_half_to_float_fast(B.s2[u][l]), fmaf(bias, xs, s2[u]), acc2[u]);
-          acc2[u] = valid ? t2 : acc2[u];
+          const float f2 = F::finish(LC, B.m2[u][l], t0[u], t1[u], xs0, xs1);
+          acc2[u] = valid ? acc2[u] + f2 : acc2[u];
         }
       }
     }
@@ -303,9 +438,9 @@ __global__ __launch_bounds__(NT) void matvec_packed(PkArgs a) {
     }
   };
   // Buffer b holds step k with k % NB == b: the step NB - 1 ahead goes into
-  // the buffer freed by the previous step.
-  // The only exit is the uniform check at the top of each step, so every
-  // buffer is consumed (its loads waited for) before it is refilled.
+  // the buffer freed by the previous step.  The only exit is the uniform
+  // check at the top of each step, so every buffer is consumed (its loads
+  // waited for) before it is refilled.
   for (;;) {
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
@@ -319,23 +454,53 @@ __global__ __launch_bounds__(NT) void matvec_packed(PkArgs a) {
 }
 
 // GGUF blocks -> packed layout, one thread per block (install-time only).
+// Block i (row-major over rows and blocks) lands at i * (region bytes per
+// block) in every region.
 template <uint32_t T>
 __global__ __launch_bounds__(256) void pack_blocks(const uint8_t* __restrict__ raw, uint8_t* __restrict__ packed,
-                                                   uint64_t rows, uint32_t nb) {
-  constexpr uint32_t BS = Fmt<T>::BS, CB = Pk<T>::CB;
+                                                   uint64_t nblocks) {
   const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= rows * nb) return;
+  if (i >= nblocks) return;
+  constexpr uint32_t BS = Fmt<T>::BS;
   const uint8_t* b = raw + i * BS;
-  uint16_t* scales = reinterpret_cast<uint16_t*>(packed + rows * nb * CB);
-  scales[i] = (uint16_t)rf_ld_u16(b);
-  uint8_t* codes = packed + i * CB;  // row r, block j -> r * nb * CB + j * CB == i * CB
-#pragma unroll
-  for (uint32_t k = 0; k < CB; ++k) codes[k] = b[2 + k];
+  auto copy = [&](uint8_t* dst, const uint8_t* src, uint32_t n) {
+    for (uint32_t k = 0; k < n; ++k) dst[k] = src[k];
+  };
+  if constexpr (T == T_Q8_0 || T == T_Q4_0) {
+    constexpr uint32_t CB = BS - 2;
+    copy(packed + nblocks * CB + 2 * i, b, 2);  // f16 scale
+    copy(packed + i * CB, b + 2, CB);           // codes
+  } else if constexpr (T == T_Q4_K) {
+    copy(packed + nblocks * 128 + 16 * i, b, 16);  // d, dmin, scales[12]
+    copy(packed + i * 128, b + 16, 128);           // qs
+  } else {
+    uint8_t* qh = packed + nblocks * 128;
+    uint8_t* sc = qh + nblocks * 64;
+    uint8_t* d = sc + nblocks * 16;
+    copy(packed + i * 128, b, 128);  // ql
+    copy(qh + i * 64, b + 128, 64);
+    copy(sc + i * 16, b + 192, 16);
+    copy(d + i * 2, b + 208, 2);
+  }
 }
 
 // ------------------------------------------------------------------ host side
 
-bool packed_type(uint32_t t) { return t == T_Q8_0 || t == T_Q4_0; }
+bool packed_type(uint32_t t) { return t == T_Q8_0 || t == T_Q4_0 || t == T_Q4_K || t == T_Q6_K; }
+
+static uint32_t pk_qk(uint32_t t) { return (t == T_Q4_K || t == T_Q6_K) ? 256u : 32u; }
+static uint32_t pk_epb(uint32_t t) { return t == T_Q8_0 ? 1u : 2u; }
+
+// Region k of format t: bytes per row.
+static uint64_t pk_row_bytes(uint32_t t, int k, uint64_t in) {
+  switch (t) {
+    case T_Q8_0: return PkFmt<T_Q8_0>::row_bytes(k, in);
+    case T_Q4_0: return PkFmt<T_Q4_0>::row_bytes(k, in);
+    case T_Q4_K: return PkFmt<T_Q4_K>::row_bytes(k, in);
+    default: return PkFmt<T_Q6_K>::row_bytes(k, in);
+  }
+}
+static int pk_nreg(uint32_t t) { return t == T_Q6_K ? 4 : 2; }
 
 static uint32_t pk_lds_limit() {
   static int cached[64] = {0};
@@ -350,16 +515,13 @@ static uint32_t pk_lds_limit() {
   return (uint32_t)cached[dev];
 }
 
-static uint64_t pk_nchunk(uint32_t t, uint64_t in_dim) {
-  const uint64_t crb = in_dim * (t == T_Q8_0 ? 32u : 16u) / 32u;
-  return (crb + 1023) / 1024;
-}
+static uint64_t pk_nchunk(uint32_t t, uint64_t in_dim) { return (in_dim / pk_epb(t) + 1023) / 1024; }
 
 PkPlan plan_packed(uint32_t t, uint64_t in_dim) {
   PkPlan p{};
-  if (!packed_type(t) || in_dim == 0 || in_dim % 32 != 0 || in_dim > (1u << 24)) return p;
-  const uint64_t nchunk = pk_nchunk(t, in_dim), epl = t == T_Q8_0 ? 16 : 32;
-  const uint64_t lds = (nchunk * 64 * epl + nchunk * 64 * (epl / 16)) * 4;
+  if (!packed_type(t) || in_dim == 0 || in_dim % pk_qk(t) != 0 || in_dim > (1u << 24)) return p;
+  const uint64_t nchunk = pk_nchunk(t, in_dim), ups = pk_epb(t), epl = 16 * ups;
+  const uint64_t lds = (nchunk * 64 * epl + nchunk * 64 * ups) * 4;
   if (lds + PK_STATIC_LDS > pk_lds_limit()) return p;
   p.ok = true;
   p.lds_bytes = (uint32_t)lds;
@@ -425,13 +587,15 @@ static hipError_t launch_pk(const PkArgs& a, uint32_t lds, hipStream_t st) {
 
 // Launch shape, from timing the 8B projections (Q8_0 and Q4_0; 4096 and
 // 14336 inputs): one row per wavefront; LPW = chunks per step, up to 4 (2 for
-// gate/up, whose step loads two matrices); 1024-thread workgroups when x fills
-// more than 40 KB of LDS (two resident workgroups then still give 32
-// wavefronts per CU), else 512.
+// gate/up, whose step loads two matrices; Q6_K, with three more loads per
+// chunk, one less doubling); 1024-thread workgroups when x fills more than
+// 40 KB of LDS (two resident workgroups then still give 32 wavefronts per
+// CU), else 512.
 template <uint32_t T, int EPI, bool NORM>
 static hipError_t launch_pk_l(const PkArgs& a, uint32_t lds, hipStream_t st) {
   const uint64_t nchunk = pk_nchunk(T, a.in_dim);
-  const uint32_t pref = EPI == EPI_SWIGLU ? 2 : 4;
+  uint32_t pref = EPI == EPI_SWIGLU ? 2 : 4;
+  if (T == T_Q6_K) pref /= 2;
   uint32_t lpw = 1;
   while (lpw * 2 <= pref && lpw * 2 <= nchunk) lpw *= 2;
   const bool big = lds > 40960;
@@ -440,8 +604,12 @@ static hipError_t launch_pk_l(const PkArgs& a, uint32_t lds, hipStream_t st) {
     case 3: return launch_pk<T, EPI, NORM, 1, 2, 1024>(a, lds, st);
     case 4: return launch_pk<T, EPI, NORM, 2, 2, 512>(a, lds, st);
     case 5: return launch_pk<T, EPI, NORM, 2, 2, 1024>(a, lds, st);
-    case 8: return launch_pk<T, EPI, NORM, 4, 2, 512>(a, lds, st);
-    case 9: return launch_pk<T, EPI, NORM, 4, 2, 1024>(a, lds, st);
+    case 8:
+      if constexpr (T != T_Q6_K && EPI != EPI_SWIGLU) return launch_pk<T, EPI, NORM, 4, 2, 512>(a, lds, st);
+      return hipErrorInvalidValue;
+    case 9:
+      if constexpr (T != T_Q6_K && EPI != EPI_SWIGLU) return launch_pk<T, EPI, NORM, 4, 2, 1024>(a, lds, st);
+      return hipErrorInvalidValue;
     default: return hipErrorInvalidValue;
   }
 }
@@ -467,22 +635,25 @@ hipError_t launch_matvec_packed(uint32_t t, const PkSegDesc* segs, int nseg, con
   if (!p.ok || nseg < 1 || nseg > 3) return hipErrorInvalidValue;
   if (!al16(x) || (norm_w && !al16(norm_w))) return hipErrorInvalidValue;
   const bool dual = epi == EPI_SWIGLU;
-  const uint64_t cb = t == T_Q8_0 ? 32 : 16, crb = in_dim * cb / 32, nb = in_dim / 32;
+  const int nreg = pk_nreg(t);
   PkArgs a{};
   uint64_t total = 0;
   for (int i = 0; i < nseg; ++i) {
     const PkSegDesc& d = segs[i];
     if (d.row_start + d.rows > d.matrix_rows) return hipErrorInvalidValue;
-    const uint8_t* base = static_cast<const uint8_t*>(d.packed);
-    a.seg[i].codes = base + d.row_start * crb;
-    a.seg[i].scales = reinterpret_cast<const uint16_t*>(base + d.matrix_rows * crb) + d.row_start * nb;
-    if (dual) {
-      const uint8_t* up = static_cast<const uint8_t*>(d.packed_up);
-      if (!up) return hipErrorInvalidValue;
-      a.seg[i].codes_up = up + d.row_start * crb;
-      a.seg[i].scales_up = reinterpret_cast<const uint16_t*>(up + d.matrix_rows * crb) + d.row_start * nb;
+    if (dual && !d.packed_up) return hipErrorInvalidValue;
+    uint64_t off = 0;  // region k starts after regions 0..k-1 of all matrix rows
+    for (int k = 0; k < nreg; ++k) {
+      const uint64_t rb = pk_row_bytes(t, k, in_dim);
+      a.seg[i].reg[k] = static_cast<const uint8_t*>(d.packed) + off + d.row_start * rb;
+      if (dual) a.seg[i].reg_up[k] = static_cast<const uint8_t*>(d.packed_up) + off + d.row_start * rb;
+      off += d.matrix_rows * rb;
     }
-    if (!al16(a.seg[i].codes) || (dual && !al16(a.seg[i].codes_up))) return hipErrorInvalidValue;
+    // 16-byte loads from region 0 (and Q4_K's headers, Q6_K's qh and scales)
+    for (int k = 0; k < nreg; ++k) {
+      const bool wide = k == 0 || t == T_Q4_K || (t == T_Q6_K && k < 3);
+      if (wide && (!al16(a.seg[i].reg[k]) || (dual && !al16(a.seg[i].reg_up[k])))) return hipErrorInvalidValue;
+    }
     a.seg[i].y = d.y;
     a.seg[i].res = d.res;
     a.seg[i].row_begin = (uint32_t)total;
@@ -499,21 +670,25 @@ hipError_t launch_matvec_packed(uint32_t t, const PkSegDesc* segs, int nseg, con
   switch (t) {
     case T_Q8_0: return launch_pk_t<T_Q8_0>(a, p.lds_bytes, epi, norm_w != nullptr, st);
     case T_Q4_0: return launch_pk_t<T_Q4_0>(a, p.lds_bytes, epi, norm_w != nullptr, st);
+    case T_Q4_K: return launch_pk_t<T_Q4_K>(a, p.lds_bytes, epi, norm_w != nullptr, st);
+    case T_Q6_K: return launch_pk_t<T_Q6_K>(a, p.lds_bytes, epi, norm_w != nullptr, st);
     default: return hipErrorInvalidValue;
   }
 }
 
 hipError_t launch_pack(uint32_t t, const void* raw, void* packed, uint64_t rows, uint64_t in_dim, hipStream_t st) {
-  if (!packed_type(t) || in_dim % 32 != 0) return hipErrorInvalidValue;
-  const uint64_t nb = in_dim / 32, n = rows * nb;
+  if (!packed_type(t) || in_dim % pk_qk(t) != 0) return hipErrorInvalidValue;
+  const uint64_t n = rows * (in_dim / pk_qk(t));
   if (n == 0) return hipSuccess;
   const dim3 grid((unsigned)((n + 255) / 256));
-  if (t == T_Q8_0)
-    hipLaunchKernelGGL(pack_blocks<T_Q8_0>, grid, dim3(256), 0, st, static_cast<const uint8_t*>(raw),
-                       static_cast<uint8_t*>(packed), rows, (uint32_t)nb);
-  else
-    hipLaunchKernelGGL(pack_blocks<T_Q4_0>, grid, dim3(256), 0, st, static_cast<const uint8_t*>(raw),
-                       static_cast<uint8_t*>(packed), rows, (uint32_t)nb);
+  const uint8_t* r = static_cast<const uint8_t*>(raw);
+  uint8_t* o = static_cast<uint8_t*>(packed);
+  switch (t) {
+    case T_Q8_0: hipLaunchKernelGGL(pack_blocks<T_Q8_0>, grid, dim3(256), 0, st, r, o, n); break;
+    case T_Q4_0: hipLaunchKernelGGL(pack_blocks<T_Q4_0>, grid, dim3(256), 0, st, r, o, n); break;
+    case T_Q4_K: hipLaunchKernelGGL(pack_blocks<T_Q4_K>, grid, dim3(256), 0, st, r, o, n); break;
+    default: hipLaunchKernelGGL(pack_blocks<T_Q6_K>, grid, dim3(256), 0, st, r, o, n); break;
+  }
   return hipGetLastError();
 }
 

@@ -149,14 +149,34 @@ float host_half_to_float(uint32_t h) {
   return f;
 }
 
-// GGUF Q8_0 / Q4_0 payload -> packed layout (same rules as pack_blocks).
+// GGUF payload -> packed layout on the host (same rules as pack_blocks): the
+// bytes of block i go to offset i * (region bytes per block) of each region.
 void host_pack(uint32_t t, const uint8_t* raw, uint64_t rows, uint64_t in, uint8_t* out) {
-  const uint64_t nb = in / 32, bs = t == T_Q8_0 ? 34 : 18, cb = bs - 2;
-  uint8_t* scales = out + rows * nb * cb;
-  for (uint64_t i = 0; i < rows * nb; ++i) {
-    const uint8_t* b = raw + i * bs;
-    memcpy(scales + 2 * i, b, 2);
-    memcpy(out + i * cb, b + 2, cb);
+  if (t == T_Q8_0 || t == T_Q4_0) {
+    const uint64_t n = rows * (in / 32), bs = t == T_Q8_0 ? 34 : 18, cb = bs - 2;
+    uint8_t* scales = out + n * cb;
+    for (uint64_t i = 0; i < n; ++i) {
+      const uint8_t* b = raw + i * bs;
+      memcpy(scales + 2 * i, b, 2);
+      memcpy(out + i * cb, b + 2, cb);
+    }
+  } else if (t == T_Q4_K) {
+    const uint64_t n = rows * (in / 256);
+    for (uint64_t i = 0; i < n; ++i) {
+      const uint8_t* b = raw + i * 144;
+      memcpy(out + n * 128 + 16 * i, b, 16);  // d, dmin, scales[12]
+      memcpy(out + 128 * i, b + 16, 128);     // qs
+    }
+  } else {  // Q6_K
+    const uint64_t n = rows * (in / 256);
+    uint8_t *qh = out + n * 128, *sc = qh + n * 64, *d = sc + n * 16;
+    for (uint64_t i = 0; i < n; ++i) {
+      const uint8_t* b = raw + i * 210;
+      memcpy(out + 128 * i, b, 128);  // ql
+      memcpy(qh + 64 * i, b + 128, 64);
+      memcpy(sc + 16 * i, b + 192, 16);
+      memcpy(d + 2 * i, b + 208, 2);
+    }
   }
 }
 

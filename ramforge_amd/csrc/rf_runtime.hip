@@ -509,9 +509,12 @@ int32_t rf_pack_weights(rf_ctx* ctx, uint32_t t, const void* raw, uint64_t raw_b
     return set_error(RF_ERR_UNSUPPORTED, "packed layout does not support tensor type %s (%u)", type_name(t), t);
   const char* nm = type_name(t);
   if (!raw || !packed) return set_error(RF_ERR_INVALID, "%s pack received a null pointer", nm);
-  if (in_dim % 32 != 0)
-    return set_error(RF_ERR_INVALID, "%s in_dim %llu not divisible by 32", nm, (unsigned long long)in_dim);
-  const uint64_t need = rows * (in_dim / 32) * (t == T_Q8_0 ? 34 : 18);
+  uint64_t qk = 0, bs = 0;
+  type_geometry(t, &qk, &bs);
+  if (in_dim % qk != 0)
+    return set_error(RF_ERR_INVALID, "%s in_dim %llu not divisible by %llu", nm, (unsigned long long)in_dim,
+                     (unsigned long long)qk);
+  const uint64_t need = rows * (in_dim / qk) * bs;
   if (raw_bytes < need)
     return set_error(RF_ERR_INVALID, "%s weight truncated: expected %llu bytes, got %llu", nm,
                      (unsigned long long)need, (unsigned long long)raw_bytes);

@@ -157,19 +157,26 @@ def test_matvec_unaligned_pointers(ctx, orc, t, kernel_mode):
     _check_matvec(ctx, orc, t, 70, 512, 370 + t, x_off=8, w_off=6, row_start=5, row_count=40)
 
 
+# Byte ranges of a GGUF block that form the packed layout's regions, in region
+# order (the layout documented in include/ramforge_hip.h).
+PACK_REGIONS = {Q8_0: [(2, 34), (0, 2)], Q4_0: [(2, 18), (0, 2)], Q4_K: [(16, 144), (0, 16)],
+                Q6_K: [(0, 128), (128, 192), (192, 208), (208, 210)]}
+PACKED = [Q8_0, Q4_0, Q4_K, Q6_K]
+
+
 def _pack_host(t, raw, rows, in_dim):
-    """Packed layout built on the host from the GGUF bytes (codes of all rows,
-    then the f16 scale bits of all rows)."""
+    """Packed layout built on the host from the GGUF bytes: each region (a
+    byte range of every block) for all blocks of all rows, one after another."""
     qk, bs = GEOM[t]
-    blocks = raw.reshape(rows * in_dim // 32, bs)
-    return np.concatenate([blocks[:, 2:].reshape(-1), blocks[:, :2].reshape(-1)])
+    blocks = raw.reshape(rows * in_dim // qk, bs)
+    return np.concatenate([blocks[:, a:b].reshape(-1) for a, b in PACK_REGIONS[t]])
 
 
-@pytest.mark.parametrize("t", [Q8_0, Q4_0])
+@pytest.mark.parametrize("t", PACKED)
 def test_pack_weights_layout_is_exact(ctx, t):
     rf = _rf()
     rng = np.random.default_rng(40 + t)
-    for rows, in_dim in ((3, 32), (17, 4096), (5, 14336)):
+    for rows, in_dim in ((3, 256), (17, 4096), (5, 14336)):
         raw = random_matrix(t, rows, in_dim, rng)
         w = ctx.array(raw)
         p = ctx.empty((raw.nbytes,), np.uint8)
@@ -204,38 +211,46 @@ def _check_matvec_packed(ctx, orc, t, out_dim, in_dim, seed, row_start=0, row_co
         a.free()
 
 
-@pytest.mark.parametrize("t", [Q8_0, Q4_0])
-@pytest.mark.parametrize("out_dim,in_dim", [(1, 32), (67, 96), (130, 1024), (33, 2048), (70, 3072), (257, 4096),
-                                            (1000, 5120), (4096, 4096), (14336, 4096), (4096, 14336), (9, 16384),
-                                            (5, 28672)])
+@pytest.mark.parametrize("t", PACKED)
+@pytest.mark.parametrize("out_dim,in_dim", [(1, 32), (67, 96), (3, 256), (130, 1024), (33, 2048), (70, 3072),
+                                            (11, 3328), (257, 4096), (1000, 5120), (4096, 4096), (14336, 4096),
+                                            (4096, 14336), (9, 16384), (5, 28672)])
 def test_matvec_packed_shapes(ctx, orc, t, out_dim, in_dim):
+    if in_dim % GEOM[t][0]:
+        pytest.skip(f"{NAMES[t]} rows are whole {GEOM[t][0]}-element blocks")
     if not _rf().packed_supported(t, in_dim):
         # x of a row must fit the workgroup's LDS (64 KiB, or what the device allows)
         pytest.skip(f"in_dim {in_dim} exceeds this device's LDS for {NAMES[t]}")
     _check_matvec_packed(ctx, orc, t, out_dim, in_dim, 1200 + t + in_dim % 977 + out_dim)
 
 
-@pytest.mark.parametrize("t", [Q8_0, Q4_0])
+@pytest.mark.parametrize("t", PACKED)
 def test_matvec_packed_row_range_and_unaligned_x(ctx, orc, t):
     _check_matvec_packed(ctx, orc, t, 300, 4096, 1300 + t, row_start=128, row_count=77)
     _check_matvec_packed(ctx, orc, t, 300, 4096, 1310 + t, row_start=299)
     _check_matvec_packed(ctx, orc, t, 50, 2048, 1320 + t, x_off=4)
 
 
-@pytest.mark.parametrize("t", [Q8_0, Q4_0])
+# byte offsets of the f16 super-scales of a block (Q4_K: d and dmin)
+F16_SCALES = {Q8_0: [0], Q4_0: [0], Q4_K: [0, 2], Q6_K: [208]}
+
+
+@pytest.mark.parametrize("t", PACKED)
 def test_matvec_packed_subnormal_and_signed_scales(ctx, orc, t):
-    """Every block scale an f16 subnormal (the reference decodes frac * 2^-25,
-    half the IEEE value), +-0 or negative: the packed kernel's hardware f16
-    conversion plus its subnormal rule against the oracle.  With no normal
-    scale in the matrix, a scale off by 2x would show at full size."""
+    """Every f16 block scale (and Q4_K min scale) an f16 subnormal (the
+    reference decodes frac * 2^-25, half the IEEE value), +-0 or negative: the
+    packed kernel's hardware f16 conversion plus its subnormal rule against
+    the oracle.  With no normal scale in the matrix, a scale off by 2x would
+    show at full size."""
     def patch(raw, rng):
         bs = GEOM[t][1]
         blocks = raw.reshape(-1, bs)
-        sc = rng.integers(1, 0x400, len(blocks)).astype(np.uint16)
-        sc[::3] |= 0x8000
-        sc[1::7] = 0
-        sc[2::11] = 0x8000
-        blocks[:, 0:2] = sc.view(np.uint8).reshape(-1, 2)
+        for off in F16_SCALES[t]:
+            sc = rng.integers(1, 0x400, len(blocks)).astype(np.uint16)
+            sc[::3] |= 0x8000
+            sc[1::7] = 0
+            sc[2::11] = 0x8000
+            blocks[:, off:off + 2] = sc.view(np.uint8).reshape(-1, 2)
         return raw
 
     _check_matvec_packed(ctx, orc, t, 96, 3072, 1400 + t, patch=patch)
@@ -253,10 +268,12 @@ def test_matvec_packed_validation(ctx):
     with pytest.raises(rf.RamforgeError, match="exceeds out_dim"):
         rf.matvec_packed(ctx, Q8_0, w, (1, 128), x, y, 2)
     with pytest.raises(rf.RamforgeError, match="does not support"):
-        rf.matvec_packed(ctx, Q4_K, w, (1, 256), x, y)
+        rf.matvec_packed(ctx, Q5_K, w, (1, 256), x, y)
     assert y.numpy().tolist() == [7.0, 7.0]  # destination untouched
     assert not rf.packed_supported(Q8_0, 1 << 16) and rf.packed_supported(Q4_0, 14336)
     assert rf.packed_supported(Q8_0, 14336) and not rf.packed_supported(Q8_0, 100)
+    assert rf.packed_supported(Q4_K, 14336) and not rf.packed_supported(Q4_K, 4000)
+    assert rf.packed_supported(Q6_K, 4096) and not rf.packed_supported(Q5_K, 4096)
     for a in (w, x, y):
         a.free()
 
