@@ -184,6 +184,10 @@ def kernel_bench(rf, syn, use_graph: bool, reps: int = 3) -> list:
     mats = [("Q8_0 4096x4096", G.Q8_0, 4096, 4096, 0.02 / 127), ("F32 4096x4096", G.F32, 4096, 4096, 1.0)]
     for t, tn in ((G.Q4_0, "Q4_0"), (G.Q4_K, "Q4_K"), (G.Q6_K, "Q6_K")):
         mats += [(f"{tn} 14336x4096", t, 14336, 4096, 0.02), (f"{tn} 4096x14336", t, 4096, 14336, 0.02)]
+    # large single matrices (not BASELINE configs): a 70B-shape FFN matrix and the
+    # Q6_K output projection of an 8B Q4_K_M model
+    mats += [("Q8_0 28672x8192 (70B ffn)", G.Q8_0, 28672, 8192, 0.02 / 127),
+             ("Q6_K 128256x4096 (8B output)", G.Q6_K, 128256, 4096, 0.02)]
     for name, t, out_dim, in_dim, mul in mats:
         qk, bs = rf.BLOCK_GEOMETRY[t]
         nblk = out_dim * in_dim // qk
