@@ -47,7 +47,7 @@ constexpr uint32_t ATT_MAX_SPLITS = 256;
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-__device__ __forceinline__ uint32_t att_chunk(uint32_t total, uint32_t nsplit) {
+__host__ __device__ __forceinline__ uint32_t att_chunk(uint32_t total, uint32_t nsplit) {
   uint32_t c = (total + nsplit - 1) / nsplit;
   c = (c + 15u) & ~15u;
   return c < ATT_MIN_CHUNK ? ATT_MIN_CHUNK : c;
@@ -113,9 +113,14 @@ __device__ __forceinline__ void load_dims(float* dst, const float* src, int n) {
   }
 }
 
-template <int G, int DPL>
-__global__ __launch_bounds__(ATT_THREADS) void attn_split(AttnArgs a) {
+// W wavefronts per workgroup: one round of loads covers 16 W positions
+// (4 W position slots of 16 lanes, U positions each in pass 1; 16 rows per
+// wavefront in pass 2), so a chunk of up to 16 W positions is one memory round
+// trip per pass.
+template <int G, int DPL, int W>
+__global__ __launch_bounds__(64 * W) void attn_split(AttnArgs a) {
   constexpr int HD = DPL * 16;
+  constexpr uint32_t NTH = 64u * W, NSLOT = 4u * W;
   constexpr int U = DPL <= 8 ? ATT_UNROLL : ATT_UNROLL / 2;  // register budget for hd = 256
   constexpr uint32_t WMASK = 16u / G - 1u;
   __shared__ __align__(16) float sc[G][ATT_MAX_CHUNK];
@@ -123,7 +128,7 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_split(AttnArgs a) {
   __shared__ __align__(16) float kcur[HD];
   __shared__ __align__(16) float vcur[HD];
   __shared__ float mh[G], lh[G];
-  __shared__ __align__(16) float ored[4][G][HD];
+  __shared__ __align__(16) float ored[W][G][HD];
 
   const uint32_t g = blockIdx.y, sp = blockIdx.x;
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
@@ -155,7 +160,7 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_split(AttnArgs a) {
   if (nmain > 0) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const uint32_t j = min(slot + 16u * u, nmain - 1u);
+      const uint32_t j = min(slot + NSLOT * u, nmain - 1u);
       load_dims(kv[u], kb + (size_t)j * kvw, DPL);
     }
 #pragma unroll
@@ -166,14 +171,14 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_split(AttnArgs a) {
   }
 
   // Rotated q of the G heads, the current k (rotated) and v, and the slot
-  // write.  Element t of [q heads..., k, v] is handled by thread t % 256; all
+  // write.  Element t of [q heads..., k, v] is handled by thread t % NTH; all
   // loads are issued before any is used (clamped indices, in bounds).
   {
-    constexpr uint32_t NE = (G + 2) * HD, NP = (NE + ATT_THREADS - 1) / ATT_THREADS, HALF = HD / 2;
+    constexpr uint32_t NE = (G + 2) * HD, NP = (NE + NTH - 1) / NTH, HALF = HD / 2;
     float va[NP], vp[NP], c0[NP], c1[NP];
 #pragma unroll
     for (uint32_t i = 0; i < NP; ++i) {
-      const uint32_t t = min(tid + i * ATT_THREADS, NE - 1u), r = t / HD, d = t % HD;
+      const uint32_t t = min(tid + i * NTH, NE - 1u), r = t / HD, d = t % HD;
       const float* src = r < (uint32_t)G ? a.q + (size_t)(g * G + r) * HD : (r == (uint32_t)G ? a.k_cur : a.v_cur) + g * HD;
       const uint32_t ci = d < HALF ? d : d - HALF;
       va[i] = src[d];
@@ -183,7 +188,7 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_split(AttnArgs a) {
     }
 #pragma unroll
     for (uint32_t i = 0; i < NP; ++i) {
-      const uint32_t t = tid + i * ATT_THREADS, r = t / HD, d = t % HD;
+      const uint32_t t = tid + i * NTH, r = t / HD, d = t % HD;
       if (t >= NE) break;
       // half-split rotation in the RoPE kernel's operation order
       const float rot = d < HALF ? va[i] * c0[i] - vp[i] * c1[i] : vp[i] * c1[i] + va[i] * c0[i];
@@ -208,11 +213,11 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_split(AttnArgs a) {
     for (int i = 0; i < DPL; ++i) qr[h][i] = qs[h][d0 + i];
 
   // Pass 1: scores.
-  for (uint32_t j0 = 0; j0 < nmain; j0 += 16u * U) {
+  for (uint32_t j0 = 0; j0 < nmain; j0 += NSLOT * U) {
     if (j0 > 0) {
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        const uint32_t j = min(j0 + slot + 16u * u, nmain - 1u);
+        const uint32_t j = min(j0 + slot + NSLOT * u, nmain - 1u);
         load_dims(kv[u], kb + (size_t)j * kvw, DPL);
       }
     }
@@ -228,7 +233,7 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_split(AttnArgs a) {
       }
       uint32_t hh = 0;
       const float r = head_reduce16<G, 8>(s, lane, hh);
-      const uint32_t j = j0 + slot + 16u * u;
+      const uint32_t j = j0 + slot + NSLOT * u;
       if (j < nmain && (lane & WMASK) == 0) sc[hh][j] = r / a.denom;
     }
   }
@@ -248,7 +253,7 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_split(AttnArgs a) {
   __syncthreads();
 
   // Chunk max and exp-sum per head (one wavefront per head).
-  for (uint32_t h = wave; h < (uint32_t)G; h += 4u) {
+  for (uint32_t h = wave; h < (uint32_t)G; h += W) {
     float m = -INFINITY;
     for (uint32_t j = lane; j < npos; j += 64u) m = fmaxf(m, sc[h][j]);
     m = rf_wave_max(m);
@@ -263,13 +268,13 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_split(AttnArgs a) {
   }
   __syncthreads();
 
-  // Pass 2: o[h] = sum_p e[h][p] * V_p, 64 rows per batch.
+  // Pass 2: o[h] = sum_p e[h][p] * V_p, 16 W rows per batch.
   float o[G][DPW];
 #pragma unroll
   for (int h = 0; h < G; ++h)
 #pragma unroll
     for (int i = 0; i < DPW; ++i) o[h][i] = 0.f;
-  for (uint32_t j0 = 0; j0 < nmain; j0 += 64u) {
+  for (uint32_t j0 = 0; j0 < nmain; j0 += 16u * W) {
     if (j0 > 0) {
 #pragma unroll
       for (int k = 0; k < 16; ++k) {
@@ -304,15 +309,17 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_split(AttnArgs a) {
       for (int i = 0; i < DPW; ++i) o[h][i] = fmaf(e, vcur[lane * DPW + i], o[h][i]);
     }
   }
-  // Sum the four wavefronts.
+  // Sum the W wavefronts.
 #pragma unroll
   for (int h = 0; h < G; ++h)
 #pragma unroll
     for (int i = 0; i < DPW; ++i) ored[wave][h][lane * DPW + i] = o[h][i];
   __syncthreads();
-  for (uint32_t t = tid; t < (uint32_t)(G * HD); t += ATT_THREADS) {
+  for (uint32_t t = tid; t < (uint32_t)(G * HD); t += NTH) {
     const uint32_t h = t / HD, d = t % HD;
-    const float v = ored[0][h][d] + ored[1][h][d] + ored[2][h][d] + ored[3][h][d];
+    float v = ored[0][h][d];
+#pragma unroll
+    for (int w = 1; w < W; ++w) v += ored[w][h][d];
     const uint32_t qhead = g * G + h;
     if (ns == 1) {
       a.out[(size_t)qhead * HD + d] = v / lh[h];
@@ -474,10 +481,18 @@ uint64_t attention_ws_floats(uint32_t nsplit, uint32_t qh, uint32_t hd) {
   return (uint64_t)nsplit * qh * (hd + 2);
 }
 
-template <int G, int DPL>
+template <int G, int DPL, int W>
 static void launch_split_t(const AttnArgs& a, hipStream_t st) {
-  hipLaunchKernelGGL((attn_split<G, DPL>), dim3(a.nsplit, a.kvh), dim3(ATT_THREADS), 0, st, a);
+  hipLaunchKernelGGL((attn_split<G, DPL, W>), dim3(a.nsplit, a.kvh), dim3(64 * W), 0, st, a);
 }
+
+// Wavefronts per workgroup for chunks of up to `chunk` positions (one round
+// of loads per pass covers 16 W positions).  Timed on 32 q / 8 KV heads, hd
+// 128, split + merge per layer, graph replay over 32 layers of K/V: W = 8
+// wins once chunks pass 64 positions (8192 positions, 32 chunks: 19.3 vs
+// 20.6 us; 4096: 13.8 vs 15.0 us) and loses below (64 positions: 6.0 vs
+// 5.6 us); W = 16 (1024 threads, 128 VGPRs) spills and was slower everywhere.
+uint32_t attention_waves(uint32_t chunk, uint32_t) { return chunk <= 64 ? 4u : 8u; }
 
 hipError_t launch_attention_naive(const AttnArgs& a, hipStream_t st) {
   hipLaunchKernelGGL(attn_naive, dim3(a.qh), dim3(256), 0, st, a);
@@ -487,9 +502,16 @@ hipError_t launch_attention_naive(const AttnArgs& a, hipStream_t st) {
 hipError_t launch_attention(const AttnArgs& a, hipStream_t st) {
   if (a.nsplit < 1 || a.nsplit > ATT_MAX_SPLITS) return hipErrorInvalidValue;
   const uint32_t G = a.qh / a.kvh, dpl = a.hd / 16;
+  // API mode knows the context on the host; model mode passes the regime's W.
+  const uint32_t w = a.waves ? a.waves : attention_waves(att_chunk(a.hist + 1, a.nsplit), G * a.hd);
+  if (w != 4 && w != 8) return hipErrorInvalidValue;
   bool done = false;
-#define RF_ATT(GG, DD) \
-  if (!done && G == GG && dpl == DD) { launch_split_t<GG, DD>(a, st); done = true; }
+#define RF_ATT(GG, DD)                                          \
+  if (!done && G == GG && dpl == DD) {                          \
+    if (w == 4) launch_split_t<GG, DD, 4>(a, st);               \
+    else launch_split_t<GG, DD, 8>(a, st);                      \
+    done = true;                                                \
+  }
   RF_ATT(1, 4) RF_ATT(1, 8) RF_ATT(1, 16) RF_ATT(2, 4) RF_ATT(2, 8) RF_ATT(2, 16)
   RF_ATT(4, 4) RF_ATT(4, 8) RF_ATT(4, 16) RF_ATT(8, 4) RF_ATT(8, 8)
 #undef RF_ATT

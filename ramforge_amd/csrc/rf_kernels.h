@@ -118,12 +118,14 @@ struct AttnArgs {
   const int32_t* d_pos;  // model mode: device position (== hist), else null
   uint32_t hist;         // API mode history length
   uint32_t qh, kvh, hd, nsplit;
+  uint32_t waves;        // wavefronts per chunk workgroup (4 or 8); 0: chosen from hist
   float denom;           // sqrt(hd) as the reference computes it
 };
 hipError_t launch_attention(const AttnArgs& a, hipStream_t st);
 // Any-shape kernel; its workspace is [qh][hist + 1] floats.
 hipError_t launch_attention_naive(const AttnArgs& a, hipStream_t st);
 uint32_t attention_splits(uint32_t total_positions, uint32_t kvh);
+uint32_t attention_waves(uint32_t chunk, uint32_t g_hd);
 uint64_t attention_ws_floats(uint32_t nsplit, uint32_t qh, uint32_t hd);
 // The split kernel handles this shape for up to `total_positions` positions.
 bool attention_supported(uint32_t qh, uint32_t kvh, uint32_t hd, uint64_t total_positions);

@@ -88,9 +88,9 @@ struct rf_model {
   uint32_t nsplit = 1;  // attention chunks per KV head past ATT_SINGLE_CHUNK positions
   uint64_t seq_len = 0;
   bool use_graph = false;
-  // one decode-step graph per attention regime: [0] single chunk, [1] nsplit chunks + merge
-  hipGraph_t graph[2] = {nullptr, nullptr};
-  hipGraphExec_t graph_exec[2] = {nullptr, nullptr};
+  // one decode-step graph per attention regime (attn_regime)
+  hipGraph_t graph[3] = {nullptr, nullptr, nullptr};
+  hipGraphExec_t graph_exec[3] = {nullptr, nullptr, nullptr};
   std::vector<std::string> charges;
   // Layer streaming: every block tensor lives in pinned host memory and is
   // uploaded on demand; an LRU cache of at most cache_cap device bytes keeps
@@ -122,7 +122,7 @@ int32_t drop_tensor(rf_model* m, DevTensor& t) {
 }
 
 void reset_graph(rf_model* m) {
-  for (int r = 0; r < 2; ++r) {
+  for (int r = 0; r < 3; ++r) {
     if (m->graph_exec[r]) hipGraphExecDestroy(m->graph_exec[r]);
     if (m->graph[r]) hipGraphDestroy(m->graph[r]);
     m->graph_exec[r] = nullptr;
@@ -714,14 +714,21 @@ int32_t enqueue_qkv(rf_model* m, size_t li) {
   return RF_OK;
 }
 
-// Attention chunks for the step at position pos.  Up to ATT_SINGLE_CHUNK
-// positions one chunk per KV head covers the context and no merge kernel runs;
-// beyond, the capacity's split count (fixed, so one graph serves the regime).
+// Attention launch for the step at position pos, in three regimes (each a
+// decode graph of its own, so the launch shapes are fixed per regime):
+//   0: up to ATT_SINGLE_CHUNK positions one chunk per KV head covers the
+//      context and no merge kernel runs;
+//   1: the capacity's split count, chunks of 64 positions, 4 wavefronts;
+//   2: the same split count once chunks grow past 64 positions, 8 wavefronts.
 constexpr uint64_t ATT_SINGLE_CHUNK = 64;
-uint32_t attn_nsplit_at(const rf_model* m, uint64_t pos) {
-  return (m->attn_fast && pos + 1 <= ATT_SINGLE_CHUNK) ? 1u : m->nsplit;
+int attn_regime(const rf_model* m, uint64_t pos) {
+  if (!m->attn_fast) return 1;
+  const uint64_t total = pos + 1;
+  if (total <= ATT_SINGLE_CHUNK && m->nsplit > 1) return 0;
+  return total <= ATT_SINGLE_CHUNK * m->nsplit ? 1 : 2;
 }
-int attn_regime(const rf_model* m, uint64_t pos) { return attn_nsplit_at(m, pos) == m->nsplit ? 1 : 0; }
+uint32_t attn_nsplit_at(const rf_model* m, uint64_t pos) { return attn_regime(m, pos) == 0 ? 1u : m->nsplit; }
+uint32_t attn_waves_at(const rf_model* m, uint64_t pos) { return attn_regime(m, pos) == 2 ? 8u : 4u; }
 
 // 2. RoPE + attention + K/V cache write.
 int32_t enqueue_attention(rf_model* m, size_t li) {
@@ -735,6 +742,7 @@ int32_t enqueue_attention(rf_model* m, size_t li) {
   a.ws = m->attn_ws; a.rope = m->rope; a.k_store = kc; a.v_store = vc; a.d_pos = m->d_pos;
   a.qh = (uint32_t)c.head_count; a.kvh = (uint32_t)c.head_count_kv; a.hd = (uint32_t)hd;
   a.nsplit = attn_nsplit_at(m, m->seq_len);  // the position this step processes
+  a.waves = attn_waves_at(m, m->seq_len);
   a.denom = sqrtf((float)hd);
   RF_LAUNCH(m->attn_fast ? launch_attention(a, st) : launch_attention_naive(a, st), "attention");
   return RF_OK;

@@ -149,20 +149,29 @@ def test_device_decode_steps_graph_replay_matches_eager(ctx):
 
 
 REGIME_CFG = dict(TINY, context_length=256, embedding_length=256, feed_forward_length=512, head_dim=64)
+# 64 KV heads: the split count stops at 256 / 64 = 4 chunks, so past 256
+# positions the chunks grow beyond 64 and the 8-wavefront regime runs
+REGIME2_CFG = dict(TINY, context_length=512, embedding_length=256, feed_forward_length=512, head_count=64,
+                   head_count_kv=64, head_dim=64)
 
 
-def test_decode_graphs_cross_the_attention_regimes(ctx, orc):
-    """Decode from position 5 to 154 with graph replay: positions up to 63 run
-    the single-chunk attention graph, later ones the split + merge graph (both
-    captured lazily).  Tokens equal the eager loop's and the oracle's."""
+@pytest.mark.parametrize("cfg,cap,steps", [(REGIME_CFG, 160, (30, 40, 80)), (REGIME2_CFG, 320, (30, 40, 200, 40))],
+                         ids=["regimes-0-1", "regimes-0-1-2"])
+def test_decode_graphs_cross_the_attention_regimes(ctx, orc, cfg, cap, steps):
+    """Decode from position 5 with graph replay across the attention regimes:
+    up to 64 positions the single-chunk graph, then the split + merge graph
+    with 64-position chunks, then (64 KV heads, past 256 positions) the graph
+    with longer chunks and 8 wavefronts; each captured lazily.  Tokens equal
+    the eager loop's and the oracle's."""
     rng = np.random.default_rng(961)
-    T = _tiny_tensors(rng, REGIME_CFG, ALL_Q8)
+    T = _tiny_tensors(rng, cfg, ALL_Q8)
     prompt = [3, 1, 4, 1, 5]
-    gm = _load_gpu(ctx, REGIME_CFG, T, 160)
-    om = orc.Model(REGIME_CFG, T, kv_capacity=160, threads=4)
+    n = sum(steps)
+    gm = _load_gpu(ctx, cfg, T, cap)
+    om = orc.Model(cfg, T, kv_capacity=cap, threads=8)
     try:
-        ref = gm.generate(prompt, 150)
-        oref, margin = om.generate(prompt, 150)
+        ref = gm.generate(prompt, n)
+        oref, margin = om.generate(prompt, n)
         first = next((i for i, (a, b) in enumerate(zip(ref, oref)) if a != b), None)
         assert ref == oref, f"eager vs oracle: first divergence at {first}, margin {margin[first]:.3g}"
         gm.reset()
@@ -170,11 +179,11 @@ def test_decode_graphs_cross_the_attention_regimes(ctx, orc):
             gm.forward(t, p)
         gm.use_graph(True)
         got = []
-        for n in (30, 40, 80):  # 5..34, 35..74 (crosses 64), 75..154
-            gm.decode_steps(n)
-            got += gm.read_tokens(n)
+        for k in steps:
+            gm.decode_steps(k)
+            got += gm.read_tokens(k)
             ctx.synchronize()
-        assert got == ref[:150]
+        assert got == ref[:n]
         gm.use_graph(False)
     finally:
         om.close()
