@@ -39,7 +39,6 @@
 
 namespace rf {
 
-constexpr int ATT_THREADS = 256;
 constexpr uint32_t ATT_MAX_CHUNK = 1024;  // positions of one chunk (LDS score rows)
 constexpr uint32_t ATT_MIN_CHUNK = 64;    // 16 position slots x 4 loads in flight
 constexpr int ATT_UNROLL = 4;
@@ -116,9 +115,13 @@ __device__ __forceinline__ void load_dims(float* dst, const float* src, int n) {
 // W wavefronts per workgroup: one round of loads covers 16 W positions
 // (4 W position slots of 16 lanes, U positions each in pass 1; 16 rows per
 // wavefront in pass 2), so a chunk of up to 16 W positions is one memory round
-// trip per pass.
-template <int G, int DPL, int W>
+// trip per pass.  PERQ: one workgroup per query head (G = 1) instead of per
+// KV head, so short contexts spread over qh workgroups; the query heads of a
+// group read the same K/V rows (from L2 or HBM) and the group's first head
+// writes the cache slot.
+template <int G, int DPL, int W, bool PERQ>
 __global__ __launch_bounds__(64 * W) void attn_split(AttnArgs a) {
+  static_assert(!PERQ || G == 1, "one query head per workgroup");
   constexpr int HD = DPL * 16;
   constexpr uint32_t NTH = 64u * W, NSLOT = 4u * W;
   constexpr int U = DPL <= 8 ? ATT_UNROLL : ATT_UNROLL / 2;  // register budget for hd = 256
@@ -130,7 +133,10 @@ __global__ __launch_bounds__(64 * W) void attn_split(AttnArgs a) {
   __shared__ float mh[G], lh[G];
   __shared__ __align__(16) float ored[W][G][HD];
 
-  const uint32_t g = blockIdx.y, sp = blockIdx.x;
+  // g: the KV head; qg: the first query head of this workgroup
+  const uint32_t qg = PERQ ? blockIdx.y : blockIdx.y * G;
+  const uint32_t g = PERQ ? blockIdx.y / (a.qh / a.kvh) : blockIdx.y, sp = blockIdx.x;
+  const bool writes_slot = sp == 0 && (!PERQ || qg % (a.qh / a.kvh) == 0);
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
   const uint32_t hist = a.d_pos ? (uint32_t)(*a.d_pos) : a.hist;
   const uint32_t total = hist + 1;
@@ -179,7 +185,7 @@ __global__ __launch_bounds__(64 * W) void attn_split(AttnArgs a) {
 #pragma unroll
     for (uint32_t i = 0; i < NP; ++i) {
       const uint32_t t = min(tid + i * NTH, NE - 1u), r = t / HD, d = t % HD;
-      const float* src = r < (uint32_t)G ? a.q + (size_t)(g * G + r) * HD : (r == (uint32_t)G ? a.k_cur : a.v_cur) + g * HD;
+      const float* src = r < (uint32_t)G ? a.q + (size_t)(qg + r) * HD : (r == (uint32_t)G ? a.k_cur : a.v_cur) + g * HD;
       const uint32_t ci = d < HALF ? d : d - HALF;
       va[i] = src[d];
       vp[i] = src[d < HALF ? d + HALF : d - HALF];
@@ -197,10 +203,10 @@ __global__ __launch_bounds__(64 * W) void attn_split(AttnArgs a) {
       } else if (r == (uint32_t)G) {
         const float kv = cs ? rot : va[i];
         kcur[d] = kv;
-        if (a.k_store && sp == 0) a.k_store[(size_t)hist * kvw + g * HD + d] = kv;
+        if (a.k_store && writes_slot) a.k_store[(size_t)hist * kvw + g * HD + d] = kv;
       } else {
         vcur[d] = va[i];
-        if (a.v_store && sp == 0) a.v_store[(size_t)hist * kvw + g * HD + d] = va[i];
+        if (a.v_store && writes_slot) a.v_store[(size_t)hist * kvw + g * HD + d] = va[i];
       }
     }
   }
@@ -320,7 +326,7 @@ __global__ __launch_bounds__(64 * W) void attn_split(AttnArgs a) {
     float v = ored[0][h][d];
 #pragma unroll
     for (int w = 1; w < W; ++w) v += ored[w][h][d];
-    const uint32_t qhead = g * G + h;
+    const uint32_t qhead = qg + h;
     if (ns == 1) {
       a.out[(size_t)qhead * HD + d] = v / lh[h];
     } else {
@@ -477,13 +483,58 @@ uint32_t attention_splits(uint32_t total, uint32_t kvh) {
   return n < 1 ? 1 : n;
 }
 
+// Launch regimes of single-query attention, each one fixed shape so that one
+// captured graph serves every position in it.  cap = the largest context the
+// caller will use (the model's KV capacity; the API passes the context
+// itself).  Workgroups target about 256 (one per CU) and chunks of at least
+// 64 positions.  Timed per layer on 32 q / 8 KV heads, hd 128, split + merge,
+// graph replay over 32 layers of K/V:
+//   0  context <= 64: one workgroup per query head, one chunk, no merge
+//      (4.7-5.6 us; per KV head 5.4-6.7);
+//   1  <= 64 Sq (Sq = min(256 / qh, 8) chunks): per query head, 64-position chunks,
+//      4 wavefronts (96-512 positions: 7.4-7.8 us; per KV head 9.1-9.5);
+//   2  <= 128 Sq: per query head, 8 wavefronts (1024 positions: 9.6 vs 10.1);
+//   3  <= 64 Skv (Skv = attention_splits(cap)): per KV head, 4 wavefronts;
+//   4  beyond: per KV head, 8 wavefronts.
+// The workgroups of one chunk's query heads sit nsplit apart in dispatch
+// order, so with nsplit a multiple of 8 they land on one XCD and the re-reads
+// of that chunk's K/V by the G heads of a group hit its L2.  Past ~1K
+// positions those re-reads (G x the K/V bytes through L2) cost more than the
+// per-query-head layout gains, so regimes 3-4 read each K/V row once per KV
+// head; Sq stops at 8 so the per-query-head regimes end by 1024 positions.
+static uint32_t regime_sq(uint32_t qh) {
+  const uint32_t s = qh >= 256 ? 1u : 256u / qh;
+  return s > 8 ? 8u : s;
+}
+static uint32_t regime_skv(uint64_t cap, uint32_t kvh) {
+  return attention_splits((uint32_t)(cap < 0xFFFFFFFFull ? cap : 0xFFFFFFFFull), kvh);
+}
+AttnShape attention_regime_shape(int r, uint32_t qh, uint32_t kvh, uint64_t cap) {
+  const uint32_t sq = regime_sq(qh);
+  const uint32_t skv = regime_skv(cap, kvh);
+  switch (r) {
+    case 0: return AttnShape{1, 1, 4};
+    case 1: return AttnShape{1, sq, 4};
+    case 2: return AttnShape{1, sq, 8};
+    case 3: return AttnShape{0, skv, 4};
+    default: return AttnShape{0, skv, 8};
+  }
+}
+int attention_regime(uint64_t total, uint32_t qh, uint32_t kvh, uint64_t cap) {
+  const uint64_t sq = regime_sq(qh);
+  if (total <= ATT_MIN_CHUNK) return 0;
+  if (total <= ATT_MIN_CHUNK * sq) return 1;
+  if (total <= 2 * ATT_MIN_CHUNK * sq) return 2;
+  return total <= ATT_MIN_CHUNK * (uint64_t)regime_skv(cap, kvh) ? 3 : 4;
+}
+
 uint64_t attention_ws_floats(uint32_t nsplit, uint32_t qh, uint32_t hd) {
   return (uint64_t)nsplit * qh * (hd + 2);
 }
 
-template <int G, int DPL, int W>
+template <int G, int DPL, int W, bool PERQ = false>
 static void launch_split_t(const AttnArgs& a, hipStream_t st) {
-  hipLaunchKernelGGL((attn_split<G, DPL, W>), dim3(a.nsplit, a.kvh), dim3(64 * W), 0, st, a);
+  hipLaunchKernelGGL((attn_split<G, DPL, W, PERQ>), dim3(a.nsplit, PERQ ? a.qh : a.kvh), dim3(64 * W), 0, st, a);
 }
 
 // Wavefronts per workgroup for chunks of up to `chunk` positions (one round
@@ -506,6 +557,18 @@ hipError_t launch_attention(const AttnArgs& a, hipStream_t st) {
   const uint32_t w = a.waves ? a.waves : attention_waves(att_chunk(a.hist + 1, a.nsplit), G * a.hd);
   if (w != 4 && w != 8) return hipErrorInvalidValue;
   bool done = false;
+  if (a.per_q) {  // one workgroup per query head: G = 1 kernels, any GQA ratio
+    switch (dpl * 2 + (w == 8 ? 1 : 0)) {
+      case 8: launch_split_t<1, 4, 4, true>(a, st); break;
+      case 9: launch_split_t<1, 4, 8, true>(a, st); break;
+      case 16: launch_split_t<1, 8, 4, true>(a, st); break;
+      case 17: launch_split_t<1, 8, 8, true>(a, st); break;
+      case 32: launch_split_t<1, 16, 4, true>(a, st); break;
+      case 33: launch_split_t<1, 16, 8, true>(a, st); break;
+      default: return hipErrorInvalidValue;
+    }
+    done = true;
+  }
 #define RF_ATT(GG, DD)                                          \
   if (!done && G == GG && dpl == DD) {                          \
     if (w == 4) launch_split_t<GG, DD, 4>(a, st);               \

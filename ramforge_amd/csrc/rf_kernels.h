@@ -119,6 +119,7 @@ struct AttnArgs {
   uint32_t hist;         // API mode history length
   uint32_t qh, kvh, hd, nsplit;
   uint32_t waves;        // wavefronts per chunk workgroup (4 or 8); 0: chosen from hist
+  uint32_t per_q;        // nonzero: one workgroup per query head and chunk (short contexts)
   float denom;           // sqrt(hd) as the reference computes it
 };
 hipError_t launch_attention(const AttnArgs& a, hipStream_t st);
@@ -126,6 +127,12 @@ hipError_t launch_attention(const AttnArgs& a, hipStream_t st);
 hipError_t launch_attention_naive(const AttnArgs& a, hipStream_t st);
 uint32_t attention_splits(uint32_t total_positions, uint32_t kvh);
 uint32_t attention_waves(uint32_t chunk, uint32_t g_hd);
+struct AttnShape {
+  uint32_t per_q, nsplit, waves;
+};
+constexpr int ATT_REGIMES = 5;
+int attention_regime(uint64_t total, uint32_t qh, uint32_t kvh, uint64_t cap);
+AttnShape attention_regime_shape(int regime, uint32_t qh, uint32_t kvh, uint64_t cap);
 uint64_t attention_ws_floats(uint32_t nsplit, uint32_t qh, uint32_t hd);
 // The split kernel handles this shape for up to `total_positions` positions.
 bool attention_supported(uint32_t qh, uint32_t kvh, uint32_t hd, uint64_t total_positions);

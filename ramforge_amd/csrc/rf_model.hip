@@ -85,12 +85,12 @@ struct rf_model {
   int32_t* d_pos = nullptr;
   uint32_t* d_token = nullptr;
   uint32_t* d_ring = nullptr;  // token chosen for position p is stored at ring[p]
-  uint32_t nsplit = 1;  // attention chunks per KV head past ATT_SINGLE_CHUNK positions
+  uint32_t attn_chunks = 1;  // largest chunk count of the attention regimes (workspace records per head)
   uint64_t seq_len = 0;
   bool use_graph = false;
   // one decode-step graph per attention regime (attn_regime)
-  hipGraph_t graph[3] = {nullptr, nullptr, nullptr};
-  hipGraphExec_t graph_exec[3] = {nullptr, nullptr, nullptr};
+  hipGraph_t graph[ATT_REGIMES] = {};
+  hipGraphExec_t graph_exec[ATT_REGIMES] = {};
   std::vector<std::string> charges;
   // Layer streaming: every block tensor lives in pinned host memory and is
   // uploaded on demand; an LRU cache of at most cache_cap device bytes keeps
@@ -122,7 +122,7 @@ int32_t drop_tensor(rf_model* m, DevTensor& t) {
 }
 
 void reset_graph(rf_model* m) {
-  for (int r = 0; r < 3; ++r) {
+  for (int r = 0; r < ATT_REGIMES; ++r) {
     if (m->graph_exec[r]) hipGraphExecDestroy(m->graph_exec[r]);
     if (m->graph[r]) hipGraphDestroy(m->graph[r]);
     m->graph_exec[r] = nullptr;
@@ -714,21 +714,14 @@ int32_t enqueue_qkv(rf_model* m, size_t li) {
   return RF_OK;
 }
 
-// Attention launch for the step at position pos, in three regimes (each a
-// decode graph of its own, so the launch shapes are fixed per regime):
-//   0: up to ATT_SINGLE_CHUNK positions one chunk per KV head covers the
-//      context and no merge kernel runs;
-//   1: the capacity's split count, chunks of 64 positions, 4 wavefronts;
-//   2: the same split count once chunks grow past 64 positions, 8 wavefronts.
-constexpr uint64_t ATT_SINGLE_CHUNK = 64;
+// Attention launch regime of the step at position pos (attention_regime with
+// the KV capacity as the longest context): each regime is a decode graph of
+// its own, so the launch shape is fixed within one.  The any-shape kernel has
+// a single shape.
 int attn_regime(const rf_model* m, uint64_t pos) {
-  if (!m->attn_fast) return 1;
-  const uint64_t total = pos + 1;
-  if (total <= ATT_SINGLE_CHUNK && m->nsplit > 1) return 0;
-  return total <= ATT_SINGLE_CHUNK * m->nsplit ? 1 : 2;
+  if (!m->attn_fast) return 0;
+  return attention_regime(pos + 1, (uint32_t)m->cfg.head_count, (uint32_t)m->cfg.head_count_kv, m->kv_cap);
 }
-uint32_t attn_nsplit_at(const rf_model* m, uint64_t pos) { return attn_regime(m, pos) == 0 ? 1u : m->nsplit; }
-uint32_t attn_waves_at(const rf_model* m, uint64_t pos) { return attn_regime(m, pos) == 2 ? 8u : 4u; }
 
 // 2. RoPE + attention + K/V cache write.
 int32_t enqueue_attention(rf_model* m, size_t li) {
@@ -741,8 +734,9 @@ int32_t enqueue_attention(rf_model* m, size_t li) {
   a.q = m->q; a.k_hist = kc; a.v_hist = vc; a.k_cur = m->k; a.v_cur = m->v; a.out = m->attn_out;
   a.ws = m->attn_ws; a.rope = m->rope; a.k_store = kc; a.v_store = vc; a.d_pos = m->d_pos;
   a.qh = (uint32_t)c.head_count; a.kvh = (uint32_t)c.head_count_kv; a.hd = (uint32_t)hd;
-  a.nsplit = attn_nsplit_at(m, m->seq_len);  // the position this step processes
-  a.waves = attn_waves_at(m, m->seq_len);
+  // the position this step processes picks the shape
+  const AttnShape sh = attention_regime_shape(attn_regime(m, m->seq_len), a.qh, a.kvh, m->kv_cap);
+  a.per_q = sh.per_q; a.nsplit = sh.nsplit; a.waves = sh.waves;
   a.denom = sqrtf((float)hd);
   RF_LAUNCH(m->attn_fast ? launch_attention(a, st) : launch_attention_naive(a, st), "attention");
   return RF_OK;
@@ -939,8 +933,12 @@ int32_t rf_model_create(rf_ctx* ctx, const rf_model_config* cfg, uint64_t kv_cap
   const bool fast = attention_supported((uint32_t)c.head_count, (uint32_t)c.head_count_kv, (uint32_t)c.head_dim,
                                         kv_cap);
   m->attn_fast = fast;
-  m->nsplit = fast ? attention_splits((uint32_t)kv_cap, (uint32_t)c.head_count_kv) : 1;
-  const uint64_t ws_floats = fast ? attention_ws_floats(m->nsplit, (uint32_t)c.head_count, (uint32_t)c.head_dim)
+  m->attn_chunks = 1;
+  for (int r = 0; fast && r < ATT_REGIMES; ++r) {
+    const AttnShape sh = attention_regime_shape(r, (uint32_t)c.head_count, (uint32_t)c.head_count_kv, kv_cap);
+    if (sh.nsplit > m->attn_chunks) m->attn_chunks = sh.nsplit;
+  }
+  const uint64_t ws_floats = fast ? attention_ws_floats(m->attn_chunks, (uint32_t)c.head_count, (uint32_t)c.head_dim)
                                   : c.head_count * kv_cap;
   rc = charge_alloc(m, "workspace:model_attention", ws_floats * 4, &p);
   if (rc) { rf_model_destroy(m); return rc; }

@@ -603,8 +603,9 @@ int32_t rf_attention_decode(rf_ctx* ctx, const float* q, const float* kh, const 
   const bool fast = attention_supported(qh, kvh, hd, total) && aligned(q) && (hist == 0 || (aligned(kh) && aligned(vh))) &&
                     aligned(kc) && aligned(vc);
   uint64_t ws_bytes;
-  if (fast) {
-    a.nsplit = attention_splits(total, kvh);
+  if (fast) {  // the context is known here: its own regime, sized to itself
+    const AttnShape sh = attention_regime_shape(attention_regime(total, qh, kvh, total), qh, kvh, total);
+    a.per_q = sh.per_q; a.nsplit = sh.nsplit; a.waves = sh.waves;
     ws_bytes = attention_ws_floats(a.nsplit, qh, hd) * 4;
   } else {
     a.nsplit = 1;

@@ -439,12 +439,15 @@ def test_attention_shapes(ctx, orc, hist, qh, kvh, hd):
     _attention_case(ctx, orc, hist, qh, kvh, hd, 600 + hist + qh + hd)
 
 
-@pytest.mark.parametrize("hist,qh,kvh", [(63, 32, 8), (64, 32, 8), (127, 32, 8), (1023, 32, 8), (1087, 32, 8),
-                                         (1100, 64, 8), (20000, 32, 8), (5000, 8, 1)])
+@pytest.mark.parametrize("hist,qh,kvh", [(63, 32, 8), (64, 32, 8), (127, 32, 8), (511, 32, 8), (512, 32, 8),
+                                         (1023, 32, 8), (1024, 32, 8), (1087, 32, 8), (300, 64, 8), (1100, 64, 8),
+                                         (20000, 32, 8), (5000, 8, 1)])
 def test_attention_chunk_tree(ctx, orc, hist, qh, kvh):
-    """Chunk counts around the in-kernel merge tree: one chunk (direct
-    output), up to 16 (one merge level), more (two levels, partly filled last
-    group).  Each case runs twice: the arrival counters must be back at zero."""
+    """Contexts on both sides of each launch-regime boundary (64, 64 Sq, 128 Sq
+    positions with Sq = min(256 / qh, 8) chunks per query head; 64-position
+    chunks per KV head; longer chunks): one chunk with direct output, and
+    split + merge with empty trailing chunks.  Each case runs twice and must
+    give the same bits."""
     rf = _rf()
     _attention_case(ctx, orc, hist, qh, kvh, 128, 900 + hist + qh)
     rng = np.random.default_rng(hist)

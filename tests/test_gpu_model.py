@@ -149,20 +149,26 @@ def test_device_decode_steps_graph_replay_matches_eager(ctx):
 
 
 REGIME_CFG = dict(TINY, context_length=256, embedding_length=256, feed_forward_length=512, head_dim=64)
-# 64 KV heads: the split count stops at 256 / 64 = 4 chunks, so past 256
-# positions the chunks grow beyond 64 and the 8-wavefront regime runs
+# 64 KV heads: per query head up to 4 chunks (256 / 64 heads), so 8 wavefronts
+# past 256 positions
 REGIME2_CFG = dict(TINY, context_length=512, embedding_length=256, feed_forward_length=512, head_count=64,
                    head_count_kv=64, head_dim=64)
+# 64 query / 16 KV heads at capacity 1100: per query head with 4 chunks up to
+# 512 positions (4 then 8 wavefronts), then per KV head with 16 chunks of 64
+# positions up to 1024 and longer chunks beyond: all five regimes
+REGIME5_CFG = dict(TINY, context_length=1100, embedding_length=256, feed_forward_length=512, head_count=64,
+                   head_count_kv=16, head_dim=32)
 
 
-@pytest.mark.parametrize("cfg,cap,steps", [(REGIME_CFG, 160, (30, 40, 80)), (REGIME2_CFG, 320, (30, 40, 200, 40))],
-                         ids=["regimes-0-1", "regimes-0-1-2"])
+@pytest.mark.parametrize("cfg,cap,steps", [(REGIME_CFG, 160, (30, 40, 80)), (REGIME2_CFG, 320, (30, 40, 200, 40)),
+                                           (REGIME5_CFG, 1100, (30, 40, 200, 300, 500, 20))],
+                         ids=["regimes-0-1", "regimes-0-1-2", "regimes-0-to-4"])
 def test_decode_graphs_cross_the_attention_regimes(ctx, orc, cfg, cap, steps):
-    """Decode from position 5 with graph replay across the attention regimes:
-    up to 64 positions the single-chunk graph, then the split + merge graph
-    with 64-position chunks, then (64 KV heads, past 256 positions) the graph
-    with longer chunks and 8 wavefronts; each captured lazily.  Tokens equal
-    the eager loop's and the oracle's."""
+    """Decode from position 5 with graph replay across the attention launch
+    regimes: one chunk per query head up to 64 positions, then several chunks
+    per query head (4 and 8 wavefronts), then chunks per KV head (64 positions
+    with 4 wavefronts, longer with 8); each regime's graph is captured lazily.
+    Tokens equal the eager loop's and the oracle's."""
     rng = np.random.default_rng(961)
     T = _tiny_tensors(rng, cfg, ALL_Q8)
     prompt = [3, 1, 4, 1, 5]
