@@ -164,6 +164,18 @@ int32_t rf_pack_weights(rf_ctx *ctx, uint32_t ggml_type, const void *raw, uint64
 int32_t rf_matvec_packed(rf_ctx *ctx, uint32_t ggml_type, const void *packed, uint64_t packed_bytes,
                          uint64_t out_dim, uint64_t in_dim, const float *x, float *y, uint64_t row_start,
                          uint64_t row_count, rf_stream_t stream);
+/* Batched matvec for prompt prefill: y[t][o] = sum_i W[o][i] x[t][i] for
+ * n_tokens rows of x ([n_tokens][in_dim]) on a packed tensor, into
+ * y[n_tokens][out_dim].  No counterpart in the reference, which runs the
+ * matvec once per prompt token (inference.rs:580-592); each y row is the
+ * matvec of quant::matvec_q8_0 / _q4_0 / _q4_k / _q6_k (quant.rs:898-1327)
+ * to f32 accuracy (summation order aside), computed on the matrix cores
+ * (bf16 MFMA on exact integer codes and a three-piece bf16 split of x).
+ * in_dim must be a whole number of blocks; validation as rf_matvec_packed
+ * (packed_bytes >= out_dim rows). */
+int32_t rf_matmul_packed(rf_ctx *ctx, uint32_t ggml_type, const void *packed, uint64_t packed_bytes,
+                         uint64_t out_dim, uint64_t in_dim, const float *x, uint64_t n_tokens, float *y,
+                         rf_stream_t stream);
 
 /* Bit-exact row decode: rows [row_start, row_start + row_count) of a
  * [rows, in_dim] GGUF tensor into out[row_count][in_dim].  Replaces
@@ -278,6 +290,21 @@ int32_t rf_model_generate(rf_model *model, const uint32_t *prompt, uint64_t prom
 int32_t rf_model_decode_steps(rf_model *model, uint64_t steps);
 /* Copies the last `n` greedy tokens produced by rf_model_decode_steps. */
 int32_t rf_model_read_tokens(rf_model *model, uint32_t *out, uint64_t n);
+/* Batched prompt prefill: forwards tokens[0..n) at positions seq_len ..
+ * seq_len + n - 1 in chunks of 64 tokens, each chunk through every layer
+ * with the projections as rf_matmul_packed GEMMs, per-token RMSNorm, RoPE,
+ * K/V cache writes and causal attention over the cache.  Same result as n
+ * rf_model_forward calls (the reference's prompt loop, inference.rs:580-592)
+ * to f32 accuracy; afterwards the model is where those calls leave it
+ * (rf_model_logits, rf_model_decode_steps continue from the last token).
+ * Models whose projections are not all in the packed layout (or whose
+ * attention shape needs the any-shape kernel) are forwarded one token at a
+ * time instead.  final_hidden as rf_model_forward, for the last token.  No
+ * counterpart in the reference. */
+int32_t rf_model_prefill(rf_model *model, const uint32_t *tokens, uint64_t n, float *final_hidden);
+/* rf_model_generate forwards the prompt with rf_model_prefill (1) or one
+ * token at a time as the reference does (0, default). */
+int32_t rf_model_set_prefill(rf_model *model, int32_t batched);
 /* Enables capture of one decode step into a hipGraph that is replayed by
  * rf_model_decode_steps (1) or eager launches (0, default). */
 int32_t rf_model_use_graph(rf_model *model, int32_t enable);

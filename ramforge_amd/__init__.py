@@ -310,6 +310,20 @@ def matvec_packed(ctx: Context, ggml_type: int, w, w_shape: Sequence[int], x, y,
     _lib.check(rc)
 
 
+def matmul_packed(ctx: Context, ggml_type: int, w, w_shape: Sequence[int], x, n_tokens: int, y,
+                  w_bytes: Optional[int] = None, stream=None) -> None:
+    """Batched matvec for prompt prefill: y[t] = W x[t] for n_tokens rows of
+    x ([n_tokens][in_dim]) on a packed tensor, y [n_tokens][out_dim], on the
+    matrix cores (no reference counterpart: the reference runs matvec_<fmt>
+    per prompt token, quant.rs:898-1327)."""
+    if len(w_shape) != 2:
+        raise RamforgeError(_lib.RF_ERR_INVALID, f"{GGML.NAMES.get(ggml_type, ggml_type)} matmul expects 2D weight")
+    out_dim, in_dim = (int(v) for v in w_shape)
+    wb = w.nbytes if (w_bytes is None and isinstance(w, DeviceArray)) else int(w_bytes or 0)
+    _lib.check(ctx.lib.rf_matmul_packed(ctx.handle, ggml_type, _ptr(w), wb, out_dim, in_dim, _ptr(x), n_tokens,
+                                        _ptr(y), stream))
+
+
 def dequantize_rows(ctx: Context, ggml_type: int, w, in_dim: int, row_start: int, row_count: int, out,
                     w_bytes: Optional[int] = None, stream=None) -> None:
     """dequantize_row_<fmt> (quant.rs:615-868) for a row range, bit-exact."""
@@ -491,6 +505,19 @@ class GpuLlamaModel:
         _lib.check(self.ctx.lib.rf_model_forward(self.handle, token, pos,
                                                  hidden.ctypes.data if hidden is not None else None))
         return hidden
+
+    def prefill(self, tokens: Sequence[int], want_hidden: bool = False) -> Optional[np.ndarray]:
+        """Forwards tokens at positions seq_len.. as batched chunks (same
+        result as one forward() per token, to f32 accuracy)."""
+        p = np.ascontiguousarray(np.asarray(tokens, dtype=np.uint32))
+        hidden = np.empty(self.cfg["embedding_length"], np.float32) if want_hidden else None
+        _lib.check(self.ctx.lib.rf_model_prefill(self.handle, p.ctypes.data, len(p),
+                                                 hidden.ctypes.data if hidden is not None else None))
+        return hidden
+
+    def set_prefill(self, batched: bool) -> None:
+        """generate() forwards its prompt batched (True) or token by token."""
+        _lib.check(self.ctx.lib.rf_model_set_prefill(self.handle, 1 if batched else 0))
 
     def logits(self) -> np.ndarray:
         out = np.empty(self.cfg["vocab_size"], np.float32)

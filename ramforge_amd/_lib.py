@@ -79,6 +79,7 @@ SIGNATURES = {
     "rf_packed_supported": (_i32, [_u32, _u64]),
     "rf_pack_weights": (_i32, [_vp, _u32, _vp, _u64, _u64, _u64, _vp, _u64, _vp]),
     "rf_matvec_packed": (_i32, [_vp, _u32, _vp, _u64, _u64, _u64, _fp, _fp, _u64, _u64, _vp]),
+    "rf_matmul_packed": (_i32, [_vp, _u32, _vp, _u64, _u64, _u64, _fp, _u64, _fp, _vp]),
     "rf_event_create": (_i32, [_vp, C.POINTER(_vp)]),
     "rf_event_destroy": (_i32, [_vp, _vp]),
     "rf_event_record": (_i32, [_vp, _vp, _vp]),
@@ -104,6 +105,8 @@ SIGNATURES = {
     "rf_model_reset": (_i32, [_vp]),
     "rf_model_seq_len": (_u64, [_vp]),
     "rf_model_forward": (_i32, [_vp, _u32, _u64, _vp]),
+    "rf_model_prefill": (_i32, [_vp, _vp, _u64, _vp]),
+    "rf_model_set_prefill": (_i32, [_vp, _i32]),
     "rf_model_logits": (_i32, [_vp, _vp]),
     "rf_model_generate": (_i32, [_vp, _vp, _u64, _u64, _i64, _vp, C.POINTER(_u64)]),
     "rf_model_decode_steps": (_i32, [_vp, _u64]),

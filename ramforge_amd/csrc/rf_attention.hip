@@ -138,7 +138,16 @@ __global__ __launch_bounds__(64 * W) void attn_split(AttnArgs a) {
   const uint32_t g = PERQ ? blockIdx.y / (a.qh / a.kvh) : blockIdx.y, sp = blockIdx.x;
   const bool writes_slot = sp == 0 && (!PERQ || qg % (a.qh / a.kvh) == 0);
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
-  const uint32_t hist = a.d_pos ? (uint32_t)(*a.d_pos) : a.hist;
+  // token batch (prefill): query z of a.ntok at position hist + z, whose own
+  // k / v are already in the cache row hist + z
+  const uint32_t z = blockIdx.z;
+  const uint32_t hist = (a.d_pos ? (uint32_t)(*a.d_pos) : a.hist) + z;
+  const uint32_t kvw = a.kvh * HD;
+  const float* qz = a.q + (size_t)z * a.qh * HD;
+  const float* kcur_p = a.ntok ? a.k_hist + (size_t)hist * kvw : a.k_cur;
+  const float* vcur_p = a.ntok ? a.v_hist + (size_t)hist * kvw : a.v_cur;
+  float* outz = a.out + (size_t)z * a.qh * HD;
+  float* wsz = a.ws + (size_t)z * a.nsplit * a.qh * (HD + 2);
   const uint32_t total = hist + 1;
   const uint32_t chunk = att_chunk(total, a.nsplit);
   const uint32_t p0 = sp * chunk;
@@ -148,7 +157,6 @@ __global__ __launch_bounds__(64 * W) void attn_split(AttnArgs a) {
   const uint32_t nmain = min(p1, hist) - p0;  // positions read from the cache
   const bool has_cur = p1 == total;           // the current position is the last one
   const uint32_t ns = (total + chunk - 1) / chunk;
-  const uint32_t kvw = a.kvh * HD;
   const float* cs = a.rope ? a.rope + (size_t)hist * HD : nullptr;  // [half][2] for this position
   const uint32_t sl = lane & 15u, slot = wave * 4u + (lane >> 4);
   const uint32_t d0 = sl * DPL;
@@ -185,7 +193,7 @@ __global__ __launch_bounds__(64 * W) void attn_split(AttnArgs a) {
 #pragma unroll
     for (uint32_t i = 0; i < NP; ++i) {
       const uint32_t t = min(tid + i * NTH, NE - 1u), r = t / HD, d = t % HD;
-      const float* src = r < (uint32_t)G ? a.q + (size_t)(qg + r) * HD : (r == (uint32_t)G ? a.k_cur : a.v_cur) + g * HD;
+      const float* src = r < (uint32_t)G ? qz + (size_t)(qg + r) * HD : (r == (uint32_t)G ? kcur_p : vcur_p) + g * HD;
       const uint32_t ci = d < HALF ? d : d - HALF;
       va[i] = src[d];
       vp[i] = src[d < HALF ? d + HALF : d - HALF];
@@ -328,9 +336,9 @@ __global__ __launch_bounds__(64 * W) void attn_split(AttnArgs a) {
     for (int w = 1; w < W; ++w) v += ored[w][h][d];
     const uint32_t qhead = qg + h;
     if (ns == 1) {
-      a.out[(size_t)qhead * HD + d] = v / lh[h];
+      outz[(size_t)qhead * HD + d] = v / lh[h];
     } else {
-      float* w = a.ws + ((size_t)sp * a.qh + qhead) * (HD + 2);
+      float* w = wsz + ((size_t)sp * a.qh + qhead) * (HD + 2);
       w[d] = v;
       if (d == 0) { w[HD] = mh[h]; w[HD + 1] = lh[h]; }
     }
@@ -345,13 +353,14 @@ __global__ __launch_bounds__(256) void attn_combine(AttnArgs a) {
   __shared__ float red[8][32];
   __shared__ float wm[4], wl[4];
   const uint32_t qhead = blockIdx.x, hd = a.hd, tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
-  const uint32_t hist = a.d_pos ? (uint32_t)(*a.d_pos) : a.hist;
+  const uint32_t z = blockIdx.z;  // token batch: see attn_split
+  const uint32_t hist = (a.d_pos ? (uint32_t)(*a.d_pos) : a.hist) + z;
   const uint32_t total = hist + 1;
   const uint32_t chunk = att_chunk(total, a.nsplit);
   const uint32_t ns = (total + chunk - 1) / chunk;
   if (ns == 1) return;
   const size_t rec = hd + 2, stride = (size_t)a.qh * rec;
-  const float* base = a.ws + (size_t)qhead * rec;
+  const float* base = a.ws + (size_t)z * a.nsplit * stride + (size_t)qhead * rec;
   const uint32_t dl = tid & 31u, grp = tid >> 5, d = blockIdx.y * 32u + dl;
   // the first four records of this lane's chunk subset, requested up front
   float pre[4];
@@ -385,7 +394,7 @@ __global__ __launch_bounds__(256) void attn_combine(AttnArgs a) {
     float v = 0.f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) v += red[i][dl];
-    a.out[(size_t)qhead * hd + d] = v / l;
+    a.out[(size_t)z * a.qh * hd + (size_t)qhead * hd + d] = v / l;
   }
 }
 
@@ -534,7 +543,8 @@ uint64_t attention_ws_floats(uint32_t nsplit, uint32_t qh, uint32_t hd) {
 
 template <int G, int DPL, int W, bool PERQ = false>
 static void launch_split_t(const AttnArgs& a, hipStream_t st) {
-  hipLaunchKernelGGL((attn_split<G, DPL, W, PERQ>), dim3(a.nsplit, PERQ ? a.qh : a.kvh), dim3(64 * W), 0, st, a);
+  hipLaunchKernelGGL((attn_split<G, DPL, W, PERQ>), dim3(a.nsplit, PERQ ? a.qh : a.kvh, a.ntok ? a.ntok : 1),
+                     dim3(64 * W), 0, st, a);
 }
 
 // Wavefronts per workgroup for chunks of up to `chunk` positions (one round
@@ -581,7 +591,7 @@ hipError_t launch_attention(const AttnArgs& a, hipStream_t st) {
   if (!done) return hipErrorInvalidValue;
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || a.nsplit == 1) return e;
-  hipLaunchKernelGGL(attn_combine, dim3(a.qh, (a.hd + 31) / 32), dim3(256), 0, st, a);
+  hipLaunchKernelGGL(attn_combine, dim3(a.qh, (a.hd + 31) / 32, a.ntok ? a.ntok : 1), dim3(256), 0, st, a);
   return hipGetLastError();
 }
 

@@ -222,7 +222,7 @@ __global__ void dequant_kernel(const uint8_t* __restrict__ w, uint32_t in_dim, u
   const uint32_t u = (uint32_t)(t % units);
   uint64_t src_row = r;
   if (token) {
-    src_row = *token;
+    src_row = token[r];
     if (src_row >= token_rows) src_row = 0;  // the host validated ids it knows; a device id is clamped
   }
   const uint8_t* row = w + src_row * row_bytes;
@@ -241,7 +241,7 @@ __global__ void decode_plain_kernel(uint32_t t, const uint8_t* __restrict__ w, u
   const uint64_t r = i / in_dim, c = i % in_dim;
   uint64_t src_row = r;
   if (token) {
-    src_row = *token;
+    src_row = token[r];
     if (src_row >= token_rows) src_row = 0;
   }
   const uint64_t e = src_row * in_dim + c;

@@ -98,7 +98,7 @@ hipError_t launch_matvec_packed(uint32_t t, const PkSegDesc* segs, int nseg, con
 hipError_t launch_pack(uint32_t t, const void* raw, void* packed, uint64_t rows, uint64_t in_dim, hipStream_t st);
 
 // Bit-exact row decode: rows [0, rows) of `w` (row_bytes each) -> out[rows][in_dim].
-// If token_index != nullptr the single row *token_index is decoded instead.
+// If token_index != nullptr, output row r is row token_index[r] of `w`.
 hipError_t launch_dequant_rows(uint32_t t, const void* w, uint64_t in_dim, uint64_t rows,
                                float* out, const uint32_t* token_index, uint64_t token_rows,
                                hipStream_t st);
@@ -120,6 +120,9 @@ struct AttnArgs {
   uint32_t qh, kvh, hd, nsplit;
   uint32_t waves;        // wavefronts per chunk workgroup (4 or 8); 0: chosen from hist
   uint32_t per_q;        // nonzero: one workgroup per query head and chunk (short contexts)
+  uint32_t ntok;         // nonzero: a batch of ntok queries (prefill): query z at position
+                         // hist + z, q / out [ntok][qh][hd], ws [ntok][nsplit][qh][hd + 2]; every
+                         // query's own k / v already in the cache (k_hist / v_hist) and rotated
   float denom;           // sqrt(hd) as the reference computes it
 };
 hipError_t launch_attention(const AttnArgs& a, hipStream_t st);
@@ -136,6 +139,32 @@ AttnShape attention_regime_shape(int regime, uint32_t qh, uint32_t kvh, uint64_t
 uint64_t attention_ws_floats(uint32_t nsplit, uint32_t qh, uint32_t hd);
 // The split kernel handles this shape for up to `total_positions` positions.
 bool attention_supported(uint32_t qh, uint32_t kvh, uint32_t hd, uint64_t total_positions);
+
+// Batched prefill (rf_prefill.hip): Y[t][r] = sum_k W[r][k] X[t][k] for up to
+// MM_MAX_TOKENS tokens on the packed layout, on the matrix cores, with split-K
+// partials in `part` and the epilogue of the decode matvec (EPI_SWIGLU:
+// segment 0 gate, segment 1 up, output in segment 0's y).
+constexpr uint64_t MM_MAX_TOKENS = 64;
+struct MmSegDesc {
+  const void* packed;    // packed matrix base
+  uint64_t matrix_rows;  // rows of the whole packed matrix (locates its regions)
+  uint64_t row_start;    // first row of this segment within the matrix
+  uint64_t rows;
+  float* y;              // [n][ld]
+  const float* res;      // EPI_RESIDUAL: [n][ld]
+  const float* bias;     // EPI_STORE: added per row, or null
+  uint64_t ld;
+};
+bool mm_supported(uint32_t t, uint64_t in_dim);
+uint64_t mm_part_floats(const uint64_t* rows, int nseg, uint64_t in_dim, uint64_t n);
+hipError_t launch_matmul_packed(uint32_t t, const MmSegDesc* segs, int nseg, const float* x, uint64_t ldx,
+                                uint64_t n, uint64_t in_dim, int epi, float* part, uint64_t part_floats,
+                                hipStream_t st);
+hipError_t launch_rmsnorm_rows(const float* x, const float* w, uint64_t n, uint64_t rows, uint64_t ld, float eps,
+                               float* y, hipStream_t st);
+hipError_t launch_rope_kv_rows(const float* q, const float* k, const float* v, const float* rope, uint64_t pos0,
+                               uint64_t ntok, uint32_t qh, uint32_t kvh, uint32_t hd, float* qr, float* kc,
+                               float* vc, hipStream_t st);
 
 // Elementwise (rf_elementwise.hip).
 hipError_t launch_rmsnorm(const float* x, const float* w, uint64_t n, float eps, float* y, hipStream_t st);

@@ -98,6 +98,13 @@ struct rf_model {
   bool streaming = false;
   uint64_t cache_cap = 0, cache_used = 0;
   std::vector<LayerRes> res;
+  // Batched prefill (rf_model_prefill): activations of one chunk of prompt
+  // tokens and its workspaces, charged "tmp:prefill" at the first use.
+  bool prefill_batched = false;  // rf_model_generate forwards its prompt batched
+  float *p_h = nullptr, *p_xn = nullptr, *p_q = nullptr, *p_k = nullptr, *p_v = nullptr, *p_qr = nullptr;
+  float *p_a = nullptr, *p_act = nullptr, *p_up = nullptr, *p_part = nullptr, *p_att = nullptr;
+  uint32_t* p_tok = nullptr;
+  uint64_t p_part_floats = 0;
   std::list<uint32_t> lru;  // cached layers, most recently used first
   uint64_t st_hits = 0, st_misses = 0, st_evictions = 0, st_uploaded = 0;
   int cache_policy = 0;    // 0: LRU (LayerCache); 1: next use within the layer cycle
@@ -885,6 +892,176 @@ int32_t forward_token(rf_model* m, uint32_t token, uint64_t pos) {
   return RF_OK;
 }
 
+// ---------------------------------------------------------------- prefill
+// A chunk of up to MM_MAX_TOKENS prompt tokens through one layer
+// (model_executor.rs:102-236 for each token): the projections as GEMMs over
+// the chunk (rf_prefill.hip), RMSNorm per token, RoPE + K/V cache rows, then
+// causal attention of each token over the cache up to its own position.
+
+bool prefill_supported(const rf_model* m) {
+  if (!m->attn_fast) return false;
+  const uint64_t d = m->cfg.embedding_length, qd = m->cfg.head_count * m->cfg.head_dim, f = m->cfg.feed_forward_length;
+  for (const Layer& L : m->layers) {
+    const DevTensor* w[] = {&L.q, &L.k, &L.v, &L.o, &L.gate, &L.up, &L.down};
+    const uint64_t in[] = {d, d, d, qd, d, d, f};
+    for (int i = 0; i < 7; ++i)
+      if (!w[i]->packed || !mm_supported(w[i]->type, in[i])) return false;
+  }
+  return true;
+}
+
+int32_t ensure_prefill_ws(rf_model* m) {
+  if (m->p_h) return RF_OK;
+  const rf_model_config& c = m->cfg;
+  const uint64_t T = MM_MAX_TOKENS, d = c.embedding_length, hd = c.head_dim, qd = c.head_count * hd;
+  const uint64_t kvd = c.head_count_kv * hd, f = c.feed_forward_length;
+  // split-K partials: the largest of the launches a layer makes
+  uint64_t part = 0;
+  auto take_max = [&](std::initializer_list<uint64_t> rows, uint64_t in) {
+    uint64_t r[3] = {0, 0, 0};
+    int n = 0;
+    for (uint64_t x : rows) r[n++] = x;
+    const uint64_t v = mm_part_floats(r, n, in, T);
+    if (v > part) part = v;
+  };
+  take_max({qd, kvd, kvd}, d);
+  take_max({qd, kvd}, d);
+  take_max({kvd, kvd}, d);
+  take_max({qd}, d);
+  take_max({kvd}, d);
+  take_max({d}, qd);
+  take_max({f, f}, d);
+  take_max({f}, d);
+  take_max({d}, f);
+  const uint64_t att = T * m->attn_chunks * c.head_count * (hd + 2);
+  const uint64_t sizes[] = {T * d, T * d, T * qd, T * kvd, T * kvd, T * qd, T * qd, T * f, T * f, part, att};
+  uint64_t total = 0;
+  for (uint64_t n : sizes) total += (n + 63) / 64 * 64;
+  void* p = nullptr;
+  int32_t rc = charge_alloc(m, "tmp:prefill", total * 4 + T * 4, &p);
+  if (rc) return rc;
+  float* base = static_cast<float*>(p);
+  float** dst[] = {&m->p_h,  &m->p_xn,  &m->p_q,  &m->p_k,    &m->p_v,  &m->p_qr,
+                   &m->p_a,  &m->p_act, &m->p_up, &m->p_part, &m->p_att};
+  for (int i = 0; i < 11; ++i) {
+    *dst[i] = base;
+    base += (sizes[i] + 63) / 64 * 64;
+  }
+  m->p_tok = reinterpret_cast<uint32_t*>(base);
+  m->p_part_floats = part;
+  return RF_OK;
+}
+
+int32_t enqueue_prefill_layer(rf_model* m, size_t li, uint64_t pos0, uint64_t nt) {
+  const rf_model_config& c = m->cfg;
+  Layer& L = m->layers[li];
+  hipStream_t st = m->ctx->compute;
+  const uint64_t d = c.embedding_length, hd = c.head_dim, qd = c.head_count * hd, kvd = c.head_count_kv * hd;
+  const uint64_t f = c.feed_forward_length;
+  const float eps = c.rms_eps;
+  auto mm = [&](const MmSegDesc* segs, int n, uint32_t t, const float* x, uint64_t in, int epi) {
+    return launch_matmul_packed(t, segs, n, x, in, nt, in, epi, m->p_part, m->p_part_floats, st);
+  };
+  // 1. attention RMSNorm, Q/K/V (+ bias), consecutive projections of one type per launch
+  RF_LAUNCH(launch_rmsnorm_rows(m->p_h, static_cast<const float*>(L.attn_norm.d), d, nt, d, eps, m->p_xn, st),
+            "prefill attn norm");
+  const DevTensor* qkv[3] = {&L.q, &L.k, &L.v};
+  const DevTensor* bias[3] = {&L.bq, &L.bk, &L.bv};
+  float* outs[3] = {m->p_q, m->p_k, m->p_v};
+  const uint64_t rows[3] = {qd, kvd, kvd};
+  for (int i = 0; i < 3;) {
+    MmSegDesc segs[3];
+    int n = 0;
+    const uint32_t t = qkv[i]->type;
+    while (i < 3 && qkv[i]->type == t) {
+      const float* b = bias[i]->present() ? static_cast<const float*>(bias[i]->d) : nullptr;
+      segs[n++] = MmSegDesc{qkv[i]->d, qkv[i]->ne1, 0, rows[i], outs[i], nullptr, b, rows[i]};
+      ++i;
+    }
+    RF_LAUNCH(mm(segs, n, t, m->p_xn, d, EPI_STORE), "prefill qkv");
+  }
+  // 2. RoPE of q and k, K/V cache rows pos0 .. pos0 + nt - 1
+  float* kc = m->k_cache + li * m->kv_cap * kvd;
+  float* vc = m->v_cache + li * m->kv_cap * kvd;
+  RF_LAUNCH(launch_rope_kv_rows(m->p_q, m->p_k, m->p_v, m->rope, pos0, nt, (uint32_t)c.head_count,
+                                (uint32_t)c.head_count_kv, (uint32_t)hd, m->p_qr, kc, vc, st),
+            "prefill rope");
+  // 3. attention of every token over positions 0 .. its own
+  AttnArgs a{};
+  a.q = m->p_qr; a.k_hist = kc; a.v_hist = vc; a.out = m->p_a; a.ws = m->p_att;
+  a.hist = (uint32_t)pos0; a.ntok = (uint32_t)nt;
+  a.qh = (uint32_t)c.head_count; a.kvh = (uint32_t)c.head_count_kv; a.hd = (uint32_t)hd;
+  const AttnShape sh = attention_regime_shape(attention_regime(pos0 + nt, a.qh, a.kvh, m->kv_cap), a.qh, a.kvh,
+                                              m->kv_cap);
+  a.per_q = sh.per_q; a.nsplit = sh.nsplit; a.waves = sh.waves;
+  a.denom = sqrtf((float)hd);
+  RF_LAUNCH(launch_attention(a, st), "prefill attention");
+  // 4. o-proj + residual
+  MmSegDesc so{L.o.d, L.o.ne1, 0, d, m->p_h, m->p_h, nullptr, d};
+  RF_LAUNCH(mm(&so, 1, L.o.type, m->p_a, qd, EPI_RESIDUAL), "prefill o-proj");
+  // 5. ffn RMSNorm, gate/up, SiLU(gate) * up
+  RF_LAUNCH(launch_rmsnorm_rows(m->p_h, static_cast<const float*>(L.ffn_norm.d), d, nt, d, eps, m->p_xn, st),
+            "prefill ffn norm");
+  MmSegDesc sg[2] = {MmSegDesc{L.gate.d, L.gate.ne1, 0, f, m->p_act, nullptr, nullptr, f},
+                     MmSegDesc{L.up.d, L.up.ne1, 0, f, m->p_up, nullptr, nullptr, f}};
+  if (L.gate.type == L.up.type) {
+    RF_LAUNCH(mm(sg, 2, L.gate.type, m->p_xn, d, EPI_SWIGLU), "prefill gate/up");
+  } else {
+    RF_LAUNCH(mm(&sg[0], 1, L.gate.type, m->p_xn, d, EPI_STORE), "prefill gate");
+    RF_LAUNCH(mm(&sg[1], 1, L.up.type, m->p_xn, d, EPI_STORE), "prefill up");
+    RF_LAUNCH(launch_binary(BIN_SWIGLU, m->p_act, m->p_up, nt * f, m->p_act, st), "prefill swiglu");
+  }
+  // 6. down + residual
+  MmSegDesc sd{L.down.d, L.down.ne1, 0, d, m->p_h, m->p_h, nullptr, d};
+  RF_LAUNCH(mm(&sd, 1, L.down.type, m->p_act, f, EPI_RESIDUAL), "prefill down");
+  return RF_OK;
+}
+
+int32_t prefill_tokens(rf_model* m, const uint32_t* tokens, uint64_t n) {
+  if (n == 0) return RF_OK;
+  if (m->seq_len + n > m->kv_cap) return set_error(RF_ERR_INVALID, "KV cache full");
+  for (uint64_t i = 0; i < n; ++i)
+    if (tokens[i] >= m->cfg.vocab_size)
+      return set_error(RF_ERR_INVALID, "token_id %u out of bounds for embedding with %llu rows", tokens[i],
+                       (unsigned long long)m->cfg.vocab_size);
+  int32_t rc = check_ready(m);
+  if (rc) return rc;
+  if (!prefill_supported(m)) {
+    for (uint64_t i = 0; i < n; ++i)
+      if ((rc = forward_token(m, tokens[i], m->seq_len))) return rc;
+    return RF_OK;
+  }
+  if ((rc = ensure_prefill_ws(m))) return rc;
+  const rf_model_config& c = m->cfg;
+  hipStream_t st = m->ctx->compute;
+  const uint64_t d = c.embedding_length;
+  const uint32_t nl = (uint32_t)m->layers.size();
+  uint64_t nt = 0;
+  for (uint64_t off = 0; off < n; off += nt) {
+    nt = n - off < MM_MAX_TOKENS ? n - off : MM_MAX_TOKENS;
+    const uint64_t pos0 = m->seq_len;
+    RF_LAUNCH(hipMemcpyAsync(m->p_tok, tokens + off, nt * 4, hipMemcpyHostToDevice, st), "upload prompt tokens");
+    RF_LAUNCH(launch_dequant_rows(m->token_embd.type, m->token_embd.d, d, nt, m->p_h, m->p_tok, c.vocab_size, st),
+              "prefill embedding");
+    for (uint32_t li = 0; li < nl; ++li) {
+      m->cur_layer = li;
+      if (m->streaming) {  // as enqueue_forward: this layer resident, the next one's upload started
+        if ((rc = acquire_layer(m, li, false))) return rc;
+        if (li + 1 < nl && (rc = acquire_layer(m, li + 1, true))) return rc;
+        RF_LAUNCH(hipStreamWaitEvent(st, m->res[li].uploaded, 0), "wait for layer upload");
+      }
+      if ((rc = enqueue_prefill_layer(m, li, pos0, nt))) return rc;
+      if (m->streaming && (rc = settle_layer(m, li))) return rc;
+    }
+    if (m->streaming && (rc = release_retired(m))) return rc;
+    m->seq_len += nt;
+  }
+  // the decode path continues from the last token's hidden state and position
+  RF_LAUNCH(hipMemcpyAsync(m->hidden, m->p_h + (nt - 1) * d, d * 4, hipMemcpyDeviceToDevice, st), "prefill hidden");
+  RF_LAUNCH(launch_set_i32(m->d_pos, (int32_t)m->seq_len, st), "prefill position");
+  return RF_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -1021,6 +1198,27 @@ int32_t rf_model_forward(rf_model* m, uint32_t token, uint64_t pos, float* final
   return sync(m);
 }
 
+int32_t rf_model_prefill(rf_model* m, const uint32_t* tokens, uint64_t n, float* final_hidden) {
+  if (!m || (n && !tokens)) return set_error(RF_ERR_INVALID, "null argument to rf_model_prefill");
+  int32_t rc = prefill_tokens(m, tokens, n);
+  if (rc) return rc;
+  if (final_hidden && m->seq_len > 0) {
+    RF_LAUNCH(launch_rmsnorm(m->hidden, static_cast<const float*>(m->output_norm.d), m->cfg.embedding_length,
+                             m->cfg.rms_eps, m->final_hidden, m->ctx->compute),
+              "output norm");
+    RF_LAUNCH(hipMemcpyAsync(final_hidden, m->final_hidden, m->cfg.embedding_length * 4, hipMemcpyDeviceToHost,
+                             m->ctx->compute),
+              "download hidden");
+  }
+  return sync(m);
+}
+
+int32_t rf_model_set_prefill(rf_model* m, int32_t batched) {
+  if (!m) return set_error(RF_ERR_INVALID, "null model");
+  m->prefill_batched = batched != 0;
+  return RF_OK;
+}
+
 int32_t rf_model_logits(rf_model* m, float* logits) {
   if (!m || !logits) return set_error(RF_ERR_INVALID, "null argument");
   if (m->seq_len == 0) return set_error(RF_ERR_INVALID, "logits requested before any forward pass");
@@ -1040,9 +1238,14 @@ int32_t rf_model_generate(rf_model* m, const uint32_t* prompt, uint64_t plen, ui
   if (plen + max_tokens > ctx_len)
     return set_error(RF_ERR_INVALID, "prompt (%llu tokens) plus max_tokens (%llu) exceeds context length %llu",
                      (unsigned long long)plen, (unsigned long long)max_tokens, (unsigned long long)ctx_len);
-  for (uint64_t p = 0; p < plen; ++p) {
-    int32_t rc = forward_token(m, prompt[p], m->seq_len);
+  if (m->prefill_batched) {
+    int32_t rc = prefill_tokens(m, prompt, plen);
     if (rc) return rc;
+  } else {
+    for (uint64_t p = 0; p < plen; ++p) {
+      int32_t rc = forward_token(m, prompt[p], m->seq_len);
+      if (rc) return rc;
+    }
   }
   uint64_t cur = m->seq_len;
   uint64_t n = 0;

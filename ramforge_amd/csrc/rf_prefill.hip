@@ -1,0 +1,606 @@
+// rf_prefill.hip — batched prompt prefill: the projections of a chunk of
+// prompt tokens as one quantized GEMM on the matrix cores, RMSNorm and RoPE +
+// K/V cache store per token.
+//
+// The reference forwards prompt tokens one at a time (inference.rs:580-592,
+// ModelExecutor::execute_layer per token, model_executor.rs:102-236); this
+// file computes the same per-token arithmetic for up to MM_MAX_TOKENS tokens
+// per launch, so each weight byte is read once per chunk instead of once per
+// token.
+//
+// GEMM (mm_packed): Y[t][r] = sum_k W[r][k] X[t][k] on the packed layout of
+// Q8_0 / Q4_0 / Q4_K / Q6_K (rf_matvec_packed.hip).  Per 32-element step the
+// weight codes are small integers (Q8_0 -128..127, Q4_0 -8..7, Q4_K 0..15,
+// Q6_K -32..31), exact in bf16; x (f32) is split into three bf16 pieces
+// hi + mid + lo that carry its 24-bit significand (|x - hi - mid - lo| <=
+// 2^-26 |x|).  Each product code * piece is exact in f32, so three
+// v_mfma_f32_16x16x32_bf16 give the step's partial dot sum_k q_k x_k at f32
+// accuracy; the block scale is then applied in f32 as the reference applies
+// it per element (quant.rs:977-1327):
+//   Q8_0  d * sum q x                      ((q * d) * x summed, quant.rs:977-1029)
+//   Q4_0  d * sum (q - 8) x                (quant.rs:875-975)
+//   Q4_K  (d*sc) * sum q x - (dmin*m) * sum x   ((d1*q - m1) * x, quant.rs:1085-1137)
+//   Q6_K  (d*sc) * sum q x per 16 elements (quant.rs:1195-1327)
+// Only the summation order differs from the reference's sequential loop.
+//
+// MFMA operand layout (16x16x32, A = x tile, B = weight tile): lane l holds
+// A row (token) l % 16 and B column (weight row) l % 16, elements 8 (l / 16)
+// .. + 7 of the step for both; the result lane l holds D[token 4 (l / 16) + i]
+// [row l % 16], i = 0..3, so every value a lane accumulates belongs to its own
+// weight row and takes that row's scale.
+//
+// Workgroup: 4 wavefronts x 32 rows (two 16-row tiles) x all tokens of the
+// chunk (NTT tiles of 16), over a range of 256-element k slices (split-K).
+// x slices are staged in LDS as f32 (16-byte skew per token row: the 16
+// token rows of an A read fall in distinct banks) and split into bf16 in
+// registers; weights go straight from HBM to registers, a slice ahead of
+// use.  Partial sums of the splits land in a workspace and mm_reduce adds
+// them in a fixed order (deterministic) and applies the epilogue.
+#include "rf_device.h"
+#include "rf_kernels.h"
+
+namespace rf {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr uint32_t MM_ROWS = 128;          // weight rows per workgroup
+constexpr uint32_t MM_KS = 256;            // k elements per staged x slice (8 steps of 32)
+constexpr uint32_t MM_XS = MM_KS + 4;      // LDS floats per token row of a slice
+
+struct MmSeg {
+  const uint8_t* reg[PK_MAX_REGIONS];  // regions at the segment's first row
+  uint32_t rows;                       // rows of the segment
+  uint32_t group_begin;                // first workgroup (blockIdx.x) of the segment
+  uint32_t col;                        // first partial column of the segment
+};
+struct MmArgs {
+  MmSeg seg[3];
+  uint32_t nseg;
+  const float* x;  // [n][ldx]
+  float* part;     // [nsplit][n][mtot]
+  uint32_t n, ldx, in_dim, mtot, nslices, spp;
+};
+
+__device__ __forceinline__ uint32_t mm_byte(uint2 w, int k) { return ((k < 4 ? w.x : w.y) >> (8 * (k & 3))) & 0xFFu; }
+
+__device__ __forceinline__ bf16x8 mm_codes(const float (&v)[8]) {
+  bf16x8 r;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) r[i] = (__bf16)v[i];
+  return r;
+}
+
+// x = hi + mid + lo, each the round-to-nearest bf16 of what remains.
+__device__ __forceinline__ void mm_split3(const float (&x)[8], bf16x8& hi, bf16x8& mid, bf16x8& lo) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const __bf16 a = (__bf16)x[i];
+    const float r1 = x[i] - (float)a;
+    const __bf16 b = (__bf16)r1;
+    const float r2 = r1 - (float)b;
+    hi[i] = a;
+    mid[i] = b;
+    lo[i] = (__bf16)r2;
+  }
+}
+
+__device__ __forceinline__ f32x4 mm_dot3(const bf16x8& hi, const bf16x8& mid, const bf16x8& lo, const bf16x8& w) {
+  f32x4 t = {0.f, 0.f, 0.f, 0.f};
+  t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(hi, w, t, 0, 0, 0);
+  t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(mid, w, t, 0, 0, 0);
+  t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(lo, w, t, 0, 0, 0);
+  return t;
+}
+
+// Per-format weight slice of one lane (row r, element group g) and its decode
+// into the B operand of step j.  `nb` = blocks per row.
+template <uint32_t T> struct MmW;
+
+template <> struct MmW<T_Q8_0> {
+  uint2 c[8];
+  uint32_t sc[8];
+  __device__ void load(const MmSeg& s, uint32_t row, uint32_t sl, uint32_t g, uint32_t nst, uint32_t K) {
+    const uint8_t* cb = s.reg[0] + (size_t)row * K + sl * MM_KS + 8u * g;
+    const uint8_t* sb = s.reg[1] + ((size_t)row * (K / 32u) + sl * 8u) * 2u;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      c[j] = (uint32_t)j < nst ? *reinterpret_cast<const uint2*>(cb + 32 * j) : make_uint2(0, 0);
+      sc[j] = (uint32_t)j < nst ? (uint32_t)rf_ld_u16(sb + 2 * j) : 0u;
+    }
+  }
+  __device__ void step(int j, uint32_t, bf16x8& b, float& d) const {
+    float v[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) v[k] = (float)(int)(int8_t)mm_byte(c[j], k);
+    b = mm_codes(v);
+    d = rf_half_to_float_fast(sc[j]);
+  }
+};
+
+template <> struct MmW<T_Q4_0> {
+  uint2 c[8];
+  uint32_t sc[8];
+  __device__ void load(const MmSeg& s, uint32_t row, uint32_t sl, uint32_t g, uint32_t nst, uint32_t K) {
+    const size_t blk = (size_t)row * (K / 32u) + sl * 8u;
+    const uint8_t* cb = s.reg[0] + blk * 16u + 8u * (g & 1u);
+    const uint8_t* sb = s.reg[1] + blk * 2u;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      c[j] = (uint32_t)j < nst ? *reinterpret_cast<const uint2*>(cb + 16 * j) : make_uint2(0, 0);
+      sc[j] = (uint32_t)j < nst ? (uint32_t)rf_ld_u16(sb + 2 * j) : 0u;
+    }
+  }
+  // elements 8g..8g+7 of a block: low nibbles of bytes 0-7 / 8-15 (g = 0, 1),
+  // high nibbles of the same bytes (g = 2, 3): value nibble - 8
+  __device__ void step(int j, uint32_t g, bf16x8& b, float& d) const {
+    const int sh = 4 * (int)(g >> 1);
+    float v[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) v[k] = (float)((int)((mm_byte(c[j], k) >> sh) & 15u) - 8);
+    b = mm_codes(v);
+    d = rf_half_to_float_fast(sc[j]);
+  }
+};
+
+template <> struct MmW<T_Q4_K> {
+  uint2 c[4];  // qs bytes 32i + 8g .. + 7: steps 2i (low nibbles) and 2i + 1 (high)
+  uint4 h;     // d | dmin << 16, scale bytes 0-3, 4-7, 8-11
+  __device__ void load(const MmSeg& s, uint32_t row, uint32_t sl, uint32_t g, uint32_t, uint32_t K) {
+    const size_t blk = (size_t)row * (K / 256u) + sl;
+    const uint8_t* cb = s.reg[0] + blk * 128u + 8u * g;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) c[i] = *reinterpret_cast<const uint2*>(cb + 32 * i);
+    h = *reinterpret_cast<const uint4*>(s.reg[1] + blk * 16u);
+  }
+  __device__ uint32_t sbyte(uint32_t i) const {
+    const uint32_t w = i < 4 ? h.y : (i < 8 ? h.z : h.w);
+    return (w >> (8 * (i & 3u))) & 0xFFu;
+  }
+  // get_scale_min (quant.rs:216-226) of sub-block j
+  __device__ void step(int j, uint32_t, bf16x8& b, float& d1, float& m1) const {
+    const int sh = 4 * (j & 1);
+    float v[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) v[k] = (float)((mm_byte(c[j >> 1], k) >> sh) & 15u);
+    b = mm_codes(v);
+    uint32_t sc, m;
+    const uint32_t ju = (uint32_t)j;
+    if (ju < 4) {
+      sc = sbyte(ju) & 63u;
+      m = sbyte(ju + 4) & 63u;
+    } else {
+      sc = (sbyte(ju + 4) & 0xFu) | ((sbyte(ju - 4) >> 6) << 4);
+      m = (sbyte(ju + 4) >> 4) | ((sbyte(ju) >> 6) << 4);
+    }
+    const float d = rf_half_to_float_fast(h.x & 0xFFFFu), dmin = rf_half_to_float_fast(h.x >> 16);
+    d1 = d * (float)sc;
+    m1 = dmin * (float)m;
+  }
+};
+
+template <> struct MmW<T_Q6_K> {
+  uint2 ql[4];  // [2h + p]: ql bytes 64h + 32p + 8g .. + 7
+  uint2 qh[2];  // [h]: qh bytes 32h + 8g .. + 7
+  uint4 sc;     // 16 int8 scales
+  uint32_t d;
+  __device__ void load(const MmSeg& s, uint32_t row, uint32_t sl, uint32_t g, uint32_t, uint32_t K) {
+    const size_t blk = (size_t)row * (K / 256u) + sl;
+    const uint8_t* lb = s.reg[0] + blk * 128u + 8u * g;
+    const uint8_t* hb = s.reg[1] + blk * 64u + 8u * g;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ql[i] = *reinterpret_cast<const uint2*>(lb + 64 * (i >> 1) + 32 * (i & 1));
+#pragma unroll
+    for (int i = 0; i < 2; ++i) qh[i] = *reinterpret_cast<const uint2*>(hb + 32 * i);
+    sc = *reinterpret_cast<const uint4*>(s.reg[2] + blk * 16u);
+    d = rf_ld_u16(s.reg[3] + blk * 2u);
+  }
+  __device__ float scale(uint32_t i) const {
+    const uint32_t w = i < 4 ? sc.x : (i < 8 ? sc.y : (i < 12 ? sc.z : sc.w));
+    return (float)(int)(int8_t)((w >> (8 * (i & 3u))) & 0xFFu);
+  }
+  // Step j = 4h + qq covers elements 128h + 32qq + l, l = 0..31 (quant.rs:376-406):
+  // q = (ql nibble qq / 2 of byte 64h + 32 (qq & 1) + l) | (qh bits 2qq of byte 32h + l) << 4, minus 32.
+  // Elements l < 16 (groups 0, 1) take scale 8h + 2qq, the rest 8h + 2qq + 1:
+  // b0 holds groups 0-1 (zeros in 2-3), b1 groups 2-3.
+  __device__ void step(int j, uint32_t g, bf16x8& b0, bf16x8& b1, float& d0, float& d1) const {
+    const int hh = j >> 2, qq = j & 3;
+    const uint2 l = ql[2 * hh + (qq & 1)], hi = qh[hh];
+    const int lsh = 4 * (qq >> 1), hsh = 2 * qq;
+    const bool first = g < 2u;
+    float v0[8], v1[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int q = (int)(((mm_byte(l, k) >> lsh) & 15u) | (((mm_byte(hi, k) >> hsh) & 3u) << 4)) - 32;
+      v0[k] = first ? (float)q : 0.f;
+      v1[k] = first ? 0.f : (float)q;
+    }
+    b0 = mm_codes(v0);
+    b1 = mm_codes(v1);
+    const float dd = rf_half_to_float_fast(d);
+    d0 = dd * scale(8u * hh + 2u * qq);
+    d1 = dd * scale(8u * hh + 2u * qq + 1u);
+  }
+};
+
+template <uint32_t T, int NTT>
+__global__ __launch_bounds__(256) void mm_packed(MmArgs a) {
+  extern __shared__ __align__(16) float xs[];  // [NTT * 16][MM_XS], then Q4_K step sums [8][NTT * 16]
+  constexpr uint32_t NT = NTT * 16;
+  float* ss = xs + NT * MM_XS;
+  const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+  const uint32_t r16 = lane & 15u, g = lane >> 4;
+  MmSeg s = a.seg[0];
+  if (a.nseg > 1 && blockIdx.x >= a.seg[1].group_begin) s = a.seg[1];
+  if (a.nseg > 2 && blockIdx.x >= a.seg[2].group_begin) s = a.seg[2];
+  const uint32_t row_base = (blockIdx.x - s.group_begin) * MM_ROWS + wave * 32u;
+  uint32_t rowc[2];
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt) rowc[rt] = min(row_base + 16u * rt + r16, s.rows - 1u);  // loads stay in bounds
+  const uint32_t K = a.in_dim, n = a.n;
+  const uint32_t sl0 = blockIdx.y * a.spp, sl1 = min(a.nslices, sl0 + a.spp);
+
+  f32x4 acc[2][NTT];
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+    for (int nt = 0; nt < NTT; ++nt) acc[rt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  MmW<T> w[2];
+  {
+    const uint32_t nst = min(8u, (K - sl0 * MM_KS) / 32u);
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) w[rt].load(s, rowc[rt], sl0, g, nst, K);
+  }
+  for (uint32_t sl = sl0; sl < sl1; ++sl) {
+    const uint32_t nst = min(8u, (K - sl * MM_KS) / 32u);
+    __syncthreads();  // the previous slice's x reads are done
+    // stage x[0..NT)[slice] (zeros past n and past K)
+#pragma unroll
+    for (uint32_t u = 0; u < NT / 4u; ++u) {
+      const uint32_t i = tid + 256u * u, t = i >> 6, c4 = i & 63u, k = sl * MM_KS + 4u * c4;
+      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (t < n && k < K) v = *reinterpret_cast<const float4*>(a.x + (size_t)t * a.ldx + k);
+      *reinterpret_cast<float4*>(&xs[t * MM_XS + 4u * c4]) = v;
+    }
+    if constexpr (T == T_Q4_K) {
+      __syncthreads();
+      for (uint32_t e = tid; e < 8u * NT; e += 256u) {
+        const uint32_t j = e / NT, t = e % NT;
+        const float* p = &xs[t * MM_XS + 32u * j];
+        float sum = 0.f;
+        for (int i = 0; i < 32; ++i) sum += p[i];
+        ss[j * NT + t] = sum;
+      }
+    }
+    __syncthreads();
+    MmW<T> cur[2] = {w[0], w[1]};
+    if (sl + 1 < sl1) {  // next slice's weights in flight during this slice's math
+      const uint32_t nn = min(8u, (K - (sl + 1) * MM_KS) / 32u);
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt) w[rt].load(s, rowc[rt], sl + 1, g, nn, K);
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      if ((uint32_t)j >= nst) break;
+      bf16x8 b[2], b2[2];
+      float d[2], e[2];
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt) {
+        if constexpr (T == T_Q4_K) cur[rt].step(j, g, b[rt], d[rt], e[rt]);
+        else if constexpr (T == T_Q6_K) cur[rt].step(j, g, b[rt], b2[rt], d[rt], e[rt]);
+        else cur[rt].step(j, g, b[rt], d[rt]);
+      }
+#pragma unroll
+      for (int nt = 0; nt < NTT; ++nt) {
+        const float* xp = &xs[(nt * 16u + r16) * MM_XS + 32u * j + 8u * g];
+        const float4 x0 = *reinterpret_cast<const float4*>(xp);
+        const float4 x1 = *reinterpret_cast<const float4*>(xp + 4);
+        const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+        bf16x8 hi, mid, lo;
+        mm_split3(xv, hi, mid, lo);
+        float4 sx = make_float4(0.f, 0.f, 0.f, 0.f);
+        if constexpr (T == T_Q4_K) sx = *reinterpret_cast<const float4*>(&ss[j * NT + nt * 16u + 4u * g]);
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt) {
+          const f32x4 t0 = mm_dot3(hi, mid, lo, b[rt]);
+          f32x4& c = acc[rt][nt];
+          if constexpr (T == T_Q6_K) {
+            const f32x4 t1 = mm_dot3(hi, mid, lo, b2[rt]);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) c[i] = fmaf(e[rt], t1[i], fmaf(d[rt], t0[i], c[i]));
+          } else if constexpr (T == T_Q4_K) {
+            const float sxa[4] = {sx.x, sx.y, sx.z, sx.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) c[i] = fmaf(-e[rt], sxa[i], fmaf(d[rt], t0[i], c[i]));
+          } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) c[i] = fmaf(d[rt], t0[i], c[i]);
+          }
+        }
+      }
+    }
+  }
+  float* out = a.part + (size_t)blockIdx.y * n * a.mtot + s.col;
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt) {
+    const uint32_t r = row_base + 16u * rt + r16;
+    if (r >= s.rows) continue;
+#pragma unroll
+    for (int nt = 0; nt < NTT; ++nt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t t = nt * 16u + 4u * g + i;
+        if (t < n) out[(size_t)t * a.mtot + r] = acc[rt][nt][i];
+      }
+  }
+}
+
+// Sum of the split partials in split order, then the epilogue:
+//   EPI_STORE     y = v (+ bias: the reference adds it after the matvec)
+//   EPI_RESIDUAL  y = res + v
+//   EPI_SWIGLU    y = silu(v_gate) * v_up  (segment 0 gate, segment 1 up)
+struct MmRedSeg {
+  float* y;
+  const float* res;
+  const float* bias;
+  uint32_t rows, col, ld;
+};
+struct MmRedArgs {
+  MmRedSeg seg[3];
+  uint32_t nseg, nsplit, n, mtot, mcols;
+  int epi;
+  const float* part;
+};
+
+__global__ __launch_bounds__(256) void mm_reduce(MmRedArgs a) {
+  const uint64_t e = (uint64_t)blockIdx.x * 256u + threadIdx.x;
+  if (e >= (uint64_t)a.n * a.mcols) return;
+  const uint32_t t = (uint32_t)(e / a.mcols), c = (uint32_t)(e % a.mcols);
+  MmRedSeg s = a.seg[0];
+  if (a.nseg > 1 && c >= a.seg[1].col) s = a.seg[1];
+  if (a.nseg > 2 && c >= a.seg[2].col) s = a.seg[2];
+  const uint32_t r = c - s.col;
+  const size_t stride = (size_t)a.n * a.mtot;
+  const float* p = a.part + (size_t)t * a.mtot + c;
+  float v = p[0];
+  for (uint32_t k = 1; k < a.nsplit; ++k) v += p[k * stride];
+  const size_t o = (size_t)t * s.ld + r;
+  if (a.epi == EPI_RESIDUAL) {
+    s.y[o] = s.res[o] + v;
+  } else if (a.epi == EPI_SWIGLU) {
+    const float* pu = a.part + (size_t)t * a.mtot + a.seg[1].col + r;
+    float u = pu[0];
+    for (uint32_t k = 1; k < a.nsplit; ++k) u += pu[k * stride];
+    s.y[o] = v / (1.0f + expf(-v)) * u;  // silu_reference * up (compute.rs:337-361)
+  } else {
+    s.y[o] = s.bias ? v + s.bias[r] : v;
+  }
+}
+
+// ------------------------------------------------------------------ host side
+
+static uint32_t mm_cu_count() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cached[dev]) {
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v < 1) v = 256;
+    cached[dev] = v;
+  }
+  return (uint32_t)cached[dev];
+}
+
+bool mm_supported(uint32_t t, uint64_t in_dim) {
+  if (!packed_type(t) || in_dim == 0 || in_dim > (1u << 24)) return false;
+  const uint64_t qk = (t == T_Q4_K || t == T_Q6_K) ? 256 : 32;
+  return in_dim % qk == 0;
+}
+
+// Split-K shape: about two workgroups per CU, whole slices per split.
+static void mm_shape(uint64_t groups, uint64_t in_dim, uint32_t* nsplit, uint32_t* spp, uint32_t* nslices) {
+  const uint64_t ns = (in_dim + MM_KS - 1) / MM_KS;
+  const uint64_t target = 2ull * mm_cu_count();
+  uint64_t sp = (target + groups - 1) / groups;
+  if (sp < 1) sp = 1;
+  if (sp > ns) sp = ns;
+  const uint64_t per = (ns + sp - 1) / sp;
+  *spp = (uint32_t)per;
+  *nsplit = (uint32_t)((ns + per - 1) / per);
+  *nslices = (uint32_t)ns;
+}
+
+static uint64_t mm_groups(const MmSegDesc* segs, int nseg) {
+  uint64_t g = 0;
+  for (int i = 0; i < nseg; ++i) g += (segs[i].rows + MM_ROWS - 1) / MM_ROWS;
+  return g;
+}
+
+uint64_t mm_part_floats(const uint64_t* rows, int nseg, uint64_t in_dim, uint64_t n) {
+  MmSegDesc d[3] = {};
+  uint64_t mtot = 0;
+  for (int i = 0; i < nseg && i < 3; ++i) {
+    d[i].rows = rows[i];
+    mtot += rows[i];
+  }
+  uint32_t nsplit, spp, ns;
+  mm_shape(mm_groups(d, nseg), in_dim, &nsplit, &spp, &ns);
+  return (uint64_t)nsplit * n * mtot;
+}
+
+static int mm_ntt(uint64_t n) { return (int)((n + 15) / 16); }
+
+template <uint32_t T, int NTT>
+static hipError_t mm_launch_t(const MmArgs& a, dim3 grid, hipStream_t st) {
+  const uint32_t lds = (NTT * 16u * MM_XS + (T == T_Q4_K ? 8u * NTT * 16u : 0u)) * 4u;
+  static bool opened = false;
+  if (!opened) {
+    if (lds > 65536) {
+      hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(mm_packed<T, NTT>),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+      if (e != hipSuccess) return e;
+    }
+    opened = true;
+  }
+  hipLaunchKernelGGL((mm_packed<T, NTT>), grid, dim3(256), lds, st, a);
+  return hipGetLastError();
+}
+
+template <uint32_t T>
+static hipError_t mm_launch_ntt(const MmArgs& a, dim3 grid, int ntt, hipStream_t st) {
+  switch (ntt) {
+    case 1: return mm_launch_t<T, 1>(a, grid, st);
+    case 2: return mm_launch_t<T, 2>(a, grid, st);
+    case 3: return mm_launch_t<T, 3>(a, grid, st);
+    case 4: return mm_launch_t<T, 4>(a, grid, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+static bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+hipError_t launch_matmul_packed(uint32_t t, const MmSegDesc* segs, int nseg, const float* x, uint64_t ldx,
+                                uint64_t n, uint64_t in_dim, int epi, float* part, uint64_t part_floats,
+                                hipStream_t st) {
+  if (!mm_supported(t, in_dim) || nseg < 1 || nseg > 3 || n == 0 || n > MM_MAX_TOKENS) return hipErrorInvalidValue;
+  if (!al16(x) || ldx % 4 != 0 || ldx < in_dim || !part) return hipErrorInvalidValue;
+  if (epi == EPI_SWIGLU && (nseg != 2 || segs[0].rows != segs[1].rows)) return hipErrorInvalidValue;
+  const int nreg = t == T_Q6_K ? 4 : 2;
+  auto row_bytes = [&](int k) -> uint64_t {
+    switch (t) {
+      case T_Q8_0: return k == 0 ? in_dim : in_dim / 32 * 2;
+      case T_Q4_0: return k == 0 ? in_dim / 2 : in_dim / 32 * 2;
+      case T_Q4_K: return k == 0 ? in_dim / 2 : in_dim / 256 * 16;
+      default: return k == 0 ? in_dim / 2 : k == 1 ? in_dim / 4 : k == 2 ? in_dim / 256 * 16 : in_dim / 256 * 2;
+    }
+  };
+  MmArgs a{};
+  MmRedArgs r{};
+  uint64_t mtot = 0, groups = 0;
+  for (int i = 0; i < nseg; ++i) {
+    const MmSegDesc& d = segs[i];
+    if (d.rows == 0 || d.row_start + d.rows > d.matrix_rows || !d.packed || !d.y) return hipErrorInvalidValue;
+    uint64_t off = 0;
+    for (int k = 0; k < nreg; ++k) {
+      const uint64_t rb = row_bytes(k);
+      a.seg[i].reg[k] = static_cast<const uint8_t*>(d.packed) + off + d.row_start * rb;
+      off += d.matrix_rows * rb;
+    }
+    // 8-byte code loads; Q4_K headers and Q6_K scales as 16 bytes
+    if ((reinterpret_cast<uintptr_t>(a.seg[i].reg[0]) & 7u) != 0) return hipErrorInvalidValue;
+    if (t == T_Q4_K && !al16(a.seg[i].reg[1])) return hipErrorInvalidValue;
+    if (t == T_Q6_K && (((reinterpret_cast<uintptr_t>(a.seg[i].reg[1]) & 7u) != 0) || !al16(a.seg[i].reg[2])))
+      return hipErrorInvalidValue;
+    a.seg[i].rows = (uint32_t)d.rows;
+    a.seg[i].group_begin = (uint32_t)groups;
+    a.seg[i].col = (uint32_t)mtot;
+    r.seg[i] = MmRedSeg{d.y, d.res, d.bias, (uint32_t)d.rows, (uint32_t)mtot, (uint32_t)d.ld};
+    if (epi == EPI_RESIDUAL && !d.res) return hipErrorInvalidValue;
+    groups += (d.rows + MM_ROWS - 1) / MM_ROWS;
+    mtot += d.rows;
+  }
+  if (mtot > 0xFFFFFFFFull || groups > 0x7FFFFFFFull) return hipErrorInvalidValue;
+  uint32_t nsplit, spp, nslices;
+  mm_shape(groups, in_dim, &nsplit, &spp, &nslices);
+  if ((uint64_t)nsplit * n * mtot > part_floats) return hipErrorInvalidValue;
+  a.nseg = (uint32_t)nseg;
+  a.x = x;
+  a.part = part;
+  a.n = (uint32_t)n;
+  a.ldx = (uint32_t)ldx;
+  a.in_dim = (uint32_t)in_dim;
+  a.mtot = (uint32_t)mtot;
+  a.nslices = nslices;
+  a.spp = spp;
+  const dim3 grid((uint32_t)groups, nsplit);
+  const int ntt = mm_ntt(n);
+  hipError_t e;
+  switch (t) {
+    case T_Q8_0: e = mm_launch_ntt<T_Q8_0>(a, grid, ntt, st); break;
+    case T_Q4_0: e = mm_launch_ntt<T_Q4_0>(a, grid, ntt, st); break;
+    case T_Q4_K: e = mm_launch_ntt<T_Q4_K>(a, grid, ntt, st); break;
+    default: e = mm_launch_ntt<T_Q6_K>(a, grid, ntt, st); break;
+  }
+  if (e != hipSuccess) return e;
+  r.nseg = (uint32_t)nseg;
+  r.nsplit = nsplit;
+  r.n = (uint32_t)n;
+  r.mtot = (uint32_t)mtot;
+  r.mcols = epi == EPI_SWIGLU ? (uint32_t)segs[0].rows : (uint32_t)mtot;
+  r.epi = epi;
+  r.part = part;
+  const uint64_t total = (uint64_t)n * r.mcols;
+  hipLaunchKernelGGL(mm_reduce, dim3((uint32_t)((total + 255) / 256)), dim3(256), 0, st, r);
+  return hipGetLastError();
+}
+
+// ------------------------------------------------------- per-token glue
+
+// RMSNorm of `rows` rows of length n (stride ld), x / rms * w as
+// rms_norm_reference (compute.rs:291-319); one workgroup per row.
+__global__ __launch_bounds__(256) void rmsnorm_rows_kernel(const float* __restrict__ x, const float* __restrict__ w,
+                                                           uint32_t n, uint32_t ld, float eps,
+                                                           float* __restrict__ y) {
+  __shared__ float part[4];
+  const uint32_t tid = threadIdx.x;
+  const float* xr = x + (size_t)blockIdx.x * ld;
+  float* yr = y + (size_t)blockIdx.x * ld;
+  float ss = 0.f;
+  for (uint32_t i = tid; i < n; i += 256u) ss = fmaf(xr[i], xr[i], ss);
+  ss = rf_wave_sum(ss);
+  if ((tid & 63u) == 0) part[tid >> 6] = ss;
+  __syncthreads();
+  const float tot = part[0] + part[1] + part[2] + part[3];
+  const float rms = sqrtf(tot / (float)n + eps);
+  for (uint32_t i = tid; i < n; i += 256u) yr[i] = xr[i] / rms * w[i];
+}
+
+hipError_t launch_rmsnorm_rows(const float* x, const float* w, uint64_t n, uint64_t rows, uint64_t ld, float eps,
+                               float* y, hipStream_t st) {
+  if (rows == 0) return hipSuccess;
+  hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3((uint32_t)rows), dim3(256), 0, st, x, w, (uint32_t)n, (uint32_t)ld,
+                     eps, y);
+  return hipGetLastError();
+}
+
+// Token z at position pos0 + z: q heads rotated into qr[z], k heads rotated
+// into the K cache row, v copied into the V cache row (rope_reference,
+// compute.rs:389-456, with the host cos/sin table; the rotation is written in
+// the same operation order as the decode attention kernel's).
+__global__ __launch_bounds__(256) void rope_kv_rows_kernel(const float* __restrict__ q, const float* __restrict__ k,
+                                                           const float* __restrict__ v, const float* __restrict__ rope,
+                                                           uint32_t pos0, uint32_t qh, uint32_t kvh, uint32_t hd,
+                                                           float* __restrict__ qr, float* __restrict__ kc,
+                                                           float* __restrict__ vc) {
+  const uint32_t z = blockIdx.x, pos = pos0 + z, half = hd >> 1;
+  const uint32_t qd = qh * hd, kvd = kvh * hd;
+  const float* cs = rope + (size_t)pos * hd;
+  for (uint32_t e = threadIdx.x; e < qd + 2 * kvd; e += 256u) {
+    if (e >= qd + kvd) {
+      const uint32_t i = e - qd - kvd;
+      vc[(size_t)pos * kvd + i] = v[(size_t)z * kvd + i];
+      continue;
+    }
+    const bool isq = e < qd;
+    const uint32_t i = isq ? e : e - qd, d = i % hd, base = i - d;
+    const float* src = isq ? q + (size_t)z * qd + base : k + (size_t)z * kvd + base;
+    const uint32_t ci = d < half ? d : d - half;
+    const float va = src[d], vp = src[d < half ? d + half : d - half];
+    const float c0 = cs[2 * ci], c1 = cs[2 * ci + 1];
+    const float rot = d < half ? va * c0 - vp * c1 : vp * c1 + va * c0;
+    if (isq) qr[(size_t)z * qd + i] = rot;
+    else kc[(size_t)pos * kvd + i] = rot;
+  }
+}
+
+hipError_t launch_rope_kv_rows(const float* q, const float* k, const float* v, const float* rope, uint64_t pos0,
+                               uint64_t ntok, uint32_t qh, uint32_t kvh, uint32_t hd, float* qr, float* kc,
+                               float* vc, hipStream_t st) {
+  if (ntok == 0) return hipSuccess;
+  hipLaunchKernelGGL(rope_kv_rows_kernel, dim3((uint32_t)ntok), dim3(256), 0, st, q, k, v, rope, (uint32_t)pos0, qh,
+                     kvh, hd, qr, kc, vc);
+  return hipGetLastError();
+}
+
+}  // namespace rf

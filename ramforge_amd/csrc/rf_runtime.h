@@ -52,7 +52,7 @@ struct rf_ctx {
   rf::Ledger ledger{0};
   std::mutex mu;
   std::map<std::string, void*> buffers;  // charge name -> device pointer
-  rf::Workspace attn_ws, scratch_ws;
+  rf::Workspace attn_ws, scratch_ws, mm_ws;
   float* amax_val = nullptr;
   uint32_t* amax_idx = nullptr;
   void* pinned_stage[2] = {nullptr, nullptr};

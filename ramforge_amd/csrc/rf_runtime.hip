@@ -559,6 +559,52 @@ int32_t rf_matvec_packed(rf_ctx* ctx, uint32_t t, const void* packed, uint64_t p
   return RF_OK;
 }
 
+int32_t rf_matmul_packed(rf_ctx* ctx, uint32_t t, const void* packed, uint64_t packed_bytes, uint64_t out_dim,
+                         uint64_t in_dim, const float* x, uint64_t n_tokens, float* y, rf_stream_t s) {
+  RF_CHECK_CTX(ctx);
+  if (!packed_type(t))
+    return set_error(RF_ERR_UNSUPPORTED, "packed matmul does not support tensor type %s (%u)", type_name(t), t);
+  const char* nm = type_name(t);
+  if (!packed || !x || !y) return set_error(RF_ERR_INVALID, "%s matmul received a null pointer", nm);
+  uint64_t qk = 0, bs = 0;
+  type_geometry(t, &qk, &bs);
+  if (in_dim == 0 || in_dim % qk != 0)
+    return set_error(RF_ERR_INVALID, "%s row size %llu not divisible by block size %llu", nm,
+                     (unsigned long long)in_dim, (unsigned long long)qk);
+  if (out_dim == 0 || n_tokens == 0) return RF_OK;
+  const uint64_t need = out_dim * (in_dim / qk * bs);
+  if (packed_bytes < need)
+    return set_error(RF_ERR_INVALID, "%s tensor truncated: %llu bytes for %llu rows of %llu (need %llu)", nm,
+                     (unsigned long long)packed_bytes, (unsigned long long)out_dim, (unsigned long long)in_dim,
+                     (unsigned long long)need);
+  if (!mm_supported(t, in_dim) || out_dim > 0xFFFFFFFFull)
+    return set_error(RF_ERR_UNSUPPORTED, "packed %s matmul does not cover %llu x %llu", nm,
+                     (unsigned long long)out_dim, (unsigned long long)in_dim);
+  hipStream_t st = pick_stream(ctx, s);
+  const uint64_t chunk = n_tokens < MM_MAX_TOKENS ? n_tokens : MM_MAX_TOKENS;
+  const uint64_t part = mm_part_floats(&out_dim, 1, in_dim, chunk);
+  int32_t rc = ensure_workspace(ctx, ctx->mm_ws, "workspace:matmul", part * 4);
+  if (rc) return rc;
+  const bool aligned = (reinterpret_cast<uintptr_t>(x) & 15u) == 0 && in_dim % 4 == 0;
+  if (!aligned) {  // the kernel stages x with 16-byte loads
+    rc = ensure_workspace(ctx, ctx->scratch_ws, "workspace:scratch", chunk * in_dim * 4);
+    if (rc) return rc;
+  }
+  for (uint64_t off = 0; off < n_tokens; off += MM_MAX_TOKENS) {
+    const uint64_t nt = n_tokens - off < MM_MAX_TOKENS ? n_tokens - off : MM_MAX_TOKENS;
+    const float* xc = x + off * in_dim;
+    if (!aligned) {
+      RF_HIP(hipMemcpyAsync(ctx->scratch_ws.ptr, xc, nt * in_dim * 4, hipMemcpyDeviceToDevice, st), "hipMemcpyAsync");
+      xc = static_cast<const float*>(ctx->scratch_ws.ptr);
+    }
+    MmSegDesc seg{packed, out_dim, 0, out_dim, y + off * out_dim, nullptr, nullptr, out_dim};
+    hipError_t e = launch_matmul_packed(t, &seg, 1, xc, in_dim, nt, in_dim, EPI_STORE,
+                                        static_cast<float*>(ctx->mm_ws.ptr), ctx->mm_ws.bytes / 4, st);
+    if (e != hipSuccess) return hip_error(e, "packed matmul launch");
+  }
+  return RF_OK;
+}
+
 int32_t rf_dequantize_rows(rf_ctx* ctx, uint32_t t, const void* w, uint64_t w_bytes, uint64_t in_dim,
                            uint64_t row_start, uint64_t row_count, float* out, rf_stream_t s) {
   RF_CHECK_CTX(ctx);

@@ -105,3 +105,17 @@ def assert_close_scaled(y, ref, scale, tol: float = 1e-4, what: str = ""):
     e = scaled_err(y, ref, scale)
     assert e <= tol, f"{what}: max scaled relative error {e:.3e} > {tol:.1e}"
     return e
+
+
+# Byte ranges of a GGUF block that form the packed layout's regions, in region
+# order (the layout documented in include/ramforge_hip.h).
+PACK_REGIONS = {Q8_0: [(2, 34), (0, 2)], Q4_0: [(2, 18), (0, 2)], Q4_K: [(16, 144), (0, 16)],
+                Q6_K: [(0, 128), (128, 192), (192, 208), (208, 210)]}
+
+
+def pack_host(t: int, raw: np.ndarray, rows: int, in_dim: int) -> np.ndarray:
+    """Packed layout built on the host from the GGUF bytes: each region (a
+    byte range of every block) for all blocks of all rows, one after another."""
+    qk, bs = GEOM[t]
+    blocks = raw.reshape(rows * in_dim // qk, bs)
+    return np.concatenate([blocks[:, a:b].reshape(-1) for a, b in PACK_REGIONS[t]])

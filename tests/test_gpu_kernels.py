@@ -9,7 +9,8 @@ import numpy as np
 import pytest
 
 from helpers import (F32, Q2_K, Q3_K, Q4_0, Q4_K, Q5_0, Q5_K, Q6_K, Q8_0, Q8_K, QUANT_TYPES, GEOM, NAMES,
-                     assert_close, assert_close_scaled, random_matrix, rel_err, scaled_err)
+                     PACK_REGIONS, assert_close, assert_close_scaled, pack_host, random_matrix, rel_err,
+                     scaled_err)
 
 pytestmark = pytest.mark.gpu
 TOL = 1e-4
@@ -157,19 +158,8 @@ def test_matvec_unaligned_pointers(ctx, orc, t, kernel_mode):
     _check_matvec(ctx, orc, t, 70, 512, 370 + t, x_off=8, w_off=6, row_start=5, row_count=40)
 
 
-# Byte ranges of a GGUF block that form the packed layout's regions, in region
-# order (the layout documented in include/ramforge_hip.h).
-PACK_REGIONS = {Q8_0: [(2, 34), (0, 2)], Q4_0: [(2, 18), (0, 2)], Q4_K: [(16, 144), (0, 16)],
-                Q6_K: [(0, 128), (128, 192), (192, 208), (208, 210)]}
 PACKED = [Q8_0, Q4_0, Q4_K, Q6_K]
-
-
-def _pack_host(t, raw, rows, in_dim):
-    """Packed layout built on the host from the GGUF bytes: each region (a
-    byte range of every block) for all blocks of all rows, one after another."""
-    qk, bs = GEOM[t]
-    blocks = raw.reshape(rows * in_dim // qk, bs)
-    return np.concatenate([blocks[:, a:b].reshape(-1) for a, b in PACK_REGIONS[t]])
+_pack_host = pack_host
 
 
 @pytest.mark.parametrize("t", PACKED)
