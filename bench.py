@@ -5,7 +5,10 @@ Workload (BASELINE.json metric): random-init Llama-3-8B-shape model (32
 layers, d 4096, 32/8 heads, FFN 14336, vocab 128256), Q8_0 weights resident in
 HBM, greedy decode.  One step = one token: output norm + logits matvec,
 on-device argmax, embedding of the chosen token, 32 transformer layers.  The
-prompt (32 random token ids) is forwarded before the timed region.
+prompt (32 random token ids) is forwarded before the timed region (batched,
+rf_model_prefill).  Also measured, outside the decode line's value: the
+prompt forwarded token by token (the reference's loop) against the batched
+prefill, and a 512-token batched prompt.
 
 Prints one JSON line with the decode tok/s, the roofline of the dominant
 kernel (ffn RMSNorm + gate/up Q8_0 matvec + SiLU*up, timed with HIP events on
@@ -27,6 +30,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 PEAK_HBM_GBS = 8000.0
+PEAK_BF16_TFLOPS = 2500.0  # dense bf16 MFMA
 METRIC = "decode tok/s (8B-shape Q8_0, 1 GPU); matvec achieved HBM GB/s vs peak"
 
 
@@ -291,6 +295,50 @@ def config5_bench(rf, syn, tokens: int, prompt_len: int, policy: int) -> dict:
     return out
 
 
+def prefill_bench(ctx, m, cfg, rf, prompt, long_len: int) -> dict:
+    """Prompt forwarding on the resident 8B-shape model: the reference's loop
+    (one forward per token, inference.rs:580-592) against rf_model_prefill
+    (64-token chunks, projections as packed-weight GEMMs on the matrix cores),
+    and a long batched prompt.  Untimed warmup prefill first (workspace, LDS
+    attributes)."""
+    import numpy as np
+
+    m.reset()
+    t0 = time.perf_counter()
+    for p, t in enumerate(prompt):
+        m.forward(t, p)
+    tbt = time.perf_counter() - t0
+    m.reset()
+    m.prefill(prompt[:8])
+    m.reset()
+    t0 = time.perf_counter()
+    m.prefill(prompt)
+    batched = time.perf_counter() - t0
+    m.reset()
+    lp = [int(t) for t in np.random.default_rng(12).integers(0, cfg["vocab_size"], long_len)]
+    t0 = time.perf_counter()
+    m.prefill(lp)
+    long_s = time.perf_counter() - t0
+    m.reset()
+    d, f = cfg["embedding_length"], cfg["feed_forward_length"]
+    qd = cfg["head_count"] * cfg["head_dim"]
+    kvd = cfg["head_count_kv"] * cfg["head_dim"]
+    params = cfg["block_count"] * (d * (qd + 2 * kvd) + qd * d + 2 * d * f + f * d)
+    chunks = -(-long_len // 64)
+    useful = 2.0 * long_len * params / long_s / 1e12
+    out = {"prompt_tokens": len(prompt), "token_by_token_ms": round(tbt * 1e3, 2),
+           "batched_ms": round(batched * 1e3, 2), "speedup": round(tbt / batched, 1),
+           "long_prompt_tokens": long_len, "long_batched_ms": round(long_s * 1e3, 2),
+           "long_tok_s": round(long_len / long_s, 1),
+           "long_useful_TFLOPs": round(useful, 2),
+           "long_mfma_frac_bf16": round(3 * useful / PEAK_BF16_TFLOPS, 4),
+           "long_weight_GBs": round(chunks * 1.0625 * params / long_s / 1e9, 1)}
+    log(f"prefill: {len(prompt)} tokens token-by-token {tbt * 1e3:.1f} ms, batched {batched * 1e3:.1f} ms "
+        f"({tbt / batched:.1f}x); {long_len} tokens batched {long_s * 1e3:.1f} ms = {long_len / long_s:.0f} tok/s, "
+        f"{useful:.1f} useful TFLOP/s ({3 * useful / PEAK_BF16_TFLOPS:.1%} of bf16 MFMA peak with the 3-piece split)")
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -300,6 +348,9 @@ def main() -> int:
     ap.add_argument("--no-graph", action="store_true", help="eager launches instead of hipGraph replay")
     ap.add_argument("--cpu-tokens", type=int, default=3)
     ap.add_argument("--skip-cpu", action="store_true")
+    ap.add_argument("--prefill-tokens", type=int, default=512,
+                    help="long batched prompt for the prefill measurement (0: skip the prefill measurement)")
+    ap.add_argument("--prefill-only", action="store_true", help="only the prefill measurement (for rocprofv3)")
     ap.add_argument("--kernel-reps", type=int, default=4)
     ap.add_argument("--tile-bytes", type=int, default=0, help="matvec LDS tile bytes (tuning)")
     ap.add_argument("--kernels", action="store_true",
@@ -337,7 +388,7 @@ def main() -> int:
     cfg = syn.CONFIG_8B
     specs = syn.llama_specs(cfg, syn.Q8_0, seed=8)
     wbytes = syn.weight_bytes(specs)
-    cap = args.prompt + args.warmup + args.steps + 8
+    cap = max(args.prompt + args.warmup + args.steps, args.prefill_tokens) + 8
     ctx = rf.Context(0)
     name, cus = ctx.device_info()
     log(f"device {name}, {cus} CUs; building 8B-shape Q8_0 model ({wbytes / 1e9:.2f} GB) in HBM")
@@ -345,10 +396,15 @@ def main() -> int:
     if args.traffic_probe:
         return traffic_probe(ctx, m, cfg, rf)
     prompt = [int(t) for t in np.random.default_rng(8).integers(0, cfg["vocab_size"], args.prompt)]
+    pre = None
+    if args.prefill_tokens:
+        pre = prefill_bench(ctx, m, cfg, rf, prompt, args.prefill_tokens)
+        if args.prefill_only:
+            print(json.dumps({"prefill": pre}), flush=True)
+            return 0
     t0 = time.perf_counter()
-    for p, t in enumerate(prompt):
-        m.forward(t, p)
-    log(f"prompt of {args.prompt} tokens forwarded in {time.perf_counter() - t0:.3f} s")
+    m.prefill(prompt)
+    log(f"prompt of {args.prompt} tokens forwarded (batched) in {time.perf_counter() - t0:.3f} s")
     m.use_graph(not args.no_graph)
     m.decode_steps(args.warmup)
     ctx.synchronize()
@@ -415,6 +471,7 @@ def main() -> int:
         "kernel_ms_per_token": round(kernel_ms, 4),
         "breakdown": breakdown,
         "matvec_q8_0_4096x4096": mv,
+        "prefill": pre,
         "tokens_head": toks[:8],
         "device": name,
     }

@@ -554,6 +554,8 @@ static void launch_split_t(const AttnArgs& a, hipStream_t st) {
 // 20.6 us; 4096: 13.8 vs 15.0 us) and loses below (64 positions: 6.0 vs
 // 5.6 us); W = 16 (1024 threads, 128 VGPRs) spills and was slower everywhere.
 uint32_t attention_waves(uint32_t chunk, uint32_t) { return chunk <= 64 ? 4u : 8u; }
+uint32_t att_chunk_positions(uint64_t total, uint32_t nsplit) { return att_chunk((uint32_t)total, nsplit); }
+static_assert(ATT_PREFILL_CHUNK == ATT_MAX_CHUNK, "prefill chunks are the kernel's longest");
 
 hipError_t launch_attention_naive(const AttnArgs& a, hipStream_t st) {
   hipLaunchKernelGGL(attn_naive, dim3(a.qh), dim3(256), 0, st, a);

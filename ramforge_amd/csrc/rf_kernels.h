@@ -130,6 +130,9 @@ hipError_t launch_attention(const AttnArgs& a, hipStream_t st);
 hipError_t launch_attention_naive(const AttnArgs& a, hipStream_t st);
 uint32_t attention_splits(uint32_t total_positions, uint32_t kvh);
 uint32_t attention_waves(uint32_t chunk, uint32_t g_hd);
+// Positions per chunk of a `nsplit`-chunk launch over `total` positions.
+uint32_t att_chunk_positions(uint64_t total, uint32_t nsplit);
+constexpr uint64_t ATT_PREFILL_CHUNK = 1024;  // longest chunk of the split kernel
 struct AttnShape {
   uint32_t per_q, nsplit, waves;
 };

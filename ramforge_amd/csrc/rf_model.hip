@@ -898,6 +898,11 @@ int32_t forward_token(rf_model* m, uint32_t token, uint64_t pos) {
 // the chunk (rf_prefill.hip), RMSNorm per token, RoPE + K/V cache rows, then
 // causal attention of each token over the cache up to its own position.
 
+uint32_t prefill_attn_splits(uint64_t total) {
+  const uint64_t n = (total + ATT_PREFILL_CHUNK - 1) / ATT_PREFILL_CHUNK;
+  return (uint32_t)(n < 1 ? 1 : n);
+}
+
 bool prefill_supported(const rf_model* m) {
   if (!m->attn_fast) return false;
   const uint64_t d = m->cfg.embedding_length, qd = m->cfg.head_count * m->cfg.head_dim, f = m->cfg.feed_forward_length;
@@ -933,7 +938,7 @@ int32_t ensure_prefill_ws(rf_model* m) {
   take_max({f, f}, d);
   take_max({f}, d);
   take_max({d}, f);
-  const uint64_t att = T * m->attn_chunks * c.head_count * (hd + 2);
+  const uint64_t att = T * prefill_attn_splits(m->kv_cap) * c.head_count * (hd + 2);
   const uint64_t sizes[] = {T * d, T * d, T * qd, T * kvd, T * kvd, T * qd, T * qd, T * f, T * f, part, att};
   uint64_t total = 0;
   for (uint64_t n : sizes) total += (n + 63) / 64 * 64;
@@ -991,9 +996,12 @@ int32_t enqueue_prefill_layer(rf_model* m, size_t li, uint64_t pos0, uint64_t nt
   a.q = m->p_qr; a.k_hist = kc; a.v_hist = vc; a.out = m->p_a; a.ws = m->p_att;
   a.hist = (uint32_t)pos0; a.ntok = (uint32_t)nt;
   a.qh = (uint32_t)c.head_count; a.kvh = (uint32_t)c.head_count_kv; a.hd = (uint32_t)hd;
-  const AttnShape sh = attention_regime_shape(attention_regime(pos0 + nt, a.qh, a.kvh, m->kv_cap), a.qh, a.kvh,
-                                              m->kv_cap);
-  a.per_q = sh.per_q; a.nsplit = sh.nsplit; a.waves = sh.waves;
+  // The chunk's tokens already give nt x kvh workgroups: one workgroup per
+  // KV head (its query heads share each K/V row read) and chunks of up to
+  // ATT_MAX_CHUNK positions, so up to 1024 positions need no merge.
+  a.per_q = 0;
+  a.nsplit = prefill_attn_splits(pos0 + nt);
+  a.waves = attention_waves(att_chunk_positions(pos0 + nt, a.nsplit), 0);
   a.denom = sqrtf((float)hd);
   RF_LAUNCH(launch_attention(a, st), "prefill attention");
   // 4. o-proj + residual

@@ -29,13 +29,15 @@
 // [row l % 16], i = 0..3, so every value a lane accumulates belongs to its own
 // weight row and takes that row's scale.
 //
-// Workgroup: 4 wavefronts x 32 rows (two 16-row tiles) x all tokens of the
-// chunk (NTT tiles of 16), over a range of 256-element k slices (split-K).
-// x slices are staged in LDS as f32 (16-byte skew per token row: the 16
-// token rows of an A read fall in distinct banks) and split into bf16 in
-// registers; weights go straight from HBM to registers, a slice ahead of
-// use.  Partial sums of the splits land in a workspace and mm_reduce adds
-// them in a fixed order (deterministic) and applies the epilogue.
+// Workgroup: 8 wavefronts x 32 rows (two 16-row tiles) x all tokens of the
+// chunk (NTT tiles of 16), over a range of 128-element k slices (split-K).
+// Each x slice is split once per workgroup while it is staged: three bf16
+// planes in LDS (16-byte skew per token row: the 16 token rows of an A read
+// fall in distinct banks), read as MFMA operands by all eight wavefronts.
+// Two slice buffers: the next slice's x (from L2) and weights (from HBM,
+// straight to registers) are loaded while the current slice is computed.
+// Partial sums of the splits land in a workspace and mm_reduce adds them in
+// a fixed order (deterministic) and applies the epilogue.
 #include "rf_device.h"
 #include "rf_kernels.h"
 
@@ -44,9 +46,10 @@ namespace rf {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-constexpr uint32_t MM_ROWS = 128;          // weight rows per workgroup
-constexpr uint32_t MM_KS = 256;            // k elements per staged x slice (8 steps of 32)
-constexpr uint32_t MM_XS = MM_KS + 4;      // LDS floats per token row of a slice
+constexpr uint32_t MM_ROWS = 256;         // weight rows per workgroup (8 wavefronts x 32)
+constexpr uint32_t MM_KS = 128;           // k elements per staged x slice
+constexpr uint32_t MM_ST = MM_KS / 32;    // 32-element steps per slice
+constexpr uint32_t MM_XB = MM_KS + 8;     // LDS bf16 per token row of one x plane (16-byte skew)
 
 struct MmSeg {
   const uint8_t* reg[PK_MAX_REGIONS];  // regions at the segment's first row
@@ -71,42 +74,20 @@ __device__ __forceinline__ bf16x8 mm_codes(const float (&v)[8]) {
   return r;
 }
 
-// x = hi + mid + lo, each the round-to-nearest bf16 of what remains.
-__device__ __forceinline__ void mm_split3(const float (&x)[8], bf16x8& hi, bf16x8& mid, bf16x8& lo) {
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const __bf16 a = (__bf16)x[i];
-    const float r1 = x[i] - (float)a;
-    const __bf16 b = (__bf16)r1;
-    const float r2 = r1 - (float)b;
-    hi[i] = a;
-    mid[i] = b;
-    lo[i] = (__bf16)r2;
-  }
-}
-
-__device__ __forceinline__ f32x4 mm_dot3(const bf16x8& hi, const bf16x8& mid, const bf16x8& lo, const bf16x8& w) {
-  f32x4 t = {0.f, 0.f, 0.f, 0.f};
-  t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(hi, w, t, 0, 0, 0);
-  t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(mid, w, t, 0, 0, 0);
-  t = __builtin_amdgcn_mfma_f32_16x16x32_bf16(lo, w, t, 0, 0, 0);
-  return t;
-}
-
-// Per-format weight slice of one lane (row r, element group g) and its decode
-// into the B operand of step j.  `nb` = blocks per row.
+// Per-format weight slice (MM_KS elements of one row) of one lane (element
+// group g) and its decode into the B operand of step j.
 template <uint32_t T> struct MmW;
 
 template <> struct MmW<T_Q8_0> {
-  uint2 c[8];
-  uint32_t sc[8];
+  uint2 c[MM_ST];
+  uint32_t sc[MM_ST];
   __device__ void load(const MmSeg& s, uint32_t row, uint32_t sl, uint32_t g, uint32_t nst, uint32_t K) {
     const uint8_t* cb = s.reg[0] + (size_t)row * K + sl * MM_KS + 8u * g;
-    const uint8_t* sb = s.reg[1] + ((size_t)row * (K / 32u) + sl * 8u) * 2u;
+    const uint8_t* sb = s.reg[1] + ((size_t)row * (K / 32u) + sl * MM_ST) * 2u;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      c[j] = (uint32_t)j < nst ? *reinterpret_cast<const uint2*>(cb + 32 * j) : make_uint2(0, 0);
-      sc[j] = (uint32_t)j < nst ? (uint32_t)rf_ld_u16(sb + 2 * j) : 0u;
+    for (uint32_t j = 0; j < MM_ST; ++j) {
+      c[j] = j < nst ? *reinterpret_cast<const uint2*>(cb + 32 * j) : make_uint2(0, 0);
+      sc[j] = j < nst ? (uint32_t)rf_ld_u16(sb + 2 * j) : 0u;
     }
   }
   __device__ void step(int j, uint32_t, bf16x8& b, float& d) const {
@@ -119,16 +100,16 @@ template <> struct MmW<T_Q8_0> {
 };
 
 template <> struct MmW<T_Q4_0> {
-  uint2 c[8];
-  uint32_t sc[8];
+  uint2 c[MM_ST];
+  uint32_t sc[MM_ST];
   __device__ void load(const MmSeg& s, uint32_t row, uint32_t sl, uint32_t g, uint32_t nst, uint32_t K) {
-    const size_t blk = (size_t)row * (K / 32u) + sl * 8u;
+    const size_t blk = (size_t)row * (K / 32u) + sl * MM_ST;
     const uint8_t* cb = s.reg[0] + blk * 16u + 8u * (g & 1u);
     const uint8_t* sb = s.reg[1] + blk * 2u;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      c[j] = (uint32_t)j < nst ? *reinterpret_cast<const uint2*>(cb + 16 * j) : make_uint2(0, 0);
-      sc[j] = (uint32_t)j < nst ? (uint32_t)rf_ld_u16(sb + 2 * j) : 0u;
+    for (uint32_t j = 0; j < MM_ST; ++j) {
+      c[j] = j < nst ? *reinterpret_cast<const uint2*>(cb + 16 * j) : make_uint2(0, 0);
+      sc[j] = j < nst ? (uint32_t)rf_ld_u16(sb + 2 * j) : 0u;
     }
   }
   // elements 8g..8g+7 of a block: low nibbles of bytes 0-7 / 8-15 (g = 0, 1),
@@ -143,35 +124,39 @@ template <> struct MmW<T_Q4_0> {
   }
 };
 
+// A slice is half a 256-element block: sub-blocks 4 hh .. 4 hh + 3.
 template <> struct MmW<T_Q4_K> {
-  uint2 c[4];  // qs bytes 32i + 8g .. + 7: steps 2i (low nibbles) and 2i + 1 (high)
+  uint2 c[2];  // qs bytes 32 (2 hh + i) + 8g .. + 7: sub-blocks 4 hh + 2i (low nibbles), + 1 (high)
   uint4 h;     // d | dmin << 16, scale bytes 0-3, 4-7, 8-11
+  uint32_t hh;
   __device__ void load(const MmSeg& s, uint32_t row, uint32_t sl, uint32_t g, uint32_t, uint32_t K) {
-    const size_t blk = (size_t)row * (K / 256u) + sl;
-    const uint8_t* cb = s.reg[0] + blk * 128u + 8u * g;
+    const size_t blk = (size_t)row * (K / 256u) + (sl >> 1);
+    hh = sl & 1u;
+    const uint8_t* cb = s.reg[0] + blk * 128u + 64u * hh + 8u * g;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) c[i] = *reinterpret_cast<const uint2*>(cb + 32 * i);
+    for (int i = 0; i < 2; ++i) c[i] = *reinterpret_cast<const uint2*>(cb + 32 * i);
     h = *reinterpret_cast<const uint4*>(s.reg[1] + blk * 16u);
   }
   __device__ uint32_t sbyte(uint32_t i) const {
     const uint32_t w = i < 4 ? h.y : (i < 8 ? h.z : h.w);
     return (w >> (8 * (i & 3u))) & 0xFFu;
   }
-  // get_scale_min (quant.rs:216-226) of sub-block j
+  // get_scale_min (quant.rs:216-226) of sub-block 4 hh + j
   __device__ void step(int j, uint32_t, bf16x8& b, float& d1, float& m1) const {
     const int sh = 4 * (j & 1);
     float v[8];
 #pragma unroll
     for (int k = 0; k < 8; ++k) v[k] = (float)((mm_byte(c[j >> 1], k) >> sh) & 15u);
     b = mm_codes(v);
+    // hh is uniform and j a compile-time index: every byte index is static
+    const uint32_t ju = (uint32_t)j, q = 4u + ju;
     uint32_t sc, m;
-    const uint32_t ju = (uint32_t)j;
-    if (ju < 4) {
+    if (hh == 0) {
       sc = sbyte(ju) & 63u;
       m = sbyte(ju + 4) & 63u;
     } else {
-      sc = (sbyte(ju + 4) & 0xFu) | ((sbyte(ju - 4) >> 6) << 4);
-      m = (sbyte(ju + 4) >> 4) | ((sbyte(ju) >> 6) << 4);
+      sc = (sbyte(q + 4) & 0xFu) | ((sbyte(q - 4) >> 6) << 4);
+      m = (sbyte(q + 4) >> 4) | ((sbyte(q) >> 6) << 4);
     }
     const float d = rf_half_to_float_fast(h.x & 0xFFFFu), dmin = rf_half_to_float_fast(h.x >> 16);
     d1 = d * (float)sc;
@@ -179,19 +164,20 @@ template <> struct MmW<T_Q4_K> {
   }
 };
 
+// A slice is one 128-element half hh of a block: steps qq = 0..3 cover
+// elements 128 hh + 32 qq + l, l = 0..31 (quant.rs:376-406).
 template <> struct MmW<T_Q6_K> {
-  uint2 ql[4];  // [2h + p]: ql bytes 64h + 32p + 8g .. + 7
-  uint2 qh[2];  // [h]: qh bytes 32h + 8g .. + 7
+  uint2 ql[2];  // [p]: ql bytes 64 hh + 32 p + 8g .. + 7
+  uint2 qh;     // qh bytes 32 hh + 8g .. + 7
   uint4 sc;     // 16 int8 scales
-  uint32_t d;
+  uint32_t d, hh;
   __device__ void load(const MmSeg& s, uint32_t row, uint32_t sl, uint32_t g, uint32_t, uint32_t K) {
-    const size_t blk = (size_t)row * (K / 256u) + sl;
-    const uint8_t* lb = s.reg[0] + blk * 128u + 8u * g;
-    const uint8_t* hb = s.reg[1] + blk * 64u + 8u * g;
+    const size_t blk = (size_t)row * (K / 256u) + (sl >> 1);
+    hh = sl & 1u;
+    const uint8_t* lb = s.reg[0] + blk * 128u + 64u * hh + 8u * g;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) ql[i] = *reinterpret_cast<const uint2*>(lb + 64 * (i >> 1) + 32 * (i & 1));
-#pragma unroll
-    for (int i = 0; i < 2; ++i) qh[i] = *reinterpret_cast<const uint2*>(hb + 32 * i);
+    for (int i = 0; i < 2; ++i) ql[i] = *reinterpret_cast<const uint2*>(lb + 32 * i);
+    qh = *reinterpret_cast<const uint2*>(s.reg[1] + blk * 64u + 32u * hh + 8u * g);
     sc = *reinterpret_cast<const uint4*>(s.reg[2] + blk * 16u);
     d = rf_ld_u16(s.reg[3] + blk * 2u);
   }
@@ -199,35 +185,45 @@ template <> struct MmW<T_Q6_K> {
     const uint32_t w = i < 4 ? sc.x : (i < 8 ? sc.y : (i < 12 ? sc.z : sc.w));
     return (float)(int)(int8_t)((w >> (8 * (i & 3u))) & 0xFFu);
   }
-  // Step j = 4h + qq covers elements 128h + 32qq + l, l = 0..31 (quant.rs:376-406):
-  // q = (ql nibble qq / 2 of byte 64h + 32 (qq & 1) + l) | (qh bits 2qq of byte 32h + l) << 4, minus 32.
-  // Elements l < 16 (groups 0, 1) take scale 8h + 2qq, the rest 8h + 2qq + 1:
+  // q = (ql nibble qq / 2 of byte 64 hh + 32 (qq & 1) + l) | (qh bits 2qq of byte 32 hh + l) << 4, minus 32.
+  // Elements l < 16 (groups 0, 1) take scale 8 hh + 2qq, the rest 8 hh + 2qq + 1:
   // b0 holds groups 0-1 (zeros in 2-3), b1 groups 2-3.
-  __device__ void step(int j, uint32_t g, bf16x8& b0, bf16x8& b1, float& d0, float& d1) const {
-    const int hh = j >> 2, qq = j & 3;
-    const uint2 l = ql[2 * hh + (qq & 1)], hi = qh[hh];
+  __device__ void step(int qq, uint32_t g, bf16x8& b0, bf16x8& b1, float& d0, float& d1) const {
+    const uint2 l = ql[qq & 1];
     const int lsh = 4 * (qq >> 1), hsh = 2 * qq;
     const bool first = g < 2u;
     float v0[8], v1[8];
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
-      const int q = (int)(((mm_byte(l, k) >> lsh) & 15u) | (((mm_byte(hi, k) >> hsh) & 3u) << 4)) - 32;
+      const int q = (int)(((mm_byte(l, k) >> lsh) & 15u) | (((mm_byte(qh, k) >> hsh) & 3u) << 4)) - 32;
       v0[k] = first ? (float)q : 0.f;
       v1[k] = first ? 0.f : (float)q;
     }
     b0 = mm_codes(v0);
     b1 = mm_codes(v1);
     const float dd = rf_half_to_float_fast(d);
-    d0 = dd * scale(8u * hh + 2u * qq);
-    d1 = dd * scale(8u * hh + 2u * qq + 1u);
+    const uint32_t q2 = 2u * (uint32_t)qq;  // hh uniform, qq compile-time: static indices
+    d0 = dd * (hh == 0 ? scale(q2) : scale(8u + q2));
+    d1 = dd * (hh == 0 ? scale(q2 + 1u) : scale(9u + q2));
   }
 };
 
+// x = hi + mid + lo, each the round-to-nearest bf16 of what remains.
+__device__ __forceinline__ void mm_split3(float x, __bf16& hi, __bf16& mid, __bf16& lo) {
+  hi = (__bf16)x;
+  const float r1 = x - (float)hi;
+  mid = (__bf16)r1;
+  lo = (__bf16)(r1 - (float)mid);
+}
+
 template <uint32_t T, int NTT>
-__global__ __launch_bounds__(256) void mm_packed(MmArgs a) {
-  extern __shared__ __align__(16) float xs[];  // [NTT * 16][MM_XS], then Q4_K step sums [8][NTT * 16]
-  constexpr uint32_t NT = NTT * 16;
-  float* ss = xs + NT * MM_XS;
+__global__ __launch_bounds__(512) void mm_packed(MmArgs a) {
+  // Two x slice buffers, each three bf16 planes [3][NT][MM_XB] and (Q4_K)
+  // step sums [MM_ST][NT]: slice s + 1 is loaded (x and weights) while slice
+  // s is computed, then split into the other buffer; one barrier per slice.
+  extern __shared__ __align__(16) __bf16 xsb[];
+  constexpr uint32_t NT = NTT * 16, PLANE = NT * MM_XB;
+  constexpr uint32_t BUF = 3 * PLANE + (T == T_Q4_K ? MM_ST * NT * 2 : 0);  // bf16 elements per buffer
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
   const uint32_t r16 = lane & 15u, g = lane >> 4;
   MmSeg s = a.seg[0];
@@ -239,6 +235,45 @@ __global__ __launch_bounds__(256) void mm_packed(MmArgs a) {
   for (int rt = 0; rt < 2; ++rt) rowc[rt] = min(row_base + 16u * rt + r16, s.rows - 1u);  // loads stay in bounds
   const uint32_t K = a.in_dim, n = a.n;
   const uint32_t sl0 = blockIdx.y * a.spp, sl1 = min(a.nslices, sl0 + a.spp);
+  // staging: thread -> (token st_t, 32-element block st_b, half st_h) of a slice
+  const uint32_t st_t = tid >> 3, st_b = (tid >> 1) & 3u, st_h = tid & 1u;
+  auto nsteps = [&](uint32_t sl) { return min(MM_ST, (K - sl * MM_KS) / 32u); };
+  auto fetch_x = [&](uint32_t sl, float4 (&xv)[4]) {
+    const bool live = st_t < n && st_b < nsteps(sl);
+    const float* xp = a.x + (size_t)(live ? st_t : 0u) * a.ldx + sl * MM_KS + 32u * st_b + 16u * st_h;
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      xv[q] = live ? *reinterpret_cast<const float4*>(xp + 4 * q) : make_float4(0.f, 0.f, 0.f, 0.f);
+  };
+  auto put_x = [&](uint32_t buf, const float4 (&xv)[4]) {
+    if (st_t >= NT) return;  // whole groups of 8 threads (one token row)
+    __bf16* dst = xsb + buf * BUF + st_t * MM_XB + 32u * st_b + 16u * st_h;
+    float sum = 0.f;
+    bf16x8 hv[2], mv[2], lv[2];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float e[4] = {xv[q].x, xv[q].y, xv[q].z, xv[q].w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        __bf16 h, m, l;
+        mm_split3(e[i], h, m, l);
+        hv[q >> 1][4 * (q & 1) + i] = h;
+        mv[q >> 1][4 * (q & 1) + i] = m;
+        lv[q >> 1][4 * (q & 1) + i] = l;
+        sum += e[i];
+      }
+    }
+#pragma unroll
+    for (int v = 0; v < 2; ++v) {
+      *reinterpret_cast<bf16x8*>(dst + 8 * v) = hv[v];
+      *reinterpret_cast<bf16x8*>(dst + PLANE + 8 * v) = mv[v];
+      *reinterpret_cast<bf16x8*>(dst + 2 * PLANE + 8 * v) = lv[v];
+    }
+    if constexpr (T == T_Q4_K) {
+      sum += __shfl_xor(sum, 1);  // the partner half is in this thread group
+      if (st_h == 0) reinterpret_cast<float*>(xsb + buf * BUF + 3 * PLANE)[st_b * NT + st_t] = sum;
+    }
+  };
 
   f32x4 acc[2][NTT];
 #pragma unroll
@@ -246,42 +281,25 @@ __global__ __launch_bounds__(256) void mm_packed(MmArgs a) {
 #pragma unroll
     for (int nt = 0; nt < NTT; ++nt) acc[rt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  MmW<T> w[2];
-  {
-    const uint32_t nst = min(8u, (K - sl0 * MM_KS) / 32u);
+  MmW<T> cur[2], nxt[2];
+  float4 xv[4];
+  fetch_x(sl0, xv);
 #pragma unroll
-    for (int rt = 0; rt < 2; ++rt) w[rt].load(s, rowc[rt], sl0, g, nst, K);
-  }
+  for (int rt = 0; rt < 2; ++rt) cur[rt].load(s, rowc[rt], sl0, g, nsteps(sl0), K);
+  put_x(0, xv);
+  __syncthreads();
   for (uint32_t sl = sl0; sl < sl1; ++sl) {
-    const uint32_t nst = min(8u, (K - sl * MM_KS) / 32u);
-    __syncthreads();  // the previous slice's x reads are done
-    // stage x[0..NT)[slice] (zeros past n and past K)
+    const uint32_t cb = (sl - sl0) & 1u, nst = nsteps(sl);
+    const bool more = sl + 1 < sl1;
+    if (more) {  // next slice's x and weights in flight during this slice's math
+      fetch_x(sl + 1, xv);
 #pragma unroll
-    for (uint32_t u = 0; u < NT / 4u; ++u) {
-      const uint32_t i = tid + 256u * u, t = i >> 6, c4 = i & 63u, k = sl * MM_KS + 4u * c4;
-      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (t < n && k < K) v = *reinterpret_cast<const float4*>(a.x + (size_t)t * a.ldx + k);
-      *reinterpret_cast<float4*>(&xs[t * MM_XS + 4u * c4]) = v;
+      for (int rt = 0; rt < 2; ++rt) nxt[rt].load(s, rowc[rt], sl + 1, g, nsteps(sl + 1), K);
     }
-    if constexpr (T == T_Q4_K) {
-      __syncthreads();
-      for (uint32_t e = tid; e < 8u * NT; e += 256u) {
-        const uint32_t j = e / NT, t = e % NT;
-        const float* p = &xs[t * MM_XS + 32u * j];
-        float sum = 0.f;
-        for (int i = 0; i < 32; ++i) sum += p[i];
-        ss[j * NT + t] = sum;
-      }
-    }
-    __syncthreads();
-    MmW<T> cur[2] = {w[0], w[1]};
-    if (sl + 1 < sl1) {  // next slice's weights in flight during this slice's math
-      const uint32_t nn = min(8u, (K - (sl + 1) * MM_KS) / 32u);
+    const __bf16* xb = xsb + cb * BUF;
+    const float* ss = reinterpret_cast<const float*>(xb + 3 * PLANE);
 #pragma unroll
-      for (int rt = 0; rt < 2; ++rt) w[rt].load(s, rowc[rt], sl + 1, g, nn, K);
-    }
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
+    for (int j = 0; j < (int)MM_ST; ++j) {
       if ((uint32_t)j >= nst) break;
       bf16x8 b[2], b2[2];
       float d[2], e[2];
@@ -291,35 +309,55 @@ __global__ __launch_bounds__(256) void mm_packed(MmArgs a) {
         else if constexpr (T == T_Q6_K) cur[rt].step(j, g, b[rt], b2[rt], d[rt], e[rt]);
         else cur[rt].step(j, g, b[rt], d[rt]);
       }
+      // All A operands of the step, then the hi / mid / lo MFMAs of every
+      // (row tile, token tile) pair in turn: each MFMA's accumulator input
+      // was written 2 NTT (4 NTT for Q6_K) MFMAs earlier, so the chains
+      // overlap instead of waiting on each other.
+      bf16x8 ax[3][NTT];
 #pragma unroll
       for (int nt = 0; nt < NTT; ++nt) {
-        const float* xp = &xs[(nt * 16u + r16) * MM_XS + 32u * j + 8u * g];
-        const float4 x0 = *reinterpret_cast<const float4*>(xp);
-        const float4 x1 = *reinterpret_cast<const float4*>(xp + 4);
-        const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-        bf16x8 hi, mid, lo;
-        mm_split3(xv, hi, mid, lo);
+        const __bf16* ap = xb + (nt * 16u + r16) * MM_XB + 32u * j + 8u * g;
+#pragma unroll
+        for (int p = 0; p < 3; ++p) ax[p][nt] = *reinterpret_cast<const bf16x8*>(ap + p * PLANE);
+      }
+      constexpr int NB = T == T_Q6_K ? 2 : 1;
+      f32x4 tmp[NB][2][NTT];
+#pragma unroll
+      for (int p = 0; p < 3; ++p)
+#pragma unroll
+        for (int h = 0; h < NB; ++h)
+#pragma unroll
+          for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+            for (int nt = 0; nt < NTT; ++nt) {
+              const bf16x8& bw = h == 0 ? b[rt] : b2[rt];
+              tmp[h][rt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                  ax[p][nt], bw, p == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : tmp[h][rt][nt], 0, 0, 0);
+            }
+#pragma unroll
+      for (int nt = 0; nt < NTT; ++nt) {
         float4 sx = make_float4(0.f, 0.f, 0.f, 0.f);
         if constexpr (T == T_Q4_K) sx = *reinterpret_cast<const float4*>(&ss[j * NT + nt * 16u + 4u * g]);
+        const float sxa[4] = {sx.x, sx.y, sx.z, sx.w};
 #pragma unroll
         for (int rt = 0; rt < 2; ++rt) {
-          const f32x4 t0 = mm_dot3(hi, mid, lo, b[rt]);
           f32x4& c = acc[rt][nt];
-          if constexpr (T == T_Q6_K) {
-            const f32x4 t1 = mm_dot3(hi, mid, lo, b2[rt]);
+          const f32x4& t0 = tmp[0][rt][nt];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) c[i] = fmaf(e[rt], t1[i], fmaf(d[rt], t0[i], c[i]));
-          } else if constexpr (T == T_Q4_K) {
-            const float sxa[4] = {sx.x, sx.y, sx.z, sx.w};
-#pragma unroll
-            for (int i = 0; i < 4; ++i) c[i] = fmaf(-e[rt], sxa[i], fmaf(d[rt], t0[i], c[i]));
-          } else {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) c[i] = fmaf(d[rt], t0[i], c[i]);
+          for (int i = 0; i < 4; ++i) {
+            if constexpr (T == T_Q6_K) c[i] = fmaf(e[rt], tmp[NB - 1][rt][nt][i], fmaf(d[rt], t0[i], c[i]));
+            else if constexpr (T == T_Q4_K) c[i] = fmaf(-e[rt], sxa[i], fmaf(d[rt], t0[i], c[i]));
+            else c[i] = fmaf(d[rt], t0[i], c[i]);
           }
         }
       }
     }
+    if (more) {
+      put_x(cb ^ 1u, xv);  // the other buffer's last reader was slice sl - 1, before the last barrier
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt) cur[rt] = nxt[rt];
+    }
+    __syncthreads();
   }
   float* out = a.part + (size_t)blockIdx.y * n * a.mtot + s.col;
 #pragma unroll
@@ -398,16 +436,31 @@ bool mm_supported(uint32_t t, uint64_t in_dim) {
   return in_dim % qk == 0;
 }
 
-// Split-K shape: about two workgroups per CU, whole slices per split.
-static void mm_shape(uint64_t groups, uint64_t in_dim, uint32_t* nsplit, uint32_t* spp, uint32_t* nslices) {
+// Split-K shape: whole slices per split, at least two slices per workgroup
+// and at most K / 4 partial floats per row (sp * n <= K / 4: the partial sums
+// stay below about the weights' bytes), and among those the split count whose
+// workgroups best fill whole rounds of one workgroup per CU (104 KB of LDS at
+// 64 tokens), fewest splits on a tie.
+static void mm_shape(uint64_t groups, uint64_t in_dim, uint64_t n, uint32_t* nsplit, uint32_t* spp,
+                     uint32_t* nslices) {
   const uint64_t ns = (in_dim + MM_KS - 1) / MM_KS;
-  const uint64_t target = 2ull * mm_cu_count();
-  uint64_t sp = (target + groups - 1) / groups;
-  if (sp < 1) sp = 1;
-  if (sp > ns) sp = ns;
-  const uint64_t per = (ns + sp - 1) / sp;
-  *spp = (uint32_t)per;
-  *nsplit = (uint32_t)((ns + per - 1) / per);
+  const uint64_t target = mm_cu_count();
+  uint64_t spmax = ns >= 2 ? ns / 2 : 1;
+  const uint64_t by_bytes = in_dim / (4 * (n ? n : 1));
+  if (spmax > by_bytes) spmax = by_bytes;
+  if (spmax < 1) spmax = 1;
+  double best = -1.0;
+  uint64_t best_per = ns;
+  for (uint64_t sp = 1; sp <= spmax; ++sp) {
+    const uint64_t per = (ns + sp - 1) / sp, eff = (ns + per - 1) / per, w = groups * eff;
+    const double util = w < target ? (double)w / target : (double)w / (double)(((w + target - 1) / target) * target);
+    if (util > best + 1e-9) {
+      best = util;
+      best_per = per;
+    }
+  }
+  *spp = (uint32_t)best_per;
+  *nsplit = (uint32_t)((ns + best_per - 1) / best_per);
   *nslices = (uint32_t)ns;
 }
 
@@ -417,6 +470,8 @@ static uint64_t mm_groups(const MmSegDesc* segs, int nseg) {
   return g;
 }
 
+// Partial-sum floats a launch of up to n tokens may need (the split count
+// depends on the token count).
 uint64_t mm_part_floats(const uint64_t* rows, int nseg, uint64_t in_dim, uint64_t n) {
   MmSegDesc d[3] = {};
   uint64_t mtot = 0;
@@ -424,16 +479,20 @@ uint64_t mm_part_floats(const uint64_t* rows, int nseg, uint64_t in_dim, uint64_
     d[i].rows = rows[i];
     mtot += rows[i];
   }
-  uint32_t nsplit, spp, ns;
-  mm_shape(mm_groups(d, nseg), in_dim, &nsplit, &spp, &ns);
-  return (uint64_t)nsplit * n * mtot;
+  uint64_t most = 0;
+  for (uint64_t k = 1; k <= n; ++k) {
+    uint32_t nsplit, spp, ns;
+    mm_shape(mm_groups(d, nseg), in_dim, k, &nsplit, &spp, &ns);
+    if ((uint64_t)nsplit * k > most) most = (uint64_t)nsplit * k;
+  }
+  return most * mtot;
 }
 
 static int mm_ntt(uint64_t n) { return (int)((n + 15) / 16); }
 
 template <uint32_t T, int NTT>
 static hipError_t mm_launch_t(const MmArgs& a, dim3 grid, hipStream_t st) {
-  const uint32_t lds = (NTT * 16u * MM_XS + (T == T_Q4_K ? 8u * NTT * 16u : 0u)) * 4u;
+  const uint32_t lds = 2u * (3u * NTT * 16u * MM_XB * 2u + (T == T_Q4_K ? MM_ST * NTT * 16u * 4u : 0u));
   static bool opened = false;
   if (!opened) {
     if (lds > 65536) {
@@ -443,7 +502,7 @@ static hipError_t mm_launch_t(const MmArgs& a, dim3 grid, hipStream_t st) {
     }
     opened = true;
   }
-  hipLaunchKernelGGL((mm_packed<T, NTT>), grid, dim3(256), lds, st, a);
+  hipLaunchKernelGGL((mm_packed<T, NTT>), grid, dim3(512), lds, st, a);
   return hipGetLastError();
 }
 
@@ -502,7 +561,7 @@ hipError_t launch_matmul_packed(uint32_t t, const MmSegDesc* segs, int nseg, con
   }
   if (mtot > 0xFFFFFFFFull || groups > 0x7FFFFFFFull) return hipErrorInvalidValue;
   uint32_t nsplit, spp, nslices;
-  mm_shape(groups, in_dim, &nsplit, &spp, &nslices);
+  mm_shape(groups, in_dim, n, &nsplit, &spp, &nslices);
   if ((uint64_t)nsplit * n * mtot > part_floats) return hipErrorInvalidValue;
   a.nseg = (uint32_t)nseg;
   a.x = x;
