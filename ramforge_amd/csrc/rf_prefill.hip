@@ -38,6 +38,8 @@
 // straight to registers) are loaded while the current slice is computed.
 // Partial sums of the splits land in a workspace and mm_reduce adds them in
 // a fixed order (deterministic) and applies the epilogue.
+#include <algorithm>
+
 #include "rf_device.h"
 #include "rf_kernels.h"
 
@@ -438,9 +440,11 @@ bool mm_supported(uint32_t t, uint64_t in_dim) {
 
 // Split-K shape: whole slices per split, at least two slices per workgroup
 // and at most K / 4 partial floats per row (sp * n <= K / 4: the partial sums
-// stay below about the weights' bytes), and among those the split count whose
-// workgroups best fill whole rounds of one workgroup per CU (104 KB of LDS at
-// 64 tokens), fewest splits on a tie.
+// stay below about the weights' bytes); among those the fewest splits whose
+// workgroups fill whole rounds of one workgroup per CU (104 KB of LDS at 64
+// tokens) within 85% of the best split count's fill (each split adds a
+// workgroup prologue and partial traffic: gate/up at 16 splits spent 23 us
+// in the reduce alone, at 2 splits 5 us).
 static void mm_shape(uint64_t groups, uint64_t in_dim, uint64_t n, uint32_t* nsplit, uint32_t* spp,
                      uint32_t* nslices) {
   const uint64_t ns = (in_dim + MM_KS - 1) / MM_KS;
@@ -449,16 +453,20 @@ static void mm_shape(uint64_t groups, uint64_t in_dim, uint64_t n, uint32_t* nsp
   const uint64_t by_bytes = in_dim / (4 * (n ? n : 1));
   if (spmax > by_bytes) spmax = by_bytes;
   if (spmax < 1) spmax = 1;
-  double best = -1.0;
-  uint64_t best_per = ns;
-  for (uint64_t sp = 1; sp <= spmax; ++sp) {
+  auto util = [&](uint64_t sp, uint64_t* per_out) {
     const uint64_t per = (ns + sp - 1) / sp, eff = (ns + per - 1) / per, w = groups * eff;
-    const double util = w < target ? (double)w / target : (double)w / (double)(((w + target - 1) / target) * target);
-    if (util > best + 1e-9) {
-      best = util;
+    *per_out = per;
+    return w < target ? (double)w / target : (double)w / (double)(((w + target - 1) / target) * target);
+  };
+  double best = 0.0;
+  uint64_t per = ns;
+  for (uint64_t sp = 1; sp <= spmax; ++sp) best = std::max(best, util(sp, &per));
+  uint64_t best_per = ns;
+  for (uint64_t sp = 1; sp <= spmax; ++sp)
+    if (util(sp, &per) >= 0.85 * best) {
       best_per = per;
+      break;
     }
-  }
   *spp = (uint32_t)best_per;
   *nsplit = (uint32_t)((ns + best_per - 1) / best_per);
   *nslices = (uint32_t)ns;
@@ -597,7 +605,10 @@ hipError_t launch_matmul_packed(uint32_t t, const MmSegDesc* segs, int nseg, con
 // ------------------------------------------------------- per-token glue
 
 // RMSNorm of `rows` rows of length n (stride ld), x / rms * w as
-// rms_norm_reference (compute.rs:291-319); one workgroup per row.
+// rms_norm_reference (compute.rs:291-319); one workgroup per row.  Rows of up
+// to 8192 elements (n % 4 == 0, 16-byte aligned) stay in registers between
+// the sum of squares and the scaling, read with 16-byte loads.
+template <int V>
 __global__ __launch_bounds__(256) void rmsnorm_rows_kernel(const float* __restrict__ x, const float* __restrict__ w,
                                                            uint32_t n, uint32_t ld, float eps,
                                                            float* __restrict__ y) {
@@ -606,50 +617,79 @@ __global__ __launch_bounds__(256) void rmsnorm_rows_kernel(const float* __restri
   const float* xr = x + (size_t)blockIdx.x * ld;
   float* yr = y + (size_t)blockIdx.x * ld;
   float ss = 0.f;
-  for (uint32_t i = tid; i < n; i += 256u) ss = fmaf(xr[i], xr[i], ss);
+  float4 v[V > 0 ? V : 1];
+  if constexpr (V > 0) {
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+      const uint32_t k = 4u * (tid + 256u * i);
+      v[i] = k < n ? *reinterpret_cast<const float4*>(xr + k) : make_float4(0.f, 0.f, 0.f, 0.f);
+      ss = fmaf(v[i].x, v[i].x, ss);
+      ss = fmaf(v[i].y, v[i].y, ss);
+      ss = fmaf(v[i].z, v[i].z, ss);
+      ss = fmaf(v[i].w, v[i].w, ss);
+    }
+  } else {
+    for (uint32_t i = tid; i < n; i += 256u) ss = fmaf(xr[i], xr[i], ss);
+  }
   ss = rf_wave_sum(ss);
   if ((tid & 63u) == 0) part[tid >> 6] = ss;
   __syncthreads();
   const float tot = part[0] + part[1] + part[2] + part[3];
   const float rms = sqrtf(tot / (float)n + eps);
-  for (uint32_t i = tid; i < n; i += 256u) yr[i] = xr[i] / rms * w[i];
+  if constexpr (V > 0) {
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+      const uint32_t k = 4u * (tid + 256u * i);
+      if (k >= n) break;
+      const float4 wv = *reinterpret_cast<const float4*>(w + k);
+      *reinterpret_cast<float4*>(yr + k) =
+          make_float4(v[i].x / rms * wv.x, v[i].y / rms * wv.y, v[i].z / rms * wv.z, v[i].w / rms * wv.w);
+    }
+  } else {
+    for (uint32_t i = tid; i < n; i += 256u) yr[i] = xr[i] / rms * w[i];
+  }
 }
 
 hipError_t launch_rmsnorm_rows(const float* x, const float* w, uint64_t n, uint64_t rows, uint64_t ld, float eps,
                                float* y, hipStream_t st) {
   if (rows == 0) return hipSuccess;
-  hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3((uint32_t)rows), dim3(256), 0, st, x, w, (uint32_t)n, (uint32_t)ld,
-                     eps, y);
+  const bool vec = n % 4 == 0 && ld % 4 == 0 && ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w) |
+                                                   reinterpret_cast<uintptr_t>(y)) & 15u) == 0;
+  const dim3 grid((uint32_t)rows), blk(256);
+  if (vec && n <= 4096) hipLaunchKernelGGL(rmsnorm_rows_kernel<4>, grid, blk, 0, st, x, w, (uint32_t)n, (uint32_t)ld, eps, y);
+  else if (vec && n <= 8192) hipLaunchKernelGGL(rmsnorm_rows_kernel<8>, grid, blk, 0, st, x, w, (uint32_t)n, (uint32_t)ld, eps, y);
+  else hipLaunchKernelGGL(rmsnorm_rows_kernel<0>, grid, blk, 0, st, x, w, (uint32_t)n, (uint32_t)ld, eps, y);
   return hipGetLastError();
 }
 
-// Token z at position pos0 + z: q heads rotated into qr[z], k heads rotated
-// into the K cache row, v copied into the V cache row (rope_reference,
+// Token z at position pos0 + z (blockIdx.x), head row blockIdx.y of [q heads,
+// k heads, v heads]: q heads rotated into qr[z], k heads rotated into the K
+// cache row, v copied into the V cache row (rope_reference,
 // compute.rs:389-456, with the host cos/sin table; the rotation is written in
-// the same operation order as the decode attention kernel's).
-__global__ __launch_bounds__(256) void rope_kv_rows_kernel(const float* __restrict__ q, const float* __restrict__ k,
-                                                           const float* __restrict__ v, const float* __restrict__ rope,
-                                                           uint32_t pos0, uint32_t qh, uint32_t kvh, uint32_t hd,
-                                                           float* __restrict__ qr, float* __restrict__ kc,
-                                                           float* __restrict__ vc) {
-  const uint32_t z = blockIdx.x, pos = pos0 + z, half = hd >> 1;
+// the same operation order as the decode attention kernel's).  One
+// wavefront per head row.
+__global__ __launch_bounds__(64) void rope_kv_rows_kernel(const float* __restrict__ q, const float* __restrict__ k,
+                                                          const float* __restrict__ v, const float* __restrict__ rope,
+                                                          uint32_t pos0, uint32_t qh, uint32_t kvh, uint32_t hd,
+                                                          float* __restrict__ qr, float* __restrict__ kc,
+                                                          float* __restrict__ vc) {
+  const uint32_t z = blockIdx.x, hr = blockIdx.y, pos = pos0 + z, half = hd >> 1;
   const uint32_t qd = qh * hd, kvd = kvh * hd;
+  if (hr >= qh + kvh) {  // v head
+    const uint32_t o = (hr - qh - kvh) * hd;
+    for (uint32_t d = threadIdx.x; d < hd; d += 64u) vc[(size_t)pos * kvd + o + d] = v[(size_t)z * kvd + o + d];
+    return;
+  }
+  const bool isq = hr < qh;
+  const uint32_t o = (isq ? hr : hr - qh) * hd;
+  const float* src = isq ? q + (size_t)z * qd + o : k + (size_t)z * kvd + o;
+  float* dst = isq ? qr + (size_t)z * qd + o : kc + (size_t)pos * kvd + o;
   const float* cs = rope + (size_t)pos * hd;
-  for (uint32_t e = threadIdx.x; e < qd + 2 * kvd; e += 256u) {
-    if (e >= qd + kvd) {
-      const uint32_t i = e - qd - kvd;
-      vc[(size_t)pos * kvd + i] = v[(size_t)z * kvd + i];
-      continue;
-    }
-    const bool isq = e < qd;
-    const uint32_t i = isq ? e : e - qd, d = i % hd, base = i - d;
-    const float* src = isq ? q + (size_t)z * qd + base : k + (size_t)z * kvd + base;
+  for (uint32_t d = threadIdx.x; d < hd; d += 64u) {
     const uint32_t ci = d < half ? d : d - half;
     const float va = src[d], vp = src[d < half ? d + half : d - half];
     const float c0 = cs[2 * ci], c1 = cs[2 * ci + 1];
-    const float rot = d < half ? va * c0 - vp * c1 : vp * c1 + va * c0;
-    if (isq) qr[(size_t)z * qd + i] = rot;
-    else kc[(size_t)pos * kvd + i] = rot;
+    dst[d] = d < half ? va * c0 - vp * c1 : vp * c1 + va * c0;
   }
 }
 
@@ -657,8 +697,8 @@ hipError_t launch_rope_kv_rows(const float* q, const float* k, const float* v, c
                                uint64_t ntok, uint32_t qh, uint32_t kvh, uint32_t hd, float* qr, float* kc,
                                float* vc, hipStream_t st) {
   if (ntok == 0) return hipSuccess;
-  hipLaunchKernelGGL(rope_kv_rows_kernel, dim3((uint32_t)ntok), dim3(256), 0, st, q, k, v, rope, (uint32_t)pos0, qh,
-                     kvh, hd, qr, kc, vc);
+  hipLaunchKernelGGL(rope_kv_rows_kernel, dim3((uint32_t)ntok, qh + 2 * kvh), dim3(64), 0, st, q, k, v, rope,
+                     (uint32_t)pos0, qh, kvh, hd, qr, kc, vc);
   return hipGetLastError();
 }
 
