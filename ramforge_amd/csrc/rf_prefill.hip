@@ -34,8 +34,9 @@
 // Each x slice is split once per workgroup while it is staged: three bf16
 // planes in LDS (16-byte skew per token row: the 16 token rows of an A read
 // fall in distinct banks), read as MFMA operands by all eight wavefronts.
-// Two slice buffers: the next slice's x (from L2) and weights (from HBM,
-// straight to registers) are loaded while the current slice is computed.
+// Two slice buffers: the next slice's x (from L2) is loaded while the
+// current slice is computed, the weights (from HBM, straight to registers)
+// two slices ahead.
 // Partial sums of the splits land in a workspace and mm_reduce adds them in
 // a fixed order (deterministic) and applies the epilogue.
 #include <algorithm>
@@ -76,6 +77,19 @@ __device__ __forceinline__ bf16x8 mm_codes(const float (&v)[8]) {
   return r;
 }
 
+// The MM_ST f16 scales of a slice of one row: one 8-byte load when the slice
+// is whole and 8-byte aligned (K a multiple of 128), else one per step.
+__device__ __forceinline__ void mm_load_scales(const uint8_t* sb, uint32_t nst, uint32_t (&sc)[MM_ST]) {
+  static_assert(MM_ST == 4, "four scales per slice");
+  if (nst == MM_ST && (reinterpret_cast<uintptr_t>(sb) & 7u) == 0) {
+    const uint2 v = *reinterpret_cast<const uint2*>(sb);
+    sc[0] = v.x & 0xFFFFu; sc[1] = v.x >> 16; sc[2] = v.y & 0xFFFFu; sc[3] = v.y >> 16;
+  } else {
+#pragma unroll
+    for (uint32_t j = 0; j < MM_ST; ++j) sc[j] = j < nst ? (uint32_t)rf_ld_u16(sb + 2 * j) : 0u;
+  }
+}
+
 // Per-format weight slice (MM_KS elements of one row) of one lane (element
 // group g) and its decode into the B operand of step j.
 template <uint32_t T> struct MmW;
@@ -87,10 +101,8 @@ template <> struct MmW<T_Q8_0> {
     const uint8_t* cb = s.reg[0] + (size_t)row * K + sl * MM_KS + 8u * g;
     const uint8_t* sb = s.reg[1] + ((size_t)row * (K / 32u) + sl * MM_ST) * 2u;
 #pragma unroll
-    for (uint32_t j = 0; j < MM_ST; ++j) {
-      c[j] = j < nst ? *reinterpret_cast<const uint2*>(cb + 32 * j) : make_uint2(0, 0);
-      sc[j] = j < nst ? (uint32_t)rf_ld_u16(sb + 2 * j) : 0u;
-    }
+    for (uint32_t j = 0; j < MM_ST; ++j) c[j] = j < nst ? *reinterpret_cast<const uint2*>(cb + 32 * j) : make_uint2(0, 0);
+    mm_load_scales(sb, nst, sc);
   }
   __device__ void step(int j, uint32_t, bf16x8& b, float& d) const {
     float v[8];
@@ -109,10 +121,8 @@ template <> struct MmW<T_Q4_0> {
     const uint8_t* cb = s.reg[0] + blk * 16u + 8u * (g & 1u);
     const uint8_t* sb = s.reg[1] + blk * 2u;
 #pragma unroll
-    for (uint32_t j = 0; j < MM_ST; ++j) {
-      c[j] = j < nst ? *reinterpret_cast<const uint2*>(cb + 16 * j) : make_uint2(0, 0);
-      sc[j] = j < nst ? (uint32_t)rf_ld_u16(sb + 2 * j) : 0u;
-    }
+    for (uint32_t j = 0; j < MM_ST; ++j) c[j] = j < nst ? *reinterpret_cast<const uint2*>(cb + 16 * j) : make_uint2(0, 0);
+    mm_load_scales(sb, nst, sc);
   }
   // elements 8g..8g+7 of a block: low nibbles of bytes 0-7 / 8-15 (g = 0, 1),
   // high nibbles of the same bytes (g = 2, 3): value nibble - 8
@@ -283,20 +293,25 @@ __global__ __launch_bounds__(512) void mm_packed(MmArgs a) {
 #pragma unroll
     for (int nt = 0; nt < NTT; ++nt) acc[rt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  MmW<T> cur[2], nxt[2];
+  // Weights two slices ahead (cur, nxt, nxt2), x one slice ahead.
+  MmW<T> cur[2], nxt[2], nxt2[2];
   float4 xv[4];
   fetch_x(sl0, xv);
 #pragma unroll
   for (int rt = 0; rt < 2; ++rt) cur[rt].load(s, rowc[rt], sl0, g, nsteps(sl0), K);
+  if (sl0 + 1 < sl1) {
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) nxt[rt].load(s, rowc[rt], sl0 + 1, g, nsteps(sl0 + 1), K);
+  }
   put_x(0, xv);
   __syncthreads();
   for (uint32_t sl = sl0; sl < sl1; ++sl) {
     const uint32_t cb = (sl - sl0) & 1u, nst = nsteps(sl);
     const bool more = sl + 1 < sl1;
-    if (more) {  // next slice's x and weights in flight during this slice's math
-      fetch_x(sl + 1, xv);
+    if (more) fetch_x(sl + 1, xv);  // next slice's x in flight during this slice's math
+    if (sl + 2 < sl1) {
 #pragma unroll
-      for (int rt = 0; rt < 2; ++rt) nxt[rt].load(s, rowc[rt], sl + 1, g, nsteps(sl + 1), K);
+      for (int rt = 0; rt < 2; ++rt) nxt2[rt].load(s, rowc[rt], sl + 2, g, nsteps(sl + 2), K);
     }
     const __bf16* xb = xsb + cb * BUF;
     const float* ss = reinterpret_cast<const float*>(xb + 3 * PLANE);
@@ -357,7 +372,10 @@ __global__ __launch_bounds__(512) void mm_packed(MmArgs a) {
     if (more) {
       put_x(cb ^ 1u, xv);  // the other buffer's last reader was slice sl - 1, before the last barrier
 #pragma unroll
-      for (int rt = 0; rt < 2; ++rt) cur[rt] = nxt[rt];
+      for (int rt = 0; rt < 2; ++rt) {
+        cur[rt] = nxt[rt];
+        nxt[rt] = nxt2[rt];
+      }
     }
     __syncthreads();
   }
