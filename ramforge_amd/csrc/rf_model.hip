@@ -957,6 +957,23 @@ int32_t ensure_prefill_ws(rf_model* m) {
   return RF_OK;
 }
 
+// A streaming model gives the prefill workspace back after the prompt: its
+// charge would otherwise hold VRAM the layer cache fills while decoding.
+int32_t release_prefill_ws(rf_model* m) {
+  if (!m->p_h) return RF_OK;
+  int32_t rc = sync(m);
+  if (rc) return rc;
+  for (size_t i = 0; i < m->charges.size(); ++i)
+    if (m->charges[i] == "tmp:prefill") {
+      m->charges.erase(m->charges.begin() + i);
+      break;
+    }
+  m->p_h = m->p_xn = m->p_q = m->p_k = m->p_v = m->p_qr = m->p_a = m->p_act = m->p_up = m->p_part = m->p_att = nullptr;
+  m->p_tok = nullptr;
+  m->p_part_floats = 0;
+  return vram_release(m->ctx, "tmp:prefill");
+}
+
 int32_t enqueue_prefill_layer(rf_model* m, size_t li, uint64_t pos0, uint64_t nt) {
   const rf_model_config& c = m->cfg;
   Layer& L = m->layers[li];
@@ -1067,7 +1084,7 @@ int32_t prefill_tokens(rf_model* m, const uint32_t* tokens, uint64_t n) {
   // the decode path continues from the last token's hidden state and position
   RF_LAUNCH(hipMemcpyAsync(m->hidden, m->p_h + (nt - 1) * d, d * 4, hipMemcpyDeviceToDevice, st), "prefill hidden");
   RF_LAUNCH(launch_set_i32(m->d_pos, (int32_t)m->seq_len, st), "prefill position");
-  return RF_OK;
+  return m->streaming ? release_prefill_ws(m) : RF_OK;
 }
 
 }  // namespace

@@ -189,7 +189,8 @@ def test_prefill_validation(ctx):
 
 def test_prefill_streaming_model(ctx, orc):
     """Layer streaming: a batched prompt loads each layer once per 64-token
-    chunk and gives the resident model's tokens."""
+    chunk, gives the resident model's tokens and hands its workspace back
+    (the layer cache may use that VRAM while decoding)."""
     cfg = dict(TINY, context_length=256)
     rng = np.random.default_rng(3700)
     T = _tiny_tensors(rng, cfg, ALL_Q8)
@@ -203,6 +204,11 @@ def test_prefill_streaming_model(ctx, orc):
         sm.enable_streaming(0)
         for name, (t, ne0, ne1, arr) in T.items():
             sm.set_tensor(name, t, ne0, ne1, arr)
+        used = ctx.vram_used
+        sm.prefill(prompt)
+        # no layer cache: every layer and the prefill workspace are released again
+        assert ctx.vram_used == used
+        sm.reset()
         sm.set_prefill(True)
         assert sm.generate(prompt, 10) == ref
     finally:
