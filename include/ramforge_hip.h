@@ -375,9 +375,10 @@ uint32_t rf_tune_matvec_tile_bytes(uint32_t bytes);
  * are 16-byte aligned (default), 0 = one-shot tile kernel everywhere, other
  * values only query.  Returns the mode in effect (process-wide). */
 int32_t rf_tune_matvec_kernel(int32_t mode);
-/* Weight layout of models created afterwards: 1 = Q8_0 / Q4_0 projection
- * weights are repacked at install into the device-native layout (default),
- * 0 = kept as GGUF bytes; other values only query.  Applies to tensors
+/* Weight layout of models created afterwards: 1 = Q8_0 / Q4_0 / Q4_K / Q6_K
+ * projection weights are repacked at install into the device-native layout
+ * (default; the batched prefill needs it), 0 = kept as GGUF bytes; other
+ * values only query.  Applies to tensors
  * installed after the call.  Returns the mode in effect (process-wide). */
 int32_t rf_tune_packed_weights(int32_t mode);
 

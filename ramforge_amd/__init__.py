@@ -566,9 +566,10 @@ def tune_matvec_kernel(mode: int = -1) -> int:
 
 
 def tune_packed_weights(mode: int = -1) -> int:
-    """1: Q8_0 / Q4_0 projection weights of models are repacked into the
-    device-native layout at install (default), 0: kept as GGUF bytes; -1
-    queries.  Returns the mode in effect."""
+    """1: Q8_0 / Q4_0 / Q4_K / Q6_K projection weights of models are repacked
+    into the device-native layout at install (default; the batched prefill
+    needs it), 0: kept as GGUF bytes; -1 queries.  Returns the mode in
+    effect."""
     return _lib.load().rf_tune_packed_weights(mode)
 
 

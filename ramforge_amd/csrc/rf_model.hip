@@ -55,8 +55,9 @@ struct LayerRes {
   hipEvent_t used = nullptr;      // compute stream: the last kernel reading the layer finished
 };
 
-// Projection weights in Q8_0 / Q4_0 are repacked at install unless disabled
-// (rf_tune_packed_weights); the embedding stays in GGUF layout for its row gather.
+// Projection weights in Q8_0 / Q4_0 / Q4_K / Q6_K are repacked at install
+// unless disabled (rf_tune_packed_weights); the embedding stays in GGUF
+// layout for its row gather.
 static int g_pack_weights = 1;
 
 struct Layer {
