@@ -340,6 +340,48 @@ def prefill_bench(ctx, m, cfg, rf, prompt, long_len: int) -> dict:
     return out
 
 
+def config4_bench(rf, syn, tokens: int = 128, prompt_len: int = 32) -> dict:
+    """random-init llama, 16 layers, d 2048, 32/8 heads, FFN
+    8192, vocab 32000, Q8_0 everywhere, fully resident; 32-token prompt, 128
+    greedy tokens.  Timed: the prompt token by token (the reference's loop) and
+    batched, then the 128 greedy tokens as device decode steps (hipGraph
+    replay; graphs captured in an untimed first pass)."""
+    import numpy as np
+
+    cfg = syn.CONFIG_4
+    specs = syn.llama_specs(cfg, syn.Q8_0, seed=4)
+    wbytes = syn.weight_bytes(specs)
+    ctx = rf.Context(0)
+    m = syn.build_device_model(ctx, cfg, specs, prompt_len + tokens + 8)
+    prompt = [int(t) for t in np.random.default_rng(4).integers(0, cfg["vocab_size"], prompt_len)]
+    t0 = time.perf_counter()
+    for p, t in enumerate(prompt):
+        m.forward(t, p)
+    tbt = time.perf_counter() - t0
+    m.use_graph(True)
+    m.decode_steps(tokens)  # captures the regimes' graphs
+    ctx.synchronize()
+    m.reset()
+    t0 = time.perf_counter()
+    m.prefill(prompt)
+    batched = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    m.decode_steps(tokens)
+    ctx.synchronize()
+    wall = time.perf_counter() - t0
+    out = {"workload": "config 4: 16 layers, d 2048, 32/8 heads, FFN 8192, vocab 32000, Q8_0, resident",
+           "prompt_tokens": prompt_len, "prompt_token_by_token_ms": round(tbt * 1e3, 2),
+           "prompt_batched_ms": round(batched * 1e3, 2), "tokens": tokens, "tok_s": round(tokens / wall, 1),
+           "ms_per_token": round(wall * 1e3 / tokens, 4), "weights_bytes_per_token": wbytes,
+           "roofline_tok_s_at_peak": round(PEAK_HBM_GBS * 1e9 / wbytes, 1),
+           "tokens_head": m.read_tokens(tokens)[:8]}
+    log(f"config 4: prompt {tbt * 1e3:.1f} ms token by token, {batched * 1e3:.1f} ms batched; "
+        f"{out['tok_s']} tok/s decode ({out['ms_per_token']} ms/token; roofline {out['roofline_tok_s_at_peak']})")
+    m.close()
+    ctx.close()
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -357,6 +399,8 @@ def main() -> int:
     ap.add_argument("--kernels", action="store_true",
                     help="kernel-level BASELINE configs 1-3 (matvec formats/shapes, attention contexts) instead of "
                          "the decode benchmark; prints one JSON line")
+    ap.add_argument("--config4", action="store_true",
+                    help="BASELINE config 4 (16-layer d2048 Q8_0 model): prompt and 128-token decode timings")
     ap.add_argument("--config5", type=int, default=0, metavar="TOKENS",
                     help="BASELINE config 5 (Q4_K/Q6_K 8B under a 4 GiB VRAM budget, layer streaming) with TOKENS "
                          "greedy tokens; prints one JSON line")
@@ -377,6 +421,9 @@ def main() -> int:
 
     if args.tile_bytes:
         rf.tune_matvec_tile_bytes(args.tile_bytes)
+    if args.config4:
+        print(json.dumps({"config4": config4_bench(rf, syn)}), flush=True)
+        return 0
     if args.config5:
         res = [config5_bench(rf, syn, args.config5, args.prompt, policy) for policy in (1, 0)]
         print(json.dumps({"config5": res}), flush=True)

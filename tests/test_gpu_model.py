@@ -200,7 +200,8 @@ def test_config4_greedy_tokens_identical(ctx, orc):
     """random-init llama, 16 layers, d 2048, 32/8 heads,
     FFN 8192, vocab 32000, Q8_0 everywhere; 32-token random prompt, 128 greedy
     tokens.  Weights are generated on the device and, byte-identically, on the
-    host for the oracle."""
+    host for the oracle.  The prompt is forwarded token by token and, again,
+    batched (rf_model_prefill)."""
     from ramforge_amd import synthetic as syn
 
     cfg = syn.CONFIG_4
@@ -226,6 +227,12 @@ def test_config4_greedy_tokens_identical(ctx, orc):
         ref, margin = om.generate(prompt, 128)
         first = next((i for i, (a, b) in enumerate(zip(toks, ref)) if a != b), None)
         assert toks == ref, f"first divergence at {first}, top-2 margin there {margin[first]:.3g}"
+        # the same prompt through the batched prefill
+        gm.reset()
+        gm.set_prefill(True)
+        ptoks = gm.generate(prompt, 128)
+        first = next((i for i, (a, b) in enumerate(zip(ptoks, ref)) if a != b), None)
+        assert ptoks == ref, f"batched prompt: first divergence at {first}"
     finally:
         orc.set_parity_threads(0)
         om.close()
