@@ -385,7 +385,7 @@ def config4_bench(rf, syn, tokens: int = 128, prompt_len: int = 32) -> dict:
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=64)
+    ap.add_argument("--steps", type=int, default=128)
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--prompt", type=int, default=32)
     ap.add_argument("--no-graph", action="store_true", help="eager launches instead of hipGraph replay")
