@@ -213,6 +213,9 @@ int32_t rf_rmsnorm(rf_ctx *ctx, const float *x, const float *weight, uint64_t n,
 /* add_reference / mul_reference / silu_reference / swiglu_reference
  * (compute.rs:321-361). */
 int32_t rf_add(rf_ctx *ctx, const float *a, const float *b, uint64_t n, float *out, rf_stream_t stream);
+/* In-place bias add v[i] += bias[i], the qwen2 Q/K/V bias step of
+ * ModelExecutor::execute_layer (runtime/src/model_executor.rs:161-194). */
+int32_t rf_bias_add(rf_ctx *ctx, float *v, const float *bias, uint64_t n, rf_stream_t stream);
 int32_t rf_mul(rf_ctx *ctx, const float *a, const float *b, uint64_t n, float *out, rf_stream_t stream);
 int32_t rf_silu(rf_ctx *ctx, const float *x, uint64_t n, float *out, rf_stream_t stream);
 int32_t rf_swiglu(rf_ctx *ctx, const float *gate, const float *up, uint64_t n, float *out, rf_stream_t stream);

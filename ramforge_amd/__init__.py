@@ -356,6 +356,11 @@ def add(ctx: Context, a, b, n: int, out, stream=None) -> None:
     _lib.check(ctx.lib.rf_add(ctx.handle, _ptr(a), _ptr(b), n, _ptr(out), stream))
 
 
+def bias_add(ctx: Context, v, bias, n: int, stream=None) -> None:
+    """v += bias in place (model_executor.rs:161-194, the Q/K/V bias step)."""
+    _lib.check(ctx.lib.rf_bias_add(ctx.handle, _ptr(v), _ptr(bias), n, stream))
+
+
 def mul(ctx: Context, a, b, n: int, out, stream=None) -> None:
     _lib.check(ctx.lib.rf_mul(ctx.handle, _ptr(a), _ptr(b), n, _ptr(out), stream))
 

@@ -92,6 +92,7 @@ SIGNATURES = {
     "rf_rope": (_i32, [_vp, _fp, _fp, _u64, _u32, _u32, _u32, _f32, _vp]),
     "rf_rmsnorm": (_i32, [_vp, _fp, _fp, _u64, _f32, _fp, _vp]),
     "rf_add": (_i32, [_vp, _fp, _fp, _u64, _fp, _vp]),
+    "rf_bias_add": (_i32, [_vp, _fp, _fp, _u64, _vp]),
     "rf_mul": (_i32, [_vp, _fp, _fp, _u64, _fp, _vp]),
     "rf_silu": (_i32, [_vp, _fp, _u64, _fp, _vp]),
     "rf_swiglu": (_i32, [_vp, _fp, _fp, _u64, _fp, _vp]),

@@ -703,6 +703,13 @@ static int32_t binop(rf_ctx* ctx, int op, const float* a, const float* b, uint64
 int32_t rf_add(rf_ctx* ctx, const float* a, const float* b, uint64_t n, float* out, rf_stream_t s) {
   return binop(ctx, BIN_ADD, a, b, n, out, s);
 }
+int32_t rf_bias_add(rf_ctx* ctx, float* v, const float* bias, uint64_t n, rf_stream_t s) {
+  RF_CHECK_CTX(ctx);
+  if (n == 0) return RF_OK;
+  if (!v || !bias) return set_error(RF_ERR_INVALID, "bias add shape mismatch: null operand");
+  hipError_t e = launch_bias_add(v, bias, n, pick_stream(ctx, s));
+  return e == hipSuccess ? RF_OK : hip_error(e, "bias add launch");
+}
 int32_t rf_mul(rf_ctx* ctx, const float* a, const float* b, uint64_t n, float* out, rf_stream_t s) {
   return binop(ctx, BIN_MUL, a, b, n, out, s);
 }

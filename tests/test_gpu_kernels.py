@@ -499,6 +499,10 @@ def test_elementwise_ops(ctx, orc):
         assert np.array_equal(do.numpy(), orc.add(a, b))
         rf.mul(ctx, da, db, n, do)
         assert np.array_equal(do.numpy(), orc.mul(a, b))
+        dv = ctx.array(a)
+        rf.bias_add(ctx, dv, db, n)  # in place, model_executor.rs:178-186
+        assert np.array_equal(dv.numpy(), orc.add(a, b))
+        dv.free()
         rf.silu(ctx, da, n, do)
         assert_close(do.numpy(), orc.silu(a), 1e-6)
         rf.swiglu(ctx, da, db, n, do)
