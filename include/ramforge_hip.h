@@ -20,8 +20,15 @@
  *     does; the weight bytes are the raw GGUF payload, row-major [out][in]).
  *   - `stream` is a hipStream_t; NULL selects the context's compute stream.
  *     Compute calls are asynchronous with respect to the host.
- *   - No compute call allocates device memory: the context owns grown
- *     workspaces (created on the first call that needs them and kept).
+ *   - Workspaces: rf_attention_decode, rf_matmul_packed and rf_matvec_packed
+ *     with a misaligned x use context-owned workspaces.  The first call that
+ *     needs one (or a larger one) allocates it, synchronising the device
+ *     before freeing a smaller one; later calls allocate nothing.  Calls that
+ *     share a workspace must be ordered (one stream, or events), and a call
+ *     to be captured in a graph must have run once outside the capture.
+ *   - A context is driven from one host thread at a time (the reference
+ *     engine calls from one thread, parallelism is internal); the ledger
+ *     calls (rf_vram_*) and rf_last_error are safe from any thread.
  */
 #ifndef RAMFORGE_HIP_H
 #define RAMFORGE_HIP_H

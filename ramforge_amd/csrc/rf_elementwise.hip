@@ -46,7 +46,9 @@ __global__ void binary_kernel(int op, const float* __restrict__ a, const float* 
 
 hipError_t launch_binary(int op, const float* a, const float* b, uint64_t n, float* out, hipStream_t st) {
   if (n == 0) return hipSuccess;
-  hipLaunchKernelGGL(binary_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, op, a, b, n, out);
+  const uint32_t gb = grid_blocks(n, 256);
+  if (!gb) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(binary_kernel, dim3(gb), dim3(256), 0, st, op, a, b, n, out);
   return hipGetLastError();
 }
 
@@ -59,7 +61,9 @@ __global__ void silu_kernel(const float* __restrict__ x, uint64_t n, float* __re
 
 hipError_t launch_silu(const float* x, uint64_t n, float* y, hipStream_t st) {
   if (n == 0) return hipSuccess;
-  hipLaunchKernelGGL(silu_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, x, n, y);
+  const uint32_t gb = grid_blocks(n, 256);
+  if (!gb) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(silu_kernel, dim3(gb), dim3(256), 0, st, x, n, y);
   return hipGetLastError();
 }
 
@@ -70,7 +74,9 @@ __global__ void bias_add_kernel(float* __restrict__ v, const float* __restrict__
 
 hipError_t launch_bias_add(float* v, const float* b, uint64_t n, hipStream_t st) {
   if (n == 0) return hipSuccess;
-  hipLaunchKernelGGL(bias_add_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, v, b, n);
+  const uint32_t gb = grid_blocks(n, 256);
+  if (!gb) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(bias_add_kernel, dim3(gb), dim3(256), 0, st, v, b, n);
   return hipGetLastError();
 }
 
@@ -261,7 +267,9 @@ hipError_t launch_dequant_rows(uint32_t t, const void* wv, uint64_t in_dim, uint
   if (rows == 0 || in_dim == 0) return hipSuccess;
   if (t == T_F32 || t == T_F16 || t == T_BF16) {
     const uint64_t n = rows * in_dim;
-    hipLaunchKernelGGL(decode_plain_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, t, w, in_dim, rows,
+    const uint32_t gb = n / rows == in_dim ? grid_blocks(n, 256) : 0u;
+    if (!gb) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(decode_plain_kernel, dim3(gb), dim3(256), 0, st, t, w, in_dim, rows,
                        out, token_index, token_rows);
     return hipGetLastError();
   }
@@ -269,7 +277,9 @@ hipError_t launch_dequant_rows(uint32_t t, const void* wv, uint64_t in_dim, uint
   if (!type_geometry(t, &qk, &bs)) return hipErrorInvalidValue;
   const uint64_t row_bytes = in_dim / qk * bs;
   const uint64_t n = rows * (in_dim / 32);
-  const dim3 grid((unsigned)((n + 255) / 256)), blk(256);
+  const uint32_t gb = n / rows == in_dim / 32 ? grid_blocks(n, 256) : 0u;
+  if (!gb || in_dim > 0xFFFFFFFFull) return hipErrorInvalidValue;
+  const dim3 grid(gb), blk(256);
   switch (t) {
 #define RF_DQ(TT) case TT: hipLaunchKernelGGL(dequant_kernel<TT>, grid, blk, 0, st, w, (uint32_t)in_dim, rows, row_bytes, out, token_index, token_rows); break;
     RF_DQ(T_Q4_0) RF_DQ(T_Q5_0) RF_DQ(T_Q8_0) RF_DQ(T_Q2_K) RF_DQ(T_Q3_K) RF_DQ(T_Q4_K) RF_DQ(T_Q5_K)
@@ -307,7 +317,9 @@ hipError_t launch_set_i32(int32_t* p, int32_t v, hipStream_t st) {
 
 hipError_t launch_fill(float* p, float v, uint64_t n, hipStream_t st) {
   if (n == 0) return hipSuccess;
-  hipLaunchKernelGGL(fill_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, p, v, n);
+  const uint32_t gb = grid_blocks(n, 256);
+  if (!gb) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(fill_kernel, dim3(gb), dim3(256), 0, st, p, v, n);
   return hipGetLastError();
 }
 
@@ -442,7 +454,9 @@ hipError_t launch_synth(uint32_t t, uint64_t seed, uint64_t first, uint64_t nblk
   if (nblk == 0) return hipSuccess;
   const uint64_t ss = host_synth_u64(seed ^ 0xA5A5A5A5A5A5A5A5ull, 0);
   const uint64_t sc = host_synth_u64(seed ^ 0x3C3C3C3C3C3C3C3Cull, 0);
-  hipLaunchKernelGGL(synth_kernel, dim3((unsigned)((nblk + 255) / 256)), dim3(256), 0, st, t, ss, sc, first, nblk,
+  const uint32_t gb = grid_blocks(nblk, 256);
+  if (!gb) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(synth_kernel, dim3(gb), dim3(256), 0, st, t, ss, sc, first, nblk,
                      mul, static_cast<uint8_t*>(dst), (uint32_t)bs);
   return hipGetLastError();
 }

@@ -7,6 +7,14 @@ namespace rf {
 
 enum { EPI_STORE = 0, EPI_RESIDUAL = 1, EPI_SWIGLU = 2 };
 
+// Workgroups of `per` threads that cover n > 0 items, or 0 when that exceeds
+// the 2^31 - 1 workgroups of a grid dimension: the launcher then fails
+// instead of covering a truncated range.
+inline uint32_t grid_blocks(uint64_t n, uint32_t per) {
+  const uint64_t b = (n + per - 1) / per;
+  return b > 0x7FFFFFFFull ? 0u : (uint32_t)b;
+}
+
 struct MvSeg {
   const uint8_t* w;
   float* y;

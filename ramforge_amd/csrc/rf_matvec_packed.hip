@@ -599,7 +599,7 @@ static hipError_t launch_pk(const PkArgs& a, uint32_t lds, hipStream_t st) {
 // gate/up, whose step loads two matrices; Q6_K, with three more loads per
 // chunk, one less doubling); 1024-thread workgroups when x fills more than
 // 40 KB of LDS (two resident workgroups then still give 32 wavefronts per
-// CU), else 512.
+// CU), else 512 (always 512 for Q6_K gate/up).
 template <uint32_t T, int EPI, bool NORM>
 static hipError_t launch_pk_l(const PkArgs& a, uint32_t lds, hipStream_t st) {
   const uint64_t nchunk = pk_nchunk(T, a.in_dim);
@@ -607,12 +607,20 @@ static hipError_t launch_pk_l(const PkArgs& a, uint32_t lds, hipStream_t st) {
   if (T == T_Q6_K) pref /= 2;
   uint32_t lpw = 1;
   while (lpw * 2 <= pref && lpw * 2 <= nchunk) lpw *= 2;
-  const bool big = lds > 40960;
+  // Q6_K gate/up keeps 512 threads: its two streams of four regions do not
+  // fit the 128 VGPRs of a 1024-thread workgroup (that form spilled to
+  // scratch), so it is never instantiated.
+  constexpr bool WIDE = !(T == T_Q6_K && EPI == EPI_SWIGLU);
+  const bool big = WIDE && lds > 40960;
   switch (lpw * 2 + (big ? 1 : 0)) {
     case 2: return launch_pk<T, EPI, NORM, 1, 2, 512>(a, lds, st);
-    case 3: return launch_pk<T, EPI, NORM, 1, 2, 1024>(a, lds, st);
+    case 3:
+      if constexpr (WIDE) return launch_pk<T, EPI, NORM, 1, 2, 1024>(a, lds, st);
+      return hipErrorInvalidValue;
     case 4: return launch_pk<T, EPI, NORM, 2, 2, 512>(a, lds, st);
-    case 5: return launch_pk<T, EPI, NORM, 2, 2, 1024>(a, lds, st);
+    case 5:
+      if constexpr (WIDE) return launch_pk<T, EPI, NORM, 2, 2, 1024>(a, lds, st);
+      return hipErrorInvalidValue;
     case 8:
       if constexpr (T != T_Q6_K && EPI != EPI_SWIGLU) return launch_pk<T, EPI, NORM, 4, 2, 512>(a, lds, st);
       return hipErrorInvalidValue;
@@ -689,7 +697,9 @@ hipError_t launch_pack(uint32_t t, const void* raw, void* packed, uint64_t rows,
   if (!packed_type(t) || in_dim % pk_qk(t) != 0) return hipErrorInvalidValue;
   const uint64_t n = rows * (in_dim / pk_qk(t));
   if (n == 0) return hipSuccess;
-  const dim3 grid((unsigned)((n + 255) / 256));
+  const uint32_t gb = n / rows == in_dim / pk_qk(t) ? grid_blocks(n, 256) : 0u;
+  if (!gb) return hipErrorInvalidValue;
+  const dim3 grid(gb);
   const uint8_t* r = static_cast<const uint8_t*>(raw);
   uint8_t* o = static_cast<uint8_t*>(packed);
   switch (t) {

@@ -120,11 +120,17 @@ int32_t charge_alloc(rf_model* m, const std::string& name, uint64_t bytes, void*
   return rc;
 }
 
+// Free a buffer made by charge_alloc and forget its charge.
+int32_t release_charge(rf_model* m, const std::string& name) {
+  const int32_t rc = vram_release(m->ctx, name);
+  for (size_t i = 0; i < m->charges.size(); ++i)
+    if (m->charges[i] == name) { m->charges.erase(m->charges.begin() + i); break; }
+  return rc;
+}
+
 int32_t drop_tensor(rf_model* m, DevTensor& t) {
   if (!t.present()) return RF_OK;
-  int32_t rc = vram_release(m->ctx, t.charge);
-  for (size_t i = 0; i < m->charges.size(); ++i)
-    if (m->charges[i] == t.charge) { m->charges.erase(m->charges.begin() + i); break; }
+  const int32_t rc = release_charge(m, t.charge);
   t = DevTensor{};
   return rc;
 }
@@ -564,6 +570,14 @@ int32_t install(rf_model* m, const char* cname, uint32_t t, uint64_t ne0, uint64
   void* d = nullptr;
   rc = charge_alloc(m, charge, final_bytes, &d);
   if (rc) return rc;
+  // Any failure from here on releases the new buffer and its charge (the slot
+  // is already empty): the model is left as if the call had not been made
+  // but for the dropped old tensor, and the same call can be retried.
+  auto fail = [&](int32_t code) {
+    hipStreamSynchronize(ctx->compute);  // nothing may still write into d
+    release_charge(m, charge);
+    return code;
+  };
   if (synth) {
     uint64_t qk = 1, bs = 4;
     type_geometry(t, &qk, &bs);
@@ -571,11 +585,11 @@ int32_t install(rf_model* m, const char* cname, uint32_t t, uint64_t ne0, uint64
     if (t == T_F32 && !std::isnan(constant)) e = launch_fill(static_cast<float*>(d), constant, ne0 * ne1, ctx->compute);
     else e = launch_synth(t, seed, 0, nblk, mul, d, ctx->compute);
     if (e == hipSuccess) e = hipStreamSynchronize(ctx->compute);
-    if (e != hipSuccess) return hip_error(e, "tensor synthesis");
+    if (e != hipSuccess) return fail(hip_error(e, "tensor synthesis"));
   } else if (widen) {
     void* tmp = nullptr;
     rc = vram_alloc(ctx, "tmp:load:" + name, bytes, &tmp);
-    if (rc) return rc;
+    if (rc) return fail(rc);
     rc = staged_upload(ctx, tmp, host, bytes);
     if (rc == RF_OK) {
       e = launch_dequant_rows(t, tmp, ne0, ne1, static_cast<float*>(d), nullptr, 0, ctx->compute);
@@ -583,24 +597,24 @@ int32_t install(rf_model* m, const char* cname, uint32_t t, uint64_t ne0, uint64
       if (e != hipSuccess) rc = hip_error(e, "F16/BF16 widen");
     }
     const int32_t rc2 = vram_release(ctx, "tmp:load:" + name);
-    if (rc) return rc;
-    if (rc2) return rc2;
+    if (rc) return fail(rc);
+    if (rc2) return fail(rc2);
   } else {
     rc = staged_upload(ctx, d, host, bytes);
-    if (rc) return rc;
+    if (rc) return fail(rc);
   }
   bool packed = false;
   if (g_pack_weights && is_projection(name) && plan_packed(t, ne0).ok) {
     // GGUF -> packed through a temporary copy (install time only)
     void* tmp = nullptr;
     rc = vram_alloc(ctx, "tmp:pack:" + name, bytes, &tmp);
-    if (rc) return rc;
+    if (rc) return fail(rc);
     e = launch_pack(t, d, tmp, ne1, ne0, ctx->compute);
     if (e == hipSuccess) e = hipMemcpyAsync(d, tmp, bytes, hipMemcpyDeviceToDevice, ctx->compute);
     if (e == hipSuccess) e = hipStreamSynchronize(ctx->compute);
     const int32_t rc2 = vram_release(ctx, "tmp:pack:" + name);
-    if (e != hipSuccess) return hip_error(e, "weight packing");
-    if (rc2) return rc2;
+    if (e != hipSuccess) return fail(hip_error(e, "weight packing"));
+    if (rc2) return fail(rc2);
     packed = true;
   }
   slot->type = widen ? T_F32 : t;
@@ -964,15 +978,10 @@ int32_t release_prefill_ws(rf_model* m) {
   if (!m->p_h) return RF_OK;
   int32_t rc = sync(m);
   if (rc) return rc;
-  for (size_t i = 0; i < m->charges.size(); ++i)
-    if (m->charges[i] == "tmp:prefill") {
-      m->charges.erase(m->charges.begin() + i);
-      break;
-    }
   m->p_h = m->p_xn = m->p_q = m->p_k = m->p_v = m->p_qr = m->p_a = m->p_act = m->p_up = m->p_part = m->p_att = nullptr;
   m->p_tok = nullptr;
   m->p_part_floats = 0;
-  return vram_release(m->ctx, "tmp:prefill");
+  return release_charge(m, "tmp:prefill");
 }
 
 int32_t enqueue_prefill_layer(rf_model* m, size_t li, uint64_t pos0, uint64_t nt) {
@@ -1107,6 +1116,17 @@ int32_t rf_model_create(rf_ctx* ctx, const rf_model_config* cfg, uint64_t kv_cap
     return set_error(RF_ERR_INVALID, "KV capacity %llu must be in 1..=context_length %llu",
                      (unsigned long long)kv_cap, (unsigned long long)c.context_length);
   if (c.vocab_size > 0xFFFFFFFFull) return set_error(RF_ERR_UNSUPPORTED, "vocabulary exceeds 2^32 entries");
+  // The kernels index rows, heads and positions with 32 bits, and every size
+  // below is then far from wrapping: widths and positions below 2^24, at
+  // most 2^16 heads and layers, and KV caches within 64 bits.
+  constexpr uint64_t kDim = 1ull << 24, kCount = 1ull << 16;
+  uint64_t kv_bytes = 0;
+  if (c.embedding_length > kDim || c.feed_forward_length > kDim || c.vocab_size > kDim ||
+      c.head_count * c.head_dim > kDim || c.head_count > kCount || c.block_count > kCount || kv_cap > kDim ||
+      __builtin_mul_overflow(c.block_count * kv_cap, c.head_count_kv * c.head_dim * 4, &kv_bytes))
+    return set_error(RF_ERR_UNSUPPORTED,
+                     "model dimensions out of range: widths, vocabulary and KV capacity must be below 2^24, heads "
+                     "and layers at most 2^16");
   rf_model* m = new rf_model();
   m->ctx = ctx;
   m->cfg = c;
@@ -1114,7 +1134,6 @@ int32_t rf_model_create(rf_ctx* ctx, const rf_model_config* cfg, uint64_t kv_cap
   m->layers.resize(c.block_count);
   const uint64_t d = c.embedding_length, qd = c.head_count * c.head_dim, kvd = c.head_count_kv * c.head_dim;
   const uint64_t f = c.feed_forward_length;
-  const uint64_t kv_bytes = c.block_count * kv_cap * kvd * 4;
   void* p = nullptr;
   int32_t rc = charge_alloc(m, "kv_cache:k", kv_bytes, &p);
   if (rc) { rf_model_destroy(m); return rc; }

@@ -55,9 +55,10 @@ struct rf_ctx {
   rf::Workspace attn_ws, scratch_ws, mm_ws;
   float* amax_val = nullptr;
   uint32_t* amax_idx = nullptr;
+  std::mutex stage_mu;  // guards the staging buffers below (one upload at a time)
   void* pinned_stage[2] = {nullptr, nullptr};
   hipEvent_t stage_ev[2] = {nullptr, nullptr};
-  uint64_t stage_bytes = 0;
+  uint64_t stage_bytes = 0;  // 0 until both buffers and events exist
 };
 
 namespace rf {

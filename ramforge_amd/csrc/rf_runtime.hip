@@ -175,12 +175,27 @@ int32_t ensure_workspace(rf_ctx* ctx, Workspace& ws, const char* charge, uint64_
 
 int32_t staged_upload(rf_ctx* ctx, void* dst, const void* src, uint64_t bytes) {
   constexpr uint64_t kStage = 64ull << 20;
-  if (!ctx->pinned_stage[0]) {
+  // one upload at a time: the two pinned buffers are the context's
+  std::lock_guard<std::mutex> lk(ctx->stage_mu);
+  if (!ctx->stage_bytes) {
+    // all four objects or none: a later call never finds half a set
+    void* pb[2] = {nullptr, nullptr};
+    hipEvent_t ev[2] = {nullptr, nullptr};
+    hipError_t e = hipSuccess;
+    for (int i = 0; i < 2 && e == hipSuccess; ++i) {
+      e = hipHostMalloc(&pb[i], kStage, hipHostMallocDefault);
+      if (e == hipSuccess) e = hipEventCreateWithFlags(&ev[i], hipEventDisableTiming);
+    }
+    if (e != hipSuccess) {
+      for (int i = 0; i < 2; ++i) {
+        if (pb[i]) hipHostFree(pb[i]);
+        if (ev[i]) hipEventDestroy(ev[i]);
+      }
+      return hip_error(e, "pinned staging setup");
+    }
     for (int i = 0; i < 2; ++i) {
-      hipError_t e = hipHostMalloc(&ctx->pinned_stage[i], kStage, hipHostMallocDefault);
-      if (e != hipSuccess) return hip_error(e, "hipHostMalloc");
-      e = hipEventCreateWithFlags(&ctx->stage_ev[i], hipEventDisableTiming);
-      if (e != hipSuccess) return hip_error(e, "hipEventCreate");
+      ctx->pinned_stage[i] = pb[i];
+      ctx->stage_ev[i] = ev[i];
     }
     ctx->stage_bytes = kStage;
   }
@@ -188,22 +203,30 @@ int32_t staged_upload(rf_ctx* ctx, void* dst, const void* src, uint64_t bytes) {
   uint8_t* d = static_cast<uint8_t*>(dst);
   int buf = 0;
   bool used[2] = {false, false};
-  for (uint64_t off = 0; off < bytes; off += kStage) {
+  hipError_t e = hipSuccess;
+  const char* what = "";
+  for (uint64_t off = 0; off < bytes && e == hipSuccess; off += kStage) {
     const uint64_t n = bytes - off < kStage ? bytes - off : kStage;
     if (used[buf]) {
-      hipError_t e = hipEventSynchronize(ctx->stage_ev[buf]);
-      if (e != hipSuccess) return hip_error(e, "hipEventSynchronize");
+      e = hipEventSynchronize(ctx->stage_ev[buf]);
+      what = "hipEventSynchronize";
+      if (e != hipSuccess) break;
     }
     std::memcpy(ctx->pinned_stage[buf], s + off, n);
-    hipError_t e = hipMemcpyAsync(d + off, ctx->pinned_stage[buf], n, hipMemcpyHostToDevice, ctx->copy);
-    if (e != hipSuccess) return hip_error(e, "hipMemcpyAsync");
-    e = hipEventRecord(ctx->stage_ev[buf], ctx->copy);
-    if (e != hipSuccess) return hip_error(e, "hipEventRecord");
+    e = hipMemcpyAsync(d + off, ctx->pinned_stage[buf], n, hipMemcpyHostToDevice, ctx->copy);
+    what = "hipMemcpyAsync";
+    if (e == hipSuccess) {
+      e = hipEventRecord(ctx->stage_ev[buf], ctx->copy);
+      what = "hipEventRecord";
+    }
     used[buf] = true;
     buf ^= 1;
   }
-  hipError_t e = hipStreamSynchronize(ctx->copy);
-  if (e != hipSuccess) return hip_error(e, "hipStreamSynchronize");
+  // also on failure: no copy may still read a staging buffer when the next
+  // upload refills it
+  const hipError_t es = hipStreamSynchronize(ctx->copy);
+  if (e != hipSuccess) return hip_error(e, what);
+  if (es != hipSuccess) return hip_error(es, "hipStreamSynchronize");
   return RF_OK;
 }
 
@@ -260,8 +283,9 @@ int32_t rf_ctx_create(int32_t device, uint64_t budget, rf_ctx** out) {
   hipError_t e = hipStreamCreateWithFlags(&c->compute, hipStreamNonBlocking);
   if (e == hipSuccess) e = hipStreamCreateWithFlags(&c->copy, hipStreamNonBlocking);
   if (e != hipSuccess) {
-    delete c;
-    return hip_error(e, "hipStreamCreate");
+    const int32_t rc = hip_error(e, "hipStreamCreate");
+    rf_ctx_destroy(c);  // the stream that was created, if any
+    return rc;
   }
   void* p = nullptr;
   int32_t rc = vram_alloc(c, "workspace:argmax", 256 * 8 + 64, &p);
@@ -337,9 +361,21 @@ int32_t rf_vram_charge(rf_ctx* ctx, const char* charge, uint64_t* bytes) {
   return RF_OK;
 }
 
-uint64_t rf_vram_used(rf_ctx* ctx) { return ctx ? ctx->ledger.used() : 0; }
-uint64_t rf_vram_total(rf_ctx* ctx) { return ctx ? ctx->ledger.total() : 0; }
-uint64_t rf_vram_peak(rf_ctx* ctx) { return ctx ? ctx->ledger.peak() : 0; }
+uint64_t rf_vram_used(rf_ctx* ctx) {
+  if (!ctx) return 0;
+  std::lock_guard<std::mutex> lk(ctx->mu);
+  return ctx->ledger.used();
+}
+uint64_t rf_vram_total(rf_ctx* ctx) {
+  if (!ctx) return 0;
+  std::lock_guard<std::mutex> lk(ctx->mu);
+  return ctx->ledger.total();
+}
+uint64_t rf_vram_peak(rf_ctx* ctx) {
+  if (!ctx) return 0;
+  std::lock_guard<std::mutex> lk(ctx->mu);
+  return ctx->ledger.peak();
+}
 
 int32_t rf_pinned_alloc(rf_ctx* ctx, uint64_t bytes, void** out) {
   RF_CHECK_CTX(ctx);
@@ -398,6 +434,7 @@ int32_t rf_copy_async(rf_ctx* ctx, void* dst, const void* src, uint64_t bytes, r
 
 int32_t rf_event_create(rf_ctx* ctx, void** ev) {
   RF_CHECK_CTX(ctx);
+  if (!ev) return set_error(RF_ERR_INVALID, "null event output");
   hipEvent_t e;
   RF_HIP(hipEventCreate(&e), "hipEventCreate");
   *ev = e;
@@ -435,6 +472,10 @@ int32_t rf_event_synchronize(rf_ctx* ctx, void* ev) {
 }
 
 // ------------------------------------------------------------------ matvec
+// a * b into *r; false when the product does not fit in 64 bits (a size
+// computed from caller shapes must not wrap past the bounds checks).
+static bool mul_u64(uint64_t a, uint64_t b, uint64_t* r) { return !__builtin_mul_overflow(a, b, r); }
+
 // Shared argument validation of the matvec entry points, in the reference's
 // order and wording (quant.rs:907-975, backend.rs:173-199).  On success
 // *count is the number of rows to compute and *rb the bytes per row; a zero
@@ -461,14 +502,18 @@ static int32_t validate_matvec(rf_ctx* ctx, uint32_t t, const void* w, uint64_t 
                      (unsigned long long)row_start, (unsigned long long)(row_start + count),
                      (unsigned long long)out_dim);
   const uint64_t rb = in_dim / qk * bs;
-  if (w_bytes < out_dim * rb) {
+  uint64_t need = 0;
+  if (!mul_u64(out_dim, rb, &need))
+    return set_error(RF_ERR_INVALID, "%s weight size of %llu rows of %llu overflows 64 bits", nm,
+                     (unsigned long long)out_dim, (unsigned long long)in_dim);
+  if (w_bytes < need) {
     if (t == T_F32)
       return set_error(RF_ERR_INVALID,
                        "backend matvec arity mismatch (ggml layout [in, out]): shape [%llu, %llu] requires %llu weight bytes, got %llu",
-                       (unsigned long long)in_dim, (unsigned long long)out_dim, (unsigned long long)(out_dim * rb),
+                       (unsigned long long)in_dim, (unsigned long long)out_dim, (unsigned long long)need,
                        (unsigned long long)w_bytes);
     return set_error(RF_ERR_INVALID, "%s weight truncated: expected %llu bytes, got %llu", nm,
-                     (unsigned long long)(out_dim * rb), (unsigned long long)w_bytes);
+                     (unsigned long long)need, (unsigned long long)w_bytes);
   }
   *count_out = count;
   *rb_out = rb;
@@ -514,7 +559,10 @@ int32_t rf_pack_weights(rf_ctx* ctx, uint32_t t, const void* raw, uint64_t raw_b
   if (in_dim % qk != 0)
     return set_error(RF_ERR_INVALID, "%s in_dim %llu not divisible by %llu", nm, (unsigned long long)in_dim,
                      (unsigned long long)qk);
-  const uint64_t need = rows * (in_dim / qk) * bs;
+  uint64_t need = 0;
+  if (!mul_u64(rows, in_dim / qk * bs, &need))
+    return set_error(RF_ERR_INVALID, "%s weight size of %llu rows of %llu overflows 64 bits", nm,
+                     (unsigned long long)rows, (unsigned long long)in_dim);
   if (raw_bytes < need)
     return set_error(RF_ERR_INVALID, "%s weight truncated: expected %llu bytes, got %llu", nm,
                      (unsigned long long)need, (unsigned long long)raw_bytes);
@@ -572,7 +620,11 @@ int32_t rf_matmul_packed(rf_ctx* ctx, uint32_t t, const void* packed, uint64_t p
     return set_error(RF_ERR_INVALID, "%s row size %llu not divisible by block size %llu", nm,
                      (unsigned long long)in_dim, (unsigned long long)qk);
   if (out_dim == 0 || n_tokens == 0) return RF_OK;
-  const uint64_t need = out_dim * (in_dim / qk * bs);
+  uint64_t need = 0, xn = 0, yn = 0;
+  if (!mul_u64(out_dim, in_dim / qk * bs, &need) || !mul_u64(n_tokens, in_dim, &xn) || !mul_u64(xn, 4, &xn) ||
+      !mul_u64(n_tokens, out_dim, &yn) || !mul_u64(yn, 4, &yn))
+    return set_error(RF_ERR_INVALID, "%s matmul of %llu tokens x %llu rows of %llu overflows 64 bits", nm,
+                     (unsigned long long)n_tokens, (unsigned long long)out_dim, (unsigned long long)in_dim);
   if (packed_bytes < need)
     return set_error(RF_ERR_INVALID, "%s tensor truncated: %llu bytes for %llu rows of %llu (need %llu)", nm,
                      (unsigned long long)packed_bytes, (unsigned long long)out_dim, (unsigned long long)in_dim,
@@ -619,7 +671,10 @@ int32_t rf_dequantize_rows(rf_ctx* ctx, uint32_t t, const void* w, uint64_t w_by
     return set_error(RF_ERR_INVALID, "%s row size %llu not divisible by block size %llu", nm,
                      (unsigned long long)in_dim, (unsigned long long)qk);
   const uint64_t rb = in_dim / qk * bs;
-  const uint64_t need = (row_start + row_count) * rb;
+  uint64_t need = 0;
+  if (row_start + row_count < row_start || !mul_u64(row_start + row_count, rb, &need))
+    return set_error(RF_ERR_INVALID, "%s row range %llu + %llu overflows 64 bits", nm,
+                     (unsigned long long)row_start, (unsigned long long)row_count);
   if (w_bytes < need)
     return set_error(RF_ERR_INVALID, "%s row truncated: expected %llu bytes, got %llu", nm,
                      (unsigned long long)need, (unsigned long long)w_bytes);
@@ -640,6 +695,7 @@ int32_t rf_attention_decode(rf_ctx* ctx, const float* q, const float* kh, const 
     return set_error(RF_ERR_INVALID, "GQA requires query_heads %u to be divisible by kv_heads %u", qh, kvh);
   if (!q || !kc || !vc || !out || (hist > 0 && (!kh || !vh)))
     return set_error(RF_ERR_INVALID, "attention tensor shape mismatch");
+  if (hist == UINT32_MAX) return set_error(RF_ERR_UNSUPPORTED, "attention over more than 2^32 - 1 positions");
   const uint32_t total = hist + 1;
   AttnArgs a{};
   a.q = q; a.k_hist = kh; a.v_hist = vh; a.k_cur = kc; a.v_cur = vc; a.out = out;

@@ -83,6 +83,11 @@ def test_dequant_validation(ctx):
         rf.dequantize_rows(ctx, Q8_0, w, 64, 0, 1, out)
     with pytest.raises(rf.RamforgeError, match="not divisible"):
         rf.dequantize_rows(ctx, Q8_0, w, 31, 0, 1, out)
+    # sizes computed from the shape must not wrap past the bounds check
+    with pytest.raises(rf.RamforgeError, match="overflows"):
+        rf.dequantize_rows(ctx, Q8_0, w, 1 << 40, 1 << 30, 1 << 30, out)
+    with pytest.raises(rf.RamforgeError, match="overflows"):
+        rf.dequantize_rows(ctx, Q8_0, w, 32, (1 << 64) - 2, 4, out)
     w.free()
     out.free()
 
@@ -259,6 +264,8 @@ def test_matvec_packed_validation(ctx):
         rf.matvec_packed(ctx, Q8_0, w, (1, 128), x, y, 2)
     with pytest.raises(rf.RamforgeError, match="does not support"):
         rf.matvec_packed(ctx, Q5_K, w, (1, 256), x, y)
+    with pytest.raises(rf.RamforgeError, match="overflows"):  # 2^40 rows of 2^40 elements
+        rf.matvec_packed(ctx, Q8_0, w, (1 << 40, 1 << 40), x, y, 0, 1)
     assert y.numpy().tolist() == [7.0, 7.0]  # destination untouched
     assert not rf.packed_supported(Q8_0, 1 << 16) and rf.packed_supported(Q4_0, 14336)
     assert rf.packed_supported(Q8_0, 14336) and not rf.packed_supported(Q8_0, 100)

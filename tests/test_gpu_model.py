@@ -106,6 +106,80 @@ def test_tiny_model_forward_and_generate(ctx, orc, kind, bias, layout_mode):
     _rf().tune_matvec_kernel(1)
 
 
+# Q6_K gate/up over an 8448-wide hidden state: x fills 43.5 KB of LDS, the
+# size at which the packed matvec would use 1024-thread workgroups; the Q6_K
+# gate/up kernel stays at 512 (its 1024-thread form spilled to scratch).
+WIDE_CFG = dict(TINY, embedding_length=8448, feed_forward_length=256, block_count=1)
+WIDE_Q6 = dict(ALL_Q8, gate=Q6_K, up=Q6_K)
+
+
+def test_wide_hidden_q6k_gateup(ctx, orc):
+    rng = np.random.default_rng(970)
+    T = _tiny_tensors(rng, WIDE_CFG, WIDE_Q6)
+    print("  wide hidden 8448, Q6_K gate/up", flush=True)
+    gm = _load_gpu(ctx, WIDE_CFG, T, 16)
+    om = orc.Model(WIDE_CFG, T, kv_capacity=16, threads=8)
+    try:
+        for pos, tok in enumerate([5, 17, 90, 3]):
+            h = gm.forward(tok, pos, want_hidden=True)
+            hr = om.forward(tok, pos)
+            assert np.max(np.abs(h - hr)) <= 2e-4 * max(1.0, np.abs(hr).max()), pos
+            # the output stage on the same input: the 8448-term projection
+            # amplifies the hidden state's allowed difference past the bound
+            lr = om.logits(h)
+            assert np.max(np.abs(gm.logits() - lr)) <= 2e-4 * max(1.0, np.abs(lr).max()), pos
+    finally:
+        gm.close()
+        om.close()
+
+
+def test_model_create_validation(ctx):
+    rf = _rf()
+    used = ctx.vram_used
+    bad = [(dict(TINY, head_dim=0), "non-zero"), (dict(TINY, head_count_kv=3), "divisible"),
+           (dict(TINY, head_dim=33), "even"), (dict(TINY, vocab_size=1 << 25), "out of range"),
+           (dict(TINY, block_count=1 << 17), "out of range"),
+           (dict(TINY, embedding_length=1 << 25), "out of range")]
+    for cfg, msg in bad:
+        with pytest.raises(rf.RamforgeError, match=msg):
+            rf.GpuLlamaModel(ctx, cfg, 16)
+    with pytest.raises(rf.RamforgeError, match="context_length"):
+        rf.GpuLlamaModel(ctx, TINY, TINY["context_length"] + 1)
+    assert ctx.vram_used == used
+
+
+def test_set_tensor_failure_rolls_back(ctx):
+    """A set_tensor that fails after its buffer was charged (here: no room for
+    the temporary packing copy) frees the buffer and drops the charge, so the
+    same call can succeed later (load_layer's rollback rule,
+    streaming_model.rs:581-847)."""
+    rf = _rf()
+    T = _tiny_tensors(np.random.default_rng(980), TINY, ALL_Q8)
+    name, charge = "blk.0.attn_q.weight", "layer:0:attn_q.weight"
+    t, ne0, ne1, arr = T[name]
+    with rf.Context(0) as probe:
+        pm = rf.GpuLlamaModel(probe, TINY, 16)
+        base = probe.vram_used
+        pm.close()
+    with rf.Context(0, vram_budget_bytes=base + arr.nbytes + arr.nbytes // 2) as small:
+        m = rf.GpuLlamaModel(small, TINY, 16)
+        try:
+            assert small.vram_used == base
+            with pytest.raises(rf.RamforgeError, match="insufficient memory"):
+                m.set_tensor(name, t, ne0, ne1, arr)
+            assert small.vram_used == base
+            assert small.charge(charge) is None
+            old = rf.tune_packed_weights(-1)
+            rf.tune_packed_weights(0)  # no packing copy: the tensor alone fits
+            try:
+                m.set_tensor(name, t, ne0, ne1, arr)
+            finally:
+                rf.tune_packed_weights(old)
+            assert small.charge(charge) == arr.nbytes
+        finally:
+            m.close()
+
+
 def test_generate_stop_rules(ctx, orc):
     rng = np.random.default_rng(950)
     T = _tiny_tensors(rng, TINY, ALL_Q8)
