@@ -1054,7 +1054,7 @@ int32_t enqueue_prefill_layer(rf_model* m, size_t li, uint64_t pos0, uint64_t nt
 
 int32_t prefill_tokens(rf_model* m, const uint32_t* tokens, uint64_t n) {
   if (n == 0) return RF_OK;
-  if (m->seq_len + n > m->kv_cap) return set_error(RF_ERR_INVALID, "KV cache full");
+  if (n > m->kv_cap - m->seq_len) return set_error(RF_ERR_INVALID, "KV cache full");  // seq_len <= kv_cap
   for (uint64_t i = 0; i < n; ++i)
     if (tokens[i] >= m->cfg.vocab_size)
       return set_error(RF_ERR_INVALID, "token_id %u out of bounds for embedding with %llu rows", tokens[i],
@@ -1280,7 +1280,7 @@ int32_t rf_model_generate(rf_model* m, const uint32_t* prompt, uint64_t plen, ui
   *n_out = 0;
   const uint64_t ctx_len = m->cfg.context_length;
   // inference.rs:465-476: the request must fit the context.
-  if (plen + max_tokens > ctx_len)
+  if (plen > ctx_len || max_tokens > ctx_len - plen)
     return set_error(RF_ERR_INVALID, "prompt (%llu tokens) plus max_tokens (%llu) exceeds context length %llu",
                      (unsigned long long)plen, (unsigned long long)max_tokens, (unsigned long long)ctx_len);
   if (m->prefill_batched) {
@@ -1331,7 +1331,7 @@ int32_t rf_model_use_graph(rf_model* m, int32_t enable) {
 int32_t rf_model_decode_steps(rf_model* m, uint64_t steps) {
   if (!m) return set_error(RF_ERR_INVALID, "null model");
   if (m->seq_len == 0) return set_error(RF_ERR_INVALID, "decode requires a forwarded prompt");
-  if (m->seq_len + steps > m->kv_cap) return set_error(RF_ERR_INVALID, "KV cache full");
+  if (steps > m->kv_cap - m->seq_len) return set_error(RF_ERR_INVALID, "KV cache full");  // seq_len <= kv_cap
   int32_t rc = check_ready(m);
   if (rc) return rc;
   hipStream_t st = m->ctx->compute;
@@ -1374,9 +1374,12 @@ int32_t rf_model_time_kernel(rf_model* m, uint32_t kind, uint32_t reps, float* a
     return set_error(RF_ERR_INVALID, "attention timing writes K/V slot %llu but the cache holds %llu",
                      (unsigned long long)m->seq_len, (unsigned long long)m->kv_cap);
   hipStream_t st = m->ctx->compute;
-  hipEvent_t e0, e1;
+  hipEvent_t e0 = nullptr, e1 = nullptr;
   RF_LAUNCH(hipEventCreate(&e0), "hipEventCreate");
-  RF_LAUNCH(hipEventCreate(&e1), "hipEventCreate");
+  if (hipError_t ec = hipEventCreate(&e1); ec != hipSuccess) {
+    hipEventDestroy(e0);
+    return hip_error(ec, "hipEventCreate");
+  }
   // Attention is timed at the current position (the kernel only reads d_pos).
   const uint64_t hist = m->seq_len;
   uint64_t n = 0, bytes = 0;

@@ -180,6 +180,28 @@ def test_set_tensor_failure_rolls_back(ctx):
             m.close()
 
 
+def test_counts_do_not_wrap_the_capacity_checks(ctx):
+    """Step and token counts near 2^64 are refused by the capacity checks
+    instead of wrapping past them (a wrapped check would let the decode write
+    K/V rows past the end of the cache)."""
+    import ctypes as C
+
+    rf = _rf()
+    gm = _load_gpu(ctx, TINY, _tiny_tensors(np.random.default_rng(990), TINY, ALL_Q8), 32)
+    try:
+        gm.forward(1, 0)
+        with pytest.raises(rf.RamforgeError, match="KV cache full"):
+            gm.decode_steps((1 << 64) - 1)
+        p = np.array([1, 2], np.uint32)
+        out = np.zeros(4, np.uint32)
+        n = C.c_uint64(7)
+        rc = ctx.lib.rf_model_generate(gm.handle, p.ctypes.data, 2, (1 << 64) - 1, -1, out.ctypes.data, C.byref(n))
+        assert rc != 0 and n.value == 0 and not out.any()
+        assert gm.seq_len == 1
+    finally:
+        gm.close()
+
+
 def test_generate_stop_rules(ctx, orc):
     rng = np.random.default_rng(950)
     T = _tiny_tensors(rng, TINY, ALL_Q8)
