@@ -103,6 +103,8 @@ class DeviceArray:
 
     def numpy(self) -> np.ndarray:
         out = np.empty(self.shape, dtype=self.dtype)
+        if out.nbytes > self.nbytes:
+            raise ValueError(f"view of {out.nbytes} bytes over a {self.nbytes}-byte buffer")
         _lib.check(self.ctx.lib.rf_download(self.ctx.handle, out.ctypes.data, self.ptr, out.nbytes))
         return out
 
@@ -146,6 +148,8 @@ class _Capture:
         if exc_type is None:
             _lib.check(rc)
             self.graph = CapturedGraph(self.ctx, h.value)
+        elif rc == _lib.RF_OK and h.value:  # the body raised: drop the graph it made
+            self.ctx.lib.rf_graph_destroy(self.ctx.handle, h.value)
         return False
 
 
@@ -215,10 +219,12 @@ class Context:
         if charge is None:
             Context._serial += 1
             charge = f"tmp:array:{Context._serial}"
+        if shape is None:
+            shape = (int(nbytes) // np.dtype(dtype).itemsize,)
+        elif int(np.prod(shape)) * np.dtype(dtype).itemsize > int(nbytes):
+            raise ValueError(f"shape {tuple(shape)} of {np.dtype(dtype)} exceeds {int(nbytes)} bytes")
         p = C.c_void_p()
         _lib.check(self.lib.rf_vram_alloc(self.handle, charge.encode(), int(nbytes), C.byref(p)))
-        if shape is None:
-            shape = (nbytes // np.dtype(dtype).itemsize,)
         return DeviceArray(self, p.value, int(nbytes), shape, dtype, charge)
 
     def empty(self, shape, dtype=np.float32, charge: Optional[str] = None) -> DeviceArray:
@@ -269,6 +275,30 @@ class Context:
 
 # --------------------------------------------------------------------- ops
 
+def _fits(op: str, **need) -> None:
+    """Raise the reference's shape-mismatch error when a DeviceArray argument
+    holds fewer bytes than the call reads or writes (raw device addresses are
+    passed through unchecked: their sizes are unknown here)."""
+    for name, (arr, nbytes) in need.items():
+        if isinstance(arr, DeviceArray) and arr.nbytes < nbytes:
+            raise RamforgeError(_lib.RF_ERR_INVALID,
+                                f"{op} shape mismatch: {name} holds {arr.nbytes} bytes, {nbytes} needed")
+
+
+def _rows(out_dim: int, row_start: int, row_count: Optional[int]) -> int:
+    return max(0, out_dim - row_start) if row_count is None else row_count
+
+
+def _fits_matvec(w_shape, x, y, rows: int) -> None:
+    """The reference's first matvec check, x / y lengths against the shape
+    (quant.rs:990-997), on DeviceArray capacities."""
+    out_dim, in_dim = w_shape
+    xl = x.nbytes // 4 if isinstance(x, DeviceArray) else None
+    yl = y.nbytes // 4 if isinstance(y, DeviceArray) else None
+    if (xl is not None and xl < in_dim) or (yl is not None and yl < rows):
+        raise RamforgeError(_lib.RF_ERR_INVALID, f"matvec shape mismatch: W {[out_dim, in_dim]}, x {xl}, y {yl}")
+
+
 def matvec(ctx: Context, ggml_type: int, w, w_shape: Sequence[int], x, y, row_start: int = 0,
            row_count: Optional[int] = None, w_bytes: Optional[int] = None, stream=None) -> None:
     """quant::matvec_<fmt>_row_range (quant.rs:913-975): kernel shape
@@ -276,6 +306,7 @@ def matvec(ctx: Context, ggml_type: int, w, w_shape: Sequence[int], x, y, row_st
     if len(w_shape) != 2:
         raise RamforgeError(_lib.RF_ERR_INVALID, f"{GGML.NAMES.get(ggml_type, ggml_type)} matvec expects 2D weight")
     out_dim, in_dim = (int(v) for v in w_shape)
+    _fits_matvec((out_dim, in_dim), x, y, _rows(out_dim, row_start, row_count))
     wb = w.nbytes if (w_bytes is None and isinstance(w, DeviceArray)) else int(w_bytes or 0)
     rc = ctx.lib.rf_matvec(ctx.handle, ggml_type, _ptr(w), wb, out_dim, in_dim, _ptr(x), _ptr(y), row_start,
                            RF_ALL_ROWS if row_count is None else row_count, stream)
@@ -304,6 +335,7 @@ def matvec_packed(ctx: Context, ggml_type: int, w, w_shape: Sequence[int], x, y,
     if len(w_shape) != 2:
         raise RamforgeError(_lib.RF_ERR_INVALID, f"{GGML.NAMES.get(ggml_type, ggml_type)} matvec expects 2D weight")
     out_dim, in_dim = (int(v) for v in w_shape)
+    _fits_matvec((out_dim, in_dim), x, y, _rows(out_dim, row_start, row_count))
     wb = w.nbytes if (w_bytes is None and isinstance(w, DeviceArray)) else int(w_bytes or 0)
     rc = ctx.lib.rf_matvec_packed(ctx.handle, ggml_type, _ptr(w), wb, out_dim, in_dim, _ptr(x), _ptr(y), row_start,
                                   RF_ALL_ROWS if row_count is None else row_count, stream)
@@ -319,6 +351,7 @@ def matmul_packed(ctx: Context, ggml_type: int, w, w_shape: Sequence[int], x, n_
     if len(w_shape) != 2:
         raise RamforgeError(_lib.RF_ERR_INVALID, f"{GGML.NAMES.get(ggml_type, ggml_type)} matmul expects 2D weight")
     out_dim, in_dim = (int(v) for v in w_shape)
+    _fits("matmul", x=(x, 4 * n_tokens * in_dim), y=(y, 4 * n_tokens * out_dim))
     wb = w.nbytes if (w_bytes is None and isinstance(w, DeviceArray)) else int(w_bytes or 0)
     _lib.check(ctx.lib.rf_matmul_packed(ctx.handle, ggml_type, _ptr(w), wb, out_dim, in_dim, _ptr(x), n_tokens,
                                         _ptr(y), stream))
@@ -327,6 +360,7 @@ def matmul_packed(ctx: Context, ggml_type: int, w, w_shape: Sequence[int], x, n_
 def dequantize_rows(ctx: Context, ggml_type: int, w, in_dim: int, row_start: int, row_count: int, out,
                     w_bytes: Optional[int] = None, stream=None) -> None:
     """dequantize_row_<fmt> (quant.rs:615-868) for a row range, bit-exact."""
+    _fits("row decode", out=(out, 4 * row_count * in_dim))
     wb = w.nbytes if (w_bytes is None and isinstance(w, DeviceArray)) else int(w_bytes or 0)
     _lib.check(ctx.lib.rf_dequantize_rows(ctx.handle, ggml_type, _ptr(w), wb, in_dim, row_start, row_count,
                                           _ptr(out), stream))
@@ -335,8 +369,11 @@ def dequantize_rows(ctx: Context, ggml_type: int, w, in_dim: int, row_start: int
 def attention_checked(ctx: Context, q, k_hist, v_hist, k_new, v_new, hist_len: int, n_heads: int,
                       n_kv_heads: int, head_dim: int, out: Optional[DeviceArray] = None, stream=None) -> DeviceArray:
     """ops::attention_checked (ops.rs:49-69) -> compute::attention_reference."""
+    qd, kvd = n_heads * head_dim, n_kv_heads * head_dim
+    _fits("attention tensor", q=(q, 4 * qd), k_hist=(k_hist, 4 * hist_len * kvd), v_hist=(v_hist, 4 * hist_len * kvd),
+          k_new=(k_new, 4 * kvd), v_new=(v_new, 4 * kvd), out=(out, 4 * qd))
     if out is None:
-        out = ctx.empty((n_heads * head_dim,))
+        out = ctx.empty((qd,))
     _lib.check(ctx.lib.rf_attention_decode(ctx.handle, _ptr(q), _ptr(k_hist), _ptr(v_hist), _ptr(k_new),
                                            _ptr(v_new), hist_len, n_heads, n_kv_heads, head_dim, _ptr(out), stream))
     return out
@@ -345,40 +382,49 @@ def attention_checked(ctx: Context, q, k_hist, v_hist, k_new, v_new, hist_len: i
 def apply_rope(ctx: Context, q, k, pos: int, head_dim: int, n_heads: int, n_kv_heads: int, freq_base: float,
                stream=None) -> None:
     """ops::apply_rope (ops.rs:9-20): half-split RoPE in place."""
+    _fits("RoPE", q=(q, 4 * n_heads * head_dim), k=(k, 4 * n_kv_heads * head_dim))
     _lib.check(ctx.lib.rf_rope(ctx.handle, _ptr(q), _ptr(k), pos, head_dim, n_heads, n_kv_heads, freq_base, stream))
 
 
 def rmsnorm(ctx: Context, x, weight, n: int, eps: float, out, stream=None) -> None:
+    _fits("RMSNorm", input=(x, 4 * n), weight=(weight, 4 * n), output=(out, 4 * n))
     _lib.check(ctx.lib.rf_rmsnorm(ctx.handle, _ptr(x), _ptr(weight), n, eps, _ptr(out), stream))
 
 
 def add(ctx: Context, a, b, n: int, out, stream=None) -> None:
+    _fits("elementwise", a=(a, 4 * n), b=(b, 4 * n), out=(out, 4 * n))
     _lib.check(ctx.lib.rf_add(ctx.handle, _ptr(a), _ptr(b), n, _ptr(out), stream))
 
 
 def bias_add(ctx: Context, v, bias, n: int, stream=None) -> None:
     """v += bias in place (model_executor.rs:161-194, the Q/K/V bias step)."""
+    _fits("bias add", v=(v, 4 * n), bias=(bias, 4 * n))
     _lib.check(ctx.lib.rf_bias_add(ctx.handle, _ptr(v), _ptr(bias), n, stream))
 
 
 def mul(ctx: Context, a, b, n: int, out, stream=None) -> None:
+    _fits("elementwise", a=(a, 4 * n), b=(b, 4 * n), out=(out, 4 * n))
     _lib.check(ctx.lib.rf_mul(ctx.handle, _ptr(a), _ptr(b), n, _ptr(out), stream))
 
 
 def silu(ctx: Context, x, n: int, out, stream=None) -> None:
+    _fits("SiLU", x=(x, 4 * n), out=(out, 4 * n))
     _lib.check(ctx.lib.rf_silu(ctx.handle, _ptr(x), n, _ptr(out), stream))
 
 
 def swiglu(ctx: Context, gate, up, n: int, out, stream=None) -> None:
+    _fits("elementwise", gate=(gate, 4 * n), up=(up, 4 * n), out=(out, 4 * n))
     _lib.check(ctx.lib.rf_swiglu(ctx.handle, _ptr(gate), _ptr(up), n, _ptr(out), stream))
 
 
 def softmax(ctx: Context, values, n: int, stream=None) -> None:
+    _fits("softmax", values=(values, 4 * n))
     _lib.check(ctx.lib.rf_softmax(ctx.handle, _ptr(values), n, stream))
 
 
 def argmax(ctx: Context, logits, n: int, out_index, stream=None) -> None:
     """Greedy Sampler::sample_checked (sampling.rs:45-57) into device memory."""
+    _fits("argmax", logits=(logits, 4 * n), out_index=(out_index, 4))
     _lib.check(ctx.lib.rf_argmax(ctx.handle, _ptr(logits), n, _ptr(out_index), stream))
 
 

@@ -85,11 +85,21 @@ def test_dequant_validation(ctx):
         rf.dequantize_rows(ctx, Q8_0, w, 31, 0, 1, out)
     # sizes computed from the shape must not wrap past the bounds check
     with pytest.raises(rf.RamforgeError, match="overflows"):
-        rf.dequantize_rows(ctx, Q8_0, w, 1 << 40, 1 << 30, 1 << 30, out)
+        rf.dequantize_rows(ctx, Q8_0, w, 1 << 40, 1 << 30, 1 << 30, out.ptr)
     with pytest.raises(rf.RamforgeError, match="overflows"):
-        rf.dequantize_rows(ctx, Q8_0, w, 32, (1 << 64) - 2, 4, out)
+        rf.dequantize_rows(ctx, Q8_0, w, 32, (1 << 64) - 2, 4, out.ptr)
     w.free()
     out.free()
+
+
+def test_device_array_views_stay_in_their_buffer(ctx):
+    with pytest.raises(ValueError, match="exceeds"):
+        ctx.alloc(8, shape=(4,), dtype=np.float32)
+    a = ctx.alloc(8, shape=(2,), dtype=np.float32)
+    a.shape = (4,)
+    with pytest.raises(ValueError, match="view"):
+        a.numpy()
+    a.free()
 
 
 # -------------------------------------------------------------- matvec
@@ -254,7 +264,7 @@ def test_matvec_packed_subnormal_and_signed_scales(ctx, orc, t):
 def test_matvec_packed_validation(ctx):
     rf = _rf()
     w = ctx.array(np.zeros(34 * 4, np.uint8))
-    x = ctx.array(np.zeros(128, np.float32))
+    x = ctx.array(np.zeros(256, np.float32))
     y = ctx.array(np.full(2, 7.0, np.float32))
     with pytest.raises(rf.RamforgeError, match="truncated"):
         rf.matvec_packed(ctx, Q8_0, w, (2, 128), x, y)
@@ -265,7 +275,7 @@ def test_matvec_packed_validation(ctx):
     with pytest.raises(rf.RamforgeError, match="does not support"):
         rf.matvec_packed(ctx, Q5_K, w, (1, 256), x, y)
     with pytest.raises(rf.RamforgeError, match="overflows"):  # 2^40 rows of 2^40 elements
-        rf.matvec_packed(ctx, Q8_0, w, (1 << 40, 1 << 40), x, y, 0, 1)
+        rf.matvec_packed(ctx, Q8_0, w, (1 << 40, 1 << 40), x.ptr, y, 0, 1)
     assert y.numpy().tolist() == [7.0, 7.0]  # destination untouched
     assert not rf.packed_supported(Q8_0, 1 << 16) and rf.packed_supported(Q4_0, 14336)
     assert rf.packed_supported(Q8_0, 14336) and not rf.packed_supported(Q8_0, 100)
@@ -349,8 +359,12 @@ def test_matvec_validation_keeps_destination(ctx):
     y = ctx.array(np.full(3, 7.0, np.float32))
     with pytest.raises(rf.RamforgeError, match="not divisible"):
         rf.matvec(ctx, Q8_0, w, (3, 31), x, y)
-    with pytest.raises(rf.RamforgeError, match="weight truncated"):
+    # x / y lengths first, as quant.rs:990-997 (DeviceArray capacities here);
+    # the library's own check of the weight bytes through a raw address
+    with pytest.raises(rf.RamforgeError, match="matvec shape mismatch"):
         rf.matvec(ctx, Q8_0, w, (4, 32), x, y)
+    with pytest.raises(rf.RamforgeError, match="weight truncated"):
+        rf.matvec(ctx, Q8_0, w, (4, 32), x, y.ptr)
     with pytest.raises(rf.RamforgeError, match="exceeds out_dim"):
         rf.matvec(ctx, Q8_0, w, (3, 32), x, y, row_start=4)
     with pytest.raises(rf.RamforgeError, match="exceeds out_dim"):

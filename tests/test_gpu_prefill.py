@@ -79,9 +79,9 @@ def test_matmul_packed_validation(ctx):
     with pytest.raises(rf.RamforgeError, match="truncated"):
         rf.matmul_packed(ctx, Q8_0, w, (2, 256), x, 1, y, w_bytes=34 * 8 - 1)
     with pytest.raises(rf.RamforgeError, match="overflows"):
-        rf.matmul_packed(ctx, Q8_0, w, (1 << 40, 1 << 30), x, 1, y)
+        rf.matmul_packed(ctx, Q8_0, w, (1 << 40, 1 << 30), x.ptr, 1, y.ptr)
     with pytest.raises(rf.RamforgeError, match="overflows"):
-        rf.matmul_packed(ctx, Q8_0, w, (1, 256), x, 1 << 60, y)
+        rf.matmul_packed(ctx, Q8_0, w, (1, 256), x.ptr, 1 << 60, y.ptr)
     for a in (w, x, y):
         a.free()
 
