@@ -29,14 +29,15 @@
 // [row l % 16], i = 0..3, so every value a lane accumulates belongs to its own
 // weight row and takes that row's scale.
 //
-// Workgroup: 8 wavefronts x 32 rows (two 16-row tiles) x all tokens of the
-// chunk (NTT tiles of 16), over a range of 128-element k slices (split-K).
+// Workgroup: 12 or 8 wavefronts (mm_pick_wide) x 32 rows (two 16-row tiles)
+// x all tokens of the chunk (NTT tiles of 16), over a range of 128-element k
+// slices (split-K).
 // Each x slice is split once per workgroup while it is staged: three bf16
 // planes in LDS (16-byte skew per token row: the 16 token rows of an A read
-// fall in distinct banks), read as MFMA operands by all eight wavefronts.
+// fall in distinct banks), read as MFMA operands by all the wavefronts.
 // Two slice buffers: the next slice's x (from L2) is loaded while the
 // current slice is computed, the weights (from HBM, straight to registers)
-// two slices ahead.
+// one or two slices ahead (the workgroup shape's ring depth).
 // Partial sums of the splits land in a workspace and mm_reduce adds them in
 // a fixed order (deterministic) and applies the epilogue.
 #include <algorithm>
@@ -49,7 +50,6 @@ namespace rf {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-constexpr uint32_t MM_ROWS = 256;         // weight rows per workgroup (8 wavefronts x 32)
 constexpr uint32_t MM_KS = 128;           // k elements per staged x slice
 constexpr uint32_t MM_ST = MM_KS / 32;    // 32-element steps per slice
 constexpr uint32_t MM_XB = MM_KS + 8;     // LDS bf16 per token row of one x plane (16-byte skew)
@@ -77,17 +77,28 @@ __device__ __forceinline__ bf16x8 mm_codes(const float (&v)[8]) {
   return r;
 }
 
-// The MM_ST f16 scales of a slice of one row: one 8-byte load when the slice
-// is whole and 8-byte aligned (K a multiple of 128), else one per step.
-__device__ __forceinline__ void mm_load_scales(const uint8_t* sb, uint32_t nst, uint32_t (&sc)[MM_ST]) {
+// The MM_ST f16 scales of a slice of one row, kept as loaded: scale j in
+// half j & 1 of word j >> 1, taken out only when step j uses it (mm_scale).
+// One 8-byte load when the slice is whole and 8-byte aligned (K a multiple of
+// 128), else one 2-byte load per step.  Splitting the halves right after the
+// load made every wavefront wait there for all its loads in flight, the
+// weights of the slices ahead included; two registers instead of four also
+// make room for a third wavefront per SIMD.
+__device__ __forceinline__ void mm_load_scales(const uint8_t* sb, uint32_t nst, uint2& sc) {
   static_assert(MM_ST == 4, "four scales per slice");
   if (nst == MM_ST && (reinterpret_cast<uintptr_t>(sb) & 7u) == 0) {
-    const uint2 v = *reinterpret_cast<const uint2*>(sb);
-    sc[0] = v.x & 0xFFFFu; sc[1] = v.x >> 16; sc[2] = v.y & 0xFFFFu; sc[3] = v.y >> 16;
+    sc = *reinterpret_cast<const uint2*>(sb);
   } else {
+    uint32_t h[MM_ST];
 #pragma unroll
-    for (uint32_t j = 0; j < MM_ST; ++j) sc[j] = j < nst ? (uint32_t)rf_ld_u16(sb + 2 * j) : 0u;
+    for (uint32_t j = 0; j < MM_ST; ++j) h[j] = j < nst ? (uint32_t)rf_ld_u16(sb + 2 * j) : 0u;
+    sc = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
   }
+}
+
+__device__ __forceinline__ uint32_t mm_scale(uint2 sc, int j) {
+  const uint32_t w = j < 2 ? sc.x : sc.y;
+  return (j & 1) ? w >> 16 : w & 0xFFFFu;
 }
 
 // Per-format weight slice (MM_KS elements of one row) of one lane (element
@@ -96,7 +107,7 @@ template <uint32_t T> struct MmW;
 
 template <> struct MmW<T_Q8_0> {
   uint2 c[MM_ST];
-  uint32_t sc[MM_ST];
+  uint2 sc;
   __device__ void load(const MmSeg& s, uint32_t row, uint32_t sl, uint32_t g, uint32_t nst, uint32_t K) {
     const uint8_t* cb = s.reg[0] + (size_t)row * K + sl * MM_KS + 8u * g;
     const uint8_t* sb = s.reg[1] + ((size_t)row * (K / 32u) + sl * MM_ST) * 2u;
@@ -109,13 +120,13 @@ template <> struct MmW<T_Q8_0> {
 #pragma unroll
     for (int k = 0; k < 8; ++k) v[k] = (float)(int)(int8_t)mm_byte(c[j], k);
     b = mm_codes(v);
-    d = rf_half_to_float_fast(sc[j]);
+    d = rf_half_to_float_fast(mm_scale(sc, j));
   }
 };
 
 template <> struct MmW<T_Q4_0> {
   uint2 c[MM_ST];
-  uint32_t sc[MM_ST];
+  uint2 sc;
   __device__ void load(const MmSeg& s, uint32_t row, uint32_t sl, uint32_t g, uint32_t nst, uint32_t K) {
     const size_t blk = (size_t)row * (K / 32u) + sl * MM_ST;
     const uint8_t* cb = s.reg[0] + blk * 16u + 8u * (g & 1u);
@@ -132,7 +143,7 @@ template <> struct MmW<T_Q4_0> {
 #pragma unroll
     for (int k = 0; k < 8; ++k) v[k] = (float)((int)((mm_byte(c[j], k) >> sh) & 15u) - 8);
     b = mm_codes(v);
-    d = rf_half_to_float_fast(sc[j]);
+    d = rf_half_to_float_fast(mm_scale(sc, j));
   }
 };
 
@@ -228,8 +239,21 @@ __device__ __forceinline__ void mm_split3(float x, __bf16& hi, __bf16& mid, __bf
   lo = (__bf16)(r1 - (float)mid);
 }
 
-template <uint32_t T, int NTT>
-__global__ __launch_bounds__(512) void mm_packed(MmArgs a) {
+// Two workgroup shapes: wavefronts per workgroup (32 weight rows each) and
+// how many slices of weights are in registers at once (DEPTH 3: loaded two
+// slices ahead, 2: one).  The x tile (104 KB at 64 tokens) allows one
+// workgroup per CU, so the wavefronts of one workgroup are all the latency
+// hiding there is.  Wide, 12 wavefronts with a two-slice ring, fits 168
+// VGPRs (three per SIMD) and ran Q4_K at 64 tokens 12-32% faster than
+// narrow, 8 with a three-slice ring (gate/up 87.5 -> 77.1 us, down 48.2 ->
+// 41.1, Q/K/V 29.5 -> 20.0).  Its 384-row workgroups leave too few for some
+// shapes (4096 rows: 11, filling 176 of 256 CUs), so each launch takes the
+// shape whose split fills the chip better (mm_pick_wide).  Q6_K's four weight
+// regions do not fit the wide register budget (63 VGPRs spilled): narrow.
+constexpr uint32_t MM_ROWS_NARROW = 8 * 32, MM_ROWS_WIDE = 12 * 32;
+
+template <uint32_t T, int NTT, int NW, int DEPTH>
+__global__ __launch_bounds__(64 * NW) void mm_packed(MmArgs a) {
   // Two x slice buffers, each three bf16 planes [3][NT][MM_XB] and (Q4_K)
   // step sums [MM_ST][NT]: slice s + 1 is loaded (x and weights) while slice
   // s is computed, then split into the other buffer; one barrier per slice.
@@ -241,7 +265,7 @@ __global__ __launch_bounds__(512) void mm_packed(MmArgs a) {
   MmSeg s = a.seg[0];
   if (a.nseg > 1 && blockIdx.x >= a.seg[1].group_begin) s = a.seg[1];
   if (a.nseg > 2 && blockIdx.x >= a.seg[2].group_begin) s = a.seg[2];
-  const uint32_t row_base = (blockIdx.x - s.group_begin) * MM_ROWS + wave * 32u;
+  const uint32_t row_base = (blockIdx.x - s.group_begin) * (NW * 32u) + wave * 32u;
   uint32_t rowc[2];
 #pragma unroll
   for (int rt = 0; rt < 2; ++rt) rowc[rt] = min(row_base + 16u * rt + r16, s.rows - 1u);  // loads stay in bounds
@@ -293,13 +317,14 @@ __global__ __launch_bounds__(512) void mm_packed(MmArgs a) {
 #pragma unroll
     for (int nt = 0; nt < NTT; ++nt) acc[rt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  // Weights two slices ahead (cur, nxt, nxt2), x one slice ahead.
+  // Weights DEPTH - 1 slices ahead (cur, nxt[, nxt2]), x one slice ahead.
+  static_assert(DEPTH == 2 || DEPTH == 3, "weight ring of two or three slices");
   MmW<T> cur[2], nxt[2], nxt2[2];
   float4 xv[4];
   fetch_x(sl0, xv);
 #pragma unroll
   for (int rt = 0; rt < 2; ++rt) cur[rt].load(s, rowc[rt], sl0, g, nsteps(sl0), K);
-  if (sl0 + 1 < sl1) {
+  if (DEPTH == 3 && sl0 + 1 < sl1) {
 #pragma unroll
     for (int rt = 0; rt < 2; ++rt) nxt[rt].load(s, rowc[rt], sl0 + 1, g, nsteps(sl0 + 1), K);
   }
@@ -309,9 +334,14 @@ __global__ __launch_bounds__(512) void mm_packed(MmArgs a) {
     const uint32_t cb = (sl - sl0) & 1u, nst = nsteps(sl);
     const bool more = sl + 1 < sl1;
     if (more) fetch_x(sl + 1, xv);  // next slice's x in flight during this slice's math
-    if (sl + 2 < sl1) {
+    if constexpr (DEPTH == 3) {
+      if (sl + 2 < sl1) {
 #pragma unroll
-      for (int rt = 0; rt < 2; ++rt) nxt2[rt].load(s, rowc[rt], sl + 2, g, nsteps(sl + 2), K);
+        for (int rt = 0; rt < 2; ++rt) nxt2[rt].load(s, rowc[rt], sl + 2, g, nsteps(sl + 2), K);
+      }
+    } else if (more) {
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt) nxt[rt].load(s, rowc[rt], sl + 1, g, nsteps(sl + 1), K);
     }
     const __bf16* xb = xsb + cb * BUF;
     const float* ss = reinterpret_cast<const float*>(xb + 3 * PLANE);
@@ -374,7 +404,7 @@ __global__ __launch_bounds__(512) void mm_packed(MmArgs a) {
 #pragma unroll
       for (int rt = 0; rt < 2; ++rt) {
         cur[rt] = nxt[rt];
-        nxt[rt] = nxt2[rt];
+        if constexpr (DEPTH == 3) nxt[rt] = nxt2[rt];
       }
     }
     __syncthreads();
@@ -464,7 +494,7 @@ bool mm_supported(uint32_t t, uint64_t in_dim) {
 // workgroup prologue and partial traffic: gate/up at 16 splits spent 23 us
 // in the reduce alone, at 2 splits 5 us).
 static void mm_shape(uint64_t groups, uint64_t in_dim, uint64_t n, uint32_t* nsplit, uint32_t* spp,
-                     uint32_t* nslices) {
+                     uint32_t* nslices, double* fill = nullptr) {
   const uint64_t ns = (in_dim + MM_KS - 1) / MM_KS;
   const uint64_t target = mm_cu_count();
   uint64_t spmax = ns >= 2 ? ns / 2 : 1;
@@ -480,24 +510,28 @@ static void mm_shape(uint64_t groups, uint64_t in_dim, uint64_t n, uint32_t* nsp
   uint64_t per = ns;
   for (uint64_t sp = 1; sp <= spmax; ++sp) best = std::max(best, util(sp, &per));
   uint64_t best_per = ns;
+  double chosen = util(1, &per);
   for (uint64_t sp = 1; sp <= spmax; ++sp)
     if (util(sp, &per) >= 0.85 * best) {
       best_per = per;
+      chosen = util(sp, &per);
       break;
     }
+  if (fill) *fill = chosen;
   *spp = (uint32_t)best_per;
   *nsplit = (uint32_t)((ns + best_per - 1) / best_per);
   *nslices = (uint32_t)ns;
 }
 
-static uint64_t mm_groups(const MmSegDesc* segs, int nseg) {
+static uint64_t mm_groups(const MmSegDesc* segs, int nseg, uint64_t rows_per_group) {
   uint64_t g = 0;
-  for (int i = 0; i < nseg; ++i) g += (segs[i].rows + MM_ROWS - 1) / MM_ROWS;
+  for (int i = 0; i < nseg; ++i) g += (segs[i].rows + rows_per_group - 1) / rows_per_group;
   return g;
 }
 
-// Partial-sum floats a launch of up to n tokens may need (the split count
-// depends on the token count).
+// Partial-sum floats a launch of up to n tokens may need, for either
+// workgroup size (the split count depends on the token count and on the
+// workgroups a launch has).
 uint64_t mm_part_floats(const uint64_t* rows, int nseg, uint64_t in_dim, uint64_t n) {
   MmSegDesc d[3] = {};
   uint64_t mtot = 0;
@@ -506,41 +540,61 @@ uint64_t mm_part_floats(const uint64_t* rows, int nseg, uint64_t in_dim, uint64_
     mtot += rows[i];
   }
   uint64_t most = 0;
-  for (uint64_t k = 1; k <= n; ++k) {
-    uint32_t nsplit, spp, ns;
-    mm_shape(mm_groups(d, nseg), in_dim, k, &nsplit, &spp, &ns);
-    if ((uint64_t)nsplit * k > most) most = (uint64_t)nsplit * k;
-  }
+  for (uint64_t rpg : {MM_ROWS_NARROW, MM_ROWS_WIDE})
+    for (uint64_t k = 1; k <= n; ++k) {
+      uint32_t nsplit, spp, ns;
+      mm_shape(mm_groups(d, nseg, rpg), in_dim, k, &nsplit, &spp, &ns);
+      if ((uint64_t)nsplit * k > most) most = (uint64_t)nsplit * k;
+    }
   return most * mtot;
 }
 
 static int mm_ntt(uint64_t n) { return (int)((n + 15) / 16); }
 
-template <uint32_t T, int NTT>
+template <uint32_t T, int NTT, int NW, int DEPTH>
 static hipError_t mm_launch_t(const MmArgs& a, dim3 grid, hipStream_t st) {
   const uint32_t lds = 2u * (3u * NTT * 16u * MM_XB * 2u + (T == T_Q4_K ? MM_ST * NTT * 16u * 4u : 0u));
   static bool opened = false;
   if (!opened) {
     if (lds > 65536) {
-      hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(mm_packed<T, NTT>),
+      hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(mm_packed<T, NTT, NW, DEPTH>),
                                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
       if (e != hipSuccess) return e;
     }
     opened = true;
   }
-  hipLaunchKernelGGL((mm_packed<T, NTT>), grid, dim3(512), lds, st, a);
+  hipLaunchKernelGGL((mm_packed<T, NTT, NW, DEPTH>), grid, dim3(64 * NW), lds, st, a);
   return hipGetLastError();
 }
 
-template <uint32_t T>
+template <uint32_t T, int NW, int DEPTH>
 static hipError_t mm_launch_ntt(const MmArgs& a, dim3 grid, int ntt, hipStream_t st) {
   switch (ntt) {
-    case 1: return mm_launch_t<T, 1>(a, grid, st);
-    case 2: return mm_launch_t<T, 2>(a, grid, st);
-    case 3: return mm_launch_t<T, 3>(a, grid, st);
-    case 4: return mm_launch_t<T, 4>(a, grid, st);
+    case 1: return mm_launch_t<T, 1, NW, DEPTH>(a, grid, st);
+    case 2: return mm_launch_t<T, 2, NW, DEPTH>(a, grid, st);
+    case 3: return mm_launch_t<T, 3, NW, DEPTH>(a, grid, st);
+    case 4: return mm_launch_t<T, 4, NW, DEPTH>(a, grid, st);
     default: return hipErrorInvalidValue;
   }
+}
+
+template <uint32_t T>
+static hipError_t mm_launch_shape(const MmArgs& a, dim3 grid, int ntt, bool wide, hipStream_t st) {
+  if constexpr (T != T_Q6_K) {
+    if (wide) return mm_launch_ntt<T, 12, 2>(a, grid, ntt, st);
+  }
+  return mm_launch_ntt<T, 8, 3>(a, grid, ntt, st);
+}
+
+// The wide shape unless its split fills the CUs clearly worse than the narrow
+// one (at least 95% of the narrow shape's fill), never for Q6_K.
+static bool mm_pick_wide(uint32_t t, const MmSegDesc* segs, int nseg, uint64_t in_dim, uint64_t n) {
+  if (t == T_Q6_K) return false;
+  uint32_t nsplit, spp, ns;
+  double fw = 0.0, fn = 0.0;
+  mm_shape(mm_groups(segs, nseg, MM_ROWS_WIDE), in_dim, n, &nsplit, &spp, &ns, &fw);
+  mm_shape(mm_groups(segs, nseg, MM_ROWS_NARROW), in_dim, n, &nsplit, &spp, &ns, &fn);
+  return fw >= 0.95 * fn;
 }
 
 static bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -560,6 +614,8 @@ hipError_t launch_matmul_packed(uint32_t t, const MmSegDesc* segs, int nseg, con
       default: return k == 0 ? in_dim / 2 : k == 1 ? in_dim / 4 : k == 2 ? in_dim / 256 * 16 : in_dim / 256 * 2;
     }
   };
+  const bool wide = mm_pick_wide(t, segs, nseg, in_dim, n);
+  const uint64_t rpg = wide ? MM_ROWS_WIDE : MM_ROWS_NARROW;
   MmArgs a{};
   MmRedArgs r{};
   uint64_t mtot = 0, groups = 0;
@@ -582,7 +638,7 @@ hipError_t launch_matmul_packed(uint32_t t, const MmSegDesc* segs, int nseg, con
     a.seg[i].col = (uint32_t)mtot;
     r.seg[i] = MmRedSeg{d.y, d.res, d.bias, (uint32_t)d.rows, (uint32_t)mtot, (uint32_t)d.ld};
     if (epi == EPI_RESIDUAL && !d.res) return hipErrorInvalidValue;
-    groups += (d.rows + MM_ROWS - 1) / MM_ROWS;
+    groups += (d.rows + rpg - 1) / rpg;
     mtot += d.rows;
   }
   if (mtot > 0xFFFFFFFFull || groups > 0x7FFFFFFFull) return hipErrorInvalidValue;
@@ -602,10 +658,10 @@ hipError_t launch_matmul_packed(uint32_t t, const MmSegDesc* segs, int nseg, con
   const int ntt = mm_ntt(n);
   hipError_t e;
   switch (t) {
-    case T_Q8_0: e = mm_launch_ntt<T_Q8_0>(a, grid, ntt, st); break;
-    case T_Q4_0: e = mm_launch_ntt<T_Q4_0>(a, grid, ntt, st); break;
-    case T_Q4_K: e = mm_launch_ntt<T_Q4_K>(a, grid, ntt, st); break;
-    default: e = mm_launch_ntt<T_Q6_K>(a, grid, ntt, st); break;
+    case T_Q8_0: e = mm_launch_shape<T_Q8_0>(a, grid, ntt, wide, st); break;
+    case T_Q4_0: e = mm_launch_shape<T_Q4_0>(a, grid, ntt, wide, st); break;
+    case T_Q4_K: e = mm_launch_shape<T_Q4_K>(a, grid, ntt, wide, st); break;
+    default: e = mm_launch_shape<T_Q6_K>(a, grid, ntt, wide, st); break;
   }
   if (e != hipSuccess) return e;
   r.nseg = (uint32_t)nseg;
