@@ -466,6 +466,59 @@ __global__ __launch_bounds__(256) void mm_reduce(MmRedArgs a) {
   }
 }
 
+// mm_reduce for four consecutive columns per thread (16-byte loads and
+// stores), when every segment boundary, row stride and pointer allows it
+// (mm_reduce_vec4).  Each column is summed in split order and finished
+// exactly as in mm_reduce: the same bits, a quarter of the memory
+// instructions.
+__global__ __launch_bounds__(256) void mm_reduce4(MmRedArgs a) {
+  const uint64_t e = ((uint64_t)blockIdx.x * 256u + threadIdx.x) * 4u;
+  if (e >= (uint64_t)a.n * a.mcols) return;
+  const uint32_t t = (uint32_t)(e / a.mcols), c = (uint32_t)(e % a.mcols);
+  MmRedSeg s = a.seg[0];
+  if (a.nseg > 1 && c >= a.seg[1].col) s = a.seg[1];
+  if (a.nseg > 2 && c >= a.seg[2].col) s = a.seg[2];
+  const uint32_t r = c - s.col;
+  const size_t stride = (size_t)a.n * a.mtot;
+  auto sum = [&](const float* p) {
+    float4 v = *reinterpret_cast<const float4*>(p);
+    for (uint32_t k = 1; k < a.nsplit; ++k) {
+      const float4 q = *reinterpret_cast<const float4*>(p + k * stride);
+      v.x += q.x;
+      v.y += q.y;
+      v.z += q.z;
+      v.w += q.w;
+    }
+    return v;
+  };
+  const float4 v = sum(a.part + (size_t)t * a.mtot + c);
+  const size_t o = (size_t)t * s.ld + r;
+  float4 out = v;
+  if (a.epi == EPI_RESIDUAL) {
+    const float4 rr = *reinterpret_cast<const float4*>(s.res + o);
+    out = make_float4(rr.x + v.x, rr.y + v.y, rr.z + v.z, rr.w + v.w);
+  } else if (a.epi == EPI_SWIGLU) {
+    const float4 u = sum(a.part + (size_t)t * a.mtot + a.seg[1].col + r);
+    out = make_float4(v.x / (1.0f + expf(-v.x)) * u.x, v.y / (1.0f + expf(-v.y)) * u.y,
+                      v.z / (1.0f + expf(-v.z)) * u.z, v.w / (1.0f + expf(-v.w)) * u.w);
+  } else if (s.bias) {
+    const float4 b = *reinterpret_cast<const float4*>(s.bias + r);
+    out = make_float4(v.x + b.x, v.y + b.y, v.z + b.z, v.w + b.w);
+  }
+  *reinterpret_cast<float4*>(s.y + o) = out;
+}
+
+static bool mm_reduce_vec4(const MmRedArgs& r) {
+  auto al = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
+  if (r.mcols % 4 || r.mtot % 4 || !al(r.part)) return false;
+  for (uint32_t i = 0; i < r.nseg; ++i) {
+    const MmRedSeg& s = r.seg[i];
+    if (s.col % 4 || s.rows % 4 || s.ld % 4 || !al(s.y) || (s.res && !al(s.res)) || (s.bias && !al(s.bias)))
+      return false;
+  }
+  return true;
+}
+
 // ------------------------------------------------------------------ host side
 
 static uint32_t mm_cu_count() {
@@ -672,7 +725,10 @@ hipError_t launch_matmul_packed(uint32_t t, const MmSegDesc* segs, int nseg, con
   r.epi = epi;
   r.part = part;
   const uint64_t total = (uint64_t)n * r.mcols;
-  hipLaunchKernelGGL(mm_reduce, dim3((uint32_t)((total + 255) / 256)), dim3(256), 0, st, r);
+  if (mm_reduce_vec4(r))
+    hipLaunchKernelGGL(mm_reduce4, dim3((uint32_t)((total / 4 + 255) / 256)), dim3(256), 0, st, r);
+  else
+    hipLaunchKernelGGL(mm_reduce, dim3((uint32_t)((total + 255) / 256)), dim3(256), 0, st, r);
   return hipGetLastError();
 }
 

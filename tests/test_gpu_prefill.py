@@ -67,6 +67,26 @@ def test_matmul_packed_matches_per_token_matvec(ctx, orc, t, out_dim, in_dim, n)
     _check_matmul(ctx, orc, t, out_dim, in_dim, n, 3100 + t + out_dim % 997 + n)
 
 
+@pytest.mark.parametrize("t", PACKED)
+def test_matmul_reduce_forms_agree(ctx, t):
+    """The four-column split-K reduce (aligned output) and the one-column
+    reduce (an output 4 bytes past alignment) give the same bits."""
+    rf = _rf()
+    rng = np.random.default_rng(3150 + t)
+    out_dim, in_dim, n = 1024, 4096, 40
+    raw = random_matrix(t, out_dim, in_dim, rng)
+    w = ctx.array(pack_host(t, raw, out_dim, in_dim))
+    x = ctx.array(rng.normal(0, 1, n * in_dim).astype(np.float32))
+    y = ctx.empty((n * out_dim + 4,))
+    rf.matmul_packed(ctx, t, w, (out_dim, in_dim), x, n, y.ptr)
+    a = y.numpy()[: n * out_dim].copy()
+    rf.matmul_packed(ctx, t, w, (out_dim, in_dim), x, n, y.ptr + 4)
+    b = y.numpy()[1: n * out_dim + 1]
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), NAMES[t]
+    for arr in (w, x, y):
+        arr.free()
+
+
 def test_matmul_packed_validation(ctx):
     rf = _rf()
     w = ctx.array(np.zeros(34 * 8, np.uint8))
