@@ -344,8 +344,9 @@ def config4_bench(rf, syn, tokens: int = 128, prompt_len: int = 32) -> dict:
     """random-init llama, 16 layers, d 2048, 32/8 heads, FFN
     8192, vocab 32000, Q8_0 everywhere, fully resident; 32-token prompt, 128
     greedy tokens.  Timed: the prompt token by token (the reference's loop) and
-    batched, then the 128 greedy tokens as device decode steps (hipGraph
-    replay; graphs captured in an untimed first pass)."""
+    batched (after an untimed batched pass that allocates the prefill
+    workspace, as prefill_bench does), then the 128 greedy tokens as device
+    decode steps (hipGraph replay; graphs captured in an untimed first pass)."""
     import numpy as np
 
     cfg = syn.CONFIG_4
@@ -361,6 +362,8 @@ def config4_bench(rf, syn, tokens: int = 128, prompt_len: int = 32) -> dict:
     m.use_graph(True)
     m.decode_steps(tokens)  # captures the regimes' graphs
     ctx.synchronize()
+    m.reset()
+    m.prefill(prompt)  # untimed: workspace and kernel attributes
     m.reset()
     t0 = time.perf_counter()
     m.prefill(prompt)

@@ -168,6 +168,7 @@ struct MmSegDesc {
 };
 bool mm_supported(uint32_t t, uint64_t in_dim);
 uint64_t mm_part_floats(const uint64_t* rows, int nseg, uint64_t in_dim, uint64_t n);
+uint64_t mm_part_floats_at(const uint64_t* rows, int nseg, uint64_t in_dim, uint64_t n);
 hipError_t launch_matmul_packed(uint32_t t, const MmSegDesc* segs, int nseg, const float* x, uint64_t ldx,
                                 uint64_t n, uint64_t in_dim, int epi, float* part, uint64_t part_floats,
                                 hipStream_t st);

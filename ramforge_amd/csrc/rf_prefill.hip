@@ -585,7 +585,8 @@ static uint64_t mm_groups(const MmSegDesc* segs, int nseg, uint64_t rows_per_gro
 // Partial-sum floats a launch of up to n tokens may need, for either
 // workgroup size (the split count depends on the token count and on the
 // workgroups a launch has).
-uint64_t mm_part_floats(const uint64_t* rows, int nseg, uint64_t in_dim, uint64_t n) {
+// Partial-sum floats of a launch of exactly n tokens, for either workgroup size.
+uint64_t mm_part_floats_at(const uint64_t* rows, int nseg, uint64_t in_dim, uint64_t n) {
   MmSegDesc d[3] = {};
   uint64_t mtot = 0;
   for (int i = 0; i < nseg && i < 3; ++i) {
@@ -593,13 +594,21 @@ uint64_t mm_part_floats(const uint64_t* rows, int nseg, uint64_t in_dim, uint64_
     mtot += rows[i];
   }
   uint64_t most = 0;
-  for (uint64_t rpg : {MM_ROWS_NARROW, MM_ROWS_WIDE})
-    for (uint64_t k = 1; k <= n; ++k) {
-      uint32_t nsplit, spp, ns;
-      mm_shape(mm_groups(d, nseg, rpg), in_dim, k, &nsplit, &spp, &ns);
-      if ((uint64_t)nsplit * k > most) most = (uint64_t)nsplit * k;
-    }
+  for (uint64_t rpg : {MM_ROWS_NARROW, MM_ROWS_WIDE}) {
+    uint32_t nsplit, spp, ns;
+    mm_shape(mm_groups(d, nseg, rpg), in_dim, n, &nsplit, &spp, &ns);
+    if ((uint64_t)nsplit * n > most) most = (uint64_t)nsplit * n;
+  }
   return most * mtot;
+}
+
+// Partial-sum floats a launch of up to n tokens may need, for either
+// workgroup size (the split count depends on the token count and on the
+// workgroups a launch has).
+uint64_t mm_part_floats(const uint64_t* rows, int nseg, uint64_t in_dim, uint64_t n) {
+  uint64_t most = 0;
+  for (uint64_t k = 1; k <= n; ++k) most = std::max(most, mm_part_floats_at(rows, nseg, in_dim, k));
+  return most;
 }
 
 static int mm_ntt(uint64_t n) { return (int)((n + 15) / 16); }

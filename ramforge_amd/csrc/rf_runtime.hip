@@ -3,6 +3,7 @@
 // translation units.
 #include "rf_runtime.h"
 
+#include <algorithm>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -634,7 +635,9 @@ int32_t rf_matmul_packed(rf_ctx* ctx, uint32_t t, const void* packed, uint64_t p
                      (unsigned long long)out_dim, (unsigned long long)in_dim);
   hipStream_t st = pick_stream(ctx, s);
   const uint64_t chunk = n_tokens < MM_MAX_TOKENS ? n_tokens : MM_MAX_TOKENS;
-  const uint64_t part = mm_part_floats(&out_dim, 1, in_dim, chunk);
+  // the launches are chunk tokens each, the last one the remainder
+  uint64_t part = mm_part_floats_at(&out_dim, 1, in_dim, chunk);
+  if (n_tokens % chunk) part = std::max(part, mm_part_floats_at(&out_dim, 1, in_dim, n_tokens % chunk));
   int32_t rc = ensure_workspace(ctx, ctx->mm_ws, "workspace:matmul", part * 4);
   if (rc) return rc;
   const bool aligned = (reinterpret_cast<uintptr_t>(x) & 15u) == 0 && in_dim % 4 == 0;
