@@ -582,9 +582,6 @@ static uint64_t mm_groups(const MmSegDesc* segs, int nseg, uint64_t rows_per_gro
   return g;
 }
 
-// Partial-sum floats a launch of up to n tokens may need, for either
-// workgroup size (the split count depends on the token count and on the
-// workgroups a launch has).
 // Partial-sum floats of a launch of exactly n tokens, for either workgroup size.
 uint64_t mm_part_floats_at(const uint64_t* rows, int nseg, uint64_t in_dim, uint64_t n) {
   MmSegDesc d[3] = {};
