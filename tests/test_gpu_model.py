@@ -133,6 +133,29 @@ def test_wide_hidden_q6k_gateup(ctx, orc):
         om.close()
 
 
+# Gate/up and down at the 8B FFN width (14336 rows / inputs) through the
+# fused ffn RMSNorm + gate/up + SiLU*up and down + residual launches; on a
+# 256-CU device gate/up leaves half of its wavefronts a fourth row.
+FFN8B_CFG = dict(TINY, feed_forward_length=14336, block_count=1)
+
+
+@pytest.mark.parametrize("kind", ["q8_0", "q4_0"])
+def test_ffn_14336_width(ctx, orc, kind):
+    types = ALL_Q8 if kind == "q8_0" else ALL_Q4
+    T = _tiny_tensors(np.random.default_rng(975), FFN8B_CFG, types)
+    print(f"  ffn 14336, {kind} gate/up", flush=True)
+    gm = _load_gpu(ctx, FFN8B_CFG, T, 16)
+    om = orc.Model(FFN8B_CFG, T, kv_capacity=16, threads=8)
+    try:
+        for pos, tok in enumerate([7, 40, 2, 88]):
+            h = gm.forward(tok, pos, want_hidden=True)
+            hr = om.forward(tok, pos)
+            assert np.max(np.abs(h - hr)) <= 2e-4 * max(1.0, np.abs(hr).max()), pos
+    finally:
+        gm.close()
+        om.close()
+
+
 def test_model_create_validation(ctx):
     rf = _rf()
     used = ctx.vram_used
