@@ -62,14 +62,24 @@ typedef __amdgpu_buffer_rsrc_t PkRsrc;
 //   unit_elem    first element of unit h of the lane whose codes start at b
 //   word         decode code word i against x words (units 0 and 1)
 //   finish       scale the unit sums into the chunk's contribution
+//   INTX         codes are summed against x's int8 digit planes (idot,
+//                ifinish) instead of decoded to float (word, finish)
 // Lane constants (which sub-block / half a lane's 16 bytes fall in) depend
 // only on b % 128 = 16 (lane % 8), because every chunk starts at a multiple of
 // 1024 bytes.
 
 template <uint32_t T> struct PkFmt;
 
+// x digits of one unit (matvec_packed's prologue): x = s (65536 a + 256 b + c)
+// with int8 digits; S[p] = sum of codes times digit plane p, exact in int32.
+// The value is s times this, rounded once.
+__device__ __forceinline__ float pk_digits(const int* S) {
+  return fmaf((float)S[0], 65536.f, fmaf((float)S[1], 256.f, (float)S[2]));
+}
+
 template <> struct PkFmt<T_Q8_0> {
   static constexpr uint32_t QK = 32, EPB = 1, NREG = 2;
+  static constexpr bool INTX = true;
   __host__ __device__ static uint64_t row_bytes(int k, uint64_t in) { return k == 0 ? in : in / 32 * 2; }
   typedef uint32_t Meta;  // f16 scale bits
   struct Lane {
@@ -90,10 +100,21 @@ template <> struct PkFmt<T_Q8_0> {
   __device__ static float finish(const Lane&, const Meta& m, float s0, float, float xs0, float) {
     return rf_half_to_float_fast(m) * fmaf(-128.f, xs0, s0);
   }
+  // the codes are signed bytes: one dot4 per word and digit plane
+  __device__ static void idot(const Lane&, const nv_u32x4& q, const nv_u32x4* P, int (*S)[3]) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int p = 0; p < 3; ++p) S[0][p] = __builtin_amdgcn_sdot4((int)q[i], (int)P[p][i], S[0][p], false);
+  }
+  __device__ static float ifinish(const Lane&, const Meta& m, int (*S)[3], const float2* u) {
+    return rf_half_to_float_fast(m) * (u[0].x * pk_digits(S[0]));
+  }
 };
 
 template <> struct PkFmt<T_Q4_0> {
   static constexpr uint32_t QK = 32, EPB = 2, NREG = 2;
+  static constexpr bool INTX = true;
   __host__ __device__ static uint64_t row_bytes(int k, uint64_t in) { return k == 0 ? in / 2 : in / 32 * 2; }
   typedef uint32_t Meta;
   struct Lane {
@@ -116,6 +137,23 @@ template <> struct PkFmt<T_Q4_0> {
   __device__ static float finish(const Lane&, const Meta& m, float s0, float s1, float xs0, float xs1) {
     return rf_half_to_float_fast(m) * fmaf(-8.f, xs0 + xs1, s0 + s1);
   }
+  // nibbles 0..15 against the digits; 8 * sum(x) of both units is taken off
+  // in ifinish, from the sums of the digit-exact x
+  __device__ static void idot(const Lane&, const nv_u32x4& q, const nv_u32x4* P, int (*S)[3]) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t lo = rf_opaque(q[i] & 0x0F0F0F0Fu), hi = rf_opaque((q[i] >> 4) & 0x0F0F0F0Fu);
+#pragma unroll
+      for (int p = 0; p < 3; ++p) {
+        S[0][p] = __builtin_amdgcn_sdot4((int)lo, (int)P[p][i], S[0][p], false);
+        S[1][p] = __builtin_amdgcn_sdot4((int)hi, (int)P[3 + p][i], S[1][p], false);
+      }
+    }
+  }
+  __device__ static float ifinish(const Lane&, const Meta& m, int (*S)[3], const float2* u) {
+    const float s = fmaf(u[0].x, pk_digits(S[0]), u[1].x * pk_digits(S[1]));
+    return rf_half_to_float_fast(m) * fmaf(-8.f, u[0].y + u[1].y, s);
+  }
 };
 
 // Q4_K (quant.rs:186-255): a 256-element block is 4 groups of 64; byte l of
@@ -125,6 +163,7 @@ template <> struct PkFmt<T_Q4_0> {
 // per get_scale_min (quant.rs:216-226); value d*sc*q - dmin*m.
 template <> struct PkFmt<T_Q4_K> {
   static constexpr uint32_t QK = 256, EPB = 2, NREG = 2;
+  static constexpr bool INTX = false;
   __host__ __device__ static uint64_t row_bytes(int k, uint64_t in) { return k == 0 ? in / 2 : in / 256 * 16; }
   typedef nv_u32x4 Meta;  // d | dmin << 16, then scale bytes 0-3, 4-7, 8-11
   struct Lane {
@@ -173,6 +212,7 @@ template <> struct PkFmt<T_Q4_K> {
 // lane's 16 bytes sit at r = 16 (lane % 4) of half hf = (lane % 8) / 4.
 template <> struct PkFmt<T_Q6_K> {
   static constexpr uint32_t QK = 256, EPB = 2, NREG = 4;
+  static constexpr bool INTX = false;
   __host__ __device__ static uint64_t row_bytes(int k, uint64_t in) {
     return k == 0 ? in / 2 : k == 1 ? in / 4 : k == 2 ? in / 256 * 16 : in / 256 * 2;
   }
@@ -233,9 +273,10 @@ struct PkStep {
 // chunk c (EPL = 16 or 32 elements per slice) is stored at
 // c * 64 * EPL + 256 (4h + i) + 4 l + k.  NB step buffers per wavefront: NB - 1
 // steps are in flight while one is decoded.
-template <uint32_t T, int EPI, bool NORM, int U, int LPW, int NB, int NT>
+template <uint32_t T, int EPI, bool NORM, int U, int LPW, int NB, int NT, bool IX>
 __global__ __launch_bounds__(NT) void matvec_packed(PkArgs a) {
   typedef PkFmt<T> F;
+  constexpr bool IXE = F::INTX && IX;  // digit planes instead of float x
   constexpr bool DUAL = EPI == EPI_SWIGLU;
   constexpr uint32_t EPB = F::EPB, UPS = EPB, EPL = 16u * UPS, NW = NT / 64;
   extern __shared__ __align__(16) float xl[];  // [nchunk * 64 * EPL] x, then [nchunk * 64 * UPS] unit sums
@@ -249,6 +290,11 @@ __global__ __launch_bounds__(NT) void matvec_packed(PkArgs a) {
   const uint32_t in = a.in_dim, crb = in / EPB;
   const uint32_t nchunk = (crb + 1023u) / 1024u, nstep = (nchunk + LPW - 1) / LPW;
   float* xsum_l = xl + nchunk * 64u * EPL;
+  // INTX: digit planes (plane p of unit h of lane l in chunk c at byte
+  // ((c UPS + h) 3 + p) 1024 + 16 l), then (scale, sum of x) of unit j at
+  // float2 j; both fit in the float layout's LDS.
+  uint8_t* xdig = reinterpret_cast<uint8_t*>(xl);
+  float2* xinfo = reinterpret_cast<float2*>(xdig + nchunk * UPS * 3072u);
   const typename F::Lane LC(lane);
 
   auto seg_of = [&](uint32_t v) -> PkSeg {
@@ -319,6 +365,58 @@ __global__ __launch_bounds__(NT) void matvec_packed(PkArgs a) {
       const uint32_t js = j / UPS, h = j % UPS;
       const uint32_t b = (js >> 6) * 1024u + 16u * (js & 63u);
       float s = 0.f;
+      if constexpr (IXE) {
+        // x = 2^(E - 22) X with 2^E above the unit's largest |x|, so |X| <=
+        // 2^22, split into balanced base-256 digits X = 65536 a + 256 b + c
+        // (a in [-64, 64]); codes times digits then sum exactly in int32.
+        // E is at least -105 (the scale stays a normal float); a non-finite
+        // element makes the scale NaN, so the rows become NaN.
+        nv_u32x4 pl[3] = {};
+        float2 info = make_float2(0.f, 0.f);
+        if (b < crb) {
+          const uint32_t e = F::unit_elem(b, h);
+          float v[16];
+          float mx = 0.f;
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            const float4 xv = x4[e / 4u + k];
+            v[4 * k] = xv.x; v[4 * k + 1] = xv.y; v[4 * k + 2] = xv.z; v[4 * k + 3] = xv.w;
+            if (NORM) {
+              const float4 wv = w4[e / 4u + k];
+              ss = fmaf(xv.x, xv.x, ss); ss = fmaf(xv.y, xv.y, ss);
+              ss = fmaf(xv.z, xv.z, ss); ss = fmaf(xv.w, xv.w, ss);
+              v[4 * k] *= wv.x; v[4 * k + 1] *= wv.y; v[4 * k + 2] *= wv.z; v[4 * k + 3] *= wv.w;
+            }
+          }
+#pragma unroll
+          for (int k = 0; k < 16; ++k) mx = fmaxf(mx, fabsf(v[k]));
+          bool fin = true;
+#pragma unroll
+          for (int k = 0; k < 16; ++k) fin = fin && fabsf(v[k]) <= 3.40282347e38f;
+          int ex = 0;
+          (void)frexpf(mx, &ex);
+          ex = ex < -105 ? -105 : ex;
+          int sx = 0;
+#pragma unroll
+          for (int k = 0; k < 16; ++k) {
+            const int X = fin ? (int)rintf(ldexpf(v[k], 22 - ex)) : 0;
+            const int c0 = (int)(int8_t)(X & 0xFF), X1 = (X - c0) >> 8;
+            const int b0 = (int)(int8_t)(X1 & 0xFF), a0 = (X1 - b0) >> 8;
+            sx += X;
+            const int sh = 8 * (k & 3);
+            pl[0][k >> 2] |= (uint32_t)(a0 & 0xFF) << sh;
+            pl[1][k >> 2] |= (uint32_t)(b0 & 0xFF) << sh;
+            pl[2][k >> 2] |= (uint32_t)(c0 & 0xFF) << sh;
+          }
+          const float sc = fin ? ldexpf(1.f, ex - 22) : __builtin_nanf("");
+          info = make_float2(sc, sc * (float)sx);
+        }
+        uint8_t* dst = xdig + (((js >> 6) * UPS + h) * 3u) * 1024u + 16u * (js & 63u);
+#pragma unroll
+        for (int p = 0; p < 3; ++p) *reinterpret_cast<nv_u32x4*>(dst + 1024u * p) = pl[p];
+        xinfo[j] = info;
+        continue;
+      }
       if (b < crb) {
         const uint32_t e = F::unit_elem(b, h);
         float4 v[4], w[4];
@@ -386,6 +484,31 @@ __global__ __launch_bounds__(NT) void matvec_packed(PkArgs a) {
       // in-bounds slice of x and keep their sums by a select.
       const uint32_t c = ss * LPW + l, cx = c < nchunk ? c : nchunk - 1u;
       const bool valid = c * 1024u + 16u * lane < crb;
+      if constexpr (IXE) {
+        nv_u32x4 P[3 * UPS];
+        float2 ui[UPS];
+#pragma unroll
+        for (uint32_t h = 0; h < UPS; ++h) {
+#pragma unroll
+          for (uint32_t p = 0; p < 3; ++p)
+            P[3 * h + p] = *reinterpret_cast<const nv_u32x4*>(xdig + ((cx * UPS + h) * 3u + p) * 1024u + 16u * lane);
+          ui[h] = xinfo[(cx * 64u + lane) * UPS + h];
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          int S[UPS][3] = {};
+          F::idot(LC, B.q[u][l], P, S);
+          const float f = F::ifinish(LC, B.m[u][l], S, ui);
+          acc[u] = valid ? acc[u] + f : acc[u];
+          if constexpr (DUAL) {
+            int S2[UPS][3] = {};
+            F::idot(LC, B.q2[u][l], P, S2);
+            const float f2 = F::ifinish(LC, B.m2[u][l], S2, ui);
+            acc2[u] = valid ? acc2[u] + f2 : acc2[u];
+          }
+        }
+        continue;
+      }
       const float* xp = xl + cx * 64u * EPL + 4u * lane;
       float s0[U], s1[U], t0[U], t1[U];
 #pragma unroll
@@ -571,7 +694,7 @@ template <uint32_t T, int EPI, bool NORM, int LPW, int NB, int NT>
 static hipError_t launch_pk(const PkArgs& a, uint32_t lds, hipStream_t st) {
   constexpr int U = 1;
   static PkOccCache cache;
-  auto kern = matvec_packed<T, EPI, NORM, U, LPW, NB, NT>;
+  auto kern = matvec_packed<T, EPI, NORM, U, LPW, NB, NT, false>;
   const int occ = pk_occupancy(cache, reinterpret_cast<const void*>(kern), NT, lds);
   if (occ < 1) return hipErrorInvalidConfiguration;
   // Grid: a whole number k of workgroups per CU (a CU with one workgroup more
@@ -589,6 +712,21 @@ static hipError_t launch_pk(const PkArgs& a, uint32_t lds, hipStream_t st) {
   if (EPI == EPI_RESIDUAL) {  // at most PK_RES_SLOTS tasks per wavefront (residuals staged in LDS)
     const uint64_t need = (tasks + nw * PK_RES_SLOTS - 1) / (nw * PK_RES_SLOTS);
     if (grid < need) grid = need;
+  }
+  // Q8_0 / Q4_0 take the int8 digit planes of x when a wavefront's rows hold
+  // at least 24 KiB of codes: their split costs each workgroup a longer
+  // prologue, which the cheaper decode repays only over that many bytes
+  // (timed: gate/up 14336x4096 x2 21.7-21.9 vs 22.7-22.9 us, the 70B-shape
+  // 28672x8192 42.0 vs 43.5 us, the 8B output rows -3%; Q/K/V, o-proj and a
+  // single 14336x4096 Q4_0 matrix 0.15-1.5 us slower with them).
+  if constexpr (PkFmt<T>::INTX) {
+    const uint64_t rows_pw = (tasks * U + grid * nw - 1) / (grid * nw);
+    const uint64_t code_bytes = rows_pw * a.in_dim / PkFmt<T>::EPB * (EPI == EPI_SWIGLU ? 2 : 1);
+    if (code_bytes >= 24576) {
+      hipLaunchKernelGGL((matvec_packed<T, EPI, NORM, U, LPW, NB, NT, true>), dim3((uint32_t)grid), dim3(NT), lds, st,
+                         a);
+      return hipGetLastError();
+    }
   }
   hipLaunchKernelGGL(kern, dim3((uint32_t)grid), dim3(NT), lds, st, a);
   return hipGetLastError();
