@@ -191,13 +191,14 @@ def test_pack_weights_layout_is_exact(ctx, t):
         p.free()
 
 
-def _check_matvec_packed(ctx, orc, t, out_dim, in_dim, seed, row_start=0, row_count=None, x_off=0, patch=None):
+def _check_matvec_packed(ctx, orc, t, out_dim, in_dim, seed, row_start=0, row_count=None, x_off=0, patch=None,
+                         xgen=None):
     rf = _rf()
     rng = np.random.default_rng(seed)
     raw = random_matrix(t, out_dim, in_dim, rng)
     if patch is not None:
         raw = patch(raw.copy(), rng)
-    x = rng.normal(0, 1, in_dim).astype(np.float32)
+    x = (rng.normal(0, 1, in_dim) if xgen is None else xgen(rng, in_dim)).astype(np.float32)
     print(f"  packed matvec {NAMES[t]} out={out_dim} in={in_dim} rows={row_start}+{row_count} seed={seed} "
           f"x_off={x_off}", flush=True)
     w = ctx.array(_pack_host(t, raw, out_dim, in_dim))
@@ -227,6 +228,30 @@ def test_matvec_packed_shapes(ctx, orc, t, out_dim, in_dim):
         # x of a row must fit the workgroup's LDS (64 KiB, or what the device allows)
         pytest.skip(f"in_dim {in_dim} exceeds this device's LDS for {NAMES[t]}")
     _check_matvec_packed(ctx, orc, t, out_dim, in_dim, 1200 + t + in_dim % 977 + out_dim)
+
+
+def _x_wide_range(rng, n):
+    """x whose 16-element units span many magnitudes: per-element log-normal
+    spread, whole units of zeros, of f32 subnormals and of values near 1e30."""
+    x = rng.normal(0, 1, n) * np.exp(rng.normal(0, 4, n))
+    u = x.reshape(-1, 16)
+    u[3::29] = 0.0
+    u[5::31] = rng.normal(0, 1, (len(u[5::31]), 16)) * 1e-40
+    u[7::37] = rng.normal(0, 1, (len(u[7::37]), 16)) * 1e30
+    u[9::41, 3] = 0.0
+    return x
+
+
+# Shapes whose wavefronts hold at least 24 KiB of codes on a 256-CU device,
+# where Q8_0 and Q4_0 take x as int8 digit planes (3 rows of 8192 Q8_0 or 16384
+# Q4_0 codes per wavefront); the others above use the float path.
+@pytest.mark.parametrize("t,out_dim,in_dim", [(Q8_0, 6144, 8192), (Q4_0, 6144, 16384), (Q8_0, 28672, 8192)])
+@pytest.mark.parametrize("xkind", ["normal", "wide"])
+def test_matvec_packed_digit_planes(ctx, orc, t, out_dim, in_dim, xkind):
+    if not _rf().packed_supported(t, in_dim):
+        pytest.skip(f"in_dim {in_dim} exceeds this device's LDS for {NAMES[t]}")
+    _check_matvec_packed(ctx, orc, t, out_dim, in_dim, 1500 + t + out_dim % 97,
+                         xgen=_x_wide_range if xkind == "wide" else None)
 
 
 @pytest.mark.parametrize("t", PACKED)

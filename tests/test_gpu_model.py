@@ -156,6 +156,26 @@ def test_ffn_14336_width(ctx, orc, kind):
         om.close()
 
 
+# d 4096 with the 14336 FFN: gate/up wavefronts hold 32 KiB of codes, so the
+# fused ffn RMSNorm + gate/up + SiLU*up launch takes x as int8 digit planes.
+DIGITS_CFG = dict(TINY, embedding_length=4096, feed_forward_length=14336, block_count=1)
+
+
+def test_gateup_digit_planes(ctx, orc):
+    T = _tiny_tensors(np.random.default_rng(976), DIGITS_CFG, ALL_Q8)
+    print("  d 4096, ffn 14336, Q8_0 gate/up on digit planes", flush=True)
+    gm = _load_gpu(ctx, DIGITS_CFG, T, 16)
+    om = orc.Model(DIGITS_CFG, T, kv_capacity=16, threads=8)
+    try:
+        for pos, tok in enumerate([7, 40, 2]):
+            h = gm.forward(tok, pos, want_hidden=True)
+            hr = om.forward(tok, pos)
+            assert np.max(np.abs(h - hr)) <= 2e-4 * max(1.0, np.abs(hr).max()), pos
+    finally:
+        gm.close()
+        om.close()
+
+
 def test_model_create_validation(ctx):
     rf = _rf()
     used = ctx.vram_used
