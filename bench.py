@@ -83,34 +83,73 @@ def matvec_q8_0_gbs(ctx, rf, syn, iters: int = 120):
                                                                                       PEAK_HBM_GBS, 4)}
 
 
-def cpu_baseline(cfg, specs, tokens: int):
-    """Time the oracle (reference CPU path restated in C, reference threading
-    policy) on `tokens` decode steps of the same model at positions 0..tokens-1."""
-    import numpy as np
+def host_cores() -> dict:
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        usable = os.cpu_count() or 1
+    return {"nproc": usable, "logical_cpus": os.cpu_count(), "model": cpu_model_name()}
 
+
+def cpu_baseline(cfg, specs, first_token: int, steps: int):
+    """Time the oracle (reference CPU path restated in C, reference threading
+    policy: Q8_0 matvecs single-threaded, compute_dispatch.rs:219-254) on the
+    same model: the prompt's first token forwarded at position 0, then `steps`
+    greedy steps (logits, first-max argmax, forward), the first one untimed
+    (warmup).  Returns the timing and the greedy tokens, which the GPU
+    reproduces from the same start."""
     import oracle as orc
 
     t0 = time.perf_counter()
     T = orc.model_tensors(specs)
     gen_s = time.perf_counter() - t0
-    m = orc.Model(cfg, T, kv_capacity=tokens + 1, threads=os.cpu_count() or 1, use_simd=True)
-    per = []
-    tok = 1
-    for pos in range(tokens):
+    m = orc.Model(cfg, T, kv_capacity=steps + 2, threads=1, use_simd=True)
+    h = m.forward(first_token, 0)
+    per, toks = [], []
+    for i in range(steps):
         t0 = time.perf_counter()
-        h = m.forward(tok, pos)
-        logits = m.logits(h)
-        tok = orc.argmax(logits)
+        tok = orc.argmax(m.logits(h))
+        h = m.forward(tok, i + 1)
         per.append(time.perf_counter() - t0)
-        log(f"cpu token {pos}: {per[-1]:.2f} s")
+        toks.append(tok)
+        log(f"cpu step {i}{' (warmup)' if i == 0 else ''}: {per[-1]:.2f} s, token {tok}")
     m.close()
-    med = statistics.median(per)
+    timed = per[1:]
+    med = statistics.median(timed)
     return {"value": round(1.0 / med, 5), "unit": "tok/s", "cores": 1, "kind": "port",
-            "sample": (f"{tokens} decode steps of the same 8B-shape Q8_0 model at positions 0..{tokens - 1}, "
-                       f"median; oracle restatement of the reference CPU path (Q8_0 matvecs single-threaded "
-                       f"as in compute_dispatch.rs:219-254), host {cpu_model_name()}; weights generated in "
-                       f"{gen_s:.1f} s, untimed"),
-            "seconds_per_token": [round(p, 3) for p in per]}
+            "sample": (f"{len(timed)} greedy decode steps (logits + argmax + forward) of the same 8B-shape Q8_0 "
+                       f"model after 1 warmup step, from the prompt's first token at position 0, median; oracle "
+                       f"restatement of the reference CPU path, Q8_0 matvecs single-threaded as in "
+                       f"compute_dispatch.rs:219-254; weights generated in {gen_s:.1f} s, untimed"),
+            "host": host_cores(), "seconds_per_step": [round(p, 3) for p in timed]}, toks
+
+
+def context_decode(ctx, m, cfg, n: int, steps: int, graph: bool) -> dict:
+    """Decode tok/s at about n positions of context: n - 1 random prompt
+    tokens forwarded by the batched prefill, then `steps` timed decode steps
+    (after 4 untimed ones that capture the step graph of that context's
+    attention regime)."""
+    import numpy as np
+
+    m.reset()
+    toks = [int(t) for t in np.random.default_rng(n).integers(0, cfg["vocab_size"], n - 1)]
+    t0 = time.perf_counter()
+    m.prefill(toks)
+    ctx.synchronize()
+    pre_s = time.perf_counter() - t0
+    m.use_graph(graph)
+    m.decode_steps(4)
+    ctx.synchronize()
+    t0 = time.perf_counter()
+    m.decode_steps(steps)
+    ctx.synchronize()
+    wall = time.perf_counter() - t0
+    kv = 2 * 4 * cfg["block_count"] * cfg["head_count_kv"] * cfg["head_dim"] * (n + 4 + steps // 2)
+    out = {"tok_s": round(steps / wall, 2), "ms_per_step": round(wall * 1e3 / steps, 4), "steps": steps,
+           "positions": [n + 3, n + 3 + steps], "kv_bytes_per_step": kv, "prefill_s": round(pre_s, 3)}
+    log(f"decode at context {n}: {out['tok_s']} tok/s ({out['ms_per_step']} ms/step; prompt of {n - 1} tokens "
+        f"prefilled in {pre_s:.2f} s)")
+    return out
 
 
 def dominant_kernel(rf) -> str:
@@ -252,6 +291,34 @@ def kernel_bench(rf, syn, use_graph: bool, reps: int = 3) -> list:
     return out
 
 
+def pinned_h2d_gbs(ctx, nbytes: int = 256 << 20, reps: int = 8) -> float:
+    """Host-link peak for config 5's roofline: hipMemcpyAsync of a pinned
+    (hipHostMalloc) buffer to device memory on the copy stream, HIP events."""
+    import ctypes as C
+
+    from ramforge_amd import _lib
+
+    hp = C.c_void_p()
+    _lib.check(ctx.lib.rf_pinned_alloc(ctx.handle, nbytes, C.byref(hp)))
+    dev = ctx.empty((nbytes,), "uint8", charge="bench:h2d")
+    try:
+        C.memset(hp.value, 1, nbytes)
+        st = ctx.copy_stream
+        _lib.check(ctx.lib.rf_upload_async(ctx.handle, dev.ptr, hp.value, nbytes, st))  # warm
+        e0, e1 = ctx.event(), ctx.event()
+        ctx.record(e0, st)
+        for _ in range(reps):
+            _lib.check(ctx.lib.rf_upload_async(ctx.handle, dev.ptr, hp.value, nbytes, st))
+        ctx.record(e1, st)
+        ms = ctx.elapsed_ms(e0, e1)
+        ctx.destroy_event(e0)
+        ctx.destroy_event(e1)
+    finally:
+        dev.free()
+        ctx.lib.rf_pinned_free(ctx.handle, hp.value)
+    return nbytes * reps / (ms * 1e-3) / 1e9
+
+
 def config5_bench(rf, syn, tokens: int, prompt_len: int, policy: int) -> dict:
     """8B shape, Q4_K body + Q6_K output, VRAM budget 4 GiB:
     the layers that do not fit stream from pinned host memory each token
@@ -282,11 +349,14 @@ def config5_bench(rf, syn, tokens: int, prompt_len: int, policy: int) -> dict:
     wall = time.perf_counter() - t0
     st = m.residency_stats()
     up = st["uploaded_bytes"] - pre["uploaded_bytes"]
+    link = pinned_h2d_gbs(ctx)
+    log(f"config 5: pinned host-to-device copy peak {link:.1f} GB/s")
     out = {"workload": "config 5: 8B shape, Q4_K body + Q6_K output, 4 GiB VRAM budget, layers streamed "
                        "from pinned host memory", "cache_policy": ["lru", "next-use"][policy], "tokens": tokens, "tok_s": round(tokens / wall, 3),
            "ms_per_token": round(wall * 1e3 / tokens, 2), "uploaded_GB_per_token": round(up / tokens / 1e9, 3),
            "prompt_tokens": prompt_len, "prompt_prefill_s": round(prompt_s, 3),
-           "host_to_device_GBs": round(up / wall / 1e9, 2), "cache": st, "vram_peak_bytes": ctx.vram_peak,
+           "host_to_device_GBs": round(up / wall / 1e9, 2), "pinned_h2d_peak_GBs": round(link, 2),
+           "host_link_frac": round(up / wall / 1e9 / link, 4), "cache": st, "vram_peak_bytes": ctx.vram_peak,
            "vram_budget_bytes": budget, "fixed_vram_bytes": fixed, "layer_bytes": layer,
            "tokens_head": m.read_tokens(tokens)[:8]}
     log(f"config 5: {out['tok_s']} tok/s, {out['uploaded_GB_per_token']} GB/token uploaded at "
@@ -392,7 +462,10 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--prompt", type=int, default=32)
     ap.add_argument("--no-graph", action="store_true", help="eager launches instead of hipGraph replay")
-    ap.add_argument("--cpu-tokens", type=int, default=3)
+    ap.add_argument("--cpu-steps", type=int, default=6, help="CPU baseline greedy steps (the first one is warmup)")
+    ap.add_argument("--ctx-decode", default="2048,8192",
+                    help="context lengths (comma separated) at which decode tok/s is also measured ('' to skip)")
+    ap.add_argument("--ctx-steps", type=int, default=32)
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--prefill-tokens", type=int, default=512,
                     help="long batched prompt for the prefill measurement (0: skip the prefill measurement)")
@@ -439,7 +512,12 @@ def main() -> int:
     cfg = syn.CONFIG_8B
     specs = syn.llama_specs(cfg, syn.Q8_0, seed=8)
     wbytes = syn.weight_bytes(specs)
-    cap = max(args.prompt + args.warmup + args.steps, args.prefill_tokens) + 8
+    embd = syn.weight_bytes([s_ for s_ in specs if s_.name == "token_embd.weight"])
+    # a step reads one row of the embedding table, every other weight once
+    step_wbytes = wbytes - embd + embd // cfg["vocab_size"]
+    ctx_lens = [int(v) for v in args.ctx_decode.split(",") if v.strip()]
+    cap = max([args.prompt + args.warmup + args.steps, args.prefill_tokens] + ctx_lens) + 8
+    cap = min(cap, cfg["context_length"])
     ctx = rf.Context(0)
     name, cus = ctx.device_info()
     log(f"device {name}, {cus} CUs; building 8B-shape Q8_0 model ({wbytes / 1e9:.2f} GB) in HBM")
@@ -497,15 +575,30 @@ def main() -> int:
                 "kernel": dominant_kernel(rf) if dom == "gateup" else dom}
     log(f"dominant group {dom}: {d['us_per_launch']} us/launch, {achieved:.0f} GB/s "
         f"({achieved / PEAK_HBM_GBS:.1%} of peak); kernel time per token {kernel_ms:.3f} ms")
+    ctx_decode = {}
+    for n in ctx_lens:
+        ctx_decode[str(n)] = context_decode(ctx, m, cfg, min(n, cap - args.ctx_steps - 4), args.ctx_steps,
+                                            not args.no_graph)
+    # the GPU's greedy tokens from the start the CPU baseline uses
+    m.use_graph(False)
+    m.reset()
+    m.forward(prompt[0], 0)
+    m.decode_steps(max(args.cpu_steps, 1))
+    gpu_cpu_start = m.read_tokens(max(args.cpu_steps, 1))
     mv = matvec_q8_0_gbs(ctx, rf, syn)
     log(f"Q8_0 4096x4096 matvec: {mv['achieved_GBs']} GB/s")
     m.close()
     ctx.close()
 
     cpu = None
+    cross = None
     if not args.skip_cpu:
-        log(f"CPU baseline: {args.cpu_tokens} tokens of the oracle restatement")
-        cpu = cpu_baseline(cfg, specs, args.cpu_tokens)
+        log(f"CPU baseline: {args.cpu_steps} greedy steps of the oracle restatement (first one warmup)")
+        cpu, cpu_toks = cpu_baseline(cfg, specs, prompt[0], args.cpu_steps)
+        cross = {"start": "prompt token 0 at position 0", "cpu_tokens": cpu_toks,
+                 "gpu_tokens": gpu_cpu_start[:len(cpu_toks)], "match": cpu_toks == gpu_cpu_start[:len(cpu_toks)]}
+        log(f"CPU and GPU greedy tokens from the same start {'match' if cross['match'] else 'DIFFER'}: "
+            f"{cpu_toks} vs {cross['gpu_tokens']}")
 
     line = {
         "metric": METRIC, "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
@@ -515,9 +608,12 @@ def main() -> int:
                    "layers": cfg["block_count"], "d_model": cfg["embedding_length"],
                    "heads": [cfg["head_count"], cfg["head_count_kv"]], "ffn": cfg["feed_forward_length"],
                    "vocab": cfg["vocab_size"], "prompt_tokens": args.prompt,
-                   "weights_bytes_per_token": wbytes, "hip_graph": not args.no_graph},
+                   "weights_bytes_per_token": step_wbytes, "model_weight_bytes": wbytes,
+                   "hip_graph": not args.no_graph},
         "roofline": roofline,
         "cpu_baseline": cpu,
+        "cpu_gpu_tokens": cross,
+        "decode_at_context": ctx_decode,
         "roofline_tok_s_at_peak": round(PEAK_HBM_GBS * 1e9 / per_token_bytes, 1),
         "kernel_ms_per_token": round(kernel_ms, 4),
         "breakdown": breakdown,

@@ -21,11 +21,16 @@
  *   - `stream` is a hipStream_t; NULL selects the context's compute stream.
  *     Compute calls are asynchronous with respect to the host.
  *   - Workspaces: rf_attention_decode, rf_matmul_packed and rf_matvec_packed
- *     with a misaligned x use context-owned workspaces.  The first call that
- *     needs one (or a larger one) allocates it, synchronising the device
- *     before freeing a smaller one; later calls allocate nothing.  Calls that
- *     share a workspace must be ordered (one stream, or events), and a call
- *     to be captured in a graph must have run once outside the capture.
+ *     with a misaligned x use context-owned workspaces.  rf_ctx_reserve sizes
+ *     them up front (rf_attention_workspace_bytes / rf_matmul_workspace_bytes
+ *     give the bytes a shape needs) and, with fixed = 1, turns any later call
+ *     that would need more into an RF_ERR_INVALID error: then no entry point
+ *     allocates or synchronises on the hot path.  Without a fixed reservation
+ *     the first call that needs a workspace (or a larger one) allocates it,
+ *     synchronising the device before freeing a smaller one; that growth is
+ *     refused while the stream is being captured, and graphs captured before
+ *     a workspace was replaced are refused by rf_graph_replay.  Calls that
+ *     share a workspace must be ordered (one stream, or events).
  *   - A context is driven from one host thread at a time (the reference
  *     engine calls from one thread, parallelism is internal); the ledger
  *     calls (rf_vram_*) and rf_last_error are safe from any thread.
@@ -86,6 +91,20 @@ const char *rf_version(void);
 int32_t rf_ctx_create(int32_t device, uint64_t vram_budget_bytes, rf_ctx **out);
 void rf_ctx_destroy(rf_ctx *ctx);
 int32_t rf_ctx_synchronize(rf_ctx *ctx);
+/* Grows the context's workspaces to at least these sizes now (charges
+ * "workspace:attention", "workspace:matmul", "workspace:scratch"; 0 leaves one
+ * as it is).  staging_bytes serves rf_matvec_packed / rf_matmul_packed with an
+ * x that is not 16-byte aligned: 4 * in_dim (times min(n_tokens, 64) for the
+ * matmul).  fixed != 0: later calls never grow a workspace; one that would
+ * need more fails with RF_ERR_INVALID.  No counterpart in the reference,
+ * whose CPU kernels allocate per call (ops.rs:49-69 returns a fresh Vec). */
+int32_t rf_ctx_reserve(rf_ctx *ctx, uint64_t attention_bytes, uint64_t matmul_bytes, uint64_t staging_bytes,
+                       int32_t fixed);
+/* Workspace bytes of rf_attention_decode for every context of up to
+ * max_positions (hist_len + 1) positions with this head shape, and of
+ * rf_matmul_packed for one call of this shape (0: none needed). */
+uint64_t rf_attention_workspace_bytes(uint64_t max_positions, uint32_t q_heads, uint32_t kv_heads, uint32_t head_dim);
+uint64_t rf_matmul_workspace_bytes(uint64_t out_dim, uint64_t in_dim, uint64_t n_tokens);
 rf_stream_t rf_ctx_compute_stream(rf_ctx *ctx);
 rf_stream_t rf_ctx_copy_stream(rf_ctx *ctx);
 /* Device name and compute-unit count (for reports). */
@@ -236,8 +255,10 @@ int32_t rf_argmax(rf_ctx *ctx, const float *logits, uint64_t n, uint32_t *out_in
 
 /* Writes n_blocks GGUF blocks of ggml_type (F32: n_blocks floats) generated
  * from `seed` starting at global block index first_block, on the device.
- * Scale fields are f16(|n| * scale_mul) with n an Irwin-Hall(12) normal;
- * Q8_0 codes are uniform in [-127, 127]; the other codes are uniform bytes.
+ * Scale fields are f16(|n| * scale_mul) with n an Irwin-Hall(12) normal,
+ * except the min scale of Q4_K / Q5_K / Q2_K: the block's decoded d times the
+ * mean code (7.5 / 15.5 / 1.5), so that the weights are zero-mean.  Q8_0
+ * codes are uniform in [-127, 127]; the other codes are uniform bytes.
  * Bench and test input generator; it has no counterpart in the reference. */
 int32_t rf_synth_blocks(rf_ctx *ctx, uint32_t ggml_type, uint64_t seed, uint64_t first_block, uint64_t n_blocks,
                         double scale_mul, void *dst, uint64_t dst_bytes, rf_stream_t stream);
@@ -371,7 +392,9 @@ int32_t rf_model_time_kernel(rf_model *model, uint32_t kind, uint32_t reps, floa
  * capture: other threads are unaffected), and replays it.  No counterpart in
  * the reference; used to time kernels without host launch overhead.
  * rf_graph_replay launches the graph `reps` times on the compute stream and
- * reports the mean milliseconds per replay (HIP events). */
+ * reports the mean milliseconds per replay (HIP events).  A graph captured
+ * before one of the context's workspaces was replaced (grown) refers to the
+ * freed buffer: rf_graph_replay refuses it with RF_ERR_INVALID. */
 int32_t rf_capture_begin(rf_ctx *ctx);
 int32_t rf_capture_end(rf_ctx *ctx, void **graph);
 int32_t rf_graph_replay(rf_ctx *ctx, void *graph, uint32_t reps, float *ms_per_replay);
@@ -385,6 +408,21 @@ uint32_t rf_tune_matvec_tile_bytes(uint32_t bytes);
  * are 16-byte aligned (default), 0 = one-shot tile kernel everywhere, other
  * values only query.  Returns the mode in effect (process-wide). */
 int32_t rf_tune_matvec_kernel(int32_t mode);
+/* x of the packed Q8_0 / Q4_0 matvec: 1 = int8 digit planes on launches whose
+ * wavefronts hold >= 24 KiB of codes (default), 2 = digit planes on every
+ * launch whose workgroup LDS holds them (in_dim up to about 36000), 0 = float
+ * x everywhere; other values only query.  Returns the mode in effect (process-wide).  With digit
+ * planes each 16-element unit of x (times the RMSNorm weights where fused) is
+ * rounded to 30-bit fixed point below its largest element: element k of unit
+ * u is off by at most 2^(E_u - 31), 2^E_u the power of two above the unit's
+ * largest |x|, so a row sum is off by at most sum_u 2^(E_u - 31) sum_k |w_k|
+ * beyond f32 rounding.  The reference multiplies f32 x by each decoded weight
+ * (quant.rs:977-1029); mode 0 does the same, in another summation order.
+ * An x holding an infinity or NaN gives, in every mode and format of the
+ * packed matvec, the reference's non-finite row results: NaN where a term
+ * (decoded weight times x) is NaN or infinities of both signs meet, else the
+ * one infinity. */
+int32_t rf_tune_matvec_digits(int32_t mode);
 /* Weight layout of models created afterwards: 1 = Q8_0 / Q4_0 / Q4_K / Q6_K
  * projection weights are repacked at install into the device-native layout
  * (default; the batched prefill needs it), 0 = kept as GGUF bytes; other

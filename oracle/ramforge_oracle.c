@@ -1058,6 +1058,23 @@ static uint16_t synth_scale_f16(uint64_t s, uint64_t j, double mul) {
 
 static void put16(uint8_t *p, uint16_t v) { p[0] = (uint8_t)v; p[1] = (uint8_t)(v >> 8); }
 
+/* K-quant min scale: the block's d as the reference decodes it
+ * (orc_f16_to_f32), times the format's mean code r, encoded so that it
+ * decodes to that value again (f16 subnormals decode at half their IEEE
+ * value, so they are encoded doubled). */
+static uint16_t synth_min_f16(uint16_t dbits, float r) {
+    float v = orc_f16_to_f32(dbits) * r;
+    uint16_t h = f32_to_f16_rne(v);
+    if ((h & 0x7C00u) == 0 && (h & 0x3FFu) != 0) {
+        uint16_t h2 = f32_to_f16_rne(2.0f * v);
+        if ((h2 & 0x7C00u) == 0) h = h2;
+        /* between the largest decoded subnormal (1023 2^-25) and the smallest
+         * normal (2^-14) nothing decodes: the nearer of the two */
+        else h = (v - 1023.0f * 0x1p-25f < 0x1p-14f - v) ? 0x03FFu : 0x0400u;
+    }
+    return h;
+}
+
 static void synth_bytes(uint64_t s, uint64_t words_per_block, uint64_t block, uint8_t *out, size_t n) {
     for (size_t i = 0; i < n; i++) {
         uint64_t r = orc_synth_u64(s, words_per_block * block + i / 8);
@@ -1071,7 +1088,10 @@ static void synth_bytes(uint64_t s, uint64_t words_per_block, uint64_t block, ui
 /* Block layout of the synthetic generator (one block at global index b):
  *   Q8_0: d = f16(|n_b| * mul); q_j = ((16-bit chunk j%4 of word 8b+j/4) * 255 >> 16) - 127
  *   F32:  element b = (float)(n_b * mul)
- *   others: scale fields f16(|n| * mul) from normals 2b (d) and 2b+1 (dmin);
+ *   others: scale fields f16(|n| * mul) from normal 2b (d); the K-quant
+ *           min scale dmin = the decoded d times the mean code (Q4_K 7.5,
+ *           Q5_K 15.5, Q2_K 1.5; synth_min_f16), so that d*sc*q - dmin*m is
+ *           zero-mean over uniform codes and scales;
  *           every other byte of the block from the code stream, words_per_block
  *           = ceil(payload / 8), byte i = byte (i % 8) of word (wpb * b + i / 8).
  *   Q8_K: d = (float)(|n_b| * mul) as f32, bsums = sums of 16-element groups. */
@@ -1100,24 +1120,31 @@ int orc_synth_blocks(uint32_t t, uint64_t seed, uint64_t first, uint64_t nblk, d
             break;
         case ORC_Q4_0: put16(p, synth_scale_f16(ss, b, mul)); synth_bytes(sc, 2, b, p + 2, 16); break;
         case ORC_Q5_0: put16(p, synth_scale_f16(ss, b, mul)); synth_bytes(sc, 3, b, p + 2, 20); break;
-        case ORC_Q4_K:
-            put16(p, synth_scale_f16(ss, 2 * b, mul));
-            put16(p + 2, synth_scale_f16(ss, 2 * b + 1, mul));
+        case ORC_Q4_K: {
+            uint16_t d = synth_scale_f16(ss, 2 * b, mul);
+            put16(p, d);
+            put16(p + 2, synth_min_f16(d, 7.5f));
             synth_bytes(sc, 18, b, p + 4, 140);
             break;
-        case ORC_Q5_K:
-            put16(p, synth_scale_f16(ss, 2 * b, mul));
-            put16(p + 2, synth_scale_f16(ss, 2 * b + 1, mul));
+        }
+        case ORC_Q5_K: {
+            uint16_t d = synth_scale_f16(ss, 2 * b, mul);
+            put16(p, d);
+            put16(p + 2, synth_min_f16(d, 15.5f));
             synth_bytes(sc, 22, b, p + 4, 172);
             break;
+        }
         case ORC_Q6_K:
             synth_bytes(sc, 26, b, p, 208);
             put16(p + 208, synth_scale_f16(ss, 2 * b, mul));
             break;
         case ORC_Q2_K:
             synth_bytes(sc, 10, b, p, 80);
-            put16(p + 80, synth_scale_f16(ss, 2 * b, mul));
-            put16(p + 82, synth_scale_f16(ss, 2 * b + 1, mul));
+            {
+                uint16_t d = synth_scale_f16(ss, 2 * b, mul);
+                put16(p + 80, d);
+                put16(p + 82, synth_min_f16(d, 1.5f));
+            }
             break;
         case ORC_Q3_K:
             synth_bytes(sc, 14, b, p, 108);

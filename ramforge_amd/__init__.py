@@ -179,6 +179,18 @@ class Context:
     def synchronize(self) -> None:
         _lib.check(self.lib.rf_ctx_synchronize(self.handle))
 
+    def reserve(self, attention_bytes: int = 0, matmul_bytes: int = 0, staging_bytes: int = 0,
+                fixed: bool = True) -> None:
+        """rf_ctx_reserve: size the context workspaces now; with ``fixed`` no
+        later call grows them (a call that needs more raises instead)."""
+        _lib.check(self.lib.rf_ctx_reserve(self.handle, attention_bytes, matmul_bytes, staging_bytes, int(fixed)))
+
+    def attention_workspace_bytes(self, max_positions: int, n_heads: int, n_kv_heads: int, head_dim: int) -> int:
+        return int(self.lib.rf_attention_workspace_bytes(max_positions, n_heads, n_kv_heads, head_dim))
+
+    def matmul_workspace_bytes(self, out_dim: int, in_dim: int, n_tokens: int) -> int:
+        return int(self.lib.rf_matmul_workspace_bytes(out_dim, in_dim, n_tokens))
+
     @property
     def compute_stream(self) -> int:
         return self.lib.rf_ctx_compute_stream(self.handle)
@@ -614,6 +626,14 @@ def tune_matvec_kernel(mode: int = -1) -> int:
     """1: persistent streaming matvec (default), 0: one-shot tile kernel;
     -1 queries.  Returns the mode in effect."""
     return _lib.load().rf_tune_matvec_kernel(mode)
+
+
+def tune_matvec_digits(mode: int = -1) -> int:
+    """1: packed Q8_0 / Q4_0 launches with >= 24 KiB of codes per wavefront
+    take x as int8 digit planes (30 bits below each 16-element unit's largest
+    element; default), 2: every launch whose LDS holds them, 0: float x
+    everywhere; -1 queries.  Returns the mode in effect."""
+    return _lib.load().rf_tune_matvec_digits(mode)
 
 
 def tune_packed_weights(mode: int = -1) -> int:

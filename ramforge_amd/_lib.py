@@ -59,6 +59,9 @@ SIGNATURES = {
     "rf_ctx_create": (_i32, [_i32, _u64, C.POINTER(_vp)]),
     "rf_ctx_destroy": (None, [_vp]),
     "rf_ctx_synchronize": (_i32, [_vp]),
+    "rf_ctx_reserve": (_i32, [_vp, _u64, _u64, _u64, _i32]),
+    "rf_attention_workspace_bytes": (_u64, [_u64, _u32, _u32, _u32]),
+    "rf_matmul_workspace_bytes": (_u64, [_u64, _u64, _u64]),
     "rf_ctx_compute_stream": (_vp, [_vp]),
     "rf_ctx_copy_stream": (_vp, [_vp]),
     "rf_ctx_device_info": (_i32, [_vp, C.c_char_p, C.c_size_t, C.POINTER(_i32)]),
@@ -116,6 +119,7 @@ SIGNATURES = {
     "rf_model_time_kernel": (_i32, [_vp, _u32, _u32, C.POINTER(_f32), C.POINTER(_u64), C.POINTER(_u64)]),
     "rf_tune_matvec_tile_bytes": (_u32, [_u32]),
     "rf_tune_matvec_kernel": (_i32, [_i32]),
+    "rf_tune_matvec_digits": (_i32, [_i32]),
     "rf_tune_packed_weights": (_i32, [_i32]),
     "rf_model_enable_streaming": (_i32, [_vp, _u64]),
     "rf_model_residency_stats": (_i32, [_vp, C.POINTER(_u64)]),

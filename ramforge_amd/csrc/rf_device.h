@@ -123,3 +123,14 @@ __device__ __forceinline__ uint32_t rf_opaque(uint32_t v) {
 
 // Unsigned byte k of a word converted to float (v_cvt_f32_ubyte{k}).
 __device__ __forceinline__ float rf_ub(uint32_t w, int k) { return (float)((w >> (8 * k)) & 0xFFu); }
+// Signed byte k of a word converted to float (one v_cvt_f32_i32 with an SDWA
+// sign-extended byte operand).
+__device__ __forceinline__ float rf_sb(uint32_t w, int k) { return (float)(int8_t)((w >> (8 * k)) & 0xFFu); }
+// Signed codes c in [-2^(b-1), 2^(b-1)) stored as b-bit fields (offset
+// binary, c + 2^(b-1)) in the low bits of each byte of w, moved to the top
+// of the byte with the sign bit restored: every byte becomes the int8
+// 2^(8-b) c, so rf_sb gives the code times an exact power of two.
+__device__ __forceinline__ uint32_t rf_top_signed(uint32_t w, int b) {
+  const uint32_t top = 0x01010101u * (0xFFu << (8 - b) & 0xFFu);
+  return ((w << (8 - b)) & top) ^ 0x80808080u;
+}

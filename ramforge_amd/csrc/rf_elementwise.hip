@@ -370,6 +370,23 @@ __device__ __forceinline__ uint32_t synth_scale(uint64_t s, uint64_t j, double m
   return f32_to_f16_rne((float)__dmul_rn(fabs(synth_normal(s, j)), mul));
 }
 
+// K-quant min scale: the block's d as the reference decodes it, times the
+// format's mean code r, encoded so that it decodes to that value again (an
+// f16 subnormal decodes at half its IEEE value, so it is encoded doubled).
+// Weights d sc q - dmin m of uniform codes and scales are then zero-mean.
+__device__ __forceinline__ uint32_t synth_min(uint32_t dbits, float r) {
+  const float v = rf_half_to_float(dbits) * r;
+  uint32_t h = f32_to_f16_rne(v);
+  if ((h & 0x7C00u) == 0 && (h & 0x3FFu) != 0) {
+    const uint32_t h2 = f32_to_f16_rne(2.0f * v);
+    if ((h2 & 0x7C00u) == 0) h = h2;
+    // between the largest decoded subnormal (1023 2^-25) and the smallest
+    // normal (2^-14) nothing decodes: the nearer of the two
+    else h = (v - 1023.0f * 0x1p-25f < 0x1p-14f - v) ? 0x03FFu : 0x0400u;
+  }
+  return h;
+}
+
 __device__ __forceinline__ void put16(uint8_t* p, uint32_t v) { p[0] = (uint8_t)v; p[1] = (uint8_t)(v >> 8); }
 
 __device__ __forceinline__ void synth_fill(uint64_t s, uint64_t wpb, uint64_t b, uint8_t* out, uint32_t n) {
@@ -402,24 +419,31 @@ __global__ void synth_kernel(uint32_t t, uint64_t ss, uint64_t sc, uint64_t firs
     }
     case T_Q4_0: put16(p, synth_scale(ss, b, mul)); synth_fill(sc, 2, b, p + 2, 16); break;
     case T_Q5_0: put16(p, synth_scale(ss, b, mul)); synth_fill(sc, 3, b, p + 2, 20); break;
-    case T_Q4_K:
-      put16(p, synth_scale(ss, 2 * b, mul));
-      put16(p + 2, synth_scale(ss, 2 * b + 1, mul));
+    case T_Q4_K: {
+      const uint32_t d = synth_scale(ss, 2 * b, mul);
+      put16(p, d);
+      put16(p + 2, synth_min(d, 7.5f));
       synth_fill(sc, 18, b, p + 4, 140);
       break;
-    case T_Q5_K:
-      put16(p, synth_scale(ss, 2 * b, mul));
-      put16(p + 2, synth_scale(ss, 2 * b + 1, mul));
+    }
+    case T_Q5_K: {
+      const uint32_t d = synth_scale(ss, 2 * b, mul);
+      put16(p, d);
+      put16(p + 2, synth_min(d, 15.5f));
       synth_fill(sc, 22, b, p + 4, 172);
       break;
+    }
     case T_Q6_K:
       synth_fill(sc, 26, b, p, 208);
       put16(p + 208, synth_scale(ss, 2 * b, mul));
       break;
     case T_Q2_K:
       synth_fill(sc, 10, b, p, 80);
-      put16(p + 80, synth_scale(ss, 2 * b, mul));
-      put16(p + 82, synth_scale(ss, 2 * b + 1, mul));
+      {
+        const uint32_t d = synth_scale(ss, 2 * b, mul);
+        put16(p + 80, d);
+        put16(p + 82, synth_min(d, 1.5f));
+      }
       break;
     case T_Q3_K:
       synth_fill(sc, 14, b, p, 108);

@@ -5,10 +5,14 @@
 //     with the reference's own operation order (core/src/quant.rs:84-612) so
 //     the floats are identical to BlockXxx::dequantize.
 //   * dot_unit: the dequant-dot used by the matvec kernels.  It returns the
-//     contribution of one 32-element unit to y[row] = sum_i W[row,i] x[i]
-//     using integer codes, per-unit x sums and one scale multiply per
-//     sub-block, which is an algebraic rearrangement of sum (q*d)*x_i
-//     (different rounding, same value within float32 accumulation error).
+//     contribution of one 32-element unit to y[row] = sum_i W[row,i] x[i] as
+//     sum_i q_i x_i times the sub-block scale: the signed codes (times an
+//     exact power of two) are converted to float, so every product q_i x_i
+//     is exact up to its own rounding and a zero code adds nothing, as the
+//     reference's (q * d) * x does.  The K-quants with a min (Q4_K, Q5_K,
+//     Q2_K) subtract dmin * m * sum(x) of the sub-block, the format's own
+//     offset.  Only the association and summation order differ from
+//     sum (q*d)*x_i.
 //
 // A "unit" is 32 consecutive elements of a row.  In every format unit u of a
 // row covers x[32u, 32u+32): Q4_0/Q5_0/Q8_0 blocks are one unit, the 256-
@@ -46,12 +50,10 @@ template <> struct Fmt<T_Q8_0> {
     rf_lds_words<8>(b, blk + 2, w);
     float acc = 0.f;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const uint32_t u = w[i] ^ 0x80808080u;  // q + 128 as unsigned bytes
+    for (int i = 0; i < 8; ++i)
 #pragma unroll
-      for (int k = 0; k < 4; ++k) acc = fmaf(rf_ub(u, k), x.v[4 * i + k], acc);
-    }
-    return d * fmaf(-128.f, x.sum, acc);
+      for (int k = 0; k < 4; ++k) acc = fmaf(rf_sb(w[i], k), x.v[4 * i + k], acc);
+    return d * acc;
   }
   __device__ static void dequant(const uint8_t* b, uint32_t blk, uint32_t, float* out) {
     const float d = rf_half_to_float(rf_ld_u16(b + blk));
@@ -67,17 +69,17 @@ template <> struct Fmt<T_Q4_0> {
     const float d = rf_half_to_float(rf_lds_u32(b, blk) & 0xFFFFu);
     uint32_t w[4];
     rf_lds_words<4>(b, blk + 2, w);
-    float acc = 0.f;
+    float acc = 0.f;  // 16 (nibble - 8) as int8 bytes: exact products
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const uint32_t lo = rf_opaque(w[i] & 0x0F0F0F0Fu), hi = rf_opaque((w[i] >> 4) & 0x0F0F0F0Fu);
+      const uint32_t lo = rf_opaque(rf_top_signed(w[i], 4)), hi = rf_opaque(rf_top_signed(w[i] >> 4, 4));
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
-        acc = fmaf(rf_ub(lo, k), x.v[4 * i + k], acc);
-        acc = fmaf(rf_ub(hi, k), x.v[16 + 4 * i + k], acc);
+        acc = fmaf(rf_sb(lo, k), x.v[4 * i + k], acc);
+        acc = fmaf(rf_sb(hi, k), x.v[16 + 4 * i + k], acc);
       }
     }
-    return d * fmaf(-8.f, x.sum, acc);
+    return d * (acc * 0.0625f);
   }
   __device__ static void dequant(const uint8_t* b, uint32_t blk, uint32_t, float* out) {
     const float d = rf_half_to_float(rf_ld_u16(b + blk));
@@ -98,20 +100,21 @@ template <> struct Fmt<T_Q5_0> {
     const uint32_t qh = rf_lds_u32(b, blk + 2);
     uint32_t w[4];
     rf_lds_words<4>(b, blk + 6, w);
-    float acc = 0.f;
+    float acc = 0.f;  // 8 (q - 16) as int8 bytes: exact products
+    // bit k of a nibble to bit 4 of byte k (k * 7 + k = 8 k, then << 4)
+    auto spread = [](uint32_t nib) { return ((nib * 0x00204081u) & 0x01010101u) << 4; };
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const uint32_t lo = rf_opaque(w[i] & 0x0F0F0F0Fu), hi = rf_opaque((w[i] >> 4) & 0x0F0F0F0Fu);
+      const uint32_t lo = (w[i] & 0x0F0F0F0Fu) | spread((qh >> (4 * i)) & 0xFu);
+      const uint32_t hi = ((w[i] >> 4) & 0x0F0F0F0Fu) | spread((qh >> (4 * i + 16)) & 0xFu);
+      const uint32_t sl = rf_opaque(rf_top_signed(lo, 5)), sh = rf_opaque(rf_top_signed(hi, 5));
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
-        const int e = 4 * i + k;
-        const float ql = rf_ub(lo, k) + (float)(((qh >> e) & 1u) << 4);
-        const float qhh = rf_ub(hi, k) + (float)(((qh >> (e + 16)) & 1u) << 4);
-        acc = fmaf(ql, x.v[e], acc);
-        acc = fmaf(qhh, x.v[16 + e], acc);
+        acc = fmaf(rf_sb(sl, k), x.v[4 * i + k], acc);
+        acc = fmaf(rf_sb(sh, k), x.v[16 + 4 * i + k], acc);
       }
     }
-    return d * fmaf(-16.f, x.sum, acc);
+    return d * (acc * 0.125f);
   }
   __device__ static void dequant(const uint8_t* b, uint32_t blk, uint32_t, float* out) {
     const float d = rf_half_to_float(rf_ld_u16(b + blk));
@@ -243,16 +246,16 @@ template <> struct Fmt<T_Q6_K> {
     const uint32_t nsh = (k >> 1) * 4u, hsh = 2u * k;
     float acc_lo = 0.f, acc_hi = 0.f;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const uint32_t q = rf_opaque(((ql[i] >> nsh) & 0x0F0F0F0Fu) | (((qh[i] >> hsh) & 0x03030303u) << 4));
+    for (int i = 0; i < 8; ++i) {  // 4 (q - 32) as int8 bytes: exact products
+      const uint32_t q =
+          rf_opaque(rf_top_signed(((ql[i] >> nsh) & 0x0F0F0F0Fu) | (((qh[i] >> hsh) & 0x03030303u) << 4), 6));
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk) {
-        if (i < 4) acc_lo = fmaf(rf_ub(q, kk), x.v[4 * i + kk], acc_lo);
-        else acc_hi = fmaf(rf_ub(q, kk), x.v[4 * i + kk], acc_hi);
+        if (i < 4) acc_lo = fmaf(rf_sb(q, kk), x.v[4 * i + kk], acc_lo);
+        else acc_hi = fmaf(rf_sb(q, kk), x.v[4 * i + kk], acc_hi);
       }
     }
-    const float lo = fmaf(-32.f, x.sum_lo, acc_lo), hi = fmaf(-32.f, x.sum_hi, acc_hi);
-    return d * fmaf(sc_lo, lo, sc_hi * hi);
+    return d * (fmaf(sc_lo, acc_lo, sc_hi * acc_hi) * 0.25f);
   }
   __device__ static void dequant(const uint8_t* b, uint32_t blk, uint32_t s, float* out) {
     const uint32_t hf = s >> 2, k = s & 3u;
@@ -343,16 +346,16 @@ template <> struct Fmt<T_Q3_K> {
     const uint32_t bit = 4 * n + j;
     float acc_lo = 0.f, acc_hi = 0.f;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const uint32_t t = ((w[i] >> (2 * j)) & 0x03030303u) | (((hm[i] >> bit) & 0x01010101u) << 2);
+    for (int i = 0; i < 8; ++i) {  // 32 (t - 4) as int8 bytes: exact products
+      const uint32_t t =
+          rf_opaque(rf_top_signed(((w[i] >> (2 * j)) & 0x03030303u) | (((hm[i] >> bit) & 0x01010101u) << 2), 3));
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk) {
-        if (i < 4) acc_lo = fmaf(rf_ub(t, kk), x.v[4 * i + kk], acc_lo);
-        else acc_hi = fmaf(rf_ub(t, kk), x.v[4 * i + kk], acc_hi);
+        if (i < 4) acc_lo = fmaf(rf_sb(t, kk), x.v[4 * i + kk], acc_lo);
+        else acc_hi = fmaf(rf_sb(t, kk), x.v[4 * i + kk], acc_hi);
       }
     }
-    const float lo = fmaf(-4.f, x.sum_lo, acc_lo), hi = fmaf(-4.f, x.sum_hi, acc_hi);
-    return d * fmaf(sc_lo, lo, sc_hi * hi);
+    return d * (fmaf(sc_lo, acc_lo, sc_hi * acc_hi) * 0.03125f);
   }
   __device__ static void dequant(const uint8_t* b, uint32_t blk, uint32_t s, float* out) {
     const uint32_t n = s >> 2, j = s & 3u;
@@ -385,12 +388,10 @@ template <> struct Fmt<T_Q8_K> {
     rf_lds_words<8>(b, blk + 4 + 32 * s, w);
     float acc = 0.f;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const uint32_t u = w[i] ^ 0x80808080u;
+    for (int i = 0; i < 8; ++i)
 #pragma unroll
-      for (int k = 0; k < 4; ++k) acc = fmaf(rf_ub(u, k), x.v[4 * i + k], acc);
-    }
-    return d * fmaf(-128.f, x.sum, acc);
+      for (int k = 0; k < 4; ++k) acc = fmaf(rf_sb(w[i], k), x.v[4 * i + k], acc);
+    return d * acc;
   }
   __device__ static void dequant(const uint8_t* b, uint32_t blk, uint32_t s, float* out) {
     float d;
@@ -416,5 +417,34 @@ template <> struct Fmt<T_F32> {
     return acc;
   }
 };
+
+// A unit of x holding an infinity or NaN: in place of the dot, the kind of
+// the reference's terms (q * d) * x_i with each weight decoded bit-exactly
+// (dequant): NaN when a term is NaN or infinities of both signs occur, else
+// the one infinity.  Adding such values reproduces the reference's row
+// result for any summation order: finite units do not change an infinity,
+// and +inf + -inf and NaN + anything are NaN.
+template <uint32_t T>
+__device__ float unit_kinds(const uint8_t* b, uint32_t blk, uint32_t sub, const XUnit& x) {
+  float deq[32];
+  Fmt<T>::dequant(b, blk, sub, deq);
+  bool nan = false, pinf = false, ninf = false;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) {
+    const float t = deq[i] * x.v[i];
+    nan = nan || t != t;
+    pinf = pinf || t == __builtin_inff();
+    ninf = ninf || t == -__builtin_inff();
+  }
+  if (nan || (pinf && ninf)) return __builtin_nanf("");
+  return pinf ? __builtin_inff() : (ninf ? -__builtin_inff() : 0.f);
+}
+
+__device__ __forceinline__ bool unit_finite(const XUnit& x) {
+  bool ok = true;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) ok = ok && fabsf(x.v[i]) <= 3.40282347e38f;
+  return ok;
+}
 
 }  // namespace rf

@@ -60,6 +60,10 @@ void set_matvec_stream_tile(uint32_t bytes);
 uint32_t matvec_tile_bytes();
 void set_matvec_stream(bool on);
 bool matvec_stream();
+// Packed Q8_0 / Q4_0 launches take x as int8 digit planes when a wavefront's
+// rows hold >= 24 KiB of codes (1), always (2), or never (0).
+void set_matvec_digits(int mode);
+int matvec_digits();
 hipError_t launch_matvec_segments(uint32_t t, const MvSegDesc* segs, int nseg, const float* x,
                                   const float* norm_w, float eps, uint64_t in_dim, int epi,
                                   hipStream_t st);

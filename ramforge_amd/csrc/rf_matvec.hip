@@ -114,6 +114,16 @@ __device__ __forceinline__ void finish_xunit(XUnit& xu) {
   xu.sum = lo + hi;
 }
 
+// Contribution of unit `sub` of the block at `blk`: the dot, or for a unit of
+// x holding an infinity or NaN the kind of the reference's terms
+// (unit_kinds), so the row sums come out as the reference's NaN / +-inf.
+// F32 products are the reference's terms already.
+template <uint32_t T>
+__device__ __forceinline__ float unit_dot(const uint8_t* b, uint32_t blk, uint32_t sub, const XUnit& x, bool finite) {
+  if constexpr (T == T_F32) return Fmt<T>::dot(b, blk, sub, x);
+  else return finite ? Fmt<T>::dot(b, blk, sub, x) : unit_kinds<T>(b, blk, sub, x);
+}
+
 template <uint32_t T, int EPI>
 __global__ __launch_bounds__(1024) void matvec_tiled(MvArgs a) {
   extern __shared__ __align__(16) uint8_t lds[];
@@ -149,6 +159,7 @@ __global__ __launch_bounds__(1024) void matvec_tiled(MvArgs a) {
     __syncthreads();
   }
   finish_xunit(xu);
+  const bool xfin = unit_finite(xu);
 
   const uint32_t blk = (u / UPB) * Fmt<T>::BS, sub = u % UPB;
   constexpr int MAXR = 8;
@@ -159,8 +170,8 @@ __global__ __launch_bounds__(1024) void matvec_tiled(MvArgs a) {
     part2[k] = 0.f;
     const uint32_t r = g + k * a.rg;
     if (active && r < nrows) {
-      part[k] = Fmt<T>::dot(lds, r * row_bytes + blk, sub, xu);
-      if (EPI == EPI_SWIGLU) part2[k] = Fmt<T>::dot(lds + a.tile_stride, r * row_bytes + blk, sub, xu);
+      part[k] = unit_dot<T>(lds, r * row_bytes + blk, sub, xu, xfin);
+      if (EPI == EPI_SWIGLU) part2[k] = unit_dot<T>(lds + a.tile_stride, r * row_bytes + blk, sub, xu, xfin);
     }
   }
   __syncthreads();
@@ -284,6 +295,7 @@ __global__ __launch_bounds__(512) void matvec_stream(MvArgs a) {
   }
   if (a.norm_w != nullptr) norm_xunit(xu, nw, active && g == 0, a.in_dim, a.eps, wsum, tid, nth);
   finish_xunit(xu);
+  const bool xfin = unit_finite(xu);
 
   const uint32_t row_bytes = a.row_bytes;
   const uint32_t blk = (u / UPB) * Fmt<T>::BS, sub = u % UPB;
@@ -305,8 +317,9 @@ __global__ __launch_bounds__(512) void matvec_stream(MvArgs a) {
     for (int k = 0; k < MAXR; ++k) {
       const uint32_t r = g + k * a.rg;
       if (active && r < nrows) {
-        red[r * units + u] = Fmt<T>::dot(lds, r * row_bytes + blk, sub, xu);
-        if (DUAL) red[(nrows + r) * units + u] = Fmt<T>::dot(lds + nrows * row_bytes, r * row_bytes + blk, sub, xu);
+        red[r * units + u] = unit_dot<T>(lds, r * row_bytes + blk, sub, xu, xfin);
+        if (DUAL)
+          red[(nrows + r) * units + u] = unit_dot<T>(lds + nrows * row_bytes, r * row_bytes + blk, sub, xu, xfin);
       }
     }
     __syncthreads();

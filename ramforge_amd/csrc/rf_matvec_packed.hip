@@ -35,6 +35,7 @@
 #include "rf_kernels.h"
 
 #include <mutex>
+#include <type_traits>
 
 namespace rf {
 
@@ -70,11 +71,27 @@ typedef __amdgpu_buffer_rsrc_t PkRsrc;
 
 template <uint32_t T> struct PkFmt;
 
-// x digits of one unit (matvec_packed's prologue): x = s (65536 a + 256 b + c)
-// with int8 digits; S[p] = sum of codes times digit plane p, exact in int32.
-// The value is s times this, rounded once.
+// x digits of one unit (matvec_packed's prologue): x = s X with the int32
+// X = 2^24 a + 2^16 b + 2^8 c + e in balanced int8 digits (PK_PLANES planes);
+// S[p] = sum of codes times digit plane p, exact in int32 (|S| < 2^18).  The
+// unit's value is s times S[0] 2^24 + S[1] 2^16 + S[2] 2^8 + S[3]: the pairs
+// are joined exactly in int32 (|S[0] 2^8 + S[1]| < 2^26), then two
+// conversions and one fma round, each at most 2^-24 relative.
+constexpr int PK_PLANES = 4;
 __device__ __forceinline__ float pk_digits(const int* S) {
-  return fmaf((float)S[0], 65536.f, fmaf((float)S[1], 256.f, (float)S[2]));
+  const int hi = S[0] * 256 + S[1], lo = S[2] * 256 + S[3];
+  return fmaf((float)hi, 65536.f, (float)lo);
+}
+
+// Non-finite x (matvec_packed's fallback): the kind of the reference's
+// term deq * x, as bit 0 NaN, bit 1 +inf, bit 2 -inf.
+__device__ __forceinline__ uint32_t pk_term_kind(float deq, float x) {
+  const float t = deq * x;
+  return t != t ? 1u : (t == __builtin_inff() ? 2u : (t == -__builtin_inff() ? 4u : 0u));
+}
+__device__ __forceinline__ uint32_t pk_word_kinds(const float* deq, const float4& x) {
+  return pk_term_kind(deq[0], x.x) | pk_term_kind(deq[1], x.y) | pk_term_kind(deq[2], x.z) |
+         pk_term_kind(deq[3], x.w);
 }
 
 template <> struct PkFmt<T_Q8_0> {
@@ -90,25 +107,34 @@ template <> struct PkFmt<T_Q8_0> {
     m = __builtin_amdgcn_raw_buffer_load_b16(r[1], (b >> 5) << 1, 0, 0);  // block b/32, 2 bytes each
   }
   __device__ static uint32_t unit_elem(uint32_t b, uint32_t) { return b; }
-  // q + 128 as unsigned bytes (XOR 0x80); the 128 * sum(x) is taken off in finish
+  // signed codes times x, each product exact up to its own rounding (a zero
+  // code adds exactly nothing, as the reference's (q * d) * x does)
   __device__ static void word(const Lane&, uint32_t q, const Meta&, int, const float4& xv, const float4&,
                               float& s0, float&) {
-    const uint32_t w = q ^ 0x80808080u;
-    s0 = fmaf(rf_ub(w, 0), xv.x, s0); s0 = fmaf(rf_ub(w, 1), xv.y, s0);
-    s0 = fmaf(rf_ub(w, 2), xv.z, s0); s0 = fmaf(rf_ub(w, 3), xv.w, s0);
+    s0 = fmaf(rf_sb(q, 0), xv.x, s0); s0 = fmaf(rf_sb(q, 1), xv.y, s0);
+    s0 = fmaf(rf_sb(q, 2), xv.z, s0); s0 = fmaf(rf_sb(q, 3), xv.w, s0);
   }
-  __device__ static float finish(const Lane&, const Meta& m, float s0, float, float xs0, float) {
-    return rf_half_to_float_fast(m) * fmaf(-128.f, xs0, s0);
+  __device__ static float finish(const Lane&, const Meta& m, float s0, float, float, float) {
+    return rf_half_to_float_fast(m) * s0;
   }
   // the codes are signed bytes: one dot4 per word and digit plane
-  __device__ static void idot(const Lane&, const nv_u32x4& q, const nv_u32x4* P, int (*S)[3]) {
+  __device__ static void idot(const Lane&, const nv_u32x4& q, const nv_u32x4* P, int (*S)[PK_PLANES]) {
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int p = 0; p < 3; ++p) S[0][p] = __builtin_amdgcn_sdot4((int)q[i], (int)P[p][i], S[0][p], false);
+      for (int p = 0; p < PK_PLANES; ++p)
+        S[0][p] = __builtin_amdgcn_sdot4((int)q[i], (int)P[p][i], S[0][p], false);
   }
-  __device__ static float ifinish(const Lane&, const Meta& m, int (*S)[3], const float2* u) {
+  __device__ static float ifinish(const Lane&, const Meta& m, int (*S)[PK_PLANES], const float2* u) {
     return rf_half_to_float_fast(m) * (u[0].x * pk_digits(S[0]));
+  }
+  // word i's terms, each weight decoded as the reference does (quant.rs:177-181: q * d)
+  __device__ static uint32_t kinds(const Lane&, uint32_t q, const Meta& m, int, const float4& xv, const float4&) {
+    const float d = rf_half_to_float_fast(m);
+    float deq[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) deq[k] = (float)(int8_t)((q >> (8 * k)) & 0xFFu) * d;
+    return pk_word_kinds(deq, xv);
   }
 };
 
@@ -126,33 +152,46 @@ template <> struct PkFmt<T_Q4_0> {
   }
   // byte j: low nibble -> element j, high nibble -> element j + 16 (quant.rs:84-113)
   __device__ static uint32_t unit_elem(uint32_t b, uint32_t h) { return 2u * b + 16u * h; }
+  // The signed codes nibble - 8 as int8 bytes 16 (nibble - 8): products with
+  // x are exact up to their own rounding (no -8 sum(x) correction to cancel
+  // against), and the factor 16 comes off exactly in finish.
   __device__ static void word(const Lane&, uint32_t q, const Meta&, int, const float4& xv, const float4& xw,
                               float& s0, float& s1) {
-    const uint32_t lo = rf_opaque(q & 0x0F0F0F0Fu), hi = rf_opaque((q >> 4) & 0x0F0F0F0Fu);
-    s0 = fmaf(rf_ub(lo, 0), xv.x, s0); s0 = fmaf(rf_ub(lo, 1), xv.y, s0);
-    s0 = fmaf(rf_ub(lo, 2), xv.z, s0); s0 = fmaf(rf_ub(lo, 3), xv.w, s0);
-    s1 = fmaf(rf_ub(hi, 0), xw.x, s1); s1 = fmaf(rf_ub(hi, 1), xw.y, s1);
-    s1 = fmaf(rf_ub(hi, 2), xw.z, s1); s1 = fmaf(rf_ub(hi, 3), xw.w, s1);
+    const uint32_t lo = rf_opaque(rf_top_signed(q, 4)), hi = rf_opaque(rf_top_signed(q >> 4, 4));
+    s0 = fmaf(rf_sb(lo, 0), xv.x, s0); s0 = fmaf(rf_sb(lo, 1), xv.y, s0);
+    s0 = fmaf(rf_sb(lo, 2), xv.z, s0); s0 = fmaf(rf_sb(lo, 3), xv.w, s0);
+    s1 = fmaf(rf_sb(hi, 0), xw.x, s1); s1 = fmaf(rf_sb(hi, 1), xw.y, s1);
+    s1 = fmaf(rf_sb(hi, 2), xw.z, s1); s1 = fmaf(rf_sb(hi, 3), xw.w, s1);
   }
-  __device__ static float finish(const Lane&, const Meta& m, float s0, float s1, float xs0, float xs1) {
-    return rf_half_to_float_fast(m) * fmaf(-8.f, xs0 + xs1, s0 + s1);
+  __device__ static float finish(const Lane&, const Meta& m, float s0, float s1, float, float) {
+    return rf_half_to_float_fast(m) * ((s0 + s1) * 0.0625f);
   }
-  // nibbles 0..15 against the digits; 8 * sum(x) of both units is taken off
-  // in ifinish, from the sums of the digit-exact x
-  __device__ static void idot(const Lane&, const nv_u32x4& q, const nv_u32x4* P, int (*S)[3]) {
+  // the same int8 bytes 16 (nibble - 8) against the digits: exact int32 sums
+  __device__ static void idot(const Lane&, const nv_u32x4& q, const nv_u32x4* P, int (*S)[PK_PLANES]) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const uint32_t lo = rf_opaque(q[i] & 0x0F0F0F0Fu), hi = rf_opaque((q[i] >> 4) & 0x0F0F0F0Fu);
+      const uint32_t lo = rf_opaque(rf_top_signed(q[i], 4)), hi = rf_opaque(rf_top_signed(q[i] >> 4, 4));
 #pragma unroll
-      for (int p = 0; p < 3; ++p) {
+      for (int p = 0; p < PK_PLANES; ++p) {
         S[0][p] = __builtin_amdgcn_sdot4((int)lo, (int)P[p][i], S[0][p], false);
-        S[1][p] = __builtin_amdgcn_sdot4((int)hi, (int)P[3 + p][i], S[1][p], false);
+        S[1][p] = __builtin_amdgcn_sdot4((int)hi, (int)P[PK_PLANES + p][i], S[1][p], false);
       }
     }
   }
-  __device__ static float ifinish(const Lane&, const Meta& m, int (*S)[3], const float2* u) {
+  __device__ static float ifinish(const Lane&, const Meta& m, int (*S)[PK_PLANES], const float2* u) {
     const float s = fmaf(u[0].x, pk_digits(S[0]), u[1].x * pk_digits(S[1]));
-    return rf_half_to_float_fast(m) * fmaf(-8.f, u[0].y + u[1].y, s);
+    return rf_half_to_float_fast(m) * (s * 0.0625f);
+  }
+  // (nibble - 8) * d, low nibbles against unit 0, high against unit 1 (quant.rs:104-112)
+  __device__ static uint32_t kinds(const Lane&, uint32_t q, const Meta& m, int, const float4& xv, const float4& xw) {
+    const float d = rf_half_to_float_fast(m);
+    float lo[4], hi[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      lo[k] = (float)((int)((q >> (8 * k)) & 0xFu) - 8) * d;
+      hi[k] = (float)((int)((q >> (8 * k + 4)) & 0xFu) - 8) * d;
+    }
+    return pk_word_kinds(lo, xv) | pk_word_kinds(hi, xw);
   }
 };
 
@@ -183,9 +222,14 @@ template <> struct PkFmt<T_Q4_K> {
     const uint32_t o = b & 127u;
     return (b >> 7) * 256u + 64u * (o >> 5) + 16u * ((o >> 4) & 1u) + 32u * h;
   }
-  __device__ static void word(const Lane& L, uint32_t q, const Meta& m, int i, const float4& xv, const float4& xw,
+  // unsigned nibbles: the min term dmin * m * sum(x) is part of the format
+  __device__ static void word(const Lane&, uint32_t q, const Meta&, int, const float4& xv, const float4& xw,
                               float& s0, float& s1) {
-    PkFmt<T_Q4_0>::word(PkFmt<T_Q4_0>::Lane(0), q, 0u, i, xv, xw, s0, s1);
+    const uint32_t lo = rf_opaque(q & 0x0F0F0F0Fu), hi = rf_opaque((q >> 4) & 0x0F0F0F0Fu);
+    s0 = fmaf(rf_ub(lo, 0), xv.x, s0); s0 = fmaf(rf_ub(lo, 1), xv.y, s0);
+    s0 = fmaf(rf_ub(lo, 2), xv.z, s0); s0 = fmaf(rf_ub(lo, 3), xv.w, s0);
+    s1 = fmaf(rf_ub(hi, 0), xw.x, s1); s1 = fmaf(rf_ub(hi, 1), xw.y, s1);
+    s1 = fmaf(rf_ub(hi, 2), xw.z, s1); s1 = fmaf(rf_ub(hi, 3), xw.w, s1);
   }
   __device__ static float finish(const Lane& L, const Meta& m, float s0, float s1, float xs0, float xs1) {
     // sub-blocks j = 2g (+0) and 2g + 1 (+8 bits): for j < 4 sc = S[j] & 63,
@@ -202,6 +246,27 @@ template <> struct PkFmt<T_Q4_K> {
     const float d = rf_half_to_float_fast(m.x & 0xFFFFu), dmin = rf_half_to_float_fast(m.x >> 16);
     const float r0 = fmaf(d * (float)sc[0], s0, -(dmin * (float)mn[0]) * xs0);
     return fmaf(d * (float)sc[1], s1, fmaf(-(dmin * (float)mn[1]), xs1, r0));
+  }
+  // d1 * q - m1 with d1 = d * sc, m1 = dmin * m (quant.rs:228-254), no fused multiply-add
+  __device__ static uint32_t kinds(const Lane& L, uint32_t q, const Meta& m, int, const float4& xv, const float4& xw) {
+    const float d = rf_half_to_float_fast(m.x & 0xFFFFu), dmin = rf_half_to_float_fast(m.x >> 16);
+    uint32_t out = 0;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const uint32_t s = L.sh + 8u * h;
+      const uint32_t a = (m.y >> s) & 0xFFu, c = (m.z >> s) & 0xFFu, e = (m.w >> s) & 0xFFu;
+      const uint32_t sc = L.hi ? ((e & 15u) | ((a >> 6) << 4)) : (a & 63u);
+      const uint32_t mn = L.hi ? ((e >> 4) | ((c >> 6) << 4)) : (c & 63u);
+      const float d1 = d * (float)sc, m1 = dmin * (float)mn;
+      float deq[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const float prod = d1 * (float)((q >> (8 * k + 4 * h)) & 0xFu);
+        deq[k] = __fsub_rn(prod, m1);
+      }
+      out |= pk_word_kinds(deq, h ? xw : xv);
+    }
+    return out;
   }
 };
 
@@ -243,20 +308,42 @@ template <> struct PkFmt<T_Q6_K> {
   }
   __device__ static void word(const Lane& L, uint32_t q, const Meta& m, int i, const float4& xv, const float4& xw,
                               float& s0, float& s1) {
+    // the 6-bit codes q - 32 as int8 bytes 4 (q - 32): exact products, the
+    // factor 4 comes off exactly in finish
     const uint32_t h = m.qh[i];
-    const uint32_t lo = rf_opaque((q & 0x0F0F0F0Fu) | (((h >> L.qsh) & 0x03030303u) << 4));
-    const uint32_t hi = rf_opaque(((q >> 4) & 0x0F0F0F0Fu) | (((h >> (L.qsh + 4u)) & 0x03030303u) << 4));
-    s0 = fmaf(rf_ub(lo, 0), xv.x, s0); s0 = fmaf(rf_ub(lo, 1), xv.y, s0);
-    s0 = fmaf(rf_ub(lo, 2), xv.z, s0); s0 = fmaf(rf_ub(lo, 3), xv.w, s0);
-    s1 = fmaf(rf_ub(hi, 0), xw.x, s1); s1 = fmaf(rf_ub(hi, 1), xw.y, s1);
-    s1 = fmaf(rf_ub(hi, 2), xw.z, s1); s1 = fmaf(rf_ub(hi, 3), xw.w, s1);
+    const uint32_t lo = rf_opaque(rf_top_signed((q & 0x0F0F0F0Fu) | (((h >> L.qsh) & 0x03030303u) << 4), 6));
+    const uint32_t hi =
+        rf_opaque(rf_top_signed(((q >> 4) & 0x0F0F0F0Fu) | (((h >> (L.qsh + 4u)) & 0x03030303u) << 4), 6));
+    s0 = fmaf(rf_sb(lo, 0), xv.x, s0); s0 = fmaf(rf_sb(lo, 1), xv.y, s0);
+    s0 = fmaf(rf_sb(lo, 2), xv.z, s0); s0 = fmaf(rf_sb(lo, 3), xv.w, s0);
+    s1 = fmaf(rf_sb(hi, 0), xw.x, s1); s1 = fmaf(rf_sb(hi, 1), xw.y, s1);
+    s1 = fmaf(rf_sb(hi, 2), xw.z, s1); s1 = fmaf(rf_sb(hi, 3), xw.w, s1);
   }
-  __device__ static float finish(const Lane& L, const Meta& m, float s0, float s1, float xs0, float xs1) {
+  __device__ static float finish(const Lane& L, const Meta& m, float s0, float s1, float, float) {
     const uint32_t w0 = L.hf ? m.sc.z : m.sc.x, w1 = L.hf ? m.sc.w : m.sc.y;
     const float sc0 = (float)(int32_t)(int8_t)((w0 >> L.bsh) & 0xFFu);
     const float sc1 = (float)(int32_t)(int8_t)((w1 >> L.bsh) & 0xFFu);
     const float d = rf_half_to_float_fast(m.d);
-    return d * fmaf(sc0, fmaf(-32.f, xs0, s0), sc1 * fmaf(-32.f, xs1, s1));
+    return d * (fmaf(sc0, s0, sc1 * s1) * 0.25f);
+  }
+  // (d * sc) * (q - 32) (quant.rs:376-406)
+  __device__ static uint32_t kinds(const Lane& L, uint32_t q, const Meta& m, int i, const float4& xv,
+                                   const float4& xw) {
+    const uint32_t h = m.qh[i];
+    const uint32_t w0 = L.hf ? m.sc.z : m.sc.x, w1 = L.hf ? m.sc.w : m.sc.y;
+    const float d = rf_half_to_float_fast(m.d);
+    const float ds0 = d * (float)(int32_t)(int8_t)((w0 >> L.bsh) & 0xFFu);
+    const float ds1 = d * (float)(int32_t)(int8_t)((w1 >> L.bsh) & 0xFFu);
+    float lo[4], hi[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const uint32_t sh = 8u * k;
+      const int ql = (int)(((q >> sh) & 0xFu) | (((h >> (L.qsh + sh)) & 3u) << 4));
+      const int qh = (int)(((q >> (sh + 4u)) & 0xFu) | (((h >> (L.qsh + 4u + sh)) & 3u) << 4));
+      lo[k] = ds0 * (float)(ql - 32);
+      hi[k] = ds1 * (float)(qh - 32);
+    }
+    return pk_word_kinds(lo, xv) | pk_word_kinds(hi, xw);
   }
 };
 
@@ -281,8 +368,10 @@ __global__ __launch_bounds__(NT) void matvec_packed(PkArgs a) {
   constexpr uint32_t EPB = F::EPB, UPS = EPB, EPL = 16u * UPS, NW = NT / 64;
   extern __shared__ __align__(16) float xl[];  // [nchunk * 64 * EPL] x, then [nchunk * 64 * UPS] unit sums
   __shared__ float wsum[NW];
+  __shared__ uint32_t wbad[NW];  // the wavefront staged a non-finite x element
   __shared__ float resl[EPI == EPI_RESIDUAL ? NW : 1][PK_RES_SLOTS][U];
-  static_assert(sizeof(wsum) + sizeof(resl) <= PK_STATIC_LDS, "static LDS above the planner's reservation");
+  static_assert(sizeof(wsum) + sizeof(wbad) + sizeof(resl) <= PK_STATIC_LDS,
+                "static LDS above the planner's reservation");
   // The wavefront index through readfirstlane: rows, segments and their
   // pointers are then scalar values, so no vector load (whose wait would also
   // wait for the codes in flight) is spent on them.
@@ -291,10 +380,11 @@ __global__ __launch_bounds__(NT) void matvec_packed(PkArgs a) {
   const uint32_t nchunk = (crb + 1023u) / 1024u, nstep = (nchunk + LPW - 1) / LPW;
   float* xsum_l = xl + nchunk * 64u * EPL;
   // INTX: digit planes (plane p of unit h of lane l in chunk c at byte
-  // ((c UPS + h) 3 + p) 1024 + 16 l), then (scale, sum of x) of unit j at
-  // float2 j; both fit in the float layout's LDS.
+  // ((c UPS + h) PK_PLANES + p) 1024 + 16 l), then (scale, scale * sum of X)
+  // of unit j at float2 j.  The launch sizes LDS for the larger of this and
+  // the float layout, which the kernel falls back to for a non-finite x.
   uint8_t* xdig = reinterpret_cast<uint8_t*>(xl);
-  float2* xinfo = reinterpret_cast<float2*>(xdig + nchunk * UPS * 3072u);
+  float2* xinfo = reinterpret_cast<float2*>(xdig + nchunk * UPS * (1024u * PK_PLANES));
   const typename F::Lane LC(lane);
 
   auto seg_of = [&](uint32_t v) -> PkSeg {
@@ -357,92 +447,110 @@ __global__ __launch_bounds__(NT) void matvec_packed(PkArgs a) {
   // scaled by 1 / sqrt(mean(x^2) + eps) in the epilogue (the same value up to
   // rounding), so the mean's reduction shares the prologue's barrier.
   const uint32_t nunit = nchunk * 64u * UPS;
+  const float4* x4 = reinterpret_cast<const float4*>(a.x);
+  const float4* w4 = reinterpret_cast<const float4*>(a.norm_w);
+  // The 16 elements of unit j (times the norm weights), their squares summed
+  // into ss; false for the zero padding past the row.
+  auto load_unit = [&](uint32_t j, float* v, float& ss, bool sq) -> bool {
+    const uint32_t js = j / UPS, h = j % UPS;
+    const uint32_t b = (js >> 6) * 1024u + 16u * (js & 63u);
+    if (b >= crb) return false;
+    const uint32_t e = F::unit_elem(b, h);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const float4 xv = x4[e / 4u + k];
+      v[4 * k] = xv.x; v[4 * k + 1] = xv.y; v[4 * k + 2] = xv.z; v[4 * k + 3] = xv.w;
+      if (NORM) {
+        const float4 wv = w4[e / 4u + k];
+        if (sq) {
+          ss = fmaf(xv.x, xv.x, ss); ss = fmaf(xv.y, xv.y, ss);
+          ss = fmaf(xv.z, xv.z, ss); ss = fmaf(xv.w, xv.w, ss);
+        }
+        v[4 * k] *= wv.x; v[4 * k + 1] *= wv.y; v[4 * k + 2] *= wv.z; v[4 * k + 3] *= wv.w;
+      }
+    }
+    return true;
+  };
+  // Float layout: the unit in its permuted LDS slots and its sum.  Returns
+  // false for a non-finite element.
+  auto stage_float = [&](uint32_t j, float& ss, bool sq) -> bool {
+    const uint32_t js = j / UPS, h = j % UPS;
+    float v[16];
+    float s = 0.f;
+    bool fin = true;
+    if (load_unit(j, v, ss, sq)) {
+      float* dst = xl + (js >> 6) * 64u * EPL + 4u * h * 256u + 4u * (js & 63u);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        *reinterpret_cast<float4*>(dst + 256 * k) = make_float4(v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]);
+        s += v[4 * k]; s += v[4 * k + 1]; s += v[4 * k + 2]; s += v[4 * k + 3];
+      }
+#pragma unroll
+      for (int k = 0; k < 16; ++k) fin = fin && fabsf(v[k]) <= 3.40282347e38f;
+    }
+    xsum_l[j] = s;
+    return fin;
+  };
+  // Digit layout: with 2^E above the unit's largest |x|, X = rint(x 2^(30 - E))
+  // (|X| < 2^30) in balanced base-256 digits X = 2^24 a + 2^16 b + 2^8 c + e
+  // (a in [-64, 64]); codes times digits then sum exactly in int32.  Each
+  // element is off by at most 2^(E - 31), i.e. x keeps 30 bits below the
+  // unit's largest element.  E is at least -96 so the scale 2^(E - 30) is a
+  // normal float.  Returns false for a non-finite element (the kernel then
+  // restages x as floats).
+  auto stage_digits = [&](uint32_t j, float& ss) -> bool {
+    const uint32_t js = j / UPS, h = j % UPS;
+    nv_u32x4 pl[PK_PLANES] = {};
+    float2 info = make_float2(0.f, 0.f);
+    float v[16];
+    bool fin = true;
+    if (load_unit(j, v, ss, true)) {
+      float mx = 0.f;
+#pragma unroll
+      for (int k = 0; k < 16; ++k) {
+        mx = fmaxf(mx, fabsf(v[k]));
+        fin = fin && fabsf(v[k]) <= 3.40282347e38f;
+      }
+      int ex = 0;
+      (void)frexpf(mx, &ex);
+      ex = ex < -96 ? -96 : ex;
+      long long sx = 0;
+#pragma unroll
+      for (int k = 0; k < 16; ++k) {
+        const int X = fin ? (int)rintf(ldexpf(v[k], 30 - ex)) : 0;
+        const int d0 = (int)(int8_t)(X & 0xFF), X1 = (X - d0) >> 8;
+        const int c0 = (int)(int8_t)(X1 & 0xFF), X2 = (X1 - c0) >> 8;
+        const int b0 = (int)(int8_t)(X2 & 0xFF), a0 = (X2 - b0) >> 8;
+        sx += X;
+        const int sh = 8 * (k & 3);
+        pl[0][k >> 2] |= (uint32_t)(a0 & 0xFF) << sh;
+        pl[1][k >> 2] |= (uint32_t)(b0 & 0xFF) << sh;
+        pl[2][k >> 2] |= (uint32_t)(c0 & 0xFF) << sh;
+        pl[3][k >> 2] |= (uint32_t)(d0 & 0xFF) << sh;
+      }
+      const float sc = ldexpf(1.f, ex - 30);
+      info = make_float2(sc, sc * (float)sx);
+    }
+    uint8_t* dst = xdig + (((js >> 6) * UPS + h) * PK_PLANES) * 1024u + 16u * (js & 63u);
+#pragma unroll
+    for (int p = 0; p < PK_PLANES; ++p) *reinterpret_cast<nv_u32x4*>(dst + 1024u * p) = pl[p];
+    xinfo[j] = info;
+    return fin;
+  };
+
+  bool finite = true;
   {
-    const float4* x4 = reinterpret_cast<const float4*>(a.x);
-    const float4* w4 = reinterpret_cast<const float4*>(a.norm_w);
     float ss = 0.f;
     for (uint32_t j = tid; j < nunit; j += NT) {
-      const uint32_t js = j / UPS, h = j % UPS;
-      const uint32_t b = (js >> 6) * 1024u + 16u * (js & 63u);
-      float s = 0.f;
-      if constexpr (IXE) {
-        // x = 2^(E - 22) X with 2^E above the unit's largest |x|, so |X| <=
-        // 2^22, split into balanced base-256 digits X = 65536 a + 256 b + c
-        // (a in [-64, 64]); codes times digits then sum exactly in int32.
-        // E is at least -105 (the scale stays a normal float); a non-finite
-        // element makes the scale NaN, so the rows become NaN.
-        nv_u32x4 pl[3] = {};
-        float2 info = make_float2(0.f, 0.f);
-        if (b < crb) {
-          const uint32_t e = F::unit_elem(b, h);
-          float v[16];
-          float mx = 0.f;
-#pragma unroll
-          for (int k = 0; k < 4; ++k) {
-            const float4 xv = x4[e / 4u + k];
-            v[4 * k] = xv.x; v[4 * k + 1] = xv.y; v[4 * k + 2] = xv.z; v[4 * k + 3] = xv.w;
-            if (NORM) {
-              const float4 wv = w4[e / 4u + k];
-              ss = fmaf(xv.x, xv.x, ss); ss = fmaf(xv.y, xv.y, ss);
-              ss = fmaf(xv.z, xv.z, ss); ss = fmaf(xv.w, xv.w, ss);
-              v[4 * k] *= wv.x; v[4 * k + 1] *= wv.y; v[4 * k + 2] *= wv.z; v[4 * k + 3] *= wv.w;
-            }
-          }
-#pragma unroll
-          for (int k = 0; k < 16; ++k) mx = fmaxf(mx, fabsf(v[k]));
-          bool fin = true;
-#pragma unroll
-          for (int k = 0; k < 16; ++k) fin = fin && fabsf(v[k]) <= 3.40282347e38f;
-          int ex = 0;
-          (void)frexpf(mx, &ex);
-          ex = ex < -105 ? -105 : ex;
-          int sx = 0;
-#pragma unroll
-          for (int k = 0; k < 16; ++k) {
-            const int X = fin ? (int)rintf(ldexpf(v[k], 22 - ex)) : 0;
-            const int c0 = (int)(int8_t)(X & 0xFF), X1 = (X - c0) >> 8;
-            const int b0 = (int)(int8_t)(X1 & 0xFF), a0 = (X1 - b0) >> 8;
-            sx += X;
-            const int sh = 8 * (k & 3);
-            pl[0][k >> 2] |= (uint32_t)(a0 & 0xFF) << sh;
-            pl[1][k >> 2] |= (uint32_t)(b0 & 0xFF) << sh;
-            pl[2][k >> 2] |= (uint32_t)(c0 & 0xFF) << sh;
-          }
-          const float sc = fin ? ldexpf(1.f, ex - 22) : __builtin_nanf("");
-          info = make_float2(sc, sc * (float)sx);
-        }
-        uint8_t* dst = xdig + (((js >> 6) * UPS + h) * 3u) * 1024u + 16u * (js & 63u);
-#pragma unroll
-        for (int p = 0; p < 3; ++p) *reinterpret_cast<nv_u32x4*>(dst + 1024u * p) = pl[p];
-        xinfo[j] = info;
-        continue;
-      }
-      if (b < crb) {
-        const uint32_t e = F::unit_elem(b, h);
-        float4 v[4], w[4];
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          v[k] = x4[e / 4u + k];
-          if (NORM) w[k] = w4[e / 4u + k];
-        }
-        float* dst = xl + (js >> 6) * 64u * EPL + 4u * h * 256u + 4u * (js & 63u);
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          if (NORM) {
-            ss = fmaf(v[k].x, v[k].x, ss); ss = fmaf(v[k].y, v[k].y, ss);
-            ss = fmaf(v[k].z, v[k].z, ss); ss = fmaf(v[k].w, v[k].w, ss);
-            v[k].x *= w[k].x; v[k].y *= w[k].y; v[k].z *= w[k].z; v[k].w *= w[k].w;
-          }
-          *reinterpret_cast<float4*>(dst + 256 * k) = v[k];
-          s += v[k].x; s += v[k].y; s += v[k].z; s += v[k].w;
-        }
-      }
-      xsum_l[j] = s;
+      if constexpr (IXE) finite = stage_digits(j, ss) && finite;
+      else finite = stage_float(j, ss, true) && finite;
     }
     if (NORM) {
       ss = rf_wave_sum(ss);
       if (lane == 0) wsum[wave] = ss;
     }
+    const bool bad = __ballot(!finite) != 0;
+    if (lane == 0) wbad[wave] = bad ? 1u : 0u;
     // EPI_RESIDUAL: the residual of every row this wavefront will finish
     // (at most PK_RES_SLOTS tasks; the launch sizes the grid for that), so
     // the epilogue reads LDS instead of waiting on a load queued behind codes.
@@ -463,6 +571,17 @@ __global__ __launch_bounds__(NT) void matvec_packed(PkArgs a) {
     }
   }
   __syncthreads();
+  // A non-finite x element (every workgroup sees the same x, so all of them
+  // agree): every row sum is then non-finite.  The reference adds the terms
+  // deq * x of a row in order (quant.rs:977-1029): NaN when a term is NaN or
+  // terms of both infinite signs occur, else the one infinity.  That depends
+  // on the terms only, not on their order, so each row's terms are classified
+  // with the reference's own weight decode instead of summed (an overflow of
+  // finite partial sums, which the reference's order could turn into NaN, is
+  // not reproduced).
+  bool bad = false;
+#pragma unroll
+  for (uint32_t i = 0; i < NW; ++i) bad = bad || wbad[i] != 0u;
   float inv = 1.f;
   if (NORM) {
     float tot = 0.f;
@@ -470,13 +589,75 @@ __global__ __launch_bounds__(NT) void matvec_packed(PkArgs a) {
     for (uint32_t i = 0; i < NW; ++i) tot += wsum[i];
     inv = 1.0f / sqrtf(tot / (float)in + a.eps);
   }
+  if (bad) {
+    if constexpr (IXE) {  // the digit layout holds no floats: stage them
+      float unused = 0.f;
+      for (uint32_t j = tid; j < nunit; j += NT) (void)stage_float(j, unused, false);
+      __syncthreads();
+    }
+    for (uint32_t t = blockIdx.x * NW + wave; t < ntask; t += gstride) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const uint32_t v = t * U + u;
+        if (v >= a.rows_total) break;
+        const PkSeg g = seg_of(v);
+        const uint32_t r = v - g.row_begin;
+        PkRsrc rr[F::NREG], rr2[F::NREG];
+#pragma unroll
+        for (int k = 0; k < (int)F::NREG; ++k) {
+          const uint32_t rb = (uint32_t)F::row_bytes(k, in);
+          rr[k] = __builtin_amdgcn_make_buffer_rsrc((void*)(g.reg[k] + (size_t)r * rb), 0, (int32_t)rb, PK_RSRC_WORD3);
+          if constexpr (DUAL)
+            rr2[k] = __builtin_amdgcn_make_buffer_rsrc((void*)(g.reg_up[k] + (size_t)r * rb), 0, (int32_t)rb,
+                                                       PK_RSRC_WORD3);
+        }
+        uint32_t kd = 0, kd2 = 0;
+        for (uint32_t c = 0; c < nchunk; ++c) {
+          const uint32_t b = c * 1024u + 16u * lane;
+          nv_u32x4 q, q2;
+          typename F::Meta m, m2;
+          F::fetch(q, m, rr, b);
+          if constexpr (DUAL) F::fetch(q2, m2, rr2, b);
+          if (b < crb) {
+            const float* xp = xl + c * 64u * EPL + 4u * lane;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const float4 xv = *reinterpret_cast<const float4*>(xp + 256 * i);
+              const float4 xw = UPS == 2 ? *reinterpret_cast<const float4*>(xp + 256 * (i + 4)) : xv;
+              kd |= F::kinds(LC, q[i], m, i, xv, xw);
+              if constexpr (DUAL) kd2 |= F::kinds(LC, q2[i], m2, i, xv, xw);
+            }
+          }
+        }
+        auto value = [&](uint32_t k) {
+          const bool nan = __ballot((k & 1u) != 0) != 0, pinf = __ballot((k & 2u) != 0) != 0,
+                     ninf = __ballot((k & 4u) != 0) != 0;
+          return (nan || (pinf && ninf) || !(pinf || ninf)) ? __builtin_nanf("")
+                                                             : (pinf ? __builtin_inff() : -__builtin_inff());
+        };
+        // with the fused RMSNorm, 1 / rms is 0 (or NaN) here: every row is NaN,
+        // as the reference's x / rms (inf / inf at the infinity) makes it
+        const float y0 = value(kd) * inv, y1 = DUAL ? value(kd2) * inv : 0.f;
+        if (lane == 0) {
+          const uint32_t o = v - g.row_begin;
+          if (EPI == EPI_STORE) g.y[o] = y0;
+          else if (EPI == EPI_RESIDUAL) g.y[o] = g.res[o] + y0;
+          else g.y[o] = y0 / (1.0f + expf(-y0)) * y1;
+        }
+      }
+    }
+    return;
+  }
 
   float acc[U], acc2[U];
 #pragma unroll
   for (int u = 0; u < U; ++u) { acc[u] = 0.f; acc2[u] = 0.f; }
   uint32_t done = 0;  // tasks this wavefront has finished
 
-  auto consume = [&](const Step& B, uint32_t tt, uint32_t ss) {
+  // One step: decode LPW chunks of U rows against x (digit planes when
+  // MODE::value, else floats), then finish the rows when the task ends.
+  auto consume = [&](auto mode, const Step& B, uint32_t tt, uint32_t ss) {
+    constexpr bool DIG = IXE && decltype(mode)::value;
 #pragma unroll
     for (int l = 0; l < LPW; ++l) {
       // Lanes past the end of the row (a partial last chunk, or a chunk past
@@ -484,55 +665,58 @@ __global__ __launch_bounds__(NT) void matvec_packed(PkArgs a) {
       // in-bounds slice of x and keep their sums by a select.
       const uint32_t c = ss * LPW + l, cx = c < nchunk ? c : nchunk - 1u;
       const bool valid = c * 1024u + 16u * lane < crb;
-      if constexpr (IXE) {
-        nv_u32x4 P[3 * UPS];
+      if constexpr (DIG) {
+        if constexpr (IXE) {  // only formats with idot / ifinish
+        nv_u32x4 P[PK_PLANES * UPS];
         float2 ui[UPS];
 #pragma unroll
         for (uint32_t h = 0; h < UPS; ++h) {
 #pragma unroll
-          for (uint32_t p = 0; p < 3; ++p)
-            P[3 * h + p] = *reinterpret_cast<const nv_u32x4*>(xdig + ((cx * UPS + h) * 3u + p) * 1024u + 16u * lane);
+          for (uint32_t p = 0; p < (uint32_t)PK_PLANES; ++p)
+            P[PK_PLANES * h + p] =
+                *reinterpret_cast<const nv_u32x4*>(xdig + ((cx * UPS + h) * PK_PLANES + p) * 1024u + 16u * lane);
           ui[h] = xinfo[(cx * 64u + lane) * UPS + h];
         }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-          int S[UPS][3] = {};
+          int S[UPS][PK_PLANES] = {};
           F::idot(LC, B.q[u][l], P, S);
           const float f = F::ifinish(LC, B.m[u][l], S, ui);
           acc[u] = valid ? acc[u] + f : acc[u];
           if constexpr (DUAL) {
-            int S2[UPS][3] = {};
+            int S2[UPS][PK_PLANES] = {};
             F::idot(LC, B.q2[u][l], P, S2);
             const float f2 = F::ifinish(LC, B.m2[u][l], S2, ui);
             acc2[u] = valid ? acc2[u] + f2 : acc2[u];
           }
         }
-        continue;
-      }
-      const float* xp = xl + cx * 64u * EPL + 4u * lane;
-      float s0[U], s1[U], t0[U], t1[U];
+        }
+      } else {
+        const float* xp = xl + cx * 64u * EPL + 4u * lane;
+        float s0[U], s1[U], t0[U], t1[U];
 #pragma unroll
-      for (int u = 0; u < U; ++u) { s0[u] = 0.f; s1[u] = 0.f; t0[u] = 0.f; t1[u] = 0.f; }
+        for (int u = 0; u < U; ++u) { s0[u] = 0.f; s1[u] = 0.f; t0[u] = 0.f; t1[u] = 0.f; }
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float4 xv = *reinterpret_cast<const float4*>(xp + 256 * i);
-        float4 xw = xv;
-        if (UPS == 2) xw = *reinterpret_cast<const float4*>(xp + 256 * (i + 4));
+        for (int i = 0; i < 4; ++i) {
+          const float4 xv = *reinterpret_cast<const float4*>(xp + 256 * i);
+          float4 xw = xv;
+          if (UPS == 2) xw = *reinterpret_cast<const float4*>(xp + 256 * (i + 4));
+#pragma unroll
+          for (int u = 0; u < U; ++u) {
+            F::word(LC, B.q[u][l][i], B.m[u][l], i, xv, xw, s0[u], s1[u]);
+            if constexpr (DUAL) F::word(LC, B.q2[u][l][i], B.m2[u][l], i, xv, xw, t0[u], t1[u]);
+          }
+        }
+        const uint32_t ui = (cx * 64u + lane) * UPS;
+        const float xs0 = xsum_l[ui], xs1 = UPS == 2 ? xsum_l[ui + 1u] : 0.f;
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-          F::word(LC, B.q[u][l][i], B.m[u][l], i, xv, xw, s0[u], s1[u]);
-          if constexpr (DUAL) F::word(LC, B.q2[u][l][i], B.m2[u][l], i, xv, xw, t0[u], t1[u]);
-        }
-      }
-      const uint32_t ui = (cx * 64u + lane) * UPS;
-      const float xs0 = xsum_l[ui], xs1 = UPS == 2 ? xsum_l[ui + 1u] : 0.f;
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const float f = F::finish(LC, B.m[u][l], s0[u], s1[u], xs0, xs1);
-        acc[u] = valid ? acc[u] + f : acc[u];
-        if constexpr (DUAL) {
-          const float f2 = F::finish(LC, B.m2[u][l], t0[u], t1[u], xs0, xs1);
-          acc2[u] = valid ? acc2[u] + f2 : acc2[u];
+          const float f = F::finish(LC, B.m[u][l], s0[u], s1[u], xs0, xs1);
+          acc[u] = valid ? acc[u] + f : acc[u];
+          if constexpr (DUAL) {
+            const float f2 = F::finish(LC, B.m2[u][l], t0[u], t1[u], xs0, xs1);
+            acc2[u] = valid ? acc2[u] + f2 : acc2[u];
+          }
         }
       }
     }
@@ -564,16 +748,19 @@ __global__ __launch_bounds__(NT) void matvec_packed(PkArgs a) {
   // the buffer freed by the previous step.  The only exit is the uniform
   // check at the top of each step, so every buffer is consumed (its loads
   // waited for) before it is refilled.
-  for (;;) {
+  auto run = [&](auto mode) {
+    for (;;) {
 #pragma unroll
-    for (int b = 0; b < NB; ++b) {
-      if (ct >= ntask) return;
-      fetch(buf[(b + NB - 1) % NB], ft, fs);
-      advance(ft, fs);
-      consume(buf[b], ct, cs);
-      advance(ct, cs);
+      for (int b = 0; b < NB; ++b) {
+        if (ct >= ntask) return;
+        fetch(buf[(b + NB - 1) % NB], ft, fs);
+        advance(ft, fs);
+        consume(mode, buf[b], ct, cs);
+        advance(ct, cs);
+      }
     }
-  }
+  };
+  run(std::integral_constant<bool, IXE>());
 }
 
 // GGUF blocks -> packed layout, one thread per block (install-time only).
@@ -690,41 +877,66 @@ static int pk_occupancy(PkOccCache& c, const void* kern, int nt, uint32_t lds) {
   return occ;
 }
 
-template <uint32_t T, int EPI, bool NORM, int LPW, int NB, int NT>
-static hipError_t launch_pk(const PkArgs& a, uint32_t lds, hipStream_t st) {
-  constexpr int U = 1;
-  static PkOccCache cache;
-  auto kern = matvec_packed<T, EPI, NORM, U, LPW, NB, NT, false>;
-  const int occ = pk_occupancy(cache, reinterpret_cast<const void*>(kern), NT, lds);
-  if (occ < 1) return hipErrorInvalidConfiguration;
-  // Grid: a whole number k of workgroups per CU (a CU with one workgroup more
-  // than its neighbours sets the launch time), k just large enough for about
-  // four rows per wavefront, at most the occupancy.  Timed on the 8B and 70B
-  // shapes against the fullest grid (CUs x occupancy): Q/K/V 6144x4096 8.3 vs
-  // 9.3 us (Q8_0), 6.3 vs 7.1 us (Q4_0); Q4_0 gate/up 15.8 vs 16.8 us; the
-  // other shapes within 0.2 us.
-  const uint64_t tasks = (a.rows_total + U - 1) / U, nw = NT / 64, cus = (uint64_t)pk_cu_count();
+// x as digit planes on the launches where they pay (1, default), on every
+// Q8_0 / Q4_0 launch whose LDS holds them (2), or float x everywhere (0):
+// rf_tune_matvec_digits.
+static int g_digits = 1;
+void set_matvec_digits(int mode) { g_digits = mode; }
+int matvec_digits() { return g_digits; }
+
+// LDS of the digit-plane variant: PK_PLANES bytes per element and a float2
+// per 16-element unit, which also holds the float layout it falls back to.
+static uint64_t pk_digit_lds(uint32_t t, uint64_t in_dim) {
+  const uint64_t nchunk = pk_nchunk(t, in_dim), ups = pk_epb(t);
+  return nchunk * ups * (1024u * PK_PLANES) + nchunk * 64u * ups * 8u;
+}
+
+// Grid: a whole number k of workgroups per CU (a CU with one workgroup more
+// than its neighbours sets the launch time), k just large enough for about
+// four rows per wavefront, at most the occupancy.  Timed on the 8B and 70B
+// shapes against the fullest grid (CUs x occupancy): Q/K/V 6144x4096 8.3 vs
+// 9.3 us (Q8_0), 6.3 vs 7.1 us (Q4_0); Q4_0 gate/up 15.8 vs 16.8 us; the
+// other shapes within 0.2 us.
+static uint64_t pk_grid(uint64_t tasks, uint64_t nw, int occ, int epi) {
+  const uint64_t cus = (uint64_t)pk_cu_count();
   const uint64_t want = (tasks + nw - 1) / nw;
   uint64_t k = (tasks + cus * nw * 4 - 1) / (cus * nw * 4);
   if (k < 1) k = 1;
   if (k > (uint64_t)occ) k = (uint64_t)occ;
   uint64_t grid = cus * k < want ? cus * k : want;
-  if (EPI == EPI_RESIDUAL) {  // at most PK_RES_SLOTS tasks per wavefront (residuals staged in LDS)
+  if (epi == EPI_RESIDUAL) {  // at most PK_RES_SLOTS tasks per wavefront (residuals staged in LDS)
     const uint64_t need = (tasks + nw * PK_RES_SLOTS - 1) / (nw * PK_RES_SLOTS);
     if (grid < need) grid = need;
   }
+  return grid;
+}
+
+template <uint32_t T, int EPI, bool NORM, int LPW, int NB, int NT>
+static hipError_t launch_pk(const PkArgs& a, uint32_t lds, hipStream_t st) {
+  constexpr int U = 1;
+  static PkOccCache cache, cache_ix;  // one per kernel variant
+  auto kern = matvec_packed<T, EPI, NORM, U, LPW, NB, NT, false>;
+  const int occ = pk_occupancy(cache, reinterpret_cast<const void*>(kern), NT, lds);
+  if (occ < 1) return hipErrorInvalidConfiguration;
+  const uint64_t tasks = (a.rows_total + U - 1) / U, nw = NT / 64;
+  uint64_t grid = pk_grid(tasks, nw, occ, EPI);
   // Q8_0 / Q4_0 take the int8 digit planes of x when a wavefront's rows hold
   // at least 24 KiB of codes: their split costs each workgroup a longer
   // prologue, which the cheaper decode repays only over that many bytes
   // (timed: gate/up 14336x4096 x2 21.7-21.9 vs 22.7-22.9 us, the 70B-shape
   // 28672x8192 42.0 vs 43.5 us, the 8B output rows -3%; Q/K/V, o-proj and a
-  // single 14336x4096 Q4_0 matrix 0.15-1.5 us slower with them).
+  // single 14336x4096 Q4_0 matrix 0.15-1.5 us slower with them).  The digit
+  // variant has its own LDS size, occupancy and grid.
   if constexpr (PkFmt<T>::INTX) {
     const uint64_t rows_pw = (tasks * U + grid * nw - 1) / (grid * nw);
     const uint64_t code_bytes = rows_pw * a.in_dim / PkFmt<T>::EPB * (EPI == EPI_SWIGLU ? 2 : 1);
-    if (code_bytes >= 24576) {
-      hipLaunchKernelGGL((matvec_packed<T, EPI, NORM, U, LPW, NB, NT, true>), dim3((uint32_t)grid), dim3(NT), lds, st,
-                         a);
+    const uint64_t lds_ix = pk_digit_lds(T, a.in_dim);
+    const bool want = g_digits == 2 || (g_digits == 1 && code_bytes >= 24576);
+    if (want && lds_ix + PK_STATIC_LDS <= pk_lds_limit()) {
+      auto kix = matvec_packed<T, EPI, NORM, U, LPW, NB, NT, true>;
+      const int occ_ix = pk_occupancy(cache_ix, reinterpret_cast<const void*>(kix), NT, (uint32_t)lds_ix);
+      if (occ_ix < 1) return hipErrorInvalidConfiguration;
+      hipLaunchKernelGGL(kix, dim3((uint32_t)pk_grid(tasks, nw, occ_ix, EPI)), dim3(NT), (uint32_t)lds_ix, st, a);
       return hipGetLastError();
     }
   }

@@ -53,6 +53,11 @@ struct rf_ctx {
   std::mutex mu;
   std::map<std::string, void*> buffers;  // charge name -> device pointer
   rf::Workspace attn_ws, scratch_ws, mm_ws;
+  // Incremented whenever a workspace buffer is replaced: graphs captured
+  // before hold the old address and are refused by rf_graph_replay.
+  uint64_t ws_generation = 0;
+  // rf_ctx_reserve(..., fixed = 1): workspaces never grow after reservation.
+  bool ws_fixed = false;
   float* amax_val = nullptr;
   uint32_t* amax_idx = nullptr;
   std::mutex stage_mu;  // guards the staging buffers below (one upload at a time)
@@ -63,8 +68,10 @@ struct rf_ctx {
 
 namespace rf {
 // Grow a context-owned workspace (charged as `charge`); synchronises the
-// device before releasing a smaller previous buffer.
-int32_t ensure_workspace(rf_ctx* ctx, Workspace& ws, const char* charge, uint64_t bytes);
+// device before releasing a smaller previous buffer.  Refused (RF_ERR_INVALID)
+// when the workspaces are fixed by rf_ctx_reserve or while `st` is being
+// captured into a graph.
+int32_t ensure_workspace(rf_ctx* ctx, Workspace& ws, const char* charge, uint64_t bytes, hipStream_t st);
 // Allocate / free a ledger-charged device buffer.
 int32_t vram_alloc(rf_ctx* ctx, const std::string& charge, uint64_t bytes, void** out);
 int32_t vram_release(rf_ctx* ctx, const std::string& charge);

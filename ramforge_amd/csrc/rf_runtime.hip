@@ -155,8 +155,17 @@ bool vram_can_allocate(rf_ctx* ctx, uint64_t bytes) {
   return ctx->ledger.used() + bytes >= ctx->ledger.used() && ctx->ledger.used() + bytes <= ctx->ledger.total();
 }
 
-int32_t ensure_workspace(rf_ctx* ctx, Workspace& ws, const char* charge, uint64_t bytes) {
+int32_t ensure_workspace(rf_ctx* ctx, Workspace& ws, const char* charge, uint64_t bytes, hipStream_t st) {
   if (ws.bytes >= bytes) return RF_OK;
+  if (ctx->ws_fixed)
+    return set_error(RF_ERR_INVALID, "%s needs %llu bytes but %llu are reserved and the workspaces are fixed", charge,
+                     (unsigned long long)bytes, (unsigned long long)ws.bytes);
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (st && hipStreamIsCapturing(st, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
+    return set_error(RF_ERR_INVALID,
+                     "%s needs %llu bytes during graph capture; reserve it first (rf_ctx_reserve) or run the call "
+                     "once before capturing",
+                     charge, (unsigned long long)bytes);
   uint64_t want = bytes < 65536 ? 65536 : bytes;
   if (ws.ptr) {
     hipError_t e = hipDeviceSynchronize();  // the old buffer may still be read by queued kernels
@@ -164,6 +173,7 @@ int32_t ensure_workspace(rf_ctx* ctx, Workspace& ws, const char* charge, uint64_
     int32_t rc = vram_release(ctx, charge);
     ws.ptr = nullptr;
     ws.bytes = 0;
+    ++ctx->ws_generation;  // graphs holding the old address are stale from here on
     if (rc) return rc;
   }
   void* p = nullptr;
@@ -313,6 +323,18 @@ void rf_ctx_destroy(rf_ctx* ctx) {
   if (ctx->compute) hipStreamDestroy(ctx->compute);
   if (ctx->copy) hipStreamDestroy(ctx->copy);
   delete ctx;
+}
+
+int32_t rf_ctx_reserve(rf_ctx* ctx, uint64_t attention_bytes, uint64_t matmul_bytes, uint64_t staging_bytes,
+                       int32_t fixed) {
+  RF_CHECK_CTX(ctx);
+  ctx->ws_fixed = false;  // growing is what reserving does
+  int32_t rc = RF_OK;
+  if (attention_bytes) rc = ensure_workspace(ctx, ctx->attn_ws, "workspace:attention", attention_bytes, ctx->compute);
+  if (!rc && matmul_bytes) rc = ensure_workspace(ctx, ctx->mm_ws, "workspace:matmul", matmul_bytes, ctx->compute);
+  if (!rc && staging_bytes) rc = ensure_workspace(ctx, ctx->scratch_ws, "workspace:scratch", staging_bytes, ctx->compute);
+  if (!rc) ctx->ws_fixed = fixed != 0;
+  return rc;
 }
 
 int32_t rf_ctx_synchronize(rf_ctx* ctx) {
@@ -597,7 +619,7 @@ int32_t rf_matvec_packed(rf_ctx* ctx, uint32_t t, const void* packed, uint64_t p
   const float* xa = x;
   if ((reinterpret_cast<uintptr_t>(x) & 15u) != 0) {
     // the kernel reads x with 16-byte loads: stage a misaligned x in the context scratch
-    rc = ensure_workspace(ctx, ctx->scratch_ws, "workspace:scratch", in_dim * 4);
+    rc = ensure_workspace(ctx, ctx->scratch_ws, "workspace:scratch", in_dim * 4, st);
     if (rc) return rc;
     RF_HIP(hipMemcpyAsync(ctx->scratch_ws.ptr, x, in_dim * 4, hipMemcpyDeviceToDevice, st), "hipMemcpyAsync");
     xa = static_cast<const float*>(ctx->scratch_ws.ptr);
@@ -606,6 +628,15 @@ int32_t rf_matvec_packed(rf_ctx* ctx, uint32_t t, const void* packed, uint64_t p
   hipError_t e = launch_matvec_packed(t, &seg, 1, xa, nullptr, 0.f, in_dim, EPI_STORE, st);
   if (e != hipSuccess) return hip_error(e, "packed matvec launch");
   return RF_OK;
+}
+
+uint64_t rf_matmul_workspace_bytes(uint64_t out_dim, uint64_t in_dim, uint64_t n_tokens) {
+  if (out_dim == 0 || in_dim == 0 || n_tokens == 0) return 0;
+  const uint64_t chunk = n_tokens < MM_MAX_TOKENS ? n_tokens : MM_MAX_TOKENS;
+  // the launches are chunk tokens each, the last one the remainder
+  uint64_t part = mm_part_floats_at(&out_dim, 1, in_dim, chunk);
+  if (n_tokens % chunk) part = std::max(part, mm_part_floats_at(&out_dim, 1, in_dim, n_tokens % chunk));
+  return part * 4;
 }
 
 int32_t rf_matmul_packed(rf_ctx* ctx, uint32_t t, const void* packed, uint64_t packed_bytes, uint64_t out_dim,
@@ -635,14 +666,12 @@ int32_t rf_matmul_packed(rf_ctx* ctx, uint32_t t, const void* packed, uint64_t p
                      (unsigned long long)out_dim, (unsigned long long)in_dim);
   hipStream_t st = pick_stream(ctx, s);
   const uint64_t chunk = n_tokens < MM_MAX_TOKENS ? n_tokens : MM_MAX_TOKENS;
-  // the launches are chunk tokens each, the last one the remainder
-  uint64_t part = mm_part_floats_at(&out_dim, 1, in_dim, chunk);
-  if (n_tokens % chunk) part = std::max(part, mm_part_floats_at(&out_dim, 1, in_dim, n_tokens % chunk));
-  int32_t rc = ensure_workspace(ctx, ctx->mm_ws, "workspace:matmul", part * 4);
+  int32_t rc = ensure_workspace(ctx, ctx->mm_ws, "workspace:matmul", rf_matmul_workspace_bytes(out_dim, in_dim, n_tokens),
+                                st);
   if (rc) return rc;
   const bool aligned = (reinterpret_cast<uintptr_t>(x) & 15u) == 0 && in_dim % 4 == 0;
   if (!aligned) {  // the kernel stages x with 16-byte loads
-    rc = ensure_workspace(ctx, ctx->scratch_ws, "workspace:scratch", chunk * in_dim * 4);
+    rc = ensure_workspace(ctx, ctx->scratch_ws, "workspace:scratch", chunk * in_dim * 4, st);
     if (rc) return rc;
   }
   for (uint64_t off = 0; off < n_tokens; off += MM_MAX_TOKENS) {
@@ -688,10 +717,14 @@ int32_t rf_dequantize_rows(rf_ctx* ctx, uint32_t t, const void* w, uint64_t w_by
 }
 
 // --------------------------------------------------------------- attention
-int32_t rf_attention_decode(rf_ctx* ctx, const float* q, const float* kh, const float* vh, const float* kc,
-                            const float* vc, uint32_t hist, uint32_t qh, uint32_t kvh, uint32_t hd, float* out,
-                            rf_stream_t s) {
-  RF_CHECK_CTX(ctx);
+namespace {
+
+// Validated launch arguments of one single-query attention call and the
+// workspace bytes its kernels need (the split kernel's chunk records, or the
+// any-shape kernel's score rows).
+int32_t attention_setup(const float* q, const float* kh, const float* vh, const float* kc, const float* vc,
+                        uint32_t hist, uint32_t qh, uint32_t kvh, uint32_t hd, float* out, AttnArgs* a, bool* fast,
+                        uint64_t* ws_bytes) {
   if (qh == 0 || kvh == 0 || hd == 0)
     return set_error(RF_ERR_INVALID, "attention requires non-zero query heads, KV heads, and head dimension");
   if (qh % kvh != 0)
@@ -700,28 +733,60 @@ int32_t rf_attention_decode(rf_ctx* ctx, const float* q, const float* kh, const 
     return set_error(RF_ERR_INVALID, "attention tensor shape mismatch");
   if (hist == UINT32_MAX) return set_error(RF_ERR_UNSUPPORTED, "attention over more than 2^32 - 1 positions");
   const uint32_t total = hist + 1;
-  AttnArgs a{};
-  a.q = q; a.k_hist = kh; a.v_hist = vh; a.k_cur = kc; a.v_cur = vc; a.out = out;
-  a.hist = hist; a.qh = qh; a.kvh = kvh; a.hd = hd;
-  a.denom = sqrtf((float)hd);
+  *a = AttnArgs{};
+  a->q = q; a->k_hist = kh; a->v_hist = vh; a->k_cur = kc; a->v_cur = vc; a->out = out;
+  a->hist = hist; a->qh = qh; a->kvh = kvh; a->hd = hd;
+  a->denom = sqrtf((float)hd);
   auto aligned = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
-  const bool fast = attention_supported(qh, kvh, hd, total) && aligned(q) && (hist == 0 || (aligned(kh) && aligned(vh))) &&
-                    aligned(kc) && aligned(vc);
-  uint64_t ws_bytes;
-  if (fast) {  // the context is known here: its own regime, sized to itself
+  *fast = attention_supported(qh, kvh, hd, total) && aligned(q) && (hist == 0 || (aligned(kh) && aligned(vh))) &&
+          aligned(kc) && aligned(vc);
+  if (*fast) {  // the context is known here: its own regime, sized to itself
     const AttnShape sh = attention_regime_shape(attention_regime(total, qh, kvh, total), qh, kvh, total);
-    a.per_q = sh.per_q; a.nsplit = sh.nsplit; a.waves = sh.waves;
-    ws_bytes = attention_ws_floats(a.nsplit, qh, hd) * 4;
+    a->per_q = sh.per_q; a->nsplit = sh.nsplit; a->waves = sh.waves;
+    *ws_bytes = attention_ws_floats(a->nsplit, qh, hd) * 4;
   } else {
-    a.nsplit = 1;
-    ws_bytes = (uint64_t)qh * total * 4;
+    a->nsplit = 1;
+    *ws_bytes = (uint64_t)qh * total * 4;
   }
-  int32_t rc = ensure_workspace(ctx, ctx->attn_ws, "workspace:attention", ws_bytes);
-  if (rc) return rc;
-  a.ws = static_cast<float*>(ctx->attn_ws.ptr);
-  const hipError_t e = fast ? launch_attention(a, pick_stream(ctx, s)) : launch_attention_naive(a, pick_stream(ctx, s));
+  return RF_OK;
+}
+
+int32_t attention_launch(const AttnArgs& a, bool fast, hipStream_t st) {
+  const hipError_t e = fast ? launch_attention(a, st) : launch_attention_naive(a, st);
   if (e != hipSuccess) return hip_error(e, "attention launch");
   return RF_OK;
+}
+
+}  // namespace
+
+int32_t rf_attention_decode(rf_ctx* ctx, const float* q, const float* kh, const float* vh, const float* kc,
+                            const float* vc, uint32_t hist, uint32_t qh, uint32_t kvh, uint32_t hd, float* out,
+                            rf_stream_t s) {
+  RF_CHECK_CTX(ctx);
+  AttnArgs a;
+  bool fast = false;
+  uint64_t ws_bytes = 0;
+  int32_t rc = attention_setup(q, kh, vh, kc, vc, hist, qh, kvh, hd, out, &a, &fast, &ws_bytes);
+  if (rc) return rc;
+  hipStream_t st = pick_stream(ctx, s);
+  rc = ensure_workspace(ctx, ctx->attn_ws, "workspace:attention", ws_bytes, st);
+  if (rc) return rc;
+  a.ws = static_cast<float*>(ctx->attn_ws.ptr);
+  return attention_launch(a, fast, st);
+}
+
+uint64_t rf_attention_workspace_bytes(uint64_t max_positions, uint32_t qh, uint32_t kvh, uint32_t hd) {
+  if (max_positions == 0 || qh == 0 || kvh == 0 || hd == 0 || max_positions > 0xFFFFFFFFull) return 0;
+  // The split kernel's record count grows with the context: 8 chunks per
+  // query head at most below 1024 positions, then the per-KV-head split
+  // count, which never decreases with the context.
+  const uint32_t total = (uint32_t)max_positions;
+  uint32_t nsplit = 1;
+  for (int r = 0; r < ATT_REGIMES; ++r)
+    nsplit = std::max(nsplit, attention_regime_shape(r, qh, kvh, total).nsplit);
+  const uint64_t split = attention_ws_floats(nsplit, qh, hd) * 4;
+  const uint64_t naive = (uint64_t)qh * max_positions * 4;
+  return std::max(split, naive);
 }
 
 // --------------------------------------------------------------- elementwise
@@ -820,6 +885,7 @@ int32_t rf_synth_blocks(rf_ctx* ctx, uint32_t t, uint64_t seed, uint64_t first, 
 struct rf_graph_h {
   hipGraph_t g = nullptr;
   hipGraphExec_t x = nullptr;
+  uint64_t ws_generation = 0;  // the context's workspace generation at capture
 };
 
 int32_t rf_capture_begin(rf_ctx* ctx) {
@@ -842,6 +908,7 @@ int32_t rf_capture_end(rf_ctx* ctx, void** graph) {
   rf_graph_h* h = new rf_graph_h;
   h->g = g;
   h->x = x;
+  h->ws_generation = ctx->ws_generation;
   *graph = h;
   return RF_OK;
 }
@@ -850,6 +917,10 @@ int32_t rf_graph_replay(rf_ctx* ctx, void* graph, uint32_t reps, float* ms_per_r
   RF_CHECK_CTX(ctx);
   if (!graph || reps == 0) return set_error(RF_ERR_INVALID, "null graph or zero repetitions");
   rf_graph_h* h = static_cast<rf_graph_h*>(graph);
+  if (h->ws_generation != ctx->ws_generation)
+    return set_error(RF_ERR_INVALID,
+                     "graph captured before a context workspace was reallocated (it holds the freed buffer); "
+                     "capture it again");
   hipEvent_t a = nullptr, b = nullptr;
   RF_HIP(hipEventCreate(&a), "hipEventCreate");
   hipError_t e = hipEventCreate(&b);
@@ -885,6 +956,11 @@ uint32_t rf_tune_matvec_tile_bytes(uint32_t bytes) {
 int32_t rf_tune_matvec_kernel(int32_t mode) {
   if (mode == 0 || mode == 1) set_matvec_stream(mode == 1);
   return matvec_stream() ? 1 : 0;
+}
+
+int32_t rf_tune_matvec_digits(int32_t mode) {
+  if (mode >= 0 && mode <= 2) set_matvec_digits(mode);
+  return matvec_digits();
 }
 
 }  // extern "C"

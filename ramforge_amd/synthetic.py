@@ -15,11 +15,14 @@ from dataclasses import dataclass
 # ggml type ids (core/src/types.rs:238-292)
 F32, Q4_0, Q8_0, Q4_K, Q6_K = 0, 2, 8, 12, 14
 
-# Per-format scale multipliers that give weights of roughly N(0, 0.02)
-# magnitude: Q8_0 d = |N(0,0.02)|/127; Q4_0 d = |N(0,0.02)|/8;
-# K-quants scale sub-block factors of up to 63 * 15 or 63 * 32.
-SCALE_MUL = {Q8_0: 0.02 / 127.0, Q4_0: 0.02 / 8.0, Q4_K: 0.02 / (63.0 * 15.0), Q6_K: 0.02 / (127.0 * 32.0),
-             F32: 0.02}
+# Per-format scale multipliers: Q8_0 d = |N(0,0.02)|/127,
+# which gives decoded weights of standard deviation 0.0117; the others are
+# set so that their decoded weights have that same spread (measured through
+# the reference's decode, whose f16 subnormal rule halves most of the small
+# K-quant scales).  With weights several times smaller, a random model's
+# layers barely move the residual stream and greedy decoding repeats one
+# token.
+SCALE_MUL = {Q8_0: 0.02 / 127.0, Q4_0: 0.02 / 8.0, Q4_K: 5.07e-5, Q6_K: 1.71e-5, F32: 0.02}
 
 # BASELINE.json configurations
 CONFIG_4 = dict(vocab_size=32000, context_length=4096, embedding_length=2048, block_count=16,

@@ -119,3 +119,39 @@ def pack_host(t: int, raw: np.ndarray, rows: int, in_dim: int) -> np.ndarray:
     qk, bs = GEOM[t]
     blocks = raw.reshape(rows * in_dim // qk, bs)
     return np.concatenate([blocks[:, a:b].reshape(-1) for a, b in PACK_REGIONS[t]])
+
+
+def zero_code_patch(t: int, raw: np.ndarray, elems) -> np.ndarray:
+    """Sets the codes of block elements `elems` (indices within a block) to
+    the format's zero weight in every block of a GGUF payload (block layouts
+    of quant.rs as the oracle decodes them)."""
+    qk, bs = GEOM[t]
+    b = raw.reshape(-1, bs)
+    for e in elems:
+        if t == Q8_0:
+            b[:, 2 + e] = 0
+        elif t == Q8_K:
+            b[:, 4 + e] = 0
+        elif t in (Q4_0, Q5_0):
+            base = 2 if t == Q4_0 else 6
+            j, hi = e % 16, e >= 16
+            col = b[:, base + j]
+            nib0 = 8 if t == Q4_0 else 0
+            b[:, base + j] = (col & 0x0F) | (nib0 << 4) if hi else (col & 0xF0) | nib0
+            if t == Q5_0:  # high bit of element e: bit e of qh (value 16 - 16 = 0)
+                qh = b[:, 2:6].copy().view(np.uint32).reshape(-1)
+                qh |= np.uint32(1 << e)
+                b[:, 2:6] = qh.view(np.uint8).reshape(-1, 4)
+        elif t == Q6_K:  # element 128 hf + 32 k + l: low nibble 0, high bits 2 (q = 32)
+            hf, k, l = e // 128, (e % 128) // 32, e % 32
+            ql = 64 * hf + 32 * (k & 1) + l
+            b[:, ql] = (b[:, ql] & 0x0F) if (k >> 1) else (b[:, ql] & 0xF0)
+            qh = 128 + 32 * hf + l
+            b[:, qh] = (b[:, qh] & ~np.uint8(3 << (2 * k))) | np.uint8(2 << (2 * k))
+        elif t == Q3_K:  # element 128 n + 32 j + l: low bits 0, hmask bit set (q = 4 - 4)
+            n, j, l = e // 128, (e % 128) // 32, e % 32
+            b[:, 32 + 32 * n + l] &= ~np.uint8(3 << (2 * j))
+            b[:, l] |= np.uint8(1 << (4 * n + j))
+        else:
+            raise ValueError(f"no zero code for type {t}")
+    return raw

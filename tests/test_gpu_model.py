@@ -106,6 +106,38 @@ def test_tiny_model_forward_and_generate(ctx, orc, kind, bias, layout_mode):
     _rf().tune_matvec_kernel(1)
 
 
+@pytest.mark.parametrize("digits", [2, 0], ids=["digit-planes", "float-x"])
+@pytest.mark.parametrize("kind", ["q8", "q4"])
+def test_tiny_model_digit_modes(ctx, orc, kind, digits):
+    """The whole forward and greedy loop with every packed Q8_0 / Q4_0 launch
+    taking x as digit planes (mode 2), and with float x everywhere (mode 0)."""
+    rf = _rf()
+    cfg = dict(TINY)
+    types = {"q8": ALL_Q8, "q4": ALL_Q4}[kind]
+    T = _tiny_tensors(np.random.default_rng(930 + digits), cfg, types, bias=True)
+    old = rf.tune_matvec_digits(-1)
+    rf.tune_matvec_digits(digits)
+    print(f"  tiny model {kind}, digits mode {digits}", flush=True)
+    try:
+        gm = _load_gpu(ctx, cfg, T, 48)
+        om = orc.Model(cfg, T, kv_capacity=48, threads=4)
+        for pos, tok in enumerate([5, 17, 90, 3]):
+            h = gm.forward(tok, pos, want_hidden=True)
+            hr = om.forward(tok, pos)
+            assert np.max(np.abs(h - hr)) <= 2e-4 * max(1.0, np.abs(hr).max()), (kind, pos)
+            lr = om.logits(hr)
+            assert np.max(np.abs(gm.logits() - lr)) <= 2e-4 * max(1.0, np.abs(lr).max()), (kind, pos)
+        gm.reset()
+        om.reset()
+        toks = gm.generate([1, 2, 3, 4], 20)
+        ref, margin = om.generate([1, 2, 3, 4], 20)
+        assert toks == ref, f"greedy divergence (min top-2 margin {margin.min():.3g})"
+        gm.close()
+        om.close()
+    finally:
+        rf.tune_matvec_digits(old)
+
+
 # Q6_K gate/up over an 8448-wide hidden state: x fills 43.5 KB of LDS, the
 # size at which the packed matvec would use 1024-thread workgroups; the Q6_K
 # gate/up kernel stays at 512 (its 1024-thread form spilled to scratch).

@@ -354,3 +354,28 @@ def test_q8_k_and_q8_0_sign(orc):
     assert np.array_equal(orc.dequantize_row(Q8_K, blk, 256), (np.arange(256) - 128).astype(np.float32) * 0.25)
     blk = q8_0_block(0x4000, list(range(-16, 16)))
     assert np.array_equal(orc.dequantize_row(Q8_0, blk, 32), np.arange(-16, 16, dtype=np.float32) * 2.0)
+
+
+def test_zero_code_patch_decodes_to_zero(orc):
+    """The GPU tests' zero-code patch (tests/helpers.py) against the oracle's
+    decode: patched elements are exact zeros in every row and block."""
+    from helpers import GEOM, NAMES, Q3_K, Q4_0, Q5_0, Q6_K, Q8_0, Q8_K, random_matrix, zero_code_patch
+
+    rng = np.random.default_rng(1)
+    for t in (Q8_0, Q4_0, Q5_0, Q8_K, Q6_K, Q3_K):
+        qk, _ = GEOM[t]
+        elems = [5, 21] if qk == 32 else list(range(5, 256, 16))
+        raw = zero_code_patch(t, random_matrix(t, 4, 2 * qk, rng), elems)
+        deq = orc.dequantize_rows(t, raw, 2 * qk, 4)
+        for blk in range(2):
+            assert (deq[:, [blk * qk + e for e in elems]] == 0).all(), NAMES[t]
+
+
+def test_synthetic_k_quant_weights_are_zero_mean(orc):
+    """The generator draws K-quant mins at the mean code times the scale, so
+    d*sc*q - dmin*m has mean near zero (a biased random model repeats one
+    token forever)."""
+    for t, mul in ((12, 0.02 / (63 * 15)), (13, 0.02 / (63 * 31)), (10, 0.02 / (15 * 3))):
+        raw = orc.synth_blocks(t, 77, 0, 4096, mul)
+        w = orc.dequantize_rows(t, raw, 256, 4096).astype(np.float64)
+        assert abs(w.mean()) < 0.05 * w.std(), (t, w.mean(), w.std())
