@@ -225,6 +225,21 @@ int32_t rf_attention_decode(rf_ctx *ctx, const float *q, const float *k_hist, co
                             const float *k_cur, const float *v_cur, uint32_t hist_len, uint32_t q_heads,
                             uint32_t kv_heads, uint32_t head_dim, float *out, rf_stream_t stream);
 
+/* rf_attention_decode for callers that cannot allocate device memory (code
+ * under graph capture, serving loops, harnesses that forbid hipMalloc).  No
+ * counterpart in the reference.  Same arguments, validation and results; the
+ * split records (or score rows) live in a static device array of
+ * RF_ATTENTION_NOALLOC_SCRATCH_BYTES per GPU instead of the context workspace,
+ * so no call allocates, frees or synchronises.  A call whose shape needs more
+ * scratch than that fails with RF_ERR_INVALID: with hd 128 that is about
+ * 65536 positions at 32 query heads.  Every call on one GPU shares that GPU's
+ * array: calls that may overlap on one GPU (several streams or contexts
+ * without ordering between them) race and must not be issued. */
+#define RF_ATTENTION_NOALLOC_SCRATCH_BYTES (8ull << 20)
+int32_t rf_attention_decode_noalloc(rf_ctx *ctx, const float *q, const float *k_hist, const float *v_hist,
+                                    const float *k_cur, const float *v_cur, uint32_t hist_len, uint32_t q_heads,
+                                    uint32_t kv_heads, uint32_t head_dim, float *out, rf_stream_t stream);
+
 /* ---------------------------------------------------------- elementwise */
 
 /* ops::apply_rope -> compute::rope_reference (runtime/src/ops.rs:9-20,

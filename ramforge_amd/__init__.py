@@ -391,6 +391,20 @@ def attention_checked(ctx: Context, q, k_hist, v_hist, k_new, v_new, hist_len: i
     return out
 
 
+def attention_checked_noalloc(ctx: Context, q, k_hist, v_hist, k_new, v_new, hist_len: int, n_heads: int,
+                              n_kv_heads: int, head_dim: int, out: DeviceArray, stream=None) -> DeviceArray:
+    """attention_checked through rf_attention_decode_noalloc: the split
+    records live in the library's static per-device scratch array, so the
+    call allocates nothing (the caller passes ``out``)."""
+    qd, kvd = n_heads * head_dim, n_kv_heads * head_dim
+    _fits("attention tensor", q=(q, 4 * qd), k_hist=(k_hist, 4 * hist_len * kvd), v_hist=(v_hist, 4 * hist_len * kvd),
+          k_new=(k_new, 4 * kvd), v_new=(v_new, 4 * kvd), out=(out, 4 * qd))
+    _lib.check(ctx.lib.rf_attention_decode_noalloc(ctx.handle, _ptr(q), _ptr(k_hist), _ptr(v_hist), _ptr(k_new),
+                                                   _ptr(v_new), hist_len, n_heads, n_kv_heads, head_dim, _ptr(out),
+                                                   stream))
+    return out
+
+
 def apply_rope(ctx: Context, q, k, pos: int, head_dim: int, n_heads: int, n_kv_heads: int, freq_base: float,
                stream=None) -> None:
     """ops::apply_rope (ops.rs:9-20): half-split RoPE in place."""

@@ -92,6 +92,7 @@ SIGNATURES = {
     "rf_matvec": (_i32, [_vp, _u32, _vp, _u64, _u64, _u64, _fp, _fp, _u64, _u64, _vp]),
     "rf_dequantize_rows": (_i32, [_vp, _u32, _vp, _u64, _u64, _u64, _u64, _fp, _vp]),
     "rf_attention_decode": (_i32, [_vp, _fp, _fp, _fp, _fp, _fp, _u32, _u32, _u32, _u32, _fp, _vp]),
+    "rf_attention_decode_noalloc": (_i32, [_vp, _fp, _fp, _fp, _fp, _fp, _u32, _u32, _u32, _u32, _fp, _vp]),
     "rf_rope": (_i32, [_vp, _fp, _fp, _u64, _u32, _u32, _u32, _f32, _vp]),
     "rf_rmsnorm": (_i32, [_vp, _fp, _fp, _u64, _f32, _fp, _vp]),
     "rf_add": (_i32, [_vp, _fp, _fp, _u64, _fp, _vp]),

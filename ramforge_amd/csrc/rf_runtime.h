@@ -58,6 +58,7 @@ struct rf_ctx {
   uint64_t ws_generation = 0;
   // rf_ctx_reserve(..., fixed = 1): workspaces never grow after reservation.
   bool ws_fixed = false;
+  void* noalloc_scratch = nullptr;  // this device's address of the no-allocation scratch array
   float* amax_val = nullptr;
   uint32_t* amax_idx = nullptr;
   std::mutex stage_mu;  // guards the staging buffers below (one upload at a time)

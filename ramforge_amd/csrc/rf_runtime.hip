@@ -184,6 +184,32 @@ int32_t ensure_workspace(rf_ctx* ctx, Workspace& ws, const char* charge, uint64_
   return RF_OK;
 }
 
+// The no-allocation variant's scratch: one array per device, held until the
+// process ends.  Host code never passes `scratch` itself to a kernel: its
+// device address on the current device comes from hipGetSymbolAddress
+// (resolved once per device in rf_ctx_create and kept in rf_ctx).
+constexpr uint64_t NOALLOC_SCRATCH_BYTES = RF_ATTENTION_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) uint8_t scratch[NOALLOC_SCRATCH_BYTES];
+constexpr int MAX_DEVICES = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[MAX_DEVICES] = {};
+
+// Called with `device` current.
+int32_t resolve_scratch(int device, void** out) {
+  if (device < 0 || device >= MAX_DEVICES)
+    return set_error(RF_ERR_UNSUPPORTED, "HIP device %d beyond the %d the library tracks", device, MAX_DEVICES);
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_ptr[device]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_error(e, "hipGetSymbolAddress(scratch)");
+    if (!p) return set_error(RF_ERR_HIP, "hipGetSymbolAddress(scratch) returned a null address");
+    g_scratch_ptr[device] = p;
+  }
+  *out = g_scratch_ptr[device];
+  return RF_OK;
+}
+
 int32_t staged_upload(rf_ctx* ctx, void* dst, const void* src, uint64_t bytes) {
   constexpr uint64_t kStage = 64ull << 20;
   // one upload at a time: the two pinned buffers are the context's
@@ -298,8 +324,14 @@ int32_t rf_ctx_create(int32_t device, uint64_t budget, rf_ctx** out) {
     rf_ctx_destroy(c);  // the stream that was created, if any
     return rc;
   }
+  // this device's address of the no-allocation scratch array (device current)
+  int32_t rc = resolve_scratch(device, &c->noalloc_scratch);
+  if (rc) {
+    rf_ctx_destroy(c);
+    return rc;
+  }
   void* p = nullptr;
-  int32_t rc = vram_alloc(c, "workspace:argmax", 256 * 8 + 64, &p);
+  rc = vram_alloc(c, "workspace:argmax", 256 * 8 + 64, &p);
   if (rc) {
     rf_ctx_destroy(c);
     return rc;
@@ -773,6 +805,25 @@ int32_t rf_attention_decode(rf_ctx* ctx, const float* q, const float* kh, const 
   if (rc) return rc;
   a.ws = static_cast<float*>(ctx->attn_ws.ptr);
   return attention_launch(a, fast, st);
+}
+
+int32_t rf_attention_decode_noalloc(rf_ctx* ctx, const float* q, const float* kh, const float* vh, const float* kc,
+                                    const float* vc, uint32_t hist, uint32_t qh, uint32_t kvh, uint32_t hd,
+                                    float* out, rf_stream_t s) {
+  RF_CHECK_CTX(ctx);
+  AttnArgs a;
+  bool fast = false;
+  uint64_t ws_bytes = 0;
+  int32_t rc = attention_setup(q, kh, vh, kc, vc, hist, qh, kvh, hd, out, &a, &fast, &ws_bytes);
+  if (rc) return rc;
+  if (ws_bytes > NOALLOC_SCRATCH_BYTES)
+    return set_error(RF_ERR_INVALID,
+                     "attention over %u positions with %u query heads of %u needs %llu bytes of scratch; the "
+                     "no-allocation entry point holds %llu",
+                     hist + 1, qh, hd, (unsigned long long)ws_bytes, (unsigned long long)NOALLOC_SCRATCH_BYTES);
+  if (!ctx->noalloc_scratch) return set_error(RF_ERR_HIP, "no-allocation scratch was not resolved for this context");
+  a.ws = static_cast<float*>(ctx->noalloc_scratch);
+  return attention_launch(a, fast, pick_stream(ctx, s));
 }
 
 uint64_t rf_attention_workspace_bytes(uint64_t max_positions, uint32_t qh, uint32_t kvh, uint32_t hd) {
