@@ -184,6 +184,38 @@ def traffic_probe(ctx, m, cfg, rf) -> int:
     return 0
 
 
+def attention_probe(rf, L: int, copies: int = 4) -> int:
+    """Launch only what the attention counters are read for: RoPE + split-K
+    attention + merge (32 q / 8 KV heads, hd 128, L positions; BASELINE config
+    3) once on each of `copies` distinct K/V copies, then four plain device
+    copies of COPY_BYTES (the calibration kernel for FETCH_SIZE/WRITE_SIZE)."""
+    import numpy as np
+
+    ctx = rf.Context(0)
+    rng = np.random.default_rng(7)
+    qh, kvh, hd, hist = 32, 8, 128, L - 1
+    kv = [(ctx.array(rng.normal(0, 1, hist * kvh * hd).astype(np.float32)),
+           ctx.array(rng.normal(0, 1, hist * kvh * hd).astype(np.float32))) for _ in range(copies)]
+    q = ctx.array(rng.normal(0, 1, qh * hd).astype(np.float32))
+    kc = ctx.array(rng.normal(0, 1, kvh * hd).astype(np.float32))
+    vc = ctx.array(rng.normal(0, 1, kvh * hd).astype(np.float32))
+    o = ctx.empty((qh * hd,))
+    ctx.reserve(attention_bytes=ctx.attention_workspace_bytes(L, qh, kvh, hd), fixed=True)
+    for kh, vh in kv:
+        rf.apply_rope(ctx, q, kc, hist, hd, qh, kvh, 10000.0)
+        rf.attention_checked(ctx, q, kh, vh, kc, vc, hist, qh, kvh, hd, out=o)
+    src = ctx.empty((COPY_BYTES,), "uint8")
+    dst = ctx.empty((COPY_BYTES,), "uint8")
+    for _ in range(4):
+        ctx.copy(dst, src, COPY_BYTES)
+    ctx.synchronize()
+    print(json.dumps({"probe": "attention", "positions": L, "launches": copies,
+                      "algorithmic_bytes": 2 * L * kvh * hd * 4 + 2 * qh * hd * 4, "copy_bytes": COPY_BYTES,
+                      "copies": 4}), flush=True)
+    ctx.close()
+    return 0
+
+
 def kernel_bench(rf, syn, use_graph: bool, reps: int = 3) -> list:
     """BASELINE configs 1-3 at kernel level: each call rotates over distinct
     weight (or K/V) copies totalling >= 1.2 GiB so the 256 MiB Infinity Cache
@@ -480,6 +512,9 @@ def main() -> int:
     ap.add_argument("--config5", type=int, default=0, metavar="TOKENS",
                     help="BASELINE config 5 (Q4_K/Q6_K 8B under a 4 GiB VRAM budget, layer streaming) with TOKENS "
                          "greedy tokens; prints one JSON line")
+    ap.add_argument("--attention-probe", type=int, default=0, metavar="L",
+                    help="only launch RoPE + attention at context L on 4 K/V copies and a 256 MiB device copy, for "
+                         "rocprofv3 --pmc runs")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="only launch the dominant kernel (32 gate/up launches) and a 256 MiB device copy, "
                          "for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs")
@@ -500,6 +535,8 @@ def main() -> int:
     if args.config4:
         print(json.dumps({"config4": config4_bench(rf, syn)}), flush=True)
         return 0
+    if args.attention_probe:
+        return attention_probe(rf, args.attention_probe)
     if args.config5:
         res = [config5_bench(rf, syn, args.config5, args.prompt, policy) for policy in (1, 0)]
         print(json.dumps({"config5": res}), flush=True)

@@ -423,10 +423,10 @@ uint32_t rf_tune_matvec_tile_bytes(uint32_t bytes);
  * are 16-byte aligned (default), 0 = one-shot tile kernel everywhere, other
  * values only query.  Returns the mode in effect (process-wide). */
 int32_t rf_tune_matvec_kernel(int32_t mode);
-/* x of the packed Q8_0 / Q4_0 matvec: 1 = int8 digit planes on launches whose
- * wavefronts hold >= 24 KiB of codes (default), 2 = digit planes on every
- * launch whose workgroup LDS holds them (in_dim up to about 36000), 0 = float
- * x everywhere; other values only query.  Returns the mode in effect (process-wide).  With digit
+/* x of the packed Q8_0 / Q4_0 matvec: 0 = float x everywhere (default), 1 =
+ * int8 digit planes on launches whose wavefronts hold >= 24 KiB of codes, 2 =
+ * digit planes on every launch whose workgroup LDS holds them (in_dim up to
+ * about 36000); other values only query.  Returns the mode in effect (process-wide).  With digit
  * planes each 16-element unit of x (times the RMSNorm weights where fused) is
  * rounded to 30-bit fixed point below its largest element: element k of unit
  * u is off by at most 2^(E_u - 31), 2^E_u the power of two above the unit's
@@ -438,6 +438,12 @@ int32_t rf_tune_matvec_kernel(int32_t mode);
  * (decoded weight times x) is NaN or infinities of both signs meet, else the
  * one infinity. */
 int32_t rf_tune_matvec_digits(int32_t mode);
+/* Packed matvec launch shape: 1 = a launch whose rows each fit one step
+ * (in_dim 4096 of Q8_0 / Q4_0 / Q4_K, float x, one matrix) with a wavefront
+ * per row requests its row before staging x (default), 0 = the two-step ring
+ * everywhere; other values only query.  Same results either way.  Returns
+ * the mode in effect (process-wide). */
+int32_t rf_tune_packed_inflight(int32_t mode);
 /* Weight layout of models created afterwards: 1 = Q8_0 / Q4_0 / Q4_K / Q6_K
  * projection weights are repacked at install into the device-native layout
  * (default; the batched prefill needs it), 0 = kept as GGUF bytes; other

@@ -643,11 +643,18 @@ def tune_matvec_kernel(mode: int = -1) -> int:
 
 
 def tune_matvec_digits(mode: int = -1) -> int:
-    """1: packed Q8_0 / Q4_0 launches with >= 24 KiB of codes per wavefront
-    take x as int8 digit planes (30 bits below each 16-element unit's largest
-    element; default), 2: every launch whose LDS holds them, 0: float x
-    everywhere; -1 queries.  Returns the mode in effect."""
+    """0: float x everywhere (default); 1: packed Q8_0 / Q4_0 launches with
+    >= 24 KiB of codes per wavefront take x as int8 digit planes (30 bits
+    below each 16-element unit's largest element); 2: every launch whose LDS
+    holds them; -1 queries.  Returns the mode in effect."""
     return _lib.load().rf_tune_matvec_digits(mode)
+
+
+def tune_packed_inflight(mode: int = -1) -> int:
+    """1: packed launches whose rows fit one step, with a wavefront per row,
+    request the row before staging x (default), 0: the two-step ring; -1
+    queries.  Same results either way."""
+    return _lib.load().rf_tune_packed_inflight(mode)
 
 
 def tune_packed_weights(mode: int = -1) -> int:

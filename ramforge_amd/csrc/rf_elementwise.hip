@@ -201,6 +201,63 @@ __global__ __launch_bounds__(64) void argmax_stage2(const float* __restrict__ x,
   }
 }
 
+// argmax_stage2 for the device decode loop, with the embedding row of the
+// chosen token decoded into `hidden` by the same workgroup (the reference
+// reads the row for the sampled token, persistent.rs:80-205): 256 threads, a
+// 32-element unit (or element, for F32 / F16 / BF16 tables) each at a time.
+template <uint32_t T>
+__global__ __launch_bounds__(256) void argmax_embed_kernel(const float* __restrict__ x, const float* __restrict__ pv,
+                                                           const uint32_t* __restrict__ pi, uint32_t np,
+                                                           uint32_t* __restrict__ out, uint32_t* __restrict__ ring,
+                                                           const int32_t* __restrict__ d_pos,
+                                                           const uint8_t* __restrict__ embd, uint32_t in_dim,
+                                                           uint64_t row_bytes, float* __restrict__ hidden) {
+  __shared__ float sv[4];
+  __shared__ uint32_t si[4];
+  __shared__ uint32_t tok;
+  const uint32_t tid = threadIdx.x;
+  float bv = -INFINITY;
+  uint32_t bi = 0xFFFFFFFFu;
+  for (uint32_t i = tid; i < np; i += 256u) amax_merge(bv, bi, pv[i], pi[i]);
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float ov = __shfl_xor(bv, o, 64);
+    const uint32_t oi = __shfl_xor(bi, o, 64);
+    amax_merge(bv, bi, ov, oi);
+  }
+  if ((tid & 63u) == 0) { sv[tid >> 6] = bv; si[tid >> 6] = bi; }
+  __syncthreads();
+  if (tid == 0) {
+    for (int w = 1; w < 4; ++w) amax_merge(bv, bi, sv[w], si[w]);
+    const uint32_t r = (isnan(x[0]) || bi == 0xFFFFFFFFu) ? 0u : bi;
+    *out = r;
+    if (ring) ring[*d_pos] = r;
+    tok = r;
+  }
+  __syncthreads();
+  const uint8_t* row = embd + (uint64_t)tok * row_bytes;  // tok < n, the table's rows
+  if constexpr (T == T_F32 || T == T_F16 || T == T_BF16) {
+    for (uint32_t c = tid; c < in_dim; c += 256u) {
+      if (T == T_F32) {
+        float f;
+        __builtin_memcpy(&f, row + 4u * c, 4);
+        hidden[c] = f;
+      } else {
+        const uint32_t h = rf_ld_u16(row + 2u * c);
+        hidden[c] = T == T_F16 ? rf_half_to_float(h) : rf_bf16_to_float(h);
+      }
+    }
+  } else {
+    constexpr uint32_t UPB = Fmt<T>::QK / 32u;
+    for (uint32_t u = tid; u < in_dim / 32u; u += 256u) {
+      float vals[32];
+      Fmt<T>::dequant(row, (u / UPB) * Fmt<T>::BS, u % UPB, vals);
+#pragma unroll
+      for (int i = 0; i < 32; ++i) hidden[32u * u + i] = vals[i];
+    }
+  }
+}
+
 uint32_t argmax_partials(uint64_t n) {
   uint64_t b = (n + 1023) / 1024;
   if (b < 1) b = 1;
@@ -213,6 +270,33 @@ hipError_t launch_argmax(const float* logits, uint64_t n, uint32_t* out, float* 
   const uint32_t np = argmax_partials(n);
   hipLaunchKernelGGL(argmax_stage1, dim3(np), dim3(256), 0, st, logits, n, ws_val, ws_idx);
   hipLaunchKernelGGL(argmax_stage2, dim3(1), dim3(64), 0, st, logits, ws_val, ws_idx, np, out, ring, d_pos);
+  return hipGetLastError();
+}
+
+hipError_t launch_argmax_embed(const float* logits, uint64_t n, uint32_t* out, float* ws_val, uint32_t* ws_idx,
+                               uint32_t* ring, const int32_t* d_pos, uint32_t et, const void* embd, uint64_t in_dim,
+                               float* hidden, hipStream_t st) {
+  if (n == 0 || in_dim == 0 || in_dim > 0xFFFFFFFFull) return hipErrorInvalidValue;
+  uint64_t qk = 1, bs = 4;
+  if (et == T_F16 || et == T_BF16) bs = 2;
+  else if (et != T_F32 && !type_geometry(et, &qk, &bs)) return hipErrorInvalidValue;
+  if (in_dim % qk != 0 || (et != T_F32 && et != T_F16 && et != T_BF16 && in_dim % 32 != 0)) return hipErrorInvalidValue;
+  const uint64_t row_bytes = in_dim / qk * bs;
+  const uint32_t np = argmax_partials(n);
+  hipLaunchKernelGGL(argmax_stage1, dim3(np), dim3(256), 0, st, logits, n, ws_val, ws_idx);
+  const uint8_t* e = static_cast<const uint8_t*>(embd);
+  const uint32_t d = (uint32_t)in_dim;
+  switch (et) {
+#define RF_AE(TT)                                                                                                   \
+  case TT:                                                                                                          \
+    hipLaunchKernelGGL(argmax_embed_kernel<TT>, dim3(1), dim3(256), 0, st, logits, ws_val, ws_idx, np, out, ring,  \
+                       d_pos, e, d, row_bytes, hidden);                                                           \
+    break;
+    RF_AE(T_F32) RF_AE(T_F16) RF_AE(T_BF16) RF_AE(T_Q4_0) RF_AE(T_Q5_0) RF_AE(T_Q8_0) RF_AE(T_Q2_K) RF_AE(T_Q3_K)
+    RF_AE(T_Q4_K) RF_AE(T_Q5_K) RF_AE(T_Q6_K) RF_AE(T_Q8_K)
+#undef RF_AE
+    default: return hipErrorInvalidValue;
+  }
   return hipGetLastError();
 }
 

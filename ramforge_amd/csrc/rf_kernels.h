@@ -64,6 +64,11 @@ bool matvec_stream();
 // rows hold >= 24 KiB of codes (1), always (2), or never (0).
 void set_matvec_digits(int mode);
 int matvec_digits();
+// Packed launches whose rows fit one step and leave at most 4 rows per
+// wavefront request all of them before the prologue (1) or use the two-step
+// ring (0).
+void set_packed_inflight(int mode);
+int packed_inflight();
 hipError_t launch_matvec_segments(uint32_t t, const MvSegDesc* segs, int nseg, const float* x,
                                   const float* norm_w, float eps, uint64_t in_dim, int epi,
                                   hipStream_t st);
@@ -88,6 +93,7 @@ struct PkArgs {
   const float* norm_w;
   float eps;
   uint32_t in_dim;
+  int32_t* advance;  // non-null: workgroup 0 adds 1 to *advance (the model's device position)
 };
 struct PkPlan {
   bool ok;
@@ -104,8 +110,10 @@ struct PkSegDesc {
 };
 bool packed_type(uint32_t t);
 PkPlan plan_packed(uint32_t t, uint64_t in_dim);
+// advance: optional device counter the launch increments once (nothing in
+// the launch reads it).
 hipError_t launch_matvec_packed(uint32_t t, const PkSegDesc* segs, int nseg, const float* x, const float* norm_w,
-                                float eps, uint64_t in_dim, int epi, hipStream_t st);
+                                float eps, uint64_t in_dim, int epi, hipStream_t st, int32_t* advance = nullptr);
 // GGUF payload [rows][in_dim] -> packed layout (distinct buffers).
 hipError_t launch_pack(uint32_t t, const void* raw, void* packed, uint64_t rows, uint64_t in_dim, hipStream_t st);
 
@@ -196,6 +204,11 @@ hipError_t launch_bias_add(float* v, const float* b, uint64_t n, hipStream_t st)
 // Writes the index to *out and, if ring != null, also to ring[*d_pos].
 hipError_t launch_argmax(const float* logits, uint64_t n, uint32_t* out, float* ws_val, uint32_t* ws_idx,
                          uint32_t* ring, const int32_t* d_pos, hipStream_t st);
+// launch_argmax whose final stage also decodes row *out of the embedding
+// table (ggml type embd_type, [rows][in_dim], GGUF layout) into `hidden`.
+hipError_t launch_argmax_embed(const float* logits, uint64_t n, uint32_t* out, float* ws_val, uint32_t* ws_idx,
+                               uint32_t* ring, const int32_t* d_pos, uint32_t embd_type, const void* embd,
+                               uint64_t in_dim, float* hidden, hipStream_t st);
 uint32_t argmax_partials(uint64_t n);
 hipError_t launch_synth(uint32_t t, uint64_t seed, uint64_t first_block, uint64_t n_blocks, double mul,
                         void* dst, hipStream_t st);

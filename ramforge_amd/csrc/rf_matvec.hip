@@ -117,11 +117,17 @@ __device__ __forceinline__ void finish_xunit(XUnit& xu) {
 // Contribution of unit `sub` of the block at `blk`: the dot, or for a unit of
 // x holding an infinity or NaN the kind of the reference's terms
 // (unit_kinds), so the row sums come out as the reference's NaN / +-inf.
-// F32 products are the reference's terms already.
+// Only the formats with a min term need that: their dot subtracts
+// dmin m sum(x), which turns the reference's infinite terms into inf - inf.
+// The signed-code dots (and F32) multiply each code by x, which gives the
+// reference's infinities and NaNs by itself.
+template <uint32_t T>
+constexpr bool has_min_term() { return T == T_Q4_K || T == T_Q5_K || T == T_Q2_K; }
+
 template <uint32_t T>
 __device__ __forceinline__ float unit_dot(const uint8_t* b, uint32_t blk, uint32_t sub, const XUnit& x, bool finite) {
-  if constexpr (T == T_F32) return Fmt<T>::dot(b, blk, sub, x);
-  else return finite ? Fmt<T>::dot(b, blk, sub, x) : unit_kinds<T>(b, blk, sub, x);
+  if constexpr (has_min_term<T>()) return finite ? Fmt<T>::dot(b, blk, sub, x) : unit_kinds<T>(b, blk, sub, x);
+  else return Fmt<T>::dot(b, blk, sub, x);
 }
 
 template <uint32_t T, int EPI>
@@ -159,7 +165,7 @@ __global__ __launch_bounds__(1024) void matvec_tiled(MvArgs a) {
     __syncthreads();
   }
   finish_xunit(xu);
-  const bool xfin = unit_finite(xu);
+  const bool xfin = !has_min_term<T>() || unit_finite(xu);
 
   const uint32_t blk = (u / UPB) * Fmt<T>::BS, sub = u % UPB;
   constexpr int MAXR = 8;
@@ -295,7 +301,7 @@ __global__ __launch_bounds__(512) void matvec_stream(MvArgs a) {
   }
   if (a.norm_w != nullptr) norm_xunit(xu, nw, active && g == 0, a.in_dim, a.eps, wsum, tid, nth);
   finish_xunit(xu);
-  const bool xfin = unit_finite(xu);
+  const bool xfin = !has_min_term<T>() || unit_finite(xu);
 
   const uint32_t row_bytes = a.row_bytes;
   const uint32_t blk = (u / UPB) * Fmt<T>::BS, sub = u % UPB;

@@ -34,6 +34,7 @@
 // epilogue, up to three output segments.
 #include "rf_kernels.h"
 
+#include <algorithm>
 #include <mutex>
 #include <type_traits>
 
@@ -359,11 +360,22 @@ struct PkStep {
 // lanes (no bank conflicts): element 4i + k of unit h of lane l's slice of
 // chunk c (EPL = 16 or 32 elements per slice) is stored at
 // c * 64 * EPL + 256 (4h + i) + 4 l + k.  NB step buffers per wavefront: NB - 1
-// steps are in flight while one is decoded.
-template <uint32_t T, int EPI, bool NORM, int U, int LPW, int NB, int NT, bool IX>
+// steps are in flight while one is decoded.  ALLF: every step of the
+// wavefront (at most NB tasks of one step each, LPW covering the whole row)
+// is requested before the prologue and none after it, so a launch makes one
+// memory round trip.
+template <uint32_t T, int EPI, bool NORM, int U, int LPW, int NB, int NT, bool IX, bool ALLF = false>
 __global__ __launch_bounds__(NT) void matvec_packed(PkArgs a) {
   typedef PkFmt<T> F;
   constexpr bool IXE = F::INTX && IX;  // digit planes instead of float x
+  // Non-finite x needs a fallback only where a decode does not multiply each
+  // signed code by x: the digit planes, and Q4_K's min term (d sc sum(q x) -
+  // dmin m sum(x) gives inf - inf where the reference's (d sc q - dmin m) x
+  // is an infinity).  The signed-code float decodes of Q8_0, Q4_0 and Q6_K
+  // produce the reference's NaN / +-inf rows by themselves: a code times an
+  // infinity is the reference's term up to a positive power of two, and
+  // finite terms cannot change an infinite or NaN sum.
+  constexpr bool KINDS = IXE || T == T_Q4_K;
   constexpr bool DUAL = EPI == EPI_SWIGLU;
   constexpr uint32_t EPB = F::EPB, UPS = EPB, EPL = 16u * UPS, NW = NT / 64;
   extern __shared__ __align__(16) float xl[];  // [nchunk * 64 * EPL] x, then [nchunk * 64 * UPS] unit sums
@@ -376,6 +388,7 @@ __global__ __launch_bounds__(NT) void matvec_packed(PkArgs a) {
   // pointers are then scalar values, so no vector load (whose wait would also
   // wait for the codes in flight) is spent on them.
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  if (a.advance != nullptr && blockIdx.x == 0 && tid == 0) *a.advance += 1;
   const uint32_t in = a.in_dim, crb = in / EPB;
   const uint32_t nchunk = (crb + 1023u) / 1024u, nstep = (nchunk + LPW - 1) / LPW;
   float* xsum_l = xl + nchunk * 64u * EPL;
@@ -431,10 +444,10 @@ __global__ __launch_bounds__(NT) void matvec_packed(PkArgs a) {
   auto advance = [&](uint32_t& tt, uint32_t& ss) {
     if (++ss == nstep) { ss = 0; tt += gstride; }
   };
-  // The first NB - 1 steps are requested before the prologue.
+  // The first NB - 1 steps (ALLF: all NB) are requested before the prologue.
   uint32_t ct = blockIdx.x * NW + wave, cs = 0, ft = ct, fs = 0;
 #pragma unroll
-  for (int b = 0; b < NB - 1; ++b) {
+  for (int b = 0; b < (ALLF ? NB : NB - 1); ++b) {
     fetch(buf[b], ft, fs);
     advance(ft, fs);
   }
@@ -473,7 +486,7 @@ __global__ __launch_bounds__(NT) void matvec_packed(PkArgs a) {
   };
   // Float layout: the unit in its permuted LDS slots and its sum.  Returns
   // false for a non-finite element.
-  auto stage_float = [&](uint32_t j, float& ss, bool sq) -> bool {
+  auto stage_float = [&](uint32_t j, float& ss, bool sq, bool check) -> bool {
     const uint32_t js = j / UPS, h = j % UPS;
     float v[16];
     float s = 0.f;
@@ -485,8 +498,10 @@ __global__ __launch_bounds__(NT) void matvec_packed(PkArgs a) {
         *reinterpret_cast<float4*>(dst + 256 * k) = make_float4(v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]);
         s += v[4 * k]; s += v[4 * k + 1]; s += v[4 * k + 2]; s += v[4 * k + 3];
       }
+      if (check) {
 #pragma unroll
-      for (int k = 0; k < 16; ++k) fin = fin && fabsf(v[k]) <= 3.40282347e38f;
+        for (int k = 0; k < 16; ++k) fin = fin && fabsf(v[k]) <= 3.40282347e38f;
+      }
     }
     xsum_l[j] = s;
     return fin;
@@ -543,14 +558,16 @@ __global__ __launch_bounds__(NT) void matvec_packed(PkArgs a) {
     float ss = 0.f;
     for (uint32_t j = tid; j < nunit; j += NT) {
       if constexpr (IXE) finite = stage_digits(j, ss) && finite;
-      else finite = stage_float(j, ss, true) && finite;
+      else finite = stage_float(j, ss, true, KINDS) && finite;
     }
     if (NORM) {
       ss = rf_wave_sum(ss);
       if (lane == 0) wsum[wave] = ss;
     }
-    const bool bad = __ballot(!finite) != 0;
-    if (lane == 0) wbad[wave] = bad ? 1u : 0u;
+    if constexpr (KINDS) {
+      const bool bad = __ballot(!finite) != 0;
+      if (lane == 0) wbad[wave] = bad ? 1u : 0u;
+    }
     // EPI_RESIDUAL: the residual of every row this wavefront will finish
     // (at most PK_RES_SLOTS tasks; the launch sizes the grid for that), so
     // the epilogue reads LDS instead of waiting on a load queued behind codes.
@@ -580,8 +597,10 @@ __global__ __launch_bounds__(NT) void matvec_packed(PkArgs a) {
   // finite partial sums, which the reference's order could turn into NaN, is
   // not reproduced).
   bool bad = false;
+  if constexpr (KINDS) {
 #pragma unroll
-  for (uint32_t i = 0; i < NW; ++i) bad = bad || wbad[i] != 0u;
+    for (uint32_t i = 0; i < NW; ++i) bad = bad || wbad[i] != 0u;
+  }
   float inv = 1.f;
   if (NORM) {
     float tot = 0.f;
@@ -589,10 +608,11 @@ __global__ __launch_bounds__(NT) void matvec_packed(PkArgs a) {
     for (uint32_t i = 0; i < NW; ++i) tot += wsum[i];
     inv = 1.0f / sqrtf(tot / (float)in + a.eps);
   }
+  if constexpr (KINDS) {
   if (bad) {
     if constexpr (IXE) {  // the digit layout holds no floats: stage them
       float unused = 0.f;
-      for (uint32_t j = tid; j < nunit; j += NT) (void)stage_float(j, unused, false);
+      for (uint32_t j = tid; j < nunit; j += NT) (void)stage_float(j, unused, false, false);
       __syncthreads();
     }
     for (uint32_t t = blockIdx.x * NW + wave; t < ntask; t += gstride) {
@@ -647,6 +667,7 @@ __global__ __launch_bounds__(NT) void matvec_packed(PkArgs a) {
       }
     }
     return;
+  }
   }
 
   float acc[U], acc2[U];
@@ -749,6 +770,15 @@ __global__ __launch_bounds__(NT) void matvec_packed(PkArgs a) {
   // check at the top of each step, so every buffer is consumed (its loads
   // waited for) before it is refilled.
   auto run = [&](auto mode) {
+    if constexpr (ALLF) {  // nstep == 1 and at most NB tasks per wavefront (the launch sees to both)
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        if (ct >= ntask) return;
+        consume(mode, buf[b], ct, cs);
+        advance(ct, cs);
+      }
+      return;
+    }
     for (;;) {
 #pragma unroll
       for (int b = 0; b < NB; ++b) {
@@ -877,10 +907,13 @@ static int pk_occupancy(PkOccCache& c, const void* kern, int nt, uint32_t lds) {
   return occ;
 }
 
-// x as digit planes on the launches where they pay (1, default), on every
-// Q8_0 / Q4_0 launch whose LDS holds them (2), or float x everywhere (0):
-// rf_tune_matvec_digits.
-static int g_digits = 1;
+// x as digit planes on the launches with >= 24 KiB of codes per wavefront
+// (1), on every Q8_0 / Q4_0 launch whose LDS holds them (2), or float x
+// everywhere (0, default): rf_tune_matvec_digits.  Measured A/B on one box,
+// 8B gate/up: 3 planes 21.6-21.9 us; 4 planes 22.3-22.5 us; float x
+// 22.4-22.5 us.  With 4 planes the digits no longer pay, so float x, which
+// is the reference's arithmetic up to summation order, is the default.
+static int g_digits = 0;
 void set_matvec_digits(int mode) { g_digits = mode; }
 int matvec_digits() { return g_digits; }
 
@@ -944,6 +977,45 @@ static hipError_t launch_pk(const PkArgs& a, uint32_t lds, hipStream_t st) {
   return hipGetLastError();
 }
 
+// All-in-flight launches (matvec_packed<..., ALLF>): when a row fits one
+// step (LPW = the row's chunks) and the grid gives every wavefront one row,
+// the wavefront requests it before the x prologue.  rf_tune_packed_inflight
+// switches them off (0) or on (1, default).
+static int g_inflight = 1;
+void set_packed_inflight(int mode) { g_inflight = mode; }
+int packed_inflight() { return g_inflight; }
+
+template <uint32_t T, int EPI, bool NORM, int LPW, int NB>
+static hipError_t launch_pk_all_nb(const PkArgs& a, uint32_t lds, uint64_t grid, hipStream_t st) {
+  hipLaunchKernelGGL((matvec_packed<T, EPI, NORM, 1, LPW, NB, 512, false, true>), dim3((uint32_t)grid), dim3(512),
+                     lds, st, a);
+  return hipGetLastError();
+}
+
+// One row per wavefront: the grid is a wavefront per row when the NB = 1
+// instance's occupancy holds that many and the two-step ring would give at
+// most 2 rows per wavefront (measured on the 8B shapes, Q8_0, A/B on one box:
+// o-proj 4096x4096 7.1 -> 6.6 us; Q/K/V with one row per wavefront in 768
+// workgroups 8.73 against 8.44 us for the ring's 3 rows in 256; with 1.5
+// rows per wavefront 8.33 against 8.21; the 14336-wide down projection 15.5
+// against 13.7 us, its x staged in twice as many workgroups, so neither
+// takes this shape).  *done stays false otherwise.
+template <uint32_t T, int EPI, bool NORM, int LPW>
+static hipError_t launch_pk_all(const PkArgs& a, uint32_t lds, hipStream_t st, bool* done) {
+  *done = false;
+  static PkOccCache cache;
+  auto k1 = matvec_packed<T, EPI, NORM, 1, LPW, 1, 512, false, true>;
+  const int occ = pk_occupancy(cache, reinterpret_cast<const void*>(k1), 512, lds);
+  if (occ < 1) return hipSuccess;
+  const uint64_t nw = 8, cus = (uint64_t)pk_cu_count(), tasks = a.rows_total;
+  const uint64_t grid = (tasks + nw - 1) / nw;
+  // the ring's grid would give at most 2 rows per wavefront (o-proj); at 3
+  // (Q/K/V) the ring's 256 workgroups beat 768 one-row ones
+  if (grid > cus * (uint64_t)occ || tasks > 2 * cus * nw) return hipSuccess;
+  *done = true;
+  return launch_pk_all_nb<T, EPI, NORM, LPW, 1>(a, lds, grid, st);
+}
+
 // Launch shape, from timing the 8B projections (Q8_0 and Q4_0; 4096 and
 // 14336 inputs): one row per wavefront; LPW = chunks per step, up to 4 (2 for
 // gate/up, whose step loads two matrices; Q6_K, with three more loads per
@@ -953,6 +1025,20 @@ static hipError_t launch_pk(const PkArgs& a, uint32_t lds, hipStream_t st) {
 template <uint32_t T, int EPI, bool NORM>
 static hipError_t launch_pk_l(const PkArgs& a, uint32_t lds, hipStream_t st) {
   const uint64_t nchunk = pk_nchunk(T, a.in_dim);
+  // All-in-flight shapes: single-matrix float-x launches whose rows are 4
+  // chunks (Q8_0) or 2 (Q4_0, Q4_K): in_dim 4096.
+  if constexpr (EPI != EPI_SWIGLU && T != T_Q6_K) {
+    bool done = false;
+    hipError_t e = hipSuccess;
+    if (g_inflight && !(PkFmt<T>::INTX && g_digits == 2)) {
+      if constexpr (T == T_Q8_0) {
+        if (nchunk == 4) e = launch_pk_all<T, EPI, NORM, 4>(a, lds, st, &done);
+      } else {
+        if (nchunk == 2) e = launch_pk_all<T, EPI, NORM, 2>(a, lds, st, &done);
+      }
+    }
+    if (done || e != hipSuccess) return e;
+  }
   uint32_t pref = EPI == EPI_SWIGLU ? 2 : 4;
   if (T == T_Q6_K) pref /= 2;
   uint32_t lpw = 1;
@@ -997,7 +1083,7 @@ static hipError_t launch_pk_t(const PkArgs& a, uint32_t lds, int epi, bool norm,
 static bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 hipError_t launch_matvec_packed(uint32_t t, const PkSegDesc* segs, int nseg, const float* x, const float* norm_w,
-                                float eps, uint64_t in_dim, int epi, hipStream_t st) {
+                                float eps, uint64_t in_dim, int epi, hipStream_t st, int32_t* advance) {
   const PkPlan p = plan_packed(t, in_dim);
   if (!p.ok || nseg < 1 || nseg > 3) return hipErrorInvalidValue;
   if (!al16(x) || (norm_w && !al16(norm_w))) return hipErrorInvalidValue;
@@ -1034,6 +1120,7 @@ hipError_t launch_matvec_packed(uint32_t t, const PkSegDesc* segs, int nseg, con
   a.norm_w = norm_w;
   a.eps = eps;
   a.in_dim = (uint32_t)in_dim;
+  a.advance = advance;
   switch (t) {
     case T_Q8_0: return launch_pk_t<T_Q8_0>(a, p.lds_bytes, epi, norm_w != nullptr, st);
     case T_Q4_0: return launch_pk_t<T_Q4_0>(a, p.lds_bytes, epi, norm_w != nullptr, st);

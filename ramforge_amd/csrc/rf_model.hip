@@ -663,8 +663,13 @@ struct MSeg {
 // does not fit the LDS tile (very wide F32 rows) — the same computation as
 // separate kernels: RMSNorm into xnorm, rowwise matvec, then the residual /
 // SiLU*up epilogue.
+hipError_t fused_matvec_impl(rf_model* m, const MSeg* ms, int nseg, const float* x, const float* norm_w,
+                             uint64_t in_dim, int epi);
+
+// advance: the device position, incremented once by the launch (the packed
+// kernel does it; the GGUF-layout path adds the one-thread kernel).
 hipError_t fused_matvec(rf_model* m, const MSeg* ms, int nseg, const float* x, const float* norm_w, uint64_t in_dim,
-                        int epi) {
+                        int epi, int32_t* advance = nullptr) {
   hipStream_t st = m->ctx->compute;
   const uint32_t t = ms[0].w->type;
   if (ms[0].w->packed) {
@@ -672,8 +677,17 @@ hipError_t fused_matvec(rf_model* m, const MSeg* ms, int nseg, const float* x, c
     for (int i = 0; i < nseg; ++i)
       ps[i] = PkSegDesc{ms[i].w->d, ms[i].w_up ? ms[i].w_up->d : nullptr, ms[i].w->ne1, 0, ms[i].rows, ms[i].y,
                         ms[i].res};
-    return launch_matvec_packed(t, ps, nseg, x, norm_w, m->cfg.rms_eps, in_dim, epi, st);
+    return launch_matvec_packed(t, ps, nseg, x, norm_w, m->cfg.rms_eps, in_dim, epi, st, advance);
   }
+  hipError_t e = fused_matvec_impl(m, ms, nseg, x, norm_w, in_dim, epi);
+  if (e == hipSuccess && advance) e = launch_advance_pos(advance, st);
+  return e;
+}
+
+hipError_t fused_matvec_impl(rf_model* m, const MSeg* ms, int nseg, const float* x, const float* norm_w,
+                             uint64_t in_dim, int epi) {
+  hipStream_t st = m->ctx->compute;
+  const uint32_t t = ms[0].w->type;
   MvSegDesc segs[3];
   for (int i = 0; i < nseg; ++i)
     segs[i] = MvSegDesc{ms[i].w->d, ms[i].w_up ? ms[i].w_up->d : nullptr, ms[i].y, ms[i].res, ms[i].rows};
@@ -795,23 +809,23 @@ int32_t enqueue_gateup(rf_model* m, size_t li) {
   return RF_OK;
 }
 
-// 5. down + residual.
-int32_t enqueue_down(rf_model* m, size_t li) {
+// 5. down + residual (advance: the position step that ends a forward pass).
+int32_t enqueue_down(rf_model* m, size_t li, int32_t* advance = nullptr) {
   const rf_model_config& c = m->cfg;
   Layer& L = m->layers[li];
   const uint64_t d = c.embedding_length, f = c.feed_forward_length;
   MSeg s{&L.down, nullptr, m->hidden, m->hidden, d};
-  RF_LAUNCH(fused_matvec(m, &s, 1, m->act, nullptr, f, EPI_RESIDUAL), "down");
+  RF_LAUNCH(fused_matvec(m, &s, 1, m->act, nullptr, f, EPI_RESIDUAL, advance), "down");
   return RF_OK;
 }
 
-int32_t enqueue_layer(rf_model* m, size_t li) {
+int32_t enqueue_layer(rf_model* m, size_t li, int32_t* advance = nullptr) {
   int32_t rc;
   if ((rc = enqueue_qkv(m, li))) return rc;
   if ((rc = enqueue_attention(m, li))) return rc;
   if ((rc = enqueue_oproj(m, li))) return rc;
   if ((rc = enqueue_gateup(m, li))) return rc;
-  return enqueue_down(m, li);
+  return enqueue_down(m, li, advance);
 }
 
 // Algorithmic HBM bytes of one launch group of layer li (weights + vectors read
@@ -835,13 +849,16 @@ uint64_t part_bytes(rf_model* m, int kind, size_t li, uint64_t hist) {
   }
 }
 
-// Embedding of *d_token, all layers, position advance.
-int32_t enqueue_forward(rf_model* m) {
+// Embedding of *d_token (unless the caller's argmax already decoded it into
+// the hidden state), all layers, position advance (inside the last layer's
+// down projection).
+int32_t enqueue_forward(rf_model* m, bool embed = true) {
   hipStream_t st = m->ctx->compute;
   const rf_model_config& c = m->cfg;
-  RF_LAUNCH(launch_dequant_rows(m->token_embd.type, m->token_embd.d, c.embedding_length, 1, m->hidden, m->d_token,
-                                c.vocab_size, st),
-            "embedding");
+  if (embed)
+    RF_LAUNCH(launch_dequant_rows(m->token_embd.type, m->token_embd.d, c.embedding_length, 1, m->hidden, m->d_token,
+                                  c.vocab_size, st),
+              "embedding");
   const uint32_t nl = (uint32_t)m->layers.size();
   for (uint32_t li = 0; li < nl; ++li) {
     int32_t rc;
@@ -853,14 +870,14 @@ int32_t enqueue_forward(rf_model* m) {
       if (li + 1 < nl && (rc = acquire_layer(m, li + 1, true))) return rc;
       RF_LAUNCH(hipStreamWaitEvent(st, m->res[li].uploaded, 0), "wait for layer upload");
     }
-    if ((rc = enqueue_layer(m, li))) return rc;
+    if ((rc = enqueue_layer(m, li, li + 1 == nl ? m->d_pos : nullptr))) return rc;
     if (m->streaming && (rc = settle_layer(m, li))) return rc;
   }
   if (m->streaming) {
     int32_t rc = release_retired(m);  // release_layer for layers the cache did not take
     if (rc) return rc;
   }
-  RF_LAUNCH(launch_advance_pos(m->d_pos, st), "advance position");
+  if (nl == 0) RF_LAUNCH(launch_advance_pos(m->d_pos, st), "advance position");
   return RF_OK;
 }
 
@@ -875,14 +892,16 @@ int32_t enqueue_logits(rf_model* m) {
   return RF_OK;
 }
 
-// One decode step: logits -> argmax (token stored at ring[pos]) -> forward.
+// One decode step: logits -> argmax (token stored at ring[pos]) with the
+// chosen token's embedding row decoded by the same kernel -> layers.
 int32_t enqueue_decode_step(rf_model* m) {
   int32_t rc = enqueue_logits(m);
   if (rc) return rc;
-  RF_LAUNCH(launch_argmax(m->logits, m->cfg.vocab_size, m->d_token, m->amax_val, m->amax_idx, m->d_ring, m->d_pos,
-                          m->ctx->compute),
+  RF_LAUNCH(launch_argmax_embed(m->logits, m->cfg.vocab_size, m->d_token, m->amax_val, m->amax_idx, m->d_ring,
+                                m->d_pos, m->token_embd.type, m->token_embd.d, m->cfg.embedding_length, m->hidden,
+                                m->ctx->compute),
             "argmax");
-  return enqueue_forward(m);
+  return enqueue_forward(m, false);
 }
 
 int32_t sync(rf_model* m) {

@@ -1009,6 +1009,11 @@ int32_t rf_tune_matvec_kernel(int32_t mode) {
   return matvec_stream() ? 1 : 0;
 }
 
+int32_t rf_tune_packed_inflight(int32_t mode) {
+  if (mode == 0 || mode == 1) set_packed_inflight(mode);
+  return packed_inflight();
+}
+
 int32_t rf_tune_matvec_digits(int32_t mode) {
   if (mode >= 0 && mode <= 2) set_matvec_digits(mode);
   return matvec_digits();

@@ -327,13 +327,14 @@ def _x_wide_range(rng, n):
 
 
 # Shapes whose wavefronts hold at least 24 KiB of codes on a 256-CU device,
-# where Q8_0 and Q4_0 take x as int8 digit planes in the default mode (Q8_0:
+# where Q8_0 and Q4_0 take x as int8 digit planes in digit mode 1 (Q8_0:
 # 3 rows of 8192 codes per wavefront; Q4_0 12288 x 16384: 3 rows of 8192
 # bytes per wavefront of 1024-thread workgroups); the others above use the
 # float path unless digits are forced.
+@pytest.mark.parametrize("digits_mode", [1], indirect=True, ids=["auto"])
 @pytest.mark.parametrize("t,out_dim,in_dim", [(Q8_0, 6144, 8192), (Q4_0, 12288, 16384), (Q8_0, 28672, 8192)])
 @pytest.mark.parametrize("xkind", ["normal", "wide"])
-def test_matvec_packed_digit_planes(ctx, orc, t, out_dim, in_dim, xkind):
+def test_matvec_packed_digit_planes(ctx, orc, digits_mode, t, out_dim, in_dim, xkind):
     if not _rf().packed_supported(t, in_dim):
         pytest.skip(f"in_dim {in_dim} exceeds this device's LDS for {NAMES[t]}")
     _check_matvec_packed(ctx, orc, t, out_dim, in_dim, 1500 + t + out_dim % 97,
@@ -446,6 +447,27 @@ def test_matvec_packed_nonfinite_x(ctx, orc, digits_mode, t, case):
           f"{np.isneginf(ref).sum()} -inf rows as the oracle", flush=True)
     for a in (w, xd, y):
         a.free()
+
+
+@pytest.fixture
+def inflight_mode(request):
+    """rf_tune_packed_inflight for the test: 1 one-row-per-wavefront launches
+    request their rows before staging x, 0 the two-step ring everywhere."""
+    rf = _rf()
+    old = rf.tune_packed_inflight(-1)
+    assert rf.tune_packed_inflight(request.param) == request.param
+    yield request.param
+    rf.tune_packed_inflight(old)
+
+
+@pytest.mark.parametrize("inflight_mode", [1, 0], indirect=True, ids=["inflight", "ring"])
+@pytest.mark.parametrize("t", PACKED)
+@pytest.mark.parametrize("out_dim,in_dim", [(4096, 4096), (1000, 4096), (2048, 4096)])
+def test_matvec_packed_inflight_shapes(ctx, orc, inflight_mode, t, out_dim, in_dim):
+    """in_dim 4096 launches with one row per wavefront (all requested before
+    the x prologue) and with the ring, against the oracle."""
+    _check_matvec_packed(ctx, orc, t, out_dim, in_dim, 2300 + t + out_dim)
+    _check_matvec_packed(ctx, orc, t, out_dim, in_dim, 2310 + t + out_dim, row_start=7, row_count=out_dim - 20)
 
 
 @pytest.mark.parametrize("t", PACKED)

@@ -194,8 +194,11 @@ DIGITS_CFG = dict(TINY, embedding_length=4096, feed_forward_length=14336, block_
 
 
 def test_gateup_digit_planes(ctx, orc):
+    rf = _rf()
     T = _tiny_tensors(np.random.default_rng(976), DIGITS_CFG, ALL_Q8)
-    print("  d 4096, ffn 14336, Q8_0 gate/up on digit planes", flush=True)
+    print("  d 4096, ffn 14336, Q8_0 gate/up on digit planes (mode 1)", flush=True)
+    old = rf.tune_matvec_digits(-1)
+    rf.tune_matvec_digits(1)
     gm = _load_gpu(ctx, DIGITS_CFG, T, 16)
     om = orc.Model(DIGITS_CFG, T, kv_capacity=16, threads=8)
     try:
@@ -204,6 +207,7 @@ def test_gateup_digit_planes(ctx, orc):
             hr = om.forward(tok, pos)
             assert np.max(np.abs(h - hr)) <= 2e-4 * max(1.0, np.abs(hr).max()), pos
     finally:
+        rf.tune_matvec_digits(old)
         gm.close()
         om.close()
 
