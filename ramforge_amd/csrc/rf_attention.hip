@@ -11,8 +11,9 @@
 //     workgroup and KV head).  A workgroup (4 wavefronts) owns one
 //     (chunk, KV head) pair and all G = qh/kvh query heads that share it, so
 //     every K/V row is read from HBM once for the whole group.
-//   * Sixteen lanes cooperate on one position (hd/16 consecutive dims each:
-//     512 contiguous bytes per position for hd = 128); a wavefront covers four
+//   * Sixteen lanes cooperate on one position (hd/16 dims each, taken four
+//     at a time so that every load of the 16 lanes reads 256 contiguous
+//     bytes of the row); a wavefront covers four
 //     positions per step and every lane issues the loads of four steps before
 //     it uses any of them, so a 64-position chunk is one round trip per pass.
 //   * The G partial dot products of a position are summed over the 16 lanes
@@ -103,11 +104,13 @@ __device__ __forceinline__ void load_few(float* dst, const float* src) {
   }
 }
 
+// n dims of a K row for one lane: four consecutive floats from every 64
+// (src points at the lane's first float of the row).
 __device__ __forceinline__ void load_dims(float* dst, const float* src, int n) {
   const f32x4* p = reinterpret_cast<const f32x4*>(src);
 #pragma unroll
   for (int i = 0; i < n / 4; ++i) {
-    const f32x4 v = __builtin_nontemporal_load(p + i);
+    const f32x4 v = __builtin_nontemporal_load(p + 16 * i);
     dst[4 * i] = v.x; dst[4 * i + 1] = v.y; dst[4 * i + 2] = v.z; dst[4 * i + 3] = v.w;
   }
 }
@@ -125,6 +128,9 @@ __global__ __launch_bounds__(64 * W) void attn_split(AttnArgs a) {
   constexpr int HD = DPL * 16;
   constexpr uint32_t NTH = 64u * W, NSLOT = 4u * W;
   constexpr int U = DPL <= 8 ? ATT_UNROLL : ATT_UNROLL / 2;  // register budget for hd = 256
+  constexpr uint32_t RV = 16;                                 // V rows per wavefront and round
+  // (Holding a whole 256-position chunk in flight, 8 K positions per lane
+  // and 32 V rows per wavefront, measured slower at 2048-8000 positions.)
   constexpr uint32_t WMASK = 16u / G - 1u;
   __shared__ __align__(16) float sc[G][ATT_MAX_CHUNK];
   __shared__ __align__(16) float qs[G][HD];
@@ -159,7 +165,9 @@ __global__ __launch_bounds__(64 * W) void attn_split(AttnArgs a) {
   const uint32_t ns = (total + chunk - 1) / chunk;
   const float* cs = a.rope ? a.rope + (size_t)hist * HD : nullptr;  // [half][2] for this position
   const uint32_t sl = lane & 15u, slot = wave * 4u + (lane >> 4);
-  const uint32_t d0 = sl * DPL;
+  // Lane sl of a position holds dims kdim(i) = 64 (i / 4) + 4 sl + i % 4, so
+  // each 16-byte load of the 16 lanes covers 256 contiguous bytes of the row.
+  const uint32_t d0 = sl * 4u;
   const float* kb = a.k_hist + (size_t)p0 * kvw + g * HD + d0;
   // Pass 2 maps lanes to dims instead: lane l owns dims [l*DPW, (l+1)*DPW) of
   // every V row and wavefront w the rows w*16 .. w*16+15 of each 64-row batch,
@@ -170,7 +178,7 @@ __global__ __launch_bounds__(64 * W) void attn_split(AttnArgs a) {
   // The first batch of K and V rows is requested before anything else, so the
   // prologue's loads and both passes of a 64-position chunk share one memory
   // round trip.  Indices are clamped: every load is in bounds.
-  float kv[U][DPL], vv[16][DPW];
+  float kv[U][DPL], vv[RV][DPW];
   if (nmain > 0) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -178,8 +186,8 @@ __global__ __launch_bounds__(64 * W) void attn_split(AttnArgs a) {
       load_dims(kv[u], kb + (size_t)j * kvw, DPL);
     }
 #pragma unroll
-    for (int k = 0; k < 16; ++k) {
-      const uint32_t j = min(wave * 16u + k, nmain - 1u);
+    for (int k = 0; k < (int)RV; ++k) {
+      const uint32_t j = min(wave * RV + k, nmain - 1u);
       load_few<DPW>(vv[k], vb + (size_t)j * kvw);
     }
   }
@@ -224,7 +232,7 @@ __global__ __launch_bounds__(64 * W) void attn_split(AttnArgs a) {
 #pragma unroll
   for (int h = 0; h < G; ++h)
 #pragma unroll
-    for (int i = 0; i < DPL; ++i) qr[h][i] = qs[h][d0 + i];
+    for (int i = 0; i < DPL; ++i) qr[h][i] = qs[h][64 * (i / 4) + d0 + i % 4];
 
   // Pass 1: scores.
   for (uint32_t j0 = 0; j0 < nmain; j0 += NSLOT * U) {
@@ -257,7 +265,7 @@ __global__ __launch_bounds__(64 * W) void attn_split(AttnArgs a) {
     for (int h = 0; h < G; ++h) {
       float acc = 0.f;
 #pragma unroll
-      for (int i = 0; i < DPL; ++i) acc = fmaf(qr[h][i], kcur[d0 + i], acc);
+      for (int i = 0; i < DPL; ++i) acc = fmaf(qr[h][i], kcur[64 * (i / 4) + d0 + i % 4], acc);
       s[h] = acc;
     }
     uint32_t hh = 0;
@@ -282,37 +290,39 @@ __global__ __launch_bounds__(64 * W) void attn_split(AttnArgs a) {
   }
   __syncthreads();
 
-  // Pass 2: o[h] = sum_p e[h][p] * V_p, 16 W rows per batch.
+  // Pass 2: o[h] = sum_p e[h][p] * V_p, RV W rows per batch.
   float o[G][DPW];
 #pragma unroll
   for (int h = 0; h < G; ++h)
 #pragma unroll
     for (int i = 0; i < DPW; ++i) o[h][i] = 0.f;
-  for (uint32_t j0 = 0; j0 < nmain; j0 += 16u * W) {
+  for (uint32_t j0 = 0; j0 < nmain; j0 += RV * W) {
     if (j0 > 0) {
 #pragma unroll
-      for (int k = 0; k < 16; ++k) {
-        const uint32_t j = min(j0 + wave * 16u + k, nmain - 1u);
+      for (int k = 0; k < (int)RV; ++k) {
+        const uint32_t j = min(j0 + wave * RV + k, nmain - 1u);
         load_few<DPW>(vv[k], vb + (size_t)j * kvw);
       }
     }
-    // weights of this wavefront's 16 rows, 16-byte LDS reads (j0 + 16w is a
-    // multiple of 16 and below ATT_MAX_CHUNK since j0 < nmain <= chunk)
-    float e[G][16];
+    // weights of this wavefront's rows, four at a time with 16-byte LDS reads
+    // (j0 + RV w is a multiple of 16, and j0 + RV (w + 1) <= ATT_MAX_CHUNK
+    // since j0 < nmain <= chunk <= ATT_MAX_CHUNK, a multiple of RV W)
 #pragma unroll
-    for (int h = 0; h < G; ++h)
+    for (int q4 = 0; q4 < (int)RV / 4; ++q4) {
+      float e[G][4];
 #pragma unroll
-      for (int q4 = 0; q4 < 4; ++q4) {
-        const float4 w4 = *reinterpret_cast<const float4*>(&sc[h][j0 + wave * 16u + 4u * q4]);
-        e[h][4 * q4] = w4.x; e[h][4 * q4 + 1] = w4.y; e[h][4 * q4 + 2] = w4.z; e[h][4 * q4 + 3] = w4.w;
+      for (int h = 0; h < G; ++h) {
+        const float4 w4 = *reinterpret_cast<const float4*>(&sc[h][j0 + wave * RV + 4u * q4]);
+        e[h][0] = w4.x; e[h][1] = w4.y; e[h][2] = w4.z; e[h][3] = w4.w;
       }
 #pragma unroll
-    for (int k = 0; k < 16; ++k) {
-      const bool use = j0 + wave * 16u + k < nmain;
+      for (int k = 0; k < 4; ++k) {
+        const bool use = j0 + wave * RV + 4u * q4 + k < nmain;
 #pragma unroll
-      for (int h = 0; h < G; ++h)
+        for (int h = 0; h < G; ++h)
 #pragma unroll
-        for (int i = 0; i < DPW; ++i) o[h][i] = use ? fmaf(e[h][k], vv[k][i], o[h][i]) : o[h][i];
+          for (int i = 0; i < DPW; ++i) o[h][i] = use ? fmaf(e[h][k], vv[4 * q4 + k][i], o[h][i]) : o[h][i];
+      }
     }
   }
   if (has_cur && wave == 0) {
@@ -479,8 +489,8 @@ bool attention_supported(uint32_t qh, uint32_t kvh, uint32_t hd, uint64_t total)
 // ATT_MAX_SPLITS chunks of at most ATT_MAX_CHUNK positions).  Timed on
 // 32 q / 8 KV heads, hd 128, split + merge per layer: 256 workgroups beat
 // 1024 at every length from 256 to 8192 positions (9.3 vs 13.2 us at 512,
-// 20.5 vs 24.5 us at 8192); workgroups of chunks past the end still cost
-// their dispatch.
+// 20.5 vs 24.5 us at 8192) and 512 beat neither (27.9 us at 8000 against
+// 18.9 for 256); workgroups of chunks past the end still cost their dispatch.
 uint32_t attention_splits(uint32_t total, uint32_t kvh) {
   uint32_t n = (total + ATT_MIN_CHUNK - 1) / ATT_MIN_CHUNK;
   uint32_t cap = 256u / (kvh ? kvh : 1u);
@@ -595,6 +605,13 @@ hipError_t launch_attention(const AttnArgs& a, hipStream_t st) {
   if (e != hipSuccess || a.nsplit == 1) return e;
   hipLaunchKernelGGL(attn_combine, dim3(a.qh, (a.hd + 31) / 32, a.ntok ? a.ntok : 1), dim3(256), 0, st, a);
   return hipGetLastError();
+}
+
+// Loads this file's code object on the current device (HIP defers that to a
+// kernel's first use, which may otherwise fall inside a stream capture).
+hipError_t load_module_attention() {
+  hipFuncAttributes fa;
+  return hipFuncGetAttributes(&fa, reinterpret_cast<const void*>(attn_combine));
 }
 
 }  // namespace rf

@@ -569,4 +569,11 @@ hipError_t launch_synth(uint32_t t, uint64_t seed, uint64_t first, uint64_t nblk
   return hipGetLastError();
 }
 
+// Loads this file's code object on the current device (HIP defers that to a
+// kernel's first use, which may otherwise fall inside a stream capture).
+hipError_t load_module_elementwise() {
+  hipFuncAttributes fa;
+  return hipFuncGetAttributes(&fa, reinterpret_cast<const void*>(set_u32_kernel));
+}
+
 }  // namespace rf

@@ -219,4 +219,12 @@ hipError_t launch_fill(float* p, float v, uint64_t n, hipStream_t st);
 
 enum { BIN_ADD = 0, BIN_MUL = 1, BIN_SWIGLU = 2 };
 
+// Per-file code-object loads (one per .hip file with kernels), called at
+// context creation so that no capture sees a first-use load.
+hipError_t load_module_attention();
+hipError_t load_module_elementwise();
+hipError_t load_module_matvec();
+hipError_t load_module_packed();
+hipError_t load_module_prefill();
+
 }  // namespace rf

@@ -627,4 +627,11 @@ hipError_t launch_matvec_segments(uint32_t t, const MvSegDesc* segs, int nseg, c
   }
 }
 
+// Loads this file's code object on the current device (HIP defers that to a
+// kernel's first use, which may otherwise fall inside a stream capture).
+hipError_t load_module_matvec() {
+  hipFuncAttributes fa;
+  return hipFuncGetAttributes(&fa, reinterpret_cast<const void*>(matvec_rowwise<T_F32>));
+}
+
 }  // namespace rf

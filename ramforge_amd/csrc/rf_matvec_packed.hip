@@ -1148,4 +1148,11 @@ hipError_t launch_pack(uint32_t t, const void* raw, void* packed, uint64_t rows,
   return hipGetLastError();
 }
 
+// Loads this file's code object on the current device (HIP defers that to a
+// kernel's first use, which may otherwise fall inside a stream capture).
+hipError_t load_module_packed() {
+  hipFuncAttributes fa;
+  return hipFuncGetAttributes(&fa, reinterpret_cast<const void*>(pack_blocks<T_Q8_0>));
+}
+
 }  // namespace rf

@@ -838,4 +838,11 @@ hipError_t launch_rope_kv_rows(const float* q, const float* k, const float* v, c
   return hipGetLastError();
 }
 
+// Loads this file's code object on the current device (HIP defers that to a
+// kernel's first use, which may otherwise fall inside a stream capture).
+hipError_t load_module_prefill() {
+  hipFuncAttributes fa;
+  return hipFuncGetAttributes(&fa, reinterpret_cast<const void*>(mm_reduce));
+}
+
 }  // namespace rf

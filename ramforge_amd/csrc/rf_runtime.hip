@@ -330,6 +330,19 @@ int32_t rf_ctx_create(int32_t device, uint64_t budget, rf_ctx** out) {
     rf_ctx_destroy(c);
     return rc;
   }
+  // Load every kernel file's code object now.  HIP loads one on the first use
+  // of any of its kernels, and a decode step's first use can be inside a
+  // stream capture (rf_model_decode_steps, rf_capture_begin), where the
+  // load's own device allocation and copies are not capturable work.
+  for (hipError_t (*load)() : {load_module_attention, load_module_elementwise, load_module_matvec,
+                               load_module_packed, load_module_prefill}) {
+    e = load();
+    if (e != hipSuccess) {
+      rc = hip_error(e, "loading the kernel code objects");
+      rf_ctx_destroy(c);
+      return rc;
+    }
+  }
   void* p = nullptr;
   rc = vram_alloc(c, "workspace:argmax", 256 * 8 + 64, &p);
   if (rc) {
