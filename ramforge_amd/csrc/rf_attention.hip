@@ -24,8 +24,9 @@
 //     reductions.  For V each lane owns hd/64 dims and each wavefront 16 of
 //     every 64 positions, so the weighted sum needs no cross-lane step; the
 //     four wavefronts are summed through LDS.
-//   * Each chunk writes (o, m, l) of its G heads; a second kernel merges
-//     the chunks with the usual max-rescaling.  (Merging inside the split
+//   * Each chunk writes (o, m, l) of its G heads; a second kernel (one
+//     wavefront per query head) merges the chunks with the usual
+//     max-rescaling.  (Merging inside the split
 //     kernel through arrival counters needs device-scope release fences,
 //     which write back the per-XCD L2 on gfx950 and cost far more than the
 //     second launch.)
@@ -175,9 +176,26 @@ __global__ __launch_bounds__(64 * W) void attn_split(AttnArgs a) {
   constexpr int DPW = HD / 64;
   const float* vb = a.v_hist + (size_t)p0 * kvw + g * HD + lane * DPW;
 
-  // The first batch of K and V rows is requested before anything else, so the
-  // prologue's loads and both passes of a 64-position chunk share one memory
-  // round trip.  Indices are clamped: every load is in bounds.
+  // Loads first: the prologue's operands (q of the G heads, the current k
+  // and v, the cos/sin row), then the first batch of K rows, then of V rows,
+  // all before any is used.  A wavefront's loads complete in order, so the
+  // prologue waits for its own operands only, pass 1 for K and not V, and a
+  // 64-position chunk still takes one memory round trip.  Indices are
+  // clamped: every load is in bounds.  Element t of [q heads..., k, v] is
+  // handled by thread t % NTH.
+  constexpr uint32_t NE = (G + 2) * HD, NP = (NE + NTH - 1) / NTH, HALF = HD / 2;
+  float va[NP], vp[NP], c0[NP], c1[NP];
+#pragma unroll
+  for (uint32_t i = 0; i < NP; ++i) {
+    const uint32_t t = min(tid + i * NTH, NE - 1u), r = t / HD, d = t % HD;
+    const float* src = r < (uint32_t)G ? qz + (size_t)(qg + r) * HD : (r == (uint32_t)G ? kcur_p : vcur_p) + g * HD;
+    const uint32_t ci = d < HALF ? d : d - HALF;
+    va[i] = src[d];
+    vp[i] = src[d < HALF ? d + HALF : d - HALF];
+    c0[i] = cs ? cs[2 * ci] : 1.f;
+    c1[i] = cs ? cs[2 * ci + 1] : 0.f;
+  }
+  __builtin_amdgcn_sched_barrier(0);
   float kv[U][DPL], vv[RV][DPW];
   if (nmain > 0) {
 #pragma unroll
@@ -185,45 +203,31 @@ __global__ __launch_bounds__(64 * W) void attn_split(AttnArgs a) {
       const uint32_t j = min(slot + NSLOT * u, nmain - 1u);
       load_dims(kv[u], kb + (size_t)j * kvw, DPL);
     }
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int k = 0; k < (int)RV; ++k) {
       const uint32_t j = min(wave * RV + k, nmain - 1u);
       load_few<DPW>(vv[k], vb + (size_t)j * kvw);
     }
   }
+  __builtin_amdgcn_sched_barrier(0);
 
-  // Rotated q of the G heads, the current k (rotated) and v, and the slot
-  // write.  Element t of [q heads..., k, v] is handled by thread t % NTH; all
-  // loads are issued before any is used (clamped indices, in bounds).
-  {
-    constexpr uint32_t NE = (G + 2) * HD, NP = (NE + NTH - 1) / NTH, HALF = HD / 2;
-    float va[NP], vp[NP], c0[NP], c1[NP];
+  // Rotated q of the G heads, the current k (rotated) and v, and the slot write.
 #pragma unroll
-    for (uint32_t i = 0; i < NP; ++i) {
-      const uint32_t t = min(tid + i * NTH, NE - 1u), r = t / HD, d = t % HD;
-      const float* src = r < (uint32_t)G ? qz + (size_t)(qg + r) * HD : (r == (uint32_t)G ? kcur_p : vcur_p) + g * HD;
-      const uint32_t ci = d < HALF ? d : d - HALF;
-      va[i] = src[d];
-      vp[i] = src[d < HALF ? d + HALF : d - HALF];
-      c0[i] = cs ? cs[2 * ci] : 1.f;
-      c1[i] = cs ? cs[2 * ci + 1] : 0.f;
-    }
-#pragma unroll
-    for (uint32_t i = 0; i < NP; ++i) {
-      const uint32_t t = tid + i * NTH, r = t / HD, d = t % HD;
-      if (t >= NE) break;
-      // half-split rotation in the RoPE kernel's operation order
-      const float rot = d < HALF ? va[i] * c0[i] - vp[i] * c1[i] : vp[i] * c1[i] + va[i] * c0[i];
-      if (r < (uint32_t)G) {
-        qs[r][d] = cs ? rot : va[i];
-      } else if (r == (uint32_t)G) {
-        const float kv = cs ? rot : va[i];
-        kcur[d] = kv;
-        if (a.k_store && writes_slot) a.k_store[(size_t)hist * kvw + g * HD + d] = kv;
-      } else {
-        vcur[d] = va[i];
-        if (a.v_store && writes_slot) a.v_store[(size_t)hist * kvw + g * HD + d] = va[i];
-      }
+  for (uint32_t i = 0; i < NP; ++i) {
+    const uint32_t t = tid + i * NTH, r = t / HD, d = t % HD;
+    if (t >= NE) break;
+    // half-split rotation in the RoPE kernel's operation order
+    const float rot = d < HALF ? va[i] * c0[i] - vp[i] * c1[i] : vp[i] * c1[i] + va[i] * c0[i];
+    if (r < (uint32_t)G) {
+      qs[r][d] = cs ? rot : va[i];
+    } else if (r == (uint32_t)G) {
+      const float kr = cs ? rot : va[i];
+      kcur[d] = kr;
+      if (a.k_store && writes_slot) a.k_store[(size_t)hist * kvw + g * HD + d] = kr;
+    } else {
+      vcur[d] = va[i];
+      if (a.v_store && writes_slot) a.v_store[(size_t)hist * kvw + g * HD + d] = va[i];
     }
   }
   __syncthreads();
@@ -355,57 +359,73 @@ __global__ __launch_bounds__(64 * W) void attn_split(AttnArgs a) {
   }
 }
 
-// Merge the chunk records (o, m, l) of one query head and 32 of its dims:
-// the factors exp(m_s - M) are computed once per workgroup in parallel over
-// the chunks, then 8 groups of 32 lanes sum disjoint chunk subsets.
-__global__ __launch_bounds__(256) void attn_combine(AttnArgs a) {
+// Merge the chunk records (o, m, l) of one query head: one wavefront per
+// head, lane l owning dims [l DPW, (l + 1) DPW).  The first 32 records (all
+// of them up to 32 chunks) are requested together with the (m, l) pairs,
+// before any arithmetic; the factors exp(m_s - M) go through LDS to every
+// lane.
+template <int DPW>
+__global__ __launch_bounds__(64) void attn_merge(AttnArgs a) {
+  constexpr uint32_t HD = 64u * DPW, B = 32, MPL = ATT_MAX_SPLITS / 64;  // (m, l) pairs per lane
   __shared__ float fac[ATT_MAX_SPLITS];
-  __shared__ float red[8][32];
-  __shared__ float wm[4], wl[4];
-  const uint32_t qhead = blockIdx.x, hd = a.hd, tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+  const uint32_t qhead = blockIdx.x, lane = threadIdx.x;
   const uint32_t z = blockIdx.z;  // token batch: see attn_split
   const uint32_t hist = (a.d_pos ? (uint32_t)(*a.d_pos) : a.hist) + z;
   const uint32_t total = hist + 1;
   const uint32_t chunk = att_chunk(total, a.nsplit);
-  const uint32_t ns = (total + chunk - 1) / chunk;
+  const uint32_t ns = (total + chunk - 1) / chunk;  // 1 < ns <= nsplit <= ATT_MAX_SPLITS
   if (ns == 1) return;
-  const size_t rec = hd + 2, stride = (size_t)a.qh * rec;
+  const size_t rec = HD + 2, stride = (size_t)a.qh * rec;
   const float* base = a.ws + (size_t)z * a.nsplit * stride + (size_t)qhead * rec;
-  const uint32_t dl = tid & 31u, grp = tid >> 5, d = blockIdx.y * 32u + dl;
-  // the first four records of this lane's chunk subset, requested up front
-  float pre[4];
+  float pre[B][DPW];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const uint32_t s = grp + 8u * i;
-    pre[i] = (s < ns && d < hd) ? base[s * stride + d] : 0.f;
-  }
-  const float m_s = tid < ns ? base[tid * stride + hd] : -INFINITY;  // ns <= 256
-  float m = rf_wave_max(m_s);
-  if (lane == 0) wm[wave] = m;
-  __syncthreads();
-  m = fmaxf(fmaxf(wm[0], wm[1]), fmaxf(wm[2], wm[3]));
-  const float f = tid < ns ? expf(m_s - m) : 0.f;
-  fac[tid] = f;
-  float l = rf_wave_sum(tid < ns ? base[tid * stride + hd + 1] * f : 0.f);
-  if (lane == 0) wl[wave] = l;
-  __syncthreads();
-  l = wl[0] + wl[1] + wl[2] + wl[3];
-  float acc = 0.f;
+  for (uint32_t s = 0; s < B; ++s) load_few<DPW>(pre[s], base + (size_t)min(s, ns - 1u) * stride + lane * DPW);
+  float ms[MPL], ls[MPL];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const uint32_t s = grp + 8u * i;
-    if (s < ns) acc = fmaf(fac[s], pre[i], acc);
+  for (uint32_t k = 0; k < MPL; ++k) {
+    const uint32_t s = lane + 64u * k;
+    ms[k] = s < ns ? base[s * stride + HD] : -INFINITY;
+    ls[k] = s < ns ? base[s * stride + HD + 1] : 0.f;
   }
-  if (d < hd)
-    for (uint32_t s = grp + 32u; s < ns; s += 8u) acc = fmaf(fac[s], base[s * stride + d], acc);
-  red[grp][dl] = acc;
-  __syncthreads();
-  if (grp == 0 && d < hd) {
-    float v = 0.f;
+  float m = ms[0];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) v += red[i][dl];
-    a.out[(size_t)z * a.qh * hd + (size_t)qhead * hd + d] = v / l;
+  for (uint32_t k = 1; k < MPL; ++k) m = fmaxf(m, ms[k]);
+  m = rf_wave_max(m);
+  float l = 0.f;
+#pragma unroll
+  for (uint32_t k = 0; k < MPL; ++k) {
+    const uint32_t s = lane + 64u * k;
+    if (s < ns) {
+      const float f = expf(ms[k] - m);
+      fac[s] = f;
+      l = fmaf(ls[k], f, l);
+    }
   }
+  l = rf_wave_sum(l);
+  __syncthreads();  // (one wavefront) the factors are in LDS
+  float acc[DPW];
+#pragma unroll
+  for (int i = 0; i < DPW; ++i) acc[i] = 0.f;
+#pragma unroll
+  for (uint32_t s = 0; s < B; ++s)
+    if (s < ns) {
+#pragma unroll
+      for (int i = 0; i < DPW; ++i) acc[i] = fmaf(fac[s], pre[s][i], acc[i]);
+    }
+  for (uint32_t s0 = B; s0 < ns; s0 += 16u) {
+    float v[16][DPW];
+#pragma unroll
+    for (uint32_t j = 0; j < 16; ++j) load_few<DPW>(v[j], base + (size_t)min(s0 + j, ns - 1u) * stride + lane * DPW);
+#pragma unroll
+    for (uint32_t j = 0; j < 16; ++j)
+      if (s0 + j < ns) {
+#pragma unroll
+        for (int i = 0; i < DPW; ++i) acc[i] = fmaf(fac[s0 + j], v[j][i], acc[i]);
+      }
+  }
+  float* o = a.out + (size_t)z * a.qh * HD + (size_t)qhead * HD + lane * DPW;
+#pragma unroll
+  for (int i = 0; i < DPW; ++i) o[i] = acc[i] / l;
 }
 
 
@@ -603,7 +623,12 @@ hipError_t launch_attention(const AttnArgs& a, hipStream_t st) {
   if (!done) return hipErrorInvalidValue;
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || a.nsplit == 1) return e;
-  hipLaunchKernelGGL(attn_combine, dim3(a.qh, (a.hd + 31) / 32, a.ntok ? a.ntok : 1), dim3(256), 0, st, a);
+  const dim3 mg(a.qh, 1, a.ntok ? a.ntok : 1);
+  switch (a.hd) {
+    case 64: hipLaunchKernelGGL(attn_merge<1>, mg, dim3(64), 0, st, a); break;
+    case 128: hipLaunchKernelGGL(attn_merge<2>, mg, dim3(64), 0, st, a); break;
+    default: hipLaunchKernelGGL(attn_merge<4>, mg, dim3(64), 0, st, a); break;  // 256 (attention_supported)
+  }
   return hipGetLastError();
 }
 
@@ -611,7 +636,7 @@ hipError_t launch_attention(const AttnArgs& a, hipStream_t st) {
 // kernel's first use, which may otherwise fall inside a stream capture).
 hipError_t load_module_attention() {
   hipFuncAttributes fa;
-  return hipFuncGetAttributes(&fa, reinterpret_cast<const void*>(attn_combine));
+  return hipFuncGetAttributes(&fa, reinterpret_cast<const void*>(attn_merge<2>));
 }
 
 }  // namespace rf

@@ -361,9 +361,9 @@ struct PkStep {
 // chunk c (EPL = 16 or 32 elements per slice) is stored at
 // c * 64 * EPL + 256 (4h + i) + 4 l + k.  NB step buffers per wavefront: NB - 1
 // steps are in flight while one is decoded.  ALLF: every step of the
-// wavefront (at most NB tasks of one step each, LPW covering the whole row)
-// is requested before the prologue and none after it, so a launch makes one
-// memory round trip.
+// wavefront (its tasks times the steps of a row at most NB) is requested
+// before the prologue and none after it, so a launch makes one memory round
+// trip.
 template <uint32_t T, int EPI, bool NORM, int U, int LPW, int NB, int NT, bool IX, bool ALLF = false>
 __global__ __launch_bounds__(NT) void matvec_packed(PkArgs a) {
   typedef PkFmt<T> F;
@@ -444,14 +444,6 @@ __global__ __launch_bounds__(NT) void matvec_packed(PkArgs a) {
   auto advance = [&](uint32_t& tt, uint32_t& ss) {
     if (++ss == nstep) { ss = 0; tt += gstride; }
   };
-  // The first NB - 1 steps (ALLF: all NB) are requested before the prologue.
-  uint32_t ct = blockIdx.x * NW + wave, cs = 0, ft = ct, fs = 0;
-#pragma unroll
-  for (int b = 0; b < (ALLF ? NB : NB - 1); ++b) {
-    fetch(buf[b], ft, fs);
-    advance(ft, fs);
-  }
-
   // Prologue, one round of loads and one barrier.  Thread j (then j + NT, ...)
   // owns unit j: 16 consecutive elements of x, unit j % UPS of lane slice
   // j / UPS.  It writes the unit into LDS and the unit's sum.  With NORM,
@@ -484,14 +476,14 @@ __global__ __launch_bounds__(NT) void matvec_packed(PkArgs a) {
     }
     return true;
   };
-  // Float layout: the unit in its permuted LDS slots and its sum.  Returns
-  // false for a non-finite element.
-  auto stage_float = [&](uint32_t j, float& ss, bool sq, bool check) -> bool {
+  // Float layout: unit j (values v, or the zero padding past the row when
+  // !have) in its permuted LDS slots and its sum.  Returns false for a
+  // non-finite element.
+  auto put_float = [&](uint32_t j, const float* v, bool have, bool check) -> bool {
     const uint32_t js = j / UPS, h = j % UPS;
-    float v[16];
     float s = 0.f;
     bool fin = true;
-    if (load_unit(j, v, ss, sq)) {
+    if (have) {
       float* dst = xl + (js >> 6) * 64u * EPL + 4u * h * 256u + 4u * (js & 63u);
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
@@ -505,6 +497,11 @@ __global__ __launch_bounds__(NT) void matvec_packed(PkArgs a) {
     }
     xsum_l[j] = s;
     return fin;
+  };
+  auto stage_float = [&](uint32_t j, float& ss, bool sq, bool check) -> bool {
+    float v[16];
+    const bool have = load_unit(j, v, ss, sq);
+    return put_float(j, v, have, check);
   };
   // Digit layout: with 2^E above the unit's largest |x|, X = rint(x 2^(30 - E))
   // (|X| < 2^30) in balanced base-256 digits X = 2^24 a + 2^16 b + 2^8 c + e
@@ -553,12 +550,60 @@ __global__ __launch_bounds__(NT) void matvec_packed(PkArgs a) {
     return fin;
   };
 
+  // x first: the raw loads of this thread's first unit are issued before
+  // any weight step, so the prologue's wait for them does not also wait for
+  // the codes requested behind them (a wavefront's loads complete in order).
+  float4 xr[4], wr[4];
+  bool xin = false;
+  if constexpr (!IXE) {
+    const uint32_t js = tid / UPS, h = tid % UPS;
+    const uint32_t b = (js >> 6) * 1024u + 16u * (js & 63u);
+    xin = tid < nunit && b < crb;
+    if (xin) {
+      const uint32_t e = F::unit_elem(b, h);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        xr[k] = x4[e / 4u + k];
+        if (NORM) wr[k] = w4[e / 4u + k];
+      }
+    }
+  }
+  // (Loading the first task's residual here too, before the weights, made
+  // the 8B down projection 2.5 us slower.)
+  __builtin_amdgcn_sched_barrier(0);
+  // The first NB - 1 steps (ALLF: all NB) are requested before the prologue.
+  uint32_t ct = blockIdx.x * NW + wave, cs = 0, ft = ct, fs = 0;
+#pragma unroll
+  for (int b = 0; b < (ALLF ? NB : NB - 1); ++b) {
+    fetch(buf[b], ft, fs);
+    advance(ft, fs);
+  }
+
   bool finite = true;
   {
     float ss = 0.f;
     for (uint32_t j = tid; j < nunit; j += NT) {
-      if constexpr (IXE) finite = stage_digits(j, ss) && finite;
-      else finite = stage_float(j, ss, true, KINDS) && finite;
+      if constexpr (IXE) {
+        finite = stage_digits(j, ss) && finite;
+      } else if (j == tid) {  // the unit loaded above (load_unit's arithmetic)
+        float v[16];
+        if (xin) {
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            const float4 xv = xr[k];
+            v[4 * k] = xv.x; v[4 * k + 1] = xv.y; v[4 * k + 2] = xv.z; v[4 * k + 3] = xv.w;
+            if (NORM) {
+              const float4 wv = wr[k];
+              ss = fmaf(xv.x, xv.x, ss); ss = fmaf(xv.y, xv.y, ss);
+              ss = fmaf(xv.z, xv.z, ss); ss = fmaf(xv.w, xv.w, ss);
+              v[4 * k] *= wv.x; v[4 * k + 1] *= wv.y; v[4 * k + 2] *= wv.z; v[4 * k + 3] *= wv.w;
+            }
+          }
+        }
+        finite = put_float(j, v, xin, KINDS) && finite;
+      } else {
+        finite = stage_float(j, ss, true, KINDS) && finite;
+      }
     }
     if (NORM) {
       ss = rf_wave_sum(ss);
@@ -770,7 +815,7 @@ __global__ __launch_bounds__(NT) void matvec_packed(PkArgs a) {
   // check at the top of each step, so every buffer is consumed (its loads
   // waited for) before it is refilled.
   auto run = [&](auto mode) {
-    if constexpr (ALLF) {  // nstep == 1 and at most NB tasks per wavefront (the launch sees to both)
+    if constexpr (ALLF) {  // at most NB steps per wavefront (the launch sees to it)
 #pragma unroll
       for (int b = 0; b < NB; ++b) {
         if (ct >= ntask) return;

@@ -470,6 +470,16 @@ def test_matvec_packed_inflight_shapes(ctx, orc, inflight_mode, t, out_dim, in_d
     _check_matvec_packed(ctx, orc, t, out_dim, in_dim, 2310 + t + out_dim, row_start=7, row_count=out_dim - 20)
 
 
+@pytest.mark.parametrize("inflight_mode", [1, 0], indirect=True, ids=["inflight", "ring"])
+@pytest.mark.parametrize("t", PACKED)
+@pytest.mark.parametrize("out_dim,in_dim", [(4096, 14336), (3000, 14336), (6144, 4096), (8000, 4096)])
+def test_matvec_packed_model_shapes(ctx, orc, inflight_mode, t, out_dim, in_dim):
+    """The 8B down-projection width (14336 inputs: four steps of a row) and
+    Q/K/V-like row counts (several rows per wavefront), both launch modes."""
+    _check_matvec_packed(ctx, orc, t, out_dim, in_dim, 2400 + t + out_dim)
+    _check_matvec_packed(ctx, orc, t, out_dim, in_dim, 2410 + t + out_dim, row_start=5, row_count=out_dim - 9)
+
+
 @pytest.mark.parametrize("t", PACKED)
 def test_matvec_packed_row_range_and_unaligned_x(ctx, orc, t):
     _check_matvec_packed(ctx, orc, t, 300, 4096, 1300 + t, row_start=128, row_count=77)

@@ -138,6 +138,37 @@ def test_tiny_model_digit_modes(ctx, orc, kind, digits):
         rf.tune_matvec_digits(old)
 
 
+@pytest.mark.parametrize("mode", [1, 0], ids=["inflight", "ring"])
+@pytest.mark.parametrize("kind", ["q8", "q4"])
+def test_tiny_model_inflight_modes(ctx, orc, kind, mode):
+    """The whole forward and greedy loop with the one-row-per-wavefront
+    launches (mode 1: residual, RMSNorm and store epilogues) and with the
+    two-step ring everywhere (mode 0)."""
+    rf = _rf()
+    cfg = dict(TINY)
+    types = {"q8": ALL_Q8, "q4": ALL_Q4}[kind]
+    T = _tiny_tensors(np.random.default_rng(950 + mode), cfg, types, bias=True)
+    old = rf.tune_packed_inflight(-1)
+    rf.tune_packed_inflight(mode)
+    print(f"  tiny model {kind}, inflight mode {mode}", flush=True)
+    try:
+        gm = _load_gpu(ctx, cfg, T, 48)
+        om = orc.Model(cfg, T, kv_capacity=48, threads=4)
+        for pos, tok in enumerate([5, 17, 90, 3]):
+            h = gm.forward(tok, pos, want_hidden=True)
+            hr = om.forward(tok, pos)
+            assert np.max(np.abs(h - hr)) <= 2e-4 * max(1.0, np.abs(hr).max()), (kind, pos)
+        gm.reset()
+        om.reset()
+        toks = gm.generate([1, 2, 3, 4], 20)
+        ref, margin = om.generate([1, 2, 3, 4], 20)
+        assert toks == ref, f"greedy divergence (min top-2 margin {margin.min():.3g})"
+        gm.close()
+        om.close()
+    finally:
+        rf.tune_packed_inflight(old)
+
+
 # Q6_K gate/up over an 8448-wide hidden state: x fills 43.5 KB of LDS, the
 # size at which the packed matvec would use 1024-thread workgroups; the Q6_K
 # gate/up kernel stays at 512 (its 1024-thread form spilled to scratch).
