@@ -301,9 +301,32 @@ typedef struct {
  * (model_executor.rs:102-236) per layer, compute_logits
  * (streaming_model.rs:1334-1370) and the greedy loop of
  * InferenceEngine::generate_impl (inference.rs:445-759).  kv_capacity is the
- * KV cache capacity in tokens (<= context_length). */
+ * KV cache capacity in tokens (<= context_length), allocated and charged
+ * ("kv_cache:k", "kv_cache:v") at creation unless rf_model_kv_growth is
+ * used; the attention workspaces and regimes are sized for it either way. */
 int32_t rf_model_create(rf_ctx *ctx, const rf_model_config *cfg, uint64_t kv_capacity, rf_model **out);
 void rf_model_destroy(rf_model *model);
+/* Chunked KV growth (KvCache::GROW_CHUNK_TOKENS and grow_to_with_budget,
+ * kv_cache.rs:49, 297-356, as inference.rs:478-496 and 666-687 use them):
+ * the cache is reallocated to initial_tokens (1..=kv_capacity; only on an
+ * empty cache) and from then on grows whenever a forward, prefill or decode
+ * step needs a position past it, to the next multiple of 256 positions, at
+ * most kv_capacity (rf_model_generate: at most the positions its prompt and
+ * max_tokens need, starting from exactly the prompt's length).  Each growth
+ * charges the replacement "kv_cache:{k,v}:growth" while the old buffers are
+ * still charged, evicting streamed layers first when the budget is short;
+ * on failure (RF_ERR_BUDGET, or the device allocation's error) the cache and
+ * its charges are unchanged.  Growth drops captured decode graphs (they are
+ * captured again at the next step). */
+int32_t rf_model_kv_growth(rf_model *model, uint64_t initial_tokens);
+/* rf_model_create with the KV cache allocated (and charged) for
+ * initial_tokens positions only and growth enabled from the start, as the
+ * reference sizes a new cache for the prompt (KvCache::new_with_budget,
+ * inference.rs:478-496); kv_capacity bounds the growth. */
+int32_t rf_model_create_growing(rf_ctx *ctx, const rf_model_config *cfg, uint64_t kv_capacity,
+                                uint64_t initial_tokens, rf_model **out);
+/* Positions the KV cache holds now (KvCache::capacity_tokens). */
+int32_t rf_model_kv_capacity(rf_model *model, uint64_t *tokens);
 
 /* Installs tensor `name` (GGUF names: token_embd.weight, output_norm.weight,
  * output.weight, blk.{i}.{attn_norm,attn_q,attn_k,attn_v,attn_output,

@@ -27,7 +27,7 @@ from typing import Optional, Sequence
 import numpy as np
 
 from . import _lib
-from ._lib import RF_ALL_ROWS, ModelConfig, RamforgeError
+from ._lib import RF_ALL_ROWS, RF_ERR_BUDGET, RF_ERR_INVALID, ModelConfig, RamforgeError
 
 __all__ = [
     "GGML", "BLOCK_GEOMETRY", "Context", "DeviceArray", "RamforgeError", "ModelConfig",
@@ -529,14 +529,19 @@ def matvec_backend(backend: GpuBackend, td: GpuTensor, x: DeviceArray, y: Device
 class GpuLlamaModel:
     """VRAM-resident dense llama decoder (rf_model_* in the C ABI)."""
 
-    def __init__(self, ctx: Context, cfg: dict, kv_capacity: Optional[int] = None):
+    def __init__(self, ctx: Context, cfg: dict, kv_capacity: Optional[int] = None, kv_initial: Optional[int] = None):
+        """kv_initial: allocate the KV cache for that many positions and grow it
+        in 256-position chunks up to kv_capacity (rf_model_create_growing)."""
         self.ctx = ctx
         self.cfg = dict(cfg)
         c = ModelConfig(**{k: self.cfg[k] for k, _ in ModelConfig._fields_})
         self._c = c
         h = C.c_void_p()
         cap = int(kv_capacity if kv_capacity is not None else cfg["context_length"])
-        _lib.check(ctx.lib.rf_model_create(ctx.handle, C.byref(c), cap, C.byref(h)))
+        if kv_initial is None:
+            _lib.check(ctx.lib.rf_model_create(ctx.handle, C.byref(c), cap, C.byref(h)))
+        else:
+            _lib.check(ctx.lib.rf_model_create_growing(ctx.handle, C.byref(c), cap, int(kv_initial), C.byref(h)))
         self.handle = h
         self.kv_capacity = cap
 
@@ -611,6 +616,17 @@ class GpuLlamaModel:
 
     def use_graph(self, enable: bool) -> None:
         _lib.check(self.ctx.lib.rf_model_use_graph(self.handle, 1 if enable else 0))
+
+    def kv_growth(self, initial_tokens: int) -> None:
+        """Start the (empty) KV cache at initial_tokens positions and grow it in
+        256-position chunks as positions are needed (KvCache::grow_to_with_budget)."""
+        _lib.check(self.ctx.lib.rf_model_kv_growth(self.handle, initial_tokens))
+
+    def kv_positions(self) -> int:
+        """Positions the KV cache holds now (KvCache::capacity_tokens); at most kv_capacity."""
+        n = C.c_uint64()
+        _lib.check(self.ctx.lib.rf_model_kv_capacity(self.handle, C.byref(n)))
+        return n.value
 
     def decode_steps(self, steps: int) -> None:
         _lib.check(self.ctx.lib.rf_model_decode_steps(self.handle, steps))

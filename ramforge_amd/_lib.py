@@ -104,6 +104,7 @@ SIGNATURES = {
     "rf_argmax": (_i32, [_vp, _fp, _u64, _vp, _vp]),
     "rf_synth_blocks": (_i32, [_vp, _u32, _u64, _u64, _u64, _f64, _vp, _u64, _vp]),
     "rf_model_create": (_i32, [_vp, C.POINTER(ModelConfig), _u64, C.POINTER(_vp)]),
+    "rf_model_create_growing": (_i32, [_vp, C.POINTER(ModelConfig), _u64, _u64, C.POINTER(_vp)]),
     "rf_model_destroy": (None, [_vp]),
     "rf_model_set_tensor": (_i32, [_vp, C.c_char_p, _u32, _u64, _u64, _vp, _u64]),
     "rf_model_synth_tensor": (_i32, [_vp, C.c_char_p, _u32, _u64, _u64, _u64, _f64, _f32]),
@@ -117,6 +118,8 @@ SIGNATURES = {
     "rf_model_decode_steps": (_i32, [_vp, _u64]),
     "rf_model_read_tokens": (_i32, [_vp, _vp, _u64]),
     "rf_model_use_graph": (_i32, [_vp, _i32]),
+    "rf_model_kv_growth": (_i32, [_vp, _u64]),
+    "rf_model_kv_capacity": (_i32, [_vp, _vp]),
     "rf_model_time_kernel": (_i32, [_vp, _u32, _u32, C.POINTER(_f32), C.POINTER(_u64), C.POINTER(_u64)]),
     "rf_tune_matvec_tile_bytes": (_u32, [_u32]),
     "rf_tune_matvec_kernel": (_i32, [_i32]),

@@ -71,7 +71,10 @@ using namespace rf;
 struct rf_model {
   rf_ctx* ctx = nullptr;
   rf_model_config cfg{};
-  uint64_t kv_cap = 0;
+  uint64_t kv_cap = 0;    // positions the K/V buffers hold now (their layer stride)
+  uint64_t kv_max = 0;    // capacity the model was created for: bounds growth, sizes workspaces and regimes
+  bool kv_grow = false;   // rf_model_kv_growth: the cache grows in 256-position chunks
+  uint64_t kv_limit = 0;  // growth bound of the running rf_model_generate (prompt + max_tokens); 0: kv_max
   DevTensor token_embd, output_norm, output;
   std::vector<Layer> layers;
   float* k_cache = nullptr;  // [layer][cap][kvh][hd]
@@ -288,6 +291,77 @@ int32_t make_headroom(rf_model* m, uint64_t bytes) {
   while (!vram_can_allocate(m->ctx, bytes)) {
     if (!evict_lru(m, &rc)) return RF_ERR_BUDGET;
     if (rc) return rc;
+  }
+  return RF_OK;
+}
+
+constexpr uint64_t KV_GROW_CHUNK = 256;  // KvCache::GROW_CHUNK_TOKENS (kv_cache.rs:49)
+
+// Reallocate the K/V caches for `target` positions, keeping the committed
+// ones (KvCache::grow_to_with_budget, kv_cache.rs:297-356): the replacement
+// is charged "kv_cache:{k,v}:growth" while the old buffers stay charged (the
+// real peak of the copy), after streamed layers have been evicted to make
+// room for it (ensure_layer_cache_headroom); then the old buffers are freed
+// and the new charges take the old names.  On any failure the cache, its
+// charges and the captured graphs are unchanged.
+int32_t kv_resize(rf_model* m, uint64_t target) {
+  const rf_model_config& c = m->cfg;
+  const uint64_t kvd = c.head_count_kv * c.head_dim, nl = c.block_count;
+  const uint64_t nb = nl * target * kvd * 4;
+  if (m->streaming) {
+    const int32_t rc = make_headroom(m, 2 * nb);
+    if (rc && rc != RF_ERR_BUDGET) return rc;  // a short budget is reported by the allocation below
+  }
+  void *nk = nullptr, *nv = nullptr;
+  int32_t rc = vram_alloc(m->ctx, "kv_cache:k:growth", nb, &nk);
+  if (rc) return rc;
+  rc = vram_alloc(m->ctx, "kv_cache:v:growth", nb, &nv);
+  if (rc) {
+    vram_release(m->ctx, "kv_cache:k:growth");
+    return rc;
+  }
+  hipStream_t st = m->ctx->compute;
+  const uint64_t keep = std::min(m->seq_len, target) * kvd * 4;
+  hipError_t e = hipSuccess;
+  for (uint64_t li = 0; li < nl && keep && e == hipSuccess; ++li) {
+    e = hipMemcpyAsync(static_cast<float*>(nk) + li * target * kvd, m->k_cache + li * m->kv_cap * kvd, keep,
+                       hipMemcpyDeviceToDevice, st);
+    if (e == hipSuccess)
+      e = hipMemcpyAsync(static_cast<float*>(nv) + li * target * kvd, m->v_cache + li * m->kv_cap * kvd, keep,
+                         hipMemcpyDeviceToDevice, st);
+  }
+  if (e == hipSuccess) e = hipStreamSynchronize(st);
+  if (e != hipSuccess) {
+    vram_release(m->ctx, "kv_cache:k:growth");
+    vram_release(m->ctx, "kv_cache:v:growth");
+    return hip_error(e, "KV cache growth copy");
+  }
+  reset_graph(m);  // the graphs hold the old buffers and layer stride
+  vram_release(m->ctx, "kv_cache:k");
+  vram_release(m->ctx, "kv_cache:v");
+  vram_rename_prefix(m->ctx, "kv_cache:k:growth", "kv_cache:k");
+  vram_rename_prefix(m->ctx, "kv_cache:v:growth", "kv_cache:v");
+  m->k_cache = static_cast<float*>(nk);
+  m->v_cache = static_cast<float*>(nv);
+  m->kv_cap = target;
+  return RF_OK;
+}
+
+// Room for `need` positions before they are written: a fixed cache refuses
+// past its capacity; a growing one takes the next multiple of 256 positions,
+// at most the growth bound (inference.rs:666-687).
+int32_t ensure_kv(rf_model* m, uint64_t need) {
+  if (need <= m->kv_cap) return RF_OK;
+  const uint64_t bound = m->kv_limit ? std::min(m->kv_limit, m->kv_max) : m->kv_max;
+  if (!m->kv_grow || need > bound) return set_error(RF_ERR_INVALID, "KV cache full");
+  uint64_t target = (need + KV_GROW_CHUNK - 1) / KV_GROW_CHUNK * KV_GROW_CHUNK;
+  if (target > bound) target = bound;
+  const int32_t rc = kv_resize(m, target);
+  if (rc) {
+    char why[512];
+    rf_last_error(why, sizeof why);
+    return set_error(rc, "failed to grow KV cache from %llu to %llu tokens: %s", (unsigned long long)m->kv_cap,
+                     (unsigned long long)target, why);
   }
   return RF_OK;
 }
@@ -756,7 +830,7 @@ int32_t enqueue_qkv(rf_model* m, size_t li) {
 // a single shape.
 int attn_regime(const rf_model* m, uint64_t pos) {
   if (!m->attn_fast) return 0;
-  return attention_regime(pos + 1, (uint32_t)m->cfg.head_count, (uint32_t)m->cfg.head_count_kv, m->kv_cap);
+  return attention_regime(pos + 1, (uint32_t)m->cfg.head_count, (uint32_t)m->cfg.head_count_kv, m->kv_max);
 }
 
 // 2. RoPE + attention + K/V cache write.
@@ -771,7 +845,7 @@ int32_t enqueue_attention(rf_model* m, size_t li) {
   a.ws = m->attn_ws; a.rope = m->rope; a.k_store = kc; a.v_store = vc; a.d_pos = m->d_pos;
   a.qh = (uint32_t)c.head_count; a.kvh = (uint32_t)c.head_count_kv; a.hd = (uint32_t)hd;
   // the position this step processes picks the shape
-  const AttnShape sh = attention_regime_shape(attn_regime(m, m->seq_len), a.qh, a.kvh, m->kv_cap);
+  const AttnShape sh = attention_regime_shape(attn_regime(m, m->seq_len), a.qh, a.kvh, m->kv_max);
   a.per_q = sh.per_q; a.nsplit = sh.nsplit; a.waves = sh.waves;
   a.denom = sqrtf((float)hd);
   RF_LAUNCH(m->attn_fast ? launch_attention(a, st) : launch_attention_naive(a, st), "attention");
@@ -913,12 +987,12 @@ int32_t forward_token(rf_model* m, uint32_t token, uint64_t pos) {
   if (pos != m->seq_len)
     return set_error(RF_ERR_INVALID, "KV position/history mismatch: position %llu requires cache history %llu, got %llu",
                      (unsigned long long)pos, (unsigned long long)pos, (unsigned long long)m->seq_len);
-  if (m->seq_len >= m->kv_cap) return set_error(RF_ERR_INVALID, "KV cache full");
   if (token >= m->cfg.vocab_size)
     return set_error(RF_ERR_INVALID, "token_id %u out of bounds for embedding with %llu rows", token,
                      (unsigned long long)m->cfg.vocab_size);
   int32_t rc = check_ready(m);
   if (rc) return rc;
+  if ((rc = ensure_kv(m, m->seq_len + 1))) return rc;
   RF_LAUNCH(launch_set_u32(m->d_token, token, m->ctx->compute), "set token");
   rc = enqueue_forward(m);
   if (rc) return rc;
@@ -972,7 +1046,7 @@ int32_t ensure_prefill_ws(rf_model* m) {
   take_max({f, f}, d);
   take_max({f}, d);
   take_max({d}, f);
-  const uint64_t att = T * prefill_attn_splits(m->kv_cap) * c.head_count * (hd + 2);
+  const uint64_t att = T * prefill_attn_splits(m->kv_max) * c.head_count * (hd + 2);
   const uint64_t sizes[] = {T * d, T * d, T * qd, T * kvd, T * kvd, T * qd, T * qd, T * f, T * f, part, att};
   uint64_t total = 0;
   for (uint64_t n : sizes) total += (n + 63) / 64 * 64;
@@ -1073,13 +1147,14 @@ int32_t enqueue_prefill_layer(rf_model* m, size_t li, uint64_t pos0, uint64_t nt
 
 int32_t prefill_tokens(rf_model* m, const uint32_t* tokens, uint64_t n) {
   if (n == 0) return RF_OK;
-  if (n > m->kv_cap - m->seq_len) return set_error(RF_ERR_INVALID, "KV cache full");  // seq_len <= kv_cap
+  if (n > m->kv_max - m->seq_len) return set_error(RF_ERR_INVALID, "KV cache full");  // seq_len <= kv_cap <= kv_max
   for (uint64_t i = 0; i < n; ++i)
     if (tokens[i] >= m->cfg.vocab_size)
       return set_error(RF_ERR_INVALID, "token_id %u out of bounds for embedding with %llu rows", tokens[i],
                        (unsigned long long)m->cfg.vocab_size);
   int32_t rc = check_ready(m);
   if (rc) return rc;
+  if ((rc = ensure_kv(m, m->seq_len + n))) return rc;
   if (!prefill_supported(m)) {
     for (uint64_t i = 0; i < n; ++i)
       if ((rc = forward_token(m, tokens[i], m->seq_len))) return rc;
@@ -1120,7 +1195,28 @@ int32_t prefill_tokens(rf_model* m, const uint32_t* tokens, uint64_t n) {
 
 extern "C" {
 
+namespace {
+int32_t model_create(rf_ctx* ctx, const rf_model_config* cfg, uint64_t kv_cap, uint64_t kv_initial, bool grow,
+                     rf_model** out);
+}
+
 int32_t rf_model_create(rf_ctx* ctx, const rf_model_config* cfg, uint64_t kv_cap, rf_model** out) {
+  return model_create(ctx, cfg, kv_cap, kv_cap, false, out);
+}
+
+int32_t rf_model_create_growing(rf_ctx* ctx, const rf_model_config* cfg, uint64_t kv_capacity, uint64_t initial_tokens,
+                                rf_model** out) {
+  if (initial_tokens == 0 || initial_tokens > kv_capacity)
+    return set_error(RF_ERR_INVALID, "initial KV capacity %llu must be in 1..=%llu", (unsigned long long)initial_tokens,
+                     (unsigned long long)kv_capacity);
+  return model_create(ctx, cfg, kv_capacity, initial_tokens, true, out);
+}
+
+}  // extern "C"
+
+namespace {
+int32_t model_create(rf_ctx* ctx, const rf_model_config* cfg, uint64_t kv_cap, uint64_t kv_initial, bool grow,
+                     rf_model** out) {
   if (!ctx || !cfg || !out) return set_error(RF_ERR_INVALID, "null argument to rf_model_create");
   const rf_model_config& c = *cfg;
   if (c.embedding_length == 0 || c.head_count == 0 || c.head_count_kv == 0 || c.head_dim == 0 || c.vocab_size == 0 ||
@@ -1149,7 +1245,10 @@ int32_t rf_model_create(rf_ctx* ctx, const rf_model_config* cfg, uint64_t kv_cap
   rf_model* m = new rf_model();
   m->ctx = ctx;
   m->cfg = c;
-  m->kv_cap = kv_cap;
+  m->kv_cap = kv_initial;
+  m->kv_max = kv_cap;
+  m->kv_grow = grow;
+  kv_bytes = kv_bytes / kv_cap * kv_initial;  // c.block_count * kv_initial * kvd * 4
   m->layers.resize(c.block_count);
   const uint64_t d = c.embedding_length, qd = c.head_count * c.head_dim, kvd = c.head_count_kv * c.head_dim;
   const uint64_t f = c.feed_forward_length;
@@ -1206,6 +1305,9 @@ int32_t rf_model_create(rf_ctx* ctx, const rf_model_config* cfg, uint64_t kv_cap
   *out = m;
   return RF_OK;
 }
+}  // namespace
+
+extern "C" {
 
 void rf_model_destroy(rf_model* m) {
   if (!m) return;
@@ -1302,6 +1404,20 @@ int32_t rf_model_generate(rf_model* m, const uint32_t* prompt, uint64_t plen, ui
   if (plen > ctx_len || max_tokens > ctx_len - plen)
     return set_error(RF_ERR_INVALID, "prompt (%llu tokens) plus max_tokens (%llu) exceeds context length %llu",
                      (unsigned long long)plen, (unsigned long long)max_tokens, (unsigned long long)ctx_len);
+  // A growing cache starts at the prompt's length and grows by 256-position
+  // chunks up to prompt + max_tokens (inference.rs:478-496, 666-687).
+  struct LimitGuard {
+    rf_model* m;
+    ~LimitGuard() { m->kv_limit = 0; }
+  } guard{m};
+  if (m->kv_grow) {
+    const uint64_t need = m->seq_len + plen;
+    m->kv_limit = std::min(need + max_tokens, m->kv_max);
+    if (need > m->kv_cap && need <= m->kv_limit) {
+      const int32_t rc = kv_resize(m, need);
+      if (rc) return rc;
+    }
+  }
   if (m->prefill_batched) {
     int32_t rc = prefill_tokens(m, prompt, plen);
     if (rc) return rc;
@@ -1338,6 +1454,26 @@ int32_t rf_model_generate(rf_model* m, const uint32_t* prompt, uint64_t plen, ui
   return sync(m);
 }
 
+int32_t rf_model_kv_growth(rf_model* m, uint64_t initial_tokens) {
+  if (!m) return set_error(RF_ERR_INVALID, "null model");
+  if (m->seq_len != 0) return set_error(RF_ERR_INVALID, "KV growth must be enabled on an empty cache (reset first)");
+  if (initial_tokens == 0 || initial_tokens > m->kv_max)
+    return set_error(RF_ERR_INVALID, "initial KV capacity %llu must be in 1..=%llu", (unsigned long long)initial_tokens,
+                     (unsigned long long)m->kv_max);
+  if (initial_tokens != m->kv_cap) {
+    const int32_t rc = kv_resize(m, initial_tokens);
+    if (rc) return rc;
+  }
+  m->kv_grow = true;
+  return RF_OK;
+}
+
+int32_t rf_model_kv_capacity(rf_model* m, uint64_t* tokens) {
+  if (!m || !tokens) return set_error(RF_ERR_INVALID, "null argument");
+  *tokens = m->kv_cap;
+  return RF_OK;
+}
+
 int32_t rf_model_use_graph(rf_model* m, int32_t enable) {
   if (!m) return set_error(RF_ERR_INVALID, "null model");
   if (enable && m->streaming)
@@ -1350,9 +1486,10 @@ int32_t rf_model_use_graph(rf_model* m, int32_t enable) {
 int32_t rf_model_decode_steps(rf_model* m, uint64_t steps) {
   if (!m) return set_error(RF_ERR_INVALID, "null model");
   if (m->seq_len == 0) return set_error(RF_ERR_INVALID, "decode requires a forwarded prompt");
-  if (steps > m->kv_cap - m->seq_len) return set_error(RF_ERR_INVALID, "KV cache full");  // seq_len <= kv_cap
+  if (steps > m->kv_max - m->seq_len) return set_error(RF_ERR_INVALID, "KV cache full");  // seq_len <= kv_cap <= kv_max
   int32_t rc = check_ready(m);
   if (rc) return rc;
+  if ((rc = ensure_kv(m, m->seq_len + steps))) return rc;  // before any graph is captured or replayed
   hipStream_t st = m->ctx->compute;
   for (uint64_t s = 0; s < steps; ++s) {
     const int r = attn_regime(m, m->seq_len);

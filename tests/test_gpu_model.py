@@ -581,3 +581,68 @@ def test_streaming_refuses_graph_and_late_enable(ctx):
         sm.use_graph(True)
     sm.close()
     sctx.close()
+
+
+def _half_tensors(rng, cfg, t, orc):
+    """Tiny-model tensors with every matrix (embedding, output and the seven
+    projections) in F16 or BF16, plus the oracle's view of them: the same
+    values decoded to F32, as the reference decodes F16 / BF16 tensors to f32
+    at load (core/src/tensor.rs:498-521, 967-1014) and multiplies them as f32
+    rows.  F16 payloads include subnormals (quant.rs:40-65 decodes them at
+    half the IEEE value) and signed zeros."""
+    from helpers import BF16, F16
+
+    base = _tiny_tensors(rng, cfg, ALL_F32)
+    T, R = {}, {}
+    for name, (bt, ne0, ne1, arr) in base.items():
+        if name.endswith("norm.weight") or name.endswith(".bias"):
+            T[name] = R[name] = (bt, ne0, ne1, arr)
+            continue
+        v = rng.normal(0, 0.05, ne0 * ne1).astype(np.float32)
+        if t == F16:
+            bits = v.astype(np.float16).view(np.uint16).copy()
+            sub = rng.random(bits.size) < 0.02  # f16 subnormals, either sign
+            bits[sub] = (rng.integers(1, 0x400, sub.sum()) | (rng.integers(0, 2, sub.sum()) << 15)).astype(np.uint16)
+            bits[rng.random(bits.size) < 0.005] = 0x8000
+        else:
+            assert t == BF16
+            bits = (v.view(np.uint32) >> 16).astype(np.uint16)
+        raw = bits.view(np.uint8)
+        T[name] = (t, ne0, ne1, raw)
+        R[name] = (F32, ne0, ne1, orc.dequantize_rows(t, raw, ne0, ne1).reshape(-1))
+    return T, R
+
+
+@pytest.mark.parametrize("streamed", [False, True], ids=["resident", "streamed"])
+@pytest.mark.parametrize("half", ["f16", "bf16"])
+def test_tiny_model_f16_bf16_weights(ctx, orc, half, streamed):
+    """F16 / BF16 weights widened to F32 at install (on the device when
+    resident, on the host when the layers stream), against the oracle running
+    the f32 values the reference decodes at load: hidden states and logits
+    within 2e-4, identical greedy tokens."""
+    from helpers import BF16, F16
+
+    t = {"f16": F16, "bf16": BF16}[half]
+    cfg = dict(TINY)
+    T, R = _half_tensors(np.random.default_rng(970 + t), cfg, t, orc)
+    print(f"  tiny model {half} weights, {'streamed' if streamed else 'resident'}", flush=True)
+    if streamed:
+        sctx, gm = _streaming_model(cfg, T, 0, 1 << 30, cap=48)
+    else:
+        sctx, gm = None, _load_gpu(ctx, cfg, T, 48)
+    om = orc.Model(cfg, R, kv_capacity=48, threads=4)
+    for pos, tok in enumerate([5, 17, 90, 3]):
+        h = gm.forward(tok, pos, want_hidden=True)
+        hr = om.forward(tok, pos)
+        assert np.max(np.abs(h - hr)) <= 2e-4 * max(1.0, np.abs(hr).max()), (half, pos)
+        lr = om.logits(hr)
+        assert np.max(np.abs(gm.logits() - lr)) <= 2e-4 * max(1.0, np.abs(lr).max()), (half, pos)
+    gm.reset()
+    om.reset()
+    toks = gm.generate([1, 2, 3, 4], 20)
+    ref, margin = om.generate([1, 2, 3, 4], 20)
+    assert toks == ref, f"greedy divergence (min top-2 margin {margin.min():.3g})"
+    gm.close()
+    om.close()
+    if sctx is not None:
+        sctx.close()
