@@ -50,6 +50,7 @@ extern "C" {
 #define RF_ERR_BUDGET 2      /* VRAM ledger refused a charge (MemoryError)     */
 #define RF_ERR_HIP 3         /* HIP runtime failure                            */
 #define RF_ERR_UNSUPPORTED 4 /* type or shape outside what the kernels cover   */
+#define RF_ERR_IO 5          /* a byte source's read failed (DataSourceError)  */
 
 /* ggml type ids: core/src/types.rs:238-292 (GgmlType::from_u32). */
 #define RF_TYPE_F32 0u
@@ -403,6 +404,32 @@ int32_t rf_model_set_cache_policy(rf_model *model, int32_t policy);
 /* out[6]: cache hits, misses (layer uploads), evictions, bytes uploaded,
  * bytes and layers currently cached. */
 int32_t rf_model_residency_stats(rf_model *model, uint64_t *out);
+
+/* Reads `length` bytes at `offset` of a model's byte source (its GGUF file or
+ * the virtual concatenation of its shards: DataSource::read_range_into,
+ * core/src/datasource.rs:574-700) into dst; returns 0 on success, any other
+ * value is reported as RF_ERR_IO. */
+typedef int32_t (*rf_read_fn)(void *user, uint64_t offset, uint64_t length, void *dst);
+/* Streamed layers read from a byte source instead of pinned host copies
+ * (the device side of load_layer's reads, streaming_model.rs:581-847): only
+ * with layer streaming enabled and before any rf_model_set_tensor_source.
+ * Two pinned staging buffers of staging_bytes each (>= 4096) are the host
+ * memory the reads use; `read` is called on the thread that runs the forward
+ * pass, one range at a time. */
+int32_t rf_model_set_reader(rf_model *model, rf_read_fn read, void *user, uint64_t staging_bytes);
+/* Declares block tensor `name` (blk.*) at [offset, offset + nbytes) of the
+ * byte source; nothing is read now.  Each load of its layer reads the layer's
+ * tensors as ranges merged while the gaps are at most 4 KiB and the span fits
+ * a staging buffer (build_layer_read_plan, layer_read.rs:6-160; a tensor
+ * larger than a buffer is read in buffer-sized pieces), copies them to the
+ * layer's device buffers and repacks (packed projections) or widens
+ * (F16 / BF16) them on the device through a raw buffer charged
+ * "workspace:layer_read", sized at declaration for the largest such tensor.
+ * A failed read releases every charge the load made (RF_ERR_IO). */
+int32_t rf_model_set_tensor_source(rf_model *model, const char *name, uint32_t ggml_type, uint64_t ne0,
+                                   uint64_t ne1, uint64_t offset, uint64_t nbytes);
+/* out[2]: reader calls and bytes read from the byte source. */
+int32_t rf_model_read_stats(rf_model *model, uint64_t *out);
 
 /* Launch groups of one decode step (see rf_model_time_kernel). */
 #define RF_KERNEL_QKV 1       /* attn RMSNorm + Q/K/V matvec (+ bias)      */

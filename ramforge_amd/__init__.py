@@ -21,13 +21,14 @@ passes device pointers.
 from __future__ import annotations
 
 import ctypes as C
+import os
 from dataclasses import dataclass
 from typing import Optional, Sequence
 
 import numpy as np
 
 from . import _lib
-from ._lib import RF_ALL_ROWS, RF_ERR_BUDGET, RF_ERR_INVALID, ModelConfig, RamforgeError
+from ._lib import RF_ALL_ROWS, RF_ERR_BUDGET, RF_ERR_INVALID, RF_ERR_IO, ModelConfig, RamforgeError
 
 __all__ = [
     "GGML", "BLOCK_GEOMETRY", "Context", "DeviceArray", "RamforgeError", "ModelConfig",
@@ -526,6 +527,50 @@ def matvec_backend(backend: GpuBackend, td: GpuTensor, x: DeviceArray, y: Device
 
 # ------------------------------------------------------------------- model
 
+class ByteSource:
+    """Byte source for streamed layers (rf_read_fn): a file read with
+    os.preadv straight into the pinned staging buffer, or an in-memory buffer.
+    ``fail_at`` (an offset) makes reads that cover it fail, for tests of the
+    error path."""
+
+    def __init__(self, path_or_buffer):
+        self.fd = None
+        self.buf = None
+        if isinstance(path_or_buffer, (str, os.PathLike)):
+            self.fd = os.open(path_or_buffer, os.O_RDONLY)
+        else:
+            self.buf = np.frombuffer(path_or_buffer, np.uint8)
+        self.fail_at = None
+        self.calls = 0
+        self.callback = _lib.READ_FN(self._read)
+
+    def _read(self, _user, offset, length, dst):
+        self.calls += 1
+        try:
+            if self.fail_at is not None and offset <= self.fail_at < offset + length:
+                return 5
+            if self.buf is not None:
+                if offset + length > self.buf.size:
+                    return 1
+                C.memmove(dst, self.buf.ctypes.data + offset, length)
+                return 0
+            view = memoryview((C.c_char * length).from_address(dst)).cast("B")
+            got = 0
+            while got < length:
+                n = os.preadv(self.fd, [view[got:]], offset + got)
+                if n <= 0:
+                    return 2
+                got += n
+            return 0
+        except Exception:  # reported to the library as a failed read
+            return 3
+
+    def close(self) -> None:
+        if self.fd is not None:
+            os.close(self.fd)
+            self.fd = None
+
+
 class GpuLlamaModel:
     """VRAM-resident dense llama decoder (rf_model_* in the C ABI)."""
 
@@ -558,6 +603,22 @@ class GpuLlamaModel:
     def set_cache_policy(self, policy: int) -> None:
         """0: least recently used (reference LayerCache); 1: next use in the layer cycle."""
         _lib.check(self.ctx.lib.rf_model_set_cache_policy(self.handle, policy))
+
+    def set_reader(self, source: "ByteSource", staging_bytes: int = 64 << 20) -> None:
+        """Streamed layers read their declared tensors from `source`
+        (rf_model_set_reader); call after enable_streaming."""
+        self._source = source  # keeps the callback alive
+        _lib.check(self.ctx.lib.rf_model_set_reader(self.handle, source.callback, None, int(staging_bytes)))
+
+    def set_tensor_source(self, name: str, ggml_type: int, ne0: int, ne1: int, offset: int, nbytes: int) -> None:
+        """Declare block tensor `name` at [offset, offset + nbytes) of the byte source."""
+        _lib.check(self.ctx.lib.rf_model_set_tensor_source(self.handle, name.encode(), ggml_type, ne0, ne1,
+                                                           int(offset), int(nbytes)))
+
+    def read_stats(self) -> dict:
+        out = (C.c_uint64 * 2)()
+        _lib.check(self.ctx.lib.rf_model_read_stats(self.handle, out))
+        return {"calls": int(out[0]), "bytes": int(out[1])}
 
     def residency_stats(self) -> dict:
         out = (C.c_uint64 * 6)()

@@ -25,6 +25,8 @@ class RamforgeError(RuntimeError):
 RF_OK = 0
 RF_ERR_INVALID = 1
 RF_ERR_BUDGET = 2
+RF_ERR_IO = 5
+READ_FN = C.CFUNCTYPE(C.c_int32, C.c_void_p, C.c_uint64, C.c_uint64, C.c_void_p)
 RF_ERR_HIP = 3
 RF_ERR_UNSUPPORTED = 4
 RF_ALL_ROWS = 0xFFFFFFFFFFFFFFFF
@@ -119,6 +121,9 @@ SIGNATURES = {
     "rf_model_read_tokens": (_i32, [_vp, _vp, _u64]),
     "rf_model_use_graph": (_i32, [_vp, _i32]),
     "rf_model_kv_growth": (_i32, [_vp, _u64]),
+    "rf_model_set_reader": (_i32, [_vp, READ_FN, _vp, _u64]),
+    "rf_model_set_tensor_source": (_i32, [_vp, C.c_char_p, _u32, _u64, _u64, _u64, _u64]),
+    "rf_model_read_stats": (_i32, [_vp, _vp]),
     "rf_model_kv_capacity": (_i32, [_vp, _vp]),
     "rf_model_time_kernel": (_i32, [_vp, _u32, _u32, C.POINTER(_f32), C.POINTER(_u64), C.POINTER(_u64)]),
     "rf_tune_matvec_tile_bytes": (_u32, [_u32]),

@@ -41,7 +41,13 @@ struct DevTensor {
   std::string charge;
   bool packed = false;  // device-native layout (rf_matvec_packed.hip), else GGUF bytes
   void* host = nullptr;  // streamed layers: pinned host copy in device layout (d set while resident)
-  bool present() const { return d != nullptr || host != nullptr; }
+  // Streamed layers read from the model's byte source (rf_model_set_tensor_source):
+  // the GGUF type and byte range of the tensor, converted on the device at each load.
+  bool src = false;
+  uint32_t src_type = 0;
+  uint64_t src_off = 0, src_bytes = 0;
+  bool streamed() const { return host != nullptr || src; }
+  bool present() const { return d != nullptr || streamed(); }
 };
 
 // Residency of one streamed layer (device side of load_layer / LayerCache,
@@ -113,6 +119,17 @@ struct rf_model {
   uint64_t st_hits = 0, st_misses = 0, st_evictions = 0, st_uploaded = 0;
   int cache_policy = 0;    // 0: LRU (LayerCache); 1: next use within the layer cycle
   uint32_t cur_layer = 0;  // layer the forward pass is at (policy 1)
+  // Byte source of streamed layers (rf_model_set_reader): ranges are read into
+  // two pinned staging buffers of stage_bytes each and converted on the device
+  // through a raw buffer charged "workspace:layer_read" (grown on demand).
+  rf_read_fn reader = nullptr;
+  void* reader_user = nullptr;
+  void* rstage[2] = {nullptr, nullptr};
+  hipEvent_t rstage_ev[2] = {nullptr, nullptr};
+  uint64_t rstage_bytes = 0;
+  void* rraw = nullptr;
+  uint64_t rraw_bytes = 0;
+  uint64_t st_read_calls = 0, st_read_bytes = 0;
 };
 
 namespace {
@@ -214,7 +231,7 @@ void update_layer_bytes(rf_model* m, uint32_t li) {
   layer_slots(m->layers[li], t);
   uint64_t b = 0;
   for (DevTensor* x : t)
-    if (x->host) b += x->nbytes;
+    if (x->streamed()) b += x->nbytes;
   m->res[li].bytes = b;
 }
 
@@ -366,6 +383,116 @@ int32_t ensure_kv(rf_model* m, uint64_t need) {
   return RF_OK;
 }
 
+constexpr uint64_t READ_GAP_BYTES = 4096;  // MAX_COALESCED_GAP_BYTES (layer_read.rs:6)
+
+// The layer's source tensors as read ranges (build_layer_read_plan,
+// layer_read.rs:51-160): sorted by offset and merged while the gap to the
+// next tensor is at most 4 KiB and the merged span fits one staging buffer
+// (the reference's bound is 64 MiB); a tensor larger than a buffer is a range
+// of its own, read in buffer-sized pieces.
+struct ReadRange {
+  uint64_t off = 0, len = 0;
+  std::vector<int> slots;
+};
+int32_t plan_layer_reads(rf_model* m, DevTensor* t[12], std::vector<ReadRange>* out) {
+  std::vector<int> idx;
+  for (int i = 0; i < 12; ++i)
+    if (t[i]->src) idx.push_back(i);
+  std::stable_sort(idx.begin(), idx.end(), [&](int a, int b) { return t[a]->src_off < t[b]->src_off; });
+  std::vector<ReadRange>& r = *out;
+  for (int i : idx) {
+    const uint64_t off = t[i]->src_off, end = off + t[i]->src_bytes;
+    if (!r.empty()) {
+      ReadRange& c = r.back();
+      const uint64_t cend = c.off + c.len;
+      if (off < cend) return set_error(RF_ERR_INVALID, "tensor ranges overlap at '%s'", slot_name(i));
+      if (off - cend <= READ_GAP_BYTES && end - c.off <= m->rstage_bytes) {
+        c.len = end - c.off;
+        c.slots.push_back(i);
+        continue;
+      }
+    }
+    ReadRange n;
+    n.off = off;
+    n.len = end - off;
+    n.slots.push_back(i);
+    r.push_back(n);
+  }
+  return RF_OK;
+}
+
+// Reads the layer's source tensors range by range into the pinned staging
+// buffers (alternating, each reused once the copy out of it has finished),
+// copies every tensor to its device buffer, or to the raw buffer and then
+// packs or widens it into its device buffer, all on the copy stream.
+int32_t read_layer_sources(rf_model* m, uint32_t li, DevTensor* t[12], hipStream_t cs) {
+  std::vector<ReadRange> plan;
+  int32_t rc = plan_layer_reads(m, t, &plan);
+  if (rc) return rc;
+  int buf = 0;
+  auto fill = [&](uint64_t off, uint64_t len) -> int32_t {  // one reader call into the next staging buffer
+    hipError_t e = hipEventSynchronize(m->rstage_ev[buf]);
+    if (e != hipSuccess) return hip_error(e, "staging buffer wait");
+    const int32_t r = m->reader(m->reader_user, off, len, m->rstage[buf]);
+    m->st_read_calls += 1;
+    if (r != 0)
+      return set_error(RF_ERR_IO, "byte source read of %llu bytes at offset %llu failed (%d) for layer %u",
+                       (unsigned long long)len, (unsigned long long)off, (int)r, li);
+    m->st_read_bytes += len;
+    return RF_OK;
+  };
+  auto convert = [&](DevTensor* x) -> hipError_t {  // raw buffer -> device layout
+    if (x->type == T_F32 && x->src_type != T_F32)
+      return launch_dequant_rows(x->src_type, m->rraw, x->ne0, x->ne1, static_cast<float*>(x->d), nullptr, 0, cs);
+    return launch_pack(x->src_type, m->rraw, x->d, x->ne1, x->ne0, cs);
+  };
+  auto needs_convert = [](const DevTensor* x) { return x->packed || (x->type == T_F32 && x->src_type != T_F32); };
+  for (const ReadRange& r : plan) {
+    if (r.len <= m->rstage_bytes) {
+      if ((rc = fill(r.off, r.len))) return rc;
+      for (int i : r.slots) {
+        DevTensor* x = t[i];
+        const bool cv = needs_convert(x);
+        hipError_t e = hipMemcpyAsync(cv ? m->rraw : x->d, static_cast<uint8_t*>(m->rstage[buf]) + (x->src_off - r.off),
+                                      x->src_bytes, hipMemcpyHostToDevice, cs);
+        if (e == hipSuccess && cv) e = convert(x);
+        if (e != hipSuccess) return hip_error(e, "layer upload");
+        m->st_uploaded += x->src_bytes;
+      }
+      hipError_t e = hipEventRecord(m->rstage_ev[buf], cs);
+      if (e != hipSuccess) return hip_error(e, "hipEventRecord");
+      buf ^= 1;
+      continue;
+    }
+    DevTensor* x = t[r.slots[0]];  // one tensor larger than a staging buffer
+    const bool cv = needs_convert(x);
+    uint8_t* dst = static_cast<uint8_t*>(cv ? m->rraw : x->d);
+    for (uint64_t p = 0; p < r.len; p += m->rstage_bytes) {
+      const uint64_t n = std::min(m->rstage_bytes, r.len - p);
+      if ((rc = fill(r.off + p, n))) return rc;
+      hipError_t e = hipMemcpyAsync(dst + p, m->rstage[buf], n, hipMemcpyHostToDevice, cs);
+      if (e == hipSuccess) e = hipEventRecord(m->rstage_ev[buf], cs);
+      if (e != hipSuccess) return hip_error(e, "layer upload");
+      buf ^= 1;
+    }
+    if (cv) {
+      const hipError_t e = convert(x);
+      if (e != hipSuccess) return hip_error(e, "layer conversion");
+    }
+    m->st_uploaded += x->src_bytes;
+  }
+  return RF_OK;
+}
+
+// A streamed pass that fails part-way releases every layer it loaded and did
+// not cache (the reference releases each computed layer before the next, so
+// its budget is back where it was), leaving cached layers cached.  Returns rc.
+int32_t abort_pass(rf_model* m, int32_t rc) {
+  for (uint32_t li = 0; li < m->res.size(); ++li)
+    if (m->res[li].state == LAYER_ACTIVE || m->res[li].state == LAYER_RETIRED) (void)layer_free(m, li);
+  return rc;
+}
+
 // load_layer (streaming_model.rs:581-847) on the device: every tensor is
 // charged "layer:{i}:{name}" before its buffer is allocated, then uploaded
 // from the pinned host copy on the copy stream.  On failure every charge made
@@ -383,31 +510,35 @@ int32_t load_layer(rf_model* m, uint32_t li) {
   DevTensor* t[12];
   layer_slots(m->layers[li], t);
   hipStream_t cs = m->ctx->copy;
+  auto rollback = [&](int32_t code) {  // release every charge of this layer
+    hipStreamSynchronize(cs);
+    for (DevTensor* y : t)
+      if (y->d) {
+        vram_release(m->ctx, y->charge);
+        y->d = nullptr;
+        y->charge.clear();
+      }
+    return code;
+  };
+  bool sourced = false;
   for (int i = 0; i < 12; ++i) {
     DevTensor* x = t[i];
-    if (!x->host) continue;
+    if (!x->streamed()) continue;
     const std::string charge = "layer:" + std::to_string(li) + ":" + slot_name(i);
     void* d = nullptr;
     rc = vram_alloc(m->ctx, charge, x->nbytes, &d);
-    hipError_t e = hipSuccess;
-    if (rc == RF_OK) {
-      x->d = d;
-      x->charge = charge;
-      e = hipMemcpyAsync(d, x->host, x->nbytes, hipMemcpyHostToDevice, cs);
-      if (e != hipSuccess) rc = hip_error(e, "layer upload");
+    if (rc) return rollback(rc);
+    x->d = d;
+    x->charge = charge;
+    if (x->src) {
+      sourced = true;
+      continue;
     }
-    if (rc) {  // roll back every charge of this layer
-      hipStreamSynchronize(cs);
-      for (DevTensor* y : t)
-        if (y->d) {
-          vram_release(m->ctx, y->charge);
-          y->d = nullptr;
-          y->charge.clear();
-        }
-      return rc;
-    }
+    const hipError_t e = hipMemcpyAsync(d, x->host, x->nbytes, hipMemcpyHostToDevice, cs);
+    if (e != hipSuccess) return rollback(hip_error(e, "layer upload"));
     m->st_uploaded += x->nbytes;
   }
+  if (sourced && (rc = read_layer_sources(m, li, t, cs))) return rollback(rc);
   hipError_t e = hipEventRecord(R.uploaded, cs);
   if (e == hipSuccess) e = hipEventRecord(R.used, m->ctx->compute);  // not in use yet
   if (e != hipSuccess) return hip_error(e, "hipEventRecord");
@@ -603,6 +734,7 @@ int32_t install_streamed(rf_model* m, const std::string& name, DevTensor* slot, 
     return rc;
   }
   if (slot->host) hipHostFree(slot->host);
+  slot->src = false;
   slot->type = widen ? T_F32 : t;
   slot->ne0 = ne0;
   slot->ne1 = ne1;
@@ -940,12 +1072,12 @@ int32_t enqueue_forward(rf_model* m, bool embed = true) {
     if (m->streaming) {
       // this layer resident (hit or load), the next one's upload started so it
       // overlaps this layer's kernels, then the kernels wait for the upload
-      if ((rc = acquire_layer(m, li, false))) return rc;
-      if (li + 1 < nl && (rc = acquire_layer(m, li + 1, true))) return rc;
+      if ((rc = acquire_layer(m, li, false))) return abort_pass(m, rc);
+      if (li + 1 < nl && (rc = acquire_layer(m, li + 1, true))) return abort_pass(m, rc);
       RF_LAUNCH(hipStreamWaitEvent(st, m->res[li].uploaded, 0), "wait for layer upload");
     }
-    if ((rc = enqueue_layer(m, li, li + 1 == nl ? m->d_pos : nullptr))) return rc;
-    if (m->streaming && (rc = settle_layer(m, li))) return rc;
+    if ((rc = enqueue_layer(m, li, li + 1 == nl ? m->d_pos : nullptr))) return m->streaming ? abort_pass(m, rc) : rc;
+    if (m->streaming && (rc = settle_layer(m, li))) return abort_pass(m, rc);
   }
   if (m->streaming) {
     int32_t rc = release_retired(m);  // release_layer for layers the cache did not take
@@ -1175,12 +1307,12 @@ int32_t prefill_tokens(rf_model* m, const uint32_t* tokens, uint64_t n) {
     for (uint32_t li = 0; li < nl; ++li) {
       m->cur_layer = li;
       if (m->streaming) {  // as enqueue_forward: this layer resident, the next one's upload started
-        if ((rc = acquire_layer(m, li, false))) return rc;
-        if (li + 1 < nl && (rc = acquire_layer(m, li + 1, true))) return rc;
+        if ((rc = acquire_layer(m, li, false))) return abort_pass(m, rc);
+        if (li + 1 < nl && (rc = acquire_layer(m, li + 1, true))) return abort_pass(m, rc);
         RF_LAUNCH(hipStreamWaitEvent(st, m->res[li].uploaded, 0), "wait for layer upload");
       }
-      if ((rc = enqueue_prefill_layer(m, li, pos0, nt))) return rc;
-      if (m->streaming && (rc = settle_layer(m, li))) return rc;
+      if ((rc = enqueue_prefill_layer(m, li, pos0, nt))) return m->streaming ? abort_pass(m, rc) : rc;
+      if (m->streaming && (rc = settle_layer(m, li))) return abort_pass(m, rc);
     }
     if (m->streaming && (rc = release_retired(m))) return rc;
     m->seq_len += nt;
@@ -1324,6 +1456,10 @@ void rf_model_destroy(rf_model* m) {
     if (m->res[li].used) hipEventDestroy(m->res[li].used);
   }
   for (auto it = m->charges.rbegin(); it != m->charges.rend(); ++it) vram_release(m->ctx, *it);
+  for (int i = 0; i < 2; ++i) {
+    if (m->rstage[i]) hipHostFree(m->rstage[i]);
+    if (m->rstage_ev[i]) hipEventDestroy(m->rstage_ev[i]);
+  }
   delete m;
 }
 
@@ -1597,6 +1733,103 @@ int32_t rf_model_enable_streaming(rf_model* m, uint64_t layer_cache_bytes) {
   m->cache_cap = layer_cache_bytes;
   m->use_graph = false;
   reset_graph(m);
+  return RF_OK;
+}
+
+int32_t rf_model_set_reader(rf_model* m, rf_read_fn read, void* user, uint64_t staging_bytes) {
+  if (!m || !read) return set_error(RF_ERR_INVALID, "null model or reader");
+  if (!m->streaming) return set_error(RF_ERR_INVALID, "a byte source needs layer streaming (rf_model_enable_streaming)");
+  if (staging_bytes < 4096) return set_error(RF_ERR_INVALID, "staging buffers of %llu bytes (at least 4096)",
+                                             (unsigned long long)staging_bytes);
+  for (Layer& L : m->layers) {
+    DevTensor* t[12];
+    layer_slots(L, t);
+    for (DevTensor* x : t)
+      if (x->src) return set_error(RF_ERR_INVALID, "the byte source must be set before source tensors are declared");
+  }
+  void* b[2] = {nullptr, nullptr};
+  hipEvent_t ev[2] = {nullptr, nullptr};
+  hipError_t e = hipSuccess;
+  for (int i = 0; i < 2 && e == hipSuccess; ++i) {
+    e = hipHostMalloc(&b[i], staging_bytes, hipHostMallocDefault);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&ev[i], hipEventDisableTiming);
+  }
+  if (e != hipSuccess) {
+    for (int i = 0; i < 2; ++i) {
+      if (b[i]) hipHostFree(b[i]);
+      if (ev[i]) hipEventDestroy(ev[i]);
+    }
+    return hip_error(e, "staging buffers");
+  }
+  for (int i = 0; i < 2; ++i) {
+    if (m->rstage[i]) hipHostFree(m->rstage[i]);
+    if (m->rstage_ev[i]) hipEventDestroy(m->rstage_ev[i]);
+    m->rstage[i] = b[i];
+    m->rstage_ev[i] = ev[i];
+  }
+  m->rstage_bytes = staging_bytes;
+  m->reader = read;
+  m->reader_user = user;
+  return RF_OK;
+}
+
+int32_t rf_model_set_tensor_source(rf_model* m, const char* cname, uint32_t t, uint64_t ne0, uint64_t ne1,
+                                   uint64_t offset, uint64_t nbytes) {
+  if (!m || !cname) return set_error(RF_ERR_INVALID, "null model or tensor name");
+  if (!m->reader) return set_error(RF_ERR_INVALID, "no byte source (rf_model_set_reader)");
+  const std::string name(cname);
+  unsigned li = 0;
+  if (name.rfind("blk.", 0) != 0 || sscanf(name.c_str(), "blk.%u.", &li) != 1 || li >= m->layers.size())
+    return set_error(RF_ERR_INVALID, "only block tensors stream from the byte source, got '%s'", name.c_str());
+  DevTensor* slot = nullptr;
+  uint64_t e0 = 0, e1 = 0, bytes = 0;
+  std::string charge;
+  int32_t rc = resolve(m, name, &slot, &e0, &e1, &charge);
+  if (rc) return rc;
+  rc = check_tensor_shape(m, name, t, ne0, ne1, e0, e1, &bytes);
+  if (rc) return rc;
+  if (nbytes != bytes)
+    return set_error(RF_ERR_INVALID, "tensor '%s' spans %llu bytes, its shape needs %llu", name.c_str(),
+                     (unsigned long long)nbytes, (unsigned long long)bytes);
+  if (offset + nbytes < offset) return set_error(RF_ERR_INVALID, "tensor '%s' range overflows", name.c_str());
+  const bool widen = (t == T_F16 || t == T_BF16);
+  const bool pack = g_pack_weights && is_projection(name) && plan_packed(t, ne0).ok;
+  if ((widen || pack) && bytes > m->rraw_bytes) {  // the raw buffer holds the largest converted tensor
+    hipError_t e = hipStreamSynchronize(m->ctx->copy);
+    if (e != hipSuccess) return hip_error(e, "hipStreamSynchronize");
+    void* d = nullptr;
+    rc = vram_alloc(m->ctx, "workspace:layer_read:new", bytes, &d);
+    if (rc) return rc;
+    if (m->rraw) release_charge(m, "workspace:layer_read");
+    vram_rename_prefix(m->ctx, "workspace:layer_read:new", "workspace:layer_read");
+    m->charges.push_back("workspace:layer_read");
+    m->rraw = d;
+    m->rraw_bytes = bytes;
+  }
+  reset_graph(m);
+  rc = layer_free(m, li);  // a resident copy of the layer is stale now
+  if (rc) return rc;
+  if (slot->host) hipHostFree(slot->host);
+  slot->host = nullptr;
+  slot->d = nullptr;
+  slot->charge.clear();
+  slot->type = widen ? T_F32 : t;
+  slot->ne0 = ne0;
+  slot->ne1 = ne1;
+  slot->nbytes = widen ? ne0 * ne1 * 4 : bytes;
+  slot->packed = pack;
+  slot->src = true;
+  slot->src_type = t;
+  slot->src_off = offset;
+  slot->src_bytes = bytes;
+  update_layer_bytes(m, li);
+  return RF_OK;
+}
+
+int32_t rf_model_read_stats(rf_model* m, uint64_t* out) {
+  if (!m || !out) return set_error(RF_ERR_INVALID, "null argument");
+  out[0] = m->st_read_calls;
+  out[1] = m->st_read_bytes;
   return RF_OK;
 }
 

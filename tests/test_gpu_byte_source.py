@@ -1,0 +1,154 @@
+"""Streamed layers read from a byte source by layer ranges (the device side
+of load_layer's reads, streaming_model.rs:581-847, with the read plan of
+layer_read.rs:6-160): a tiny model laid out as a GGUF-like file (tensors
+32-byte aligned, layer by layer, with small gaps) gives the same hidden
+states and tokens as the pinned-host streaming tier and the oracle; merged
+ranges make one read per layer load; tensors larger than a staging buffer
+are read in pieces; a failed read releases every charge of the load."""
+import os
+
+import numpy as np
+import pytest
+
+from helpers import BF16, F16
+from test_gpu_model import STREAM_CFG, STREAM_TYPES, _half_tensors, _tiny_tensors
+
+pytestmark = pytest.mark.gpu
+
+
+def _rf():
+    import ramforge_amd as rf
+
+    return rf
+
+
+def _layout(T, gap=16):
+    """File image: non-block tensors first, then each layer's tensors in GGUF
+    order, each start aligned to 32 bytes with `gap` spare bytes between."""
+    names = [n for n in T if not n.startswith("blk.")] + [n for n in T if n.startswith("blk.")]
+    off, spans = 0, {}
+    for n in names:
+        off = (off + 31) // 32 * 32
+        nb = np.asarray(T[n][3]).nbytes
+        spans[n] = (off, nb)
+        off += nb + gap
+    blob = np.full(off, 0xA5, np.uint8)  # filler where no tensor lies
+    for n, (o, nb) in spans.items():
+        blob[o:o + nb] = np.frombuffer(np.ascontiguousarray(T[n][3]).tobytes(), np.uint8)
+    return blob, spans
+
+
+def _sourced_model(ctx, cfg, T, source, staging, cache_bytes=1 << 30, cap=40):
+    rf = _rf()
+    m = rf.GpuLlamaModel(ctx, cfg, cap)
+    m.enable_streaming(cache_bytes)
+    m.set_reader(source, staging)
+    spans = source.spans
+    for name, (t, ne0, ne1, arr) in T.items():
+        if name.startswith("blk."):
+            o, nb = spans[name]
+            m.set_tensor_source(name, t, ne0, ne1, o, nb)
+        else:
+            m.set_tensor(name, t, ne0, ne1, arr)
+    return m
+
+
+def _pinned_model(cfg, T, cache_bytes=1 << 30, cap=40):
+    """The pinned-host streaming tier, in a context of its own (a context
+    holds one model's charges)."""
+    rf = _rf()
+    m = rf.GpuLlamaModel(rf.Context(0), cfg, cap)
+    m.enable_streaming(cache_bytes)
+    for name, (t, ne0, ne1, arr) in T.items():
+        m.set_tensor(name, t, ne0, ne1, arr)
+    return m
+
+
+@pytest.mark.parametrize("staging", [1 << 20, 4096], ids=["merged-ranges", "pieces"])
+@pytest.mark.parametrize("kind", ["file", "buffer"])
+def test_byte_source_matches_pinned_streaming(ctx, orc, tmp_path, staging, kind):
+    rf = _rf()
+    cfg = STREAM_CFG
+    T = _tiny_tensors(np.random.default_rng(1400), cfg, STREAM_TYPES, bias=True)
+    blob, spans = _layout(T)
+    if kind == "file":
+        path = tmp_path / "model.bin"
+        blob.tofile(path)
+        src = rf.ByteSource(str(path))
+    else:
+        src = rf.ByteSource(blob.tobytes())
+    src.spans = spans
+    # cache of 0 bytes: every layer is read again for every token
+    sm = _sourced_model(ctx, cfg, T, src, staging, cache_bytes=0)
+    pm = _pinned_model(cfg, T, cache_bytes=0)
+    om = orc.Model(cfg, T, kv_capacity=40, threads=4)
+    for pos, tok in enumerate([5, 17, 90, 3]):
+        a = sm.forward(tok, pos, want_hidden=True)
+        b = pm.forward(tok, pos, want_hidden=True)
+        r = om.forward(tok, pos)
+        assert np.array_equal(a, b), pos
+        assert np.max(np.abs(a - r)) <= 2e-4 * max(1.0, np.abs(r).max()), pos
+    st = sm.read_stats()
+    nl = cfg["block_count"]
+    layer_bytes = sum(nb for n, (o, nb) in spans.items() if n.startswith("blk."))
+    if staging == 1 << 20:
+        # each layer's tensors are one merged range: one read per layer load
+        assert st["calls"] == 4 * nl, st
+    else:
+        assert st["calls"] > 4 * nl, st
+    # merged reads include the gaps between a layer's tensors (<= 4 KiB each)
+    assert 4 * layer_bytes <= st["bytes"] <= 4 * (layer_bytes + 16 * 12 * nl + 32 * 12 * nl)
+    sm.reset()
+    pm.reset()
+    assert sm.generate([1, 2, 3], 12) == pm.generate([1, 2, 3], 12)
+    for m in (sm, pm):
+        m.close()
+    pm.ctx.close()
+    om.close()
+    src.close()
+
+
+@pytest.mark.parametrize("half", ["f16", "bf16"])
+def test_byte_source_widens_half_weights(ctx, orc, half):
+    """F16 / BF16 block tensors read from the source are widened on the device
+    (tensor.rs:967-1014) into the same values the oracle decodes."""
+    rf = _rf()
+    t = {"f16": F16, "bf16": BF16}[half]
+    cfg = dict(STREAM_CFG)
+    T, R = _half_tensors(np.random.default_rng(1410 + t), cfg, t, orc)
+    blob, spans = _layout(T)
+    src = rf.ByteSource(blob.tobytes())
+    src.spans = spans
+    sm = _sourced_model(ctx, cfg, T, src, 1 << 20)
+    om = orc.Model(cfg, R, kv_capacity=40, threads=4)
+    for pos, tok in enumerate([7, 1, 33]):
+        a = sm.forward(tok, pos, want_hidden=True)
+        r = om.forward(tok, pos)
+        assert np.max(np.abs(a - r)) <= 2e-4 * max(1.0, np.abs(r).max()), pos
+    sm.close()
+    om.close()
+
+
+def test_failed_read_releases_the_load(ctx):
+    rf = _rf()
+    cfg = STREAM_CFG
+    T = _tiny_tensors(np.random.default_rng(1420), cfg, STREAM_TYPES)
+    blob, spans = _layout(T)
+    src = rf.ByteSource(blob.tobytes())
+    src.spans = spans
+    m = _sourced_model(ctx, cfg, T, src, 1 << 20, cache_bytes=0)
+    used = ctx.vram_used
+    src.fail_at = spans["blk.2.ffn_up.weight"][0] + 10  # layer 2's range fails
+    with pytest.raises(rf.RamforgeError) as ei:
+        m.forward(4, 0)
+    assert ei.value.code == rf.RF_ERR_IO and "layer 2" in str(ei.value)
+    assert ctx.vram_used == used
+    assert all(ctx.charge(f"layer:2:{s}") is None for s in ("attn_q.weight", "ffn_up.weight", "ffn_down.weight"))
+    src.fail_at = None
+    m.reset()
+    h = m.forward(4, 0, want_hidden=True)
+    pm = _pinned_model(cfg, T, cache_bytes=0)
+    assert np.array_equal(h, pm.forward(4, 0, want_hidden=True))
+    m.close()
+    pm.close()
+    pm.ctx.close()
