@@ -155,7 +155,8 @@ def context_decode(ctx, m, cfg, n: int, steps: int, graph: bool) -> dict:
 def dominant_kernel(rf) -> str:
     """Kernel that runs the ffn RMSNorm + gate/up + SiLU*up group of the 8B Q8_0 model."""
     if rf.tune_packed_weights(-1) == 1 and rf.packed_supported(rf.GGML.Q8_0, 4096):
-        return "matvec_packed<Q8_0, EPI_SWIGLU, norm> (ffn RMSNorm + gate/up + SiLU*up, packed layout)"
+        x = "float x" if rf.tune_matvec_digits(-1) == 0 else "x as digit planes"
+        return f"matvec_packed<Q8_0, EPI_SWIGLU, norm> (ffn RMSNorm + gate/up + SiLU*up, packed layout, {x})"
     return "matvec_stream<Q8_0, EPI_SWIGLU> (ffn RMSNorm + gate/up + SiLU*up, GGUF layout)"
 
 
@@ -211,6 +212,46 @@ def attention_probe(rf, L: int, copies: int = 4) -> int:
     ctx.synchronize()
     print(json.dumps({"probe": "attention", "positions": L, "launches": copies,
                       "algorithmic_bytes": 2 * L * kvh * hd * 4 + 2 * qh * hd * 4, "copy_bytes": COPY_BYTES,
+                      "copies": 4}), flush=True)
+    ctx.close()
+    return 0
+
+
+def matvec_probe(rf, spec: str, copies: int = 4) -> int:
+    """Launch only what the matvec counters are read for: the GGUF-layout and
+    the packed matvec of one shape ("Q4_0,14336,4096": type, out, in) once on
+    each of `copies` distinct weight copies, then four plain device copies of
+    COPY_BYTES (the calibration kernel for FETCH_SIZE / WRITE_SIZE)."""
+    import numpy as np
+
+    tn, out_dim, in_dim = spec.split(",")
+    t = getattr(rf.GGML, tn)
+    out_dim, in_dim = int(out_dim), int(in_dim)
+    ctx = rf.Context(0)
+    qk, bs = rf.BLOCK_GEOMETRY[t]
+    nblk = out_dim * in_dim // qk
+    wbytes = nblk * bs
+    ws, ps = [], []
+    for i in range(copies):
+        w = ctx.empty((wbytes,), "uint8")
+        ctx.synth_blocks(t, 7000 + i, 0, nblk, 0.02, w)
+        p = ctx.empty((wbytes,), "uint8")
+        rf.pack_weights(ctx, t, w, out_dim, in_dim, p)
+        ws.append(w)
+        ps.append(p)
+    x = ctx.array(np.random.default_rng(3).normal(0, 1, in_dim).astype(np.float32))
+    y = ctx.empty((out_dim,))
+    for w in ws:
+        rf.matvec(ctx, t, w, (out_dim, in_dim), x, y)
+    for p in ps:
+        rf.matvec_packed(ctx, t, p, (out_dim, in_dim), x, y)
+    src = ctx.empty((COPY_BYTES,), "uint8")
+    dst = ctx.empty((COPY_BYTES,), "uint8")
+    for _ in range(4):
+        ctx.copy(dst, src, COPY_BYTES)
+    ctx.synchronize()
+    print(json.dumps({"probe": "matvec", "type": tn, "shape": [out_dim, in_dim], "launches": copies,
+                      "algorithmic_bytes": wbytes + 4 * in_dim + 4 * out_dim, "copy_bytes": COPY_BYTES,
                       "copies": 4}), flush=True)
     ctx.close()
     return 0
@@ -515,6 +556,9 @@ def main() -> int:
     ap.add_argument("--attention-probe", type=int, default=0, metavar="L",
                     help="only launch RoPE + attention at context L on 4 K/V copies and a 256 MiB device copy, for "
                          "rocprofv3 --pmc runs")
+    ap.add_argument("--matvec-probe", default="", metavar="TYPE,OUT,IN",
+                    help="only launch the GGUF-layout and packed matvec of one shape on 4 weight copies and a 256 "
+                         "MiB device copy, for rocprofv3 --pmc runs")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="only launch the dominant kernel (32 gate/up launches) and a 256 MiB device copy, "
                          "for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs")
@@ -537,6 +581,8 @@ def main() -> int:
         return 0
     if args.attention_probe:
         return attention_probe(rf, args.attention_probe)
+    if args.matvec_probe:
+        return matvec_probe(rf, args.matvec_probe)
     if args.config5:
         res = [config5_bench(rf, syn, args.config5, args.prompt, policy) for policy in (1, 0)]
         print(json.dumps({"config5": res}), flush=True)
