@@ -91,13 +91,15 @@ def weight_bytes(specs: list[TensorSpec]) -> int:
 
 
 def build_device_model(ctx, cfg: dict, specs: list[TensorSpec], kv_capacity: int,
-                       stream_cache_bytes: int | None = None, cache_policy: int = 0):
+                       stream_cache_bytes: int | None = None, cache_policy: int = 0, kv_initial: int | None = None):
     """A GpuLlamaModel with every tensor generated on the device.  With
     stream_cache_bytes the block tensors go to pinned host memory and layers
-    stream through a device LRU cache of that many bytes."""
+    stream through a device LRU cache of that many bytes; with kv_initial the
+    KV cache starts at that many positions and grows in 256-position chunks
+    up to kv_capacity."""
     from . import GpuLlamaModel
 
-    m = GpuLlamaModel(ctx, cfg, kv_capacity)
+    m = GpuLlamaModel(ctx, cfg, kv_capacity, kv_initial=kv_initial)
     if stream_cache_bytes is not None:
         m.enable_streaming(stream_cache_bytes)
         m.set_cache_policy(cache_policy)
