@@ -430,6 +430,18 @@ int32_t rf_model_set_tensor_source(rf_model *model, const char *name, uint32_t g
                                    uint64_t ne1, uint64_t offset, uint64_t nbytes);
 /* out[2]: reader calls and bytes read from the byte source. */
 int32_t rf_model_read_stats(rf_model *model, uint64_t *out);
+/* Persistent weights of a streaming model (persistent.rs:1-6, 466-470):
+ * policy 0 (default) keeps token_embd.weight / output.weight resident when
+ * its device bytes are at most a quarter of the context's VRAM budget
+ * (should_keep_resident) and streams it otherwise; 1 streams both, 2 keeps
+ * both resident.  A streamed one stays in mapped pinned host memory (in the
+ * device layout) that the kernels read in place: the embedding gather reads
+ * one row per token, the logits matvec every row (streamed_matvec_into,
+ * persistent.rs:286-463), and no VRAM is charged for it.  Set before those
+ * tensors load; applies only with layer streaming enabled. */
+int32_t rf_model_set_persistent_policy(rf_model *model, int32_t policy);
+/* Bit 0: token_embd.weight is streamed; bit 1: output.weight is streamed. */
+int32_t rf_model_persistent_streamed(rf_model *model, uint32_t *mask);
 
 /* Launch groups of one decode step (see rf_model_time_kernel). */
 #define RF_KERNEL_QKV 1       /* attn RMSNorm + Q/K/V matvec (+ bias)      */

@@ -615,6 +615,17 @@ class GpuLlamaModel:
         _lib.check(self.ctx.lib.rf_model_set_tensor_source(self.handle, name.encode(), ggml_type, ne0, ne1,
                                                            int(offset), int(nbytes)))
 
+    def set_persistent_policy(self, policy: int) -> None:
+        """0: token_embd / output resident when at most 25% of the budget, else
+        streamed from mapped pinned host memory; 1: always streamed; 2: always
+        resident (streaming models only; before those tensors load)."""
+        _lib.check(self.ctx.lib.rf_model_set_persistent_policy(self.handle, policy))
+
+    def persistent_streamed(self) -> dict:
+        v = C.c_uint32()
+        _lib.check(self.ctx.lib.rf_model_persistent_streamed(self.handle, C.byref(v)))
+        return {"token_embd": bool(v.value & 1), "output": bool(v.value & 2)}
+
     def read_stats(self) -> dict:
         out = (C.c_uint64 * 2)()
         _lib.check(self.ctx.lib.rf_model_read_stats(self.handle, out))

@@ -98,6 +98,12 @@ struct rf_model {
   uint32_t attn_chunks = 1;  // largest chunk count of the attention regimes (workspace records per head)
   uint64_t seq_len = 0;
   bool use_graph = false;
+  // Persistent weights of a streaming model (persistent.rs:1-6, 466-470):
+  // 0 = resident when at most 25% of the budget, else streamed (the
+  // reference's rule); 1 = always streamed; 2 = always resident.  A streamed
+  // embedding / output projection stays in mapped pinned host memory that the
+  // kernels read in place (a row for the embedding, every row for logits).
+  int persistent_policy = 0;
   // one decode-step graph per attention regime (attn_regime)
   hipGraph_t graph[ATT_REGIMES] = {};
   hipGraphExec_t graph_exec[ATT_REGIMES] = {};
@@ -150,6 +156,12 @@ int32_t release_charge(rf_model* m, const std::string& name) {
 
 int32_t drop_tensor(rf_model* m, DevTensor& t) {
   if (!t.present()) return RF_OK;
+  if (t.charge.empty() && t.host) {  // a streamed persistent weight: pinned host memory, no charge
+    hipError_t e = hipStreamSynchronize(m->ctx->compute);
+    hipHostFree(t.host);
+    t = DevTensor{};
+    return e == hipSuccess ? RF_OK : hip_error(e, "hipStreamSynchronize");
+  }
   const int32_t rc = release_charge(m, t.charge);
   t = DevTensor{};
   return rc;
@@ -677,6 +689,10 @@ bool is_projection(const std::string& name) {
   return false;
 }
 
+int32_t fill_pinned(rf_model* m, const std::string& name, uint32_t t, uint64_t ne0, uint64_t ne1, uint64_t bytes,
+                    const void* host, bool synth, uint64_t seed, double mul, float constant, bool pack,
+                    unsigned flags, void** out);
+
 // A block tensor of a streaming model: its device-layout bytes go to pinned
 // host memory (packed / widened as on the device path); the layer is uploaded
 // when a forward pass needs it.
@@ -686,7 +702,6 @@ int32_t install_streamed(rf_model* m, const std::string& name, DevTensor* slot, 
   unsigned li = 0;
   if (sscanf(name.c_str(), "blk.%u.", &li) != 1 || li >= m->layers.size())
     return set_error(RF_ERR_INVALID, "unknown tensor '%s'", name.c_str());
-  rf_ctx* ctx = m->ctx;
   reset_graph(m);
   int32_t rc = layer_free(m, li);  // a resident copy of the layer is stale now
   if (rc) return rc;
@@ -694,7 +709,34 @@ int32_t install_streamed(rf_model* m, const std::string& name, DevTensor* slot, 
   const bool pack = g_pack_weights && is_projection(name) && plan_packed(t, ne0).ok;
   const uint64_t fbytes = widen ? ne0 * ne1 * 4 : bytes;
   void* pin = nullptr;
-  hipError_t e = hipHostMalloc(&pin, fbytes, hipHostMallocDefault);
+  rc = fill_pinned(m, name, t, ne0, ne1, bytes, host, synth, seed, mul, constant, pack, hipHostMallocDefault, &pin);
+  if (rc) return rc;
+  if (slot->host) hipHostFree(slot->host);
+  slot->src = false;
+  slot->type = widen ? T_F32 : t;
+  slot->ne0 = ne0;
+  slot->ne1 = ne1;
+  slot->nbytes = fbytes;
+  slot->d = nullptr;
+  slot->charge.clear();
+  slot->packed = pack;
+  slot->host = pin;
+  update_layer_bytes(m, li);
+  return RF_OK;
+}
+
+// The device-layout bytes of a tensor (packed, widened, or as given) in new
+// pinned host memory allocated with `flags`: synthesized on the device and
+// copied back, widened or packed on the host, or copied.
+int32_t fill_pinned(rf_model* m, const std::string& name, uint32_t t, uint64_t ne0, uint64_t ne1, uint64_t bytes,
+                    const void* host, bool synth, uint64_t seed, double mul, float constant, bool pack,
+                    unsigned flags, void** out) {
+  rf_ctx* ctx = m->ctx;
+  const bool widen = (t == T_F16 || t == T_BF16);
+  const uint64_t fbytes = widen ? ne0 * ne1 * 4 : bytes;
+  int32_t rc = RF_OK;
+  void* pin = nullptr;
+  hipError_t e = hipHostMalloc(&pin, fbytes, flags);
   if (e != hipSuccess) return hip_error(e, "hipHostMalloc");
   if (synth) {
     void *tmp = nullptr, *tmp2 = nullptr;
@@ -733,17 +775,44 @@ int32_t install_streamed(rf_model* m, const std::string& name, DevTensor* slot, 
     hipHostFree(pin);
     return rc;
   }
-  if (slot->host) hipHostFree(slot->host);
+  *out = pin;
+  return RF_OK;
+}
+
+// An embedding or output projection of a streaming model that the policy
+// streams (streamed_matvec_into / get_embedding_into, persistent.rs:60-463):
+// its device-layout bytes stay in mapped pinned host memory and the kernels
+// read them there, one row per token for the embedding and every row for the
+// logits, so no device memory is charged for it.
+int32_t install_persistent_streamed(rf_model* m, const std::string& name, DevTensor* slot, uint32_t t,
+                                    uint64_t ne0, uint64_t ne1, uint64_t bytes, const void* host, bool synth,
+                                    uint64_t seed, double mul, float constant) {
+  const bool widen = (t == T_F16 || t == T_BF16);
+  const bool pack = g_pack_weights && is_projection(name) && plan_packed(t, ne0).ok;
+  void* pin = nullptr;
+  int32_t rc = fill_pinned(m, name, t, ne0, ne1, bytes, host, synth, seed, mul, constant, pack, hipHostMallocMapped,
+                           &pin);
+  if (rc) return rc;
+  void* dptr = nullptr;
+  const hipError_t e = hipHostGetDevicePointer(&dptr, pin, 0);
+  if (e != hipSuccess) {
+    hipHostFree(pin);
+    return hip_error(e, "hipHostGetDevicePointer");
+  }
+  rc = drop_tensor(m, *slot);
+  if (rc) {
+    hipHostFree(pin);
+    return rc;
+  }
   slot->src = false;
   slot->type = widen ? T_F32 : t;
   slot->ne0 = ne0;
   slot->ne1 = ne1;
-  slot->nbytes = fbytes;
-  slot->d = nullptr;
+  slot->nbytes = widen ? ne0 * ne1 * 4 : bytes;
+  slot->d = dptr;
   slot->charge.clear();
   slot->packed = pack;
   slot->host = pin;
-  update_layer_bytes(m, li);
   return RF_OK;
 }
 
@@ -765,6 +834,17 @@ int32_t install(rf_model* m, const char* cname, uint32_t t, uint64_t ne0, uint64
     return set_error(RF_ERR_UNSUPPORTED, "synthetic generator does not emit %s", type_name(t));
   if (m->streaming && name.rfind("blk.", 0) == 0)
     return install_streamed(m, name, slot, t, ne0, ne1, bytes, host, synth, seed, mul, constant);
+  if (m->streaming && (name == "token_embd.weight" || name == "output.weight")) {
+    // should_keep_resident (persistent.rs:466-470): resident when its device
+    // bytes are at most a quarter of the budget
+    const uint64_t resident = (t == T_F16 || t == T_BF16) ? ne0 * ne1 * 4 : bytes;
+    const bool stream = m->persistent_policy == 1 ||
+                        (m->persistent_policy == 0 && resident > m->ctx->ledger.total() / 4);
+    if (stream) {
+      reset_graph(m);
+      return install_persistent_streamed(m, name, slot, t, ne0, ne1, bytes, host, synth, seed, mul, constant);
+    }
+  }
   rf_ctx* ctx = m->ctx;
   reset_graph(m);
   hipError_t e = hipStreamSynchronize(ctx->compute);
@@ -1456,6 +1536,8 @@ void rf_model_destroy(rf_model* m) {
     if (m->res[li].used) hipEventDestroy(m->res[li].used);
   }
   for (auto it = m->charges.rbegin(); it != m->charges.rend(); ++it) vram_release(m->ctx, *it);
+  for (DevTensor* x : {&m->token_embd, &m->output, &m->output_norm})
+    if (x->host) hipHostFree(x->host);
   for (int i = 0; i < 2; ++i) {
     if (m->rstage[i]) hipHostFree(m->rstage[i]);
     if (m->rstage_ev[i]) hipEventDestroy(m->rstage_ev[i]);
@@ -1823,6 +1905,22 @@ int32_t rf_model_set_tensor_source(rf_model* m, const char* cname, uint32_t t, u
   slot->src_off = offset;
   slot->src_bytes = bytes;
   update_layer_bytes(m, li);
+  return RF_OK;
+}
+
+int32_t rf_model_set_persistent_policy(rf_model* m, int32_t policy) {
+  if (!m) return set_error(RF_ERR_INVALID, "null model");
+  if (policy < 0 || policy > 2) return set_error(RF_ERR_INVALID, "unknown persistent-weight policy %d", policy);
+  if (m->token_embd.present() || m->output.present())
+    return set_error(RF_ERR_INVALID, "the persistent-weight policy must be set before token_embd / output load");
+  m->persistent_policy = policy;
+  return RF_OK;
+}
+
+int32_t rf_model_persistent_streamed(rf_model* m, uint32_t* mask) {
+  if (!m || !mask) return set_error(RF_ERR_INVALID, "null argument");
+  *mask = (m->token_embd.present() && m->token_embd.charge.empty() && m->token_embd.host ? 1u : 0u) |
+          (m->output.present() && m->output.charge.empty() && m->output.host ? 2u : 0u);
   return RF_OK;
 }
 
