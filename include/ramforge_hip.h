@@ -442,6 +442,18 @@ int32_t rf_model_read_stats(rf_model *model, uint64_t *out);
 int32_t rf_model_set_persistent_policy(rf_model *model, int32_t policy);
 /* Bit 0: token_embd.weight is streamed; bit 1: output.weight is streamed. */
 int32_t rf_model_persistent_streamed(rf_model *model, uint32_t *mask);
+/* Profiler of the real forward (the reference's per-event records around each
+ * matvec, compute_dispatch.rs:48-56, profile.rs:7-23): with enable = 1 every
+ * launch group of the forwards, logits and eager decode steps that follow is
+ * bracketed by HIP events on the compute stream and its device time added to
+ * a per-group total.  Eager launches only: refused while graph replay is on
+ * (and rf_model_use_graph(model, 1) is refused while it is on).  Same results
+ * either way. */
+int32_t rf_model_profile(rf_model *model, int32_t enable);
+/* ms[6] / counts[6]: accumulated device milliseconds and launches per group,
+ * indexed RF_KERNEL_QKV - 1 .. RF_KERNEL_LOGITS - 1; reset != 0 zeroes them
+ * after reading (waits for the recorded events). */
+int32_t rf_model_profile_read(rf_model *model, double *ms, uint64_t *counts, int32_t reset);
 
 /* Launch groups of one decode step (see rf_model_time_kernel). */
 #define RF_KERNEL_QKV 1       /* attn RMSNorm + Q/K/V matvec (+ bias)      */

@@ -626,6 +626,17 @@ class GpuLlamaModel:
         _lib.check(self.ctx.lib.rf_model_persistent_streamed(self.handle, C.byref(v)))
         return {"token_embd": bool(v.value & 1), "output": bool(v.value & 2)}
 
+    def profile(self, enable: bool) -> None:
+        """Bracket every launch group of the following eager forwards with HIP
+        events (rf_model_profile)."""
+        _lib.check(self.ctx.lib.rf_model_profile(self.handle, 1 if enable else 0))
+
+    def profile_read(self, reset: bool = False) -> dict:
+        """{group: (device ms, launches)} accumulated by the forward profiler."""
+        ms, n = (C.c_double * 6)(), (C.c_uint64 * 6)()
+        _lib.check(self.ctx.lib.rf_model_profile_read(self.handle, ms, n, 1 if reset else 0))
+        return {k: (ms[v - 1], int(n[v - 1])) for k, v in self.KERNELS.items()}
+
     def read_stats(self) -> dict:
         out = (C.c_uint64 * 2)()
         _lib.check(self.ctx.lib.rf_model_read_stats(self.handle, out))

@@ -104,6 +104,14 @@ struct rf_model {
   // embedding / output projection stays in mapped pinned host memory that the
   // kernels read in place (a row for the embedding, every row for logits).
   int persistent_policy = 0;
+  // Profiler of the real forward (rf_model_profile): an event pair around
+  // every launch group, collected when the pool is reused or read.
+  bool prof = false;
+  std::vector<hipEvent_t> prof_ev;  // pairs: [2k] before, [2k + 1] after
+  std::vector<int> prof_kind;       // group of pair k (0..5 = RF_KERNEL_QKV - 1 ..)
+  size_t prof_used = 0;             // pairs recorded and not collected
+  double prof_ms[6] = {0, 0, 0, 0, 0, 0};
+  uint64_t prof_n[6] = {0, 0, 0, 0, 0, 0};
   // one decode-step graph per attention regime (attn_regime)
   hipGraph_t graph[ATT_REGIMES] = {};
   hipGraphExec_t graph_exec[ATT_REGIMES] = {};
@@ -1105,13 +1113,49 @@ int32_t enqueue_down(rf_model* m, size_t li, int32_t* advance = nullptr) {
   return RF_OK;
 }
 
+// Adds the recorded event pairs to the per-group totals (waits for the
+// last one) and frees the pool for reuse.
+int32_t prof_collect(rf_model* m) {
+  if (m->prof_used == 0) return RF_OK;
+  hipError_t e = hipEventSynchronize(m->prof_ev[2 * m->prof_used - 1]);
+  for (size_t k = 0; k < m->prof_used && e == hipSuccess; ++k) {
+    float ms = 0.f;
+    e = hipEventElapsedTime(&ms, m->prof_ev[2 * k], m->prof_ev[2 * k + 1]);
+    m->prof_ms[m->prof_kind[k]] += ms;
+    m->prof_n[m->prof_kind[k]] += 1;
+  }
+  m->prof_used = 0;
+  return e == hipSuccess ? RF_OK : hip_error(e, "profiler events");
+}
+
+// One launch group, bracketed by profiler events when profiling is on
+// (ProfileEvent::QuantizedMatvec around each matvec, compute_dispatch.rs:48-56;
+// LayerCompute for attention, profile.rs:8-23).
+template <typename F>
+int32_t prof_group(rf_model* m, int kind, F&& body) {
+  if (!m->prof) return body();
+  if (m->prof_used * 2 + 2 > m->prof_ev.size()) {
+    int32_t rc = prof_collect(m);
+    if (rc) return rc;
+  }
+  const size_t k = m->prof_used;
+  hipStream_t st = m->ctx->compute;
+  RF_LAUNCH(hipEventRecord(m->prof_ev[2 * k], st), "profiler event");
+  const int32_t rc = body();
+  if (rc) return rc;
+  RF_LAUNCH(hipEventRecord(m->prof_ev[2 * k + 1], st), "profiler event");
+  m->prof_kind[k] = kind;
+  m->prof_used = k + 1;
+  return RF_OK;
+}
+
 int32_t enqueue_layer(rf_model* m, size_t li, int32_t* advance = nullptr) {
   int32_t rc;
-  if ((rc = enqueue_qkv(m, li))) return rc;
-  if ((rc = enqueue_attention(m, li))) return rc;
-  if ((rc = enqueue_oproj(m, li))) return rc;
-  if ((rc = enqueue_gateup(m, li))) return rc;
-  return enqueue_down(m, li, advance);
+  if ((rc = prof_group(m, 0, [&] { return enqueue_qkv(m, li); }))) return rc;
+  if ((rc = prof_group(m, 1, [&] { return enqueue_attention(m, li); }))) return rc;
+  if ((rc = prof_group(m, 2, [&] { return enqueue_oproj(m, li); }))) return rc;
+  if ((rc = prof_group(m, 3, [&] { return enqueue_gateup(m, li); }))) return rc;
+  return prof_group(m, 4, [&] { return enqueue_down(m, li, advance); });
 }
 
 // Algorithmic HBM bytes of one launch group of layer li (weights + vectors read
@@ -1172,10 +1216,12 @@ int32_t enqueue_logits(rf_model* m) {
   const rf_model_config& c = m->cfg;
   const DevTensor& w = m->output.present() ? m->output : m->token_embd;
   MSeg s{&w, nullptr, m->logits, nullptr, c.vocab_size};
-  RF_LAUNCH(fused_matvec(m, &s, 1, m->hidden, static_cast<const float*>(m->output_norm.d), c.embedding_length,
-                         EPI_STORE),
-            "logits");
-  return RF_OK;
+  return prof_group(m, 5, [&]() -> int32_t {
+    RF_LAUNCH(fused_matvec(m, &s, 1, m->hidden, static_cast<const float*>(m->output_norm.d), c.embedding_length,
+                           EPI_STORE),
+              "logits");
+    return RF_OK;
+  });
 }
 
 // One decode step: logits -> argmax (token stored at ring[pos]) with the
@@ -1538,6 +1584,8 @@ void rf_model_destroy(rf_model* m) {
   for (auto it = m->charges.rbegin(); it != m->charges.rend(); ++it) vram_release(m->ctx, *it);
   for (DevTensor* x : {&m->token_embd, &m->output, &m->output_norm})
     if (x->host) hipHostFree(x->host);
+  for (hipEvent_t e : m->prof_ev)
+    if (e) hipEventDestroy(e);
   for (int i = 0; i < 2; ++i) {
     if (m->rstage[i]) hipHostFree(m->rstage[i]);
     if (m->rstage_ev[i]) hipEventDestroy(m->rstage_ev[i]);
@@ -1694,6 +1742,8 @@ int32_t rf_model_kv_capacity(rf_model* m, uint64_t* tokens) {
 
 int32_t rf_model_use_graph(rf_model* m, int32_t enable) {
   if (!m) return set_error(RF_ERR_INVALID, "null model");
+  if (enable && m->prof)
+    return set_error(RF_ERR_INVALID, "graph replay is unavailable while the forward profiler is on");
   if (enable && m->streaming)
     return set_error(RF_ERR_UNSUPPORTED, "graph replay needs every layer resident; this model streams its layers");
   m->use_graph = enable != 0;
@@ -1905,6 +1955,42 @@ int32_t rf_model_set_tensor_source(rf_model* m, const char* cname, uint32_t t, u
   slot->src_off = offset;
   slot->src_bytes = bytes;
   update_layer_bytes(m, li);
+  return RF_OK;
+}
+
+int32_t rf_model_profile(rf_model* m, int32_t enable) {
+  if (!m) return set_error(RF_ERR_INVALID, "null model");
+  if (enable && m->use_graph)
+    return set_error(RF_ERR_INVALID, "the forward profiler needs eager launches (rf_model_use_graph(model, 0))");
+  int32_t rc = prof_collect(m);
+  if (rc) return rc;
+  if (enable && m->prof_ev.empty()) {
+    const size_t pairs = 5 * m->layers.size() + 2;
+    std::vector<hipEvent_t> ev(2 * pairs, nullptr);
+    for (hipEvent_t& e : ev) {
+      const hipError_t he = hipEventCreate(&e);
+      if (he != hipSuccess) {
+        for (hipEvent_t x : ev)
+          if (x) hipEventDestroy(x);
+        return hip_error(he, "hipEventCreate");
+      }
+    }
+    m->prof_ev.swap(ev);
+    m->prof_kind.assign(pairs, 0);
+  }
+  m->prof = enable != 0;
+  return RF_OK;
+}
+
+int32_t rf_model_profile_read(rf_model* m, double* ms, uint64_t* counts, int32_t reset) {
+  if (!m || !ms || !counts) return set_error(RF_ERR_INVALID, "null argument");
+  int32_t rc = prof_collect(m);
+  if (rc) return rc;
+  for (int i = 0; i < 6; ++i) {
+    ms[i] = m->prof_ms[i];
+    counts[i] = m->prof_n[i];
+    if (reset) { m->prof_ms[i] = 0; m->prof_n[i] = 0; }
+  }
   return RF_OK;
 }
 

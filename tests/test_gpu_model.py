@@ -646,3 +646,32 @@ def test_tiny_model_f16_bf16_weights(ctx, orc, half, streamed):
     om.close()
     if sctx is not None:
         sctx.close()
+
+
+def test_forward_profiler_records_every_group(ctx):
+    """rf_model_profile: per-group device time of real forwards, logits and
+    eager decode steps (compute_dispatch.rs:48-56, profile.rs:7-23), with the
+    results unchanged and graph replay refused while it is on."""
+    rf = _rf()
+    cfg = dict(TINY)
+    T = _tiny_tensors(np.random.default_rng(990), cfg, ALL_Q8)
+    gm = _load_gpu(ctx, cfg, T, 48)
+    plain = [gm.forward(t, p, want_hidden=True) for p, t in enumerate([5, 17, 90])]
+    gm.reset()
+    gm.profile(True)
+    with pytest.raises(rf.RamforgeError, match="profiler"):
+        gm.use_graph(True)
+    prof = [gm.forward(t, p, want_hidden=True) for p, t in enumerate([5, 17, 90])]
+    for a, b in zip(plain, prof):
+        assert np.array_equal(a, b)
+    gm.logits()
+    gm.decode_steps(2)
+    r = gm.profile_read(reset=True)
+    nl = cfg["block_count"]
+    for k in ("qkv", "attention", "oproj", "gateup", "down"):
+        assert r[k][1] == 5 * nl and r[k][0] > 0, (k, r[k])
+    assert r["logits"][1] == 3 and r["logits"][0] > 0, r["logits"]  # logits() + 2 decode steps
+    assert all(v == (0.0, 0) for v in gm.profile_read().values())
+    gm.profile(False)
+    gm.use_graph(True)
+    gm.close()
