@@ -64,15 +64,25 @@ def matvec_q8_0_gbs(ctx, rf, syn, iters: int = 120):
 
     x = ctx.array(np.random.default_rng(1).normal(0, 1, in_dim).astype(np.float32), "bench:q8_0_4096:x")
     y = ctx.empty((out_dim,), charge="bench:q8_0_4096:y")
-    for i in range(copies):
-        rf.matvec(ctx, syn.Q8_0, ws[i], (out_dim, in_dim), x, y)
-    ctx.synchronize()
-    e0, e1 = ctx.event(), ctx.event()
-    ctx.record(e0, ctx.compute_stream)
-    for i in range(iters):
-        rf.matvec(ctx, syn.Q8_0, ws[i % copies], (out_dim, in_dim), x, y, stream=ctx.compute_stream)
-    ctx.record(e1, ctx.compute_stream)
-    ms = ctx.elapsed_ms(e0, e1) / iters
+
+    def per_call_ms():
+        for i in range(copies):  # warm-up; with the repack cache on, packs each copy
+            rf.matvec(ctx, syn.Q8_0, ws[i], (out_dim, in_dim), x, y)
+        ctx.synchronize()
+        e0, e1 = ctx.event(), ctx.event()
+        ctx.record(e0, ctx.compute_stream)
+        for i in range(iters):
+            rf.matvec(ctx, syn.Q8_0, ws[i % copies], (out_dim, in_dim), x, y, stream=ctx.compute_stream)
+        ctx.record(e1, ctx.compute_stream)
+        ms = ctx.elapsed_ms(e0, e1) / iters
+        ctx.destroy_event(e0)
+        ctx.destroy_event(e1)
+        return ms
+
+    ms = per_call_ms()
+    ctx.matvec_cache(copies * wbytes)
+    ms_cached = per_call_ms()
+    ctx.matvec_cache(0)
     alg = wbytes + 4 * in_dim + 4 * out_dim
     for a in ws + [x, y]:
         a.free()
@@ -80,7 +90,11 @@ def matvec_q8_0_gbs(ctx, rf, syn, iters: int = 120):
                                                                                       copies * wbytes / 2 ** 30),
             "us_per_call": round(ms * 1e3, 3), "algorithmic_bytes": alg,
             "achieved_GBs": round(alg / (ms * 1e-3) / 1e9, 1), "frac_of_peak": round(alg / (ms * 1e-3) / 1e9 /
-                                                                                      PEAK_HBM_GBS, 4)}
+                                                                                      PEAK_HBM_GBS, 4),
+            "repack_cache": {"us_per_call": round(ms_cached * 1e3, 3),
+                             "frac_of_peak": round(alg / (ms_cached * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+                             "note": "the same eager rf_matvec calls with rf_matvec_cache on (packed once, "
+                                     "the packed kernel after)"}}
 
 
 def host_cores() -> dict:
@@ -320,6 +334,14 @@ def kernel_bench(rf, syn, use_graph: bool, reps: int = 3) -> list:
         calls = [lambda w=w: rf.matvec(ctx, t, w, (out_dim, in_dim), x, y) for w in ws]
         record(name, "matvec (GGUF layout)", timed(calls, len(calls)), alg)
         if rf.packed_supported(t, in_dim):
+            # the same rf_matvec calls on GGUF bytes with the repack cache on:
+            # the first call on each copy packs it, the timed ones hit
+            ctx.matvec_cache(len(ws) * wbytes)
+            for c in calls:
+                c()
+            ctx.synchronize()
+            record(name, "matvec (GGUF, repack cache)", timed(calls, len(calls)), alg)
+            ctx.matvec_cache(0)
             ps = []
             for i, w in enumerate(ws):
                 p = ctx.empty((wbytes,), "uint8", charge=f"kbench:{name}:p{i}")

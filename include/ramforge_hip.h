@@ -165,6 +165,30 @@ int32_t rf_matvec(rf_ctx *ctx, uint32_t ggml_type, const void *w, uint64_t w_byt
                   uint64_t in_dim, const float *x, float *y, uint64_t row_start, uint64_t row_count,
                   rf_stream_t stream);
 
+/* Repack cache of rf_matvec (off by default; no counterpart in the
+ * reference).  The reference's matvec seam is handed the same immutable
+ * tensor bytes every token (compute_dispatch.rs:40-58 over a loaded
+ * TensorData); with the cache on, rf_matvec's first call on a Q8_0, Q4_0,
+ * Q4_K or Q6_K tensor packs all out_dim rows into a device copy in the
+ * packed layout (below), and later calls with the same pointer, type,
+ * out_dim and in_dim run the packed kernel on it.  Results are those of
+ * rf_matvec_packed.  max_bytes bounds the copies (least recently used
+ * evicted first); each is charged to the ledger as "workspace:repack:<n>"
+ * and a tensor that does not fit runs uncached.  max_bytes = 0 turns the
+ * cache off and frees it.  Eviction synchronises the device.  No entry is
+ * added while the stream is being captured into a graph or once
+ * rf_ctx_reserve has fixed the workspaces; a capture uses the entries whose
+ * pack has completed by rf_capture_begin, and rf_graph_replay refuses such a
+ * graph after any entry has been dropped (it may hold the freed copy).  A
+ * graph captured by other means must not be replayed after a drop.
+ * The caller's bytes must stay unchanged while cached: after changing or
+ * freeing them, call rf_matvec_cache_forget on their range, which drops every
+ * entry whose source bytes overlap [base, base + bytes). */
+int32_t rf_matvec_cache(rf_ctx *ctx, uint64_t max_bytes);
+int32_t rf_matvec_cache_forget(rf_ctx *ctx, const void *base, uint64_t bytes);
+int32_t rf_matvec_cache_stats(rf_ctx *ctx, uint64_t *entries, uint64_t *bytes, uint64_t *hits,
+                              uint64_t *misses);
+
 /* Device-native ("packed") layout of Q8_0, Q4_0, Q4_K and Q6_K tensors, used
  * by the model for its weights.  No counterpart in the reference, which reads
  * GGUF blocks as stored; the arithmetic of rf_matvec_packed is that of

@@ -227,6 +227,23 @@ class Context:
     def rename_prefix(self, old: str, new: str) -> None:
         _lib.check(self.lib.rf_vram_rename_prefix(self.handle, old.encode(), new.encode()))
 
+    # rf_matvec's repack cache (off by default)
+    def matvec_cache(self, max_bytes: int) -> None:
+        """Keep packed copies of the GGUF tensors matvec() is handed, up to
+        max_bytes (0 turns the cache off and frees it).  The tensors' bytes
+        must not change while cached (see matvec_cache_forget)."""
+        _lib.check(self.lib.rf_matvec_cache(self.handle, int(max_bytes)))
+
+    def matvec_cache_forget(self, w, nbytes: Optional[int] = None) -> None:
+        """Drop the cached copies of every tensor whose bytes overlap w's."""
+        n = w.nbytes if (nbytes is None and isinstance(w, DeviceArray)) else int(nbytes or 0)
+        _lib.check(self.lib.rf_matvec_cache_forget(self.handle, _ptr(w), n))
+
+    def matvec_cache_stats(self) -> dict:
+        v = [C.c_uint64() for _ in range(4)]
+        _lib.check(self.lib.rf_matvec_cache_stats(self.handle, *(C.byref(x) for x in v)))
+        return dict(zip(("entries", "bytes", "hits", "misses"), (x.value for x in v)))
+
     # buffers
     def alloc(self, nbytes: int, charge: Optional[str] = None, shape=None, dtype=np.uint8) -> DeviceArray:
         if charge is None:

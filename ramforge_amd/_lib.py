@@ -92,6 +92,9 @@ SIGNATURES = {
     "rf_event_elapsed_ms": (_i32, [_vp, _vp, _vp, C.POINTER(_f32)]),
     "rf_event_synchronize": (_i32, [_vp, _vp]),
     "rf_matvec": (_i32, [_vp, _u32, _vp, _u64, _u64, _u64, _fp, _fp, _u64, _u64, _vp]),
+    "rf_matvec_cache": (_i32, [_vp, _u64]),
+    "rf_matvec_cache_forget": (_i32, [_vp, _vp, _u64]),
+    "rf_matvec_cache_stats": (_i32, [_vp, C.POINTER(_u64), C.POINTER(_u64), C.POINTER(_u64), C.POINTER(_u64)]),
     "rf_dequantize_rows": (_i32, [_vp, _u32, _vp, _u64, _u64, _u64, _u64, _fp, _vp]),
     "rf_attention_decode": (_i32, [_vp, _fp, _fp, _fp, _fp, _fp, _u32, _u32, _u32, _u32, _fp, _vp]),
     "rf_attention_decode_noalloc": (_i32, [_vp, _fp, _fp, _fp, _fp, _fp, _u32, _u32, _u32, _u32, _fp, _vp]),

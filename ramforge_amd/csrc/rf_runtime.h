@@ -7,6 +7,7 @@
 #include <map>
 #include <mutex>
 #include <string>
+#include <vector>
 
 #include "../../include/ramforge_hip.h"
 #include "rf_kernels.h"
@@ -43,6 +44,30 @@ struct Workspace {
   uint64_t bytes = 0;
 };
 
+// One GGUF tensor held in the packed layout by rf_matvec's repack cache.
+// Keyed by the caller's pointer, type and shape; the caller's bytes are
+// assumed unchanged while the entry lives (rf_matvec_cache_forget drops it).
+struct RepackEntry {
+  const uint8_t* src = nullptr;
+  uint32_t type = 0;
+  uint64_t rows = 0, in_dim = 0, bytes = 0;
+  void* packed = nullptr;
+  std::string charge;
+  hipEvent_t ready = nullptr;  // recorded on `packed_on` after the pack
+  hipStream_t packed_on = nullptr;
+  bool settled = false;  // the pack is known to have completed
+  uint64_t last_use = 0;
+};
+
+struct RepackCache {
+  std::mutex mu;
+  uint64_t limit = 0;  // bytes; 0 = off
+  uint64_t bytes = 0, hits = 0, misses = 0, clock = 0, seq = 0;
+  uint64_t generation = 0;     // incremented whenever an entry is dropped
+  uint64_t captured_hits = 0;  // hits served inside a stream capture
+  std::vector<RepackEntry> entries;
+};
+
 }  // namespace rf
 
 struct rf_ctx {
@@ -65,6 +90,7 @@ struct rf_ctx {
   void* pinned_stage[2] = {nullptr, nullptr};
   hipEvent_t stage_ev[2] = {nullptr, nullptr};
   uint64_t stage_bytes = 0;  // 0 until both buffers and events exist
+  rf::RepackCache repack;    // rf_matvec_cache
 };
 
 namespace rf {

@@ -8,6 +8,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <functional>
 #include <vector>
 
 namespace rf {
@@ -359,8 +360,10 @@ void rf_ctx_destroy(rf_ctx* ctx) {
   if (!ctx) return;
   hipSetDevice(ctx->device);
   hipDeviceSynchronize();
-  for (auto& kv : ctx->buffers) hipFree(kv.second);
+  for (auto& kv : ctx->buffers) hipFree(kv.second);  // includes the repack cache's buffers
   ctx->buffers.clear();
+  for (auto& en : ctx->repack.entries)
+    if (en.ready) hipEventDestroy(en.ready);
   for (int i = 0; i < 2; ++i) {
     if (ctx->pinned_stage[i]) hipHostFree(ctx->pinned_stage[i]);
     if (ctx->stage_ev[i]) hipEventDestroy(ctx->stage_ev[i]);
@@ -599,6 +602,186 @@ static int32_t validate_matvec(rf_ctx* ctx, uint32_t t, const void* w, uint64_t 
   return RF_OK;
 }
 
+// Rows [row_start, row_start + count) of a validated packed tensor into y.
+static int32_t launch_packed_rows(rf_ctx* ctx, uint32_t t, const void* packed, uint64_t out_dim, uint64_t in_dim,
+                                  const float* x, float* y, uint64_t row_start, uint64_t count, hipStream_t st) {
+  const float* xa = x;
+  if ((reinterpret_cast<uintptr_t>(x) & 15u) != 0) {
+    // the kernel reads x with 16-byte loads: stage a misaligned x in the context scratch
+    int32_t rc = ensure_workspace(ctx, ctx->scratch_ws, "workspace:scratch", in_dim * 4, st);
+    if (rc) return rc;
+    RF_HIP(hipMemcpyAsync(ctx->scratch_ws.ptr, x, in_dim * 4, hipMemcpyDeviceToDevice, st), "hipMemcpyAsync");
+    xa = static_cast<const float*>(ctx->scratch_ws.ptr);
+  }
+  PkSegDesc seg{packed, nullptr, out_dim, row_start, count, y, nullptr};
+  hipError_t e = launch_matvec_packed(t, &seg, 1, xa, nullptr, 0.f, in_dim, EPI_STORE, st);
+  if (e != hipSuccess) return hip_error(e, "packed matvec launch");
+  return RF_OK;
+}
+
+// ------------------------------------------------------ repack cache
+// rf_matvec's opt-in cache of packed copies of the GGUF tensors it is handed.
+// Callers of the reference's matvec seam pass the same immutable tensor bytes
+// token after token (TensorData of a loaded model, compute_dispatch.rs:40-58);
+// the first call packs them once, later calls run the packed kernel.
+
+// Drop entries [i] for which drop(entry) holds.  Buffers may still be read by
+// queued work on any stream, so the device is synchronised before any free.
+static int32_t repack_drop(rf_ctx* ctx, const std::function<bool(const RepackEntry&)>& drop) {
+  RepackCache& c = ctx->repack;
+  bool any = false;
+  for (auto& en : c.entries) any = any || drop(en);
+  if (!any) return RF_OK;
+  RF_HIP(hipDeviceSynchronize(), "hipDeviceSynchronize");
+  ++c.generation;  // graphs that captured a hit on the cache are stale from here on
+  int32_t rc = RF_OK;
+  std::vector<RepackEntry> keep;
+  for (auto& en : c.entries) {
+    if (!drop(en)) {
+      keep.push_back(std::move(en));
+      continue;
+    }
+    if (en.ready) hipEventDestroy(en.ready);
+    const int32_t r = vram_release(ctx, en.charge);
+    if (!rc) rc = r;
+    c.bytes -= en.bytes;
+  }
+  c.entries.swap(keep);
+  return rc;
+}
+
+// Evict least-recently-used entries until `need` more bytes fit both under
+// the cache limit and in the device ledger.  False when they cannot.
+static bool repack_make_room(rf_ctx* ctx, uint64_t need, int32_t* rc) {
+  RepackCache& c = ctx->repack;
+  *rc = RF_OK;
+  if (need > c.limit) return false;
+  uint64_t freed = 0;
+  std::vector<const RepackEntry*> order;
+  for (auto& en : c.entries) order.push_back(&en);
+  std::sort(order.begin(), order.end(),
+            [](const RepackEntry* a, const RepackEntry* b) { return a->last_use < b->last_use; });
+  size_t n = 0;
+  const auto fits = [&] {
+    return c.bytes - freed + need <= c.limit && vram_can_allocate(ctx, need > freed ? need - freed : 0);
+  };
+  while (!fits() && n < order.size()) freed += order[n++]->bytes;
+  if (!fits()) return false;
+  if (n == 0) return true;
+  const uint64_t evict = order[n - 1]->last_use;
+  *rc = repack_drop(ctx, [evict](const RepackEntry& en) { return en.last_use <= evict; });
+  return *rc == RF_OK;
+}
+
+// Marks entries whose pack has completed (host query of its event; not
+// called inside a capture).
+static void repack_settle(RepackCache& c) {
+  for (auto& en : c.entries)
+    if (!en.settled && hipEventQuery(en.ready) == hipSuccess) en.settled = true;
+}
+
+// The packed copy of w for this call, or nullptr when rf_matvec is to run the
+// GGUF-layout kernel: the type has no packed layout, the shape is beyond the
+// packed kernel, or the tensor does not fit.  Inside a stream capture only a
+// hit on an entry whose pack has completed is served (nothing is allocated or
+// waited for there); rf_capture_end notes that the graph holds cached
+// buffers, and rf_graph_replay refuses it once an entry has been dropped.
+// Once the context's workspaces are fixed (rf_ctx_reserve), no entry is
+// added: a miss would allocate.
+static int32_t repack_lookup(rf_ctx* ctx, uint32_t t, const void* w, uint64_t rows, uint64_t in_dim, uint64_t rb,
+                             hipStream_t st, const void** out) {
+  *out = nullptr;
+  if (!packed_type(t) || !plan_packed(t, in_dim).ok) return RF_OK;
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  RF_HIP(hipStreamIsCapturing(st, &cs), "hipStreamIsCapturing");
+  const bool capturing = cs != hipStreamCaptureStatusNone;
+  RepackCache& c = ctx->repack;
+  std::lock_guard<std::mutex> lk(c.mu);
+  const uint8_t* src = static_cast<const uint8_t*>(w);
+  for (auto& en : c.entries) {
+    if (en.src != src || en.type != t || en.rows != rows || en.in_dim != in_dim) continue;
+    if (capturing) {
+      if (!en.settled) return RF_OK;
+      ++c.captured_hits;
+    } else {
+      if (!en.settled && hipEventQuery(en.ready) == hipSuccess) en.settled = true;
+      if (!en.settled && en.packed_on != st) RF_HIP(hipStreamWaitEvent(st, en.ready, 0), "hipStreamWaitEvent");
+    }
+    en.last_use = ++c.clock;
+    ++c.hits;
+    *out = en.packed;
+    return RF_OK;
+  }
+  if (capturing || ctx->ws_fixed) return RF_OK;
+  const uint64_t bytes = rows * rb;
+  int32_t rc = RF_OK;
+  if (!repack_make_room(ctx, bytes, &rc)) return rc;
+  RepackEntry en;
+  en.src = src;
+  en.type = t;
+  en.rows = rows;
+  en.in_dim = in_dim;
+  en.bytes = bytes;
+  en.charge = "workspace:repack:" + std::to_string(++c.seq);
+  if (vram_alloc(ctx, en.charge, bytes, &en.packed) != RF_OK) return RF_OK;  // the GGUF kernel instead
+  hipError_t e = launch_pack(t, w, en.packed, rows, in_dim, st);
+  if (e == hipSuccess) e = hipEventCreateWithFlags(&en.ready, hipEventDisableTiming);
+  if (e == hipSuccess) e = hipEventRecord(en.ready, st);
+  if (e != hipSuccess) {
+    if (en.ready) hipEventDestroy(en.ready);
+    hipStreamSynchronize(st);  // the pack may be queued on the buffer
+    vram_release(ctx, en.charge);
+    return hip_error(e, "repack");
+  }
+  en.packed_on = st;
+  en.last_use = ++c.clock;
+  ++c.misses;
+  c.bytes += bytes;
+  *out = en.packed;
+  c.entries.push_back(std::move(en));
+  return RF_OK;
+}
+
+int32_t rf_matvec_cache(rf_ctx* ctx, uint64_t max_bytes) {
+  RF_CHECK_CTX(ctx);
+  RepackCache& c = ctx->repack;
+  std::lock_guard<std::mutex> lk(c.mu);
+  c.limit = max_bytes;
+  if (c.bytes <= max_bytes) return RF_OK;
+  // drop least-recently-used entries down to the new limit
+  std::vector<uint64_t> uses;
+  for (auto& en : c.entries) uses.push_back(en.last_use);
+  std::sort(uses.begin(), uses.end());
+  uint64_t left = c.bytes, cut = 0;
+  for (uint64_t u : uses) {
+    if (left <= max_bytes) break;
+    for (auto& en : c.entries)
+      if (en.last_use == u) left -= en.bytes;
+    cut = u;
+  }
+  return repack_drop(ctx, [cut](const RepackEntry& en) { return en.last_use <= cut; });
+}
+
+int32_t rf_matvec_cache_forget(rf_ctx* ctx, const void* base, uint64_t bytes) {
+  RF_CHECK_CTX(ctx);
+  RepackCache& c = ctx->repack;
+  std::lock_guard<std::mutex> lk(c.mu);
+  const uint8_t* lo = static_cast<const uint8_t*>(base);
+  const uint8_t* hi = lo + bytes;
+  return repack_drop(ctx, [lo, hi](const RepackEntry& en) { return en.src < hi && lo < en.src + en.bytes; });
+}
+
+int32_t rf_matvec_cache_stats(rf_ctx* ctx, uint64_t* entries, uint64_t* bytes, uint64_t* hits, uint64_t* misses) {
+  RF_CHECK_CTX(ctx);
+  RepackCache& c = ctx->repack;
+  std::lock_guard<std::mutex> lk(c.mu);
+  if (entries) *entries = c.entries.size();
+  if (bytes) *bytes = c.bytes;
+  if (hits) *hits = c.hits;
+  if (misses) *misses = c.misses;
+  return RF_OK;
+}
+
 int32_t rf_matvec(rf_ctx* ctx, uint32_t t, const void* w, uint64_t w_bytes, uint64_t out_dim, uint64_t in_dim,
                   const float* x, float* y, uint64_t row_start, uint64_t row_count, rf_stream_t s) {
   RF_CHECK_CTX(ctx);
@@ -607,8 +790,15 @@ int32_t rf_matvec(rf_ctx* ctx, uint32_t t, const void* w, uint64_t w_bytes, uint
   int32_t rc = validate_matvec(ctx, t, w, w_bytes, out_dim, in_dim, x, y, row_start, row_count, s, &count, &rb,
                                &done);
   if (rc || done) return rc;
+  hipStream_t st = pick_stream(ctx, s);
+  if (ctx->repack.limit) {
+    const void* packed = nullptr;
+    rc = repack_lookup(ctx, t, w, out_dim, in_dim, rb, st, &packed);
+    if (rc) return rc;
+    if (packed) return launch_packed_rows(ctx, t, packed, out_dim, in_dim, x, y, row_start, count, st);
+  }
   MvSegDesc seg{static_cast<const uint8_t*>(w) + row_start * rb, nullptr, y, nullptr, count};
-  hipError_t e = launch_matvec_segments(t, &seg, 1, x, nullptr, 0.f, in_dim, EPI_STORE, pick_stream(ctx, s));
+  hipError_t e = launch_matvec_segments(t, &seg, 1, x, nullptr, 0.f, in_dim, EPI_STORE, st);
   if (e != hipSuccess) return hip_error(e, "matvec launch");
   return RF_OK;
 }
@@ -660,19 +850,7 @@ int32_t rf_matvec_packed(rf_ctx* ctx, uint32_t t, const void* packed, uint64_t p
     return set_error(RF_ERR_UNSUPPORTED,
                      "packed %s matvec stages x in LDS: in_dim %llu exceeds this device's workgroup LDS",
                      type_name(t), (unsigned long long)in_dim);
-  hipStream_t st = pick_stream(ctx, s);
-  const float* xa = x;
-  if ((reinterpret_cast<uintptr_t>(x) & 15u) != 0) {
-    // the kernel reads x with 16-byte loads: stage a misaligned x in the context scratch
-    rc = ensure_workspace(ctx, ctx->scratch_ws, "workspace:scratch", in_dim * 4, st);
-    if (rc) return rc;
-    RF_HIP(hipMemcpyAsync(ctx->scratch_ws.ptr, x, in_dim * 4, hipMemcpyDeviceToDevice, st), "hipMemcpyAsync");
-    xa = static_cast<const float*>(ctx->scratch_ws.ptr);
-  }
-  PkSegDesc seg{packed, nullptr, out_dim, row_start, count, y, nullptr};
-  hipError_t e = launch_matvec_packed(t, &seg, 1, xa, nullptr, 0.f, in_dim, EPI_STORE, st);
-  if (e != hipSuccess) return hip_error(e, "packed matvec launch");
-  return RF_OK;
+  return launch_packed_rows(ctx, t, packed, out_dim, in_dim, x, y, row_start, count, pick_stream(ctx, s));
 }
 
 uint64_t rf_matmul_workspace_bytes(uint64_t out_dim, uint64_t in_dim, uint64_t n_tokens) {
@@ -950,10 +1128,20 @@ struct rf_graph_h {
   hipGraph_t g = nullptr;
   hipGraphExec_t x = nullptr;
   uint64_t ws_generation = 0;  // the context's workspace generation at capture
+  bool repack = false;         // holds rf_matvec calls served by the repack cache
+  uint64_t repack_generation = 0;
 };
+
+static thread_local uint64_t t_capture_hits = 0;  // repack hits before this thread's capture began
 
 int32_t rf_capture_begin(rf_ctx* ctx) {
   RF_CHECK_CTX(ctx);
+  {
+    // completed packs become usable inside the capture
+    std::lock_guard<std::mutex> lk(ctx->repack.mu);
+    repack_settle(ctx->repack);
+    t_capture_hits = ctx->repack.captured_hits;
+  }
   RF_HIP(hipStreamBeginCapture(ctx->compute, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
   return RF_OK;
 }
@@ -973,6 +1161,11 @@ int32_t rf_capture_end(rf_ctx* ctx, void** graph) {
   h->g = g;
   h->x = x;
   h->ws_generation = ctx->ws_generation;
+  {
+    std::lock_guard<std::mutex> lk(ctx->repack.mu);
+    h->repack = ctx->repack.captured_hits != t_capture_hits;
+    h->repack_generation = ctx->repack.generation;
+  }
   *graph = h;
   return RF_OK;
 }
@@ -985,6 +1178,13 @@ int32_t rf_graph_replay(rf_ctx* ctx, void* graph, uint32_t reps, float* ms_per_r
     return set_error(RF_ERR_INVALID,
                      "graph captured before a context workspace was reallocated (it holds the freed buffer); "
                      "capture it again");
+  if (h->repack) {
+    std::lock_guard<std::mutex> lk(ctx->repack.mu);
+    if (h->repack_generation != ctx->repack.generation)
+      return set_error(RF_ERR_INVALID,
+                       "graph holds rf_matvec calls served by the repack cache, which has dropped entries since "
+                       "(the graph may hold a freed copy); capture it again");
+  }
   hipEvent_t a = nullptr, b = nullptr;
   RF_HIP(hipEventCreate(&a), "hipEventCreate");
   hipError_t e = hipEventCreate(&b);
