@@ -140,6 +140,7 @@ struct rf_model {
   void* reader_user = nullptr;
   void* rstage[2] = {nullptr, nullptr};
   hipEvent_t rstage_ev[2] = {nullptr, nullptr};
+  hipEvent_t up2 = nullptr;  // a streamed layer's copies on the second upload stream ended
   uint64_t rstage_bytes = 0;
   void* rraw = nullptr;
   uint64_t rraw_bytes = 0;
@@ -517,21 +518,71 @@ int32_t abort_pass(rf_model* m, int32_t rc) {
 // charged "layer:{i}:{name}" before its buffer is allocated, then uploaded
 // from the pinned host copy on the copy stream.  On failure every charge made
 // for the layer is released and the layer stays host-only.
+// Whether layer v's resident buffers can hold layer li: the same tensors
+// streamed, with the same sizes (all blocks of one model, in practice).
+bool same_layout(rf_model* m, uint32_t v, uint32_t li) {
+  DevTensor *a[12], *b[12];
+  layer_slots(m->layers[v], a);
+  layer_slots(m->layers[li], b);
+  for (int i = 0; i < 12; ++i) {
+    if (a[i]->streamed() != b[i]->streamed()) return false;
+    if (a[i]->streamed() && (a[i]->nbytes != b[i]->nbytes || !a[i]->d)) return false;
+  }
+  return true;
+}
+
+// The layer whose buffers load_layer takes over instead of freeing them and
+// allocating new ones: a retired layer first, then the cache's victim (the
+// order make_headroom frees in).  -1 when none has li's layout.
+int64_t recycle_candidate(rf_model* m, uint32_t li) {
+  for (uint32_t v = 0; v < m->res.size(); ++v)
+    if (v != li && m->res[v].state == LAYER_RETIRED && same_layout(m, v, li)) return v;
+  if (m->lru.empty()) return -1;
+  const uint32_t v = pick_victim(m);
+  return same_layout(m, v, li) ? (int64_t)v : -1;
+}
+
+// Layer v's buffers become layer li's: its charges are renamed "layer:{li}:*"
+// (the ledger's release of v and charge of li in one step, the same bytes),
+// and the copy stream waits on the GPU for v's last kernel before writing
+// them.  An eviction (release_layer + load) with no hipFree, hipMalloc or
+// host wait in between.
+int32_t adopt_buffers(rf_model* m, uint32_t v, uint32_t li) {
+  LayerRes& V = m->res[v];
+  hipError_t e = hipStreamWaitEvent(m->ctx->copy, V.used, 0);
+  if (e == hipSuccess) e = hipStreamWaitEvent(m->ctx->copy2, V.used, 0);
+  if (e != hipSuccess) return hip_error(e, "wait for the recycled layer's kernels");
+  const bool cached = V.state == LAYER_CACHED;
+  const std::string to = "layer:" + std::to_string(li) + ":";
+  int32_t rc = vram_rename_prefix(m->ctx, (cached ? "cache:layer:" : "layer:") + std::to_string(v) + ":", to);
+  if (rc) return rc;
+  DevTensor *a[12], *b[12];
+  layer_slots(m->layers[v], a);
+  layer_slots(m->layers[li], b);
+  for (int i = 0; i < 12; ++i) {
+    if (!a[i]->streamed()) continue;
+    b[i]->d = a[i]->d;
+    b[i]->charge = to + slot_name(i);
+    a[i]->d = nullptr;
+    a[i]->charge.clear();
+  }
+  if (cached) {
+    m->lru.remove(v);
+    m->cache_used -= V.bytes;
+    m->st_evictions += 1;
+  }
+  V.state = LAYER_HOST;
+  return RF_OK;
+}
+
 int32_t load_layer(rf_model* m, uint32_t li) {
   LayerRes& R = m->res[li];
-  int32_t rc = make_headroom(m, R.bytes);
-  if (rc == RF_ERR_BUDGET)
-    return set_error(RF_ERR_BUDGET,
-                     "insufficient memory: layer %u needs %llu bytes, %llu of %llu in use after evicting every cached "
-                     "layer",
-                     li, (unsigned long long)R.bytes, (unsigned long long)m->ctx->ledger.used(),
-                     (unsigned long long)m->ctx->ledger.total());
-  if (rc) return rc;
   DevTensor* t[12];
   layer_slots(m->layers[li], t);
-  hipStream_t cs = m->ctx->copy;
+  hipStream_t cs = m->ctx->copy, cs2 = m->ctx->copy2;
   auto rollback = [&](int32_t code) {  // release every charge of this layer
     hipStreamSynchronize(cs);
+    hipStreamSynchronize(cs2);
     for (DevTensor* y : t)
       if (y->d) {
         vram_release(m->ctx, y->charge);
@@ -540,26 +591,56 @@ int32_t load_layer(rf_model* m, uint32_t li) {
       }
     return code;
   };
+  int32_t rc = RF_OK;
+  const int64_t v = vram_can_allocate(m->ctx, R.bytes) ? -1 : recycle_candidate(m, li);
+  if (v >= 0) {
+    if ((rc = adopt_buffers(m, (uint32_t)v, li))) return rc;
+  } else {
+    rc = make_headroom(m, R.bytes);
+    if (rc == RF_ERR_BUDGET)
+      return set_error(RF_ERR_BUDGET,
+                       "insufficient memory: layer %u needs %llu bytes, %llu of %llu in use after evicting every "
+                       "cached layer",
+                       li, (unsigned long long)R.bytes, (unsigned long long)m->ctx->ledger.used(),
+                       (unsigned long long)m->ctx->ledger.total());
+    if (rc) return rc;
+    for (int i = 0; i < 12; ++i) {
+      DevTensor* x = t[i];
+      if (!x->streamed()) continue;
+      const std::string charge = "layer:" + std::to_string(li) + ":" + slot_name(i);
+      void* d = nullptr;
+      rc = vram_alloc(m->ctx, charge, x->nbytes, &d);
+      if (rc) return rollback(rc);
+      x->d = d;
+      x->charge = charge;
+    }
+  }
+  // The copies go to whichever of the two upload streams has been given
+  // fewer of this layer's bytes: each copy carries a fixed setup cost
+  // (about 40 us between back-to-back copies on one stream, measured), which
+  // the other stream's transfer hides.
   bool sourced = false;
+  uint64_t given[2] = {0, 0};
   for (int i = 0; i < 12; ++i) {
     DevTensor* x = t[i];
     if (!x->streamed()) continue;
-    const std::string charge = "layer:" + std::to_string(li) + ":" + slot_name(i);
-    void* d = nullptr;
-    rc = vram_alloc(m->ctx, charge, x->nbytes, &d);
-    if (rc) return rollback(rc);
-    x->d = d;
-    x->charge = charge;
     if (x->src) {
       sourced = true;
       continue;
     }
-    const hipError_t e = hipMemcpyAsync(d, x->host, x->nbytes, hipMemcpyHostToDevice, cs);
+    const int k = given[1] < given[0] ? 1 : 0;
+    given[k] += x->nbytes;
+    const hipError_t e = hipMemcpyAsync(x->d, x->host, x->nbytes, hipMemcpyHostToDevice, k ? cs2 : cs);
     if (e != hipSuccess) return rollback(hip_error(e, "layer upload"));
     m->st_uploaded += x->nbytes;
   }
   if (sourced && (rc = read_layer_sources(m, li, t, cs))) return rollback(rc);
-  hipError_t e = hipEventRecord(R.uploaded, cs);
+  hipError_t e = hipSuccess;
+  if (given[1]) {  // the second stream's copies join the first before the layer counts as uploaded
+    e = hipEventRecord(m->up2, cs2);
+    if (e == hipSuccess) e = hipStreamWaitEvent(cs, m->up2, 0);
+  }
+  if (e == hipSuccess) e = hipEventRecord(R.uploaded, cs);
   if (e == hipSuccess) e = hipEventRecord(R.used, m->ctx->compute);  // not in use yet
   if (e != hipSuccess) return hip_error(e, "hipEventRecord");
   R.state = LAYER_ACTIVE;
@@ -589,7 +670,8 @@ int32_t acquire_layer(rf_model* m, uint32_t li, bool prefetch) {
     m->st_hits += 1;
     return RF_OK;
   }
-  if (prefetch && !vram_can_allocate(m->ctx, R.bytes) && m->lru.empty()) return RF_OK;
+  if (prefetch && !vram_can_allocate(m->ctx, R.bytes) && m->lru.empty() && recycle_candidate(m, li) < 0)
+    return RF_OK;
   int32_t rc = load_layer(m, li);
   if (prefetch && rc == RF_ERR_BUDGET) return RF_OK;
   if (rc == RF_OK) m->st_misses += 1;
@@ -1572,6 +1654,7 @@ void rf_model_destroy(rf_model* m) {
   reset_graph(m);
   hipStreamSynchronize(m->ctx->compute);
   hipStreamSynchronize(m->ctx->copy);
+  hipStreamSynchronize(m->ctx->copy2);
   for (uint32_t li = 0; li < m->res.size(); ++li) {
     layer_free(m, li);
     DevTensor* t[12];
@@ -1581,6 +1664,7 @@ void rf_model_destroy(rf_model* m) {
     if (m->res[li].uploaded) hipEventDestroy(m->res[li].uploaded);
     if (m->res[li].used) hipEventDestroy(m->res[li].used);
   }
+  if (m->up2) hipEventDestroy(m->up2);
   for (auto it = m->charges.rbegin(); it != m->charges.rend(); ++it) vram_release(m->ctx, *it);
   for (DevTensor* x : {&m->token_embd, &m->output, &m->output_norm})
     if (x->host) hipHostFree(x->host);
@@ -1859,6 +1943,10 @@ int32_t rf_model_enable_streaming(rf_model* m, uint64_t layer_cache_bytes) {
   for (LayerRes& R : m->res) {
     hipError_t e = hipEventCreateWithFlags(&R.uploaded, hipEventDisableTiming);
     if (e == hipSuccess) e = hipEventCreateWithFlags(&R.used, hipEventDisableTiming);
+    if (e != hipSuccess) return hip_error(e, "hipEventCreate");
+  }
+  if (!m->up2) {
+    const hipError_t e = hipEventCreateWithFlags(&m->up2, hipEventDisableTiming);
     if (e != hipSuccess) return hip_error(e, "hipEventCreate");
   }
   m->streaming = true;

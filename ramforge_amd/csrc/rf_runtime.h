@@ -74,6 +74,7 @@ struct rf_ctx {
   int device = 0;
   hipStream_t compute = nullptr;
   hipStream_t copy = nullptr;
+  hipStream_t copy2 = nullptr;  // second upload stream: a streamed layer's copies are split over both
   rf::Ledger ledger{0};
   std::mutex mu;
   std::map<std::string, void*> buffers;  // charge name -> device pointer

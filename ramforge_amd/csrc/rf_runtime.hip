@@ -89,18 +89,32 @@ int32_t Ledger::resize(const std::string& name, uint64_t bytes) {
   return RF_OK;
 }
 
-int32_t Ledger::rename_prefix(const std::string& op, const std::string& np) {
-  std::vector<std::pair<std::string, std::string>> ren;
-  for (auto& kv : allocs_)
-    if (kv.first.compare(0, op.size(), op) == 0) ren.emplace_back(kv.first, np + kv.first.substr(op.size()));
-  if (ren.empty()) return set_error(RF_ERR_BUDGET, "allocation '%s' not found", op.c_str());
-  for (auto& r : ren)
-    if (allocs_.count(r.second)) return set_error(RF_ERR_BUDGET, "allocation '%s' already exists", r.second.c_str());
-  for (auto& r : ren) {
-    const uint64_t b = allocs_[r.first];
-    allocs_.erase(r.first);
-    allocs_[r.second] = b;
+// Keys that start with a prefix form one contiguous range of an ordered map,
+// from lower_bound(prefix) on; renames walk that range only and re-key the
+// nodes in place (the streaming tier renames a layer's charges twice a step).
+template <class M>
+static void prefix_keys(const M& m, const std::string& op, std::vector<std::string>* out) {
+  for (auto it = m.lower_bound(op); it != m.end() && it->first.compare(0, op.size(), op) == 0; ++it)
+    out->push_back(it->first);
+}
+template <class M>
+static void rekey(M& m, const std::vector<std::string>& keys, const std::string& op, const std::string& np) {
+  for (const std::string& k : keys) {
+    auto nh = m.extract(k);
+    nh.key() = np + k.substr(op.size());
+    m.insert(std::move(nh));
   }
+}
+
+int32_t Ledger::rename_prefix(const std::string& op, const std::string& np) {
+  std::vector<std::string> keys;
+  prefix_keys(allocs_, op, &keys);
+  if (keys.empty()) return set_error(RF_ERR_BUDGET, "allocation '%s' not found", op.c_str());
+  for (const std::string& k : keys) {
+    const std::string n = np + k.substr(op.size());
+    if (allocs_.count(n)) return set_error(RF_ERR_BUDGET, "allocation '%s' already exists", n.c_str());
+  }
+  rekey(allocs_, keys, op, np);
   return RF_OK;
 }
 
@@ -142,12 +156,9 @@ int32_t vram_rename_prefix(rf_ctx* ctx, const std::string& o, const std::string&
   std::lock_guard<std::mutex> lk(ctx->mu);
   int32_t rc = ctx->ledger.rename_prefix(o, n);
   if (rc) return rc;
-  std::map<std::string, void*> nb;
-  for (auto& kv : ctx->buffers) {
-    if (kv.first.compare(0, o.size(), o) == 0) nb[n + kv.first.substr(o.size())] = kv.second;
-    else nb[kv.first] = kv.second;
-  }
-  ctx->buffers.swap(nb);
+  std::vector<std::string> keys;
+  prefix_keys(ctx->buffers, o, &keys);
+  rekey(ctx->buffers, keys, o, n);
   return RF_OK;
 }
 
@@ -320,6 +331,7 @@ int32_t rf_ctx_create(int32_t device, uint64_t budget, rf_ctx** out) {
   c->ledger = Ledger(budget ? budget : (uint64_t)total_b);
   hipError_t e = hipStreamCreateWithFlags(&c->compute, hipStreamNonBlocking);
   if (e == hipSuccess) e = hipStreamCreateWithFlags(&c->copy, hipStreamNonBlocking);
+  if (e == hipSuccess) e = hipStreamCreateWithFlags(&c->copy2, hipStreamNonBlocking);
   if (e != hipSuccess) {
     const int32_t rc = hip_error(e, "hipStreamCreate");
     rf_ctx_destroy(c);  // the stream that was created, if any
@@ -370,6 +382,7 @@ void rf_ctx_destroy(rf_ctx* ctx) {
   }
   if (ctx->compute) hipStreamDestroy(ctx->compute);
   if (ctx->copy) hipStreamDestroy(ctx->copy);
+  if (ctx->copy2) hipStreamDestroy(ctx->copy2);
   delete ctx;
 }
 
@@ -389,6 +402,7 @@ int32_t rf_ctx_synchronize(rf_ctx* ctx) {
   RF_CHECK_CTX(ctx);
   RF_HIP(hipStreamSynchronize(ctx->compute), "hipStreamSynchronize");
   RF_HIP(hipStreamSynchronize(ctx->copy), "hipStreamSynchronize");
+  RF_HIP(hipStreamSynchronize(ctx->copy2), "hipStreamSynchronize");
   return RF_OK;
 }
 

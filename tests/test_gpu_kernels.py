@@ -831,3 +831,28 @@ def test_vram_ledger_semantics(ctx):
         assert c.vram_used == base and c.vram_peak >= base + 1000
         with pytest.raises(rf.RamforgeError, match="not found"):
             rf._lib.check(c.lib.rf_vram_release(c.handle, b"layer:9:nothing"))
+
+
+def test_vram_rename_prefix_touches_only_its_prefix(ctx):
+    """Renames act on exactly the charges that start with the prefix
+    ("layer:1:" is not a prefix of "layer:10:"), refuse a rename onto an
+    existing charge without changing anything, and keep each buffer freeable
+    under its new name."""
+    rf = _rf()
+    with rf.Context(0, vram_budget_bytes=1 << 24) as c:
+        base = c.vram_used
+        names = ["layer:1:a", "layer:1:b", "layer:10:a", "layer:2:a", "cache:layer:3:a"]
+        arrs = {n: c.alloc(100 + i, n) for i, n in enumerate(names)}
+        c.rename_prefix("layer:1:", "cache:layer:1:")
+        assert c.charge("cache:layer:1:a") == 100 and c.charge("cache:layer:1:b") == 101
+        assert c.charge("layer:10:a") == 102 and c.charge("layer:1:a") is None
+        with pytest.raises(rf.RamforgeError, match="already exists"):
+            c.rename_prefix("cache:layer:3:", "cache:layer:1:")
+        assert c.charge("cache:layer:3:a") == 104 and c.charge("cache:layer:1:a") == 100
+        with pytest.raises(rf.RamforgeError, match="not found"):
+            c.rename_prefix("layer:7:", "x:")
+        c.rename_prefix("cache:layer:1:", "layer:5:")
+        arrs["layer:1:a"].charge, arrs["layer:1:b"].charge = "layer:5:a", "layer:5:b"
+        for a in arrs.values():
+            a.free()
+        assert c.vram_used == base
