@@ -414,11 +414,14 @@ def pinned_h2d_gbs(ctx, nbytes: int = 256 << 20, reps: int = 8) -> float:
     return nbytes * reps / (ms * 1e-3) / 1e9
 
 
-def config5_bench(rf, syn, tokens: int, prompt_len: int, policy: int) -> dict:
+def config5_bench(rf, syn, tokens: int, prompt_len: int, policy: int, persistent: int = 0) -> dict:
     """8B shape, Q4_K body + Q6_K output, VRAM budget 4 GiB:
     the layers that do not fit stream from pinned host memory each token
-    (LRU layer cache on the device, uploads on the copy stream overlapped
-    with the previous layer's kernels)."""
+    (layer cache on the device with LRU or next-use eviction, uploads on the
+    copy streams overlapped with the previous layers' kernels).  persistent:
+    0 keeps the embedding and output resident by the reference's 25% rule,
+    3 keeps the embedding table in mapped host memory (a step reads one
+    row), leaving its VRAM to cached layers."""
     import numpy as np
 
     cfg = syn.CONFIG_8B
@@ -431,7 +434,7 @@ def config5_bench(rf, syn, tokens: int, prompt_len: int, policy: int) -> dict:
     # context 8192 (2 GiB of f32 K/V at full length), the cache starting at the
     # prompt's length and growing in 256-position chunks as the reference's does
     m = syn.build_device_model(ctx, cfg, specs, cfg["context_length"], stream_cache_bytes=budget,
-                               cache_policy=policy, kv_initial=prompt_len)
+                               cache_policy=policy, kv_initial=prompt_len, persistent_policy=persistent)
     fixed = ctx.vram_used
     layer = syn.weight_bytes([s for s in specs if s.name.startswith("blk.0.")])
     log(f"config 5: built in {time.perf_counter() - t0:.1f} s; fixed VRAM {fixed / 1e9:.2f} GB, "
@@ -451,7 +454,10 @@ def config5_bench(rf, syn, tokens: int, prompt_len: int, policy: int) -> dict:
     up = st["uploaded_bytes"] - pre["uploaded_bytes"]
     out = {"workload": "config 5: 8B shape, Q4_K body + Q6_K output, context 8192, 4 GiB VRAM budget, layers "
                        "streamed from pinned host memory, KV cache grown in 256-position chunks",
-           "cache_policy": ["lru", "next-use"][policy], "tokens": tokens, "tok_s": round(tokens / wall, 3),
+           "cache_policy": ["lru", "next-use"][policy],
+           "persistent": {0: "embedding and output resident (25% rule)",
+                          3: "embedding in mapped host memory, output resident"}[persistent],
+           "tokens": tokens, "tok_s": round(tokens / wall, 3),
            "kv_positions": m.kv_positions(),
            "ms_per_token": round(wall * 1e3 / tokens, 2), "uploaded_GB_per_token": round(up / tokens / 1e9, 3),
            "prompt_tokens": prompt_len, "prompt_prefill_s": round(prompt_s, 3),
@@ -611,7 +617,8 @@ def main() -> int:
     if args.matvec_probe:
         return matvec_probe(rf, args.matvec_probe)
     if args.config5:
-        res = [config5_bench(rf, syn, args.config5, args.prompt, policy) for policy in (1, 0)]
+        res = [config5_bench(rf, syn, args.config5, args.prompt, policy, persistent)
+               for policy, persistent in ((1, 3), (1, 0), (0, 0))]
         print(json.dumps({"config5": res}), flush=True)
         return 0
     if args.kernels:

@@ -86,8 +86,9 @@ const char *rf_version(void);
 /* Creates a context on HIP device `device` with a device-memory ledger of
  * `vram_budget_bytes` (0 = the device's total memory).  The ledger is the
  * device-domain MemoryBudget (core/src/memory.rs:30-384) that the GPU
- * residency tier charges; the context also owns one compute stream and one
- * copy stream at default priority.  Replaces CpuBackend::new
+ * residency tier charges; the context also owns one compute stream and two
+ * copy streams at default priority (rf_ctx_copy_stream returns the first; the
+ * streaming tier splits a layer's uploads over both).  Replaces CpuBackend::new
  * (runtime/src/backend.rs:72-84) as the compute backend handle. */
 int32_t rf_ctx_create(int32_t device, uint64_t vram_budget_bytes, rf_ctx **out);
 void rf_ctx_destroy(rf_ctx *ctx);
@@ -458,7 +459,11 @@ int32_t rf_model_read_stats(rf_model *model, uint64_t *out);
  * policy 0 (default) keeps token_embd.weight / output.weight resident when
  * its device bytes are at most a quarter of the context's VRAM budget
  * (should_keep_resident) and streams it otherwise; 1 streams both, 2 keeps
- * both resident.  A streamed one stays in mapped pinned host memory (in the
+ * both resident; 3 streams token_embd.weight regardless of its size (a
+ * decode step reads one of its rows, so the VRAM it would take holds cached
+ * layers instead) and applies policy 0 to output.weight (no counterpart in
+ * the reference; for models with an output projection: a tied one reads the
+ * embedding for the logits).  A streamed one stays in mapped pinned host memory (in the
  * device layout) that the kernels read in place: the embedding gather reads
  * one row per token, the logits matvec every row (streamed_matvec_into,
  * persistent.rs:286-463), and no VRAM is charged for it.  Set before those

@@ -635,7 +635,8 @@ class GpuLlamaModel:
     def set_persistent_policy(self, policy: int) -> None:
         """0: token_embd / output resident when at most 25% of the budget, else
         streamed from mapped pinned host memory; 1: always streamed; 2: always
-        resident (streaming models only; before those tensors load)."""
+        resident; 3: token_embd always streamed, output by the 25% rule
+        (streaming models only; before those tensors load)."""
         _lib.check(self.ctx.lib.rf_model_set_persistent_policy(self.handle, policy))
 
     def persistent_streamed(self) -> dict:

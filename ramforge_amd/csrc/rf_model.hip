@@ -926,10 +926,14 @@ int32_t install(rf_model* m, const char* cname, uint32_t t, uint64_t ne0, uint64
     return install_streamed(m, name, slot, t, ne0, ne1, bytes, host, synth, seed, mul, constant);
   if (m->streaming && (name == "token_embd.weight" || name == "output.weight")) {
     // should_keep_resident (persistent.rs:466-470): resident when its device
-    // bytes are at most a quarter of the budget
+    // bytes are at most a quarter of the budget; policy 3 streams the
+    // embedding table regardless (its gather reads one row per token) and
+    // applies that rule to the output projection
     const uint64_t resident = (t == T_F16 || t == T_BF16) ? ne0 * ne1 * 4 : bytes;
-    const bool stream = m->persistent_policy == 1 ||
-                        (m->persistent_policy == 0 && resident > m->ctx->ledger.total() / 4);
+    const bool embd = name == "token_embd.weight";
+    const int pol = m->persistent_policy;
+    const bool by_rule = pol == 0 || (pol == 3 && !embd);
+    const bool stream = pol == 1 || (pol == 3 && embd) || (by_rule && resident > m->ctx->ledger.total() / 4);
     if (stream) {
       reset_graph(m);
       return install_persistent_streamed(m, name, slot, t, ne0, ne1, bytes, host, synth, seed, mul, constant);
@@ -2084,7 +2088,7 @@ int32_t rf_model_profile_read(rf_model* m, double* ms, uint64_t* counts, int32_t
 
 int32_t rf_model_set_persistent_policy(rf_model* m, int32_t policy) {
   if (!m) return set_error(RF_ERR_INVALID, "null model");
-  if (policy < 0 || policy > 2) return set_error(RF_ERR_INVALID, "unknown persistent-weight policy %d", policy);
+  if (policy < 0 || policy > 3) return set_error(RF_ERR_INVALID, "unknown persistent-weight policy %d", policy);
   if (m->token_embd.present() || m->output.present())
     return set_error(RF_ERR_INVALID, "the persistent-weight policy must be set before token_embd / output load");
   m->persistent_policy = policy;

@@ -91,18 +91,22 @@ def weight_bytes(specs: list[TensorSpec]) -> int:
 
 
 def build_device_model(ctx, cfg: dict, specs: list[TensorSpec], kv_capacity: int,
-                       stream_cache_bytes: int | None = None, cache_policy: int = 0, kv_initial: int | None = None):
+                       stream_cache_bytes: int | None = None, cache_policy: int = 0, kv_initial: int | None = None,
+                       persistent_policy: int = 0):
     """A GpuLlamaModel with every tensor generated on the device.  With
     stream_cache_bytes the block tensors go to pinned host memory and layers
-    stream through a device LRU cache of that many bytes; with kv_initial the
-    KV cache starts at that many positions and grows in 256-position chunks
-    up to kv_capacity."""
+    stream through a device LRU cache of that many bytes (cache_policy 1:
+    next-use eviction; persistent_policy: where the embedding and output
+    projection live, see GpuLlamaModel.set_persistent_policy); with
+    kv_initial the KV cache starts at that many positions and grows in
+    256-position chunks up to kv_capacity."""
     from . import GpuLlamaModel
 
     m = GpuLlamaModel(ctx, cfg, kv_capacity, kv_initial=kv_initial)
     if stream_cache_bytes is not None:
         m.enable_streaming(stream_cache_bytes)
         m.set_cache_policy(cache_policy)
+        m.set_persistent_policy(persistent_policy)
     for s in specs:
         m.synth_tensor(s.name, s.ggml_type, s.ne0, s.ne1, s.seed, s.scale_mul, s.constant)
     return m

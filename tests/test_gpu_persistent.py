@@ -87,3 +87,35 @@ def test_quarter_budget_rule():
     h = m.forward(3, 0, want_hidden=True)
     assert np.all(np.isfinite(h))
     m.close(); ctx.close()
+
+
+def test_embedding_only_policy():
+    """Policy 3: the embedding table streamed whatever its size (a step reads
+    one of its rows), the output projection by the 25% rule; the same results
+    as the resident policy."""
+    cfg = STREAM_CFG
+    T = _tiny_tensors(np.random.default_rng(1502), cfg, STREAM_TYPES)
+    sctx, sm = _model(cfg, T, 3)
+    rctx, rm = _model(cfg, T, 2)
+    assert sm.persistent_streamed() == {"token_embd": True, "output": False}
+    assert sctx.charge("persistent:token_embd.weight") is None
+    assert sctx.charge("persistent:output.weight") is not None
+    for pos, tok in enumerate([8, 1, 44]):
+        assert np.array_equal(sm.forward(tok, pos, want_hidden=True), rm.forward(tok, pos, want_hidden=True))
+        assert np.array_equal(sm.logits(), rm.logits())
+    for m in (sm, rm):
+        m.reset()
+    assert sm.generate([4, 5], 12) == rm.generate([4, 5], 12)
+    sm.close(); rm.close()
+    sctx.close(); rctx.close()
+    # with a budget whose quarter holds neither tensor the rule streams the output too
+    cfg2 = dict(STREAM_CFG, vocab_size=8192)
+    T2 = _tiny_tensors(np.random.default_rng(1503), cfg2, dict(STREAM_TYPES, embd=Q8_0, out=Q6_K))
+    rf = _rf()
+    probe = rf.Context(0, 0)
+    base = probe.vram_used
+    probe.close()
+    lb = sum(arr.nbytes for n, (t, a, b, arr) in T2.items() if n.startswith("blk.0."))
+    ctx, m = _model(cfg2, T2, 3, budget=base + 4 * lb + (2 << 20))
+    assert m.persistent_streamed() == {"token_embd": True, "output": True}
+    m.close(); ctx.close()
