@@ -77,21 +77,49 @@ __device__ __forceinline__ bf16x8 mm_codes(const float (&v)[8]) {
   return r;
 }
 
+// Every load of the GEMM is a raw buffer load over one segment's region (all
+// its rows) or over x: an offset at or past the region's size returns zeros
+// and reads nothing, so the loads of a partial slice, of the rows past a
+// segment and of the slices past a split are issued unconditionally.  (With
+// those loads behind branches the compiler could not count the loads in
+// flight and waited for all of them before each slice's MFMAs: the next
+// slice's prefetched weights and x arrived before the current slice could
+// start.)
+typedef __amdgpu_buffer_rsrc_t MmRsrc;
+constexpr int MM_RSRC_WORD3 = 0x00020000;  // raw buffer, 32-bit data (as the decode kernel's)
+constexpr uint32_t MM_OOR = 0xFFFFFFF0u;   // past every region the host allows (< 2^31 bytes)
+
+__device__ __forceinline__ MmRsrc mm_rsrc(const void* base, uint64_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int32_t)bytes, MM_RSRC_WORD3);
+}
+__device__ __forceinline__ uint2 mm_ld8(MmRsrc r, uint32_t off) {
+  const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+  return make_uint2(v[0], v[1]);
+}
+__device__ __forceinline__ uint4 mm_ld16(MmRsrc r, uint32_t off) {
+  const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
+__device__ __forceinline__ uint32_t mm_ld2(MmRsrc r, uint32_t off) {
+  return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
+}
+
 // The MM_ST f16 scales of a slice of one row, kept as loaded: scale j in
 // half j & 1 of word j >> 1, taken out only when step j uses it (mm_scale).
-// One 8-byte load when the slice is whole and 8-byte aligned (K a multiple of
-// 128), else one 2-byte load per step.  Splitting the halves right after the
-// load made every wavefront wait there for all its loads in flight, the
-// weights of the slices ahead included; two registers instead of four also
-// make room for a third wavefront per SIMD.
-__device__ __forceinline__ void mm_load_scales(const uint8_t* sb, uint32_t nst, uint2& sc) {
+// SC8 (K a multiple of 128: whole slices, the four scales 8-byte aligned): one
+// 8-byte load; else one 2-byte load per step.  Splitting the halves right
+// after the load made every wavefront wait there for all its loads in flight,
+// the weights of the slices ahead included; two registers instead of four
+// also make room for a third wavefront per SIMD.
+template <bool SC8>
+__device__ __forceinline__ void mm_load_scales(MmRsrc r, uint32_t off, uint32_t nst, uint2& sc) {
   static_assert(MM_ST == 4, "four scales per slice");
-  if (nst == MM_ST && (reinterpret_cast<uintptr_t>(sb) & 7u) == 0) {
-    sc = *reinterpret_cast<const uint2*>(sb);
+  if constexpr (SC8) {
+    sc = mm_ld8(r, nst ? off : MM_OOR);
   } else {
     uint32_t h[MM_ST];
 #pragma unroll
-    for (uint32_t j = 0; j < MM_ST; ++j) h[j] = j < nst ? (uint32_t)rf_ld_u16(sb + 2 * j) : 0u;
+    for (uint32_t j = 0; j < MM_ST; ++j) h[j] = mm_ld2(r, j < nst ? off + 2u * j : MM_OOR);
     sc = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
   }
 }
@@ -101,19 +129,31 @@ __device__ __forceinline__ uint32_t mm_scale(uint2 sc, int j) {
   return (j & 1) ? w >> 16 : w & 0xFFFFu;
 }
 
+// Bytes of one row in region k of the packed layout (rf_matvec_packed.hip).
+__host__ __device__ inline uint64_t mm_row_bytes(uint32_t t, int k, uint64_t K) {
+  switch (t) {
+    case T_Q8_0: return k == 0 ? K : K / 32 * 2;
+    case T_Q4_0: return k == 0 ? K / 2 : K / 32 * 2;
+    case T_Q4_K: return k == 0 ? K / 2 : K / 256 * 16;
+    default: return k == 0 ? K / 2 : k == 1 ? K / 4 : k == 2 ? K / 256 * 16 : K / 256 * 2;
+  }
+}
+
 // Per-format weight slice (MM_KS elements of one row) of one lane (element
-// group g) and its decode into the B operand of step j.
+// group g) and its decode into the B operand of step j.  nst = 0 (a slice
+// past the split) loads nothing.
 template <uint32_t T> struct MmW;
 
 template <> struct MmW<T_Q8_0> {
+  static constexpr uint32_t NREG = 2;
   uint2 c[MM_ST];
   uint2 sc;
-  __device__ void load(const MmSeg& s, uint32_t row, uint32_t sl, uint32_t g, uint32_t nst, uint32_t K) {
-    const uint8_t* cb = s.reg[0] + (size_t)row * K + sl * MM_KS + 8u * g;
-    const uint8_t* sb = s.reg[1] + ((size_t)row * (K / 32u) + sl * MM_ST) * 2u;
+  template <bool SC8>
+  __device__ void load(const MmRsrc* rs, uint32_t row, uint32_t sl, uint32_t g, uint32_t nst, uint32_t K) {
+    const uint32_t cb = row * K + sl * MM_KS + 8u * g;
 #pragma unroll
-    for (uint32_t j = 0; j < MM_ST; ++j) c[j] = j < nst ? *reinterpret_cast<const uint2*>(cb + 32 * j) : make_uint2(0, 0);
-    mm_load_scales(sb, nst, sc);
+    for (uint32_t j = 0; j < MM_ST; ++j) c[j] = mm_ld8(rs[0], j < nst ? cb + 32u * j : MM_OOR);
+    mm_load_scales<SC8>(rs[1], (row * (K / 32u) + sl * MM_ST) * 2u, nst, sc);
   }
   __device__ void step(int j, uint32_t, bf16x8& b, float& d) const {
     float v[8];
@@ -125,15 +165,16 @@ template <> struct MmW<T_Q8_0> {
 };
 
 template <> struct MmW<T_Q4_0> {
+  static constexpr uint32_t NREG = 2;
   uint2 c[MM_ST];
   uint2 sc;
-  __device__ void load(const MmSeg& s, uint32_t row, uint32_t sl, uint32_t g, uint32_t nst, uint32_t K) {
-    const size_t blk = (size_t)row * (K / 32u) + sl * MM_ST;
-    const uint8_t* cb = s.reg[0] + blk * 16u + 8u * (g & 1u);
-    const uint8_t* sb = s.reg[1] + blk * 2u;
+  template <bool SC8>
+  __device__ void load(const MmRsrc* rs, uint32_t row, uint32_t sl, uint32_t g, uint32_t nst, uint32_t K) {
+    const uint32_t blk = row * (K / 32u) + sl * MM_ST;
+    const uint32_t cb = blk * 16u + 8u * (g & 1u);
 #pragma unroll
-    for (uint32_t j = 0; j < MM_ST; ++j) c[j] = j < nst ? *reinterpret_cast<const uint2*>(cb + 16 * j) : make_uint2(0, 0);
-    mm_load_scales(sb, nst, sc);
+    for (uint32_t j = 0; j < MM_ST; ++j) c[j] = mm_ld8(rs[0], j < nst ? cb + 16u * j : MM_OOR);
+    mm_load_scales<SC8>(rs[1], blk * 2u, nst, sc);
   }
   // elements 8g..8g+7 of a block: low nibbles of bytes 0-7 / 8-15 (g = 0, 1),
   // high nibbles of the same bytes (g = 2, 3): value nibble - 8
@@ -149,16 +190,18 @@ template <> struct MmW<T_Q4_0> {
 
 // A slice is half a 256-element block: sub-blocks 4 hh .. 4 hh + 3.
 template <> struct MmW<T_Q4_K> {
+  static constexpr uint32_t NREG = 2;
   uint2 c[2];  // qs bytes 32 (2 hh + i) + 8g .. + 7: sub-blocks 4 hh + 2i (low nibbles), + 1 (high)
   uint4 h;     // d | dmin << 16, scale bytes 0-3, 4-7, 8-11
   uint32_t hh;
-  __device__ void load(const MmSeg& s, uint32_t row, uint32_t sl, uint32_t g, uint32_t, uint32_t K) {
-    const size_t blk = (size_t)row * (K / 256u) + (sl >> 1);
+  template <bool>
+  __device__ void load(const MmRsrc* rs, uint32_t row, uint32_t sl, uint32_t g, uint32_t nst, uint32_t K) {
+    const uint32_t blk = row * (K / 256u) + (sl >> 1);
     hh = sl & 1u;
-    const uint8_t* cb = s.reg[0] + blk * 128u + 64u * hh + 8u * g;
+    const uint32_t cb = blk * 128u + 64u * hh + 8u * g;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) c[i] = *reinterpret_cast<const uint2*>(cb + 32 * i);
-    h = *reinterpret_cast<const uint4*>(s.reg[1] + blk * 16u);
+    for (int i = 0; i < 2; ++i) c[i] = mm_ld8(rs[0], nst ? cb + 32u * i : MM_OOR);
+    h = mm_ld16(rs[1], nst ? blk * 16u : MM_OOR);
   }
   __device__ uint32_t sbyte(uint32_t i) const {
     const uint32_t w = i < 4 ? h.y : (i < 8 ? h.z : h.w);
@@ -190,19 +233,21 @@ template <> struct MmW<T_Q4_K> {
 // A slice is one 128-element half hh of a block: steps qq = 0..3 cover
 // elements 128 hh + 32 qq + l, l = 0..31 (quant.rs:376-406).
 template <> struct MmW<T_Q6_K> {
+  static constexpr uint32_t NREG = 4;
   uint2 ql[2];  // [p]: ql bytes 64 hh + 32 p + 8g .. + 7
   uint2 qh;     // qh bytes 32 hh + 8g .. + 7
   uint4 sc;     // 16 int8 scales
   uint32_t d, hh;
-  __device__ void load(const MmSeg& s, uint32_t row, uint32_t sl, uint32_t g, uint32_t, uint32_t K) {
-    const size_t blk = (size_t)row * (K / 256u) + (sl >> 1);
+  template <bool>
+  __device__ void load(const MmRsrc* rs, uint32_t row, uint32_t sl, uint32_t g, uint32_t nst, uint32_t K) {
+    const uint32_t blk = row * (K / 256u) + (sl >> 1);
     hh = sl & 1u;
-    const uint8_t* lb = s.reg[0] + blk * 128u + 64u * hh + 8u * g;
+    const uint32_t lb = blk * 128u + 64u * hh + 8u * g;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) ql[i] = *reinterpret_cast<const uint2*>(lb + 32 * i);
-    qh = *reinterpret_cast<const uint2*>(s.reg[1] + blk * 64u + 32u * hh + 8u * g);
-    sc = *reinterpret_cast<const uint4*>(s.reg[2] + blk * 16u);
-    d = rf_ld_u16(s.reg[3] + blk * 2u);
+    for (int i = 0; i < 2; ++i) ql[i] = mm_ld8(rs[0], nst ? lb + 32u * i : MM_OOR);
+    qh = mm_ld8(rs[1], nst ? blk * 64u + 32u * hh + 8u * g : MM_OOR);
+    sc = mm_ld16(rs[2], nst ? blk * 16u : MM_OOR);
+    d = mm_ld2(rs[3], nst ? blk * 2u : MM_OOR);
   }
   __device__ float scale(uint32_t i) const {
     const uint32_t w = i < 4 ? sc.x : (i < 8 ? sc.y : (i < 12 ? sc.z : sc.w));
@@ -252,7 +297,7 @@ __device__ __forceinline__ void mm_split3(float x, __bf16& hi, __bf16& mid, __bf
 // regions do not fit the wide register budget (63 VGPRs spilled): narrow.
 constexpr uint32_t MM_ROWS_NARROW = 8 * 32, MM_ROWS_WIDE = 12 * 32;
 
-template <uint32_t T, int NTT, int NW, int DEPTH>
+template <uint32_t T, int NTT, int NW, int DEPTH, bool SC8>
 __global__ __launch_bounds__(64 * NW) void mm_packed(MmArgs a) {
   // Two x slice buffers, each three bf16 planes [3][NT][MM_XB] and (Q4_K)
   // step sums [MM_ST][NT]: slice s + 1 is loaded (x and weights) while slice
@@ -273,13 +318,20 @@ __global__ __launch_bounds__(64 * NW) void mm_packed(MmArgs a) {
   const uint32_t sl0 = blockIdx.y * a.spp, sl1 = min(a.nslices, sl0 + a.spp);
   // staging: thread -> (token st_t, 32-element block st_b, half st_h) of a slice
   const uint32_t st_t = tid >> 3, st_b = (tid >> 1) & 3u, st_h = tid & 1u;
-  auto nsteps = [&](uint32_t sl) { return min(MM_ST, (K - sl * MM_KS) / 32u); };
+  // steps of slice sl of this split (0 past the split's last slice)
+  auto nsteps = [&](uint32_t sl) { return sl < sl1 ? min(MM_ST, (K - sl * MM_KS) / 32u) : 0u; };
+  MmRsrc rs[MmW<T>::NREG];
+#pragma unroll
+  for (int k = 0; k < (int)MmW<T>::NREG; ++k) rs[k] = mm_rsrc(s.reg[k], (uint64_t)s.rows * mm_row_bytes(T, k, K));
+  const MmRsrc xr = mm_rsrc(a.x, (uint64_t)n * a.ldx * 4u);
   auto fetch_x = [&](uint32_t sl, float4 (&xv)[4]) {
     const bool live = st_t < n && st_b < nsteps(sl);
-    const float* xp = a.x + (size_t)(live ? st_t : 0u) * a.ldx + sl * MM_KS + 32u * st_b + 16u * st_h;
+    const uint32_t off = (st_t * a.ldx + sl * MM_KS + 32u * st_b + 16u * st_h) * 4u;
 #pragma unroll
-    for (int q = 0; q < 4; ++q)
-      xv[q] = live ? *reinterpret_cast<const float4*>(xp + 4 * q) : make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int q = 0; q < 4; ++q) {
+      const auto v = __builtin_amdgcn_raw_buffer_load_b128(xr, live ? off + 16u * q : MM_OOR, 0, 0);
+      xv[q] = make_float4(__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]), __uint_as_float(v[3]));
+    }
   };
   auto put_x = [&](uint32_t buf, const float4 (&xv)[4]) {
     if (st_t >= NT) return;  // whole groups of 8 threads (one token row)
@@ -317,32 +369,23 @@ __global__ __launch_bounds__(64 * NW) void mm_packed(MmArgs a) {
 #pragma unroll
     for (int nt = 0; nt < NTT; ++nt) acc[rt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  // Weights DEPTH - 1 slices ahead (cur, nxt[, nxt2]), x one slice ahead.
+  // Weights DEPTH - 1 slices ahead, x one slice ahead.  The ring of weight
+  // registers rotates by unrolling the slice loop DEPTH times (a copy of the
+  // registers would wait for the loads that fill them).
   static_assert(DEPTH == 2 || DEPTH == 3, "weight ring of two or three slices");
-  MmW<T> cur[2], nxt[2], nxt2[2];
+  typedef MmW<T> Wt[2];
+  auto load_w = [&](Wt& w, uint32_t sl) {
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) w[rt].template load<SC8>(rs, rowc[rt], sl, g, nsteps(sl), K);
+  };
   float4 xv[4];
-  fetch_x(sl0, xv);
-#pragma unroll
-  for (int rt = 0; rt < 2; ++rt) cur[rt].load(s, rowc[rt], sl0, g, nsteps(sl0), K);
-  if (DEPTH == 3 && sl0 + 1 < sl1) {
-#pragma unroll
-    for (int rt = 0; rt < 2; ++rt) nxt[rt].load(s, rowc[rt], sl0 + 1, g, nsteps(sl0 + 1), K);
-  }
-  put_x(0, xv);
-  __syncthreads();
-  for (uint32_t sl = sl0; sl < sl1; ++sl) {
+  // Slice sl with weights w: the next slice's x and the weights of slice
+  // sl + DEPTH - 1 (into the buffer slice sl - 1 used) are requested first.
+  auto run_slice = [&](uint32_t sl, const Wt& w, Wt& refill) {
     const uint32_t cb = (sl - sl0) & 1u, nst = nsteps(sl);
     const bool more = sl + 1 < sl1;
-    if (more) fetch_x(sl + 1, xv);  // next slice's x in flight during this slice's math
-    if constexpr (DEPTH == 3) {
-      if (sl + 2 < sl1) {
-#pragma unroll
-        for (int rt = 0; rt < 2; ++rt) nxt2[rt].load(s, rowc[rt], sl + 2, g, nsteps(sl + 2), K);
-      }
-    } else if (more) {
-#pragma unroll
-      for (int rt = 0; rt < 2; ++rt) nxt[rt].load(s, rowc[rt], sl + 1, g, nsteps(sl + 1), K);
-    }
+    fetch_x(sl + 1, xv);
+    load_w(refill, sl + DEPTH - 1);
     const __bf16* xb = xsb + cb * BUF;
     const float* ss = reinterpret_cast<const float*>(xb + 3 * PLANE);
 #pragma unroll
@@ -352,9 +395,9 @@ __global__ __launch_bounds__(64 * NW) void mm_packed(MmArgs a) {
       float d[2], e[2];
 #pragma unroll
       for (int rt = 0; rt < 2; ++rt) {
-        if constexpr (T == T_Q4_K) cur[rt].step(j, g, b[rt], d[rt], e[rt]);
-        else if constexpr (T == T_Q6_K) cur[rt].step(j, g, b[rt], b2[rt], d[rt], e[rt]);
-        else cur[rt].step(j, g, b[rt], d[rt]);
+        if constexpr (T == T_Q4_K) w[rt].step(j, g, b[rt], d[rt], e[rt]);
+        else if constexpr (T == T_Q6_K) w[rt].step(j, g, b[rt], b2[rt], d[rt], e[rt]);
+        else w[rt].step(j, g, b[rt], d[rt]);
       }
       // All A operands of the step, then the hi / mid / lo MFMAs of every
       // (row tile, token tile) pair in turn: each MFMA's accumulator input
@@ -399,15 +442,26 @@ __global__ __launch_bounds__(64 * NW) void mm_packed(MmArgs a) {
         }
       }
     }
-    if (more) {
-      put_x(cb ^ 1u, xv);  // the other buffer's last reader was slice sl - 1, before the last barrier
-#pragma unroll
-      for (int rt = 0; rt < 2; ++rt) {
-        cur[rt] = nxt[rt];
-        if constexpr (DEPTH == 3) nxt[rt] = nxt2[rt];
-      }
-    }
+    if (more) put_x(cb ^ 1u, xv);  // the other buffer's last reader was slice sl - 1, before the last barrier
     __syncthreads();
+  };
+  Wt wa, wb, wc;
+  fetch_x(sl0, xv);
+  load_w(wa, sl0);
+  if constexpr (DEPTH == 3) load_w(wb, sl0 + 1);
+  put_x(0, xv);
+  __syncthreads();
+  if constexpr (DEPTH == 2) {
+    for (uint32_t sl = sl0; sl < sl1; sl += 2) {
+      run_slice(sl, wa, wb);
+      if (sl + 1 < sl1) run_slice(sl + 1, wb, wa);
+    }
+  } else {
+    for (uint32_t sl = sl0; sl < sl1; sl += 3) {
+      run_slice(sl, wa, wc);
+      if (sl + 1 < sl1) run_slice(sl + 1, wb, wa);
+      if (sl + 2 < sl1) run_slice(sl + 2, wc, wb);
+    }
   }
   float* out = a.part + (size_t)blockIdx.y * n * a.mtot + s.col;
 #pragma unroll
@@ -610,39 +664,52 @@ uint64_t mm_part_floats(const uint64_t* rows, int nseg, uint64_t in_dim, uint64_
 
 static int mm_ntt(uint64_t n) { return (int)((n + 15) / 16); }
 
-template <uint32_t T, int NTT, int NW, int DEPTH>
+template <uint32_t T, int NTT, int NW, int DEPTH, bool SC8>
 static hipError_t mm_launch_t(const MmArgs& a, dim3 grid, hipStream_t st) {
   const uint32_t lds = 2u * (3u * NTT * 16u * MM_XB * 2u + (T == T_Q4_K ? MM_ST * NTT * 16u * 4u : 0u));
   static bool opened = false;
   if (!opened) {
     if (lds > 65536) {
-      hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(mm_packed<T, NTT, NW, DEPTH>),
+      hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(mm_packed<T, NTT, NW, DEPTH, SC8>),
                                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
       if (e != hipSuccess) return e;
     }
     opened = true;
   }
-  hipLaunchKernelGGL((mm_packed<T, NTT, NW, DEPTH>), grid, dim3(64 * NW), lds, st, a);
+  hipLaunchKernelGGL((mm_packed<T, NTT, NW, DEPTH, SC8>), grid, dim3(64 * NW), lds, st, a);
   return hipGetLastError();
 }
 
-template <uint32_t T, int NW, int DEPTH>
+template <uint32_t T, int NW, int DEPTH, bool SC8>
 static hipError_t mm_launch_ntt(const MmArgs& a, dim3 grid, int ntt, hipStream_t st) {
   switch (ntt) {
-    case 1: return mm_launch_t<T, 1, NW, DEPTH>(a, grid, st);
-    case 2: return mm_launch_t<T, 2, NW, DEPTH>(a, grid, st);
-    case 3: return mm_launch_t<T, 3, NW, DEPTH>(a, grid, st);
-    case 4: return mm_launch_t<T, 4, NW, DEPTH>(a, grid, st);
+    case 1: return mm_launch_t<T, 1, NW, DEPTH, SC8>(a, grid, st);
+    case 2: return mm_launch_t<T, 2, NW, DEPTH, SC8>(a, grid, st);
+    case 3: return mm_launch_t<T, 3, NW, DEPTH, SC8>(a, grid, st);
+    case 4: return mm_launch_t<T, 4, NW, DEPTH, SC8>(a, grid, st);
     default: return hipErrorInvalidValue;
   }
 }
 
-template <uint32_t T>
-static hipError_t mm_launch_shape(const MmArgs& a, dim3 grid, int ntt, bool wide, hipStream_t st) {
-  if constexpr (T != T_Q6_K) {
-    if (wide) return mm_launch_ntt<T, 12, 2>(a, grid, ntt, st);
+template <uint32_t T, bool SC8>
+static hipError_t mm_launch_sc(const MmArgs& a, dim3 grid, int ntt, bool wide, hipStream_t st) {
+  if constexpr (T == T_Q6_K) {
+    return mm_launch_ntt<T, 8, 2, SC8>(a, grid, ntt, st);  // a three-slice ring spills at 64 tokens
+  } else {
+    if (wide) return mm_launch_ntt<T, 12, 2, SC8>(a, grid, ntt, st);
+    return mm_launch_ntt<T, 8, 3, SC8>(a, grid, ntt, st);
   }
-  return mm_launch_ntt<T, 8, 3>(a, grid, ntt, st);
+}
+
+// SC8 (Q8_0 / Q4_0 with K a multiple of 128 and 8-byte aligned scale rows):
+// one 8-byte scale load per slice; the K-quants keep their scales in the
+// block headers and take one instantiation.
+template <uint32_t T>
+static hipError_t mm_launch_shape(const MmArgs& a, dim3 grid, int ntt, bool wide, bool sc8, hipStream_t st) {
+  if constexpr (T == T_Q8_0 || T == T_Q4_0) {
+    if (sc8) return mm_launch_sc<T, true>(a, grid, ntt, wide, st);
+  }
+  return mm_launch_sc<T, false>(a, grid, ntt, wide, st);
 }
 
 // The wide shape unless its split fills the CUs clearly worse than the narrow
@@ -665,14 +732,11 @@ hipError_t launch_matmul_packed(uint32_t t, const MmSegDesc* segs, int nseg, con
   if (!al16(x) || ldx % 4 != 0 || ldx < in_dim || !part) return hipErrorInvalidValue;
   if (epi == EPI_SWIGLU && (nseg != 2 || segs[0].rows != segs[1].rows)) return hipErrorInvalidValue;
   const int nreg = t == T_Q6_K ? 4 : 2;
-  auto row_bytes = [&](int k) -> uint64_t {
-    switch (t) {
-      case T_Q8_0: return k == 0 ? in_dim : in_dim / 32 * 2;
-      case T_Q4_0: return k == 0 ? in_dim / 2 : in_dim / 32 * 2;
-      case T_Q4_K: return k == 0 ? in_dim / 2 : in_dim / 256 * 16;
-      default: return k == 0 ? in_dim / 2 : k == 1 ? in_dim / 4 : k == 2 ? in_dim / 256 * 16 : in_dim / 256 * 2;
-    }
-  };
+  auto row_bytes = [&](int k) -> uint64_t { return mm_row_bytes(t, k, in_dim); };
+  // the kernel addresses each segment's regions and x through 32-bit buffer
+  // offsets, with offsets from MM_OOR on reading as zeros
+  if ((uint64_t)n * ldx * 4 >= (1ull << 31)) return hipErrorInvalidValue;
+  bool sc8 = in_dim % MM_KS == 0;
   const bool wide = mm_pick_wide(t, segs, nseg, in_dim, n);
   const uint64_t rpg = wide ? MM_ROWS_WIDE : MM_ROWS_NARROW;
   MmArgs a{};
@@ -687,6 +751,9 @@ hipError_t launch_matmul_packed(uint32_t t, const MmSegDesc* segs, int nseg, con
       a.seg[i].reg[k] = static_cast<const uint8_t*>(d.packed) + off + d.row_start * rb;
       off += d.matrix_rows * rb;
     }
+    for (int k = 0; k < nreg; ++k)
+      if (d.rows * row_bytes(k) >= (1ull << 31)) return hipErrorInvalidValue;
+    sc8 = sc8 && (reinterpret_cast<uintptr_t>(a.seg[i].reg[1]) & 7u) == 0;
     // 8-byte code loads; Q4_K headers and Q6_K scales as 16 bytes
     if ((reinterpret_cast<uintptr_t>(a.seg[i].reg[0]) & 7u) != 0) return hipErrorInvalidValue;
     if (t == T_Q4_K && !al16(a.seg[i].reg[1])) return hipErrorInvalidValue;
@@ -717,10 +784,10 @@ hipError_t launch_matmul_packed(uint32_t t, const MmSegDesc* segs, int nseg, con
   const int ntt = mm_ntt(n);
   hipError_t e;
   switch (t) {
-    case T_Q8_0: e = mm_launch_shape<T_Q8_0>(a, grid, ntt, wide, st); break;
-    case T_Q4_0: e = mm_launch_shape<T_Q4_0>(a, grid, ntt, wide, st); break;
-    case T_Q4_K: e = mm_launch_shape<T_Q4_K>(a, grid, ntt, wide, st); break;
-    default: e = mm_launch_shape<T_Q6_K>(a, grid, ntt, wide, st); break;
+    case T_Q8_0: e = mm_launch_shape<T_Q8_0>(a, grid, ntt, wide, sc8, st); break;
+    case T_Q4_0: e = mm_launch_shape<T_Q4_0>(a, grid, ntt, wide, sc8, st); break;
+    case T_Q4_K: e = mm_launch_shape<T_Q4_K>(a, grid, ntt, wide, false, st); break;
+    default: e = mm_launch_shape<T_Q6_K>(a, grid, ntt, wide, false, st); break;
   }
   if (e != hipSuccess) return e;
   r.nseg = (uint32_t)nseg;
