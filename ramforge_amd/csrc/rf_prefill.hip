@@ -495,6 +495,35 @@ struct MmRedArgs {
   const float* part;
 };
 
+// Sums of the n split partials p[s][0], p[s][stride], ... of NS streams, each
+// in split order.  The loads of a batch (MM_RED_BATCH / NS splits of every
+// stream) are issued before any of its adds (indices past the last split are
+// clamped to it: L2 hits, never added), so a batch costs one memory round
+// trip instead of one per split.
+constexpr uint32_t MM_RED_BATCH = 16;
+__device__ __forceinline__ float4 add4(float4 v, float4 q) {
+  return make_float4(v.x + q.x, v.y + q.y, v.z + q.z, v.w + q.w);
+}
+__device__ __forceinline__ float add4(float v, float q) { return v + q; }
+template <int NS, typename V>
+__device__ __forceinline__ void mm_split_sums(const V* const (&p)[NS], size_t stride, uint32_t n, V (&v)[NS]) {
+  constexpr uint32_t B = MM_RED_BATCH / NS;
+#pragma unroll
+  for (int i = 0; i < NS; ++i) v[i] = p[i][0];
+  for (uint32_t k0 = 1; k0 < n; k0 += B) {
+    V q[NS][B];
+#pragma unroll
+    for (int i = 0; i < NS; ++i)
+#pragma unroll
+      for (uint32_t j = 0; j < B; ++j) q[i][j] = p[i][min(k0 + j, n - 1u) * stride];
+#pragma unroll
+    for (int i = 0; i < NS; ++i)
+#pragma unroll
+      for (uint32_t j = 0; j < B; ++j)
+        if (k0 + j < n) v[i] = add4(v[i], q[i][j]);
+  }
+}
+
 __global__ __launch_bounds__(256) void mm_reduce(MmRedArgs a) {
   const uint64_t e = (uint64_t)blockIdx.x * 256u + threadIdx.x;
   if (e >= (uint64_t)a.n * a.mcols) return;
@@ -504,19 +533,24 @@ __global__ __launch_bounds__(256) void mm_reduce(MmRedArgs a) {
   if (a.nseg > 2 && c >= a.seg[2].col) s = a.seg[2];
   const uint32_t r = c - s.col;
   const size_t stride = (size_t)a.n * a.mtot;
-  const float* p = a.part + (size_t)t * a.mtot + c;
-  float v = p[0];
-  for (uint32_t k = 1; k < a.nsplit; ++k) v += p[k * stride];
   const size_t o = (size_t)t * s.ld + r;
+  const float* pv = a.part + (size_t)t * a.mtot + c;
+  if (a.epi == EPI_SWIGLU) {
+    const float* p2[2] = {pv, a.part + (size_t)t * a.mtot + a.seg[1].col + r};
+    float vu[2];
+    mm_split_sums<2>(p2, stride, a.nsplit, vu);
+    s.y[o] = vu[0] / (1.0f + expf(-vu[0])) * vu[1];  // silu_reference * up (compute.rs:337-361)
+    return;
+  }
+  // the residual (unused otherwise: the output's own element) requested with the partials
+  const float rr = (a.epi == EPI_RESIDUAL ? s.res : s.y)[o];
+  const float* p1[1] = {pv};
+  float v[1];
+  mm_split_sums<1>(p1, stride, a.nsplit, v);
   if (a.epi == EPI_RESIDUAL) {
-    s.y[o] = s.res[o] + v;
-  } else if (a.epi == EPI_SWIGLU) {
-    const float* pu = a.part + (size_t)t * a.mtot + a.seg[1].col + r;
-    float u = pu[0];
-    for (uint32_t k = 1; k < a.nsplit; ++k) u += pu[k * stride];
-    s.y[o] = v / (1.0f + expf(-v)) * u;  // silu_reference * up (compute.rs:337-361)
+    s.y[o] = rr + v[0];
   } else {
-    s.y[o] = s.bias ? v + s.bias[r] : v;
+    s.y[o] = s.bias ? v[0] + s.bias[r] : v[0];
   }
 }
 
@@ -533,31 +567,30 @@ __global__ __launch_bounds__(256) void mm_reduce4(MmRedArgs a) {
   if (a.nseg > 1 && c >= a.seg[1].col) s = a.seg[1];
   if (a.nseg > 2 && c >= a.seg[2].col) s = a.seg[2];
   const uint32_t r = c - s.col;
-  const size_t stride = (size_t)a.n * a.mtot;
-  auto sum = [&](const float* p) {
-    float4 v = *reinterpret_cast<const float4*>(p);
-    for (uint32_t k = 1; k < a.nsplit; ++k) {
-      const float4 q = *reinterpret_cast<const float4*>(p + k * stride);
-      v.x += q.x;
-      v.y += q.y;
-      v.z += q.z;
-      v.w += q.w;
-    }
-    return v;
-  };
-  const float4 v = sum(a.part + (size_t)t * a.mtot + c);
+  const size_t stride = (size_t)a.n * a.mtot / 4;  // float4 units (mtot % 4 == 0)
   const size_t o = (size_t)t * s.ld + r;
-  float4 out = v;
-  if (a.epi == EPI_RESIDUAL) {
-    const float4 rr = *reinterpret_cast<const float4*>(s.res + o);
-    out = make_float4(rr.x + v.x, rr.y + v.y, rr.z + v.z, rr.w + v.w);
-  } else if (a.epi == EPI_SWIGLU) {
-    const float4 u = sum(a.part + (size_t)t * a.mtot + a.seg[1].col + r);
+  const float4* pv = reinterpret_cast<const float4*>(a.part + (size_t)t * a.mtot + c);
+  float4 out;
+  if (a.epi == EPI_SWIGLU) {
+    const float4* p2[2] = {pv, reinterpret_cast<const float4*>(a.part + (size_t)t * a.mtot + a.seg[1].col + r)};
+    float4 vu[2];
+    mm_split_sums<2>(p2, stride, a.nsplit, vu);
+    const float4 v = vu[0], u = vu[1];
     out = make_float4(v.x / (1.0f + expf(-v.x)) * u.x, v.y / (1.0f + expf(-v.y)) * u.y,
                       v.z / (1.0f + expf(-v.z)) * u.z, v.w / (1.0f + expf(-v.w)) * u.w);
-  } else if (s.bias) {
-    const float4 b = *reinterpret_cast<const float4*>(s.bias + r);
-    out = make_float4(v.x + b.x, v.y + b.y, v.z + b.z, v.w + b.w);
+  } else {
+    // the residual (unused otherwise: the output's own elements) requested with the partials
+    const float4 rr = *reinterpret_cast<const float4*>((a.epi == EPI_RESIDUAL ? s.res : s.y) + o);
+    const float4* p1[1] = {pv};
+    float4 v[1];
+    mm_split_sums<1>(p1, stride, a.nsplit, v);
+    out = v[0];
+    if (a.epi == EPI_RESIDUAL) {
+      out = make_float4(rr.x + v[0].x, rr.y + v[0].y, rr.z + v[0].z, rr.w + v[0].w);
+    } else if (s.bias) {
+      const float4 b = *reinterpret_cast<const float4*>(s.bias + r);
+      out = make_float4(v[0].x + b.x, v[0].y + b.y, v[0].z + b.z, v[0].w + b.w);
+    }
   }
   *reinterpret_cast<float4*>(s.y + o) = out;
 }
