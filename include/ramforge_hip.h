@@ -547,6 +547,15 @@ int32_t rf_tune_matvec_digits(int32_t mode);
  * everywhere; other values only query.  Same results either way.  Returns
  * the mode in effect (process-wide). */
 int32_t rf_tune_packed_inflight(int32_t mode);
+/* Decode attention at contexts split per query head (up to 1024 positions
+ * with 32 query heads): 1 = the o-projection merges the chunk records of the
+ * split kernel while staging its x, so no merge kernel is launched (default;
+ * packed Q8_0 / Q4_0 / Q4_K o-projections of q_heads * head_dim up to 4096),
+ * 0 = the merge kernel, then the o-projection; other values only query.  The
+ * two differ in rounding only (the merge's sums in another order).  Applies
+ * to steps enqueued or captured afterwards.  Returns the mode in effect
+ * (process-wide). */
+int32_t rf_tune_attention_merge(int32_t mode);
 /* Weight layout of models created afterwards: 1 = Q8_0 / Q4_0 / Q4_K / Q6_K
  * projection weights are repacked at install into the device-native layout
  * (default; the batched prefill needs it), 0 = kept as GGUF bytes; other

@@ -774,6 +774,15 @@ def tune_packed_inflight(mode: int = -1) -> int:
     return _lib.load().rf_tune_packed_inflight(mode)
 
 
+def tune_attention_merge(mode: int = -1) -> int:
+    """1: in decode steps whose attention splits per query head, the
+    o-projection merges the attention's chunk records while staging its x
+    (no merge kernel; default), 0: the merge kernel, then the o-projection;
+    -1 queries.  The two differ in rounding only.  Returns the mode in
+    effect."""
+    return _lib.load().rf_tune_attention_merge(mode)
+
+
 def tune_packed_weights(mode: int = -1) -> int:
     """1: Q8_0 / Q4_0 / Q4_K / Q6_K projection weights of models are repacked
     into the device-native layout at install (default; the batched prefill

@@ -42,17 +42,10 @@
 namespace rf {
 
 constexpr uint32_t ATT_MAX_CHUNK = 1024;  // positions of one chunk (LDS score rows)
-constexpr uint32_t ATT_MIN_CHUNK = 64;    // 16 position slots x 4 loads in flight
 constexpr int ATT_UNROLL = 4;
 constexpr uint32_t ATT_MAX_SPLITS = 256;
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
-
-__host__ __device__ __forceinline__ uint32_t att_chunk(uint32_t total, uint32_t nsplit) {
-  uint32_t c = (total + nsplit - 1) / nsplit;
-  c = (c + 15u) & ~15u;
-  return c < ATT_MIN_CHUNK ? ATT_MIN_CHUNK : c;
-}
 
 // Rotated element d of a head vector v (half-split RoPE, cs = [half][2] cos/sin).
 __device__ __forceinline__ float rope_elem(const float* v, const float* cs, uint32_t d, uint32_t hd) {
@@ -154,7 +147,7 @@ __global__ __launch_bounds__(64 * W) void attn_split(AttnArgs a) {
   const float* kcur_p = a.ntok ? a.k_hist + (size_t)hist * kvw : a.k_cur;
   const float* vcur_p = a.ntok ? a.v_hist + (size_t)hist * kvw : a.v_cur;
   float* outz = a.out + (size_t)z * a.qh * HD;
-  float* wsz = a.ws + (size_t)z * a.nsplit * a.qh * (HD + 2);
+  float* wsz = a.ws + (size_t)z * a.nsplit * a.qh * att_rec(HD);
   const uint32_t total = hist + 1;
   const uint32_t chunk = att_chunk(total, a.nsplit);
   const uint32_t p0 = sp * chunk;
@@ -352,7 +345,7 @@ __global__ __launch_bounds__(64 * W) void attn_split(AttnArgs a) {
     if (ns == 1) {
       outz[(size_t)qhead * HD + d] = v / lh[h];
     } else {
-      float* w = wsz + ((size_t)sp * a.qh + qhead) * (HD + 2);
+      float* w = wsz + ((size_t)sp * a.qh + qhead) * att_rec(HD);
       w[d] = v;
       if (d == 0) { w[HD] = mh[h]; w[HD + 1] = lh[h]; }
     }
@@ -375,7 +368,7 @@ __global__ __launch_bounds__(64) void attn_merge(AttnArgs a) {
   const uint32_t chunk = att_chunk(total, a.nsplit);
   const uint32_t ns = (total + chunk - 1) / chunk;  // 1 < ns <= nsplit <= ATT_MAX_SPLITS
   if (ns == 1) return;
-  const size_t rec = HD + 2, stride = (size_t)a.qh * rec;
+  const size_t rec = att_rec(HD), stride = (size_t)a.qh * rec;
   const float* base = a.ws + (size_t)z * a.nsplit * stride + (size_t)qhead * rec;
   float pre[B][DPW];
 #pragma unroll
@@ -568,7 +561,7 @@ int attention_regime(uint64_t total, uint32_t qh, uint32_t kvh, uint64_t cap) {
 }
 
 uint64_t attention_ws_floats(uint32_t nsplit, uint32_t qh, uint32_t hd) {
-  return (uint64_t)nsplit * qh * (hd + 2);
+  return (uint64_t)nsplit * qh * att_rec(hd);
 }
 
 template <int G, int DPL, int W, bool PERQ = false>
@@ -622,7 +615,7 @@ hipError_t launch_attention(const AttnArgs& a, hipStream_t st) {
 #undef RF_ATT
   if (!done) return hipErrorInvalidValue;
   hipError_t e = hipGetLastError();
-  if (e != hipSuccess || a.nsplit == 1) return e;
+  if (e != hipSuccess || a.nsplit == 1 || a.defer_merge) return e;
   const dim3 mg(a.qh, 1, a.ntok ? a.ntok : 1);
   switch (a.hd) {
     case 64: hipLaunchKernelGGL(attn_merge<1>, mg, dim3(64), 0, st, a); break;

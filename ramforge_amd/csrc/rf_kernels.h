@@ -94,6 +94,21 @@ struct PkArgs {
   float eps;
   uint32_t in_dim;
   int32_t* advance;  // non-null: workgroup 0 adds 1 to *advance (the model's device position)
+  // Merged x (matvec_packed<..., MRG>): x is the merge of single-query
+  // attention's chunk records (o[hd], m, l at mws[(c * m_qh + h) * att_rec(hd)],
+  // hd = 2^m_hd_log2, m_nsplit chunks per head, the chunk count following
+  // from *m_pos as in the attention kernels); with one chunk, x itself holds
+  // the output.
+  const float* mws;
+  const int32_t* m_pos;
+  uint32_t m_nsplit, m_qh, m_hd_log2;
+};
+// Chunk records of the attention launch that precedes an o-projection which
+// merges them (launch_matvec_packed's mrg argument).
+struct PkMerge {
+  const float* ws;
+  const int32_t* d_pos;
+  uint32_t nsplit, qh, hd;
 };
 struct PkPlan {
   bool ok;
@@ -113,7 +128,13 @@ PkPlan plan_packed(uint32_t t, uint64_t in_dim);
 // advance: optional device counter the launch increments once (nothing in
 // the launch reads it).
 hipError_t launch_matvec_packed(uint32_t t, const PkSegDesc* segs, int nseg, const float* x, const float* norm_w,
-                                float eps, uint64_t in_dim, int epi, hipStream_t st, int32_t* advance = nullptr);
+                                float eps, uint64_t in_dim, int epi, hipStream_t st, int32_t* advance = nullptr,
+                                const PkMerge* mrg = nullptr);
+// True when launch_matvec_packed can merge attention chunk records into x
+// for this projection (EPI_RESIDUAL, no norm, one segment of `rows` rows):
+// the single-step launch of Q8_0 / Q4_0 / Q4_K with in_dim = qh * hd, hd a
+// power of two from 16, at most 8 chunks and nsplit * qh <= 512.
+bool pk_merge_supported(uint32_t t, uint64_t in_dim, uint64_t rows, uint32_t nsplit, uint32_t qh, uint32_t hd);
 // GGUF payload [rows][in_dim] -> packed layout (distinct buffers).
 hipError_t launch_pack(uint32_t t, const void* raw, void* packed, uint64_t rows, uint64_t in_dim, hipStream_t st);
 
@@ -131,7 +152,7 @@ struct AttnArgs {
   const float* k_cur;    // [kvh][hd]
   const float* v_cur;
   float* out;            // [qh][hd]
-  float* ws;             // chunk records [nsplit][qh][hd + 2]
+  float* ws;             // chunk records [nsplit][qh][att_rec(hd)]
   const float* rope;     // model mode: [cap][hd/2][2] cos/sin table, else null
   float* k_store;        // model mode: cache slot base (k_cache), else null
   float* v_store;
@@ -140,8 +161,9 @@ struct AttnArgs {
   uint32_t qh, kvh, hd, nsplit;
   uint32_t waves;        // wavefronts per chunk workgroup (4 or 8); 0: chosen from hist
   uint32_t per_q;        // nonzero: one workgroup per query head and chunk (short contexts)
+  uint32_t defer_merge;  // nonzero: no merge launch (the o-projection merges the chunk records)
   uint32_t ntok;         // nonzero: a batch of ntok queries (prefill): query z at position
-                         // hist + z, q / out [ntok][qh][hd], ws [ntok][nsplit][qh][hd + 2]; every
+                         // hist + z, q / out [ntok][qh][hd], ws [ntok][nsplit][qh][att_rec(hd)]; every
                          // query's own k / v already in the cache (k_hist / v_hist) and rotated
   float denom;           // sqrt(hd) as the reference computes it
 };
@@ -153,6 +175,19 @@ uint32_t attention_waves(uint32_t chunk, uint32_t g_hd);
 // Positions per chunk of a `nsplit`-chunk launch over `total` positions.
 uint32_t att_chunk_positions(uint64_t total, uint32_t nsplit);
 constexpr uint64_t ATT_PREFILL_CHUNK = 1024;  // longest chunk of the split kernel
+constexpr uint32_t ATT_MIN_CHUNK = 64;        // 16 position slots x 4 loads in flight
+// Positions per chunk of an nsplit-chunk split over `total` positions (a
+// multiple of 16, at least ATT_MIN_CHUNK); the chunk count is
+// ceil(total / chunk).  Shared by the attention kernels and the o-projection
+// that merges their chunk records.
+__host__ __device__ __forceinline__ uint32_t att_chunk(uint32_t total, uint32_t nsplit) {
+  uint32_t c = (total + nsplit - 1) / nsplit;
+  c = (c + 15u) & ~15u;
+  return c < ATT_MIN_CHUNK ? ATT_MIN_CHUNK : c;
+}
+// Floats per chunk record of the split kernel: o[hd], m, l and two unused
+// floats, so that records (hd a multiple of 4) start on 16-byte boundaries.
+__host__ __device__ constexpr uint32_t att_rec(uint32_t hd) { return hd + 4; }
 struct AttnShape {
   uint32_t per_q, nsplit, waves;
 };

@@ -364,10 +364,19 @@ struct PkStep {
 // wavefront (its tasks times the steps of a row at most NB) is requested
 // before the prologue and none after it, so a launch makes one memory round
 // trip.
-template <uint32_t T, int EPI, bool NORM, int U, int LPW, int NB, int NT, bool IX, bool ALLF = false>
+//
+// MRG: x is merged from single-query attention's chunk records in the
+// prologue (the merge the attention's own merge kernel does, so that launch
+// is saved): per head, M = max of the chunks' m, factors f_c = exp(m_c - M),
+// L = sum of l_c f_c and x = (sum of f_c o_c) / L, taken as a product with
+// 1 / L.  Each thread merges half a unit (8 elements) over all chunks; the
+// launch sees to 2 nunit = NT and at most 8 chunks.
+template <uint32_t T, int EPI, bool NORM, int U, int LPW, int NB, int NT, bool IX, bool ALLF = false,
+          bool MRG = false>
 __global__ __launch_bounds__(NT) void matvec_packed(PkArgs a) {
   typedef PkFmt<T> F;
   constexpr bool IXE = F::INTX && IX;  // digit planes instead of float x
+  static_assert(!MRG || (!IXE && !NORM && EPI == EPI_RESIDUAL && ALLF), "merged x: one float-x residual step");
   // Non-finite x needs a fallback only where a decode does not multiply each
   // signed code by x: the digit planes, and Q4_K's min term (d sc sum(q x) -
   // dmin m sum(x) gives inf - inf where the reference's (d sc q - dmin m) x
@@ -550,12 +559,52 @@ __global__ __launch_bounds__(NT) void matvec_packed(PkArgs a) {
     return fin;
   };
 
+  // MRG: the (m, l) pair of record tid, then this thread's half of its unit
+  // (thread t: unit t / 2, elements 8 (t % 2) .. + 7) from every chunk, all
+  // before the weights.  Only the valid chunks' records are read (a uniform
+  // count); with a single chunk the attention wrote x itself.
+  uint32_t m_ns = 1, m_head = 0;
+  float2 mlv = make_float2(0.f, 0.f);
+  float4 mo[MRG ? 8 : 1][2];
+  if constexpr (MRG) {
+    const uint32_t total = (uint32_t)(*a.m_pos) + 1u, chunk = att_chunk(total, a.m_nsplit);
+    m_ns = (total + chunk - 1u) / chunk;
+    const uint32_t rec = att_rec(1u << a.m_hd_log2), hmask = (1u << a.m_hd_log2) - 1u;
+    const PkRsrc wsr =
+        __builtin_amdgcn_make_buffer_rsrc((void*)a.mws, 0, (int32_t)(m_ns * a.m_qh * rec * 4u), PK_RSRC_WORD3);
+    if (m_ns > 1u && tid < m_ns * a.m_qh) {  // record tid = chunk * qh + head
+      const auto v = __builtin_amdgcn_raw_buffer_load_b64(wsr, (tid * rec + hmask + 1u) * 4u, 0, 0);
+      mlv = make_float2(__uint_as_float(v[0]), __uint_as_float(v[1]));
+    }
+    const uint32_t j = tid >> 1, js = j / UPS, hh = j % UPS;
+    const uint32_t b = (js >> 6) * 1024u + 16u * (js & 63u);
+    const uint32_t e = (j < nunit && b < crb ? F::unit_elem(b, hh) : 0u) + 8u * (tid & 1u);
+    m_head = e >> a.m_hd_log2;
+    if (m_ns == 1u) {
+      const float4* xs = reinterpret_cast<const float4*>(a.x) + e / 4u;
+      mo[0][0] = xs[0];
+      mo[0][1] = xs[1];
+    } else {
+      const uint32_t off = ((m_head * rec) + (e & hmask)) * 4u, cstride = a.m_qh * rec * 4u;
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        if ((uint32_t)c < m_ns) {  // uniform
+#pragma unroll
+          for (int k = 0; k < 2; ++k) {
+            const auto v = __builtin_amdgcn_raw_buffer_load_b128(wsr, off + c * cstride + 16u * k, 0, 0);
+            mo[c][k] = make_float4(__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]),
+                                   __uint_as_float(v[3]));
+          }
+        }
+      }
+    }
+  }
   // x first: the raw loads of this thread's first unit are issued before
   // any weight step, so the prologue's wait for them does not also wait for
   // the codes requested behind them (a wavefront's loads complete in order).
   float4 xr[4], wr[4];
   bool xin = false;
-  if constexpr (!IXE) {
+  if constexpr (!IXE && !MRG) {
     const uint32_t js = tid / UPS, h = tid % UPS;
     const uint32_t b = (js >> 6) * 1024u + 16u * (js & 63u);
     xin = tid < nunit && b < crb;
@@ -580,9 +629,82 @@ __global__ __launch_bounds__(NT) void matvec_packed(PkArgs a) {
   }
 
   bool finite = true;
+  if constexpr (MRG) {
+    // The merge's per-record work once per workgroup, in LDS behind the unit
+    // sums: (m, l) of every valid record, then per head (one thread each)
+    // M = the largest m, the factors exp(m - M) and 1 / L with L the sum of
+    // l times factor in chunk order.  Each thread then sums factor times o
+    // over the chunks for its 8 elements, scales by 1 / L and stages them;
+    // the unit's sum joins the two halves (adjacent lanes).
+    const uint32_t nrec = a.m_nsplit * a.m_qh;
+    float2* mls = reinterpret_cast<float2*>(xsum_l + nunit);
+    float* fac = reinterpret_cast<float*>(mls + nrec);
+    float* invl = fac + nrec;
+    if (m_ns > 1u) {
+      if (tid < m_ns * a.m_qh) mls[tid] = mlv;
+      __syncthreads();
+      if (tid < a.m_qh) {
+        float M = -INFINITY;
+        for (uint32_t c = 0; c < m_ns; ++c) M = fmaxf(M, mls[c * a.m_qh + tid].x);
+        float L = 0.f;
+        for (uint32_t c = 0; c < m_ns; ++c) {
+          const float2 ml = mls[c * a.m_qh + tid];
+          const float f = expf(ml.x - M);
+          fac[c * a.m_qh + tid] = f;
+          L = fmaf(ml.y, f, L);
+        }
+        invl[tid] = 1.0f / L;
+      }
+      __syncthreads();
+    }
+    const uint32_t j = tid >> 1, half = tid & 1u, js = j / UPS, hh = j % UPS;
+    const bool have = j < nunit && (js >> 6) * 1024u + 16u * (js & 63u) < crb;
+    float v[8];
+    if (m_ns == 1u) {
+#pragma unroll
+      for (int k = 0; k < 2; ++k) {
+        v[4 * k] = mo[0][k].x; v[4 * k + 1] = mo[0][k].y; v[4 * k + 2] = mo[0][k].z; v[4 * k + 3] = mo[0][k].w;
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < 8; ++k) v[k] = 0.f;
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        if ((uint32_t)c < m_ns) {
+          const float f = fac[c * a.m_qh + m_head];
+#pragma unroll
+          for (int k = 0; k < 2; ++k) {
+            v[4 * k] = fmaf(f, mo[c][k].x, v[4 * k]);
+            v[4 * k + 1] = fmaf(f, mo[c][k].y, v[4 * k + 1]);
+            v[4 * k + 2] = fmaf(f, mo[c][k].z, v[4 * k + 2]);
+            v[4 * k + 3] = fmaf(f, mo[c][k].w, v[4 * k + 3]);
+          }
+        }
+      }
+      const float r = invl[m_head];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) v[k] *= r;
+    }
+    // the unit's slots (put_float's layout): this half's two float4
+    float s8 = 0.f;
+    bool fin = true;
+    if (have) {
+      float* dst = xl + (js >> 6) * 64u * EPL + 4u * hh * 256u + 4u * (js & 63u) + 512u * half;
+#pragma unroll
+      for (int k = 0; k < 2; ++k) {
+        *reinterpret_cast<float4*>(dst + 256 * k) = make_float4(v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]);
+        s8 += v[4 * k]; s8 += v[4 * k + 1]; s8 += v[4 * k + 2]; s8 += v[4 * k + 3];
+      }
+#pragma unroll
+      for (int k = 0; k < 8; ++k) fin = fin && fabsf(v[k]) <= 3.40282347e38f;
+    }
+    const float s16 = s8 + __shfl_xor(s8, 1);
+    if (j < nunit && half == 0u) xsum_l[j] = have ? s16 : 0.f;
+    if constexpr (KINDS) finite = fin;
+  }
   {
     float ss = 0.f;
-    for (uint32_t j = tid; j < nunit; j += NT) {
+    for (uint32_t j = tid; j < (MRG ? 0u : nunit); j += NT) {
       if constexpr (IXE) {
         finite = stage_digits(j, ss) && finite;
       } else if (j == tid) {  // the unit loaded above (load_unit's arithmetic)
@@ -1061,6 +1183,59 @@ static hipError_t launch_pk_all(const PkArgs& a, uint32_t lds, hipStream_t st, b
   return launch_pk_all_nb<T, EPI, NORM, LPW, 1>(a, lds, grid, st);
 }
 
+// The single-step launch above with x merged from attention chunk records
+// (matvec_packed<..., MRG>): Q8_0 rows of 4 chunks, Q4_0 / Q4_K rows of 2,
+// with the MRG kernel's own occupancy and LDS (x, its unit sums, then the
+// records' (m, l) pairs and factors and the heads' 1 / L).
+// hipErrorNotSupported when the shape does not take it;
+// with launch false it only says so.
+static bool pk_merge_shape(uint32_t t, uint64_t in_dim, uint32_t nsplit, uint32_t qh, uint32_t hd, uint32_t* lds) {
+  const PkPlan p = plan_packed(t, in_dim);
+  if (!p.ok || !g_inflight) return false;
+  if (t == T_Q8_0 || t == T_Q4_0) {
+    if (g_digits == 2) return false;  // digit planes everywhere: no float-x launch
+  }
+  const uint64_t nchunk = pk_nchunk(t, in_dim);
+  if (!((t == T_Q8_0 && nchunk == 4) || ((t == T_Q4_0 || t == T_Q4_K) && nchunk == 2))) return false;
+  if (hd < 16 || (hd & (hd - 1)) != 0 || (uint64_t)qh * hd != in_dim) return false;
+  if (nsplit < 1 || nsplit > 8 || (uint64_t)nsplit * qh > 512) return false;
+  if (2 * nchunk * 64 * pk_epb(t) != 512) return false;  // two threads per unit of 16 elements
+  const uint64_t l = p.lds_bytes + (uint64_t)nsplit * qh * 12 + (uint64_t)qh * 4;  // (m, l), factors, 1 / L
+  if (l + PK_STATIC_LDS > pk_lds_limit()) return false;
+  *lds = (uint32_t)l;
+  return true;
+}
+
+template <uint32_t T, int LPW>
+static hipError_t launch_pk_merge(const PkArgs& a, uint32_t lds, bool launch, hipStream_t st) {
+  static PkOccCache cache;
+  auto k = matvec_packed<T, EPI_RESIDUAL, false, 1, LPW, 1, 512, false, true, true>;
+  const int occ = pk_occupancy(cache, reinterpret_cast<const void*>(k), 512, lds);
+  const uint64_t nw = 8, cus = (uint64_t)pk_cu_count(), tasks = a.rows_total;
+  const uint64_t grid = (tasks + nw - 1) / nw;
+  if (occ < 1 || grid > cus * (uint64_t)occ || tasks > 2 * cus * nw) return hipErrorNotSupported;
+  if (!launch) return hipSuccess;
+  hipLaunchKernelGGL(k, dim3((uint32_t)grid), dim3(512), lds, st, a);
+  return hipGetLastError();
+}
+
+static hipError_t launch_pk_merge_t(uint32_t t, const PkArgs& a, uint32_t lds, bool launch, hipStream_t st) {
+  switch (t) {
+    case T_Q8_0: return launch_pk_merge<T_Q8_0, 4>(a, lds, launch, st);
+    case T_Q4_0: return launch_pk_merge<T_Q4_0, 2>(a, lds, launch, st);
+    case T_Q4_K: return launch_pk_merge<T_Q4_K, 2>(a, lds, launch, st);
+    default: return hipErrorNotSupported;
+  }
+}
+
+bool pk_merge_supported(uint32_t t, uint64_t in_dim, uint64_t rows, uint32_t nsplit, uint32_t qh, uint32_t hd) {
+  uint32_t lds = 0;
+  if (rows == 0 || rows > 0xFFFFFFFFull || !pk_merge_shape(t, in_dim, nsplit, qh, hd, &lds)) return false;
+  PkArgs a{};
+  a.rows_total = (uint32_t)rows;
+  return launch_pk_merge_t(t, a, lds, false, nullptr) == hipSuccess;
+}
+
 // Launch shape, from timing the 8B projections (Q8_0 and Q4_0; 4096 and
 // 14336 inputs): one row per wavefront; LPW = chunks per step, up to 4 (2 for
 // gate/up, whose step loads two matrices; Q6_K, with three more loads per
@@ -1128,9 +1303,17 @@ static hipError_t launch_pk_t(const PkArgs& a, uint32_t lds, int epi, bool norm,
 static bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 hipError_t launch_matvec_packed(uint32_t t, const PkSegDesc* segs, int nseg, const float* x, const float* norm_w,
-                                float eps, uint64_t in_dim, int epi, hipStream_t st, int32_t* advance) {
+                                float eps, uint64_t in_dim, int epi, hipStream_t st, int32_t* advance,
+                                const PkMerge* mrg) {
   const PkPlan p = plan_packed(t, in_dim);
   if (!p.ok || nseg < 1 || nseg > 3) return hipErrorInvalidValue;
+  uint32_t mlds = 0;
+  if (mrg) {
+    if (epi != EPI_RESIDUAL || norm_w || nseg != 1 || !mrg->ws || !mrg->d_pos ||
+        (reinterpret_cast<uintptr_t>(mrg->ws) & 15u) != 0)
+      return hipErrorInvalidValue;
+    if (!pk_merge_shape(t, in_dim, mrg->nsplit, mrg->qh, mrg->hd, &mlds)) return hipErrorNotSupported;
+  }
   if (!al16(x) || (norm_w && !al16(norm_w))) return hipErrorInvalidValue;
   const bool dual = epi == EPI_SWIGLU;
   const int nreg = pk_nreg(t);
@@ -1166,6 +1349,14 @@ hipError_t launch_matvec_packed(uint32_t t, const PkSegDesc* segs, int nseg, con
   a.eps = eps;
   a.in_dim = (uint32_t)in_dim;
   a.advance = advance;
+  if (mrg) {
+    a.mws = mrg->ws;
+    a.m_pos = mrg->d_pos;
+    a.m_nsplit = mrg->nsplit;
+    a.m_qh = mrg->qh;
+    a.m_hd_log2 = (uint32_t)__builtin_ctz(mrg->hd);
+    return launch_pk_merge_t(t, a, mlds, true, st);
+  }
   switch (t) {
     case T_Q8_0: return launch_pk_t<T_Q8_0>(a, p.lds_bytes, epi, norm_w != nullptr, st);
     case T_Q4_0: return launch_pk_t<T_Q4_0>(a, p.lds_bytes, epi, norm_w != nullptr, st);

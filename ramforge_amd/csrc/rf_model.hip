@@ -1139,6 +1139,20 @@ int attn_regime(const rf_model* m, uint64_t pos) {
   return attention_regime(pos + 1, (uint32_t)m->cfg.head_count, (uint32_t)m->cfg.head_count_kv, m->kv_max);
 }
 
+// Whether layer li's o-projection merges the attention's chunk records
+// itself (matvec_packed's merged-x launch), which saves the merge launch:
+// the regimes that split per query head (at most 8 chunks) and packed
+// Q8_0 / Q4_0 / Q4_K o-projections whose rows take the single-step launch
+// (q_heads * head_dim up to 4096).  rf_tune_attention_merge switches it off.
+static int g_oproj_merge = 1;
+static bool oproj_merges(const rf_model* m, size_t li, const AttnShape& sh) {
+  if (!g_oproj_merge || !m->attn_fast || !sh.per_q || sh.nsplit < 2) return false;
+  const rf_model_config& c = m->cfg;
+  const Layer& L = m->layers[li];
+  return L.o.packed && pk_merge_supported(L.o.type, c.head_count * c.head_dim, c.embedding_length, sh.nsplit,
+                                          (uint32_t)c.head_count, (uint32_t)c.head_dim);
+}
+
 // 2. RoPE + attention + K/V cache write.
 int32_t enqueue_attention(rf_model* m, size_t li) {
   const rf_model_config& c = m->cfg;
@@ -1153,16 +1167,28 @@ int32_t enqueue_attention(rf_model* m, size_t li) {
   // the position this step processes picks the shape
   const AttnShape sh = attention_regime_shape(attn_regime(m, m->seq_len), a.qh, a.kvh, m->kv_max);
   a.per_q = sh.per_q; a.nsplit = sh.nsplit; a.waves = sh.waves;
+  a.defer_merge = oproj_merges(m, li, sh) ? 1u : 0u;
   a.denom = sqrtf((float)hd);
   RF_LAUNCH(m->attn_fast ? launch_attention(a, st) : launch_attention_naive(a, st), "attention");
   return RF_OK;
 }
 
-// 3. o-proj + residual.
+// 3. o-proj + residual (merging the attention's chunk records into its x
+// when oproj_merges).
 int32_t enqueue_oproj(rf_model* m, size_t li) {
   const rf_model_config& c = m->cfg;
   Layer& L = m->layers[li];
   const uint64_t d = c.embedding_length, qd = c.head_count * c.head_dim;
+  const AttnShape sh = attention_regime_shape(attn_regime(m, m->seq_len), (uint32_t)c.head_count,
+                                              (uint32_t)c.head_count_kv, m->kv_max);
+  if (oproj_merges(m, li, sh)) {
+    const PkMerge mg{m->attn_ws, m->d_pos, sh.nsplit, (uint32_t)c.head_count, (uint32_t)c.head_dim};
+    PkSegDesc ps{L.o.d, nullptr, L.o.ne1, 0, d, m->hidden, m->hidden};
+    RF_LAUNCH(launch_matvec_packed(L.o.type, &ps, 1, m->attn_out, nullptr, 0.f, qd, EPI_RESIDUAL, m->ctx->compute,
+                                   nullptr, &mg),
+              "o-proj (merging attention chunks)");
+    return RF_OK;
+  }
   MSeg s{&L.o, nullptr, m->hidden, m->hidden, d};
   RF_LAUNCH(fused_matvec(m, &s, 1, m->attn_out, nullptr, qd, EPI_RESIDUAL), "o-proj");
   return RF_OK;
@@ -1390,7 +1416,7 @@ int32_t ensure_prefill_ws(rf_model* m) {
   take_max({f, f}, d);
   take_max({f}, d);
   take_max({d}, f);
-  const uint64_t att = T * prefill_attn_splits(m->kv_max) * c.head_count * (hd + 2);
+  const uint64_t att = T * prefill_attn_splits(m->kv_max) * c.head_count * att_rec((uint32_t)hd);
   const uint64_t sizes[] = {T * d, T * d, T * qd, T * kvd, T * kvd, T * qd, T * qd, T * f, T * f, part, att};
   uint64_t total = 0;
   for (uint64_t n : sizes) total += (n + 63) / 64 * 64;
@@ -2125,6 +2151,11 @@ int32_t rf_model_residency_stats(rf_model* m, uint64_t* out) {
   out[4] = m->cache_used;
   out[5] = m->lru.size();
   return RF_OK;
+}
+
+int32_t rf_tune_attention_merge(int32_t mode) {
+  if (mode == 0 || mode == 1) g_oproj_merge = mode;
+  return g_oproj_merge;
 }
 
 int32_t rf_tune_packed_weights(int32_t mode) {

@@ -66,8 +66,9 @@ def test_workspace_size_queries_without_a_gpu():
     lib = _lib.load()
     assert lib.rf_attention_workspace_bytes(0, 32, 8, 128) == 0
     # 8192 positions, 32 q / 8 KV heads, hd 128: the score rows (32 x 8192
-    # floats) exceed the 32-chunk split records (32 x 32 x 130 floats)
+    # floats) exceed the 32-chunk split records (32 x 32 x 132 floats)
     assert lib.rf_attention_workspace_bytes(8192, 32, 8, 128) == 32 * 8192 * 4
-    # short contexts: per query head, up to 8 chunks of (hd + 2) floats
-    assert lib.rf_attention_workspace_bytes(64, 32, 8, 128) == max(8 * 32 * 130 * 4, 32 * 64 * 4)
+    # short contexts: per query head, up to 8 chunks of hd + 4 floats (o, m,
+    # l and two unused, 16-byte aligned)
+    assert lib.rf_attention_workspace_bytes(64, 32, 8, 128) == max(8 * 32 * 132 * 4, 32 * 64 * 4)
     assert lib.rf_matmul_workspace_bytes(0, 4096, 8) == 0

@@ -20,9 +20,10 @@ def test_fixed_reservation_allocates_nothing():
     rng = np.random.default_rng(31)
     with rf.Context(0) as c:
         # up to 64 positions: 8 chunks per query head at most (the split
-        # records of 32 heads), more than the any-shape kernel's score rows
+        # records of 32 heads, hd + 4 floats each), more than the any-shape
+        # kernel's score rows
         need = c.attention_workspace_bytes(64, 32, 8, 128)
-        assert need == 8 * 32 * 130 * 4
+        assert need == 8 * 32 * 132 * 4
         dev = _attention_inputs(c, rng, 8191)
         out = c.empty((32 * 128,))
         c.reserve(attention_bytes=need, fixed=True)
