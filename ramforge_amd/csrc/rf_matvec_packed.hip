@@ -397,6 +397,9 @@ __global__ __launch_bounds__(NT) void matvec_packed(PkArgs a) {
   // pointers are then scalar values, so no vector load (whose wait would also
   // wait for the codes in flight) is spent on them.
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  // MRG: the position first, before any store of the kernel (so that it is a
+  // scalar load: nothing this kernel writes comes before it)
+  const uint32_t m_posv = MRG ? (uint32_t)(*a.m_pos) : 0u;
   if (a.advance != nullptr && blockIdx.x == 0 && tid == 0) *a.advance += 1;
   const uint32_t in = a.in_dim, crb = in / EPB;
   const uint32_t nchunk = (crb + 1023u) / 1024u, nstep = (nchunk + LPW - 1) / LPW;
@@ -567,7 +570,7 @@ __global__ __launch_bounds__(NT) void matvec_packed(PkArgs a) {
   float2 mlv = make_float2(0.f, 0.f);
   float4 mo[MRG ? 8 : 1][2];
   if constexpr (MRG) {
-    const uint32_t total = (uint32_t)(*a.m_pos) + 1u, chunk = att_chunk(total, a.m_nsplit);
+    const uint32_t total = m_posv + 1u, chunk = att_chunk(total, a.m_nsplit);
     m_ns = (total + chunk - 1u) / chunk;
     const uint32_t rec = att_rec(1u << a.m_hd_log2), hmask = (1u << a.m_hd_log2) - 1u;
     const PkRsrc wsr =
