@@ -216,9 +216,13 @@ struct MmSegDesc {
 bool mm_supported(uint32_t t, uint64_t in_dim);
 uint64_t mm_part_floats(const uint64_t* rows, int nseg, uint64_t in_dim, uint64_t n);
 uint64_t mm_part_floats_at(const uint64_t* rows, int nseg, uint64_t in_dim, uint64_t n);
+// norm_w (EPI_RESIDUAL, one segment): also xn = RMSNorm(y) * norm_w per token
+// row (stride ld), the norm that follows a residual projection; fused into
+// the split-K reduce where the rows allow it, else a separate launch.
 hipError_t launch_matmul_packed(uint32_t t, const MmSegDesc* segs, int nseg, const float* x, uint64_t ldx,
                                 uint64_t n, uint64_t in_dim, int epi, float* part, uint64_t part_floats,
-                                hipStream_t st);
+                                hipStream_t st, const float* norm_w = nullptr, float eps = 0.f,
+                                float* xn = nullptr);
 hipError_t launch_rmsnorm_rows(const float* x, const float* w, uint64_t n, uint64_t rows, uint64_t ld, float eps,
                                float* y, hipStream_t st);
 hipError_t launch_rope_kv_rows(const float* q, const float* k, const float* v, const float* rope, uint64_t pos0,

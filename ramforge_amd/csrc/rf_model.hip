@@ -1447,19 +1447,28 @@ int32_t release_prefill_ws(rf_model* m) {
   return release_charge(m, "tmp:prefill");
 }
 
-int32_t enqueue_prefill_layer(rf_model* m, size_t li, uint64_t pos0, uint64_t nt) {
+// normed: p_xn already holds this layer's attention RMSNorm (the previous
+// layer's down projection produced it).  next_norm: the next layer's
+// attention norm weights, produced with this layer's down projection (null
+// for the last layer, and when streaming: the next layer may still be
+// uploading).
+int32_t enqueue_prefill_layer(rf_model* m, size_t li, uint64_t pos0, uint64_t nt, bool normed,
+                              const float* next_norm) {
   const rf_model_config& c = m->cfg;
   Layer& L = m->layers[li];
   hipStream_t st = m->ctx->compute;
   const uint64_t d = c.embedding_length, hd = c.head_dim, qd = c.head_count * hd, kvd = c.head_count_kv * hd;
   const uint64_t f = c.feed_forward_length;
   const float eps = c.rms_eps;
-  auto mm = [&](const MmSegDesc* segs, int n, uint32_t t, const float* x, uint64_t in, int epi) {
-    return launch_matmul_packed(t, segs, n, x, in, nt, in, epi, m->p_part, m->p_part_floats, st);
+  auto mm = [&](const MmSegDesc* segs, int n, uint32_t t, const float* x, uint64_t in, int epi,
+                const float* norm_w = nullptr) {
+    return launch_matmul_packed(t, segs, n, x, in, nt, in, epi, m->p_part, m->p_part_floats, st, norm_w, eps,
+                                norm_w ? m->p_xn : nullptr);
   };
   // 1. attention RMSNorm, Q/K/V (+ bias), consecutive projections of one type per launch
-  RF_LAUNCH(launch_rmsnorm_rows(m->p_h, static_cast<const float*>(L.attn_norm.d), d, nt, d, eps, m->p_xn, st),
-            "prefill attn norm");
+  if (!normed)
+    RF_LAUNCH(launch_rmsnorm_rows(m->p_h, static_cast<const float*>(L.attn_norm.d), d, nt, d, eps, m->p_xn, st),
+              "prefill attn norm");
   const DevTensor* qkv[3] = {&L.q, &L.k, &L.v};
   const DevTensor* bias[3] = {&L.bq, &L.bk, &L.bv};
   float* outs[3] = {m->p_q, m->p_k, m->p_v};
@@ -1494,12 +1503,11 @@ int32_t enqueue_prefill_layer(rf_model* m, size_t li, uint64_t pos0, uint64_t nt
   a.waves = attention_waves(att_chunk_positions(pos0 + nt, a.nsplit), 0);
   a.denom = sqrtf((float)hd);
   RF_LAUNCH(launch_attention(a, st), "prefill attention");
-  // 4. o-proj + residual
+  // 4. o-proj + residual, with the ffn RMSNorm
   MmSegDesc so{L.o.d, L.o.ne1, 0, d, m->p_h, m->p_h, nullptr, d};
-  RF_LAUNCH(mm(&so, 1, L.o.type, m->p_a, qd, EPI_RESIDUAL), "prefill o-proj");
-  // 5. ffn RMSNorm, gate/up, SiLU(gate) * up
-  RF_LAUNCH(launch_rmsnorm_rows(m->p_h, static_cast<const float*>(L.ffn_norm.d), d, nt, d, eps, m->p_xn, st),
-            "prefill ffn norm");
+  RF_LAUNCH(mm(&so, 1, L.o.type, m->p_a, qd, EPI_RESIDUAL, static_cast<const float*>(L.ffn_norm.d)),
+            "prefill o-proj + ffn norm");
+  // 5. gate/up, SiLU(gate) * up
   MmSegDesc sg[2] = {MmSegDesc{L.gate.d, L.gate.ne1, 0, f, m->p_act, nullptr, nullptr, f},
                      MmSegDesc{L.up.d, L.up.ne1, 0, f, m->p_up, nullptr, nullptr, f}};
   if (L.gate.type == L.up.type) {
@@ -1509,9 +1517,9 @@ int32_t enqueue_prefill_layer(rf_model* m, size_t li, uint64_t pos0, uint64_t nt
     RF_LAUNCH(mm(&sg[1], 1, L.up.type, m->p_xn, d, EPI_STORE), "prefill up");
     RF_LAUNCH(launch_binary(BIN_SWIGLU, m->p_act, m->p_up, nt * f, m->p_act, st), "prefill swiglu");
   }
-  // 6. down + residual
+  // 6. down + residual (with the next layer's attention RMSNorm)
   MmSegDesc sd{L.down.d, L.down.ne1, 0, d, m->p_h, m->p_h, nullptr, d};
-  RF_LAUNCH(mm(&sd, 1, L.down.type, m->p_act, f, EPI_RESIDUAL), "prefill down");
+  RF_LAUNCH(mm(&sd, 1, L.down.type, m->p_act, f, EPI_RESIDUAL, next_norm), "prefill down");
   return RF_OK;
 }
 
@@ -1549,7 +1557,11 @@ int32_t prefill_tokens(rf_model* m, const uint32_t* tokens, uint64_t n) {
         if (li + 1 < nl && (rc = acquire_layer(m, li + 1, true))) return abort_pass(m, rc);
         RF_LAUNCH(hipStreamWaitEvent(st, m->res[li].uploaded, 0), "wait for layer upload");
       }
-      if ((rc = enqueue_prefill_layer(m, li, pos0, nt))) return m->streaming ? abort_pass(m, rc) : rc;
+      const float* next_norm =
+          !m->streaming && li + 1 < nl ? static_cast<const float*>(m->layers[li + 1].attn_norm.d) : nullptr;
+      const bool normed = li > 0 && !m->streaming;
+      if ((rc = enqueue_prefill_layer(m, li, pos0, nt, normed, next_norm)))
+        return m->streaming ? abort_pass(m, rc) : rc;
       if (m->streaming && (rc = settle_layer(m, li))) return abort_pass(m, rc);
     }
     if (m->streaming && (rc = release_retired(m))) return rc;

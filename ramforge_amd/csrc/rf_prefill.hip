@@ -595,6 +595,60 @@ __global__ __launch_bounds__(256) void mm_reduce4(MmRedArgs a) {
   *reinterpret_cast<float4*>(s.y + o) = out;
 }
 
+// mm_reduce4's EPI_RESIDUAL for one segment of rows <= 4096 V columns,
+// fused with the RMSNorm that follows it: one workgroup per token row,
+// thread tid owning columns 4 (tid + 1024 i).  y = res + the partials in
+// split order (mm_reduce4's bits), then xn = y / rms(y) * w with
+// rms_norm_reference's arithmetic (compute.rs:291-319); the sum of squares
+// runs over the row's slots and wavefronts in a fixed order.
+template <int V>
+__global__ __launch_bounds__(1024) void mm_reduce_norm(MmRedArgs a, const float* __restrict__ w, float eps,
+                                                      float* __restrict__ xn) {
+  __shared__ float part[16];
+  const uint32_t t = blockIdx.x, tid = threadIdx.x;
+  const MmRedSeg s = a.seg[0];
+  const uint32_t cols = s.rows;
+  const size_t stride = (size_t)a.n * a.mtot / 4;  // float4 units (mtot % 4 == 0)
+  const float4* pv[V];
+  float4 rr[V], v[V];
+  uint32_t c[V];
+#pragma unroll
+  for (int i = 0; i < V; ++i) {
+    c[i] = 4u * (tid + 1024u * i);
+    const uint32_t cc = c[i] < cols ? c[i] : 0u;  // slots past the row: in bounds, unused
+    pv[i] = reinterpret_cast<const float4*>(a.part + (size_t)t * a.mtot + s.col + cc);
+    rr[i] = *reinterpret_cast<const float4*>(s.res + (size_t)t * s.ld + cc);
+  }
+  mm_split_sums<V>(pv, stride, a.nsplit, v);
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < V; ++i) {
+    const float4 y = make_float4(rr[i].x + v[i].x, rr[i].y + v[i].y, rr[i].z + v[i].z, rr[i].w + v[i].w);
+    v[i] = y;
+    if (c[i] < cols) {
+      *reinterpret_cast<float4*>(s.y + (size_t)t * s.ld + c[i]) = y;
+      ss = fmaf(y.x, y.x, ss);
+      ss = fmaf(y.y, y.y, ss);
+      ss = fmaf(y.z, y.z, ss);
+      ss = fmaf(y.w, y.w, ss);
+    }
+  }
+  ss = rf_wave_sum(ss);
+  if ((tid & 63u) == 0) part[tid >> 6] = ss;
+  __syncthreads();
+  float tot = 0.f;
+#pragma unroll
+  for (int k = 0; k < 16; ++k) tot += part[k];
+  const float rms = sqrtf(tot / (float)cols + eps);
+#pragma unroll
+  for (int i = 0; i < V; ++i) {
+    if (c[i] >= cols) break;
+    const float4 wv = *reinterpret_cast<const float4*>(w + c[i]);
+    *reinterpret_cast<float4*>(xn + (size_t)t * s.ld + c[i]) =
+        make_float4(v[i].x / rms * wv.x, v[i].y / rms * wv.y, v[i].z / rms * wv.z, v[i].w / rms * wv.w);
+  }
+}
+
 static bool mm_reduce_vec4(const MmRedArgs& r) {
   auto al = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
   if (r.mcols % 4 || r.mtot % 4 || !al(r.part)) return false;
@@ -760,7 +814,8 @@ static bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) 
 
 hipError_t launch_matmul_packed(uint32_t t, const MmSegDesc* segs, int nseg, const float* x, uint64_t ldx,
                                 uint64_t n, uint64_t in_dim, int epi, float* part, uint64_t part_floats,
-                                hipStream_t st) {
+                                hipStream_t st, const float* norm_w, float eps, float* xn) {
+  if (norm_w && (epi != EPI_RESIDUAL || nseg != 1 || !xn)) return hipErrorInvalidValue;
   if (!mm_supported(t, in_dim) || nseg < 1 || nseg > 3 || n == 0 || n > MM_MAX_TOKENS) return hipErrorInvalidValue;
   if (!al16(x) || ldx % 4 != 0 || ldx < in_dim || !part) return hipErrorInvalidValue;
   if (epi == EPI_SWIGLU && (nseg != 2 || segs[0].rows != segs[1].rows)) return hipErrorInvalidValue;
@@ -831,11 +886,20 @@ hipError_t launch_matmul_packed(uint32_t t, const MmSegDesc* segs, int nseg, con
   r.epi = epi;
   r.part = part;
   const uint64_t total = (uint64_t)n * r.mcols;
+  const bool al = ((reinterpret_cast<uintptr_t>(norm_w) | reinterpret_cast<uintptr_t>(xn)) & 15u) == 0;
+  if (norm_w && al && mm_reduce_vec4(r) && r.mcols <= 8192) {
+    if (r.mcols <= 4096) hipLaunchKernelGGL(mm_reduce_norm<1>, dim3((uint32_t)n), dim3(1024), 0, st, r, norm_w, eps, xn);
+    else hipLaunchKernelGGL(mm_reduce_norm<2>, dim3((uint32_t)n), dim3(1024), 0, st, r, norm_w, eps, xn);
+    return hipGetLastError();
+  }
   if (mm_reduce_vec4(r))
     hipLaunchKernelGGL(mm_reduce4, dim3((uint32_t)((total / 4 + 255) / 256)), dim3(256), 0, st, r);
   else
     hipLaunchKernelGGL(mm_reduce, dim3((uint32_t)((total + 255) / 256)), dim3(256), 0, st, r);
-  return hipGetLastError();
+  e = hipGetLastError();
+  if (e != hipSuccess || !norm_w) return e;
+  const MmSegDesc& d = segs[0];
+  return launch_rmsnorm_rows(d.y, norm_w, d.rows, n, d.ld, eps, xn, st);
 }
 
 // ------------------------------------------------------- per-token glue
