@@ -3,10 +3,10 @@
 (mode 0) and the oracle (attention_reference, compute.rs:461-547, then the
 o-projection, model_executor.rs:102-236).
 
-The model has 32 query heads of 128 dims (q_heads * head_dim = 4096, as the
-8B shape), so the packed Q8_0 / Q4_0 / Q4_K o-projection takes the merged-x
-launch at every context the attention splits per query head (65 to 1024
-positions here: 2 to 8 chunks).  The two modes differ in the merge's
+The models have 32 query heads of 128 dims (q_heads * head_dim = 4096, as
+the 8B shape) or 64 of 64, so the packed Q8_0 / Q4_0 / Q4_K o-projection
+takes the merged-x launch at every context the attention splits per query
+head (65 to 1024 positions here: 2 to 8 chunks, or to 4 with 64 heads).  The two modes differ in the merge's
 rounding only: hidden states within 1e-5 of each other, both within 2e-4 of
 the oracle, and identical greedy tokens, eager and replayed from the decode
 graphs, across the launch regimes."""
@@ -20,6 +20,8 @@ pytestmark = pytest.mark.gpu
 
 CFG = dict(vocab_size=192, context_length=1100, embedding_length=256, block_count=2, feed_forward_length=512,
            head_count=32, head_count_kv=8, head_dim=128, rms_eps=1e-5, rope_freq_base=10000.0)
+# 64 heads of 64 dims: at most 4 chunks per query head (256 / 64), records of 68 floats
+CFG64 = dict(CFG, head_count=64, head_count_kv=16, head_dim=64)
 CAP = 1100
 
 
@@ -37,15 +39,16 @@ def merge_mode():
 
 
 @pytest.mark.timeout(600)
-@pytest.mark.parametrize("o", [Q8_0, Q4_0, Q4_K], ids=["q8_0", "q4_0", "q4_k"])
-def test_merged_oproj_matches_merge_kernel(ctx, orc, merge_mode, o):
-    T = _tiny_tensors(np.random.default_rng(2400 + o), CFG, _types(o))
+@pytest.mark.parametrize("o,cfg", [(Q8_0, CFG), (Q4_0, CFG), (Q4_K, CFG), (Q8_0, CFG64)],
+                         ids=["q8_0", "q4_0", "q4_k", "q8_0-hd64"])
+def test_merged_oproj_matches_merge_kernel(ctx, orc, merge_mode, o, cfg):
+    T = _tiny_tensors(np.random.default_rng(2400 + o), cfg, _types(o))
     import ramforge_amd as rf
 
-    om = orc.Model(CFG, T, kv_capacity=CAP, threads=8)
+    om = orc.Model(cfg, T, kv_capacity=CAP, threads=8)
     ctxs = {1: ctx, 0: rf.Context(0)}  # a model's ledger names are per context
-    gm = {mode: _load_gpu(ctxs[mode], CFG, T, CAP) for mode in (1, 0)}
-    prompt = [int(t) for t in np.random.default_rng(7).integers(0, CFG["vocab_size"], 40)]
+    gm = {mode: _load_gpu(ctxs[mode], cfg, T, CAP) for mode in (1, 0)}
+    prompt = [int(t) for t in np.random.default_rng(7).integers(0, cfg["vocab_size"], 40)]
     differs = False
     try:
         # eager forward across positions 0..199 (regimes 0 and 1) and a few
