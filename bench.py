@@ -548,6 +548,7 @@ def config4_bench(rf, syn, tokens: int = 128, prompt_len: int = 32) -> dict:
     m.decode_steps(tokens)
     ctx.synchronize()
     wall = time.perf_counter() - t0
+    gen = m.read_tokens(tokens)
     out = {"workload": "config 4: 16 layers, d 2048, 32/8 heads, FFN 8192, vocab 32000, Q8_0, resident",
            "prompt_tokens": prompt_len, "prompt_token_by_token_ms": round(tbt * 1e3, 2),
            "prompt_batched_ms": round(batched * 1e3, 2), "tokens": tokens, "tok_s": round(tokens / wall, 1),
