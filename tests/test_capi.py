@@ -72,3 +72,20 @@ def test_workspace_size_queries_without_a_gpu():
     # l and two unused, 16-byte aligned)
     assert lib.rf_attention_workspace_bytes(64, 32, 8, 128) == max(8 * 32 * 132 * 4, 32 * 64 * 4)
     assert lib.rf_matmul_workspace_bytes(0, 4096, 8) == 0
+
+
+def test_tune_switches_without_a_gpu():
+    """The process-wide tune switches are host state: each returns the mode in
+    effect, values outside its range only query, and the defaults are the
+    measured choices (merged attention records, in-flight packed launches,
+    packed weights, float x everywhere: the digit planes are opt-in)."""
+    from ramforge_amd import _lib
+
+    lib = _lib.load()
+    for name, default, modes in (("rf_tune_attention_merge", 1, (0, 1)), ("rf_tune_packed_inflight", 1, (0, 1)),
+                                 ("rf_tune_packed_weights", 1, (0, 1)), ("rf_tune_matvec_digits", 0, (0, 1, 2))):
+        fn = getattr(lib, name)
+        assert fn(-1) == default, name
+        for m in modes:
+            assert fn(m) == m and fn(99) == m, (name, m)
+        assert fn(default) == default
