@@ -133,7 +133,7 @@ hipError_t launch_matvec_packed(uint32_t t, const PkSegDesc* segs, int nseg, con
 // True when launch_matvec_packed can merge attention chunk records into x
 // for this projection (EPI_RESIDUAL, no norm, one segment of `rows` rows):
 // the single-step launch of Q8_0 / Q4_0 / Q4_K with in_dim = qh * hd, hd a
-// power of two from 16, at most 8 chunks and nsplit * qh <= 512.
+// power of two from 16, at most 8 chunks and 64 query heads.
 bool pk_merge_supported(uint32_t t, uint64_t in_dim, uint64_t rows, uint32_t nsplit, uint32_t qh, uint32_t hd);
 // GGUF payload [rows][in_dim] -> packed layout (distinct buffers).
 hipError_t launch_pack(uint32_t t, const void* raw, void* packed, uint64_t rows, uint64_t in_dim, hipStream_t st);

@@ -575,8 +575,12 @@ __global__ __launch_bounds__(NT) void matvec_packed(PkArgs a) {
     const uint32_t rec = att_rec(1u << a.m_hd_log2), hmask = (1u << a.m_hd_log2) - 1u;
     const PkRsrc wsr =
         __builtin_amdgcn_make_buffer_rsrc((void*)a.mws, 0, (int32_t)(m_ns * a.m_qh * rec * 4u), PK_RSRC_WORD3);
-    if (m_ns > 1u && tid < m_ns * a.m_qh) {  // record tid = chunk * qh + head
-      const auto v = __builtin_amdgcn_raw_buffer_load_b64(wsr, (tid * rec + hmask + 1u) * 4u, 0, 0);
+    // lanes 8 h .. 8 h + 7: head h's (m, l) of chunks 0..7 (m = -inf, l = 0
+    // past the valid ones)
+    mlv = make_float2(-INFINITY, 0.f);
+    if (m_ns > 1u && (tid >> 3) < a.m_qh && (tid & 7u) < m_ns) {
+      const uint32_t r = (tid & 7u) * a.m_qh + (tid >> 3);
+      const auto v = __builtin_amdgcn_raw_buffer_load_b64(wsr, (r * rec + hmask + 1u) * 4u, 0, 0);
       mlv = make_float2(__uint_as_float(v[0]), __uint_as_float(v[1]));
     }
     const uint32_t j = tid >> 1, js = j / UPS, hh = j % UPS;
@@ -633,30 +637,28 @@ __global__ __launch_bounds__(NT) void matvec_packed(PkArgs a) {
 
   bool finite = true;
   if constexpr (MRG) {
-    // The merge's per-record work once per workgroup, in LDS behind the unit
-    // sums: (m, l) of every valid record, then per head (one thread each)
-    // M = the largest m, the factors exp(m - M) and 1 / L with L the sum of
-    // l times factor in chunk order.  Each thread then sums factor times o
-    // over the chunks for its 8 elements, scales by 1 / L and stages them;
-    // the unit's sum joins the two halves (adjacent lanes).
-    const uint32_t nrec = a.m_nsplit * a.m_qh;
-    float2* mls = reinterpret_cast<float2*>(xsum_l + nunit);
-    float* fac = reinterpret_cast<float*>(mls + nrec);
-    float* invl = fac + nrec;
+    // The merge's per-record work once per workgroup: each group of 8 lanes
+    // holds one head's chunks, so M = the largest m, the factors exp(m - M)
+    // and L = the sum of l times factor (a fixed butterfly order) take three
+    // lane exchanges each; the factors and 1 / L go to LDS behind the unit
+    // sums.  Each thread then sums factor times o over the chunks for its 8
+    // elements, scales by 1 / L and stages them.
+    float* fac = xsum_l + nunit;                 // [nsplit][qh]
+    float* invl = fac + a.m_nsplit * a.m_qh;     // [qh]
     if (m_ns > 1u) {
-      if (tid < m_ns * a.m_qh) mls[tid] = mlv;
-      __syncthreads();
-      if (tid < a.m_qh) {
-        float M = -INFINITY;
-        for (uint32_t c = 0; c < m_ns; ++c) M = fmaxf(M, mls[c * a.m_qh + tid].x);
-        float L = 0.f;
-        for (uint32_t c = 0; c < m_ns; ++c) {
-          const float2 ml = mls[c * a.m_qh + tid];
-          const float f = expf(ml.x - M);
-          fac[c * a.m_qh + tid] = f;
-          L = fmaf(ml.y, f, L);
-        }
-        invl[tid] = 1.0f / L;
+      float M = mlv.x;
+      M = fmaxf(M, __shfl_xor(M, 1));
+      M = fmaxf(M, __shfl_xor(M, 2));
+      M = fmaxf(M, __shfl_xor(M, 4));
+      const float f = expf(mlv.x - M);  // 0 past the valid chunks
+      float L = mlv.y * f;
+      L += __shfl_xor(L, 1);
+      L += __shfl_xor(L, 2);
+      L += __shfl_xor(L, 4);
+      const uint32_t h = tid >> 3, c = tid & 7u;
+      if (h < a.m_qh) {
+        if (c < m_ns) fac[c * a.m_qh + h] = f;
+        if (c == 0u) invl[h] = 1.0f / L;
       }
       __syncthreads();
     }
@@ -669,10 +671,14 @@ __global__ __launch_bounds__(NT) void matvec_packed(PkArgs a) {
         v[4 * k] = mo[0][k].x; v[4 * k + 1] = mo[0][k].y; v[4 * k + 2] = mo[0][k].z; v[4 * k + 3] = mo[0][k].w;
       }
     } else {
+      const float f0 = fac[m_head];  // chunk 0 (m_ns >= 2)
 #pragma unroll
-      for (int k = 0; k < 8; ++k) v[k] = 0.f;
+      for (int k = 0; k < 2; ++k) {
+        v[4 * k] = f0 * mo[0][k].x; v[4 * k + 1] = f0 * mo[0][k].y;
+        v[4 * k + 2] = f0 * mo[0][k].z; v[4 * k + 3] = f0 * mo[0][k].w;
+      }
 #pragma unroll
-      for (int c = 0; c < 8; ++c) {
+      for (int c = 1; c < 8; ++c) {
         if ((uint32_t)c < m_ns) {
           const float f = fac[c * a.m_qh + m_head];
 #pragma unroll
@@ -688,22 +694,27 @@ __global__ __launch_bounds__(NT) void matvec_packed(PkArgs a) {
 #pragma unroll
       for (int k = 0; k < 8; ++k) v[k] *= r;
     }
-    // the unit's slots (put_float's layout): this half's two float4
-    float s8 = 0.f;
-    bool fin = true;
+    // the unit's slots (put_float's layout): this half's two float4; the
+    // unit's sum (the two halves, adjacent lanes) where the format reads it
     if (have) {
       float* dst = xl + (js >> 6) * 64u * EPL + 4u * hh * 256u + 4u * (js & 63u) + 512u * half;
 #pragma unroll
-      for (int k = 0; k < 2; ++k) {
+      for (int k = 0; k < 2; ++k)
         *reinterpret_cast<float4*>(dst + 256 * k) = make_float4(v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]);
-        s8 += v[4 * k]; s8 += v[4 * k + 1]; s8 += v[4 * k + 2]; s8 += v[4 * k + 3];
-      }
+    }
+    if constexpr (T == T_Q4_K) {
+      float s8 = 0.f;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) s8 += v[k];
+      const float s16 = s8 + __shfl_xor(s8, 1);
+      if (j < nunit && half == 0u) xsum_l[j] = have ? s16 : 0.f;
+    }
+    if constexpr (KINDS) {
+      bool fin = true;
 #pragma unroll
       for (int k = 0; k < 8; ++k) fin = fin && fabsf(v[k]) <= 3.40282347e38f;
+      finite = !have || fin;
     }
-    const float s16 = s8 + __shfl_xor(s8, 1);
-    if (j < nunit && half == 0u) xsum_l[j] = have ? s16 : 0.f;
-    if constexpr (KINDS) finite = fin;
   }
   {
     float ss = 0.f;
@@ -1189,7 +1200,7 @@ static hipError_t launch_pk_all(const PkArgs& a, uint32_t lds, hipStream_t st, b
 // The single-step launch above with x merged from attention chunk records
 // (matvec_packed<..., MRG>): Q8_0 rows of 4 chunks, Q4_0 / Q4_K rows of 2,
 // with the MRG kernel's own occupancy and LDS (x, its unit sums, then the
-// records' (m, l) pairs and factors and the heads' 1 / L).
+// records' factors and the heads' 1 / L).
 // hipErrorNotSupported when the shape does not take it;
 // with launch false it only says so.
 static bool pk_merge_shape(uint32_t t, uint64_t in_dim, uint32_t nsplit, uint32_t qh, uint32_t hd, uint32_t* lds) {
@@ -1201,9 +1212,9 @@ static bool pk_merge_shape(uint32_t t, uint64_t in_dim, uint32_t nsplit, uint32_
   const uint64_t nchunk = pk_nchunk(t, in_dim);
   if (!((t == T_Q8_0 && nchunk == 4) || ((t == T_Q4_0 || t == T_Q4_K) && nchunk == 2))) return false;
   if (hd < 16 || (hd & (hd - 1)) != 0 || (uint64_t)qh * hd != in_dim) return false;
-  if (nsplit < 1 || nsplit > 8 || (uint64_t)nsplit * qh > 512) return false;
+  if (nsplit < 1 || nsplit > 8 || qh > 64) return false;  // 8 lanes per head's chunk records
   if (2 * nchunk * 64 * pk_epb(t) != 512) return false;  // two threads per unit of 16 elements
-  const uint64_t l = p.lds_bytes + (uint64_t)nsplit * qh * 12 + (uint64_t)qh * 4;  // (m, l), factors, 1 / L
+  const uint64_t l = p.lds_bytes + (uint64_t)nsplit * qh * 4 + (uint64_t)qh * 4;  // factors, 1 / L
   if (l + PK_STATIC_LDS > pk_lds_limit()) return false;
   *lds = (uint32_t)l;
   return true;
