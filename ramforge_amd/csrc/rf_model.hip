@@ -89,6 +89,9 @@ struct rf_model {
   float *hidden = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attn_out = nullptr, *act = nullptr;
   float *logits = nullptr, *final_hidden = nullptr, *attn_ws = nullptr, *up_tmp = nullptr;
   bool attn_fast = false;  // split kernel (else the any-shape kernel)
+  // set by enqueue_attention when it left the chunk records for the
+  // o-projection to merge; enqueue_oproj follows it (one decision per layer)
+  bool oproj_merge = false;
   float *xnorm = nullptr, *mvtmp = nullptr;  // scratch of the unfused fallback
   float* amax_val = nullptr;
   uint32_t* amax_idx = nullptr;
@@ -1167,7 +1170,8 @@ int32_t enqueue_attention(rf_model* m, size_t li) {
   // the position this step processes picks the shape
   const AttnShape sh = attention_regime_shape(attn_regime(m, m->seq_len), a.qh, a.kvh, m->kv_max);
   a.per_q = sh.per_q; a.nsplit = sh.nsplit; a.waves = sh.waves;
-  a.defer_merge = oproj_merges(m, li, sh) ? 1u : 0u;
+  m->oproj_merge = oproj_merges(m, li, sh);
+  a.defer_merge = m->oproj_merge ? 1u : 0u;
   a.denom = sqrtf((float)hd);
   RF_LAUNCH(m->attn_fast ? launch_attention(a, st) : launch_attention_naive(a, st), "attention");
   return RF_OK;
@@ -1179,9 +1183,10 @@ int32_t enqueue_oproj(rf_model* m, size_t li) {
   const rf_model_config& c = m->cfg;
   Layer& L = m->layers[li];
   const uint64_t d = c.embedding_length, qd = c.head_count * c.head_dim;
-  const AttnShape sh = attention_regime_shape(attn_regime(m, m->seq_len), (uint32_t)c.head_count,
-                                              (uint32_t)c.head_count_kv, m->kv_max);
-  if (oproj_merges(m, li, sh)) {
+  if (m->oproj_merge) {  // the attention just enqueued left its chunk records
+    m->oproj_merge = false;
+    const AttnShape sh = attention_regime_shape(attn_regime(m, m->seq_len), (uint32_t)c.head_count,
+                                                (uint32_t)c.head_count_kv, m->kv_max);
     const PkMerge mg{m->attn_ws, m->d_pos, sh.nsplit, (uint32_t)c.head_count, (uint32_t)c.head_dim};
     PkSegDesc ps{L.o.d, nullptr, L.o.ne1, 0, d, m->hidden, m->hidden};
     RF_LAUNCH(launch_matvec_packed(L.o.type, &ps, 1, m->attn_out, nullptr, 0.f, qd, EPI_RESIDUAL, m->ctx->compute,
@@ -1953,6 +1958,7 @@ int32_t rf_model_time_kernel(rf_model* m, uint32_t kind, uint32_t reps, float* a
       ++n;
     }
   }
+  m->oproj_merge = false;  // a timed attention's deferred merge is not the next o-projection's
   if (e == hipSuccess) e = hipEventRecord(e1, st);
   if (e == hipSuccess) e = hipEventSynchronize(e1);
   float ms = 0.f;
