@@ -166,12 +166,30 @@ def context_decode(ctx, m, cfg, n: int, steps: int, graph: bool) -> dict:
     return out
 
 
-def dominant_kernel(rf) -> str:
-    """Kernel that runs the ffn RMSNorm + gate/up + SiLU*up group of the 8B Q8_0 model."""
-    if rf.tune_packed_weights(-1) == 1 and rf.packed_supported(rf.GGML.Q8_0, 4096):
-        x = "float x" if rf.tune_matvec_digits(-1) == 0 else "x as digit planes"
-        return f"matvec_packed<Q8_0, EPI_SWIGLU, norm> (ffn RMSNorm + gate/up + SiLU*up, packed layout, {x})"
-    return "matvec_stream<Q8_0, EPI_SWIGLU> (ffn RMSNorm + gate/up + SiLU*up, GGUF layout)"
+def dominant_kernel(m) -> str:
+    """Kernel instance that runs the ffn RMSNorm + gate/up + SiLU*up group of
+    the 8B Q8_0 model, as the rocprofv3 kernel trace names it (the library
+    reports the instance its launcher picks)."""
+    return m.kernel_name("gateup") or "matvec_stream<Q8_0, EPI_SWIGLU> (GGUF layout)"
+
+
+def under_tracer() -> bool:
+    """True when this process runs under rocprofv3 (it exports its settings
+    as ROCPROF_* / ROCPROFILER_* variables to the profiled program)."""
+    return any(k.startswith(("ROCPROF_", "ROCPROFILER_")) for k in os.environ)
+
+
+def trace_mean_us(kernel: str):
+    """Mean duration of `kernel` in the committed kernel trace of the decode
+    step (profiles/decode_8b_q8_0_kernel_stats.json), or None when the
+    committed trace does not hold that exact kernel."""
+    path = os.path.join(ROOT, "profiles", "decode_8b_q8_0_kernel_stats.json")
+    try:
+        tj = json.load(open(path))
+    except (OSError, ValueError):
+        return None
+    row = tj.get("kernels", {}).get(kernel)
+    return None if row is None else row.get("mean_us")
 
 
 
@@ -190,7 +208,7 @@ def traffic_probe(ctx, m, cfg, rf) -> int:
     for _ in range(4):
         ctx.copy(dst, src, COPY_BYTES)
     ctx.synchronize()
-    print(json.dumps({"probe": "gateup", "kernel": dominant_kernel(rf), "launches": n, "algorithmic_bytes": b,
+    print(json.dumps({"probe": "gateup", "kernel": dominant_kernel(m), "launches": n, "algorithmic_bytes": b,
                       "copy_bytes": COPY_BYTES, "copies": 4, "layers": cfg["block_count"]}), flush=True)
     src.free()
     dst.free()
@@ -602,6 +620,15 @@ def main() -> int:
         print("bench.py measures the decode hot path on ONE GPU only: this build has no multi-GPU path "
               "(no collectives or sharding); run with --gpus 1.", file=sys.stderr)
         return 2
+    model_graph = not (args.kernels or args.attention_probe or args.matvec_probe or args.traffic_probe
+                       or args.prefill_only or args.config5)
+    if model_graph and not args.no_graph and under_tracer():
+        # Three kernel traces of the graph-replayed decode step crashed on the
+        # host inside rf_model_decode_steps (a profiler callback under the HIP
+        # runtime reading an unmapped address), cause not established.
+        print("bench.py: graph-replayed decode is not run under rocprofv3 (the kernel tracer has crashed inside "
+              "the decode step's capture/replay); trace the same kernels with --no-graph.", file=sys.stderr)
+        return 2
 
     import numpy as np
 
@@ -680,17 +707,23 @@ def main() -> int:
     d = breakdown[dom]
     achieved = d["bytes_per_launch"] / (d["us_per_launch"] * 1e-6) / 1e9
     traffic = None
+    kname = dominant_kernel(m) if dom == "gateup" else dom
     tpath = os.path.join(ROOT, "profiles", "gateup_q8_0_8b_traffic.json")
     if dom == "gateup" and os.path.exists(tpath):
         try:
             tj = json.load(open(tpath))
-            # only a measurement of the kernel that ran counts
-            traffic = tj.get("bytes_per_launch") if tj.get("bench_kernel") == dominant_kernel(rf) else None
+            # only a measurement of the exact kernel instance that ran counts
+            traffic = tj.get("bytes_per_launch") if tj.get("kernel") == kname else None
         except (OSError, ValueError):
             traffic = None
+    # the same figure from the committed rocprofv3 trace of this kernel
+    t_us = trace_mean_us(kname)
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": traffic,
-                "kernel": dominant_kernel(rf) if dom == "gateup" else dom}
+                "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": traffic, "kernel": kname,
+                "timing": "HIP events around back-to-back launches on the compute stream",
+                "trace_us_per_launch": t_us,
+                "frac_from_trace": None if t_us is None else round(d["bytes_per_launch"] / (t_us * 1e-6) / 1e9
+                                                                    / PEAK_HBM_GBS, 4)}
     log(f"dominant group {dom}: {d['us_per_launch']} us/launch, {achieved:.0f} GB/s "
         f"({achieved / PEAK_HBM_GBS:.1%} of peak); kernel time per token {kernel_ms:.3f} ms")
     ctx_decode = {}

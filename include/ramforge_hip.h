@@ -353,6 +353,17 @@ int32_t rf_model_create_growing(rf_ctx *ctx, const rf_model_config *cfg, uint64_
                                 uint64_t initial_tokens, rf_model **out);
 /* Positions the KV cache holds now (KvCache::capacity_tokens). */
 int32_t rf_model_kv_capacity(rf_model *model, uint64_t *tokens);
+/* Which kernels the model runs (no counterpart in the reference, which has
+ * one CPU path; for tests and tools that must know which path they cover):
+ * split_attention = 1 when decode attention runs the split-K kernel
+ * (32/8/... query-KV head ratios with head_dim 64, 128 or 256), 0 for the
+ * any-shape kernel; regime = the split kernel's launch regime (0-4) of a
+ * decode step at position pos (0 for the any-shape kernel);
+ * batched_prefill = 1 when rf_model_prefill (and rf_model_generate after
+ * rf_model_set_prefill(1)) forwards prompts as batched GEMMs with the
+ * tensors installed now, 0 when it falls back to one forward per token. */
+int32_t rf_model_paths(rf_model *model, uint64_t pos, int32_t *split_attention, int32_t *regime,
+                       int32_t *batched_prefill);
 
 /* Installs tensor `name` (GGUF names: token_embd.weight, output_norm.weight,
  * output.weight, blk.{i}.{attn_norm,attn_q,attn_k,attn_v,attn_output,
@@ -502,6 +513,14 @@ int32_t rf_model_profile_read(rf_model *model, double *ms, uint64_t *counts, int
  * for the profiler's per-event times (runtime/src/profile.rs:7-23). */
 int32_t rf_model_time_kernel(rf_model *model, uint32_t kind, uint32_t reps, float *avg_ms,
                              uint64_t *bytes_per_launch, uint64_t *launches);
+/* Name of the packed matvec kernel instance one launch group runs (layer 0;
+ * the o-projection as it follows the attention at the current position),
+ * spelled as the profiler's kernel trace spells it, e.g.
+ * "void rf::matvec_packed<8u, 2, true, 1, 2, 2, 512, false, false, false>(rf::PkArgs)";
+ * "" when the group launches no packed matvec.  Nothing is launched.  No
+ * counterpart in the reference: it ties measurements to the kernel that
+ * ran. */
+int32_t rf_model_kernel_name(rf_model *model, uint32_t kind, char *buf, uint64_t cap);
 
 /* ------------------------------------------------------- graph capture */
 

@@ -779,12 +779,19 @@ int orc_attention(const float *q, size_t q_len, const float *kh, const float *vh
     if (q_len != qw || hist_elems != hist * kvw || cur_len != kvw || out_len != qw)
         return fail("attention tensor shape mismatch");
     size_t total = hist + 1;
-    float *scores = (float *)malloc(total * sizeof(float));
+    /* Heads are independent; with parity threads (never for the timed CPU
+     * baseline) they are spread over threads, each head's arithmetic and
+     * order unchanged, so the output is bit-identical. */
+    int nth = g_parity_threads > 1 ? g_parity_threads : 1;
+    float *scores = (float *)malloc((size_t)nth * total * sizeof(float));
     if (!scores) return fail("failed to reserve attention scores");
     float *acc = (float *)calloc(qw, sizeof(float));
     if (!acc) { free(scores); return fail("failed to reserve attention output"); }
     float denom = sqrtf((float)hd);
+    int err = 0;
+#pragma omp parallel for num_threads(nth) schedule(static) reduction(| : err) if (nth > 1)
     for (size_t h = 0; h < qhn; h++) {
+        float *sc = scores + (size_t)omp_get_thread_num() * total;
         size_t g = h * kvhn / qhn;
         const float *qv = q + h * hd;
         for (size_t p = 0; p < total; p++) {
@@ -792,16 +799,17 @@ int orc_attention(const float *q, size_t q_len, const float *kh, const float *vh
             const float *kv = kall + g * hd;
             float dot = 0.0f;
             for (size_t i = 0; i < hd; i++) dot += qv[i] * kv[i];
-            scores[p] = dot / denom;
+            sc[p] = dot / denom;
         }
-        if (orc_softmax(scores, total)) { free(scores); free(acc); return 1; }
+        if (orc_softmax(sc, total)) { err |= 1; continue; }
         float *oh = acc + h * hd;
         for (size_t p = 0; p < total; p++) {
             const float *vall = (p < hist) ? vh + p * kvw : vc;
             const float *vv = vall + g * hd;
-            for (size_t i = 0; i < hd; i++) oh[i] += scores[p] * vv[i];
+            for (size_t i = 0; i < hd; i++) oh[i] += sc[p] * vv[i];
         }
     }
+    if (err) { free(scores); free(acc); return 1; }
     memcpy(out, acc, qw * sizeof(float));
     free(scores);
     free(acc);

@@ -732,6 +732,14 @@ class GpuLlamaModel:
     def decode_steps(self, steps: int) -> None:
         _lib.check(self.ctx.lib.rf_model_decode_steps(self.handle, steps))
 
+    def paths(self, pos: int = 0) -> dict:
+        """Which kernels run: the split-K attention kernel (else the any-shape
+        one), its launch regime for a decode step at `pos`, and whether
+        prefill is batched (else one forward per token)."""
+        sa, rg, bp = C.c_int32(), C.c_int32(), C.c_int32()
+        _lib.check(self.ctx.lib.rf_model_paths(self.handle, pos, C.byref(sa), C.byref(rg), C.byref(bp)))
+        return {"split_attention": bool(sa.value), "regime": rg.value, "batched_prefill": bool(bp.value)}
+
     KERNELS = {"qkv": 1, "attention": 2, "oproj": 3, "gateup": 4, "down": 5, "logits": 6}
 
     def time_kernel(self, kind: str, reps: int = 1):
@@ -741,6 +749,13 @@ class GpuLlamaModel:
         _lib.check(self.ctx.lib.rf_model_time_kernel(self.handle, self.KERNELS[kind], reps, C.byref(ms), C.byref(b),
                                                      C.byref(n)))
         return ms.value, b.value, n.value
+
+    def kernel_name(self, kind: str) -> str:
+        """The packed matvec kernel instance a launch group runs, as the
+        profiler's kernel trace names it ("" for none)."""
+        buf = C.create_string_buffer(256)
+        _lib.check(self.ctx.lib.rf_model_kernel_name(self.handle, self.KERNELS[kind], buf, 256))
+        return buf.value.decode()
 
     def read_tokens(self, n: int) -> list:
         out = np.zeros(max(n, 1), np.uint32)

@@ -132,6 +132,8 @@ SIGNATURES = {
     "rf_model_profile": (_i32, [_vp, _i32]),
     "rf_model_profile_read": (_i32, [_vp, _vp, _vp, _i32]),
     "rf_model_kv_capacity": (_i32, [_vp, _vp]),
+    "rf_model_paths": (_i32, [_vp, _u64, _vp, _vp, _vp]),
+    "rf_model_kernel_name": (_i32, [_vp, _u32, C.c_char_p, _u64]),
     "rf_model_time_kernel": (_i32, [_vp, _u32, _u32, C.POINTER(_f32), C.POINTER(_u64), C.POINTER(_u64)]),
     "rf_tune_matvec_tile_bytes": (_u32, [_u32]),
     "rf_tune_matvec_kernel": (_i32, [_i32]),

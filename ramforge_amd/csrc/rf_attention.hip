@@ -566,7 +566,7 @@ uint64_t attention_ws_floats(uint32_t nsplit, uint32_t qh, uint32_t hd) {
 
 template <int G, int DPL, int W, bool PERQ = false>
 static void launch_split_t(const AttnArgs& a, hipStream_t st) {
-  hipLaunchKernelGGL((attn_split<G, DPL, W, PERQ>), dim3(a.nsplit, PERQ ? a.qh : a.kvh, a.ntok ? a.ntok : 1),
+  RF_KLAUNCH((attn_split<G, DPL, W, PERQ>), dim3(a.nsplit, PERQ ? a.qh : a.kvh, a.ntok ? a.ntok : 1),
                      dim3(64 * W), 0, st, a);
 }
 
@@ -581,7 +581,7 @@ uint32_t att_chunk_positions(uint64_t total, uint32_t nsplit) { return att_chunk
 static_assert(ATT_PREFILL_CHUNK == ATT_MAX_CHUNK, "prefill chunks are the kernel's longest");
 
 hipError_t launch_attention_naive(const AttnArgs& a, hipStream_t st) {
-  hipLaunchKernelGGL(attn_naive, dim3(a.qh), dim3(256), 0, st, a);
+  RF_KLAUNCH(attn_naive, dim3(a.qh), dim3(256), 0, st, a);
   return hipGetLastError();
 }
 
@@ -618,9 +618,9 @@ hipError_t launch_attention(const AttnArgs& a, hipStream_t st) {
   if (e != hipSuccess || a.nsplit == 1 || a.defer_merge) return e;
   const dim3 mg(a.qh, 1, a.ntok ? a.ntok : 1);
   switch (a.hd) {
-    case 64: hipLaunchKernelGGL(attn_merge<1>, mg, dim3(64), 0, st, a); break;
-    case 128: hipLaunchKernelGGL(attn_merge<2>, mg, dim3(64), 0, st, a); break;
-    default: hipLaunchKernelGGL(attn_merge<4>, mg, dim3(64), 0, st, a); break;  // 256 (attention_supported)
+    case 64: RF_KLAUNCH(attn_merge<1>, mg, dim3(64), 0, st, a); break;
+    case 128: RF_KLAUNCH(attn_merge<2>, mg, dim3(64), 0, st, a); break;
+    default: RF_KLAUNCH(attn_merge<4>, mg, dim3(64), 0, st, a); break;  // 256 (attention_supported)
   }
   return hipGetLastError();
 }

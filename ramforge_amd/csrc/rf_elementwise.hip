@@ -29,7 +29,7 @@ __global__ __launch_bounds__(1024) void rmsnorm_kernel(const float* __restrict__
 }
 
 hipError_t launch_rmsnorm(const float* x, const float* w, uint64_t n, float eps, float* y, hipStream_t st) {
-  hipLaunchKernelGGL(rmsnorm_kernel, dim3(1), dim3(1024), 0, st, x, w, (uint32_t)n, eps, y);
+  RF_KLAUNCH(rmsnorm_kernel, dim3(1), dim3(1024), 0, st, x, w, (uint32_t)n, eps, y);
   return hipGetLastError();
 }
 
@@ -48,7 +48,7 @@ hipError_t launch_binary(int op, const float* a, const float* b, uint64_t n, flo
   if (n == 0) return hipSuccess;
   const uint32_t gb = grid_blocks(n, 256);
   if (!gb) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(binary_kernel, dim3(gb), dim3(256), 0, st, op, a, b, n, out);
+  RF_KLAUNCH(binary_kernel, dim3(gb), dim3(256), 0, st, op, a, b, n, out);
   return hipGetLastError();
 }
 
@@ -63,7 +63,7 @@ hipError_t launch_silu(const float* x, uint64_t n, float* y, hipStream_t st) {
   if (n == 0) return hipSuccess;
   const uint32_t gb = grid_blocks(n, 256);
   if (!gb) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(silu_kernel, dim3(gb), dim3(256), 0, st, x, n, y);
+  RF_KLAUNCH(silu_kernel, dim3(gb), dim3(256), 0, st, x, n, y);
   return hipGetLastError();
 }
 
@@ -76,7 +76,7 @@ hipError_t launch_bias_add(float* v, const float* b, uint64_t n, hipStream_t st)
   if (n == 0) return hipSuccess;
   const uint32_t gb = grid_blocks(n, 256);
   if (!gb) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(bias_add_kernel, dim3(gb), dim3(256), 0, st, v, b, n);
+  RF_KLAUNCH(bias_add_kernel, dim3(gb), dim3(256), 0, st, v, b, n);
   return hipGetLastError();
 }
 
@@ -118,7 +118,7 @@ __global__ __launch_bounds__(1024) void softmax_kernel(float* __restrict__ v, ui
 }
 
 hipError_t launch_softmax(float* v, uint64_t n, hipStream_t st) {
-  hipLaunchKernelGGL(softmax_kernel, dim3(1), dim3(1024), 0, st, v, (uint32_t)n);
+  RF_KLAUNCH(softmax_kernel, dim3(1), dim3(1024), 0, st, v, (uint32_t)n);
   return hipGetLastError();
 }
 
@@ -144,7 +144,7 @@ hipError_t launch_rope_pair(float* q, float* k, const RopeCS& cs, uint32_t hd, u
                             hipStream_t st) {
   const uint32_t n = (qh + kvh) * (hd / 2);
   if (n == 0) return hipSuccess;
-  hipLaunchKernelGGL(rope_kernel, dim3((n + 255) / 256), dim3(256), 0, st, q, k, cs, hd, qh, kvh);
+  RF_KLAUNCH(rope_kernel, dim3((n + 255) / 256), dim3(256), 0, st, q, k, cs, hd, qh, kvh);
   return hipGetLastError();
 }
 
@@ -268,8 +268,8 @@ uint32_t argmax_partials(uint64_t n) {
 hipError_t launch_argmax(const float* logits, uint64_t n, uint32_t* out, float* ws_val, uint32_t* ws_idx,
                          uint32_t* ring, const int32_t* d_pos, hipStream_t st) {
   const uint32_t np = argmax_partials(n);
-  hipLaunchKernelGGL(argmax_stage1, dim3(np), dim3(256), 0, st, logits, n, ws_val, ws_idx);
-  hipLaunchKernelGGL(argmax_stage2, dim3(1), dim3(64), 0, st, logits, ws_val, ws_idx, np, out, ring, d_pos);
+  RF_KLAUNCH(argmax_stage1, dim3(np), dim3(256), 0, st, logits, n, ws_val, ws_idx);
+  RF_KLAUNCH(argmax_stage2, dim3(1), dim3(64), 0, st, logits, ws_val, ws_idx, np, out, ring, d_pos);
   return hipGetLastError();
 }
 
@@ -283,13 +283,13 @@ hipError_t launch_argmax_embed(const float* logits, uint64_t n, uint32_t* out, f
   if (in_dim % qk != 0 || (et != T_F32 && et != T_F16 && et != T_BF16 && in_dim % 32 != 0)) return hipErrorInvalidValue;
   const uint64_t row_bytes = in_dim / qk * bs;
   const uint32_t np = argmax_partials(n);
-  hipLaunchKernelGGL(argmax_stage1, dim3(np), dim3(256), 0, st, logits, n, ws_val, ws_idx);
+  RF_KLAUNCH(argmax_stage1, dim3(np), dim3(256), 0, st, logits, n, ws_val, ws_idx);
   const uint8_t* e = static_cast<const uint8_t*>(embd);
   const uint32_t d = (uint32_t)in_dim;
   switch (et) {
 #define RF_AE(TT)                                                                                                   \
   case TT:                                                                                                          \
-    hipLaunchKernelGGL(argmax_embed_kernel<TT>, dim3(1), dim3(256), 0, st, logits, ws_val, ws_idx, np, out, ring,  \
+    RF_KLAUNCH(argmax_embed_kernel<TT>, dim3(1), dim3(256), 0, st, logits, ws_val, ws_idx, np, out, ring,  \
                        d_pos, e, d, row_bytes, hidden);                                                           \
     break;
     RF_AE(T_F32) RF_AE(T_F16) RF_AE(T_BF16) RF_AE(T_Q4_0) RF_AE(T_Q5_0) RF_AE(T_Q8_0) RF_AE(T_Q2_K) RF_AE(T_Q3_K)
@@ -353,7 +353,7 @@ hipError_t launch_dequant_rows(uint32_t t, const void* wv, uint64_t in_dim, uint
     const uint64_t n = rows * in_dim;
     const uint32_t gb = n / rows == in_dim ? grid_blocks(n, 256) : 0u;
     if (!gb) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(decode_plain_kernel, dim3(gb), dim3(256), 0, st, t, w, in_dim, rows,
+    RF_KLAUNCH(decode_plain_kernel, dim3(gb), dim3(256), 0, st, t, w, in_dim, rows,
                        out, token_index, token_rows);
     return hipGetLastError();
   }
@@ -365,7 +365,7 @@ hipError_t launch_dequant_rows(uint32_t t, const void* wv, uint64_t in_dim, uint
   if (!gb || in_dim > 0xFFFFFFFFull) return hipErrorInvalidValue;
   const dim3 grid(gb), blk(256);
   switch (t) {
-#define RF_DQ(TT) case TT: hipLaunchKernelGGL(dequant_kernel<TT>, grid, blk, 0, st, w, (uint32_t)in_dim, rows, row_bytes, out, token_index, token_rows); break;
+#define RF_DQ(TT) case TT: RF_KLAUNCH(dequant_kernel<TT>, grid, blk, 0, st, w, (uint32_t)in_dim, rows, row_bytes, out, token_index, token_rows); break;
     RF_DQ(T_Q4_0) RF_DQ(T_Q5_0) RF_DQ(T_Q8_0) RF_DQ(T_Q2_K) RF_DQ(T_Q3_K) RF_DQ(T_Q4_K) RF_DQ(T_Q5_K)
     RF_DQ(T_Q6_K) RF_DQ(T_Q8_K)
 #undef RF_DQ
@@ -378,7 +378,7 @@ hipError_t launch_dequant_rows(uint32_t t, const void* wv, uint64_t in_dim, uint
 __global__ void advance_pos_kernel(int32_t* p) { *p += 1; }
 
 hipError_t launch_advance_pos(int32_t* d_pos, hipStream_t st) {
-  hipLaunchKernelGGL(advance_pos_kernel, dim3(1), dim3(1), 0, st, d_pos);
+  RF_KLAUNCH(advance_pos_kernel, dim3(1), dim3(1), 0, st, d_pos);
   return hipGetLastError();
 }
 
@@ -390,12 +390,12 @@ __global__ void fill_kernel(float* p, float v, uint64_t n) {
 }
 
 hipError_t launch_set_u32(uint32_t* p, uint32_t v, hipStream_t st) {
-  hipLaunchKernelGGL(set_u32_kernel, dim3(1), dim3(1), 0, st, p, v);
+  RF_KLAUNCH(set_u32_kernel, dim3(1), dim3(1), 0, st, p, v);
   return hipGetLastError();
 }
 
 hipError_t launch_set_i32(int32_t* p, int32_t v, hipStream_t st) {
-  hipLaunchKernelGGL(set_i32_kernel, dim3(1), dim3(1), 0, st, p, v);
+  RF_KLAUNCH(set_i32_kernel, dim3(1), dim3(1), 0, st, p, v);
   return hipGetLastError();
 }
 
@@ -403,7 +403,7 @@ hipError_t launch_fill(float* p, float v, uint64_t n, hipStream_t st) {
   if (n == 0) return hipSuccess;
   const uint32_t gb = grid_blocks(n, 256);
   if (!gb) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(fill_kernel, dim3(gb), dim3(256), 0, st, p, v, n);
+  RF_KLAUNCH(fill_kernel, dim3(gb), dim3(256), 0, st, p, v, n);
   return hipGetLastError();
 }
 
@@ -564,7 +564,7 @@ hipError_t launch_synth(uint32_t t, uint64_t seed, uint64_t first, uint64_t nblk
   const uint64_t sc = host_synth_u64(seed ^ 0x3C3C3C3C3C3C3C3Cull, 0);
   const uint32_t gb = grid_blocks(nblk, 256);
   if (!gb) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(synth_kernel, dim3(gb), dim3(256), 0, st, t, ss, sc, first, nblk,
+  RF_KLAUNCH(synth_kernel, dim3(gb), dim3(256), 0, st, t, ss, sc, first, nblk,
                      mul, static_cast<uint8_t*>(dst), (uint32_t)bs);
   return hipGetLastError();
 }

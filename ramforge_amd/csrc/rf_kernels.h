@@ -7,6 +7,21 @@ namespace rf {
 
 enum { EPI_STORE = 0, EPI_RESIDUAL = 1, EPI_SWIGLU = 2 };
 
+// Planning pass: while set on the calling thread, the launchers do all their
+// host-side work (dispatch, the one-time kernel setup of dynamic LDS and
+// occupancy) but launch nothing.  The model runs a decode step this way
+// before it captures one, so no setup call falls inside the capture.
+extern thread_local bool g_plan_only;
+#define RF_KLAUNCH(...)                                   \
+  do {                                                    \
+    if (!::rf::g_plan_only) hipLaunchKernelGGL(__VA_ARGS__); \
+  } while (0)
+
+// hipSuccess, or hipErrorStreamCaptureUnsupported when st is being captured:
+// a launcher's one-time kernel setup (hipFuncSetAttribute, occupancy
+// queries) runs outside stream captures only.
+hipError_t setup_outside_capture(hipStream_t st);
+
 // Workgroups of `per` threads that cover n > 0 items, or 0 when that exceeds
 // the 2^31 - 1 workgroups of a grid dimension: the launcher then fails
 // instead of covering a truncated range.
@@ -130,11 +145,19 @@ PkPlan plan_packed(uint32_t t, uint64_t in_dim);
 hipError_t launch_matvec_packed(uint32_t t, const PkSegDesc* segs, int nseg, const float* x, const float* norm_w,
                                 float eps, uint64_t in_dim, int epi, hipStream_t st, int32_t* advance = nullptr,
                                 const PkMerge* mrg = nullptr);
-// True when launch_matvec_packed can merge attention chunk records into x
-// for this projection (EPI_RESIDUAL, no norm, one segment of `rows` rows):
+// hipSuccess when launch_matvec_packed can merge attention chunk records into
+// x for this projection (EPI_RESIDUAL, no norm, one segment of `rows` rows):
 // the single-step launch of Q8_0 / Q4_0 / Q4_K with in_dim = qh * hd, hd a
-// power of two from 16, at most 8 chunks and 64 query heads.
-bool pk_merge_supported(uint32_t t, uint64_t in_dim, uint64_t rows, uint32_t nsplit, uint32_t qh, uint32_t hd);
+// power of two from 16, at most 8 chunks and 64 query heads;
+// hipErrorNotSupported when it cannot; hipErrorStreamCaptureUnsupported when
+// answering needs the kernel's one-time setup while st is being captured.
+hipError_t pk_merge_supported(uint32_t t, uint64_t in_dim, uint64_t rows, uint32_t nsplit, uint32_t qh, uint32_t hd,
+                              hipStream_t st);
+// The matvec_packed instance the calling thread launched last (also in a
+// planning pass), as the kernel trace names it; "" after a clear or when the
+// last launch was not a packed one.
+const char* last_packed_kernel();
+void clear_last_packed_kernel();
 // GGUF payload [rows][in_dim] -> packed layout (distinct buffers).
 hipError_t launch_pack(uint32_t t, const void* raw, void* packed, uint64_t rows, uint64_t in_dim, hipStream_t st);
 

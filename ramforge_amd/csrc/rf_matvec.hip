@@ -510,19 +510,21 @@ static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 
 template <uint32_t T, int EPI>
 static hipError_t launch_tiled_t(const MvArgs& a, uint32_t grid, const MvPlan& p, hipStream_t st) {
-  hipLaunchKernelGGL((matvec_tiled<T, EPI>), dim3(grid), dim3(p.threads), p.lds_bytes, st, a);
+  RF_KLAUNCH((matvec_tiled<T, EPI>), dim3(grid), dim3(p.threads), p.lds_bytes, st, a);
   return hipGetLastError();
 }
 
 // Resident workgroups per CU of one persistent kernel instance (registers,
-// LDS and waves all counted by the runtime), cached per shape.
+// LDS and waves all counted by the runtime), cached per shape.  0 when the
+// query would run while st is being captured (setup_outside_capture).
 template <uint32_t T, int EPI>
-static uint32_t stream_occupancy(uint32_t threads, uint32_t lds) {
+static uint32_t stream_occupancy(uint32_t threads, uint32_t lds, hipStream_t st) {
   static std::mutex mu;
   std::lock_guard<std::mutex> lock(mu);
   static uint32_t cache_threads[8] = {0}, cache_lds[8] = {0}, cache_val[8] = {0};
   for (int i = 0; i < 8; ++i)
     if (cache_threads[i] == threads && cache_lds[i] == lds) return cache_val[i];
+  if (setup_outside_capture(st) != hipSuccess) return 0;
   int n = 0;
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, matvec_stream<T, EPI>, (int)threads, (size_t)lds) !=
           hipSuccess || n < 1)
@@ -540,10 +542,12 @@ static uint32_t stream_occupancy(uint32_t threads, uint32_t lds) {
 template <uint32_t T, int EPI>
 static hipError_t launch_stream_t(const MvArgs& a, uint32_t tiles, const MvPlan& p, hipStream_t st) {
   // balanced persistent grid: every workgroup walks k tiles
-  const uint64_t max_grid = (uint64_t)cu_count() * stream_occupancy<T, EPI>(p.s_threads, p.s_lds_bytes);
+  const uint32_t occ = stream_occupancy<T, EPI>(p.s_threads, p.s_lds_bytes, st);
+  if (occ == 0) return hipErrorStreamCaptureUnsupported;
+  const uint64_t max_grid = (uint64_t)cu_count() * occ;
   const uint64_t k = (tiles + max_grid - 1) / max_grid;
   const uint32_t grid = (uint32_t)((tiles + k - 1) / k);
-  hipLaunchKernelGGL((matvec_stream<T, EPI>), dim3(grid), dim3(p.s_threads), p.s_lds_bytes, st, a);
+  RF_KLAUNCH((matvec_stream<T, EPI>), dim3(grid), dim3(p.s_threads), p.s_lds_bytes, st, a);
   return hipGetLastError();
 }
 
@@ -576,7 +580,7 @@ hipError_t launch_matvec_segments(uint32_t t, const MvSegDesc* segs, int nseg, c
       if (rows == 0) continue;
       dim3 grid((rows + 3) / 4);
       switch (t) {
-#define RF_ROWWISE(TT) case TT: hipLaunchKernelGGL(matvec_rowwise<TT>, grid, dim3(256), 0, st, static_cast<const uint8_t*>(segs[i].w), x, segs[i].y, (uint32_t)in_dim, rows, p.row_bytes); break;
+#define RF_ROWWISE(TT) case TT: RF_KLAUNCH(matvec_rowwise<TT>, grid, dim3(256), 0, st, static_cast<const uint8_t*>(segs[i].w), x, segs[i].y, (uint32_t)in_dim, rows, p.row_bytes); break;
         RF_ROWWISE(T_Q8_0) RF_ROWWISE(T_Q4_0) RF_ROWWISE(T_Q5_0) RF_ROWWISE(T_Q4_K) RF_ROWWISE(T_Q5_K)
         RF_ROWWISE(T_Q6_K) RF_ROWWISE(T_Q2_K) RF_ROWWISE(T_Q3_K) RF_ROWWISE(T_Q8_K) RF_ROWWISE(T_F32)
 #undef RF_ROWWISE
@@ -628,8 +632,10 @@ hipError_t launch_matvec_segments(uint32_t t, const MvSegDesc* segs, int nseg, c
 }
 
 // Loads this file's code object on the current device (HIP defers that to a
-// kernel's first use, which may otherwise fall inside a stream capture).
+// kernel's first use, which may otherwise fall inside a stream capture) and
+// caches the device's CU count the launchers read.
 hipError_t load_module_matvec() {
+  (void)cu_count();
   hipFuncAttributes fa;
   return hipFuncGetAttributes(&fa, reinterpret_cast<const void*>(matvec_rowwise<T_F32>));
 }

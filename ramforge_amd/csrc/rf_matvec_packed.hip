@@ -35,6 +35,7 @@
 #include "rf_kernels.h"
 
 #include <algorithm>
+#include <cstdio>
 #include <mutex>
 #include <type_traits>
 
@@ -1062,7 +1063,9 @@ static int pk_cu_count() {
 }
 
 // Resident workgroups per CU of one kernel at one LDS size; the caller keeps
-// one cache per kernel (a few distinct sizes per model).
+// one cache per kernel (a few distinct sizes per model).  A miss runs the
+// one-time setup (dynamic LDS attribute, occupancy query) and is refused (-1)
+// while st is being captured.
 struct PkOccCache {
   std::mutex mu;
   uint32_t keys[16];
@@ -1070,10 +1073,11 @@ struct PkOccCache {
   int n = 0;
   uint32_t attr = 0;  // dynamic LDS the kernel has been opened up to (above 64 KiB)
 };
-static int pk_occupancy(PkOccCache& c, const void* kern, int nt, uint32_t lds) {
+static int pk_occupancy(PkOccCache& c, const void* kern, int nt, uint32_t lds, hipStream_t st) {
   std::lock_guard<std::mutex> lock(c.mu);
   for (int i = 0; i < c.n; ++i)
     if (c.keys[i] == lds) return c.vals[i];
+  if (setup_outside_capture(st) != hipSuccess) return -1;
   if (lds > 65536 && lds > c.attr) {
     if (hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) return 0;
     c.attr = lds;
@@ -1087,6 +1091,19 @@ static int pk_occupancy(PkOccCache& c, const void* kern, int nt, uint32_t lds) {
   }
   return occ;
 }
+
+// Name of the matvec_packed instance the calling thread launched (or, in a
+// planning pass, would launch) last, spelled as the profiler's kernel trace
+// spells it, so that a measurement can be matched to the kernel that ran.
+static thread_local char t_last_kernel[128];
+template <uint32_t T, int EPI, bool NORM, int U, int LPW, int NB, int NT, bool IX, bool ALLF, bool MRG>
+static void note_kernel() {
+  auto b = [](bool v) { return v ? "true" : "false"; };
+  snprintf(t_last_kernel, sizeof t_last_kernel, "void rf::matvec_packed<%uu, %d, %s, %d, %d, %d, %d, %s, %s, %s>(rf::PkArgs)",
+           T, EPI, b(NORM), U, LPW, NB, NT, b(IX), b(ALLF), b(MRG));
+}
+const char* last_packed_kernel() { return t_last_kernel; }
+void clear_last_packed_kernel() { t_last_kernel[0] = 0; }
 
 // x as digit planes on the launches with >= 24 KiB of codes per wavefront
 // (1), on every Q8_0 / Q4_0 launch whose LDS holds them (2), or float x
@@ -1130,7 +1147,8 @@ static hipError_t launch_pk(const PkArgs& a, uint32_t lds, hipStream_t st) {
   constexpr int U = 1;
   static PkOccCache cache, cache_ix;  // one per kernel variant
   auto kern = matvec_packed<T, EPI, NORM, U, LPW, NB, NT, false>;
-  const int occ = pk_occupancy(cache, reinterpret_cast<const void*>(kern), NT, lds);
+  const int occ = pk_occupancy(cache, reinterpret_cast<const void*>(kern), NT, lds, st);
+  if (occ < 0) return hipErrorStreamCaptureUnsupported;
   if (occ < 1) return hipErrorInvalidConfiguration;
   const uint64_t tasks = (a.rows_total + U - 1) / U, nw = NT / 64;
   uint64_t grid = pk_grid(tasks, nw, occ, EPI);
@@ -1148,13 +1166,16 @@ static hipError_t launch_pk(const PkArgs& a, uint32_t lds, hipStream_t st) {
     const bool want = g_digits == 2 || (g_digits == 1 && code_bytes >= 24576);
     if (want && lds_ix + PK_STATIC_LDS <= pk_lds_limit()) {
       auto kix = matvec_packed<T, EPI, NORM, U, LPW, NB, NT, true>;
-      const int occ_ix = pk_occupancy(cache_ix, reinterpret_cast<const void*>(kix), NT, (uint32_t)lds_ix);
+      const int occ_ix = pk_occupancy(cache_ix, reinterpret_cast<const void*>(kix), NT, (uint32_t)lds_ix, st);
+      if (occ_ix < 0) return hipErrorStreamCaptureUnsupported;
       if (occ_ix < 1) return hipErrorInvalidConfiguration;
-      hipLaunchKernelGGL(kix, dim3((uint32_t)pk_grid(tasks, nw, occ_ix, EPI)), dim3(NT), (uint32_t)lds_ix, st, a);
+      note_kernel<T, EPI, NORM, U, LPW, NB, NT, true, false, false>();
+      RF_KLAUNCH(kix, dim3((uint32_t)pk_grid(tasks, nw, occ_ix, EPI)), dim3(NT), (uint32_t)lds_ix, st, a);
       return hipGetLastError();
     }
   }
-  hipLaunchKernelGGL(kern, dim3((uint32_t)grid), dim3(NT), lds, st, a);
+  note_kernel<T, EPI, NORM, U, LPW, NB, NT, false, false, false>();
+  RF_KLAUNCH(kern, dim3((uint32_t)grid), dim3(NT), lds, st, a);
   return hipGetLastError();
 }
 
@@ -1168,7 +1189,8 @@ int packed_inflight() { return g_inflight; }
 
 template <uint32_t T, int EPI, bool NORM, int LPW, int NB>
 static hipError_t launch_pk_all_nb(const PkArgs& a, uint32_t lds, uint64_t grid, hipStream_t st) {
-  hipLaunchKernelGGL((matvec_packed<T, EPI, NORM, 1, LPW, NB, 512, false, true>), dim3((uint32_t)grid), dim3(512),
+  note_kernel<T, EPI, NORM, 1, LPW, NB, 512, false, true, false>();
+  RF_KLAUNCH((matvec_packed<T, EPI, NORM, 1, LPW, NB, 512, false, true>), dim3((uint32_t)grid), dim3(512),
                      lds, st, a);
   return hipGetLastError();
 }
@@ -1186,7 +1208,8 @@ static hipError_t launch_pk_all(const PkArgs& a, uint32_t lds, hipStream_t st, b
   *done = false;
   static PkOccCache cache;
   auto k1 = matvec_packed<T, EPI, NORM, 1, LPW, 1, 512, false, true>;
-  const int occ = pk_occupancy(cache, reinterpret_cast<const void*>(k1), 512, lds);
+  const int occ = pk_occupancy(cache, reinterpret_cast<const void*>(k1), 512, lds, st);
+  if (occ < 0) return hipErrorStreamCaptureUnsupported;
   if (occ < 1) return hipSuccess;
   const uint64_t nw = 8, cus = (uint64_t)pk_cu_count(), tasks = a.rows_total;
   const uint64_t grid = (tasks + nw - 1) / nw;
@@ -1224,12 +1247,14 @@ template <uint32_t T, int LPW>
 static hipError_t launch_pk_merge(const PkArgs& a, uint32_t lds, bool launch, hipStream_t st) {
   static PkOccCache cache;
   auto k = matvec_packed<T, EPI_RESIDUAL, false, 1, LPW, 1, 512, false, true, true>;
-  const int occ = pk_occupancy(cache, reinterpret_cast<const void*>(k), 512, lds);
+  const int occ = pk_occupancy(cache, reinterpret_cast<const void*>(k), 512, lds, st);
+  if (occ < 0) return hipErrorStreamCaptureUnsupported;
   const uint64_t nw = 8, cus = (uint64_t)pk_cu_count(), tasks = a.rows_total;
   const uint64_t grid = (tasks + nw - 1) / nw;
   if (occ < 1 || grid > cus * (uint64_t)occ || tasks > 2 * cus * nw) return hipErrorNotSupported;
   if (!launch) return hipSuccess;
-  hipLaunchKernelGGL(k, dim3((uint32_t)grid), dim3(512), lds, st, a);
+  note_kernel<T, EPI_RESIDUAL, false, 1, LPW, 1, 512, false, true, true>();
+  RF_KLAUNCH(k, dim3((uint32_t)grid), dim3(512), lds, st, a);
   return hipGetLastError();
 }
 
@@ -1242,12 +1267,14 @@ static hipError_t launch_pk_merge_t(uint32_t t, const PkArgs& a, uint32_t lds, b
   }
 }
 
-bool pk_merge_supported(uint32_t t, uint64_t in_dim, uint64_t rows, uint32_t nsplit, uint32_t qh, uint32_t hd) {
+hipError_t pk_merge_supported(uint32_t t, uint64_t in_dim, uint64_t rows, uint32_t nsplit, uint32_t qh, uint32_t hd,
+                              hipStream_t st) {
   uint32_t lds = 0;
-  if (rows == 0 || rows > 0xFFFFFFFFull || !pk_merge_shape(t, in_dim, nsplit, qh, hd, &lds)) return false;
+  if (rows == 0 || rows > 0xFFFFFFFFull || !pk_merge_shape(t, in_dim, nsplit, qh, hd, &lds))
+    return hipErrorNotSupported;
   PkArgs a{};
   a.rows_total = (uint32_t)rows;
-  return launch_pk_merge_t(t, a, lds, false, nullptr) == hipSuccess;
+  return launch_pk_merge_t(t, a, lds, false, st);
 }
 
 // Launch shape, from timing the 8B projections (Q8_0 and Q4_0; 4096 and
@@ -1390,17 +1417,20 @@ hipError_t launch_pack(uint32_t t, const void* raw, void* packed, uint64_t rows,
   const uint8_t* r = static_cast<const uint8_t*>(raw);
   uint8_t* o = static_cast<uint8_t*>(packed);
   switch (t) {
-    case T_Q8_0: hipLaunchKernelGGL(pack_blocks<T_Q8_0>, grid, dim3(256), 0, st, r, o, n); break;
-    case T_Q4_0: hipLaunchKernelGGL(pack_blocks<T_Q4_0>, grid, dim3(256), 0, st, r, o, n); break;
-    case T_Q4_K: hipLaunchKernelGGL(pack_blocks<T_Q4_K>, grid, dim3(256), 0, st, r, o, n); break;
-    default: hipLaunchKernelGGL(pack_blocks<T_Q6_K>, grid, dim3(256), 0, st, r, o, n); break;
+    case T_Q8_0: RF_KLAUNCH(pack_blocks<T_Q8_0>, grid, dim3(256), 0, st, r, o, n); break;
+    case T_Q4_0: RF_KLAUNCH(pack_blocks<T_Q4_0>, grid, dim3(256), 0, st, r, o, n); break;
+    case T_Q4_K: RF_KLAUNCH(pack_blocks<T_Q4_K>, grid, dim3(256), 0, st, r, o, n); break;
+    default: RF_KLAUNCH(pack_blocks<T_Q6_K>, grid, dim3(256), 0, st, r, o, n); break;
   }
   return hipGetLastError();
 }
 
 // Loads this file's code object on the current device (HIP defers that to a
-// kernel's first use, which may otherwise fall inside a stream capture).
+// kernel's first use, which may otherwise fall inside a stream capture) and
+// caches the device limits the launchers read.
 hipError_t load_module_packed() {
+  (void)pk_cu_count();
+  (void)pk_lds_limit();
   hipFuncAttributes fa;
   return hipFuncGetAttributes(&fa, reinterpret_cast<const void*>(pack_blocks<T_Q8_0>));
 }

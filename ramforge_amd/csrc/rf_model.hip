@@ -26,6 +26,7 @@
 #include <algorithm>
 #include <list>
 #include <cmath>
+#include <cstdio>
 #include <cstring>
 #include <string>
 #include <vector>
@@ -1148,12 +1149,17 @@ int attn_regime(const rf_model* m, uint64_t pos) {
 // Q8_0 / Q4_0 / Q4_K o-projections whose rows take the single-step launch
 // (q_heads * head_dim up to 4096).  rf_tune_attention_merge switches it off.
 static int g_oproj_merge = 1;
-static bool oproj_merges(const rf_model* m, size_t li, const AttnShape& sh) {
-  if (!g_oproj_merge || !m->attn_fast || !sh.per_q || sh.nsplit < 2) return false;
+static hipError_t oproj_merges(const rf_model* m, size_t li, const AttnShape& sh, bool* merge) {
+  *merge = false;
+  if (!g_oproj_merge || !m->attn_fast || !sh.per_q || sh.nsplit < 2) return hipSuccess;
   const rf_model_config& c = m->cfg;
   const Layer& L = m->layers[li];
-  return L.o.packed && pk_merge_supported(L.o.type, c.head_count * c.head_dim, c.embedding_length, sh.nsplit,
-                                          (uint32_t)c.head_count, (uint32_t)c.head_dim);
+  if (!L.o.packed) return hipSuccess;
+  const hipError_t e = pk_merge_supported(L.o.type, c.head_count * c.head_dim, c.embedding_length, sh.nsplit,
+                                          (uint32_t)c.head_count, (uint32_t)c.head_dim, m->ctx->compute);
+  if (e == hipErrorNotSupported) return hipSuccess;
+  *merge = e == hipSuccess;
+  return e;
 }
 
 // 2. RoPE + attention + K/V cache write.
@@ -1170,10 +1176,13 @@ int32_t enqueue_attention(rf_model* m, size_t li) {
   // the position this step processes picks the shape
   const AttnShape sh = attention_regime_shape(attn_regime(m, m->seq_len), a.qh, a.kvh, m->kv_max);
   a.per_q = sh.per_q; a.nsplit = sh.nsplit; a.waves = sh.waves;
-  m->oproj_merge = oproj_merges(m, li, sh);
-  a.defer_merge = m->oproj_merge ? 1u : 0u;
+  m->oproj_merge = false;
+  bool merge = false;
+  RF_LAUNCH(oproj_merges(m, li, sh, &merge), "attention (o-projection merge plan)");
+  a.defer_merge = merge ? 1u : 0u;
   a.denom = sqrtf((float)hd);
   RF_LAUNCH(m->attn_fast ? launch_attention(a, st) : launch_attention_naive(a, st), "attention");
+  m->oproj_merge = merge;  // only once the launch that leaves the chunk records succeeded
   return RF_OK;
 }
 
@@ -1268,6 +1277,7 @@ int32_t prof_group(rf_model* m, int kind, F&& body) {
 
 int32_t enqueue_layer(rf_model* m, size_t li, int32_t* advance = nullptr) {
   int32_t rc;
+  m->oproj_merge = false;
   if ((rc = prof_group(m, 0, [&] { return enqueue_qkv(m, li); }))) return rc;
   if ((rc = prof_group(m, 1, [&] { return enqueue_attention(m, li); }))) return rc;
   if ((rc = prof_group(m, 2, [&] { return enqueue_oproj(m, li); }))) return rc;
@@ -1343,6 +1353,20 @@ int32_t enqueue_logits(rf_model* m) {
 
 // One decode step: logits -> argmax (token stored at ring[pos]) with the
 // chosen token's embedding row decoded by the same kernel -> layers.
+int32_t enqueue_decode_step(rf_model* m);
+
+// The host side of one decode step with no launch (g_plan_only): every
+// launcher's one-time kernel setup for this step's shapes (dynamic LDS,
+// occupancy) runs here, before the step is captured; inside the capture
+// such setup is refused (setup_outside_capture).
+int32_t plan_decode_step(rf_model* m) {
+  g_plan_only = true;
+  const int32_t rc = enqueue_decode_step(m);
+  g_plan_only = false;
+  m->oproj_merge = false;
+  return rc;
+}
+
 int32_t enqueue_decode_step(rf_model* m) {
   int32_t rc = enqueue_logits(m);
   if (rc) return rc;
@@ -1871,6 +1895,15 @@ int32_t rf_model_kv_capacity(rf_model* m, uint64_t* tokens) {
   return RF_OK;
 }
 
+int32_t rf_model_paths(rf_model* m, uint64_t pos, int32_t* split_attention, int32_t* regime,
+                       int32_t* batched_prefill) {
+  if (!m || !split_attention || !regime || !batched_prefill) return set_error(RF_ERR_INVALID, "null argument");
+  *split_attention = m->attn_fast ? 1 : 0;
+  *regime = attn_regime(m, pos);
+  *batched_prefill = prefill_supported(m) ? 1 : 0;
+  return RF_OK;
+}
+
 int32_t rf_model_use_graph(rf_model* m, int32_t enable) {
   if (!m) return set_error(RF_ERR_INVALID, "null model");
   if (enable && m->prof)
@@ -1894,6 +1927,7 @@ int32_t rf_model_decode_steps(rf_model* m, uint64_t steps) {
     const int r = attn_regime(m, m->seq_len);
     if (m->use_graph && !m->graph_exec[r]) {
       // captured at the first step of its regime; replays read the position from d_pos
+      if ((rc = plan_decode_step(m))) return rc;
       RF_LAUNCH(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal), "begin capture");
       rc = enqueue_decode_step(m);
       hipGraph_t g = nullptr;
@@ -1912,6 +1946,39 @@ int32_t rf_model_decode_steps(rf_model* m, uint64_t steps) {
     }
     m->seq_len += 1;
   }
+  return RF_OK;
+}
+
+int32_t rf_model_kernel_name(rf_model* m, uint32_t kind, char* buf, uint64_t cap) {
+  if (!m || !buf || cap == 0) return set_error(RF_ERR_INVALID, "null argument");
+  if (kind < RF_KERNEL_QKV || kind > RF_KERNEL_LOGITS)
+    return set_error(RF_ERR_INVALID, "unknown kernel group %u", kind);
+  int32_t rc = check_ready(m);
+  if (rc) return rc;
+  if (m->streaming) return set_error(RF_ERR_UNSUPPORTED, "kernel naming needs every layer resident");
+  // a planning pass of the group on layer 0 (the o-projection after its
+  // attention, whose regime decides whether it merges chunk records)
+  clear_last_packed_kernel();
+  g_plan_only = true;
+  m->oproj_merge = false;
+  switch (kind) {
+    case RF_KERNEL_QKV: rc = enqueue_qkv(m, 0); break;
+    case RF_KERNEL_ATTENTION: rc = enqueue_attention(m, 0); break;
+    case RF_KERNEL_OPROJ:
+      rc = enqueue_attention(m, 0);
+      if (!rc) {
+        clear_last_packed_kernel();
+        rc = enqueue_oproj(m, 0);
+      }
+      break;
+    case RF_KERNEL_GATEUP: rc = enqueue_gateup(m, 0); break;
+    case RF_KERNEL_DOWN: rc = enqueue_down(m, 0); break;
+    default: rc = enqueue_logits(m); break;
+  }
+  g_plan_only = false;
+  m->oproj_merge = false;
+  if (rc) return rc;
+  snprintf(buf, cap, "%s", last_packed_kernel());
   return RF_OK;
 }
 
@@ -1938,6 +2005,7 @@ int32_t rf_model_time_kernel(rf_model* m, uint32_t kind, uint32_t reps, float* a
   // Attention is timed at the current position (the kernel only reads d_pos).
   const uint64_t hist = m->seq_len;
   uint64_t n = 0, bytes = 0;
+  m->oproj_merge = false;
   hipError_t e = hipEventRecord(e0, st);
   for (uint32_t r = 0; r < reps && e == hipSuccess && rc == RF_OK; ++r) {
     if (kind == RF_KERNEL_LOGITS) {

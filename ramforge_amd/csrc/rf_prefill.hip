@@ -756,6 +756,7 @@ static hipError_t mm_launch_t(const MmArgs& a, dim3 grid, hipStream_t st) {
   const uint32_t lds = 2u * (3u * NTT * 16u * MM_XB * 2u + (T == T_Q4_K ? MM_ST * NTT * 16u * 4u : 0u));
   static bool opened = false;
   if (!opened) {
+    if (setup_outside_capture(st) != hipSuccess) return hipErrorStreamCaptureUnsupported;
     if (lds > 65536) {
       hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(mm_packed<T, NTT, NW, DEPTH, SC8>),
                                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
@@ -763,7 +764,7 @@ static hipError_t mm_launch_t(const MmArgs& a, dim3 grid, hipStream_t st) {
     }
     opened = true;
   }
-  hipLaunchKernelGGL((mm_packed<T, NTT, NW, DEPTH, SC8>), grid, dim3(64 * NW), lds, st, a);
+  RF_KLAUNCH((mm_packed<T, NTT, NW, DEPTH, SC8>), grid, dim3(64 * NW), lds, st, a);
   return hipGetLastError();
 }
 
@@ -888,14 +889,14 @@ hipError_t launch_matmul_packed(uint32_t t, const MmSegDesc* segs, int nseg, con
   const uint64_t total = (uint64_t)n * r.mcols;
   const bool al = ((reinterpret_cast<uintptr_t>(norm_w) | reinterpret_cast<uintptr_t>(xn)) & 15u) == 0;
   if (norm_w && al && mm_reduce_vec4(r) && r.mcols <= 8192) {
-    if (r.mcols <= 4096) hipLaunchKernelGGL(mm_reduce_norm<1>, dim3((uint32_t)n), dim3(1024), 0, st, r, norm_w, eps, xn);
-    else hipLaunchKernelGGL(mm_reduce_norm<2>, dim3((uint32_t)n), dim3(1024), 0, st, r, norm_w, eps, xn);
+    if (r.mcols <= 4096) RF_KLAUNCH(mm_reduce_norm<1>, dim3((uint32_t)n), dim3(1024), 0, st, r, norm_w, eps, xn);
+    else RF_KLAUNCH(mm_reduce_norm<2>, dim3((uint32_t)n), dim3(1024), 0, st, r, norm_w, eps, xn);
     return hipGetLastError();
   }
   if (mm_reduce_vec4(r))
-    hipLaunchKernelGGL(mm_reduce4, dim3((uint32_t)((total / 4 + 255) / 256)), dim3(256), 0, st, r);
+    RF_KLAUNCH(mm_reduce4, dim3((uint32_t)((total / 4 + 255) / 256)), dim3(256), 0, st, r);
   else
-    hipLaunchKernelGGL(mm_reduce, dim3((uint32_t)((total + 255) / 256)), dim3(256), 0, st, r);
+    RF_KLAUNCH(mm_reduce, dim3((uint32_t)((total + 255) / 256)), dim3(256), 0, st, r);
   e = hipGetLastError();
   if (e != hipSuccess || !norm_w) return e;
   const MmSegDesc& d = segs[0];
@@ -956,9 +957,9 @@ hipError_t launch_rmsnorm_rows(const float* x, const float* w, uint64_t n, uint6
   const bool vec = n % 4 == 0 && ld % 4 == 0 && ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w) |
                                                    reinterpret_cast<uintptr_t>(y)) & 15u) == 0;
   const dim3 grid((uint32_t)rows), blk(256);
-  if (vec && n <= 4096) hipLaunchKernelGGL(rmsnorm_rows_kernel<4>, grid, blk, 0, st, x, w, (uint32_t)n, (uint32_t)ld, eps, y);
-  else if (vec && n <= 8192) hipLaunchKernelGGL(rmsnorm_rows_kernel<8>, grid, blk, 0, st, x, w, (uint32_t)n, (uint32_t)ld, eps, y);
-  else hipLaunchKernelGGL(rmsnorm_rows_kernel<0>, grid, blk, 0, st, x, w, (uint32_t)n, (uint32_t)ld, eps, y);
+  if (vec && n <= 4096) RF_KLAUNCH(rmsnorm_rows_kernel<4>, grid, blk, 0, st, x, w, (uint32_t)n, (uint32_t)ld, eps, y);
+  else if (vec && n <= 8192) RF_KLAUNCH(rmsnorm_rows_kernel<8>, grid, blk, 0, st, x, w, (uint32_t)n, (uint32_t)ld, eps, y);
+  else RF_KLAUNCH(rmsnorm_rows_kernel<0>, grid, blk, 0, st, x, w, (uint32_t)n, (uint32_t)ld, eps, y);
   return hipGetLastError();
 }
 
@@ -997,14 +998,16 @@ hipError_t launch_rope_kv_rows(const float* q, const float* k, const float* v, c
                                uint64_t ntok, uint32_t qh, uint32_t kvh, uint32_t hd, float* qr, float* kc,
                                float* vc, hipStream_t st) {
   if (ntok == 0) return hipSuccess;
-  hipLaunchKernelGGL(rope_kv_rows_kernel, dim3((uint32_t)ntok, qh + 2 * kvh), dim3(64), 0, st, q, k, v, rope,
+  RF_KLAUNCH(rope_kv_rows_kernel, dim3((uint32_t)ntok, qh + 2 * kvh), dim3(64), 0, st, q, k, v, rope,
                      (uint32_t)pos0, qh, kvh, hd, qr, kc, vc);
   return hipGetLastError();
 }
 
 // Loads this file's code object on the current device (HIP defers that to a
-// kernel's first use, which may otherwise fall inside a stream capture).
+// kernel's first use, which may otherwise fall inside a stream capture) and
+// caches the device's CU count the launchers read.
 hipError_t load_module_prefill() {
+  (void)mm_cu_count();
   hipFuncAttributes fa;
   return hipFuncGetAttributes(&fa, reinterpret_cast<const void*>(mm_reduce));
 }

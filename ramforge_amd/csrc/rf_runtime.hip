@@ -25,7 +25,21 @@ int32_t set_error(int32_t code, const char* fmt, ...) {
   return code;
 }
 
+thread_local bool g_plan_only = false;
+
+hipError_t setup_outside_capture(hipStream_t st) {
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (st && hipStreamIsCapturing(st, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
+    return hipErrorStreamCaptureUnsupported;
+  return hipSuccess;
+}
+
 int32_t hip_error(hipError_t e, const char* what) {
+  if (e == hipErrorStreamCaptureUnsupported)
+    return set_error(RF_ERR_INVALID,
+                     "%s: first launch of this kernel shape inside a stream capture; its one-time setup (dynamic "
+                     "LDS, occupancy) runs outside captures only: launch the same shape once before capturing",
+                     what);
   return set_error(RF_ERR_HIP, "%s failed: %s (%d)", what, hipGetErrorString(e), (int)e);
 }
 

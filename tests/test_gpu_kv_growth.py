@@ -10,11 +10,12 @@ import numpy as np
 import pytest
 
 from helpers import Q8_0
-from test_gpu_model import ALL_Q8, STREAM_CFG, STREAM_TYPES, TINY, _tiny_tensors
+from test_gpu_model import ALL_Q8, REGIME5_CFG, STREAM_CFG, STREAM_TYPES, TINY, _tiny_tensors
 
 pytestmark = pytest.mark.gpu
 
-GCFG = dict(TINY, context_length=1024)
+# head_dim 64: the split attention kernel (the any-shape kernel takes 32)
+GCFG = dict(TINY, context_length=1024, head_dim=64)
 
 
 def _rf():
@@ -151,6 +152,7 @@ def test_graph_replay_across_growth(ctx):
     fixed.close()
 
     m = _model(ctx, GCFG, T, 900, initial=40)
+    assert m.paths()["split_attention"]
     m.prefill(prompt)
     m.use_graph(True)
     m.decode_steps(200)
@@ -159,4 +161,37 @@ def test_graph_replay_across_growth(ctx):
     m.decode_steps(300)
     assert m.kv_positions() == 768
     assert m.read_tokens(300) == b
+    m.close()
+
+
+def test_graph_replay_across_growth_and_all_regimes(ctx):
+    """The split kernel's five regimes (64 query / 16 KV heads, head_dim 64,
+    capacity 1100: per KV head past 512 positions, longer chunks past 1024)
+    on a cache that starts at the prompt's 40 positions and grows in
+    256-position chunks while graph-replayed decode steps cross every growth
+    and regime boundary: the tokens of eager steps on a cache allocated up
+    front."""
+    T = _tiny_tensors(np.random.default_rng(1304), REGIME5_CFG, ALL_Q8)
+    prompt = [int(t) for t in np.random.default_rng(6).integers(0, REGIME5_CFG["vocab_size"], 40)]
+    steps = (150, 250, 300, 200, 150, 9)  # ends at position 1099, the last slot of the capacity
+    fixed = _model(ctx, REGIME5_CFG, T, 1100)
+    fixed.prefill(prompt)
+    want = []
+    for k in steps:
+        fixed.decode_steps(k)
+        want.append(fixed.read_tokens(k))
+    fixed.close()
+
+    m = _model(ctx, REGIME5_CFG, T, 1100, initial=40)
+    assert m.paths()["split_attention"]
+    assert {m.paths(p)["regime"] for p in range(40, 40 + sum(steps))} == {0, 1, 2, 3, 4}
+    m.prefill(prompt)
+    m.use_graph(True)
+    caps = []
+    for k, w in zip(steps, want):
+        m.decode_steps(k)
+        assert m.read_tokens(k) == w
+        caps.append(m.kv_positions())
+    m.use_graph(False)
+    assert caps == [256, 512, 768, 1024, 1100, 1100], caps
     m.close()

@@ -359,29 +359,37 @@ REGIME_CFG = dict(TINY, context_length=256, embedding_length=256, feed_forward_l
 # past 256 positions
 REGIME2_CFG = dict(TINY, context_length=512, embedding_length=256, feed_forward_length=512, head_count=64,
                    head_count_kv=64, head_dim=64)
-# 64 query / 16 KV heads at capacity 1100: per query head with 4 chunks up to
-# 512 positions (4 then 8 wavefronts), then per KV head with 16 chunks of 64
-# positions up to 1024 and longer chunks beyond: all five regimes
+# 64 query / 16 KV heads (4:1 GQA, head_dim 64) at capacity 1100: per query
+# head with 4 chunks up to 512 positions (4 then 8 wavefronts), then per KV
+# head with 16 chunks of 64 positions up to 1024 and longer chunks beyond:
+# all five regimes of the split kernel
 REGIME5_CFG = dict(TINY, context_length=1100, embedding_length=256, feed_forward_length=512, head_count=64,
-                   head_count_kv=16, head_dim=32)
+                   head_count_kv=16, head_dim=64)
 
 
-@pytest.mark.parametrize("cfg,cap,steps", [(REGIME_CFG, 160, (30, 40, 80)), (REGIME2_CFG, 320, (30, 40, 200, 40)),
-                                           (REGIME5_CFG, 1100, (30, 40, 200, 300, 500, 20))],
+@pytest.mark.parametrize("cfg,cap,steps,regimes",
+                         [(REGIME_CFG, 160, (30, 40, 80), {0, 1}), (REGIME2_CFG, 320, (30, 40, 200, 40), {0, 1, 2}),
+                          (REGIME5_CFG, 1100, (30, 40, 200, 300, 500, 20), {0, 1, 2, 3, 4})],
                          ids=["regimes-0-1", "regimes-0-1-2", "regimes-0-to-4"])
-def test_decode_graphs_cross_the_attention_regimes(ctx, orc, cfg, cap, steps):
+def test_decode_graphs_cross_the_attention_regimes(ctx, orc, cfg, cap, steps, regimes):
     """Decode from position 5 with graph replay across the attention launch
-    regimes: one chunk per query head up to 64 positions, then several chunks
-    per query head (4 and 8 wavefronts), then chunks per KV head (64 positions
-    with 4 wavefronts, longer with 8); each regime's graph is captured lazily.
-    Tokens equal the eager loop's and the oracle's."""
+    regimes of the split kernel: one chunk per query head up to 64
+    positions, then several chunks per query head (4 and 8 wavefronts), then
+    chunks per KV head (64 positions with 4 wavefronts, longer with 8); each
+    regime's graph is captured lazily.  The model must run the split kernel
+    and visit the listed regimes; tokens equal the eager loop's and the
+    oracle's."""
     rng = np.random.default_rng(961)
     T = _tiny_tensors(rng, cfg, ALL_Q8)
     prompt = [3, 1, 4, 1, 5]
     n = sum(steps)
     gm = _load_gpu(ctx, cfg, T, cap)
     om = orc.Model(cfg, T, kv_capacity=cap, threads=8)
+    orc.set_parity_threads(8)
     try:
+        assert gm.paths()["split_attention"], "the model fell back to the any-shape attention kernel"
+        seen = {gm.paths(p)["regime"] for p in range(len(prompt), len(prompt) + n)}
+        assert seen == regimes, seen
         ref = gm.generate(prompt, n)
         oref, margin = om.generate(prompt, n)
         first = next((i for i, (a, b) in enumerate(zip(ref, oref)) if a != b), None)
@@ -398,6 +406,7 @@ def test_decode_graphs_cross_the_attention_regimes(ctx, orc, cfg, cap, steps):
         assert got == ref[:n]
         gm.use_graph(False)
     finally:
+        orc.set_parity_threads(0)
         om.close()
         gm.close()
 

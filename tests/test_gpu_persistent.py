@@ -56,6 +56,7 @@ def test_streamed_persistent_matches_resident(orc, tied):
     for m in (sm, rm):
         m.reset()
     prompt = [int(t) for t in np.random.default_rng(7).integers(0, cfg["vocab_size"], 20)]
+    assert sm.paths()["batched_prefill"] and rm.paths()["batched_prefill"]
     ha = sm.prefill(prompt, want_hidden=True)  # batched: embedding rows read from host memory
     hb = rm.prefill(prompt, want_hidden=True)
     assert np.array_equal(ha, hb)

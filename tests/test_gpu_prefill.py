@@ -107,6 +107,10 @@ def test_matmul_packed_validation(ctx):
 
 
 KQ_CFG = dict(TINY, embedding_length=256, feed_forward_length=512, head_dim=64, context_length=256)
+# head_dim 64: the split attention kernel, which the batched prefill needs
+# (with head_dim 32 the model runs the any-shape kernel and prefill falls
+# back to one forward per token)
+PF_CFG = dict(TINY, context_length=256, head_dim=64)
 ALL_KQ = dict(embd=Q4_K, out=Q6_K, q=Q4_K, k=Q4_K, v=Q6_K, o=Q4_K, gate=Q4_K, up=Q4_K, down=Q6_K)
 
 
@@ -119,13 +123,14 @@ def test_prefill_matches_token_by_token(ctx, orc, kind, history, plen):
     tokens at history 3 crosses the 64-position attention regime inside a
     chunk."""
     types = {"q8": ALL_Q8, "q4": ALL_Q4, "mixed": MIXED, "kq": ALL_KQ, "kq_bias": ALL_KQ}[kind]
-    cfg = dict(TINY, context_length=256) if kind in ("q8", "q4") else dict(KQ_CFG)
+    cfg = dict(PF_CFG) if kind in ("q8", "q4") else dict(KQ_CFG)
     rng = np.random.default_rng(3300 + plen + history)
     T = _tiny_tensors(rng, cfg, types, bias=kind == "kq_bias")
     cap = history + plen + 24
     gm = _load_gpu(ctx, cfg, T, cap)
     om = orc.Model(cfg, T, kv_capacity=cap, threads=8)
     try:
+        assert gm.paths()["batched_prefill"], "prefill fell back to one forward per token"
         prompt = [int(v) for v in rng.integers(0, cfg["vocab_size"], history + plen)]
         print(f"  prefill {kind} history={history} plen={plen}", flush=True)
         for p in range(history):
@@ -153,11 +158,12 @@ def test_prefill_matches_token_by_token(ctx, orc, kind, history, plen):
 def test_prefill_then_device_decode_graph(ctx, orc):
     """A batched prompt followed by graph-replayed device decode steps gives
     the tokens of the host generate loop with a token-by-token prompt."""
-    cfg = dict(TINY, context_length=256)
+    cfg = dict(PF_CFG)
     rng = np.random.default_rng(3400)
     T = _tiny_tensors(rng, cfg, ALL_Q8)
     gm = _load_gpu(ctx, cfg, T, 200)
     try:
+        assert gm.paths()["batched_prefill"]
         prompt = [int(v) for v in rng.integers(0, cfg["vocab_size"], 45)]
         ref = gm.generate(prompt, 41)
         gm.reset()
@@ -175,7 +181,7 @@ def test_prefill_falls_back_for_unpacked_weights(ctx, orc):
     """With packing disabled the projections stay in GGUF layout and the
     prefill runs the token-by-token forward: bit-identical hidden state."""
     rf = _rf()
-    cfg = dict(TINY, context_length=128)
+    cfg = dict(PF_CFG, context_length=128)
     rng = np.random.default_rng(3500)
     T = _tiny_tensors(rng, cfg, ALL_Q8)
     prompt = [int(v) for v in rng.integers(0, cfg["vocab_size"], 12)]
@@ -183,6 +189,7 @@ def test_prefill_falls_back_for_unpacked_weights(ctx, orc):
     rf.tune_packed_weights(0)
     try:
         gm = _load_gpu(ctx, cfg, T, 32)
+        assert not gm.paths()["batched_prefill"]
         h = gm.prefill(prompt, want_hidden=True)
         gm.reset()
         hr = None
@@ -215,7 +222,7 @@ def test_prefill_streaming_model(ctx, orc):
     """Layer streaming: a batched prompt loads each layer once per 64-token
     chunk, gives the resident model's tokens and hands its workspace back
     (the layer cache may use that VRAM while decoding)."""
-    cfg = dict(TINY, context_length=256)
+    cfg = dict(PF_CFG)
     rng = np.random.default_rng(3700)
     T = _tiny_tensors(rng, cfg, ALL_Q8)
     prompt = [int(v) for v in rng.integers(0, cfg["vocab_size"], 80)]
@@ -229,6 +236,7 @@ def test_prefill_streaming_model(ctx, orc):
         for name, (t, ne0, ne1, arr) in T.items():
             sm.set_tensor(name, t, ne0, ne1, arr)
         used = ctx.vram_used
+        assert sm.paths()["batched_prefill"]
         sm.prefill(prompt)
         # no layer cache: every layer and the prefill workspace are released again
         assert ctx.vram_used == used

@@ -100,3 +100,58 @@ def test_stale_graph_refused_after_workspace_growth():
         cap2.graph.replay(2)
         assert np.array_equal(out.numpy().view(np.uint32), want.view(np.uint32))
         cap2.graph.close()
+
+
+_SETUP_SCRIPT = r"""
+import sys
+import numpy as np
+sys.path.insert(0, sys.argv[1])
+import ramforge_amd as rf
+from ramforge_amd import GGML
+
+rng = np.random.default_rng(35)
+rows, k = 96, 4096
+raw = rng.integers(0, 256, size=(rows, k // 32, 34), dtype=np.uint8)
+raw[:, :, 0:2] = np.frombuffer(np.full(rows * k // 32, 0x2000, np.uint16).tobytes(), np.uint8).reshape(rows, -1, 2)
+with rf.Context(0) as c:
+    w = c.array(raw.reshape(-1))
+    p = c.empty((raw.size,), "uint8")
+    rf.pack_weights(c, GGML.Q8_0, w, rows, k, p)
+    x = c.array(rng.normal(0, 1, k).astype(np.float32))
+    y = c.empty((rows,))
+    # the first launch of this kernel shape in the process: its setup
+    # (dynamic LDS attribute, occupancy) is refused inside a capture
+    try:
+        with c.capture():
+            rf.matvec_packed(c, GGML.Q8_0, p, (rows, k), x, y)
+        print("captured without refusal")
+        sys.exit(1)
+    except rf.RamforgeError as e:
+        assert "inside a stream capture" in str(e), str(e)
+    # once launched outside a capture, the same shape captures and replays
+    rf.matvec_packed(c, GGML.Q8_0, p, (rows, k), x, y)
+    c.synchronize()
+    want = y.numpy()
+    y.upload(np.zeros(rows, np.float32))
+    with c.capture() as cap:
+        rf.matvec_packed(c, GGML.Q8_0, p, (rows, k), x, y)
+    cap.graph.replay(2)
+    assert np.array_equal(y.numpy().view(np.uint32), want.view(np.uint32))
+    cap.graph.close()
+print("ok")
+"""
+
+
+def test_first_launch_setup_refused_inside_capture():
+    """A launcher's one-time kernel setup (dynamic LDS attribute, occupancy
+    query) is never made inside a stream capture: the first launch of a
+    kernel shape inside a capture is refused with a clear error, and the
+    same shape captures and replays once it has run outside.  Run in a fresh
+    process, where no shape has been set up yet."""
+    import os
+    import subprocess
+    import sys
+
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    r = subprocess.run([sys.executable, "-c", _SETUP_SCRIPT, root], capture_output=True, text=True, timeout=240)
+    assert r.returncode == 0 and r.stdout.strip().endswith("ok"), r.stdout + r.stderr

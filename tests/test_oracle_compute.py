@@ -323,6 +323,23 @@ def test_attention_kat_and_float64(orc):
     assert np.allclose(got.reshape(qh, hd), mean_v[np.arange(qh) * kvh // qh], atol=1e-5)
 
 
+def test_attention_parity_threads_bit_identical(orc):
+    """The parity-run accelerator spreads attention heads over threads; each
+    head's arithmetic is unchanged, so the output is bit-identical to the
+    single-threaded restatement (which the timed CPU baseline runs)."""
+    rng = np.random.default_rng(12)
+    hist, qh, kvh, hd = 700, 32, 8, 128
+    args = [rng.normal(0, 1, n).astype(np.float32) for n in (qh * hd, hist * kvh * hd, hist * kvh * hd, kvh * hd,
+                                                              kvh * hd)]
+    one = orc.attention(*args, hist, qh, kvh, hd)
+    orc.set_parity_threads(8)
+    try:
+        many = orc.attention(*args, hist, qh, kvh, hd)
+    finally:
+        orc.set_parity_threads(0)
+    assert np.array_equal(one.view(np.uint32), many.view(np.uint32))
+
+
 def test_argmax_tie_and_nan_rules(orc):
     assert orc.argmax([1.0, 3.0, 3.0, 2.0]) == 1
     assert orc.argmax([float("nan"), 5.0, 6.0]) == 0
