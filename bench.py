@@ -432,14 +432,18 @@ def pinned_h2d_gbs(ctx, nbytes: int = 256 << 20, reps: int = 8) -> float:
     return nbytes * reps / (ms * 1e-3) / 1e9
 
 
-def config5_bench(rf, syn, tokens: int, prompt_len: int, policy: int, persistent: int = 0) -> dict:
+def config5_bench(rf, syn, tokens: int, prompt_len: int, policy: int, persistent: int = 0,
+                  model_file=None) -> dict:
     """8B shape, Q4_K body + Q6_K output, VRAM budget 4 GiB:
     the layers that do not fit stream from pinned host memory each token
     (layer cache on the device with LRU or next-use eviction, uploads on the
     copy streams overlapped with the previous layers' kernels).  persistent:
     0 keeps the embedding and output resident by the reference's 25% rule,
     3 keeps the embedding table in mapped host memory (a step reads one
-    row), leaving its VRAM to cached layers."""
+    row), leaving its VRAM to cached layers.  model_file: (path, spans) of
+    the block tensors written by synthetic.write_model_file, read on every
+    layer load through the library's pread reader and two 64 MiB pinned
+    staging buffers instead of kept in pinned host memory."""
     import numpy as np
 
     cfg = syn.CONFIG_8B
@@ -451,8 +455,12 @@ def config5_bench(rf, syn, tokens: int, prompt_len: int, policy: int, persistent
     t0 = time.perf_counter()
     # context 8192 (2 GiB of f32 K/V at full length), the cache starting at the
     # prompt's length and growing in 256-position chunks as the reference's does
-    m = syn.build_device_model(ctx, cfg, specs, cfg["context_length"], stream_cache_bytes=budget,
-                               cache_policy=policy, kv_initial=prompt_len, persistent_policy=persistent)
+    if model_file is None:
+        m = syn.build_device_model(ctx, cfg, specs, cfg["context_length"], stream_cache_bytes=budget,
+                                   cache_policy=policy, kv_initial=prompt_len, persistent_policy=persistent)
+    else:
+        m = syn.build_file_model(ctx, cfg, specs, model_file[0], model_file[1], cfg["context_length"], budget,
+                                 cache_policy=policy, kv_initial=prompt_len, persistent_policy=persistent)
     fixed = ctx.vram_used
     layer = syn.weight_bytes([s for s in specs if s.name.startswith("blk.0.")])
     log(f"config 5: built in {time.perf_counter() - t0:.1f} s; fixed VRAM {fixed / 1e9:.2f} GB, "
@@ -470,8 +478,11 @@ def config5_bench(rf, syn, tokens: int, prompt_len: int, policy: int, persistent
     wall = time.perf_counter() - t0
     st = m.residency_stats()
     up = st["uploaded_bytes"] - pre["uploaded_bytes"]
+    where = ("read from the model file on every layer load (pread, two 64 MiB pinned staging buffers)"
+             if model_file is not None else "streamed from pinned host memory")
     out = {"workload": "config 5: 8B shape, Q4_K body + Q6_K output, context 8192, 4 GiB VRAM budget, layers "
-                       "streamed from pinned host memory, KV cache grown in 256-position chunks",
+                       f"{where}, KV cache grown in 256-position chunks",
+           "pinned_host_bytes": m.host_bytes(),
            "cache_policy": ["lru", "next-use"][policy],
            "persistent": {0: "embedding and output resident (25% rule)",
                           3: "embedding in mapped host memory, output resident"}[persistent],
@@ -647,6 +658,26 @@ def main() -> int:
     if args.config5:
         res = [config5_bench(rf, syn, args.config5, args.prompt, policy, persistent)
                for policy, persistent in ((1, 3), (1, 0), (0, 0))]
+        # the same model with its block tensors read from a model file
+        import shutil
+        import tempfile
+
+        specs5 = syn.llama_specs(syn.CONFIG_8B, syn.Q4_K, output_type=syn.Q6_K, seed=5)
+        d = tempfile.mkdtemp(prefix="rf_config5_")
+        try:
+            need = syn.weight_bytes([s_ for s_ in specs5 if s_.name.startswith("blk.")])
+            if shutil.disk_usage(d).free > need + (2 << 30):
+                path = os.path.join(d, "config5_blocks.bin")
+                t0 = time.perf_counter()
+                with rf.Context(0) as wctx:
+                    spans = syn.write_model_file(wctx, specs5, path)
+                log(f"config 5: wrote {need / 1e9:.2f} GB of block tensors to {path} in "
+                    f"{time.perf_counter() - t0:.1f} s")
+                res.append(config5_bench(rf, syn, args.config5, args.prompt, 1, 3, model_file=(path, spans)))
+            else:
+                log("config 5: not enough free disk for the model file; file-read row skipped")
+        finally:
+            shutil.rmtree(d, ignore_errors=True)
         print(json.dumps({"config5": res}), flush=True)
         return 0
     if args.kernels:

@@ -440,6 +440,10 @@ int32_t rf_model_set_cache_policy(rf_model *model, int32_t policy);
 /* out[6]: cache hits, misses (layer uploads), evictions, bytes uploaded,
  * bytes and layers currently cached. */
 int32_t rf_model_residency_stats(rf_model *model, uint64_t *out);
+/* Pinned host memory the model holds: host copies of streamed block tensors,
+ * streamed persistent weights (mapped) and the byte source's two staging
+ * buffers.  No counterpart in the reference. */
+int32_t rf_model_host_bytes(rf_model *model, uint64_t *pinned);
 
 /* Reads `length` bytes at `offset` of a model's byte source (its GGUF file or
  * the virtual concatenation of its shards: DataSource::read_range_into,
@@ -453,6 +457,17 @@ typedef int32_t (*rf_read_fn)(void *user, uint64_t offset, uint64_t length, void
  * memory the reads use; `read` is called on the thread that runs the forward
  * pass, one range at a time. */
 int32_t rf_model_set_reader(rf_model *model, rf_read_fn read, void *user, uint64_t staging_bytes);
+/* A byte source over a model file, for rf_model_set_reader: pass
+ * rf_file_source_read as `read` and the handle as `user`.  Each read of
+ * [offset, offset + length) is split over up to `threads` threads (pieces of
+ * at least 4 MiB), each a pread loop into its part of dst (GgufDataSource's
+ * read_range, core/src/datasource.rs:574-700, is one pread loop; the split is
+ * this build's own, for reads from the page cache at memory speed).  Returns
+ * 0 or the failing piece's errno (EIO for a short read past the file's end). */
+typedef struct rf_file_source rf_file_source;
+int32_t rf_file_source_open(const char *path, uint32_t threads, rf_file_source **out);
+void rf_file_source_close(rf_file_source *source);
+int32_t rf_file_source_read(void *source, uint64_t offset, uint64_t length, void *dst);
 /* Declares block tensor `name` (blk.*) at [offset, offset + nbytes) of the
  * byte source; nothing is read now.  Each load of its layer reads the layer's
  * tensors as ranges merged while the gaps are at most 4 KiB and the span fits

@@ -588,6 +588,26 @@ class ByteSource:
             self.fd = None
 
 
+class FileSource:
+    """Byte source over a model file read by the library itself
+    (rf_file_source_read: each range split over `threads` pread loops), for
+    GpuLlamaModel.set_reader."""
+
+    def __init__(self, path, threads: int = 8):
+        self.lib = _lib.load()
+        h = C.c_void_p()
+        _lib.check(self.lib.rf_file_source_open(os.fsencode(path), threads, C.byref(h)))
+        self.handle = h.value
+        # the library's own rf_read_fn, called with the handle as `user`
+        self.callback = _lib.READ_FN(C.cast(self.lib.rf_file_source_read, C.c_void_p).value)
+        self.user = self.handle
+
+    def close(self) -> None:
+        if self.handle:
+            self.lib.rf_file_source_close(self.handle)
+            self.handle = None
+
+
 class GpuLlamaModel:
     """VRAM-resident dense llama decoder (rf_model_* in the C ABI)."""
 
@@ -625,7 +645,8 @@ class GpuLlamaModel:
         """Streamed layers read their declared tensors from `source`
         (rf_model_set_reader); call after enable_streaming."""
         self._source = source  # keeps the callback alive
-        _lib.check(self.ctx.lib.rf_model_set_reader(self.handle, source.callback, None, int(staging_bytes)))
+        _lib.check(self.ctx.lib.rf_model_set_reader(self.handle, source.callback, getattr(source, "user", None),
+                                                    int(staging_bytes)))
 
     def set_tensor_source(self, name: str, ggml_type: int, ne0: int, ne1: int, offset: int, nbytes: int) -> None:
         """Declare block tensor `name` at [offset, offset + nbytes) of the byte source."""
@@ -659,6 +680,13 @@ class GpuLlamaModel:
         out = (C.c_uint64 * 2)()
         _lib.check(self.ctx.lib.rf_model_read_stats(self.handle, out))
         return {"calls": int(out[0]), "bytes": int(out[1])}
+
+    def host_bytes(self) -> int:
+        """Pinned host bytes the model holds (streamed tensors' host copies,
+        mapped persistent weights, the byte source's staging buffers)."""
+        v = C.c_uint64()
+        _lib.check(self.ctx.lib.rf_model_host_bytes(self.handle, C.byref(v)))
+        return v.value
 
     def residency_stats(self) -> dict:
         out = (C.c_uint64 * 6)()

@@ -125,6 +125,8 @@ SIGNATURES = {
     "rf_model_use_graph": (_i32, [_vp, _i32]),
     "rf_model_kv_growth": (_i32, [_vp, _u64]),
     "rf_model_set_reader": (_i32, [_vp, READ_FN, _vp, _u64]),
+    "rf_file_source_open": (_i32, [C.c_char_p, _u32, C.POINTER(_vp)]),
+    "rf_file_source_close": (None, [_vp]),
     "rf_model_set_tensor_source": (_i32, [_vp, C.c_char_p, _u32, _u64, _u64, _u64, _u64]),
     "rf_model_read_stats": (_i32, [_vp, _vp]),
     "rf_model_set_persistent_policy": (_i32, [_vp, _i32]),
@@ -134,6 +136,7 @@ SIGNATURES = {
     "rf_model_kv_capacity": (_i32, [_vp, _vp]),
     "rf_model_paths": (_i32, [_vp, _u64, _vp, _vp, _vp]),
     "rf_model_kernel_name": (_i32, [_vp, _u32, C.c_char_p, _u64]),
+    "rf_model_host_bytes": (_i32, [_vp, C.POINTER(_u64)]),
     "rf_model_time_kernel": (_i32, [_vp, _u32, _u32, C.POINTER(_f32), C.POINTER(_u64), C.POINTER(_u64)]),
     "rf_tune_matvec_tile_bytes": (_u32, [_u32]),
     "rf_tune_matvec_kernel": (_i32, [_i32]),

@@ -1320,15 +1320,19 @@ int32_t enqueue_forward(rf_model* m, bool embed = true) {
   for (uint32_t li = 0; li < nl; ++li) {
     int32_t rc;
     m->cur_layer = li;
+    // A byte source's reads run on this thread: the next layer is read once
+    // this layer's kernels are queued, so the device computes meanwhile.
+    const bool read_after = m->streaming && m->reader != nullptr;
     if (m->streaming) {
       // this layer resident (hit or load), the next one's upload started so it
       // overlaps this layer's kernels, then the kernels wait for the upload
       if ((rc = acquire_layer(m, li, false))) return abort_pass(m, rc);
-      if (li + 1 < nl && (rc = acquire_layer(m, li + 1, true))) return abort_pass(m, rc);
+      if (!read_after && li + 1 < nl && (rc = acquire_layer(m, li + 1, true))) return abort_pass(m, rc);
       RF_LAUNCH(hipStreamWaitEvent(st, m->res[li].uploaded, 0), "wait for layer upload");
     }
     if ((rc = enqueue_layer(m, li, li + 1 == nl ? m->d_pos : nullptr))) return m->streaming ? abort_pass(m, rc) : rc;
     if (m->streaming && (rc = settle_layer(m, li))) return abort_pass(m, rc);
+    if (read_after && li + 1 < nl && (rc = acquire_layer(m, li + 1, true))) return abort_pass(m, rc);
   }
   if (m->streaming) {
     int32_t rc = release_retired(m);  // release_layer for layers the cache did not take
@@ -2225,6 +2229,23 @@ int32_t rf_model_set_cache_policy(rf_model* m, int32_t policy) {
   if (!m) return set_error(RF_ERR_INVALID, "null model");
   if (policy != 0 && policy != 1) return set_error(RF_ERR_INVALID, "unknown layer cache policy %d", policy);
   m->cache_policy = policy;
+  return RF_OK;
+}
+
+int32_t rf_model_host_bytes(rf_model* m, uint64_t* pinned) {
+  if (!m || !pinned) return set_error(RF_ERR_INVALID, "null argument");
+  uint64_t n = 0;
+  for (Layer& L : m->layers) {
+    DevTensor* t[12];
+    layer_slots(L, t);
+    for (DevTensor* x : t)
+      if (x->host) n += x->nbytes;
+  }
+  for (DevTensor* x : {&m->token_embd, &m->output, &m->output_norm})
+    if (x->host) n += x->nbytes;
+  for (int i = 0; i < 2; ++i)
+    if (m->rstage[i]) n += m->rstage_bytes;
+  *pinned = n;
   return RF_OK;
 }
 

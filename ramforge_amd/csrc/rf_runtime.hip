@@ -9,7 +9,12 @@
 #include <cstdio>
 #include <cstring>
 #include <functional>
+#include <thread>
 #include <vector>
+
+#include <cerrno>
+#include <fcntl.h>
+#include <unistd.h>
 
 namespace rf {
 
@@ -487,6 +492,66 @@ int32_t rf_pinned_free(rf_ctx* ctx, void* p) {
   RF_CHECK_CTX(ctx);
   if (p) RF_HIP(hipHostFree(p), "hipHostFree");
   return RF_OK;
+}
+
+}  // extern "C"
+
+struct rf_file_source {
+  int fd = -1;
+  uint32_t threads = 1;
+};
+
+extern "C" {
+
+int32_t rf_file_source_open(const char* path, uint32_t threads, rf_file_source** out) {
+  if (!path || !out) return set_error(RF_ERR_INVALID, "null argument to rf_file_source_open");
+  *out = nullptr;
+  const int fd = open(path, O_RDONLY | O_CLOEXEC);
+  if (fd < 0) return set_error(RF_ERR_IO, "cannot open '%s': %s", path, strerror(errno));
+  rf_file_source* f = new rf_file_source();
+  f->fd = fd;
+  f->threads = threads < 1 ? 1u : (threads > 64 ? 64u : threads);
+  *out = f;
+  return RF_OK;
+}
+
+void rf_file_source_close(rf_file_source* f) {
+  if (!f) return;
+  if (f->fd >= 0) close(f->fd);
+  delete f;
+}
+
+int32_t rf_file_source_read(void* user, uint64_t offset, uint64_t length, void* dst) {
+  rf_file_source* f = static_cast<rf_file_source*>(user);
+  if (!f || f->fd < 0 || (length && !dst)) return EINVAL;
+  auto piece = [f, dst, offset](uint64_t a, uint64_t b) -> int32_t {  // [a, b) of the request
+    uint8_t* d = static_cast<uint8_t*>(dst);
+    while (a < b) {
+      const uint64_t want = std::min<uint64_t>(b - a, 1ull << 30);
+      const ssize_t n = pread(f->fd, d + a, (size_t)want, (off_t)(offset + a));
+      if (n < 0) {
+        if (errno == EINTR) continue;
+        return errno ? errno : EIO;
+      }
+      if (n == 0) return EIO;  // past the end of the file
+      a += (uint64_t)n;
+    }
+    return 0;
+  };
+  constexpr uint64_t kPiece = 4ull << 20;
+  uint64_t np = std::min<uint64_t>(f->threads, (length + kPiece - 1) / kPiece);
+  if (np <= 1) return piece(0, length);
+  const uint64_t per = (length + np - 1) / np;
+  std::vector<int32_t> rc(np, 0);
+  std::vector<std::thread> th;
+  th.reserve(np - 1);
+  for (uint64_t i = 1; i < np; ++i)
+    th.emplace_back([&, i] { rc[i] = piece(i * per, std::min(length, (i + 1) * per)); });
+  rc[0] = piece(0, std::min(length, per));
+  for (std::thread& t : th) t.join();
+  for (int32_t r : rc)
+    if (r) return r;
+  return 0;
 }
 
 int32_t rf_upload_async(rf_ctx* ctx, void* dst, const void* src, uint64_t bytes, rf_stream_t s) {

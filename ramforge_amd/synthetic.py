@@ -110,3 +110,64 @@ def build_device_model(ctx, cfg: dict, specs: list[TensorSpec], kv_capacity: int
     for s in specs:
         m.synth_tensor(s.name, s.ggml_type, s.ne0, s.ne1, s.seed, s.scale_mul, s.constant)
     return m
+
+
+def write_model_file(ctx, specs: list[TensorSpec], path: str, chunk_bytes: int = 256 << 20) -> dict:
+    """Writes the block tensors (blk.*) of `specs` to a file laid out as a
+    GGUF tensor-data section (each tensor 32-byte aligned, in spec order, so
+    a layer's tensors are contiguous), generating each payload on the device
+    (rf_synth_blocks, the bytes rf_model_synth_tensor installs) and copying
+    it back in chunks.  Returns {name: (offset, nbytes)}."""
+    import numpy as np
+
+    geo = {F32: (1, 4), Q4_0: (32, 18), Q8_0: (32, 34), Q4_K: (256, 144), Q6_K: (256, 210)}
+    spans = {}
+    off = 0
+    buf = ctx.empty((chunk_bytes,), np.uint8, charge="synthetic:file_chunk")
+    try:
+        with open(path, "wb") as f:
+            for s in specs:
+                if not s.name.startswith("blk."):
+                    continue
+                off = (off + 31) // 32 * 32
+                f.seek(off)
+                qk, bs = geo[s.ggml_type]
+                nblk = s.ne0 // qk * s.ne1
+                spans[s.name] = (off, nblk * bs)
+                if s.ggml_type == F32 and s.constant == s.constant:  # a constant fill (norm weights)
+                    f.write(np.full(nblk, s.constant, np.float32).tobytes())
+                else:
+                    per = chunk_bytes // bs
+                    for b0 in range(0, nblk, per):
+                        n = min(per, nblk - b0)
+                        ctx.synth_blocks(s.ggml_type, s.seed, b0, n, s.scale_mul, buf)
+                        f.write(buf.numpy()[: n * bs].tobytes())
+                off += nblk * bs
+    finally:
+        buf.free()
+    return spans
+
+
+def build_file_model(ctx, cfg: dict, specs: list[TensorSpec], path: str, spans: dict, kv_capacity: int,
+                     stream_cache_bytes: int, cache_policy: int = 1, kv_initial: int | None = None,
+                     persistent_policy: int = 0, staging_bytes: int = 64 << 20, threads: int = 8):
+    """A streaming GpuLlamaModel whose block tensors are read from the model
+    file written by write_model_file (a FileSource: the library's own
+    multi-threaded pread reader, `staging_bytes` per pinned staging buffer)
+    each time their layer is loaded; the embedding, output norm and output
+    projection are generated on the device as in build_device_model."""
+    from . import FileSource, GpuLlamaModel
+
+    m = GpuLlamaModel(ctx, cfg, kv_capacity, kv_initial=kv_initial)
+    m.enable_streaming(stream_cache_bytes)
+    m.set_cache_policy(cache_policy)
+    m.set_persistent_policy(persistent_policy)
+    src = FileSource(path, threads)
+    m.set_reader(src, staging_bytes)
+    for s in specs:
+        if s.name in spans:
+            o, nb = spans[s.name]
+            m.set_tensor_source(s.name, s.ggml_type, s.ne0, s.ne1, o, nb)
+        else:
+            m.synth_tensor(s.name, s.ggml_type, s.ne0, s.ne1, s.seed, s.scale_mul, s.constant)
+    return m

@@ -89,3 +89,28 @@ def test_tune_switches_without_a_gpu():
         for m in modes:
             assert fn(m) == m and fn(99) == m, (name, m)
         assert fn(default) == default
+
+
+def test_file_source_reads_ranges_on_threads(tmp_path):
+    """rf_file_source_read (host code, no GPU): ranges split over threads
+    equal the file's bytes at every offset and length, including ranges
+    shorter than one 4 MiB piece; a range past the end of the file fails."""
+    import numpy as np
+
+    import ramforge_amd as rf
+
+    data = np.random.default_rng(44).integers(0, 256, size=(19 << 20) + 123, dtype=np.uint8)
+    path = tmp_path / "blob.bin"
+    path.write_bytes(data.tobytes())
+    src = rf.FileSource(str(path), threads=5)
+    try:
+        for off, n in ((0, data.size), (7, 1), (4095, (9 << 20) + 17), (data.size - 1000, 1000), (12345, 0)):
+            dst = np.zeros(max(n, 1), np.uint8)
+            assert src.callback(src.user, off, n, dst.ctypes.data) == 0, (off, n)
+            assert np.array_equal(dst[:n], data[off:off + n]), (off, n)
+        dst = np.zeros(64, np.uint8)
+        assert src.callback(src.user, data.size - 10, 64, dst.ctypes.data) != 0
+    finally:
+        src.close()
+    with pytest.raises(rf.RamforgeError, match="cannot open"):
+        rf.FileSource(str(tmp_path / "missing.bin"))
