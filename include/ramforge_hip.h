@@ -590,6 +590,15 @@ int32_t rf_tune_packed_inflight(int32_t mode);
  * to steps enqueued or captured afterwards.  Returns the mode in effect
  * (process-wide). */
 int32_t rf_tune_attention_merge(int32_t mode);
+/* Decode-step attention kernel (rf_attention_decode and model decode
+ * steps; batched prefill keeps the two-pass kernel): the one-pass kernel
+ * with an online softmax (each position slot keeps a running maximum,
+ * exp-sum and weighted V sum) for launches with one workgroup per query head
+ * (short contexts; 1, default), for every launch (2), or for none (0: the
+ * two-pass kernel, scores of a chunk in LDS, then V).  Both write the same
+ * chunk records; they differ in rounding only.  Other values only query.
+ * Returns the mode in effect (process-wide). */
+int32_t rf_tune_attention_kernel(int32_t mode);
 /* Weight layout of models created afterwards: 1 = Q8_0 / Q4_0 / Q4_K / Q6_K
  * projection weights are repacked at install into the device-native layout
  * (default; the batched prefill needs it), 0 = kept as GGUF bytes; other

@@ -826,6 +826,14 @@ def tune_attention_merge(mode: int = -1) -> int:
     return _lib.load().rf_tune_attention_merge(mode)
 
 
+def tune_attention_kernel(mode: int = -1) -> int:
+    """Decode-step attention: the one-pass online-softmax kernel for launches
+    per query head (1, default), for every launch (2) or none (0: two-pass,
+    scores in LDS, then V); -1 queries.  Batched prefill keeps the two-pass
+    kernel.  Returns the mode in effect."""
+    return _lib.load().rf_tune_attention_kernel(mode)
+
+
 def tune_packed_weights(mode: int = -1) -> int:
     """1: Q8_0 / Q4_0 / Q4_K / Q6_K projection weights of models are repacked
     into the device-native layout at install (default; the batched prefill

@@ -352,6 +352,211 @@ __global__ __launch_bounds__(64 * W) void attn_split(AttnArgs a) {
   }
 }
 
+// One-pass (online-softmax) form of attn_split for decode steps: every
+// 16-lane slot streams K and V rows of its positions (U per round, K and V in
+// the same lane-to-dims layout) and keeps a running maximum, exp-sum and
+// weighted V sum per query head, rescaled once per round by exp2(m - m');
+// scores are scaled by log2(e) / sqrt(hd) through q, so exp2 gives the
+// reference's exp(score - max) (compute.rs:363-384, 461-547) up to rounding.
+// The W x 4 slots are combined once at the end (lane exchanges, then LDS).
+// There is no score array, no chunk-length limit and one workgroup barrier
+// after the prologue.  Records are written as attn_split writes them (m in
+// natural-log units), so attn_merge and the merging o-projection read either.
+template <int G, int DPL, int W, bool PERQ>
+__global__ __launch_bounds__(64 * W) void attn_flash(AttnArgs a) {
+  static_assert(!PERQ || G == 1, "one query head per workgroup");
+  constexpr int HD = DPL * 16;
+  constexpr uint32_t NTH = 64u * W, NSLOT = 4u * W;
+  // positions per slot and round: K, V (2 U DPL) and q, o (2 G DPL) within
+  // about 128 registers
+  constexpr int U = DPL * (8 + 2 * G) <= 128 ? 4 : 2;
+  constexpr float LOG2E = 1.4426950408889634f, LN2 = 0.6931471805599453f;
+  __shared__ __align__(16) float qs[G][HD];
+  __shared__ __align__(16) float kcur[HD];
+  __shared__ __align__(16) float vcur[HD];
+  __shared__ __align__(16) float po[W][G][HD];
+  __shared__ float pm[W][G], pl[W][G];
+
+  const uint32_t qg = PERQ ? blockIdx.y : blockIdx.y * G;
+  const uint32_t g = PERQ ? blockIdx.y / (a.qh / a.kvh) : blockIdx.y, sp = blockIdx.x;
+  const bool writes_slot = sp == 0 && (!PERQ || qg % (a.qh / a.kvh) == 0);
+  const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+  const uint32_t hist = a.d_pos ? (uint32_t)(*a.d_pos) : a.hist;
+  const uint32_t kvw = a.kvh * HD;
+  const uint32_t total = hist + 1;
+  const uint32_t chunk = att_chunk(total, a.nsplit);
+  const uint32_t p0 = sp * chunk;
+  if (p0 >= total) return;
+  const uint32_t p1 = min(total, p0 + chunk);
+  const uint32_t nmain = min(p1, hist) - p0;  // positions read from the cache
+  const bool has_cur = p1 == total;
+  const uint32_t ns = (total + chunk - 1) / chunk;
+  const float* cs = a.rope ? a.rope + (size_t)hist * HD : nullptr;
+  const uint32_t sl = lane & 15u, slot = wave * 4u + (lane >> 4);
+  const uint32_t d0 = sl * 4u;  // dims 64 (i / 4) + d0 + i % 4 of K and V rows
+  const float* kb = a.k_hist + (size_t)p0 * kvw + g * HD + d0;
+  const float* vb = a.v_hist + (size_t)p0 * kvw + g * HD + d0;
+
+  // Loads first: prologue operands, then the first round of K and V rows.
+  constexpr uint32_t NE = (G + 2) * HD, NP = (NE + NTH - 1) / NTH, HALF = HD / 2;
+  float va[NP], vp[NP], c0[NP], c1[NP];
+#pragma unroll
+  for (uint32_t i = 0; i < NP; ++i) {
+    const uint32_t t = min(tid + i * NTH, NE - 1u), r = t / HD, d = t % HD;
+    const float* src = r < (uint32_t)G ? a.q + (size_t)(qg + r) * HD : (r == (uint32_t)G ? a.k_cur : a.v_cur) + g * HD;
+    const uint32_t ci = d < HALF ? d : d - HALF;
+    va[i] = src[d];
+    vp[i] = src[d < HALF ? d + HALF : d - HALF];
+    c0[i] = cs ? cs[2 * ci] : 1.f;
+    c1[i] = cs ? cs[2 * ci + 1] : 0.f;
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  float kv[U][DPL], vv[U][DPL];
+  auto issue = [&](uint32_t j0) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const uint32_t j = min(j0 + slot + NSLOT * u, nmain - 1u);
+      load_dims(kv[u], kb + (size_t)j * kvw, DPL);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const uint32_t j = min(j0 + slot + NSLOT * u, nmain - 1u);
+      load_dims(vv[u], vb + (size_t)j * kvw, DPL);
+    }
+  };
+  if (nmain > 0) issue(0);
+  __builtin_amdgcn_sched_barrier(0);
+
+  // Rotated q of the G heads, the current k (rotated) and v, and the slot write.
+#pragma unroll
+  for (uint32_t i = 0; i < NP; ++i) {
+    const uint32_t t = tid + i * NTH, r = t / HD, d = t % HD;
+    if (t >= NE) break;
+    const float rot = d < HALF ? va[i] * c0[i] - vp[i] * c1[i] : vp[i] * c1[i] + va[i] * c0[i];
+    if (r < (uint32_t)G) {
+      qs[r][d] = cs ? rot : va[i];
+    } else if (r == (uint32_t)G) {
+      const float kr = cs ? rot : va[i];
+      kcur[d] = kr;
+      if (a.k_store && writes_slot) a.k_store[(size_t)hist * kvw + g * HD + d] = kr;
+    } else {
+      vcur[d] = va[i];
+      if (a.v_store && writes_slot) a.v_store[(size_t)hist * kvw + g * HD + d] = va[i];
+    }
+  }
+  __syncthreads();
+
+  const float qscale = LOG2E / a.denom;
+  float qr[G][DPL];
+#pragma unroll
+  for (int h = 0; h < G; ++h)
+#pragma unroll
+    for (int i = 0; i < DPL; ++i) qr[h][i] = qs[h][64 * (i / 4) + d0 + i % 4] * qscale;
+  float m[G], l[G], o[G][DPL];
+#pragma unroll
+  for (int h = 0; h < G; ++h) {
+    m[h] = -INFINITY;
+    l[h] = 0.f;
+#pragma unroll
+    for (int i = 0; i < DPL; ++i) o[h][i] = 0.f;
+  }
+  // Scores of U positions (invalid ones -inf), then one rescale per head.
+  auto consume = [&](const float (&kk)[U][DPL], const float (&vw)[U][DPL], uint32_t j0, uint32_t nvalid) {
+    float s[U][G];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const bool ok = j0 + slot + NSLOT * u < nvalid;
+#pragma unroll
+      for (int h = 0; h < G; ++h) {
+        float acc = 0.f;
+#pragma unroll
+        for (int i = 0; i < DPL; ++i) acc = fmaf(qr[h][i], kk[u][i], acc);
+        acc = rf_row16_sum(acc);
+        s[u][h] = ok ? acc : -INFINITY;
+      }
+    }
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      float mx = m[h];
+#pragma unroll
+      for (int u = 0; u < U; ++u) mx = fmaxf(mx, s[u][h]);
+      if (mx == -INFINITY) continue;  // nothing valid yet in this slot
+      const float corr = __builtin_amdgcn_exp2f(m[h] - mx);  // exp2(-inf) = 0
+      l[h] *= corr;
+#pragma unroll
+      for (int i = 0; i < DPL; ++i) o[h][i] *= corr;
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const float p = __builtin_amdgcn_exp2f(s[u][h] - mx);
+        l[h] += p;
+#pragma unroll
+        for (int i = 0; i < DPL; ++i) o[h][i] = fmaf(p, vw[u][i], o[h][i]);
+      }
+      m[h] = mx;
+    }
+  };
+  for (uint32_t j0 = 0; j0 < nmain; j0 += NSLOT * U) {
+    if (j0 > 0) issue(j0);
+    consume(kv, vv, j0, nmain);
+  }
+  if (has_cur) {  // the current position: slot 0 with k and v from LDS
+    float kk[U][DPL], vw[U][DPL];
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int i = 0; i < DPL; ++i) {
+        kk[u][i] = kcur[64 * (i / 4) + d0 + i % 4];
+        vw[u][i] = vcur[64 * (i / 4) + d0 + i % 4];
+      }
+    consume(kk, vw, 0, 1);  // only slot 0, u = 0 is valid
+  }
+  // The four slots of the wavefront, then the W wavefronts.
+#pragma unroll
+  for (uint32_t off = 16; off <= 32; off *= 2) {
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      const float mo = __shfl_xor(m[h], off), lo = __shfl_xor(l[h], off);
+      const float mx = fmaxf(m[h], mo);
+      const float fs = mx == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m[h] - mx);
+      const float fo = mx == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mo - mx);
+      l[h] = l[h] * fs + lo * fo;
+#pragma unroll
+      for (int i = 0; i < DPL; ++i) o[h][i] = o[h][i] * fs + __shfl_xor(o[h][i], off) * fo;
+      m[h] = mx;
+    }
+  }
+  if (lane < 16u) {
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+#pragma unroll
+      for (int i = 0; i < DPL; ++i) po[wave][h][64 * (i / 4) + d0 + i % 4] = o[h][i];
+      if (lane == 0) { pm[wave][h] = m[h]; pl[wave][h] = l[h]; }
+    }
+  }
+  __syncthreads();
+  for (uint32_t t = tid; t < (uint32_t)(G * HD); t += NTH) {
+    const uint32_t h = t / HD, d = t % HD;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < W; ++w) M = fmaxf(M, pm[w][h]);
+    float acc = 0.f, lsum = 0.f;
+#pragma unroll
+    for (int w = 0; w < W; ++w) {
+      const float f = pm[w][h] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(pm[w][h] - M);
+      acc = fmaf(po[w][h][d], f, acc);
+      lsum = fmaf(pl[w][h], f, lsum);
+    }
+    const uint32_t qhead = qg + h;
+    if (ns == 1) {
+      a.out[(size_t)qhead * HD + d] = acc / lsum;
+    } else {
+      float* w = a.ws + ((size_t)sp * a.qh + qhead) * att_rec(HD);
+      w[d] = acc;
+      if (d == 0) { w[HD] = M * LN2; w[HD + 1] = lsum; }
+    }
+  }
+}
+
 // Merge the chunk records (o, m, l) of one query head: one wavefront per
 // head, lane l owning dims [l DPW, (l + 1) DPW).  The first 32 records (all
 // of them up to 32 chunks) are requested together with the (m, l) pairs,
@@ -564,8 +769,26 @@ uint64_t attention_ws_floats(uint32_t nsplit, uint32_t qh, uint32_t hd) {
   return (uint64_t)nsplit * qh * att_rec(hd);
 }
 
+// Which decode launches (ntok == 0) take the one-pass kernel
+// (rf_tune_attention_kernel): 1 (default) those per query head, 2 all, 0
+// none; prefill batches take the two-pass kernel.  Timed in the 8B Q8_0
+// decode (graph replay, attention group per layer incl. the merge kernel):
+// positions 32-96 (per query head) 4.47 against 4.89 us, 540 against 536
+// tok/s; about 2048 positions (per KV head, G = 4) 13.8 against 12.1 us;
+// about 8100 positions 19.9 against 19.5 us.  With four query heads per
+// slot the one-pass kernel needs all four scores in every lane (16 row sums
+// per four positions) and 218 registers; the two-pass kernel transposes the
+// four sums in 5 exchanges and owns V dims per lane.
+static int g_att_kernel = 1;
+void set_attention_kernel(int mode) { g_att_kernel = mode; }
+int attention_kernel() { return g_att_kernel; }
+
 template <int G, int DPL, int W, bool PERQ = false>
 static void launch_split_t(const AttnArgs& a, hipStream_t st) {
+  if (a.ntok == 0 && (g_att_kernel == 2 || (g_att_kernel == 1 && PERQ))) {
+    RF_KLAUNCH((attn_flash<G, DPL, W, PERQ>), dim3(a.nsplit, PERQ ? a.qh : a.kvh, 1), dim3(64 * W), 0, st, a);
+    return;
+  }
   RF_KLAUNCH((attn_split<G, DPL, W, PERQ>), dim3(a.nsplit, PERQ ? a.qh : a.kvh, a.ntok ? a.ntok : 1),
                      dim3(64 * W), 0, st, a);
 }

@@ -191,6 +191,10 @@ struct AttnArgs {
   float denom;           // sqrt(hd) as the reference computes it
 };
 hipError_t launch_attention(const AttnArgs& a, hipStream_t st);
+// Decode launches that take the one-pass online-softmax kernel (attn_flash):
+// 1 (default) those per query head, 2 all, 0 none (attn_split, scores in LDS).
+void set_attention_kernel(int mode);
+int attention_kernel();
 // Any-shape kernel; its workspace is [qh][hist + 1] floats.
 hipError_t launch_attention_naive(const AttnArgs& a, hipStream_t st);
 uint32_t attention_splits(uint32_t total_positions, uint32_t kvh);

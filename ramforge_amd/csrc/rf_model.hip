@@ -2260,6 +2260,11 @@ int32_t rf_model_residency_stats(rf_model* m, uint64_t* out) {
   return RF_OK;
 }
 
+int32_t rf_tune_attention_kernel(int32_t mode) {
+  if (mode >= 0 && mode <= 2) set_attention_kernel(mode);
+  return attention_kernel();
+}
+
 int32_t rf_tune_attention_merge(int32_t mode) {
   if (mode == 0 || mode == 1) g_oproj_merge = mode;
   return g_oproj_merge;

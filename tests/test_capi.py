@@ -78,12 +78,14 @@ def test_tune_switches_without_a_gpu():
     """The process-wide tune switches are host state: each returns the mode in
     effect, values outside its range only query, and the defaults are the
     measured choices (merged attention records, in-flight packed launches,
-    packed weights, float x everywhere: the digit planes are opt-in)."""
+    packed weights, float x everywhere: the digit planes are opt-in, the
+    one-pass attention kernel for launches per query head)."""
     from ramforge_amd import _lib
 
     lib = _lib.load()
     for name, default, modes in (("rf_tune_attention_merge", 1, (0, 1)), ("rf_tune_packed_inflight", 1, (0, 1)),
-                                 ("rf_tune_packed_weights", 1, (0, 1)), ("rf_tune_matvec_digits", 0, (0, 1, 2))):
+                                 ("rf_tune_packed_weights", 1, (0, 1)), ("rf_tune_matvec_digits", 0, (0, 1, 2)),
+                                 ("rf_tune_attention_kernel", 1, (0, 1, 2))):
         fn = getattr(lib, name)
         assert fn(-1) == default, name
         for m in modes:

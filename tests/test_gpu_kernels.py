@@ -724,6 +724,23 @@ def test_attention_chunk_tree(ctx, orc, hist, qh, kvh):
         a.free()
 
 
+@pytest.mark.parametrize("mode", [0, 2], ids=["two-pass", "one-pass"])
+@pytest.mark.parametrize("hist,qh,kvh,hd", [(0, 32, 8, 128), (63, 32, 8, 128), (127, 32, 8, 128),
+                                            (1087, 32, 8, 128), (8191, 32, 8, 128), (5000, 8, 1, 128),
+                                            (300, 64, 8, 64), (700, 16, 2, 256), (33, 4, 1, 256)])
+def test_attention_kernel_modes(ctx, orc, mode, hist, qh, kvh, hd):
+    """Both decode attention kernels on every launch regime (mode 2 runs the
+    one-pass online-softmax kernel per KV head too, mode 0 the two-pass
+    kernel per query head too), against the oracle."""
+    rf = _rf()
+    old = rf.tune_attention_kernel(-1)
+    rf.tune_attention_kernel(mode)
+    try:
+        _attention_case(ctx, orc, hist, qh, kvh, hd, 1200 + hist + qh + hd, rope_pos=hist)
+    finally:
+        rf.tune_attention_kernel(old)
+
+
 @pytest.mark.parametrize("ctx_len", [512, 2048, 8192])
 def test_attention_baseline_config(ctx, orc, ctx_len):
     """32 q heads, 8 KV heads, hd 128, RoPE theta 1e4 at
