@@ -797,7 +797,10 @@ def tune_matvec_tile_bytes(nbytes: int = 0) -> int:
 
 
 def tune_matvec_kernel(mode: int = -1) -> int:
-    """1: persistent streaming matvec (default), 0: one-shot tile kernel;
+    """GGUF-layout matvec kernels: 2 (default) plain Q8_0 matvecs of up to
+    4096 inputs read rows into registers and realign the blocks there, the
+    rest as 1; 1
+    persistent streaming kernel with LDS row tiles; 0 one-shot tile kernel;
     -1 queries.  Returns the mode in effect."""
     return _lib.load().rf_tune_matvec_kernel(mode)
 

@@ -551,6 +551,140 @@ static hipError_t launch_stream_t(const MvArgs& a, uint32_t tiles, const MvPlan&
   return hipGetLastError();
 }
 
+// ------------------------------------------------ lane kernel (Q8_0)
+// GGUF rows read straight into registers, realigned there: one row per
+// wavefront at a time, lane l owning blocks l, l + 64, ... of the row.  A
+// 34-byte block at byte 34 b starts 0 (even b) or 2 (odd b) bytes into a
+// dword: the lane loads the 9 dwords covering it with raw buffer loads
+// (dword alignment; offsets past the row return zeros) and takes the codes
+// as dwords 1..8 (odd b) or shifts them down by two bytes with v_alignbyte
+// (even b).  No LDS tile and no barrier in the row loop: x sits in LDS once
+// per workgroup of four wavefronts, about two rows per wavefront.  Signed
+// codes times x, the block scale once per block, as the other kernels
+// (quant.rs:977-1029 up to the order of the sums).  Rows must start on
+// dwords (an even block count per row, a dword-aligned base).
+// Timed against the LDS-tiled streaming kernel (graph replay, weights
+// rotated over >= 1.2 GiB): Q8_0 4096 x 4096 8.9 against 11.0 us; but
+// slower for wider rows (Q8_0 28672 x 8192 67 against 57 us) and for Q4_0
+// (14336 x 4096 21 against 17 us, 18-byte blocks: two loads per 32
+// weights), and a persistent grid of 8-wavefront workgroups with two blocks
+// per lane (always dword aligned) was slower still (12.2 us at 4096 x
+// 4096), so it takes Q8_0 rows of up to 4096 inputs only.
+typedef __amdgpu_buffer_rsrc_t MvRsrc;
+constexpr int MV_RSRC_WORD3 = 0x00020000;
+constexpr uint32_t MVL_WAVES = 4;
+constexpr uint32_t MVL_MAX_IN = 4096;
+
+// BPL blocks per lane and row (ceil(blocks / 64)); NB rows in flight per
+// wavefront (the next row's dwords requested before this row is summed).
+template <int BPL, int NB>
+__global__ __launch_bounds__(64 * MVL_WAVES) void matvec_lanes(const uint8_t* __restrict__ w,
+                                                               const float* __restrict__ x, float* __restrict__ y,
+                                                               uint32_t in_dim, uint32_t rows, uint32_t row_bytes) {
+  constexpr uint32_t BS = 34, NDW = 9;
+  extern __shared__ __align__(16) float xs[];
+  const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const uint32_t nblk = in_dim / 32u;
+  const uint32_t stride = gridDim.x * MVL_WAVES;
+  uint32_t dw[NB][BPL][NDW];
+  auto fetch = [&](uint32_t (&d)[BPL][NDW], uint32_t r) {
+    const bool live = r < rows;  // wave-uniform: past the last row every load returns zeros
+    const MvRsrc rs = __builtin_amdgcn_make_buffer_rsrc((void*)(w + (size_t)(live ? r : 0u) * row_bytes), 0,
+                                                        live ? (int32_t)row_bytes : 0, MV_RSRC_WORD3);
+#pragma unroll
+    for (int k = 0; k < BPL; ++k) {
+      const uint32_t off = (BS * (lane + 64u * k)) & ~3u;
+      const auto v0 = __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0);
+      const auto v1 = __builtin_amdgcn_raw_buffer_load_b128(rs, off + 16u, 0, 0);
+      d[k][0] = v0[0]; d[k][1] = v0[1]; d[k][2] = v0[2]; d[k][3] = v0[3];
+      d[k][4] = v1[0]; d[k][5] = v1[1]; d[k][6] = v1[2]; d[k][7] = v1[3];
+      d[k][8] = __builtin_amdgcn_raw_buffer_load_b32(rs, off + 32u, 0, 0);
+    }
+  };
+  uint32_t r = blockIdx.x * MVL_WAVES + wave;
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) fetch(dw[nb], r + (uint32_t)nb * stride);
+  // x into LDS behind the first rows' loads
+  for (uint32_t i = tid; i < in_dim / 4u; i += 64u * MVL_WAVES)
+    reinterpret_cast<float4*>(xs)[i] = reinterpret_cast<const float4*>(x)[i];
+  __syncthreads();
+  auto finish = [&](const uint32_t (&d)[BPL][NDW], uint32_t rr) {
+    float acc = 0.f;
+#pragma unroll
+    for (int k = 0; k < BPL; ++k) {
+      const uint32_t b = lane + 64u * k;
+      if (b < nblk) {
+        const bool odd = (b & 1u) != 0u;
+        const uint32_t h = odd ? d[k][0] >> 16 : d[k][0] & 0xFFFFu;
+        const float* xb = xs + 32u * b;
+        float s = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const uint32_t c = odd ? d[k][i + 1] : __builtin_amdgcn_alignbyte(d[k][i + 1], d[k][i], 2);
+          const float4 xv = *reinterpret_cast<const float4*>(xb + 4 * i);
+          s = fmaf(rf_sb(c, 0), xv.x, s);
+          s = fmaf(rf_sb(c, 1), xv.y, s);
+          s = fmaf(rf_sb(c, 2), xv.z, s);
+          s = fmaf(rf_sb(c, 3), xv.w, s);
+        }
+        acc += rf_half_to_float_fast(h) * s;
+      }
+    }
+    acc = rf_wave_sum(acc);
+    if (lane == 0 && rr < rows) y[rr] = acc;
+  };
+  for (; r < rows; r += (uint32_t)NB * stride) {
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      finish(dw[nb], r + (uint32_t)nb * stride);
+      fetch(dw[nb], r + (uint32_t)(nb + NB) * stride);
+    }
+  }
+}
+
+// Whether the lane kernel takes this launch: Q8_0 rows of an even block
+// count (dword-aligned rows) and at most MVL_MAX_IN inputs, a dword-aligned
+// base and 16-byte aligned x.
+static bool lanes_ok(uint32_t t, uint64_t in_dim, const void* w, const float* x) {
+  if (t != T_Q8_0 || in_dim == 0 || in_dim % 64 != 0 || in_dim > MVL_MAX_IN) return false;
+  return (reinterpret_cast<uintptr_t>(w) & 3u) == 0 && aligned16(x);
+}
+
+static int g_lanes_enabled = 1;
+void set_matvec_lanes(bool on) { g_lanes_enabled = on ? 1 : 0; }
+bool matvec_lanes_on() { return g_lanes_enabled != 0; }
+
+template <int BPL>
+static hipError_t launch_lanes_b(const MvSegDesc& s, const float* x, uint64_t in_dim, hipStream_t st) {
+  constexpr int NB = 2;
+  static std::mutex mu;
+  static uint32_t occ = 0;
+  const uint32_t lds = (uint32_t)in_dim * 4u;
+  {
+    std::lock_guard<std::mutex> lock(mu);
+    if (occ == 0) {
+      if (setup_outside_capture(st) != hipSuccess) return hipErrorStreamCaptureUnsupported;
+      int n = 0;
+      if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, matvec_lanes<BPL, NB>, 64 * MVL_WAVES,
+                                                       (size_t)MVL_MAX_IN * 4u) != hipSuccess || n < 1)
+        n = 1;
+      occ = (uint32_t)n;
+    }
+  }
+  const uint64_t rows = s.rows;
+  const uint64_t want = (rows + MVL_WAVES * NB - 1) / (MVL_WAVES * NB);  // about NB rows per wavefront
+  const uint64_t cap = (uint64_t)cu_count() * occ;
+  const uint32_t grid = (uint32_t)std::max<uint64_t>(1, std::min(want, cap));
+  const uint32_t row_bytes = (uint32_t)(in_dim / 32u * 34u);
+  RF_KLAUNCH((matvec_lanes<BPL, NB>), dim3(grid), dim3(64 * MVL_WAVES), lds, st, static_cast<const uint8_t*>(s.w),
+             x, s.y, (uint32_t)in_dim, (uint32_t)rows, row_bytes);
+  return hipGetLastError();
+}
+
+static hipError_t launch_lanes(const MvSegDesc& s, const float* x, uint64_t in_dim, hipStream_t st) {
+  return in_dim <= 2048 ? launch_lanes_b<1>(s, x, in_dim, st) : launch_lanes_b<2>(s, x, in_dim, st);
+}
+
 template <int EPI>
 static hipError_t launch_tiled_e(uint32_t t, const MvArgs& a, uint32_t grid, const MvPlan& p, hipStream_t st,
                                  bool stream) {
@@ -591,6 +725,9 @@ hipError_t launch_matvec_segments(uint32_t t, const MvSegDesc* segs, int nseg, c
     }
     return hipSuccess;
   }
+  if (g_lanes_enabled && epi == EPI_STORE && norm_w == nullptr && nseg == 1 && segs[0].rows > 0 &&
+      segs[0].rows <= 0xFFFFFFFFull && lanes_ok(t, in_dim, segs[0].w, x))
+    return launch_lanes(segs[0], x, in_dim, st);
   bool stream = p.stream && g_stream_enabled;
   for (int i = 0; i < nseg && stream; ++i)
     stream = aligned16(segs[i].w) && (!dual || aligned16(segs[i].w_up));

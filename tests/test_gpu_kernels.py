@@ -140,13 +140,33 @@ def _check_matvec(ctx, orc, t, out_dim, in_dim, seed, row_start=0, row_count=Non
     return err
 
 
-@pytest.fixture(params=[1, 0], ids=["stream", "oneshot"])
+@pytest.fixture(params=[2, 1, 0], ids=["lanes", "stream", "oneshot"])
 def kernel_mode(request):
     rf = _rf()
     old = rf.tune_matvec_kernel(-1)
     rf.tune_matvec_kernel(request.param)
     yield request.param
     rf.tune_matvec_kernel(old)
+
+
+@pytest.mark.parametrize("out_dim,in_dim", [(1, 64), (7, 128), (513, 4096), (130, 2048), (33, 4096), (4096, 4096)])
+def test_matvec_lane_kernel_shapes(ctx, orc, out_dim, in_dim):
+    """The register-realigning lane kernel (plain Q8_0 rf_matvec of up to
+    4096 inputs) at one and two blocks per lane, row counts that leave
+    wavefronts idle, and the even / odd block alignments of every lane."""
+    rf = _rf()
+    assert rf.tune_matvec_kernel(-1) == 2
+    _check_matvec(ctx, orc, Q8_0, out_dim, in_dim, 1500 + out_dim + in_dim)
+
+
+@pytest.mark.parametrize("t", [Q8_0, Q4_0])
+def test_matvec_lane_kernel_offsets(ctx, orc, t):
+    """Row ranges (the base moves by whole rows, still dword aligned), a
+    weight base 4 bytes past an aligned allocation (Q8_0: lane kernel) and 2
+    bytes past (not dword aligned: the other kernels); Q4_0 takes the other
+    kernels throughout."""
+    for i, (rs, rc, w_off) in enumerate(((37, 100, 0), (0, None, 4), (5, 11, 2), (299, 1, 4))):
+        _check_matvec(ctx, orc, t, 300, 4096, 1600 + i, row_start=rs, row_count=rc, w_off=w_off)
 
 
 @pytest.mark.parametrize("t", QUANT_TYPES + [F32])
