@@ -603,6 +603,12 @@ int32_t rf_tune_attention_merge(int32_t mode);
  * chunk records; they differ in rounding only.  Other values only query.
  * Returns the mode in effect (process-wide). */
 int32_t rf_tune_attention_kernel(int32_t mode);
+/* Longest context (64, 128 or 256 positions) that decode attention serves
+ * with one chunk per query head (no chunk records to merge, so the
+ * o-projection reads x directly); 8 wavefronts per workgroup above 64.
+ * Other values only query.  Applies to steps enqueued or captured
+ * afterwards.  Returns the value in effect (process-wide). */
+int32_t rf_tune_attention_single(int32_t positions);
 /* Weight layout of models created afterwards: 1 = Q8_0 / Q4_0 / Q4_K / Q6_K
  * projection weights are repacked at install into the device-native layout
  * (default; the batched prefill needs it), 0 = kept as GGUF bytes; other

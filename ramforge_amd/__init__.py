@@ -837,6 +837,13 @@ def tune_attention_kernel(mode: int = -1) -> int:
     return _lib.load().rf_tune_attention_kernel(mode)
 
 
+def tune_attention_single(positions: int = -1) -> int:
+    """Longest context (64, 128 or 256) decode attention serves with one
+    chunk per query head and no merge; -1 queries.  Returns the value in
+    effect."""
+    return _lib.load().rf_tune_attention_single(positions)
+
+
 def tune_packed_weights(mode: int = -1) -> int:
     """1: Q8_0 / Q4_0 / Q4_K / Q6_K projection weights of models are repacked
     into the device-native layout at install (default; the batched prefill

@@ -746,11 +746,20 @@ static uint32_t regime_sq(uint32_t qh) {
 static uint32_t regime_skv(uint64_t cap, uint32_t kvh) {
   return attention_splits((uint32_t)(cap < 0xFFFFFFFFull ? cap : 0xFFFFFFFFull), kvh);
 }
+// Regime 0's longest context (one chunk per query head, no merge): 64, or
+// rf_tune_attention_single's 128 / 256 (8 wavefronts above 64).  Timed in
+// the 8B decode at positions 40-168 (graph replay, one-pass kernel): 64
+// gives 536 tok/s, 128 529, 256 520 (two passes of the split kernel with
+// the merging o-projection beat one longer chunk there).
+static uint32_t g_single_max = ATT_MIN_CHUNK;
+void set_attention_single(uint32_t n) { g_single_max = n; }
+uint32_t attention_single() { return g_single_max; }
+
 AttnShape attention_regime_shape(int r, uint32_t qh, uint32_t kvh, uint64_t cap) {
   const uint32_t sq = regime_sq(qh);
   const uint32_t skv = regime_skv(cap, kvh);
   switch (r) {
-    case 0: return AttnShape{1, 1, 4};
+    case 0: return AttnShape{1, 1, g_single_max > ATT_MIN_CHUNK ? 8u : 4u};
     case 1: return AttnShape{1, sq, 4};
     case 2: return AttnShape{1, sq, 8};
     case 3: return AttnShape{0, skv, 4};
@@ -759,7 +768,7 @@ AttnShape attention_regime_shape(int r, uint32_t qh, uint32_t kvh, uint64_t cap)
 }
 int attention_regime(uint64_t total, uint32_t qh, uint32_t kvh, uint64_t cap) {
   const uint64_t sq = regime_sq(qh);
-  if (total <= ATT_MIN_CHUNK) return 0;
+  if (total <= g_single_max) return 0;
   if (total <= ATT_MIN_CHUNK * sq) return 1;
   if (total <= 2 * ATT_MIN_CHUNK * sq) return 2;
   return total <= ATT_MIN_CHUNK * (uint64_t)regime_skv(cap, kvh) ? 3 : 4;

@@ -225,6 +225,8 @@ struct AttnShape {
 };
 constexpr int ATT_REGIMES = 5;
 int attention_regime(uint64_t total, uint32_t qh, uint32_t kvh, uint64_t cap);
+void set_attention_single(uint32_t n);
+uint32_t attention_single();
 AttnShape attention_regime_shape(int regime, uint32_t qh, uint32_t kvh, uint64_t cap);
 uint64_t attention_ws_floats(uint32_t nsplit, uint32_t qh, uint32_t hd);
 // The split kernel handles this shape for up to `total_positions` positions.

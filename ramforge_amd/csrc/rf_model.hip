@@ -2260,6 +2260,11 @@ int32_t rf_model_residency_stats(rf_model* m, uint64_t* out) {
   return RF_OK;
 }
 
+int32_t rf_tune_attention_single(int32_t positions) {
+  if (positions == 64 || positions == 128 || positions == 256) set_attention_single((uint32_t)positions);
+  return (int32_t)attention_single();
+}
+
 int32_t rf_tune_attention_kernel(int32_t mode) {
   if (mode >= 0 && mode <= 2) set_attention_kernel(mode);
   return attention_kernel();
