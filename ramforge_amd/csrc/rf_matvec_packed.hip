@@ -156,7 +156,10 @@ template <> struct PkFmt<T_Q4_0> {
   __device__ static uint32_t unit_elem(uint32_t b, uint32_t h) { return 2u * b + 16u * h; }
   // The signed codes nibble - 8 as int8 bytes 16 (nibble - 8): products with
   // x are exact up to their own rounding (no -8 sum(x) correction to cancel
-  // against), and the factor 16 comes off exactly in finish.
+  // against), and the factor 16 comes off exactly in finish.  (Converting
+  // each nibble with v_cvt_off_f32_i4 instead, (nibble ^ 8) / 16 with the
+  // byte picked by SDWA, saves two instructions per word but timed the same:
+  // 14336 x 4096 9.52 against 9.47 us, 4096 x 14336 10.60 against 10.56.)
   __device__ static void word(const Lane&, uint32_t q, const Meta&, int, const float4& xv, const float4& xw,
                               float& s0, float& s1) {
     const uint32_t lo = rf_opaque(rf_top_signed(q, 4)), hi = rf_opaque(rf_top_signed(q >> 4, 4));
