@@ -1453,8 +1453,14 @@ int32_t ensure_prefill_ws(rf_model* m) {
   const uint64_t sizes[] = {T * d, T * d, T * qd, T * kvd, T * kvd, T * qd, T * qd, T * f, T * f, part, att};
   uint64_t total = 0;
   for (uint64_t n : sizes) total += (n + 63) / 64 * 64;
+  const uint64_t bytes = total * 4 + T * 4;
+  int32_t rc = RF_OK;
+  // a streaming model evicts cached layers to make room, as a KV growth does
+  // (ensure_layer_cache_headroom, streaming_model.rs:555-572); when that is
+  // not enough, the charge below reports the budget
+  if (m->streaming && (rc = make_headroom(m, bytes)) && rc != RF_ERR_BUDGET) return rc;
   void* p = nullptr;
-  int32_t rc = charge_alloc(m, "tmp:prefill", total * 4 + T * 4, &p);
+  rc = charge_alloc(m, "tmp:prefill", bytes, &p);
   if (rc) return rc;
   float* base = static_cast<float*>(p);
   float** dst[] = {&m->p_h,  &m->p_xn,  &m->p_q,  &m->p_k,    &m->p_v,  &m->p_qr,

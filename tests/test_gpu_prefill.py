@@ -245,3 +245,53 @@ def test_prefill_streaming_model(ctx, orc):
         assert sm.generate(prompt, 10) == ref
     finally:
         sm.close()
+
+
+def test_prefill_evicts_cached_layers_for_its_workspace():
+    """A streaming model whose layer cache has filled the budget makes room
+    for the batched prefill's workspace by evicting cached layers (as a KV
+    growth does, ensure_layer_cache_headroom, streaming_model.rs:555-572)
+    instead of failing, and gives the tokens of the same model with room to
+    spare."""
+    from test_gpu_model import STREAM_CFG, STREAM_TYPES
+
+    rf = _rf()
+    cfg = dict(STREAM_CFG, context_length=256)
+    T = _tiny_tensors(np.random.default_rng(3800), cfg, STREAM_TYPES)
+    prompt = [int(v) for v in np.random.default_rng(3801).integers(0, cfg["vocab_size"], 70)]
+
+    def model(c):
+        m = rf.GpuLlamaModel(c, cfg, 128)
+        m.enable_streaming(1 << 30)
+        for name, (t, ne0, ne1, arr) in T.items():
+            m.set_tensor(name, t, ne0, ne1, arr)
+        return m
+
+    pctx = rf.Context(0, 0)
+    pm = model(pctx)
+    pm.generate([1, 2, 3], 4)  # token by token: every layer cached, no prefill workspace
+    cached = pctx.vram_used
+    assert pm.paths()["batched_prefill"]
+    pm.reset()
+    pm.prefill(prompt)
+    ws = pctx.vram_peak - cached
+    pm.reset()
+    pm.set_prefill(True)
+    ref = pm.generate(prompt, 12)
+    pm.close()
+    pctx.close()
+    assert ws > 0
+    budget = cached + ws // 2  # the cached layers fit, the workspace beside them does not
+    sctx = rf.Context(0, budget)
+    m = model(sctx)
+    try:
+        m.generate([1, 2, 3], 4)
+        before = m.residency_stats()["evictions"]
+        m.reset()
+        m.set_prefill(True)
+        assert m.generate(prompt, 12) == ref
+        assert m.residency_stats()["evictions"] > before
+        assert sctx.vram_peak <= budget
+    finally:
+        m.close()
+        sctx.close()
