@@ -609,6 +609,14 @@ int32_t rf_tune_attention_kernel(int32_t mode);
  * Other values only query.  Applies to steps enqueued or captured
  * afterwards.  Returns the value in effect (process-wide). */
 int32_t rf_tune_attention_single(int32_t positions);
+/* Batched-prefill attention: the matrix-core kernel (16-token tiles per KV
+ * head, each K / V row read once per tile; G = 1, 2, 4 or 8 query heads per
+ * KV head, head_dim 64 or 128) for chunks whose last token sees more than
+ * 1024 positions (1, default), for every chunk (2), or never (0: the decode
+ * split kernel with a token dimension, each K / V row read once per token).
+ * They differ in rounding only.  Other values only query.  Returns the mode
+ * in effect (process-wide). */
+int32_t rf_tune_prefill_attention(int32_t mode);
 /* Weight layout of models created afterwards: 1 = Q8_0 / Q4_0 / Q4_K / Q6_K
  * projection weights are repacked at install into the device-native layout
  * (default; the batched prefill needs it), 0 = kept as GGUF bytes; other

@@ -844,6 +844,15 @@ def tune_attention_single(positions: int = -1) -> int:
     return _lib.load().rf_tune_attention_single(positions)
 
 
+def tune_prefill_attention(mode: int = -1) -> int:
+    """Batched-prefill attention on the matrix-core kernel (16-token tiles,
+    each K / V row read once per tile) past 1024 positions (1, default), for
+    every chunk (2), or never (0: the decode split kernel with a token
+    dimension); -1 queries.  They differ in rounding only.  Returns the mode
+    in effect."""
+    return _lib.load().rf_tune_prefill_attention(mode)
+
+
 def tune_packed_weights(mode: int = -1) -> int:
     """1: Q8_0 / Q4_0 / Q4_K / Q6_K projection weights of models are repacked
     into the device-native layout at install (default; the batched prefill

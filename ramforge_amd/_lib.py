@@ -145,6 +145,7 @@ SIGNATURES = {
     "rf_tune_attention_merge": (_i32, [_i32]),
     "rf_tune_attention_kernel": (_i32, [_i32]),
     "rf_tune_attention_single": (_i32, [_i32]),
+    "rf_tune_prefill_attention": (_i32, [_i32]),
     "rf_tune_packed_weights": (_i32, [_i32]),
     "rf_model_enable_streaming": (_i32, [_vp, _u64]),
     "rf_model_residency_stats": (_i32, [_vp, C.POINTER(_u64)]),

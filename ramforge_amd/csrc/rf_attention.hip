@@ -109,6 +109,39 @@ __device__ __forceinline__ void load_dims(float* dst, const float* src, int n) {
   }
 }
 
+// Raw buffer loads over one chunk's rows of one KV head: offsets past the
+// region read as zeros, so the loads of a round's positions past the chunk
+// need no clamping (and fetch nothing).
+typedef __amdgpu_buffer_rsrc_t AttRsrc;
+constexpr int ATT_RSRC_WORD3 = 0x00020000;  // raw buffer, 32-bit data
+constexpr int ATT_AUX_NT = 2;               // streaming loads
+__device__ __forceinline__ AttRsrc att_rsrc(const float* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), 0, (int32_t)bytes, ATT_RSRC_WORD3);
+}
+// n dims of a K row for one lane (four consecutive floats from every 64) at
+// byte offset off of the region
+__device__ __forceinline__ void load_dims_buf(float* dst, AttRsrc r, uint32_t off, int n) {
+#pragma unroll
+  for (int i = 0; i < n / 4; ++i) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, off + 256u * i, 0, ATT_AUX_NT);
+    dst[4 * i] = __uint_as_float(v[0]); dst[4 * i + 1] = __uint_as_float(v[1]);
+    dst[4 * i + 2] = __uint_as_float(v[2]); dst[4 * i + 3] = __uint_as_float(v[3]);
+  }
+}
+template <int N>
+__device__ __forceinline__ void load_few_buf(float* dst, AttRsrc r, uint32_t off) {
+  if constexpr (N == 1) {
+    dst[0] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, ATT_AUX_NT));
+  } else if constexpr (N == 2) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, ATT_AUX_NT);
+    dst[0] = __uint_as_float(v[0]); dst[1] = __uint_as_float(v[1]);
+  } else {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, ATT_AUX_NT);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dst[i] = __uint_as_float(v[i]);
+  }
+}
+
 // W wavefronts per workgroup: one round of loads covers 16 W positions
 // (4 W position slots of 16 lanes, U positions each in pass 1; 16 rows per
 // wavefront in pass 2), so a chunk of up to 16 W positions is one memory round
@@ -162,12 +195,15 @@ __global__ __launch_bounds__(64 * W) void attn_split(AttnArgs a) {
   // Lane sl of a position holds dims kdim(i) = 64 (i / 4) + 4 sl + i % 4, so
   // each 16-byte load of the 16 lanes covers 256 contiguous bytes of the row.
   const uint32_t d0 = sl * 4u;
-  const float* kb = a.k_hist + (size_t)p0 * kvw + g * HD + d0;
+  // K and V rows p0 .. p0 + nmain - 1 of KV head g: a region ending with the
+  // last row's head segment; rows past it (a round's tail) read as zeros
+  const uint32_t rbytes = nmain ? ((nmain - 1u) * kvw + HD) * 4u : 0u;
+  const AttRsrc kr = att_rsrc(a.k_hist + (size_t)p0 * kvw + g * HD, rbytes);
+  const AttRsrc vr = att_rsrc(a.v_hist + (size_t)p0 * kvw + g * HD, rbytes);
   // Pass 2 maps lanes to dims instead: lane l owns dims [l*DPW, (l+1)*DPW) of
   // every V row and wavefront w the rows w*16 .. w*16+15 of each 64-row batch,
   // so the weighted V sum needs no cross-lane reduction.
   constexpr int DPW = HD / 64;
-  const float* vb = a.v_hist + (size_t)p0 * kvw + g * HD + lane * DPW;
 
   // Loads first: the prologue's operands (q of the G heads, the current k
   // and v, the cos/sin row), then the first batch of K rows, then of V rows,
@@ -190,19 +226,11 @@ __global__ __launch_bounds__(64 * W) void attn_split(AttnArgs a) {
   }
   __builtin_amdgcn_sched_barrier(0);
   float kv[U][DPL], vv[RV][DPW];
-  if (nmain > 0) {
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const uint32_t j = min(slot + NSLOT * u, nmain - 1u);
-      load_dims(kv[u], kb + (size_t)j * kvw, DPL);
-    }
-    __builtin_amdgcn_sched_barrier(0);
+  for (int u = 0; u < U; ++u) load_dims_buf(kv[u], kr, ((slot + NSLOT * u) * kvw + d0) * 4u, DPL);
+  __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int k = 0; k < (int)RV; ++k) {
-      const uint32_t j = min(wave * RV + k, nmain - 1u);
-      load_few<DPW>(vv[k], vb + (size_t)j * kvw);
-    }
-  }
+  for (int k = 0; k < (int)RV; ++k) load_few_buf<DPW>(vv[k], vr, ((wave * RV + k) * kvw + lane * DPW) * 4u);
   __builtin_amdgcn_sched_barrier(0);
 
   // Rotated q of the G heads, the current k (rotated) and v, and the slot write.
@@ -235,10 +263,7 @@ __global__ __launch_bounds__(64 * W) void attn_split(AttnArgs a) {
   for (uint32_t j0 = 0; j0 < nmain; j0 += NSLOT * U) {
     if (j0 > 0) {
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const uint32_t j = min(j0 + slot + NSLOT * u, nmain - 1u);
-        load_dims(kv[u], kb + (size_t)j * kvw, DPL);
-      }
+      for (int u = 0; u < U; ++u) load_dims_buf(kv[u], kr, ((j0 + slot + NSLOT * u) * kvw + d0) * 4u, DPL);
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -271,7 +296,10 @@ __global__ __launch_bounds__(64 * W) void attn_split(AttnArgs a) {
   }
   __syncthreads();
 
-  // Chunk max and exp-sum per head (one wavefront per head).
+  // Chunk max and exp-sum per head (one wavefront per head).  The weights
+  // of the last round's positions past the chunk are zeroed: pass 2 adds
+  // their (zero) V rows without a mask.
+  const uint32_t rend = (npos + RV * W - 1) / (RV * W) * (RV * W);
   for (uint32_t h = wave; h < (uint32_t)G; h += W) {
     float m = -INFINITY;
     for (uint32_t j = lane; j < npos; j += 64u) m = fmaxf(m, sc[h][j]);
@@ -282,6 +310,7 @@ __global__ __launch_bounds__(64 * W) void attn_split(AttnArgs a) {
       sc[h][j] = e;
       l += e;
     }
+    for (uint32_t j = npos + lane; j < rend; j += 64u) sc[h][j] = 0.f;
     l = rf_wave_sum(l);
     if (lane == 0) { mh[h] = m; lh[h] = l; }
   }
@@ -293,13 +322,13 @@ __global__ __launch_bounds__(64 * W) void attn_split(AttnArgs a) {
   for (int h = 0; h < G; ++h)
 #pragma unroll
     for (int i = 0; i < DPW; ++i) o[h][i] = 0.f;
+  // Rows past the chunk hold zeros and zero weights (the current position's
+  // row, read from vcur below, among them): adding them changes no bit, as o
+  // is never -0.
   for (uint32_t j0 = 0; j0 < nmain; j0 += RV * W) {
     if (j0 > 0) {
 #pragma unroll
-      for (int k = 0; k < (int)RV; ++k) {
-        const uint32_t j = min(j0 + wave * RV + k, nmain - 1u);
-        load_few<DPW>(vv[k], vb + (size_t)j * kvw);
-      }
+      for (int k = 0; k < (int)RV; ++k) load_few_buf<DPW>(vv[k], vr, ((j0 + wave * RV + k) * kvw + lane * DPW) * 4u);
     }
     // weights of this wavefront's rows, four at a time with 16-byte LDS reads
     // (j0 + RV w is a multiple of 16, and j0 + RV (w + 1) <= ATT_MAX_CHUNK
@@ -313,13 +342,11 @@ __global__ __launch_bounds__(64 * W) void attn_split(AttnArgs a) {
         e[h][0] = w4.x; e[h][1] = w4.y; e[h][2] = w4.z; e[h][3] = w4.w;
       }
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const bool use = j0 + wave * RV + 4u * q4 + k < nmain;
+      for (int k = 0; k < 4; ++k)
 #pragma unroll
         for (int h = 0; h < G; ++h)
 #pragma unroll
-          for (int i = 0; i < DPW; ++i) o[h][i] = use ? fmaf(e[h][k], vv[4 * q4 + k][i], o[h][i]) : o[h][i];
-      }
+          for (int i = 0; i < DPW; ++i) o[h][i] = fmaf(e[h][k], vv[4 * q4 + k][i], o[h][i]);
     }
   }
   if (has_cur && wave == 0) {
@@ -627,6 +654,179 @@ __global__ __launch_bounds__(64) void attn_merge(AttnArgs a) {
 }
 
 
+// Batched-prefill attention on the matrix cores (FlashAttention-style): a
+// workgroup owns 16 consecutive prompt tokens, the G query heads of one KV
+// head (one wavefront per head) and one position split, and reads each K / V
+// row of its positions once for all 16 G query rows (the decode kernel with a
+// token dimension reads them once per token).  Per tile of 16 positions:
+//   * S^T = K Q^T on v_mfma_f32_16x16x4f32 (f32 products, f32 sums): lane l
+//     supplies K[position l % 16][dim] and q[token l % 16][dim] for the dims of
+//     its group l / 16 (HD / 4 consecutive dims each; the dims are summed in
+//     two interleaved chains), so the result lane holds the scores of token
+//     l % 16 at positions 4 (l / 16) + v, v = 0..3;
+//   * online softmax per token (running maximum m, exp-sum l, output rescaled
+//     by exp(m - m')), each token's maximum reduced over its 4 lanes;
+//   * O^T += V^T P^T, four MFMAs per 16 dims: MFMA t takes positions
+//     4 k + t (k = l / 16), the order in which the lane already holds P, so
+//     the scores never move between lanes; V is staged transposed in LDS.
+// K and V tiles are staged through LDS (double-buffered, one barrier per
+// tile); rows past the split read as zeros through a bounded buffer resource.
+// Token z (position hist + z) attends positions 0 .. hist + z in the split's
+// range [sp c, (sp + 1) c) with c = att_chunk(hist + z + 1, nsplit), the
+// chunking attn_merge reads, and writes the same chunk records (m in
+// natural-log units) or, when its positions fit one chunk, its output.
+// Scores are dot / denom (division) and exp is expf, as in attn_split; only
+// the order of the sums differs.
+constexpr uint32_t APF_TOK = 16;  // tokens per workgroup = positions per tile
+template <int G, int HD>
+__global__ __launch_bounds__(64 * G) void attn_prefill(AttnArgs a) {
+  constexpr uint32_t KS = HD / 4;              // dims per lane group (k steps of S)
+  constexpr uint32_t DT = HD / 16;             // 16-dim tiles of O^T
+  constexpr uint32_t KP = HD + 4;              // LDS row stride of the K tile (floats)
+  constexpr uint32_t VP = APF_TOK + 4;         // LDS row stride of the V^T tile
+  constexpr uint32_t NTH = 64u * G;
+  constexpr uint32_t NCH = APF_TOK * HD / 4;   // 16-byte chunks of one K (or V) tile
+  constexpr uint32_t CPT = (NCH + NTH - 1) / NTH;
+  __shared__ __align__(16) float kt[2][APF_TOK * KP];
+  __shared__ __align__(16) float vt[2][HD * VP];
+  const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+  const uint32_t r = lane & 15u, gq = lane >> 4;
+  const uint32_t sp = blockIdx.x, g = blockIdx.y, z0 = blockIdx.z * APF_TOK;
+  const uint32_t qhead = g * G + wave, kvw = a.kvh * HD;
+  const uint32_t zl = min(a.ntok, z0 + APF_TOK) - 1u;  // last token of the tile
+  const uint32_t z = z0 + r;
+  const bool zok = z < a.ntok;
+  // this token's range in split sp, and the union over the tile's tokens
+  // (chunks never shrink with the token: first start .. last end)
+  const uint32_t tot = a.hist + (zok ? z : zl) + 1u, ch = att_chunk(tot, a.nsplit);
+  const uint32_t r0 = sp * ch, r1 = min(tot, r0 + ch);
+  const uint32_t totl = a.hist + zl + 1u, chl = att_chunk(totl, a.nsplit);
+  const uint32_t lo = sp * att_chunk(a.hist + z0 + 1u, a.nsplit), hi = min(totl, sp * chl + chl);
+  if (lo >= hi) return;  // uniform: no token of the tile has positions in this split
+  // K / V rows 0 .. hi - 1 of KV head g; rows past hi read as zeros
+  const uint32_t rb = ((hi - 1u) * kvw + HD) * 4u;
+  const AttRsrc kr = att_rsrc(a.k_hist + g * HD, rb), vr = att_rsrc(a.v_hist + g * HD, rb);
+
+  // q of token z (the tile's last token for rows past the prompt), dims gq KS ..
+  float qv[KS];
+  {
+    const float* qp = a.q + ((size_t)(zok ? z : zl) * a.qh + qhead) * HD + gq * KS;
+#pragma unroll
+    for (uint32_t i = 0; i < KS / 4; ++i) {
+      const float4 v = *reinterpret_cast<const float4*>(qp + 4 * i);
+      qv[4 * i] = v.x; qv[4 * i + 1] = v.y; qv[4 * i + 2] = v.z; qv[4 * i + 3] = v.w;
+    }
+  }
+  // staging: chunk c = tid + NTH i of a tile: row c / (HD / 4), dims 4 (c % (HD / 4)) ..
+  float4 kreg[CPT], vreg[CPT];
+  auto fetch = [&](uint32_t p) {
+#pragma unroll
+    for (uint32_t i = 0; i < CPT; ++i) {
+      const uint32_t c = min(tid + NTH * i, NCH - 1u), row = c / (HD / 4), c4 = c % (HD / 4);
+      const uint32_t off = ((p + row) * kvw + 4u * c4) * 4u;
+      const auto k4 = __builtin_amdgcn_raw_buffer_load_b128(kr, off, 0, ATT_AUX_NT);
+      const auto v4 = __builtin_amdgcn_raw_buffer_load_b128(vr, off, 0, ATT_AUX_NT);
+      kreg[i] = make_float4(__uint_as_float(k4[0]), __uint_as_float(k4[1]), __uint_as_float(k4[2]), __uint_as_float(k4[3]));
+      vreg[i] = make_float4(__uint_as_float(v4[0]), __uint_as_float(v4[1]), __uint_as_float(v4[2]), __uint_as_float(v4[3]));
+    }
+  };
+  auto stage = [&](uint32_t b) {
+#pragma unroll
+    for (uint32_t i = 0; i < CPT; ++i) {
+      const uint32_t c = tid + NTH * i, row = c / (HD / 4), c4 = c % (HD / 4);
+      if (c < NCH) {
+        *reinterpret_cast<float4*>(&kt[b][row * KP + 4u * c4]) = kreg[i];
+        float* vd = &vt[b][(4u * c4) * VP + row];
+        vd[0] = vreg[i].x; vd[VP] = vreg[i].y; vd[2 * VP] = vreg[i].z; vd[3 * VP] = vreg[i].w;
+      }
+    }
+  };
+
+  f32x4 o[DT];
+#pragma unroll
+  for (uint32_t d = 0; d < DT; ++d) o[d] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m = -INFINITY, l = 0.f;
+  fetch(lo);
+  stage(0);
+  __syncthreads();
+  uint32_t b = 0;
+  for (uint32_t p = lo; p < hi; p += APF_TOK, b ^= 1u) {
+    const bool more = p + APF_TOK < hi;
+    if (more) fetch(p + APF_TOK);
+    // S^T: two chains over the lane group's dims
+    f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+    const float* kp = &kt[b][r * KP + gq * KS];
+#pragma unroll
+    for (uint32_t i = 0; i < KS / 4; ++i) {
+      const float4 k4 = *reinterpret_cast<const float4*>(kp + 4 * i);
+      const float kk[4] = {k4.x, k4.y, k4.z, k4.w};
+#pragma unroll
+      for (uint32_t e = 0; e < 4; ++e)
+        acc[e & 1u] = __builtin_amdgcn_mfma_f32_16x16x4f32(kk[e], qv[4 * i + e], acc[e & 1u], 0, 0, 0);
+    }
+    // scores of token z at positions p + 4 gq + v, masked to its range
+    float sv[4], mx = -INFINITY;
+#pragma unroll
+    for (uint32_t v = 0; v < 4; ++v) {
+      const uint32_t pos = p + 4u * gq + v;
+      const float sc = (acc[0][v] + acc[1][v]) / a.denom;
+      sv[v] = (zok && pos >= r0 && pos < r1) ? sc : -INFINITY;
+      mx = fmaxf(mx, sv[v]);
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 16));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float mn = fmaxf(m, mx);
+    float pv[4];
+    if (mn == -INFINITY) {  // nothing of this token's range yet
+#pragma unroll
+      for (uint32_t v = 0; v < 4; ++v) pv[v] = 0.f;
+    } else {
+      const float al = expf(m - mn);  // m = -inf: 0
+      float ps = 0.f;
+#pragma unroll
+      for (uint32_t v = 0; v < 4; ++v) {
+        pv[v] = expf(sv[v] - mn);
+        ps += pv[v];
+      }
+      l = fmaf(l, al, ps);
+#pragma unroll
+      for (uint32_t d = 0; d < DT; ++d)
+#pragma unroll
+        for (uint32_t v = 0; v < 4; ++v) o[d][v] *= al;
+      m = mn;
+    }
+    // O^T += V^T P^T: MFMA t takes positions 4 gq + t
+#pragma unroll
+    for (uint32_t d = 0; d < DT; ++d) {
+      const float4 v4 = *reinterpret_cast<const float4*>(&vt[b][(16u * d + r) * VP + 4u * gq]);
+      o[d] = __builtin_amdgcn_mfma_f32_16x16x4f32(v4.x, pv[0], o[d], 0, 0, 0);
+      o[d] = __builtin_amdgcn_mfma_f32_16x16x4f32(v4.y, pv[1], o[d], 0, 0, 0);
+      o[d] = __builtin_amdgcn_mfma_f32_16x16x4f32(v4.z, pv[2], o[d], 0, 0, 0);
+      o[d] = __builtin_amdgcn_mfma_f32_16x16x4f32(v4.w, pv[3], o[d], 0, 0, 0);
+    }
+    if (more) stage(b ^ 1u);  // its last readers were the previous tile's, before the last barrier
+    __syncthreads();
+  }
+  // the token's exp-sum over its four lane groups
+  l += __shfl_xor(l, 16);
+  l += __shfl_xor(l, 32);
+  if (!zok || r0 >= r1) return;
+  const uint32_t ns = (tot + ch - 1u) / ch;
+  // lane holds O^T[16 d + 4 gq + v][token z]
+  if (ns == 1) {
+    float* op = a.out + ((size_t)z * a.qh + qhead) * HD + 4u * gq;
+#pragma unroll
+    for (uint32_t d = 0; d < DT; ++d)
+      *reinterpret_cast<float4*>(op + 16u * d) = make_float4(o[d][0] / l, o[d][1] / l, o[d][2] / l, o[d][3] / l);
+  } else {
+    float* w = a.ws + (((size_t)z * a.nsplit + sp) * a.qh + qhead) * att_rec(HD);
+#pragma unroll
+    for (uint32_t d = 0; d < DT; ++d)
+      *reinterpret_cast<float4*>(w + 16u * d + 4u * gq) = make_float4(o[d][0], o[d][1], o[d][2], o[d][3]);
+    if (gq == 0) { w[HD] = m; w[HD + 1] = l; }
+  }
+}
+
 // Any-shape fallback (tiny heads, large GQA groups): one workgroup per query
 // head, scores in the workspace ([qh][total]), plain loops.
 __global__ __launch_bounds__(256) void attn_naive(AttnArgs a) {
@@ -817,9 +1017,64 @@ hipError_t launch_attention_naive(const AttnArgs& a, hipStream_t st) {
   return hipGetLastError();
 }
 
+// Token batches on the matrix-core kernel (rf_tune_prefill_attention):
+// G = 1, 2, 4 or 8 query heads per KV head, head_dim 64 or 128, cache
+// offsets within 32 bits, and more than APF_MIN_TOTAL positions.  Timed on
+// the 8B Q8_0 prompt (32 / 8 heads, hd 128), whole prompt: 8000 tokens
+// 998 ms against 1520 ms with the split kernel, 2048 tokens 209 against 224
+// ms, but 512 tokens 49.5 against 47.8 ms: for short contexts the split
+// kernel's workgroup per token and KV head (K / V from L2) is quicker.
+// Mode 2 takes the kernel at every length (tests of short prompts).
+constexpr uint64_t APF_MIN_TOTAL = 1024;
+static int g_apf = 1;
+void set_prefill_attention_mfma(int mode) { g_apf = mode; }
+int prefill_attention_mfma() { return g_apf; }
+bool prefill_attention_mfma_supported(uint32_t qh, uint32_t kvh, uint32_t hd, uint64_t total) {
+  if (g_apf == 0 || kvh == 0 || qh % kvh || (g_apf == 1 && total <= APF_MIN_TOTAL)) return false;
+  const uint32_t G = qh / kvh;
+  return (G == 1 || G == 2 || G == 4 || G == 8) && (hd == 64 || hd == 128) &&
+         total * kvh * hd * 4 < (1ull << 31);
+}
+// Position splits of a prefill launch on that kernel: at least enough
+// workgroups (16-token tiles x KV heads x splits) for 256 CUs, and about 256
+// positions per split past that, at most 32 and no more than chunks of
+// ATT_MIN_CHUNK positions give (att_chunk's smallest chunk).
+uint32_t prefill_attention_mfma_splits(uint64_t total, uint64_t ntok, uint32_t kvh) {
+  const uint64_t tiles = (ntok + APF_TOK - 1) / APF_TOK * (kvh ? kvh : 1);
+  uint64_t n = (256 + tiles - 1) / tiles;
+  const uint64_t by_len = (total + 255) / 256, most = (total + ATT_MIN_CHUNK - 1) / ATT_MIN_CHUNK;
+  if (n < by_len) n = by_len;
+  if (n > 32) n = 32;
+  if (n > most) n = most;
+  return (uint32_t)(n < 1 ? 1 : n);
+}
+
+template <int G, int HD>
+static void launch_apf_t(const AttnArgs& a, hipStream_t st) {
+  RF_KLAUNCH((attn_prefill<G, HD>), dim3(a.nsplit, a.kvh, (a.ntok + APF_TOK - 1) / APF_TOK), dim3(64 * G), 0, st, a);
+}
+
 hipError_t launch_attention(const AttnArgs& a, hipStream_t st) {
   if (a.nsplit < 1 || a.nsplit > ATT_MAX_SPLITS) return hipErrorInvalidValue;
   const uint32_t G = a.qh / a.kvh, dpl = a.hd / 16;
+  if (a.ntok && !a.per_q && prefill_attention_mfma_supported(a.qh, a.kvh, a.hd, (uint64_t)a.hist + a.ntok)) {
+    switch (G * 1000 + a.hd) {
+      case 1064: launch_apf_t<1, 64>(a, st); break;
+      case 1128: launch_apf_t<1, 128>(a, st); break;
+      case 2064: launch_apf_t<2, 64>(a, st); break;
+      case 2128: launch_apf_t<2, 128>(a, st); break;
+      case 4064: launch_apf_t<4, 64>(a, st); break;
+      case 4128: launch_apf_t<4, 128>(a, st); break;
+      case 8064: launch_apf_t<8, 64>(a, st); break;
+      default: launch_apf_t<8, 128>(a, st); break;
+    }
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || a.nsplit == 1 || a.defer_merge) return e;
+    const dim3 mg(a.qh, 1, a.ntok);
+    if (a.hd == 64) RF_KLAUNCH(attn_merge<1>, mg, dim3(64), 0, st, a);
+    else RF_KLAUNCH(attn_merge<2>, mg, dim3(64), 0, st, a);
+    return hipGetLastError();
+  }
   // API mode knows the context on the host; model mode passes the regime's W.
   const uint32_t w = a.waves ? a.waves : attention_waves(att_chunk(a.hist + 1, a.nsplit), G * a.hd);
   if (w != 4 && w != 8) return hipErrorInvalidValue;

@@ -196,6 +196,13 @@ struct AttnArgs {
   float denom;           // sqrt(hd) as the reference computes it
 };
 hipError_t launch_attention(const AttnArgs& a, hipStream_t st);
+// Token batches (ntok > 0) run attn_prefill, the matrix-core kernel, where
+// supported (rf_tune_prefill_attention: 0 never, 1 past 1024 positions, 2
+// always); its launches take prefill_attention_mfma_splits position splits.
+void set_prefill_attention_mfma(int mode);
+int prefill_attention_mfma();
+bool prefill_attention_mfma_supported(uint32_t qh, uint32_t kvh, uint32_t hd, uint64_t total);
+uint32_t prefill_attention_mfma_splits(uint64_t total, uint64_t ntok, uint32_t kvh);
 // Decode launches that take the one-pass online-softmax kernel (attn_flash):
 // 1 (default) those per query head, 2 all, 0 none (attn_split, scores in LDS).
 void set_attention_kernel(int mode);

@@ -1449,7 +1449,15 @@ int32_t ensure_prefill_ws(rf_model* m) {
   take_max({f, f}, d);
   take_max({f}, d);
   take_max({d}, f);
-  const uint64_t att = T * prefill_attn_splits(m->kv_max) * c.head_count * att_rec((uint32_t)hd);
+  // chunk records of either prefill attention kernel: tokens x splits of
+  // the largest launch (the matrix-core kernel takes more splits for fewer
+  // tokens)
+  uint64_t recs = 0;
+  for (uint64_t nt = 1; nt <= T; ++nt)
+    recs = std::max<uint64_t>(recs, nt * std::max<uint64_t>(prefill_attn_splits(m->kv_max),
+                                                            prefill_attention_mfma_splits(
+                                                                m->kv_max, nt, (uint32_t)c.head_count_kv)));
+  const uint64_t att = recs * c.head_count * att_rec((uint32_t)hd);
   const uint64_t sizes[] = {T * d, T * d, T * qd, T * kvd, T * kvd, T * qd, T * qd, T * f, T * f, part, att};
   uint64_t total = 0;
   for (uint64_t n : sizes) total += (n + 63) / 64 * 64;
@@ -1534,11 +1542,15 @@ int32_t enqueue_prefill_layer(rf_model* m, size_t li, uint64_t pos0, uint64_t nt
   a.q = m->p_qr; a.k_hist = kc; a.v_hist = vc; a.out = m->p_a; a.ws = m->p_att;
   a.hist = (uint32_t)pos0; a.ntok = (uint32_t)nt;
   a.qh = (uint32_t)c.head_count; a.kvh = (uint32_t)c.head_count_kv; a.hd = (uint32_t)hd;
-  // The chunk's tokens already give nt x kvh workgroups: one workgroup per
-  // KV head (its query heads share each K/V row read) and chunks of up to
-  // ATT_MAX_CHUNK positions, so up to 1024 positions need no merge.
+  // The matrix-core kernel: 16-token tiles x KV heads x position splits.
+  // Otherwise the decode split kernel with a token dimension: nt x kvh
+  // workgroups, one per KV head (its query heads share each K/V row read)
+  // and chunks of up to ATT_MAX_CHUNK positions, so up to 1024 positions
+  // need no merge.
   a.per_q = 0;
-  a.nsplit = prefill_attn_splits(pos0 + nt);
+  a.nsplit = prefill_attention_mfma_supported(a.qh, a.kvh, a.hd, pos0 + nt)
+                 ? prefill_attention_mfma_splits(pos0 + nt, nt, a.kvh)
+                 : prefill_attn_splits(pos0 + nt);
   a.waves = attention_waves(att_chunk_positions(pos0 + nt, a.nsplit), 0);
   a.denom = sqrtf((float)hd);
   RF_LAUNCH(launch_attention(a, st), "prefill attention");
@@ -2269,6 +2281,11 @@ int32_t rf_model_residency_stats(rf_model* m, uint64_t* out) {
 int32_t rf_tune_attention_single(int32_t positions) {
   if (positions == 64 || positions == 128 || positions == 256) set_attention_single((uint32_t)positions);
   return (int32_t)attention_single();
+}
+
+int32_t rf_tune_prefill_attention(int32_t mode) {
+  if (mode >= 0 && mode <= 2) set_prefill_attention_mfma(mode);
+  return prefill_attention_mfma();
 }
 
 int32_t rf_tune_attention_kernel(int32_t mode) {

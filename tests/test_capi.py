@@ -85,7 +85,8 @@ def test_tune_switches_without_a_gpu():
     lib = _lib.load()
     for name, default, modes in (("rf_tune_attention_merge", 1, (0, 1)), ("rf_tune_packed_inflight", 1, (0, 1)),
                                  ("rf_tune_packed_weights", 1, (0, 1)), ("rf_tune_matvec_digits", 0, (0, 1, 2)),
-                                 ("rf_tune_attention_kernel", 1, (0, 1, 2)), ("rf_tune_matvec_kernel", 2, (0, 1, 2))):
+                                 ("rf_tune_attention_kernel", 1, (0, 1, 2)), ("rf_tune_matvec_kernel", 2, (0, 1, 2)),
+                                 ("rf_tune_prefill_attention", 1, (0, 1, 2))):
         fn = getattr(lib, name)
         assert fn(-1) == default, name
         for m in modes:

@@ -115,13 +115,27 @@ ALL_KQ = dict(embd=Q4_K, out=Q6_K, q=Q4_K, k=Q4_K, v=Q6_K, o=Q4_K, gate=Q4_K, up
 
 
 @pytest.mark.parametrize("kind,history,plen", [("q8", 0, 1), ("q8", 0, 37), ("q8", 3, 64), ("q8", 0, 150),
-                                               ("q4", 0, 70), ("mixed", 0, 40), ("kq", 2, 90), ("kq_bias", 0, 20)])
+                                               ("q4", 0, 70), ("mixed", 0, 40), ("kq", 2, 90), ("kq_bias", 0, 20),
+                                               ("q8_attn0", 3, 150), ("kq_attn0", 0, 90)])
 def test_prefill_matches_token_by_token(ctx, orc, kind, history, plen):
     """Prompt of plen tokens after `history` single-token forwards: hidden
     state and logits of the last token against the oracle, then greedy
     tokens from there.  150 and 90 tokens span several 64-token chunks; 64
     tokens at history 3 crosses the 64-position attention regime inside a
-    chunk."""
+    chunk.  The matrix-core prefill attention runs every chunk (these
+    contexts are below its default threshold); *_attn0: the decode split
+    kernel with a token dimension instead."""
+    import ramforge_amd as rf
+
+    old_attn = rf.tune_prefill_attention(0 if kind.endswith("_attn0") else 2)
+    kind = kind.replace("_attn0", "")
+    try:
+        _prefill_case(ctx, orc, kind, history, plen)
+    finally:
+        rf.tune_prefill_attention(old_attn)
+
+
+def _prefill_case(ctx, orc, kind, history, plen):
     types = {"q8": ALL_Q8, "q4": ALL_Q4, "mixed": MIXED, "kq": ALL_KQ, "kq_bias": ALL_KQ}[kind]
     cfg = dict(PF_CFG) if kind in ("q8", "q4") else dict(KQ_CFG)
     rng = np.random.default_rng(3300 + plen + history)
@@ -152,6 +166,45 @@ def test_prefill_matches_token_by_token(ctx, orc, kind, history, plen):
         assert toks == ref, f"greedy divergence (min top-2 margin {margin.min():.3g})"
     finally:
         om.close()
+        gm.close()
+
+
+@pytest.mark.parametrize("qh,kvh,hd", [(4, 4, 64), (8, 1, 64), (8, 4, 128), (16, 2, 128), (4, 2, 64)])
+def test_prefill_attention_gqa_shapes(ctx, qh, kvh, hd):
+    """The matrix-core prefill attention (forced on every chunk) for every
+    query-head group size it takes (1, 2, 4, 8) and head_dim 64 / 128: a
+    150-token prompt after 70
+    single-token forwards (position splits with chunk records and their
+    merge, partial 16-token tiles) gives the hidden state and logits of the
+    token-by-token forward within 2e-4 of their maximum, and so does the
+    split kernel it replaces."""
+    import ramforge_amd as rf
+
+    cfg = dict(PF_CFG, head_count=qh, head_count_kv=kvh, head_dim=hd, embedding_length=max(128, qh * hd // 2),
+               context_length=256)
+    rng = np.random.default_rng(3500 + qh * 10 + kvh + hd)
+    T = _tiny_tensors(rng, cfg, ALL_Q8)
+    gm = _load_gpu(ctx, cfg, T, 240)
+    prompt = [int(v) for v in rng.integers(0, cfg["vocab_size"], 220)]
+    print(f"  prefill attention qh={qh} kvh={kvh} hd={hd}", flush=True)
+    try:
+        assert gm.paths()["batched_prefill"]
+        gm.reset()
+        href = None
+        for p, t in enumerate(prompt):
+            href = gm.forward(t, p, want_hidden=True)
+        lref = gm.logits().copy()
+        for mode in (2, 0):
+            rf.tune_prefill_attention(mode)
+            gm.reset()
+            for p in range(70):
+                gm.forward(prompt[p], p)
+            h = gm.prefill(prompt[70:], want_hidden=True)
+            lg = gm.logits()
+            assert np.max(np.abs(h - href)) <= 2e-4 * max(1.0, np.abs(href).max()), (mode, qh, kvh, hd)
+            assert np.max(np.abs(lg - lref)) <= 2e-4 * max(1.0, np.abs(lref).max()), (mode, qh, kvh, hd)
+    finally:
+        rf.tune_prefill_attention(1)
         gm.close()
 
 
