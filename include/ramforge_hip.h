@@ -455,8 +455,20 @@ typedef int32_t (*rf_read_fn)(void *user, uint64_t offset, uint64_t length, void
  * with layer streaming enabled and before any rf_model_set_tensor_source.
  * Two pinned staging buffers of staging_bytes each (>= 4096) are the host
  * memory the reads use; `read` is called on the thread that runs the forward
- * pass, one range at a time. */
+ * pass, one range at a time, and, with read-ahead on (rf_model_set_read_ahead;
+ * the default for rf_file_source_read), also from the model's worker thread. */
 int32_t rf_model_set_reader(rf_model *model, rf_read_fn read, void *user, uint64_t staging_bytes);
+/* Read-ahead of the byte source (1 on, 0 off):
+ * a worker thread of the model reads the next layer the pass will load from
+ * the source (the next host-only layer in layer order) into a pinned buffer
+ * of one layer's source bytes (allocated at the first read-ahead) while the
+ * calling thread queues the layers before it; the pass then uploads from
+ * that buffer.  `read` is then also called from the worker thread, so it
+ * must be thread-safe.  On by default when `read` is rf_file_source_read,
+ * off for other readers.  A failed read-ahead is reported by the load that
+ * needs it, as RF_ERR_IO.  No counterpart in the reference (its reads run
+ * on the forward pass's thread). */
+int32_t rf_model_set_read_ahead(rf_model *model, int32_t on);
 /* A byte source over a model file, for rf_model_set_reader: pass
  * rf_file_source_read as `read` and the handle as `user`.  Each read of
  * [offset, offset + length) is split over up to `threads` threads (pieces of

@@ -648,6 +648,12 @@ class GpuLlamaModel:
         _lib.check(self.ctx.lib.rf_model_set_reader(self.handle, source.callback, getattr(source, "user", None),
                                                     int(staging_bytes)))
 
+    def set_read_ahead(self, on: bool) -> None:
+        """Read the next layer the pass will load from the byte source on a
+        worker thread (rf_model_set_read_ahead; the reader must then be
+        thread-safe; on by default for FileSource, off for ByteSource)."""
+        _lib.check(self.ctx.lib.rf_model_set_read_ahead(self.handle, int(bool(on))))
+
     def set_tensor_source(self, name: str, ggml_type: int, ne0: int, ne1: int, offset: int, nbytes: int) -> None:
         """Declare block tensor `name` at [offset, offset + nbytes) of the byte source."""
         _lib.check(self.ctx.lib.rf_model_set_tensor_source(self.handle, name.encode(), ggml_type, ne0, ne1,

@@ -125,6 +125,7 @@ SIGNATURES = {
     "rf_model_use_graph": (_i32, [_vp, _i32]),
     "rf_model_kv_growth": (_i32, [_vp, _u64]),
     "rf_model_set_reader": (_i32, [_vp, READ_FN, _vp, _u64]),
+    "rf_model_set_read_ahead": (_i32, [_vp, _i32]),
     "rf_file_source_open": (_i32, [C.c_char_p, _u32, C.POINTER(_vp)]),
     "rf_file_source_close": (None, [_vp]),
     "rf_model_set_tensor_source": (_i32, [_vp, C.c_char_p, _u32, _u64, _u64, _u64, _u64]),

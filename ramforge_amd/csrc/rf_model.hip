@@ -24,7 +24,11 @@
 // in VRAM so a decode step needs no host round-trip and can be captured once
 // into a hipGraph and replayed.
 #include <algorithm>
+#include <condition_variable>
 #include <list>
+#include <mutex>
+#include <thread>
+#include <utility>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
@@ -149,6 +153,27 @@ struct rf_model {
   void* rraw = nullptr;
   uint64_t rraw_bytes = 0;
   uint64_t st_read_calls = 0, st_read_bytes = 0;
+  // Read-ahead (rf_model_set_read_ahead; on by default with the library's
+  // own rf_file_source_read, whose reads are thread-safe): a worker thread
+  // reads the next host-only layer's ranges into one of two pinned buffers
+  // of a layer's source bytes while this thread queues the layers before it
+  // (two, so that one layer's upload and the next one's read overlap).
+  struct ReadAhead {
+    std::thread th;
+    std::mutex mu;
+    std::condition_variable cv;
+    bool on = false, stop = false;
+    int state = 0;       // 0 idle, 1 requested (being read), 2 read, 3 the read failed
+    int64_t layer = -1;  // layer of the request
+    std::vector<std::pair<uint64_t, uint64_t>> ranges;  // (offset, length) of its reads, in buffer order
+    int32_t err = 0;     // a failed read: the reader's code and range
+    uint64_t err_off = 0, err_len = 0;
+    void* buf[2] = {nullptr, nullptr};
+    uint64_t bytes = 0;                     // of each buffer
+    hipEvent_t done[2] = {nullptr, nullptr};  // the copies out of buf[i] ended
+    int slot = 0;                           // buffer of the request
+    uint64_t used = 0;                      // layers served from the buffers
+  } ra;
 };
 
 namespace {
@@ -446,6 +471,130 @@ int32_t plan_layer_reads(rf_model* m, DevTensor* t[12], std::vector<ReadRange>* 
   return RF_OK;
 }
 
+// Read-ahead worker: waits for a request, for the copies out of the buffer
+// to end, then reads the request's ranges into it.
+void ra_worker(rf_model* m) {
+  rf_model::ReadAhead& ra = m->ra;
+  (void)hipSetDevice(m->ctx->device);
+  std::unique_lock<std::mutex> lk(ra.mu);
+  for (;;) {
+    ra.cv.wait(lk, [&] { return ra.stop || ra.state == 1; });
+    if (ra.stop) return;
+    const std::vector<std::pair<uint64_t, uint64_t>> ranges = ra.ranges;
+    const int slot = ra.slot;
+    lk.unlock();
+    (void)hipEventSynchronize(ra.done[slot]);
+    int32_t err = 0;
+    uint64_t eo = 0, el = 0, pos = 0;
+    for (const auto& r : ranges) {
+      const int32_t rc = m->reader(m->reader_user, r.first, r.second, static_cast<uint8_t*>(ra.buf[slot]) + pos);
+      if (rc != 0) {
+        err = rc;
+        eo = r.first;
+        el = r.second;
+        break;
+      }
+      pos += r.second;
+    }
+    lk.lock();
+    ra.err = err;
+    ra.err_off = eo;
+    ra.err_len = el;
+    ra.state = err ? 3 : 2;
+    ra.cv.notify_all();
+  }
+}
+
+void ra_stop(rf_model* m) {
+  rf_model::ReadAhead& ra = m->ra;
+  if (ra.th.joinable()) {
+    {
+      std::lock_guard<std::mutex> g(ra.mu);
+      ra.stop = true;
+    }
+    ra.cv.notify_all();
+    ra.th.join();
+  }
+  ra.stop = false;
+  ra.state = 0;
+  ra.layer = -1;
+  for (int i = 0; i < 2; ++i) {
+    if (ra.done[i]) (void)hipEventSynchronize(ra.done[i]);
+    if (ra.buf[i]) hipHostFree(ra.buf[i]);
+    ra.buf[i] = nullptr;
+  }
+  ra.bytes = 0;
+}
+
+int32_t plan_layer_reads(rf_model* m, DevTensor* t[12], std::vector<ReadRange>* out);
+
+// Bytes a layer's reads fill (0 when it has no source tensors).
+uint64_t layer_read_bytes(rf_model* m, uint32_t li) {
+  DevTensor* t[12];
+  layer_slots(m->layers[li], t);
+  std::vector<ReadRange> plan;
+  if (plan_layer_reads(m, t, &plan) != RF_OK) return 0;
+  uint64_t n = 0;
+  for (const ReadRange& r : plan) n += r.len;
+  return n;
+}
+
+// Requests layer li's bytes from the worker (started, with its buffer sized
+// for the largest layer, at the first request).  A request while the worker
+// reads is dropped; the layer is then read by the pass itself.
+void ra_post(rf_model* m, uint32_t li) {
+  rf_model::ReadAhead& ra = m->ra;
+  if (!ra.on || !m->reader) return;
+  if (!ra.buf[0]) {
+    uint64_t most = 0;
+    for (uint32_t j = 0; j < m->layers.size(); ++j) most = std::max(most, layer_read_bytes(m, j));
+    if (most == 0) return;
+    for (int i = 0; i < 2; ++i) {
+      if (!ra.done[i] && hipEventCreateWithFlags(&ra.done[i], hipEventDisableTiming) != hipSuccess) ra.done[i] = nullptr;
+      if (ra.done[i] && hipHostMalloc(&ra.buf[i], most, hipHostMallocDefault) != hipSuccess) ra.buf[i] = nullptr;
+    }
+    if (!ra.buf[0] || !ra.buf[1]) {  // no room for them: the pass reads as without
+      for (int i = 0; i < 2; ++i) {
+        if (ra.buf[i]) hipHostFree(ra.buf[i]);
+        ra.buf[i] = nullptr;
+      }
+      ra.on = false;
+      return;
+    }
+    ra.bytes = most;
+  }
+  if (!ra.th.joinable()) ra.th = std::thread(ra_worker, m);
+  DevTensor* t[12];
+  layer_slots(m->layers[li], t);
+  std::vector<ReadRange> plan;
+  if (plan_layer_reads(m, t, &plan) != RF_OK) return;
+  uint64_t total = 0;
+  for (const ReadRange& r : plan) total += r.len;
+  if (total == 0 || total > ra.bytes) return;
+  std::lock_guard<std::mutex> g(ra.mu);
+  if (ra.state == 1 || (ra.state == 2 && ra.layer == (int64_t)li)) return;
+  ra.ranges.clear();
+  for (const ReadRange& r : plan) ra.ranges.emplace_back(r.off, r.len);
+  // the last read's buffer may still be uploading from: read into the other
+  // one (a read nobody took keeps its buffer)
+  if (ra.state == 0) ra.slot ^= 1;
+  ra.layer = li;
+  ra.state = 1;
+  ra.cv.notify_all();
+}
+
+// The next layer the pass will load from the byte source, in the layer cycle
+// from `from` on: a host-only layer of this pass, else of the next one (a
+// retired layer is released at the end of this pass); -1 when none.
+int64_t next_read_layer(rf_model* m, uint32_t from) {
+  const uint32_t nl = (uint32_t)m->layers.size();
+  for (uint32_t j = from; j < nl; ++j)
+    if (m->res[j].state == LAYER_HOST) return j;
+  for (uint32_t j = 0; j < std::min(from, nl); ++j)
+    if (m->res[j].state == LAYER_HOST || m->res[j].state == LAYER_RETIRED) return j;
+  return -1;
+}
+
 // Reads the layer's source tensors range by range into the pinned staging
 // buffers (alternating, each reused once the copy out of it has finished),
 // copies every tensor to its device buffer, or to the raw buffer and then
@@ -454,6 +603,52 @@ int32_t read_layer_sources(rf_model* m, uint32_t li, DevTensor* t[12], hipStream
   std::vector<ReadRange> plan;
   int32_t rc = plan_layer_reads(m, t, &plan);
   if (rc) return rc;
+  auto convert = [&](DevTensor* x) -> hipError_t {  // raw buffer -> device layout
+    if (x->type == T_F32 && x->src_type != T_F32)
+      return launch_dequant_rows(x->src_type, m->rraw, x->ne0, x->ne1, static_cast<float*>(x->d), nullptr, 0, cs);
+    return launch_pack(x->src_type, m->rraw, x->d, x->ne1, x->ne0, cs);
+  };
+  auto needs_convert = [](const DevTensor* x) { return x->packed || (x->type == T_F32 && x->src_type != T_F32); };
+  // read ahead by the worker: the layer's ranges are in its buffer, in plan order
+  if (m->ra.on) {
+    rf_model::ReadAhead& ra = m->ra;
+    std::unique_lock<std::mutex> lk(ra.mu);
+    if (ra.layer == (int64_t)li && ra.state != 0) {
+      ra.cv.wait(lk, [&] { return ra.state != 1; });
+      const bool failed = ra.state == 3;
+      const int32_t err = ra.err;
+      const uint64_t eo = ra.err_off, el = ra.err_len;
+      uint64_t calls = 0, bytes = 0;
+      for (const auto& r : ra.ranges) {
+        calls += 1;
+        bytes += r.second;
+      }
+      ra.state = 0;
+      ra.layer = -1;
+      if (failed)
+        return set_error(RF_ERR_IO, "byte source read of %llu bytes at offset %llu failed (%d) for layer %u",
+                         (unsigned long long)el, (unsigned long long)eo, (int)err, li);
+      m->st_read_calls += calls;
+      m->st_read_bytes += bytes;
+      uint64_t pos = 0;
+      for (const ReadRange& r : plan) {
+        for (int i : r.slots) {
+          DevTensor* x = t[i];
+          const bool cv = needs_convert(x);
+          hipError_t e = hipMemcpyAsync(cv ? m->rraw : x->d,
+                                        static_cast<uint8_t*>(ra.buf[ra.slot]) + pos + (x->src_off - r.off),
+                                        x->src_bytes, hipMemcpyHostToDevice, cs);
+          if (e == hipSuccess && cv) e = convert(x);
+          if (e != hipSuccess) return hip_error(e, "layer upload");
+          m->st_uploaded += x->src_bytes;
+        }
+        pos += r.len;
+      }
+      ra.used += 1;
+      const hipError_t e = hipEventRecord(ra.done[ra.slot], cs);
+      return e == hipSuccess ? RF_OK : hip_error(e, "hipEventRecord");
+    }
+  }
   int buf = 0;
   auto fill = [&](uint64_t off, uint64_t len) -> int32_t {  // one reader call into the next staging buffer
     hipError_t e = hipEventSynchronize(m->rstage_ev[buf]);
@@ -466,12 +661,6 @@ int32_t read_layer_sources(rf_model* m, uint32_t li, DevTensor* t[12], hipStream
     m->st_read_bytes += len;
     return RF_OK;
   };
-  auto convert = [&](DevTensor* x) -> hipError_t {  // raw buffer -> device layout
-    if (x->type == T_F32 && x->src_type != T_F32)
-      return launch_dequant_rows(x->src_type, m->rraw, x->ne0, x->ne1, static_cast<float*>(x->d), nullptr, 0, cs);
-    return launch_pack(x->src_type, m->rraw, x->d, x->ne1, x->ne0, cs);
-  };
-  auto needs_convert = [](const DevTensor* x) { return x->packed || (x->type == T_F32 && x->src_type != T_F32); };
   for (const ReadRange& r : plan) {
     if (r.len <= m->rstage_bytes) {
       if ((rc = fill(r.off, r.len))) return rc;
@@ -1333,6 +1522,10 @@ int32_t enqueue_forward(rf_model* m, bool embed = true) {
     if ((rc = enqueue_layer(m, li, li + 1 == nl ? m->d_pos : nullptr))) return m->streaming ? abort_pass(m, rc) : rc;
     if (m->streaming && (rc = settle_layer(m, li))) return abort_pass(m, rc);
     if (read_after && li + 1 < nl && (rc = acquire_layer(m, li + 1, true))) return abort_pass(m, rc);
+    if (read_after && m->ra.on) {  // the worker reads the next host-only layer meanwhile
+      const int64_t nx = next_read_layer(m, li + 2);
+      if (nx >= 0) ra_post(m, (uint32_t)nx);
+    }
   }
   if (m->streaming) {
     int32_t rc = release_retired(m);  // release_layer for layers the cache did not take
@@ -1744,6 +1937,9 @@ extern "C" {
 
 void rf_model_destroy(rf_model* m) {
   if (!m) return;
+  ra_stop(m);
+  for (hipEvent_t e : m->ra.done)
+    if (e) hipEventDestroy(e);
   reset_graph(m);
   hipStreamSynchronize(m->ctx->compute);
   hipStreamSynchronize(m->ctx->copy);
@@ -2125,9 +2321,20 @@ int32_t rf_model_set_reader(rf_model* m, rf_read_fn read, void* user, uint64_t s
     m->rstage[i] = b[i];
     m->rstage_ev[i] = ev[i];
   }
+  ra_stop(m);
   m->rstage_bytes = staging_bytes;
   m->reader = read;
   m->reader_user = user;
+  m->ra.on = read == rf_file_source_read;  // thread-safe: read ahead by default
+  return RF_OK;
+}
+
+int32_t rf_model_set_read_ahead(rf_model* m, int32_t on) {
+  if (!m) return set_error(RF_ERR_INVALID, "null model");
+  if (on != 0 && on != 1) return set_error(RF_ERR_INVALID, "read-ahead is 0 or 1, got %d", (int)on);
+  if (on && !m->reader) return set_error(RF_ERR_INVALID, "no byte source (rf_model_set_reader)");
+  if (!on) ra_stop(m);
+  m->ra.on = on == 1;
   return RF_OK;
 }
 
@@ -2263,6 +2470,7 @@ int32_t rf_model_host_bytes(rf_model* m, uint64_t* pinned) {
     if (x->host) n += x->nbytes;
   for (int i = 0; i < 2; ++i)
     if (m->rstage[i]) n += m->rstage_bytes;
+  n += 2 * m->ra.bytes;
   *pinned = n;
   return RF_OK;
 }

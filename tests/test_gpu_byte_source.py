@@ -152,3 +152,90 @@ def test_failed_read_releases_the_load(ctx):
     m.close()
     pm.close()
     pm.ctx.close()
+
+
+def _layer_bytes(T, i):
+    return sum(np.asarray(a).nbytes for n, (_, _, _, a) in T.items() if n.startswith(f"blk.{i}."))
+
+
+@pytest.mark.parametrize("kind", ["file_source", "python_source"])
+@pytest.mark.parametrize("cached_layers", [0, 2])
+def test_read_ahead_matches_pinned_streaming(ctx, tmp_path, kind, cached_layers):
+    """Read-ahead (the model's worker thread reads the next layer the pass
+    will load into a pinned buffer of one layer while the pass queues the
+    layers before it): every layer streamed each token, or two cached,
+    through the library's file source (read-ahead on by default) and a
+    Python source with read-ahead turned on.  Hidden states and greedy
+    tokens equal the pinned tier's and the same source's without read-ahead
+    bit for bit; the read-ahead buffer shows in the pinned host bytes."""
+    rf = _rf()
+    cfg = STREAM_CFG
+    T = _tiny_tensors(np.random.default_rng(1450 + cached_layers), cfg, STREAM_TYPES, bias=True)
+    blob, spans = _layout(T)
+    path = tmp_path / "model.bin"
+    blob.tofile(path)
+    cache = cached_layers * _layer_bytes(T, 0)
+    prompt = [7, 1, 33, 90]
+
+    def run(read_ahead):
+        src = rf.FileSource(str(path), threads=2) if kind == "file_source" else rf.ByteSource(blob.tobytes())
+        src.spans = spans
+        m = _sourced_model(ctx, cfg, T, src, 1 << 20, cache_bytes=cache)
+        try:
+            if kind == "python_source" or not read_ahead:
+                m.set_read_ahead(read_ahead)
+            before = m.host_bytes()
+            h = m.forward(prompt[0], 0, want_hidden=True)
+            m.reset()
+            toks = m.generate(prompt, 12)
+            return h, toks, m.host_bytes() - before
+        finally:
+            m.close()
+            src.close()
+
+    h1, t1, grown = run(True)
+    h0, t0, grown0 = run(False)
+    pm = _pinned_model(cfg, T, cache_bytes=cache)
+    hp = pm.forward(prompt[0], 0, want_hidden=True)
+    pm.reset()
+    tp = pm.generate(prompt, 12)
+    pm.close()
+    pm.ctx.close()
+    assert np.array_equal(h1, h0) and np.array_equal(h1, hp)
+    assert t1 == t0 == tp
+    assert grown >= _layer_bytes(T, 1) and grown0 == 0, (grown, grown0)
+
+
+def test_read_ahead_failed_read_releases_the_load(ctx):
+    """A read-ahead that fails is reported by the load that needs it
+    (RF_ERR_IO naming the layer), with every charge of that load released;
+    the model then runs normally."""
+    rf = _rf()
+    cfg = STREAM_CFG
+    T = _tiny_tensors(np.random.default_rng(1460), cfg, STREAM_TYPES)
+    blob, spans = _layout(T)
+    src = rf.ByteSource(blob.tobytes())
+    src.spans = spans
+    m = _sourced_model(ctx, cfg, T, src, 1 << 20, cache_bytes=0)
+    m.set_read_ahead(True)
+    used = ctx.vram_used
+    src.fail_at = spans["blk.2.ffn_up.weight"][0] + 10  # layer 2's range fails
+    with pytest.raises(rf.RamforgeError) as ei:
+        m.forward(4, 0)
+    assert ei.value.code == rf.RF_ERR_IO and "layer 2" in str(ei.value)
+    assert ctx.vram_used == used
+    assert all(ctx.charge(f"layer:2:{s}") is None for s in ("attn_q.weight", "ffn_up.weight", "ffn_down.weight"))
+    src.fail_at = None
+    m.reset()
+    h = m.forward(4, 0, want_hidden=True)
+    pm = _pinned_model(cfg, T, cache_bytes=0)
+    assert np.array_equal(h, pm.forward(4, 0, want_hidden=True))
+    m.close()
+    pm.close()
+    pm.ctx.close()
+    with pytest.raises(rf.RamforgeError, match="0 or 1"):
+        m2 = _sourced_model(ctx, cfg, T, src, 1 << 20, cache_bytes=0)
+        try:
+            _rf()._lib.check(ctx.lib.rf_model_set_read_ahead(m2.handle, 7))
+        finally:
+            m2.close()
