@@ -442,8 +442,10 @@ def config5_bench(rf, syn, tokens: int, prompt_len: int, policy: int, persistent
     3 keeps the embedding table in mapped host memory (a step reads one
     row), leaving its VRAM to cached layers.  model_file: (path, spans) of
     the block tensors written by synthetic.write_model_file, read on every
-    layer load through the library's pread reader and two 64 MiB pinned
-    staging buffers instead of kept in pinned host memory."""
+    layer load through the library's pread reader instead of kept in pinned
+    host memory; the model's worker thread reads the next layer to load into
+    one of two pinned layer buffers while the pass runs (read-ahead, on by
+    default for that reader)."""
     import numpy as np
 
     cfg = syn.CONFIG_8B
@@ -478,8 +480,8 @@ def config5_bench(rf, syn, tokens: int, prompt_len: int, policy: int, persistent
     wall = time.perf_counter() - t0
     st = m.residency_stats()
     up = st["uploaded_bytes"] - pre["uploaded_bytes"]
-    where = ("read from the model file on every layer load (pread, two 64 MiB pinned staging buffers)"
-             if model_file is not None else "streamed from pinned host memory")
+    where = ("read from the model file on every layer load (pread, read ahead of the pass into two pinned "
+             "layer buffers)" if model_file is not None else "streamed from pinned host memory")
     out = {"workload": "config 5: 8B shape, Q4_K body + Q6_K output, context 8192, 4 GiB VRAM budget, layers "
                        f"{where}, KV cache grown in 256-position chunks",
            "pinned_host_bytes": m.host_bytes(),
