@@ -208,6 +208,36 @@ def test_prefill_attention_gqa_shapes(ctx, qh, kvh, hd):
         gm.close()
 
 
+def test_prefill_attention_past_threshold_small_chunks(ctx):
+    """Chunks of 1 and 17 tokens after 1030 positions (the default mode runs
+    the matrix-core prefill attention there): hidden state and logits equal
+    the token-by-token forward's within 2e-4 of their maximum."""
+    cfg = dict(PF_CFG, context_length=1100)
+    rng = np.random.default_rng(3600)
+    T = _tiny_tensors(rng, cfg, ALL_Q8)
+    gm = _load_gpu(ctx, cfg, T, 1100)
+    prompt = [int(v) for v in rng.integers(0, cfg["vocab_size"], 1048)]
+    try:
+        assert gm.paths()["batched_prefill"]
+        gm.reset()
+        ref = {}
+        for p, t in enumerate(prompt):
+            h = gm.forward(t, p, want_hidden=p in (1030, 1047))
+            if p in (1030, 1047):
+                ref[p] = (h, gm.logits().copy())
+        gm.reset()
+        for p in range(1030):
+            gm.forward(prompt[p], p)
+        for end in (1031, 1048):
+            h = gm.prefill(prompt[gm.seq_len:end], want_hidden=True)
+            hr, lr = ref[end - 1]
+            assert np.max(np.abs(h - hr)) <= 2e-4 * max(1.0, np.abs(hr).max()), end
+            lg = gm.logits()
+            assert np.max(np.abs(lg - lr)) <= 2e-4 * max(1.0, np.abs(lr).max()), end
+    finally:
+        gm.close()
+
+
 def test_prefill_then_device_decode_graph(ctx, orc):
     """A batched prompt followed by graph-replayed device decode steps gives
     the tokens of the host generate loop with a token-by-token prompt."""
