@@ -803,11 +803,10 @@ def tune_matvec_tile_bytes(nbytes: int = 0) -> int:
 
 
 def tune_matvec_kernel(mode: int = -1) -> int:
-    """GGUF-layout matvec kernels: 2 (default) plain Q8_0 matvecs of up to
-    4096 inputs read rows into registers and realign the blocks there, the
-    rest as 1; 1
-    persistent streaming kernel with LDS row tiles; 0 one-shot tile kernel;
-    -1 queries.  Returns the mode in effect."""
+    """GGUF-layout matvec kernels: 2 (default) plain Q8_0 / Q4_0 matvecs
+    stage each row per wavefront in LDS through 16-byte loads, the rest as
+    1; 1 persistent streaming kernel with LDS row tiles; 0 one-shot tile
+    kernel; -1 queries.  Returns the mode in effect."""
     return _lib.load().rf_tune_matvec_kernel(mode)
 
 

@@ -75,11 +75,10 @@ void set_matvec_stream_tile(uint32_t bytes);
 uint32_t matvec_tile_bytes();
 void set_matvec_stream(bool on);
 bool matvec_stream();
-// Plain (store, no norm, one segment) Q8_0 matvecs of up to 4096 inputs on
-// GGUF bytes take the register-realigning lane kernel (rf_tune_matvec_kernel
-// 2, default).
-void set_matvec_lanes(bool on);
-bool matvec_lanes_on();
+// Plain (store, no norm, one segment) Q8_0 / Q4_0 matvecs on GGUF bytes take
+// the wave-staged kernel (rf_tune_matvec_kernel 2, default).
+void set_matvec_wave(bool on);
+bool matvec_wave_on();
 // Packed Q8_0 / Q4_0 launches take x as int8 digit planes when a wavefront's
 // rows hold >= 24 KiB of codes (1), always (2), or never (0).
 void set_matvec_digits(int mode);

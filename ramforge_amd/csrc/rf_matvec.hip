@@ -551,138 +551,290 @@ static hipError_t launch_stream_t(const MvArgs& a, uint32_t tiles, const MvPlan&
   return hipGetLastError();
 }
 
-// ------------------------------------------------ lane kernel (Q8_0)
-// GGUF rows read straight into registers, realigned there: one row per
-// wavefront at a time, lane l owning blocks l, l + 64, ... of the row.  A
-// 34-byte block at byte 34 b starts 0 (even b) or 2 (odd b) bytes into a
-// dword: the lane loads the 9 dwords covering it with raw buffer loads
-// (dword alignment; offsets past the row return zeros) and takes the codes
-// as dwords 1..8 (odd b) or shifts them down by two bytes with v_alignbyte
-// (even b).  No LDS tile and no barrier in the row loop: x sits in LDS once
-// per workgroup of four wavefronts, about two rows per wavefront.  Signed
-// codes times x, the block scale once per block, as the other kernels
-// (quant.rs:977-1029 up to the order of the sums).  Rows must start on
-// dwords (an even block count per row, a dword-aligned base).
-// Timed against the LDS-tiled streaming kernel (graph replay, weights
-// rotated over >= 1.2 GiB): Q8_0 4096 x 4096 8.9 against 11.0 us; but
-// slower for wider rows (Q8_0 28672 x 8192 67 against 57 us) and for Q4_0
-// (14336 x 4096 21 against 17 us, 18-byte blocks: two loads per 32
-// weights), and a persistent grid of 8-wavefront workgroups with two blocks
-// per lane (always dword aligned) was slower still (12.2 us at 4096 x
-// 4096), so it takes Q8_0 rows of up to 4096 inputs only.
+// ------------------------------------------------ wave-staged kernel (Q8_0, Q4_0)
+// GGUF rows staged per wavefront: each wavefront owns whole rows (row i,
+// i + G, ... for G wavefronts in the grid), loads the bytes of its next row
+// (or of its next chunk of at most 8 KiB, for longer rows) with 16-byte
+// loads that are contiguous across lanes, writes them into its own LDS
+// region and reads the blocks back from there, four lanes per block.  The
+// next item's loads are in flight while the current one is summed; no
+// barrier after the prologue (a wavefront's LDS writes and reads complete in
+// order).  x sits in LDS once per workgroup.
+//   Q8_0: lane q of a block takes codes 8q..8q+7 (bytes 2+8q.., realigned
+//   with v_alignbyte; a block starts 0 or 2 bytes into a dword) times
+//   x[8q..8q+7]; Q4_0: bytes 2+4q..2+4q+3, low nibbles times x[4q..4q+3],
+//   high nibbles times x[16+4q..16+4q+3].
+// Signed codes times x, the block scale once per block and lane, as the
+// other kernels (quant.rs:977-1029 up to the order of the sums); a code of 0
+// meets an infinite x as the reference's 0 * inf = NaN term does.
+// Timed under graph replay with >= 1.2 GiB of rotated copies against the
+// lane kernel it replaced (registers only, lane = block, 34-byte strided
+// loads): Q8_0 4096 x 4096 6.4 against 8.6 us, 1024 x 4096 4.0 against 5.3,
+// 14336 x 4096 14.3 against 20.4; Q4_0 14336 x 4096 10.7 us and 4096 x 14336
+// 14.0 against 17.1 and 16.6 for the LDS-tiled streaming kernel.  Two items
+// in flight per wavefront, two rows per item sharing the x reads and a
+// contiguous eight-element lane mapping for Q4_0 were slower.
 typedef __amdgpu_buffer_rsrc_t MvRsrc;
 constexpr int MV_RSRC_WORD3 = 0x00020000;
-constexpr uint32_t MVL_WAVES = 4;
-constexpr uint32_t MVL_MAX_IN = 4096;
+constexpr uint32_t MVW_CHUNK = 8192;  // most bytes one item stages
+constexpr uint32_t MVW_LDS = 160 * 1024;
 
-// BPL blocks per lane and row (ceil(blocks / 64)); NB rows in flight per
-// wavefront (the next row's dwords requested before this row is summed).
-template <int BPL, int NB>
-__global__ __launch_bounds__(64 * MVL_WAVES) void matvec_lanes(const uint8_t* __restrict__ w,
-                                                               const float* __restrict__ x, float* __restrict__ y,
-                                                               uint32_t in_dim, uint32_t rows, uint32_t row_bytes) {
-  constexpr uint32_t BS = 34, NDW = 9;
-  extern __shared__ __align__(16) float xs[];
+struct WvArgs {
+  const uint8_t* w;
+  const float* x;
+  float* y;
+  uint32_t in_dim, rows, row_bytes;
+  uint32_t region;  // LDS bytes per wavefront: an item's bytes + 16, rounded to 16
+  uint32_t nch;     // items (chunks) per row
+  uint32_t cblk;    // blocks per chunk; a multiple of 16 when nch > 1
+};
+
+template <uint32_t T>
+struct WvFmt;
+template <>
+struct WvFmt<T_Q8_0> {
+  static constexpr uint32_t BS = 34;
+  // x of lane q of the block whose x starts at xb
+  __device__ static void xload(const float* xb, uint32_t q, float4& x0, float4& x1) {
+    x0 = *reinterpret_cast<const float4*>(xb + 8u * q);
+    x1 = *reinterpret_cast<const float4*>(xb + 8u * q + 4u);
+  }
+  // lane q's share of the block at LDS byte o
+  __device__ static float dot(const uint8_t* wr, uint32_t o, const float4& x0, const float4& x1, uint32_t q) {
+    const uint32_t h = *reinterpret_cast<const uint16_t*>(wr + o);
+    const uint32_t oc = o + 2u + 8u * q;
+    const uint32_t* p = reinterpret_cast<const uint32_t*>(wr + (oc & ~3u));
+    const uint32_t d0 = p[0], d1 = p[1], d2 = p[2], sh = oc & 3u;
+    const uint32_t c0 = __builtin_amdgcn_alignbyte(d1, d0, sh), c1 = __builtin_amdgcn_alignbyte(d2, d1, sh);
+    float t = 0.f;
+    t = fmaf(rf_sb(c0, 0), x0.x, t); t = fmaf(rf_sb(c0, 1), x0.y, t);
+    t = fmaf(rf_sb(c0, 2), x0.z, t); t = fmaf(rf_sb(c0, 3), x0.w, t);
+    t = fmaf(rf_sb(c1, 0), x1.x, t); t = fmaf(rf_sb(c1, 1), x1.y, t);
+    t = fmaf(rf_sb(c1, 2), x1.z, t); t = fmaf(rf_sb(c1, 3), x1.w, t);
+    return rf_half_to_float_fast(h) * t;
+  }
+};
+template <>
+struct WvFmt<T_Q4_0> {
+  static constexpr uint32_t BS = 18;
+  __device__ static void xload(const float* xb, uint32_t q, float4& x0, float4& x1) {
+    x0 = *reinterpret_cast<const float4*>(xb + 4u * q);
+    x1 = *reinterpret_cast<const float4*>(xb + 16u + 4u * q);
+  }
+  __device__ static float dot(const uint8_t* wr, uint32_t o, const float4& x0, const float4& x1, uint32_t q) {
+    const uint32_t h = *reinterpret_cast<const uint16_t*>(wr + o);
+    const uint32_t oc = o + 2u + 4u * q;
+    const uint32_t* p = reinterpret_cast<const uint32_t*>(wr + (oc & ~3u));
+    const uint32_t c = __builtin_amdgcn_alignbyte(p[1], p[0], oc & 3u);
+    // (nibble - 8) moved to the top of each byte: the int8 16 (nibble - 8)
+    const uint32_t lo = rf_opaque(rf_top_signed(c, 4)), hi = rf_opaque(rf_top_signed(c >> 4, 4));
+    float t = 0.f;
+    t = fmaf(rf_sb(lo, 0), x0.x, t); t = fmaf(rf_sb(lo, 1), x0.y, t);
+    t = fmaf(rf_sb(lo, 2), x0.z, t); t = fmaf(rf_sb(lo, 3), x0.w, t);
+    t = fmaf(rf_sb(hi, 0), x1.x, t); t = fmaf(rf_sb(hi, 1), x1.y, t);
+    t = fmaf(rf_sb(hi, 2), x1.z, t); t = fmaf(rf_sb(hi, 3), x1.w, t);
+    return rf_half_to_float_fast(h) * (t * 0.0625f);
+  }
+};
+
+// NQ 16-byte loads per lane and item (NQ * 1024 >= the item's bytes).  XR:
+// rows of at most 4096 inputs (one item each) with each lane's x of all
+// eight 16-block steps held in registers, read from LDS once per wavefront;
+// otherwise x is read from LDS per step.
+template <uint32_t T, int NQ, bool XR>
+__global__ __launch_bounds__(512) void matvec_wave(WvArgs a) {
+  constexpr uint32_t BS = WvFmt<T>::BS;
+  constexpr int XS = XR ? 8 : 1;
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  extern __shared__ __align__(16) uint8_t mvw_sm[];
+  const float* xs = reinterpret_cast<const float*>(mvw_sm);
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const uint32_t nblk = in_dim / 32u;
-  const uint32_t stride = gridDim.x * MVL_WAVES;
-  uint32_t dw[NB][BPL][NDW];
-  auto fetch = [&](uint32_t (&d)[BPL][NDW], uint32_t r) {
-    const bool live = r < rows;  // wave-uniform: past the last row every load returns zeros
-    const MvRsrc rs = __builtin_amdgcn_make_buffer_rsrc((void*)(w + (size_t)(live ? r : 0u) * row_bytes), 0,
-                                                        live ? (int32_t)row_bytes : 0, MV_RSRC_WORD3);
+  const uint32_t nw = blockDim.x >> 6;
+  uint8_t* wr = mvw_sm + a.in_dim * 4u + wave * a.region;
+  const uint32_t G = gridDim.x * nw;
+  const uint32_t chb = a.cblk * BS;  // bytes of a full chunk
+  auto item_bytes = [&](uint32_t c) { return c + 1u < a.nch ? chb : a.row_bytes - c * chb; };
+  u32x4 buf[NQ];
+  auto fetch = [&](uint32_t r, uint32_t c) {
+    const bool live = r < a.rows;  // wave-uniform; past the last row every load returns zeros
+    const uint8_t* base = a.w + (live ? (uint64_t)r * a.row_bytes + (uint64_t)c * chb : 0u);
+    const MvRsrc rs = __builtin_amdgcn_make_buffer_rsrc((void*)base, 0, live ? (int32_t)item_bytes(c) : 0,
+                                                        MV_RSRC_WORD3);
 #pragma unroll
-    for (int k = 0; k < BPL; ++k) {
-      const uint32_t off = (BS * (lane + 64u * k)) & ~3u;
-      const auto v0 = __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0);
-      const auto v1 = __builtin_amdgcn_raw_buffer_load_b128(rs, off + 16u, 0, 0);
-      d[k][0] = v0[0]; d[k][1] = v0[1]; d[k][2] = v0[2]; d[k][3] = v0[3];
-      d[k][4] = v1[0]; d[k][5] = v1[1]; d[k][6] = v1[2]; d[k][7] = v1[3];
-      d[k][8] = __builtin_amdgcn_raw_buffer_load_b32(rs, off + 32u, 0, 0);
-    }
+    for (int i = 0; i < NQ; ++i)  // streamed once: non-temporal
+      buf[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, 16u * (lane + 64u * i), 0, 2);
   };
-  uint32_t r = blockIdx.x * MVL_WAVES + wave;
-#pragma unroll
-  for (int nb = 0; nb < NB; ++nb) fetch(dw[nb], r + (uint32_t)nb * stride);
-  // x into LDS behind the first rows' loads
-  for (uint32_t i = tid; i < in_dim / 4u; i += 64u * MVL_WAVES)
-    reinterpret_cast<float4*>(xs)[i] = reinterpret_cast<const float4*>(x)[i];
+  // item k of this wavefront: row r0 + (k / nch) G, chunk k % nch
+  uint32_t r = blockIdx.x * nw + wave, c = 0;
+  fetch(r, c);
+  for (uint32_t i = tid; i < a.in_dim / 4u; i += blockDim.x)
+    reinterpret_cast<float4*>(mvw_sm)[i] = reinterpret_cast<const float4*>(a.x)[i];
   __syncthreads();
-  auto finish = [&](const uint32_t (&d)[BPL][NDW], uint32_t rr) {
-    float acc = 0.f;
+  const uint32_t q = lane & 3u, bl = lane >> 2;
+  float4 xr0[XS], xr1[XS];
+  if constexpr (XR) {
+    const uint32_t last = a.in_dim / 32u - 1u;
 #pragma unroll
-    for (int k = 0; k < BPL; ++k) {
-      const uint32_t b = lane + 64u * k;
-      if (b < nblk) {
-        const bool odd = (b & 1u) != 0u;
-        const uint32_t h = odd ? d[k][0] >> 16 : d[k][0] & 0xFFFFu;
-        const float* xb = xs + 32u * b;
-        float s = 0.f;
+    for (int k = 0; k < XS; ++k) WvFmt<T>::xload(xs + 32u * min(16u * k + bl, last), q, xr0[k], xr1[k]);
+  }
+  float acc = 0.f;
+  while (r < a.rows) {
+    const uint32_t nb = item_bytes(c);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const uint32_t c = odd ? d[k][i + 1] : __builtin_amdgcn_alignbyte(d[k][i + 1], d[k][i], 2);
-          const float4 xv = *reinterpret_cast<const float4*>(xb + 4 * i);
-          s = fmaf(rf_sb(c, 0), xv.x, s);
-          s = fmaf(rf_sb(c, 1), xv.y, s);
-          s = fmaf(rf_sb(c, 2), xv.z, s);
-          s = fmaf(rf_sb(c, 3), xv.w, s);
-        }
-        acc += rf_half_to_float_fast(h) * s;
+    for (int i = 0; i < NQ; ++i) {
+      const uint32_t o = 16u * (lane + 64u * i);
+      if (o < nb) *reinterpret_cast<u32x4*>(wr + o) = buf[i];
+    }
+    const uint32_t rn = c + 1u < a.nch ? r : r + G, cn = c + 1u < a.nch ? c + 1u : 0u;
+    fetch(rn, cn);
+    const uint32_t nbk = nb / BS;
+    if constexpr (XR) {
+#pragma unroll
+      for (int k = 0; k < XS; ++k) {
+        const uint32_t bk = 16u * k + bl;
+        if (16u * k < nbk && bk < nbk) acc += WvFmt<T>::dot(wr, BS * bk, xr0[k], xr1[k], q);
+      }
+    } else {
+      const uint32_t b0 = c * a.cblk, nfull = nbk & ~15u;
+#pragma unroll 2
+      for (uint32_t j = 0; j < nfull; j += 16u) {
+        WvFmt<T>::xload(xs + 32u * (b0 + j + bl), q, xr0[0], xr1[0]);
+        acc += WvFmt<T>::dot(wr, BS * (j + bl), xr0[0], xr1[0], q);
+      }
+      const uint32_t bk = nfull + bl;
+      if (nfull < nbk && bk < nbk) {
+        WvFmt<T>::xload(xs + 32u * (b0 + bk), q, xr0[0], xr1[0]);
+        acc += WvFmt<T>::dot(wr, BS * bk, xr0[0], xr1[0], q);
       }
     }
-    acc = rf_wave_sum(acc);
-    if (lane == 0 && rr < rows) y[rr] = acc;
-  };
-  for (; r < rows; r += (uint32_t)NB * stride) {
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
-      finish(dw[nb], r + (uint32_t)nb * stride);
-      fetch(dw[nb], r + (uint32_t)(nb + NB) * stride);
+    if (cn == 0u) {
+      const float v = rf_wave_sum(acc);
+      if (lane == 0) a.y[r] = v;
+      acc = 0.f;
     }
+    r = rn;
+    c = cn;
   }
 }
 
-// Whether the lane kernel takes this launch: Q8_0 rows of an even block
-// count (dword-aligned rows) and at most MVL_MAX_IN inputs, a dword-aligned
-// base and 16-byte aligned x.
-static bool lanes_ok(uint32_t t, uint64_t in_dim, const void* w, const float* x) {
-  if (t != T_Q8_0 || in_dim == 0 || in_dim % 64 != 0 || in_dim > MVL_MAX_IN) return false;
-  return (reinterpret_cast<uintptr_t>(w) & 3u) == 0 && aligned16(x);
+// Whether the wave-staged kernel takes this launch: Q8_0 / Q4_0 rows of an
+// even block count (dword-aligned rows), a dword-aligned base, 16-byte
+// aligned x, and x plus four wavefronts' regions within the LDS.
+static bool wave_ok(uint32_t t, uint64_t in_dim, const void* w, const float* x) {
+  if ((t != T_Q8_0 && t != T_Q4_0) || in_dim == 0 || in_dim % 64 != 0) return false;
+  if ((reinterpret_cast<uintptr_t>(w) & 3u) != 0 || !aligned16(x)) return false;
+  return in_dim * 4u + 4u * (MVW_CHUNK + 16u) <= MVW_LDS;
 }
 
-static int g_lanes_enabled = 1;
-void set_matvec_lanes(bool on) { g_lanes_enabled = on ? 1 : 0; }
-bool matvec_lanes_on() { return g_lanes_enabled != 0; }
+static int g_wave_enabled = 1;
+void set_matvec_wave(bool on) { g_wave_enabled = on ? 1 : 0; }
+bool matvec_wave_on() { return g_wave_enabled != 0; }
 
-template <int BPL>
-static hipError_t launch_lanes_b(const MvSegDesc& s, const float* x, uint64_t in_dim, hipStream_t st) {
-  constexpr int NB = 2;
+// Resident workgroups per CU for (kernel, threads, LDS), cached; 0 when the
+// query would run inside a capture.
+template <uint32_t T, int NQ, bool XR>
+static uint32_t wave_occupancy(uint32_t threads, uint32_t lds, hipStream_t st) {
   static std::mutex mu;
-  static uint32_t occ = 0;
-  const uint32_t lds = (uint32_t)in_dim * 4u;
-  {
-    std::lock_guard<std::mutex> lock(mu);
-    if (occ == 0) {
-      if (setup_outside_capture(st) != hipSuccess) return hipErrorStreamCaptureUnsupported;
-      int n = 0;
-      if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, matvec_lanes<BPL, NB>, 64 * MVL_WAVES,
-                                                       (size_t)MVL_MAX_IN * 4u) != hipSuccess || n < 1)
-        n = 1;
-      occ = (uint32_t)n;
-    }
+  std::lock_guard<std::mutex> lock(mu);
+  static uint32_t key[16] = {0}, val[16] = {0};
+  static bool attr = false;
+  const uint32_t k = threads << 20 | lds;
+  for (int i = 0; i < 16; ++i)
+    if (key[i] == k) return val[i];
+  if (setup_outside_capture(st) != hipSuccess) return 0;
+  if (!attr) {
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(matvec_wave<T, NQ, XR>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)MVW_LDS) != hipSuccess)
+      return 0;
+    attr = true;
   }
-  const uint64_t rows = s.rows;
-  const uint64_t want = (rows + MVL_WAVES * NB - 1) / (MVL_WAVES * NB);  // about NB rows per wavefront
-  const uint64_t cap = (uint64_t)cu_count() * occ;
-  const uint32_t grid = (uint32_t)std::max<uint64_t>(1, std::min(want, cap));
-  const uint32_t row_bytes = (uint32_t)(in_dim / 32u * 34u);
-  RF_KLAUNCH((matvec_lanes<BPL, NB>), dim3(grid), dim3(64 * MVL_WAVES), lds, st, static_cast<const uint8_t*>(s.w),
-             x, s.y, (uint32_t)in_dim, (uint32_t)rows, row_bytes);
+  int n = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, matvec_wave<T, NQ, XR>, (int)threads, (size_t)lds) !=
+          hipSuccess || n < 1)
+    n = 1;
+  for (int i = 0; i < 16; ++i)
+    if (key[i] == 0) {
+      key[i] = k;
+      val[i] = (uint32_t)n;
+      break;
+    }
+  return (uint32_t)n;
+}
+
+template <uint32_t T, int NQ, bool XR>
+static hipError_t launch_wave_q(const WvArgs& a, hipStream_t st) {
+  const uint32_t ncu = (uint32_t)cu_count();
+  // eight wavefronts per workgroup unless there are fewer rows than that
+  // per CU; whole workgroups per CU, about two rows per wavefront
+  uint32_t nw = a.rows >= 8u * ncu ? 8u : 4u;
+  uint32_t lds = a.in_dim * 4u + nw * a.region;
+  if (lds > MVW_LDS) {
+    nw = 4u;
+    lds = a.in_dim * 4u + nw * a.region;
+  }
+  const uint32_t occ = wave_occupancy<T, NQ, XR>(64u * nw, lds, st);
+  if (occ == 0) return hipErrorStreamCaptureUnsupported;
+  uint32_t grid;
+  if ((uint64_t)a.rows <= (uint64_t)nw * ncu) {
+    grid = (a.rows + nw - 1) / nw;
+  } else {
+    const uint64_t k = ((uint64_t)a.rows + 2ull * nw * ncu - 1) / (2ull * nw * ncu);
+    grid = (uint32_t)(std::min<uint64_t>(k, occ) * ncu);
+  }
+  RF_KLAUNCH((matvec_wave<T, NQ, XR>), dim3(grid), dim3(64u * nw), lds, st, a);
   return hipGetLastError();
 }
 
-static hipError_t launch_lanes(const MvSegDesc& s, const float* x, uint64_t in_dim, hipStream_t st) {
-  return in_dim <= 2048 ? launch_lanes_b<1>(s, x, in_dim, st) : launch_lanes_b<2>(s, x, in_dim, st);
+// x in registers pays for its per-wavefront load from about three rows per
+// wavefront of an eight-wavefront workgroup per CU on (Q8_0 14336 x 4096:
+// 13.3 against 15.5 us; Q4_0 4096 x 4096, two rows per wavefront: 5.8
+// against 5.5 us).
+constexpr uint32_t MVW_XR_ROWS_PER_WAVE = 3;
+
+template <uint32_t T>
+static hipError_t launch_wave_t(const WvArgs& a, hipStream_t st) {
+  const uint32_t nq = (std::min(a.row_bytes, a.cblk * WvFmt<T>::BS) + 1023u) / 1024u;
+  if (a.nch == 1 && a.in_dim <= 4096 && a.rows >= MVW_XR_ROWS_PER_WAVE * 8u * (uint32_t)cu_count()) {
+    switch (nq) {
+      case 1: return launch_wave_q<T, 1, true>(a, st);
+      case 2: return launch_wave_q<T, 2, true>(a, st);
+      case 3: return launch_wave_q<T, 3, true>(a, st);
+      case 4: return launch_wave_q<T, 4, true>(a, st);
+      default: return launch_wave_q<T, 5, true>(a, st);
+    }
+  }
+  switch (nq) {
+    case 1: return launch_wave_q<T, 1, false>(a, st);
+    case 2: return launch_wave_q<T, 2, false>(a, st);
+    case 3: return launch_wave_q<T, 3, false>(a, st);
+    case 4: return launch_wave_q<T, 4, false>(a, st);
+    case 5: return launch_wave_q<T, 5, false>(a, st);
+    case 6: return launch_wave_q<T, 6, false>(a, st);
+    default: return launch_wave_q<T, 8, false>(a, st);
+  }
+}
+
+static hipError_t launch_wave(uint32_t t, const MvSegDesc& s, const float* x, uint64_t in_dim, hipStream_t st) {
+  const uint32_t bs = t == T_Q8_0 ? 34u : 18u;
+  const uint32_t nblk = (uint32_t)(in_dim / 32u);
+  WvArgs a{};
+  a.w = static_cast<const uint8_t*>(s.w);
+  a.x = x;
+  a.y = s.y;
+  a.in_dim = (uint32_t)in_dim;
+  a.rows = (uint32_t)s.rows;
+  a.row_bytes = nblk * bs;
+  if (a.row_bytes <= MVW_CHUNK) {
+    a.nch = 1;
+    a.cblk = nblk;
+  } else {  // chunks of about equal size, whole 16-block steps
+    const uint32_t n = (a.row_bytes + MVW_CHUNK - 1) / MVW_CHUNK;
+    a.cblk = ((nblk + n - 1) / n + 15u) / 16u * 16u;
+    if (a.cblk * bs > MVW_CHUNK) a.cblk = MVW_CHUNK / bs / 16u * 16u;
+    a.nch = (nblk + a.cblk - 1) / a.cblk;
+  }
+  a.region = (std::min(a.row_bytes, a.cblk * bs) + 16u + 15u) & ~15u;
+  return t == T_Q8_0 ? launch_wave_t<T_Q8_0>(a, st) : launch_wave_t<T_Q4_0>(a, st);
 }
 
 template <int EPI>
@@ -725,9 +877,9 @@ hipError_t launch_matvec_segments(uint32_t t, const MvSegDesc* segs, int nseg, c
     }
     return hipSuccess;
   }
-  if (g_lanes_enabled && epi == EPI_STORE && norm_w == nullptr && nseg == 1 && segs[0].rows > 0 &&
-      segs[0].rows <= 0xFFFFFFFFull && lanes_ok(t, in_dim, segs[0].w, x))
-    return launch_lanes(segs[0], x, in_dim, st);
+  if (g_wave_enabled && epi == EPI_STORE && norm_w == nullptr && nseg == 1 && segs[0].rows > 0 &&
+      segs[0].rows <= 0x7FFFFFFFull && wave_ok(t, in_dim, segs[0].w, x))
+    return launch_wave(t, segs[0], x, in_dim, st);
   bool stream = p.stream && g_stream_enabled;
   for (int i = 0; i < nseg && stream; ++i)
     stream = aligned16(segs[i].w) && (!dual || aligned16(segs[i].w_up));

@@ -1313,9 +1313,9 @@ uint32_t rf_tune_matvec_tile_bytes(uint32_t bytes) {
 int32_t rf_tune_matvec_kernel(int32_t mode) {
   if (mode >= 0 && mode <= 2) {
     set_matvec_stream(mode >= 1);
-    set_matvec_lanes(mode == 2);
+    set_matvec_wave(mode == 2);
   }
-  return matvec_lanes_on() ? 2 : (matvec_stream() ? 1 : 0);
+  return matvec_wave_on() ? 2 : (matvec_stream() ? 1 : 0);
 }
 
 int32_t rf_tune_packed_inflight(int32_t mode) {

@@ -140,7 +140,7 @@ def _check_matvec(ctx, orc, t, out_dim, in_dim, seed, row_start=0, row_count=Non
     return err
 
 
-@pytest.fixture(params=[2, 1, 0], ids=["lanes", "stream", "oneshot"])
+@pytest.fixture(params=[2, 1, 0], ids=["wave", "stream", "oneshot"])
 def kernel_mode(request):
     rf = _rf()
     old = rf.tune_matvec_kernel(-1)
@@ -149,22 +149,28 @@ def kernel_mode(request):
     rf.tune_matvec_kernel(old)
 
 
-@pytest.mark.parametrize("out_dim,in_dim", [(1, 64), (7, 128), (513, 4096), (130, 2048), (33, 4096), (4096, 4096)])
-def test_matvec_lane_kernel_shapes(ctx, orc, out_dim, in_dim):
-    """The register-realigning lane kernel (plain Q8_0 rf_matvec of up to
-    4096 inputs) at one and two blocks per lane, row counts that leave
-    wavefronts idle, and the even / odd block alignments of every lane."""
+@pytest.mark.parametrize("t", [Q8_0, Q4_0])
+@pytest.mark.parametrize("out_dim,in_dim", [(1, 64), (7, 128), (513, 4096), (130, 2048), (33, 4096), (4096, 4096),
+                                            (6000, 1024), (7000, 4096), (6200, 1088), (300, 9024), (64, 14336),
+                                            (41, 16448)])
+def test_matvec_wave_kernel_shapes(ctx, orc, t, out_dim, in_dim):
+    """The wave-staged kernel (plain Q8_0 / Q4_0 rf_matvec): rows that leave
+    wavefronts of a workgroup idle, four- and eight-wavefront workgroups and
+    more than one row per wavefront (6000 rows), x held in registers (7000
+    and 6200 rows, the second with a partial 16-block step), partial steps
+    with x read from LDS, and rows longer than one 8 KiB item (Q8_0 at 9024
+    and 14336 inputs, Q4_0 at 16448: two chunks per row, the last one
+    partial)."""
     rf = _rf()
     assert rf.tune_matvec_kernel(-1) == 2
-    _check_matvec(ctx, orc, Q8_0, out_dim, in_dim, 1500 + out_dim + in_dim)
+    _check_matvec(ctx, orc, t, out_dim, in_dim, 1500 + out_dim + in_dim + t)
 
 
 @pytest.mark.parametrize("t", [Q8_0, Q4_0])
-def test_matvec_lane_kernel_offsets(ctx, orc, t):
+def test_matvec_wave_kernel_offsets(ctx, orc, t):
     """Row ranges (the base moves by whole rows, still dword aligned), a
-    weight base 4 bytes past an aligned allocation (Q8_0: lane kernel) and 2
-    bytes past (not dword aligned: the other kernels); Q4_0 takes the other
-    kernels throughout."""
+    weight base 4 bytes past an aligned allocation (the wave-staged kernel)
+    and 2 bytes past (not dword aligned: the other kernels)."""
     for i, (rs, rc, w_off) in enumerate(((37, 100, 0), (0, None, 4), (5, 11, 2), (299, 1, 4))):
         _check_matvec(ctx, orc, t, 300, 4096, 1600 + i, row_start=rs, row_count=rc, w_off=w_off)
 
