@@ -568,10 +568,11 @@ int32_t rf_graph_destroy(rf_ctx *ctx, void *graph);
 
 /* LDS bytes per one-shot matvec tile (4096..61440); returns the value in effect. */
 uint32_t rf_tune_matvec_tile_bytes(uint32_t bytes);
-/* Matvec kernel family for GGUF bytes: 2 = plain Q8_0 / Q4_0 matvecs
- * (rf_matvec, no fused norm or epilogue; rows of an even block count, 16-byte
- * aligned x, 4-byte aligned weights, at most about 32000 inputs) stage each
- * row per wavefront in LDS through 16-byte loads, the rest as 1 (default);
+/* Matvec kernel family for GGUF bytes: 2 = plain Q8_0 / Q4_0 / Q6_K
+ * matvecs and Q4_K ones of up to 4096 inputs (rf_matvec, no fused norm or
+ * epilogue; rows of an even block count, 16-byte aligned x, 4-byte aligned
+ * weights, at most about 29000 inputs) stage each row per wavefront in LDS
+ * through 16-byte loads, the rest as 1 (default);
  * 1 = persistent streaming kernel where rows and bases are
  * 16-byte aligned, LDS-staged row tiles; 0 = one-shot tile kernel
  * everywhere; other values only query.  Returns the mode in effect

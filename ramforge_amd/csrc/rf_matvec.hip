@@ -551,22 +551,27 @@ static hipError_t launch_stream_t(const MvArgs& a, uint32_t tiles, const MvPlan&
   return hipGetLastError();
 }
 
-// ------------------------------------------------ wave-staged kernel (Q8_0, Q4_0)
+// ------------------------------------------------ wave-staged kernel (Q8_0, Q4_0, Q4_K, Q6_K)
 // GGUF rows staged per wavefront: each wavefront owns whole rows (row i,
 // i + G, ... for G wavefronts in the grid), loads the bytes of its next row
 // (or of its next chunk of at most 8 KiB, for longer rows) with 16-byte
 // loads that are contiguous across lanes, writes them into its own LDS
-// region and reads the blocks back from there, four lanes per block.  The
-// next item's loads are in flight while the current one is summed; no
-// barrier after the prologue (a wavefront's LDS writes and reads complete in
-// order).  x sits in LDS once per workgroup.
-//   Q8_0: lane q of a block takes codes 8q..8q+7 (bytes 2+8q.., realigned
+// region and reads the blocks back from there.  The next item's loads are in
+// flight while the current one is summed; no barrier after the prologue (a
+// wavefront's LDS writes and reads complete in order).  x sits in LDS once
+// per workgroup.  Each lane takes eight weights of a block per step: four
+// lanes per 32-element block (16 blocks per step), 32 lanes per 256-element
+// super-block (2 per step).
+//   Q8_0: lane p of a block takes codes 8p..8p+7 (bytes 2+8p.., realigned
 //   with v_alignbyte; a block starts 0 or 2 bytes into a dword) times
-//   x[8q..8q+7]; Q4_0: bytes 2+4q..2+4q+3, low nibbles times x[4q..4q+3],
-//   high nibbles times x[16+4q..16+4q+3].
+//   x[8p..8p+7]; Q4_0: bytes 2+4p..2+4p+3, low nibbles times x[4p..4p+3],
+//   high nibbles times x[16+4p..16+4p+3]; Q4_K / Q6_K: elements 8p..8p+7 of
+//   the super-block, with the sub-block's scale (and min).
 // Signed codes times x, the block scale once per block and lane, as the
 // other kernels (quant.rs:977-1029 up to the order of the sums); a code of 0
-// meets an infinite x as the reference's 0 * inf = NaN term does.
+// meets an infinite x as the reference's 0 * inf = NaN term does.  Q4_K
+// subtracts dmin m sum(x) of its eight elements; with an infinity or NaN in
+// x it takes the kind of the reference's terms instead (unit_kinds).
 // Timed under graph replay with >= 1.2 GiB of rotated copies against the
 // lane kernel it replaced (registers only, lane = block, 34-byte strided
 // loads): Q8_0 4096 x 4096 6.4 against 8.6 us, 1024 x 4096 4.0 against 5.3,
@@ -577,7 +582,7 @@ static hipError_t launch_stream_t(const MvArgs& a, uint32_t tiles, const MvPlan&
 typedef __amdgpu_buffer_rsrc_t MvRsrc;
 constexpr int MV_RSRC_WORD3 = 0x00020000;
 constexpr uint32_t MVW_CHUNK = 8192;  // most bytes one item stages
-constexpr uint32_t MVW_LDS = 160 * 1024;
+constexpr uint32_t MVW_LDS = 160 * 1024 - 256;  // dynamic LDS; the rest for static use (__syncthreads_or)
 
 struct WvArgs {
   const uint8_t* w;
@@ -586,71 +591,216 @@ struct WvArgs {
   uint32_t in_dim, rows, row_bytes;
   uint32_t region;  // LDS bytes per wavefront: an item's bytes + 16, rounded to 16
   uint32_t nch;     // items (chunks) per row
-  uint32_t cblk;    // blocks per chunk; a multiple of 16 when nch > 1
+  uint32_t cblk;    // blocks per chunk; a multiple of the blocks per step when nch > 1
 };
 
+// x in LDS: element e at float e + 4 (e / 64), so that the 16-byte reads of
+// lanes 16 or 32 floats apart fall on different banks.
+__device__ __forceinline__ uint32_t wv_xi(uint32_t e) { return e + ((e >> 6) << 2); }
+// LDS bytes of x; min-term formats also keep the sum of every 16 elements
+// after it.
+__host__ __device__ constexpr uint32_t wv_x_bytes(uint32_t in_dim, bool sums) {
+  return in_dim * 4u + (in_dim / 64u) * 16u + (sums ? in_dim / 16u * 4u : 0u);
+}
+
+// x values of one lane for one block: N float4.
+template <int N>
+struct WvX {
+  float4 v[N];
+};
+
+// x of lane p when the lane takes elements 4N p .. 4N p + 4N - 1 of the block
+// whose first element is e0.
+template <int N>
+__device__ __forceinline__ void wv_xload(const float* xs, uint32_t e0, uint32_t p, WvX<N>& x) {
+#pragma unroll
+  for (int i = 0; i < N; ++i) x.v[i] = *reinterpret_cast<const float4*>(xs + wv_xi(e0 + 4u * (N * p + i)));
+}
+
+template <int N>
+__device__ __forceinline__ bool wv_finite(const WvX<N>& x) {
+  bool ok = true;
+#pragma unroll
+  for (int i = 0; i < N; ++i)
+    ok = ok && fabsf(x.v[i].x) <= 3.40282347e38f && fabsf(x.v[i].y) <= 3.40282347e38f &&
+         fabsf(x.v[i].z) <= 3.40282347e38f && fabsf(x.v[i].w) <= 3.40282347e38f;
+  return ok;
+}
+
+template <int N>
+__device__ __forceinline__ float wv_xsum(const WvX<N>& x) {
+  float t = 0.f;
+#pragma unroll
+  for (int i = 0; i < N; ++i) t += (x.v[i].x + x.v[i].y) + (x.v[i].z + x.v[i].w);
+  return t;
+}
+
+// Kind of the terms w_i x_i (NaN, +inf, -inf, or 0 when all are finite).
+template <int N>
+__device__ __forceinline__ float wv_kinds(const float (&w)[4 * N], const WvX<N>& x) {
+  bool nan = false, pinf = false, ninf = false;
+#pragma unroll
+  for (int i = 0; i < 4 * N; ++i) {
+    const float4& q = x.v[i / 4];
+    const float xv = (i & 3) == 0 ? q.x : ((i & 3) == 1 ? q.y : ((i & 3) == 2 ? q.z : q.w));
+    const float t = w[i] * xv;
+    nan = nan || t != t;
+    pinf = pinf || t == __builtin_inff();
+    ninf = ninf || t == -__builtin_inff();
+  }
+  if (nan || (pinf && ninf)) return __builtin_nanf("");
+  return pinf ? __builtin_inff() : (ninf ? -__builtin_inff() : 0.f);
+}
+
+// sum over four signed bytes of c times x
+__device__ __forceinline__ float wv_dot4s(uint32_t c, const float4& x, float t) {
+  t = fmaf(rf_sb(c, 0), x.x, t); t = fmaf(rf_sb(c, 1), x.y, t);
+  t = fmaf(rf_sb(c, 2), x.z, t); t = fmaf(rf_sb(c, 3), x.w, t);
+  return t;
+}
+// sum over four unsigned bytes of n times x
+__device__ __forceinline__ float wv_dot4u(uint32_t n, const float4& x, float t) {
+  t = fmaf(rf_ub(n, 0), x.x, t); t = fmaf(rf_ub(n, 1), x.y, t);
+  t = fmaf(rf_ub(n, 2), x.z, t); t = fmaf(rf_ub(n, 3), x.w, t);
+  return t;
+}
+
+// Per format: QK elements and BS bytes per block, EPL elements per lane
+// (QK / EPL lanes per block), MIN for a min term; xload, dot (and kinds for
+// MIN) of lane p's share of the block at LDS byte o.
 template <uint32_t T>
 struct WvFmt;
 template <>
 struct WvFmt<T_Q8_0> {
-  static constexpr uint32_t BS = 34;
-  // x of lane q of the block whose x starts at xb
-  __device__ static void xload(const float* xb, uint32_t q, float4& x0, float4& x1) {
-    x0 = *reinterpret_cast<const float4*>(xb + 8u * q);
-    x1 = *reinterpret_cast<const float4*>(xb + 8u * q + 4u);
-  }
-  // lane q's share of the block at LDS byte o
-  __device__ static float dot(const uint8_t* wr, uint32_t o, const float4& x0, const float4& x1, uint32_t q) {
+  static constexpr uint32_t BS = 34, QK = 32, EPL = 8;
+  static constexpr bool MIN = false;
+  using X = WvX<2>;
+  __device__ static void xload(const float* xs, uint32_t e0, uint32_t p, X& x) { wv_xload<2>(xs, e0, p, x); }
+  __device__ static float dot(const uint8_t* wr, uint32_t o, const X& x, uint32_t p, float) {
     const uint32_t h = *reinterpret_cast<const uint16_t*>(wr + o);
-    const uint32_t oc = o + 2u + 8u * q;
-    const uint32_t* p = reinterpret_cast<const uint32_t*>(wr + (oc & ~3u));
-    const uint32_t d0 = p[0], d1 = p[1], d2 = p[2], sh = oc & 3u;
-    const uint32_t c0 = __builtin_amdgcn_alignbyte(d1, d0, sh), c1 = __builtin_amdgcn_alignbyte(d2, d1, sh);
-    float t = 0.f;
-    t = fmaf(rf_sb(c0, 0), x0.x, t); t = fmaf(rf_sb(c0, 1), x0.y, t);
-    t = fmaf(rf_sb(c0, 2), x0.z, t); t = fmaf(rf_sb(c0, 3), x0.w, t);
-    t = fmaf(rf_sb(c1, 0), x1.x, t); t = fmaf(rf_sb(c1, 1), x1.y, t);
-    t = fmaf(rf_sb(c1, 2), x1.z, t); t = fmaf(rf_sb(c1, 3), x1.w, t);
+    const uint32_t oc = o + 2u + 8u * p;  // a block starts 0 or 2 bytes into a dword
+    const uint32_t* w = reinterpret_cast<const uint32_t*>(wr + (oc & ~3u));
+    const uint32_t d0 = w[0], d1 = w[1], d2 = w[2], sh = oc & 3u;
+    const float t = wv_dot4s(__builtin_amdgcn_alignbyte(d2, d1, sh), x.v[1],
+                             wv_dot4s(__builtin_amdgcn_alignbyte(d1, d0, sh), x.v[0], 0.f));
     return rf_half_to_float_fast(h) * t;
   }
 };
 template <>
 struct WvFmt<T_Q4_0> {
-  static constexpr uint32_t BS = 18;
-  __device__ static void xload(const float* xb, uint32_t q, float4& x0, float4& x1) {
-    x0 = *reinterpret_cast<const float4*>(xb + 4u * q);
-    x1 = *reinterpret_cast<const float4*>(xb + 16u + 4u * q);
+  static constexpr uint32_t BS = 18, QK = 32, EPL = 8;
+  static constexpr bool MIN = false;
+  using X = WvX<2>;
+  // lane p: x[4p..4p+3] (low nibbles of bytes 4p..) and x[16+4p..] (high)
+  __device__ static void xload(const float* xs, uint32_t e0, uint32_t p, X& x) {
+    x.v[0] = *reinterpret_cast<const float4*>(xs + wv_xi(e0 + 4u * p));
+    x.v[1] = *reinterpret_cast<const float4*>(xs + wv_xi(e0 + 16u + 4u * p));
   }
-  __device__ static float dot(const uint8_t* wr, uint32_t o, const float4& x0, const float4& x1, uint32_t q) {
+  __device__ static float dot(const uint8_t* wr, uint32_t o, const X& x, uint32_t p, float) {
     const uint32_t h = *reinterpret_cast<const uint16_t*>(wr + o);
-    const uint32_t oc = o + 2u + 4u * q;
-    const uint32_t* p = reinterpret_cast<const uint32_t*>(wr + (oc & ~3u));
-    const uint32_t c = __builtin_amdgcn_alignbyte(p[1], p[0], oc & 3u);
+    const uint32_t oc = o + 2u + 4u * p;
+    const uint32_t* w = reinterpret_cast<const uint32_t*>(wr + (oc & ~3u));
+    const uint32_t c = __builtin_amdgcn_alignbyte(w[1], w[0], oc & 3u);
     // (nibble - 8) moved to the top of each byte: the int8 16 (nibble - 8)
     const uint32_t lo = rf_opaque(rf_top_signed(c, 4)), hi = rf_opaque(rf_top_signed(c >> 4, 4));
+    return rf_half_to_float_fast(h) * (wv_dot4s(hi, x.v[1], wv_dot4s(lo, x.v[0], 0.f)) * 0.0625f);
+  }
+};
+// quant.rs:186-255: d @0, dmin @2, scales[12] @4, qs[128] @16; sub-block s
+// uses qs[32(s/2) + l], low nibble if s even, high if odd; (d*sc)*q - dmin*m.
+// Lane p: sub-block s = p / 2, elements 16(p % 2).. of it (one 16-byte read).
+template <>
+struct WvFmt<T_Q4_K> {
+  static constexpr uint32_t BS = 144, QK = 256, EPL = 16;
+  static constexpr bool MIN = true;
+  using X = WvX<4>;
+  __device__ static void xload(const float* xs, uint32_t e0, uint32_t p, X& x) { wv_xload<4>(xs, e0, p, x); }
+  __device__ static void codes(const uint8_t* wr, uint32_t o, uint32_t p, float& d1, float& m1, uint32_t (&n)[4]) {
+    const uint32_t s = p >> 1;
+    const uint32_t dd = *reinterpret_cast<const uint32_t*>(wr + o);
+    // get_scale_min_k4 (quant.rs:216-226) from the three scale bytes lane s
+    // needs: s < 4: sc = b[s] & 63, m = b[s+4] & 63; else sc = (b[s+4] & 15) |
+    // (b[s-4] >> 6) << 4, m = (b[s+4] >> 4) | (b[s] >> 6) << 4
+    const bool lo4 = s < 4u;
+    const uint8_t* sb = wr + o + 4u;
+    const uint32_t u = sb[lo4 ? s : s + 4u], v = sb[lo4 ? s + 4u : s - 4u], w = sb[s];
+    const uint32_t sc = lo4 ? (u & 63u) : ((u & 15u) | ((v >> 6) << 4));
+    const uint32_t m = lo4 ? (v & 63u) : ((u >> 4) | ((w >> 6) << 4));
+    d1 = rf_half_to_float_fast(dd & 0xFFFFu) * (float)sc;
+    m1 = rf_half_to_float_fast(dd >> 16) * (float)m;
+    const uint4 q = *reinterpret_cast<const uint4*>(wr + o + 16u + 32u * (s >> 1) + 16u * (p & 1u));
+    const uint32_t sh = (s & 1u) * 4u;
+    n[0] = rf_opaque((q.x >> sh) & 0x0F0F0F0Fu);
+    n[1] = rf_opaque((q.y >> sh) & 0x0F0F0F0Fu);
+    n[2] = rf_opaque((q.z >> sh) & 0x0F0F0F0Fu);
+    n[3] = rf_opaque((q.w >> sh) & 0x0F0F0F0Fu);
+  }
+  // xsum: the sum of the lane's sixteen x values
+  __device__ static float dot(const uint8_t* wr, uint32_t o, const X& x, uint32_t p, float xsum) {
+    float d1, m1;
+    uint32_t n[4];
+    codes(wr, o, p, d1, m1, n);
     float t = 0.f;
-    t = fmaf(rf_sb(lo, 0), x0.x, t); t = fmaf(rf_sb(lo, 1), x0.y, t);
-    t = fmaf(rf_sb(lo, 2), x0.z, t); t = fmaf(rf_sb(lo, 3), x0.w, t);
-    t = fmaf(rf_sb(hi, 0), x1.x, t); t = fmaf(rf_sb(hi, 1), x1.y, t);
-    t = fmaf(rf_sb(hi, 2), x1.z, t); t = fmaf(rf_sb(hi, 3), x1.w, t);
-    return rf_half_to_float_fast(h) * (t * 0.0625f);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) t = wv_dot4u(n[i], x.v[i], t);
+    return fmaf(d1, t, -m1 * xsum);
+  }
+  __device__ static float kinds(const uint8_t* wr, uint32_t o, const X& x, uint32_t p) {
+    float d1, m1;
+    uint32_t n[4];
+    codes(wr, o, p, d1, m1, n);
+    float w[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) w[i] = d1 * rf_ub(n[i / 4], i & 3) - m1;
+    return wv_kinds<4>(w, x);
+  }
+};
+// quant.rs:347-407: ql[128] @0, qh[64] @128, scales i8[16] @192, d f16 @208.
+// Element e = 128 hf + 32 k + l: low 4 bits from ql[64hf + 32(k&1) + l]
+// (nibble k>>1), high 2 bits from qh[32hf + l] >> 2k, scale
+// scales[8hf + 2k + l/16]; (d*sc)*(q-32).  Lane p: elements 8p..8p+7 (one
+// l/16 group, one scale).
+template <>
+struct WvFmt<T_Q6_K> {
+  static constexpr uint32_t BS = 210, QK = 256, EPL = 8;
+  static constexpr bool MIN = false;
+  using X = WvX<2>;
+  __device__ static void xload(const float* xs, uint32_t e0, uint32_t p, X& x) { wv_xload<2>(xs, e0, p, x); }
+  __device__ static float dot(const uint8_t* wr, uint32_t o, const X& x, uint32_t p, float) {
+    const uint32_t hf = p >> 4, k = (p >> 2) & 3u, l0 = 8u * (p & 3u);
+    const float d = rf_half_to_float_fast(*reinterpret_cast<const uint16_t*>(wr + o + 208u));
+    const float sc = (float)*reinterpret_cast<const int8_t*>(wr + o + 192u + 8u * hf + 2u * k + (l0 >> 4));
+    uint32_t ql[2], qh[2];
+    rf_lds_words<2>(wr, o + 64u * hf + 32u * (k & 1u) + l0, ql);
+    rf_lds_words<2>(wr, o + 128u + 32u * hf + l0, qh);
+    const uint32_t nsh = (k >> 1) * 4u, hsh = 2u * k;
+    // 4 (q - 32) as int8 bytes: exact products
+    const uint32_t c0 =
+        rf_opaque(rf_top_signed(((ql[0] >> nsh) & 0x0F0F0F0Fu) | (((qh[0] >> hsh) & 0x03030303u) << 4), 6));
+    const uint32_t c1 =
+        rf_opaque(rf_top_signed(((ql[1] >> nsh) & 0x0F0F0F0Fu) | (((qh[1] >> hsh) & 0x03030303u) << 4), 6));
+    return d * (sc * (wv_dot4s(c1, x.v[1], wv_dot4s(c0, x.v[0], 0.f)) * 0.25f));
   }
 };
 
 // NQ 16-byte loads per lane and item (NQ * 1024 >= the item's bytes).  XR:
 // rows of at most 4096 inputs (one item each) with each lane's x of all
-// eight 16-block steps held in registers, read from LDS once per wavefront;
-// otherwise x is read from LDS per step.
+// steps held in registers, read from LDS once per wavefront; otherwise x is
+// read from LDS per step.
 template <uint32_t T, int NQ, bool XR>
 __global__ __launch_bounds__(512) void matvec_wave(WvArgs a) {
-  constexpr uint32_t BS = WvFmt<T>::BS;
-  constexpr int XS = XR ? 8 : 1;
+  using F = WvFmt<T>;
+  using X = typename F::X;
+  // lanes per block, blocks per step, steps of a 4096-input row
+  constexpr uint32_t BS = F::BS, PL = F::QK / F::EPL, SB = 64u / PL;
+  constexpr int XS = XR ? (int)(4096u / (64u * F::EPL)) : 1;
   typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
   extern __shared__ __align__(16) uint8_t mvw_sm[];
   const float* xs = reinterpret_cast<const float*>(mvw_sm);
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const uint32_t nw = blockDim.x >> 6;
-  uint8_t* wr = mvw_sm + a.in_dim * 4u + wave * a.region;
+  float* xsum16 = reinterpret_cast<float*>(mvw_sm + wv_x_bytes(a.in_dim, false));
+  uint8_t* wr = mvw_sm + wv_x_bytes(a.in_dim, F::MIN) + wave * a.region;
   const uint32_t G = gridDim.x * nw;
   const uint32_t chb = a.cblk * BS;  // bytes of a full chunk
   auto item_bytes = [&](uint32_t c) { return c + 1u < a.nch ? chb : a.row_bytes - c * chb; };
@@ -667,16 +817,39 @@ __global__ __launch_bounds__(512) void matvec_wave(WvArgs a) {
   // item k of this wavefront: row r0 + (k / nch) G, chunk k % nch
   uint32_t r = blockIdx.x * nw + wave, c = 0;
   fetch(r, c);
-  for (uint32_t i = tid; i < a.in_dim / 4u; i += blockDim.x)
-    reinterpret_cast<float4*>(mvw_sm)[i] = reinterpret_cast<const float4*>(a.x)[i];
-  __syncthreads();
-  const uint32_t q = lane & 3u, bl = lane >> 2;
-  float4 xr0[XS], xr1[XS];
-  if constexpr (XR) {
-    const uint32_t last = a.in_dim / 32u - 1u;
-#pragma unroll
-    for (int k = 0; k < XS; ++k) WvFmt<T>::xload(xs + 32u * min(16u * k + bl, last), q, xr0[k], xr1[k]);
+  for (uint32_t i = tid; i < a.in_dim / 4u; i += blockDim.x) {
+    const float4 v = reinterpret_cast<const float4*>(a.x)[i];
+    *reinterpret_cast<float4*>(mvw_sm + 4u * wv_xi(4u * i)) = v;
   }
+  __syncthreads();
+  int bad = 0;  // an infinity or NaN in x (min-term formats)
+  if constexpr (F::MIN) {  // sums of 16 elements, and whether x is finite
+    for (uint32_t g = tid; g < a.in_dim / 16u; g += blockDim.x) {
+      WvX<4> v;
+      wv_xload<4>(xs, 0u, g, v);
+      xsum16[g] = wv_xsum(v);
+      bad |= !wv_finite(v);
+    }
+    bad = __syncthreads_or(bad);
+  }
+  const uint32_t p = lane % PL, bl = lane / PL;
+  X xr[XS];
+  float xsr[XS];
+  if constexpr (XR) {
+    const uint32_t last = a.in_dim / F::QK - 1u;
+#pragma unroll
+    for (int k = 0; k < XS; ++k) {
+      F::xload(xs, F::QK * min(SB * k + bl, last), p, xr[k]);
+      if constexpr (F::MIN) xsr[k] = wv_xsum(xr[k]);
+    }
+  }
+  // lane's share of block bk of the item
+  auto term = [&](uint32_t bk, const X& x, float xsum) -> float {
+    if constexpr (F::MIN) {
+      if (bad && !wv_finite(x)) return F::kinds(wr, BS * bk, x, p);
+    }
+    return F::dot(wr, BS * bk, x, p, xsum);
+  };
   float acc = 0.f;
   while (r < a.rows) {
     const uint32_t nb = item_bytes(c);
@@ -691,20 +864,20 @@ __global__ __launch_bounds__(512) void matvec_wave(WvArgs a) {
     if constexpr (XR) {
 #pragma unroll
       for (int k = 0; k < XS; ++k) {
-        const uint32_t bk = 16u * k + bl;
-        if (16u * k < nbk && bk < nbk) acc += WvFmt<T>::dot(wr, BS * bk, xr0[k], xr1[k], q);
+        const uint32_t bk = SB * k + bl;
+        if (SB * k < nbk && bk < nbk) acc += term(bk, xr[k], F::MIN ? xsr[k] : 0.f);
       }
     } else {
-      const uint32_t b0 = c * a.cblk, nfull = nbk & ~15u;
+      const uint32_t b0 = c * a.cblk, nfull = nbk / SB * SB;
 #pragma unroll 2
-      for (uint32_t j = 0; j < nfull; j += 16u) {
-        WvFmt<T>::xload(xs + 32u * (b0 + j + bl), q, xr0[0], xr1[0]);
-        acc += WvFmt<T>::dot(wr, BS * (j + bl), xr0[0], xr1[0], q);
+      for (uint32_t j = 0; j < nfull; j += SB) {
+        F::xload(xs, F::QK * (b0 + j + bl), p, xr[0]);
+        acc += term(j + bl, xr[0], F::MIN ? xsum16[(F::QK * (b0 + j + bl) + F::EPL * p) / 16u] : 0.f);
       }
       const uint32_t bk = nfull + bl;
       if (nfull < nbk && bk < nbk) {
-        WvFmt<T>::xload(xs + 32u * (b0 + bk), q, xr0[0], xr1[0]);
-        acc += WvFmt<T>::dot(wr, BS * bk, xr0[0], xr1[0], q);
+        F::xload(xs, F::QK * (b0 + bk), p, xr[0]);
+        acc += term(bk, xr[0], F::MIN ? xsum16[(F::QK * (b0 + bk) + F::EPL * p) / 16u] : 0.f);
       }
     }
     if (cn == 0u) {
@@ -717,35 +890,44 @@ __global__ __launch_bounds__(512) void matvec_wave(WvArgs a) {
   }
 }
 
-// Whether the wave-staged kernel takes this launch: Q8_0 / Q4_0 rows of an
-// even block count (dword-aligned rows), a dword-aligned base, 16-byte
-// aligned x, and x plus four wavefronts' regions within the LDS.
+// Whether the wave-staged kernel takes this launch: Q8_0 / Q4_0 / Q6_K rows
+// and Q4_K rows of at most 4096 inputs, of an even block count
+// (dword-aligned rows), a dword-aligned base, 16-byte aligned x, and x plus
+// four wavefronts' regions within the LDS.  (Q4_K at 4096 x 14336 took 24.4
+// us against 19.1 on the streaming kernel.)
 static bool wave_ok(uint32_t t, uint64_t in_dim, const void* w, const float* x) {
-  if ((t != T_Q8_0 && t != T_Q4_0) || in_dim == 0 || in_dim % 64 != 0) return false;
+  const uint64_t qk = t == T_Q8_0 || t == T_Q4_0 ? 32 : (t == T_Q4_K || t == T_Q6_K ? 256 : 0);
+  if (qk == 0 || in_dim == 0 || in_dim % (2 * qk) != 0) return false;
+  if (t == T_Q4_K && in_dim > 4096) return false;
   if ((reinterpret_cast<uintptr_t>(w) & 3u) != 0 || !aligned16(x)) return false;
-  return in_dim * 4u + 4u * (MVW_CHUNK + 16u) <= MVW_LDS;
+  return wv_x_bytes((uint32_t)in_dim, true) + 4u * (MVW_CHUNK + 16u) <= MVW_LDS;
 }
 
 static int g_wave_enabled = 1;
 void set_matvec_wave(bool on) { g_wave_enabled = on ? 1 : 0; }
 bool matvec_wave_on() { return g_wave_enabled != 0; }
 
-// Resident workgroups per CU for (kernel, threads, LDS), cached; 0 when the
-// query would run inside a capture.
+// Resident workgroups per CU for (kernel, threads, LDS), cached; the first
+// query for a kernel also raises its dynamic LDS limit.  Both run outside
+// captures only (hipErrorStreamCaptureUnsupported inside one).
 template <uint32_t T, int NQ, bool XR>
-static uint32_t wave_occupancy(uint32_t threads, uint32_t lds, hipStream_t st) {
+static hipError_t wave_occupancy(uint32_t threads, uint32_t lds, hipStream_t st, uint32_t* occ) {
   static std::mutex mu;
   std::lock_guard<std::mutex> lock(mu);
   static uint32_t key[16] = {0}, val[16] = {0};
   static bool attr = false;
   const uint32_t k = threads << 20 | lds;
   for (int i = 0; i < 16; ++i)
-    if (key[i] == k) return val[i];
-  if (setup_outside_capture(st) != hipSuccess) return 0;
+    if (key[i] == k) {
+      *occ = val[i];
+      return hipSuccess;
+    }
+  hipError_t e = setup_outside_capture(st);
+  if (e != hipSuccess) return e;
   if (!attr) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(matvec_wave<T, NQ, XR>),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)MVW_LDS) != hipSuccess)
-      return 0;
+    e = hipFuncSetAttribute(reinterpret_cast<const void*>(matvec_wave<T, NQ, XR>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)MVW_LDS);
+    if (e != hipSuccess) return e;
     attr = true;
   }
   int n = 0;
@@ -758,7 +940,8 @@ static uint32_t wave_occupancy(uint32_t threads, uint32_t lds, hipStream_t st) {
       val[i] = (uint32_t)n;
       break;
     }
-  return (uint32_t)n;
+  *occ = (uint32_t)n;
+  return hipSuccess;
 }
 
 template <uint32_t T, int NQ, bool XR>
@@ -767,13 +950,15 @@ static hipError_t launch_wave_q(const WvArgs& a, hipStream_t st) {
   // eight wavefronts per workgroup unless there are fewer rows than that
   // per CU; whole workgroups per CU, about two rows per wavefront
   uint32_t nw = a.rows >= 8u * ncu ? 8u : 4u;
-  uint32_t lds = a.in_dim * 4u + nw * a.region;
+  const uint32_t xb = wv_x_bytes(a.in_dim, WvFmt<T>::MIN);
+  uint32_t lds = xb + nw * a.region;
   if (lds > MVW_LDS) {
     nw = 4u;
-    lds = a.in_dim * 4u + nw * a.region;
+    lds = xb + nw * a.region;
   }
-  const uint32_t occ = wave_occupancy<T, NQ, XR>(64u * nw, lds, st);
-  if (occ == 0) return hipErrorStreamCaptureUnsupported;
+  uint32_t occ = 0;
+  const hipError_t e = wave_occupancy<T, NQ, XR>(64u * nw, lds, st, &occ);
+  if (e != hipSuccess) return e;
   uint32_t grid;
   if ((uint64_t)a.rows <= (uint64_t)nw * ncu) {
     grid = (a.rows + nw - 1) / nw;
@@ -814,9 +999,10 @@ static hipError_t launch_wave_t(const WvArgs& a, hipStream_t st) {
   }
 }
 
-static hipError_t launch_wave(uint32_t t, const MvSegDesc& s, const float* x, uint64_t in_dim, hipStream_t st) {
-  const uint32_t bs = t == T_Q8_0 ? 34u : 18u;
-  const uint32_t nblk = (uint32_t)(in_dim / 32u);
+template <uint32_t T>
+static hipError_t launch_wave_f(const MvSegDesc& s, const float* x, uint64_t in_dim, hipStream_t st) {
+  constexpr uint32_t bs = WvFmt<T>::BS, sb = 64u / (WvFmt<T>::QK / WvFmt<T>::EPL);
+  const uint32_t nblk = (uint32_t)(in_dim / WvFmt<T>::QK);
   WvArgs a{};
   a.w = static_cast<const uint8_t*>(s.w);
   a.x = x;
@@ -827,14 +1013,24 @@ static hipError_t launch_wave(uint32_t t, const MvSegDesc& s, const float* x, ui
   if (a.row_bytes <= MVW_CHUNK) {
     a.nch = 1;
     a.cblk = nblk;
-  } else {  // chunks of about equal size, whole 16-block steps
+  } else {  // chunks of about equal size, whole steps
     const uint32_t n = (a.row_bytes + MVW_CHUNK - 1) / MVW_CHUNK;
-    a.cblk = ((nblk + n - 1) / n + 15u) / 16u * 16u;
-    if (a.cblk * bs > MVW_CHUNK) a.cblk = MVW_CHUNK / bs / 16u * 16u;
+    a.cblk = ((nblk + n - 1) / n + sb - 1) / sb * sb;
+    if (a.cblk * bs > MVW_CHUNK) a.cblk = MVW_CHUNK / bs / sb * sb;
     a.nch = (nblk + a.cblk - 1) / a.cblk;
   }
   a.region = (std::min(a.row_bytes, a.cblk * bs) + 16u + 15u) & ~15u;
-  return t == T_Q8_0 ? launch_wave_t<T_Q8_0>(a, st) : launch_wave_t<T_Q4_0>(a, st);
+  return launch_wave_t<T>(a, st);
+}
+
+static hipError_t launch_wave(uint32_t t, const MvSegDesc& s, const float* x, uint64_t in_dim, hipStream_t st) {
+  switch (t) {
+    case T_Q8_0: return launch_wave_f<T_Q8_0>(s, x, in_dim, st);
+    case T_Q4_0: return launch_wave_f<T_Q4_0>(s, x, in_dim, st);
+    case T_Q4_K: return launch_wave_f<T_Q4_K>(s, x, in_dim, st);
+    case T_Q6_K: return launch_wave_f<T_Q6_K>(s, x, in_dim, st);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 template <int EPI>

@@ -149,24 +149,60 @@ def kernel_mode(request):
     rf.tune_matvec_kernel(old)
 
 
-@pytest.mark.parametrize("t", [Q8_0, Q4_0])
-@pytest.mark.parametrize("out_dim,in_dim", [(1, 64), (7, 128), (513, 4096), (130, 2048), (33, 4096), (4096, 4096),
-                                            (6000, 1024), (7000, 4096), (6200, 1088), (300, 9024), (64, 14336),
-                                            (41, 16448)])
+WAVE_SHAPES_32 = [(1, 64), (7, 128), (513, 4096), (130, 2048), (33, 4096), (4096, 4096), (6000, 1024), (7000, 4096),
+                  (6200, 1088), (300, 9024), (64, 14336), (41, 16448)]
+WAVE_SHAPES_256 = [(1, 512), (7, 1024), (513, 4096), (130, 2048), (4096, 4096), (6000, 1024), (7000, 4096),
+                   (6200, 1536), (77, 1536), (300, 10240), (64, 14336), (41, 16384)]
+
+
+@pytest.mark.parametrize("t,out_dim,in_dim", [(t, o, n) for t in (Q8_0, Q4_0) for o, n in WAVE_SHAPES_32] +
+                         [(t, o, n) for t in (Q4_K, Q6_K) for o, n in WAVE_SHAPES_256])
 def test_matvec_wave_kernel_shapes(ctx, orc, t, out_dim, in_dim):
-    """The wave-staged kernel (plain Q8_0 / Q4_0 rf_matvec): rows that leave
-    wavefronts of a workgroup idle, four- and eight-wavefront workgroups and
-    more than one row per wavefront (6000 rows), x held in registers (7000
-    and 6200 rows, the second with a partial 16-block step), partial steps
-    with x read from LDS, and rows longer than one 8 KiB item (Q8_0 at 9024
-    and 14336 inputs, Q4_0 at 16448: two chunks per row, the last one
-    partial)."""
+    """The wave-staged kernel (plain Q8_0 / Q4_0 / Q4_K / Q6_K rf_matvec):
+    rows that leave wavefronts of a workgroup idle, four- and eight-wavefront
+    workgroups and more than one row per wavefront (6000 rows), x held in
+    registers (7000 and 6200 rows, the second with a partial step: 16
+    blocks per step for Q8_0 / Q4_0, 4 super-blocks for Q4_K, 2 for Q6_K),
+    partial steps with x read from LDS, and rows longer than one 8 KiB item
+    (Q8_0 at 9024 and 14336 inputs, Q4_0 at 16448, Q6_K at 10240 and 14336:
+    two chunks per row; Q4_K rows of more than 4096 inputs take the
+    streaming kernel)."""
     rf = _rf()
     assert rf.tune_matvec_kernel(-1) == 2
     _check_matvec(ctx, orc, t, out_dim, in_dim, 1500 + out_dim + in_dim + t)
 
 
-@pytest.mark.parametrize("t", [Q8_0, Q4_0])
+@pytest.mark.parametrize("t", [Q4_K, Q8_0])
+@pytest.mark.parametrize("case", ["pinf", "both", "nan"])
+def test_matvec_wave_nonfinite_x_in_registers(ctx, orc, t, case):
+    """x holding infinities or a NaN on the wave-staged kernel's
+    x-in-registers path (7000 rows): every row's kind (NaN, +inf, -inf)
+    equals the oracle's.  Q4_K switches the eight-element shares that meet a
+    non-finite x to the kind of the reference's terms."""
+    rf = _rf()
+    rng = np.random.default_rng(2250 + t)
+    out_dim, in_dim = 7000, 1024
+    raw = random_matrix(t, out_dim, in_dim, rng)
+    x = rng.normal(0, 1, in_dim).astype(np.float32)
+    if case in ("pinf", "both"):
+        x[70] = np.inf
+    if case == "both":
+        x[900] = -np.inf
+    if case == "nan":
+        x[513] = np.nan
+    print(f"  wave kernel non-finite x {NAMES[t]} {case}", flush=True)
+    w, xd, y = ctx.array(raw), ctx.array(x), ctx.empty((out_dim,))
+    rf.matvec(ctx, t, w, (out_dim, in_dim), xd, y)
+    got = y.numpy()
+    with np.errstate(all="ignore"):
+        ref = orc.dispatch_matvec(t, raw, in_dim, out_dim, x, 16)
+    for kind in (np.isnan, np.isposinf, np.isneginf):
+        assert np.array_equal(kind(got), kind(ref)), (NAMES[t], case, kind.__name__)
+    for a in (w, xd, y):
+        a.free()
+
+
+@pytest.mark.parametrize("t", [Q8_0, Q4_0, Q6_K])
 def test_matvec_wave_kernel_offsets(ctx, orc, t):
     """Row ranges (the base moves by whole rows, still dword aligned), a
     weight base 4 bytes past an aligned allocation (the wave-staged kernel)
