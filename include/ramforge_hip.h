@@ -572,7 +572,9 @@ uint32_t rf_tune_matvec_tile_bytes(uint32_t bytes);
  * matvecs and Q4_K ones of up to 4096 inputs (rf_matvec, no fused norm or
  * epilogue; rows of an even block count, 16-byte aligned x, 4-byte aligned
  * weights, at most about 29000 inputs) stage each row per wavefront in LDS
- * through 16-byte loads, the rest as 1 (default);
+ * through 16-byte loads, and plain F32 ones (16-byte aligned, at most 16384
+ * inputs) load rows per wavefront straight into registers; the rest as 1
+ * (default);
  * 1 = persistent streaming kernel where rows and bases are
  * 16-byte aligned, LDS-staged row tiles; 0 = one-shot tile kernel
  * everywhere; other values only query.  Returns the mode in effect

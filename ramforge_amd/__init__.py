@@ -805,9 +805,9 @@ def tune_matvec_tile_bytes(nbytes: int = 0) -> int:
 def tune_matvec_kernel(mode: int = -1) -> int:
     """GGUF-layout matvec kernels: 2 (default) plain Q8_0 / Q4_0 / Q6_K
     matvecs (Q4_K up to 4096 inputs) stage each row per wavefront in LDS
-    through 16-byte loads, the rest as 1; 1 persistent streaming kernel with
-    LDS row tiles; 0 one-shot tile kernel; -1 queries.  Returns the mode in
-    effect."""
+    through 16-byte loads, plain F32 ones load rows per wavefront into
+    registers, the rest as 1; 1 persistent streaming kernel with LDS row
+    tiles; 0 one-shot tile kernel; -1 queries.  Returns the mode in effect."""
     return _lib.load().rf_tune_matvec_kernel(mode)
 
 

@@ -1033,6 +1033,136 @@ static hipError_t launch_wave(uint32_t t, const MvSegDesc& s, const float* x, ui
   }
 }
 
+// ------------------------------------------------ F32 rows, per wavefront
+// F32 weights need no decode and are naturally aligned: a wavefront owns
+// rows (rows r, r + G, ... of G wavefronts) and reads each in items of up to
+// NQ 256-float chunks, lane l taking floats 4l, 4l + 256, ... of the item
+// with 16-byte loads straight into registers, times the same floats of x
+// from LDS (zero-padded to whole items); two register sets alternate, so the
+// next item's loads are in flight while the current one is summed.  Each
+// lane sums its floats in order, then the wavefront sums the lanes (the
+// reference's AVX2 kernel keeps 8 lanes of FMA partials, backend.rs:173-218,
+// simd.rs:21-45: the same sum up to the order of the additions).
+constexpr uint32_t MVF_NQ = 8;  // 256-float chunks per item
+
+struct F32WArgs {
+  const float* w;
+  const float* x;
+  float* y;
+  uint32_t in_dim, rows, nch;  // nch = items per row
+};
+
+__global__ __launch_bounds__(512) void matvec_f32_wave(F32WArgs a) {
+  typedef float f32x4 __attribute__((ext_vector_type(4)));
+  constexpr uint32_t ICH = MVF_NQ * 256u;  // floats per item
+  extern __shared__ __align__(16) float mvf_x[];
+  const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const uint32_t nw = blockDim.x >> 6, G = gridDim.x * nw;
+  f32x4 buf[2][MVF_NQ];
+  auto fetch = [&](f32x4 (&b)[MVF_NQ], uint32_t r, uint32_t c) {
+    const bool live = r < a.rows;  // wave-uniform; past the last row every load returns zeros
+    const uint32_t first = c * ICH, n = live ? min(ICH, a.in_dim - first) : 0u;
+    const MvRsrc rs = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(a.w + (live ? (uint64_t)r * a.in_dim + first : 0u)), 0, (int32_t)(n * 4u), MV_RSRC_WORD3);
+#pragma unroll
+    for (int i = 0; i < (int)MVF_NQ; ++i)  // streamed once: non-temporal
+      b[i] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, 16u * (lane + 64u * i), 0, 2));
+  };
+  uint32_t r = blockIdx.x * nw + wave, c = 0;
+  fetch(buf[0], r, c);
+  const uint32_t npad = a.nch * ICH;
+  for (uint32_t i = tid; i < npad / 4u; i += blockDim.x)
+    reinterpret_cast<float4*>(mvf_x)[i] =
+        4u * i < a.in_dim ? reinterpret_cast<const float4*>(a.x)[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+  __syncthreads();
+  float acc = 0.f;
+  auto next = [&](uint32_t& rr, uint32_t& cc) {
+    if (++cc == a.nch) {
+      cc = 0;
+      rr += G;
+    }
+  };
+  auto consume = [&](const f32x4 (&b)[MVF_NQ], uint32_t rr, uint32_t cc) {
+#pragma unroll
+    for (int i = 0; i < (int)MVF_NQ; ++i) {
+      const float4 xv = *reinterpret_cast<const float4*>(mvf_x + cc * ICH + 4u * (lane + 64u * i));
+      acc = fmaf(b[i].x, xv.x, acc);
+      acc = fmaf(b[i].y, xv.y, acc);
+      acc = fmaf(b[i].z, xv.z, acc);
+      acc = fmaf(b[i].w, xv.w, acc);
+    }
+    if (cc + 1u == a.nch) {
+      const float v = rf_wave_sum(acc);
+      if (lane == 0) a.y[rr] = v;
+      acc = 0.f;
+    }
+  };
+  while (r < a.rows) {
+    uint32_t r1 = r, c1 = c;
+    next(r1, c1);
+    fetch(buf[1], r1, c1);
+    consume(buf[0], r, c);
+    if (r1 >= a.rows) break;
+    uint32_t r2 = r1, c2 = c1;
+    next(r2, c2);
+    fetch(buf[0], r2, c2);
+    consume(buf[1], r1, c1);
+    r = r2;
+    c = c2;
+  }
+}
+
+static bool f32_wave_ok(uint64_t in_dim, const void* w, const float* x) {
+  if (in_dim == 0 || in_dim % 4 != 0 || in_dim > 16384) return false;
+  return aligned16(w) && aligned16(x);
+}
+
+static hipError_t launch_f32_wave(const MvSegDesc& s, const float* x, uint64_t in_dim, hipStream_t st) {
+  F32WArgs a{};
+  a.w = static_cast<const float*>(s.w);
+  a.x = x;
+  a.y = s.y;
+  a.in_dim = (uint32_t)in_dim;
+  a.rows = (uint32_t)s.rows;
+  a.nch = (uint32_t)((in_dim + MVF_NQ * 256u - 1) / (MVF_NQ * 256u));
+  const uint32_t lds = a.nch * MVF_NQ * 256u * 4u;
+  const uint32_t ncu = (uint32_t)cu_count();
+  const uint32_t nw = a.rows >= 8u * ncu ? 8u : 4u;
+  static std::mutex mu;
+  static uint32_t key[8] = {0}, val[8] = {0};
+  uint32_t occ = 0;
+  {
+    std::lock_guard<std::mutex> lock(mu);
+    const uint32_t k = nw << 20 | lds;
+    for (int i = 0; i < 8 && !occ; ++i)
+      if (key[i] == k) occ = val[i];
+    if (!occ) {
+      const hipError_t e = setup_outside_capture(st);
+      if (e != hipSuccess) return e;
+      int n = 0;
+      if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, matvec_f32_wave, (int)(64u * nw), (size_t)lds) !=
+              hipSuccess || n < 1)
+        n = 1;
+      occ = (uint32_t)n;
+      for (int i = 0; i < 8; ++i)
+        if (key[i] == 0) {
+          key[i] = k;
+          val[i] = occ;
+          break;
+        }
+    }
+  }
+  uint32_t grid;
+  if ((uint64_t)a.rows <= (uint64_t)nw * ncu) {
+    grid = (a.rows + nw - 1) / nw;
+  } else {
+    const uint64_t k = ((uint64_t)a.rows + 2ull * nw * ncu - 1) / (2ull * nw * ncu);
+    grid = (uint32_t)(std::min<uint64_t>(k, occ) * ncu);
+  }
+  RF_KLAUNCH(matvec_f32_wave, dim3(grid), dim3(64u * nw), lds, st, a);
+  return hipGetLastError();
+}
+
 template <int EPI>
 static hipError_t launch_tiled_e(uint32_t t, const MvArgs& a, uint32_t grid, const MvPlan& p, hipStream_t st,
                                  bool stream) {
@@ -1074,8 +1204,10 @@ hipError_t launch_matvec_segments(uint32_t t, const MvSegDesc* segs, int nseg, c
     return hipSuccess;
   }
   if (g_wave_enabled && epi == EPI_STORE && norm_w == nullptr && nseg == 1 && segs[0].rows > 0 &&
-      segs[0].rows <= 0x7FFFFFFFull && wave_ok(t, in_dim, segs[0].w, x))
-    return launch_wave(t, segs[0], x, in_dim, st);
+      segs[0].rows <= 0x7FFFFFFFull) {
+    if (wave_ok(t, in_dim, segs[0].w, x)) return launch_wave(t, segs[0], x, in_dim, st);
+    if (t == T_F32 && f32_wave_ok(in_dim, segs[0].w, x)) return launch_f32_wave(segs[0], x, in_dim, st);
+  }
   bool stream = p.stream && g_stream_enabled;
   for (int i = 0; i < nseg && stream; ++i)
     stream = aligned16(segs[i].w) && (!dual || aligned16(segs[i].w_up));

@@ -155,8 +155,12 @@ WAVE_SHAPES_256 = [(1, 512), (7, 1024), (513, 4096), (130, 2048), (4096, 4096), 
                    (6200, 1536), (77, 1536), (300, 10240), (64, 14336), (41, 16384)]
 
 
+WAVE_SHAPES_F32 = [(1, 32), (7, 96), (513, 4096), (4096, 4096), (6000, 1024), (300, 9024), (77, 16384)]
+
+
 @pytest.mark.parametrize("t,out_dim,in_dim", [(t, o, n) for t in (Q8_0, Q4_0) for o, n in WAVE_SHAPES_32] +
-                         [(t, o, n) for t in (Q4_K, Q6_K) for o, n in WAVE_SHAPES_256])
+                         [(t, o, n) for t in (Q4_K, Q6_K) for o, n in WAVE_SHAPES_256] +
+                         [(F32, o, n) for o, n in WAVE_SHAPES_F32])
 def test_matvec_wave_kernel_shapes(ctx, orc, t, out_dim, in_dim):
     """The wave-staged kernel (plain Q8_0 / Q4_0 / Q4_K / Q6_K rf_matvec):
     rows that leave wavefronts of a workgroup idle, four- and eight-wavefront
@@ -166,7 +170,8 @@ def test_matvec_wave_kernel_shapes(ctx, orc, t, out_dim, in_dim):
     partial steps with x read from LDS, and rows longer than one 8 KiB item
     (Q8_0 at 9024 and 14336 inputs, Q4_0 at 16448, Q6_K at 10240 and 14336:
     two chunks per row; Q4_K rows of more than 4096 inputs take the
-    streaming kernel)."""
+    streaming kernel).  F32 rows take the per-wavefront F32 kernel: items of
+    2048 floats, the last one partial (96, 9024), up to 8 per row (16384)."""
     rf = _rf()
     assert rf.tune_matvec_kernel(-1) == 2
     _check_matvec(ctx, orc, t, out_dim, in_dim, 1500 + out_dim + in_dim + t)
