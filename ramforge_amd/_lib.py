@@ -151,6 +151,7 @@ SIGNATURES = {
     "rf_model_enable_streaming": (_i32, [_vp, _u64]),
     "rf_model_residency_stats": (_i32, [_vp, C.POINTER(_u64)]),
     "rf_model_set_cache_policy": (_i32, [_vp, _i32]),
+    "rf_model_set_stream_units": (_i32, [_vp, _i32]),
     "rf_capture_begin": (_i32, [_vp]),
     "rf_capture_end": (_i32, [_vp, C.POINTER(_vp)]),
     "rf_graph_replay": (_i32, [_vp, _vp, _u32, C.POINTER(_f32)]),

@@ -140,7 +140,11 @@ struct rf_model {
   std::list<uint32_t> lru;  // cached layers, most recently used first
   uint64_t st_hits = 0, st_misses = 0, st_evictions = 0, st_uploaded = 0;
   int cache_policy = 0;    // 0: LRU (LayerCache); 1: next use within the layer cycle
-  uint32_t cur_layer = 0;  // layer the forward pass is at (policy 1)
+  // Streaming unit (rf_model_set_stream_units): false, a whole layer (the
+  // reference's LayerCache entry); true, half a layer (unit_slots).  res,
+  // lru and cur_layer then count units.
+  bool half_units = false;
+  uint32_t cur_layer = 0;  // streaming unit the forward pass is at (policy 1)
   // Byte source of streamed layers (rf_model_set_reader): ranges are read into
   // two pinned staging buffers of stage_bytes each and converted on the device
   // through a raw buffer charged "workspace:layer_read" (grown on demand).
@@ -276,13 +280,62 @@ const char* slot_name(int i) {
   return n[i];
 }
 
-void update_layer_bytes(rf_model* m, uint32_t li) {
+// Streaming units.  Whole layers: unit i = layer i.  Half units: unit 2i
+// holds layer i's attention tensors and both norms (the prefill's o-projection
+// applies the feed-forward norm), unit 2i + 1 its feed-forward matrices
+// (gate, up, down); the pass acquires the second while the first one's
+// kernels run.
+bool slot_in_ffn_unit(int i) { return i == 6 || i == 7 || i == 8; }
+
+uint32_t unit_count(const rf_model* m) {
+  return (uint32_t)m->layers.size() * (m->half_units ? 2u : 1u);
+}
+
+uint32_t unit_layer(const rf_model* m, uint32_t u) { return m->half_units ? u >> 1 : u; }
+
+// The 12 tensor slots of unit u; with half units the other half's slots are
+// an empty tensor (not streamed, no buffer), which every streaming loop skips.
+void unit_slots(rf_model* m, uint32_t u, DevTensor* out[12]) {
+  layer_slots(m->layers[unit_layer(m, u)], out);
+  if (!m->half_units) return;
+  static DevTensor none;
+  const bool ffn = (u & 1u) != 0;
+  for (int i = 0; i < 12; ++i)
+    if (slot_in_ffn_unit(i) != ffn) out[i] = &none;
+}
+
+// Charge of slot i of unit u while the unit is active ("layer:{layer}:{tensor}").
+std::string unit_charge(const rf_model* m, uint32_t u, int i) {
+  return "layer:" + std::to_string(unit_layer(m, u)) + ":" + slot_name(i);
+}
+
+// Renames the charges of unit u's device tensors from prefix `from` + their
+// active names to `to` + them ("" or "cache:"), tensor by tensor, so that the
+// other half of a split layer keeps its names.
+int32_t rename_unit(rf_model* m, uint32_t u, const std::string& from, const std::string& to) {
   DevTensor* t[12];
-  layer_slots(m->layers[li], t);
-  uint64_t b = 0;
-  for (DevTensor* x : t)
-    if (x->streamed()) b += x->nbytes;
-  m->res[li].bytes = b;
+  unit_slots(m, u, t);
+  for (int i = 0; i < 12; ++i) {
+    if (!t[i]->d) continue;
+    const std::string name = unit_charge(m, u, i);
+    const int32_t rc = vram_rename_prefix(m->ctx, from + name, to + name);
+    if (rc) return rc;
+    t[i]->charge = to + name;
+  }
+  return RF_OK;
+}
+
+// Device bytes of each streaming unit of layer li.
+void update_layer_bytes(rf_model* m, uint32_t li) {
+  const uint32_t per = m->half_units ? 2u : 1u;
+  for (uint32_t u = li * per; u < (li + 1) * per && u < m->res.size(); ++u) {
+    DevTensor* t[12];
+    unit_slots(m, u, t);
+    uint64_t b = 0;
+    for (DevTensor* x : t)
+      if (x->streamed()) b += x->nbytes;
+    m->res[u].bytes = b;
+  }
 }
 
 // Physical free of a resident layer's buffers, then release of its charges
@@ -294,7 +347,7 @@ int32_t layer_free(rf_model* m, uint32_t li) {
   if (e == hipSuccess) e = hipEventSynchronize(R.uploaded);
   if (e != hipSuccess) return hip_error(e, "layer release");
   DevTensor* t[12];
-  layer_slots(m->layers[li], t);
+  unit_slots(m, li, t);
   int32_t rc = RF_OK;
   for (DevTensor* x : t) {
     if (!x->d) continue;
@@ -315,7 +368,7 @@ int32_t layer_free(rf_model* m, uint32_t li) {
 // (every pass visits the layers in order; the current layer counts as a
 // full cycle away once computed).
 uint32_t next_use(const rf_model* m, uint32_t j) {
-  const uint32_t n = (uint32_t)m->layers.size();
+  const uint32_t n = unit_count(m);
   const uint32_t d = (j + n - m->cur_layer) % n;
   return d == 0 ? n : d;
 }
@@ -531,7 +584,7 @@ int32_t plan_layer_reads(rf_model* m, DevTensor* t[12], std::vector<ReadRange>* 
 // Bytes a layer's reads fill (0 when it has no source tensors).
 uint64_t layer_read_bytes(rf_model* m, uint32_t li) {
   DevTensor* t[12];
-  layer_slots(m->layers[li], t);
+  unit_slots(m, li, t);
   std::vector<ReadRange> plan;
   if (plan_layer_reads(m, t, &plan) != RF_OK) return 0;
   uint64_t n = 0;
@@ -547,7 +600,7 @@ void ra_post(rf_model* m, uint32_t li) {
   if (!ra.on || !m->reader) return;
   if (!ra.buf[0]) {
     uint64_t most = 0;
-    for (uint32_t j = 0; j < m->layers.size(); ++j) most = std::max(most, layer_read_bytes(m, j));
+    for (uint32_t j = 0; j < unit_count(m); ++j) most = std::max(most, layer_read_bytes(m, j));
     if (most == 0) return;
     for (int i = 0; i < 2; ++i) {
       if (!ra.done[i] && hipEventCreateWithFlags(&ra.done[i], hipEventDisableTiming) != hipSuccess) ra.done[i] = nullptr;
@@ -565,7 +618,7 @@ void ra_post(rf_model* m, uint32_t li) {
   }
   if (!ra.th.joinable()) ra.th = std::thread(ra_worker, m);
   DevTensor* t[12];
-  layer_slots(m->layers[li], t);
+  unit_slots(m, li, t);
   std::vector<ReadRange> plan;
   if (plan_layer_reads(m, t, &plan) != RF_OK) return;
   uint64_t total = 0;
@@ -587,7 +640,7 @@ void ra_post(rf_model* m, uint32_t li) {
 // from `from` on: a host-only layer of this pass, else of the next one (a
 // retired layer is released at the end of this pass); -1 when none.
 int64_t next_read_layer(rf_model* m, uint32_t from) {
-  const uint32_t nl = (uint32_t)m->layers.size();
+  const uint32_t nl = unit_count(m);
   for (uint32_t j = from; j < nl; ++j)
     if (m->res[j].state == LAYER_HOST) return j;
   for (uint32_t j = 0; j < std::min(from, nl); ++j)
@@ -627,7 +680,7 @@ int32_t read_layer_sources(rf_model* m, uint32_t li, DevTensor* t[12], hipStream
       ra.layer = -1;
       if (failed)
         return set_error(RF_ERR_IO, "byte source read of %llu bytes at offset %llu failed (%d) for layer %u",
-                         (unsigned long long)el, (unsigned long long)eo, (int)err, li);
+                         (unsigned long long)el, (unsigned long long)eo, (int)err, unit_layer(m, li));
       m->st_read_calls += calls;
       m->st_read_bytes += bytes;
       uint64_t pos = 0;
@@ -657,7 +710,7 @@ int32_t read_layer_sources(rf_model* m, uint32_t li, DevTensor* t[12], hipStream
     m->st_read_calls += 1;
     if (r != 0)
       return set_error(RF_ERR_IO, "byte source read of %llu bytes at offset %llu failed (%d) for layer %u",
-                       (unsigned long long)len, (unsigned long long)off, (int)r, li);
+                       (unsigned long long)len, (unsigned long long)off, (int)r, unit_layer(m, li));
     m->st_read_bytes += len;
     return RF_OK;
   };
@@ -715,8 +768,8 @@ int32_t abort_pass(rf_model* m, int32_t rc) {
 // streamed, with the same sizes (all blocks of one model, in practice).
 bool same_layout(rf_model* m, uint32_t v, uint32_t li) {
   DevTensor *a[12], *b[12];
-  layer_slots(m->layers[v], a);
-  layer_slots(m->layers[li], b);
+  unit_slots(m, v, a);
+  unit_slots(m, li, b);
   for (int i = 0; i < 12; ++i) {
     if (a[i]->streamed() != b[i]->streamed()) return false;
     if (a[i]->streamed() && (a[i]->nbytes != b[i]->nbytes || !a[i]->d)) return false;
@@ -746,16 +799,16 @@ int32_t adopt_buffers(rf_model* m, uint32_t v, uint32_t li) {
   if (e == hipSuccess) e = hipStreamWaitEvent(m->ctx->copy2, V.used, 0);
   if (e != hipSuccess) return hip_error(e, "wait for the recycled layer's kernels");
   const bool cached = V.state == LAYER_CACHED;
-  const std::string to = "layer:" + std::to_string(li) + ":";
-  int32_t rc = vram_rename_prefix(m->ctx, (cached ? "cache:layer:" : "layer:") + std::to_string(v) + ":", to);
-  if (rc) return rc;
   DevTensor *a[12], *b[12];
-  layer_slots(m->layers[v], a);
-  layer_slots(m->layers[li], b);
+  unit_slots(m, v, a);
+  unit_slots(m, li, b);
   for (int i = 0; i < 12; ++i) {
     if (!a[i]->streamed()) continue;
+    const std::string to = unit_charge(m, li, i);
+    const int32_t rc = vram_rename_prefix(m->ctx, (cached ? "cache:" : "") + unit_charge(m, v, i), to);
+    if (rc) return rc;
     b[i]->d = a[i]->d;
-    b[i]->charge = to + slot_name(i);
+    b[i]->charge = to;
     a[i]->d = nullptr;
     a[i]->charge.clear();
   }
@@ -771,7 +824,7 @@ int32_t adopt_buffers(rf_model* m, uint32_t v, uint32_t li) {
 int32_t load_layer(rf_model* m, uint32_t li) {
   LayerRes& R = m->res[li];
   DevTensor* t[12];
-  layer_slots(m->layers[li], t);
+  unit_slots(m, li, t);
   hipStream_t cs = m->ctx->copy, cs2 = m->ctx->copy2;
   auto rollback = [&](int32_t code) {  // release every charge of this layer
     hipStreamSynchronize(cs);
@@ -800,7 +853,7 @@ int32_t load_layer(rf_model* m, uint32_t li) {
     for (int i = 0; i < 12; ++i) {
       DevTensor* x = t[i];
       if (!x->streamed()) continue;
-      const std::string charge = "layer:" + std::to_string(li) + ":" + slot_name(i);
+      const std::string charge = unit_charge(m, li, i);
       void* d = nullptr;
       rc = vram_alloc(m->ctx, charge, x->nbytes, &d);
       if (rc) return rollback(rc);
@@ -850,13 +903,8 @@ int32_t acquire_layer(rf_model* m, uint32_t li, bool prefetch) {
     return RF_OK;
   }
   if (R.state == LAYER_CACHED) {
-    int32_t rc = vram_rename_prefix(m->ctx, "cache:layer:" + std::to_string(li) + ":",
-                                    "layer:" + std::to_string(li) + ":");
+    const int32_t rc = rename_unit(m, li, "cache:", "");
     if (rc) return rc;
-    DevTensor* t[12];
-    layer_slots(m->layers[li], t);
-    for (DevTensor* x : t)
-      if (x->d) x->charge = "layer:" + x->charge.substr(std::string("cache:layer:").size());
     m->lru.remove(li);
     m->cache_used -= R.bytes;
     R.state = LAYER_ACTIVE;
@@ -890,12 +938,7 @@ int32_t settle_layer(rf_model* m, uint32_t li) {
   int32_t rc = RF_OK;
   while (m->cache_used + R.bytes > m->cache_cap)
     if (!evict_lru(m, &rc) || rc) return rc;
-  rc = vram_rename_prefix(m->ctx, "layer:" + std::to_string(li) + ":", "cache:layer:" + std::to_string(li) + ":");
-  if (rc) return rc;
-  DevTensor* t[12];
-  layer_slots(m->layers[li], t);
-  for (DevTensor* x : t)
-    if (x->d) x->charge = "cache:" + x->charge;
+  if ((rc = rename_unit(m, li, "", "cache:"))) return rc;
   R.state = LAYER_CACHED;
   m->lru.push_front(li);
   m->cache_used += R.bytes;
@@ -1464,14 +1507,22 @@ int32_t prof_group(rf_model* m, int kind, F&& body) {
   return RF_OK;
 }
 
-int32_t enqueue_layer(rf_model* m, size_t li, int32_t* advance = nullptr) {
+// Part 0: Q/K/V, attention, o-projection; part 1: gate/up, down.
+int32_t enqueue_layer_part(rf_model* m, size_t li, int part, int32_t* advance = nullptr) {
   int32_t rc;
-  m->oproj_merge = false;
-  if ((rc = prof_group(m, 0, [&] { return enqueue_qkv(m, li); }))) return rc;
-  if ((rc = prof_group(m, 1, [&] { return enqueue_attention(m, li); }))) return rc;
-  if ((rc = prof_group(m, 2, [&] { return enqueue_oproj(m, li); }))) return rc;
+  if (part == 0) {
+    m->oproj_merge = false;
+    if ((rc = prof_group(m, 0, [&] { return enqueue_qkv(m, li); }))) return rc;
+    if ((rc = prof_group(m, 1, [&] { return enqueue_attention(m, li); }))) return rc;
+    return prof_group(m, 2, [&] { return enqueue_oproj(m, li); });
+  }
   if ((rc = prof_group(m, 3, [&] { return enqueue_gateup(m, li); }))) return rc;
   return prof_group(m, 4, [&] { return enqueue_down(m, li, advance); });
+}
+
+int32_t enqueue_layer(rf_model* m, size_t li, int32_t* advance = nullptr) {
+  const int32_t rc = enqueue_layer_part(m, li, 0);
+  return rc ? rc : enqueue_layer_part(m, li, 1, advance);
 }
 
 // Algorithmic HBM bytes of one launch group of layer li (weights + vectors read
@@ -1495,6 +1546,40 @@ uint64_t part_bytes(rf_model* m, int kind, size_t li, uint64_t hist) {
   }
 }
 
+// Layer li of a streamed pass with half units (unit a = 2 li: attention,
+// unit f = a + 1: feed-forward).  Unit a is acquired, unit f's upload
+// started, and part 0's kernels wait for unit a only; unit f is then acquired
+// and the next layer's unit a requested before part 1's kernels wait for
+// unit f.  Both units are settled after part 1 (part 1 reads the
+// feed-forward norm of unit a).  With a byte source, reads run on this thread
+// between the parts, and the worker reads the next host-only unit meanwhile.
+// `part(p)` enqueues part p's kernels.
+template <class Part>
+int32_t forward_layer_halves(rf_model* m, uint32_t li, Part part) {
+  hipStream_t st = m->ctx->compute;
+  const uint32_t a = 2 * li, f = a + 1, nu = unit_count(m);
+  const bool read_after = m->reader != nullptr;
+  int32_t rc;
+  m->cur_layer = a;
+  if ((rc = acquire_layer(m, a, false))) return abort_pass(m, rc);
+  if (!read_after && (rc = acquire_layer(m, f, true))) return abort_pass(m, rc);
+  RF_LAUNCH(hipStreamWaitEvent(st, m->res[a].uploaded, 0), "wait for layer upload");
+  if ((rc = part(0))) return abort_pass(m, rc);
+  m->cur_layer = f;
+  if ((rc = acquire_layer(m, f, false))) return abort_pass(m, rc);
+  if (!read_after && f + 1 < nu && (rc = acquire_layer(m, f + 1, true))) return abort_pass(m, rc);
+  RF_LAUNCH(hipStreamWaitEvent(st, m->res[f].uploaded, 0), "wait for layer upload");
+  if ((rc = part(1))) return abort_pass(m, rc);
+  if ((rc = settle_layer(m, a))) return abort_pass(m, rc);
+  if ((rc = settle_layer(m, f))) return abort_pass(m, rc);
+  if (read_after && f + 1 < nu && (rc = acquire_layer(m, f + 1, true))) return abort_pass(m, rc);
+  if (read_after && m->ra.on) {
+    const int64_t nx = next_read_layer(m, f + 2);
+    if (nx >= 0) ra_post(m, (uint32_t)nx);
+  }
+  return RF_OK;
+}
+
 // Embedding of *d_token (unless the caller's argmax already decoded it into
 // the hidden state), all layers, position advance (inside the last layer's
 // down projection).
@@ -1506,6 +1591,18 @@ int32_t enqueue_forward(rf_model* m, bool embed = true) {
                                   c.vocab_size, st),
               "embedding");
   const uint32_t nl = (uint32_t)m->layers.size();
+  if (m->streaming && m->half_units) {
+    for (uint32_t li = 0; li < nl; ++li) {
+      const int32_t rc = forward_layer_halves(m, li, [&](int part) {
+        return enqueue_layer_part(m, li, part, part == 1 && li + 1 == nl ? m->d_pos : nullptr);
+      });
+      if (rc) return rc;
+    }
+    const int32_t rc = release_retired(m);
+    if (rc) return rc;
+    if (nl == 0) RF_LAUNCH(launch_advance_pos(m->d_pos, st), "advance position");
+    return RF_OK;
+  }
   for (uint32_t li = 0; li < nl; ++li) {
     int32_t rc;
     m->cur_layer = li;
@@ -1692,8 +1789,10 @@ int32_t release_prefill_ws(rf_model* m) {
 // attention norm weights, produced with this layer's down projection (null
 // for the last layer, and when streaming: the next layer may still be
 // uploading).
+// Part 0: norm, Q/K/V, RoPE and K/V rows, attention, o-projection (with the
+// feed-forward norm); part 1: gate/up, down; -1: both.
 int32_t enqueue_prefill_layer(rf_model* m, size_t li, uint64_t pos0, uint64_t nt, bool normed,
-                              const float* next_norm) {
+                              const float* next_norm, int part = -1) {
   const rf_model_config& c = m->cfg;
   Layer& L = m->layers[li];
   hipStream_t st = m->ctx->compute;
@@ -1705,65 +1804,69 @@ int32_t enqueue_prefill_layer(rf_model* m, size_t li, uint64_t pos0, uint64_t nt
     return launch_matmul_packed(t, segs, n, x, in, nt, in, epi, m->p_part, m->p_part_floats, st, norm_w, eps,
                                 norm_w ? m->p_xn : nullptr);
   };
-  // 1. attention RMSNorm, Q/K/V (+ bias), consecutive projections of one type per launch
-  if (!normed)
-    RF_LAUNCH(launch_rmsnorm_rows(m->p_h, static_cast<const float*>(L.attn_norm.d), d, nt, d, eps, m->p_xn, st),
-              "prefill attn norm");
-  const DevTensor* qkv[3] = {&L.q, &L.k, &L.v};
-  const DevTensor* bias[3] = {&L.bq, &L.bk, &L.bv};
-  float* outs[3] = {m->p_q, m->p_k, m->p_v};
-  const uint64_t rows[3] = {qd, kvd, kvd};
-  for (int i = 0; i < 3;) {
-    MmSegDesc segs[3];
-    int n = 0;
-    const uint32_t t = qkv[i]->type;
-    while (i < 3 && qkv[i]->type == t) {
-      const float* b = bias[i]->present() ? static_cast<const float*>(bias[i]->d) : nullptr;
-      segs[n++] = MmSegDesc{qkv[i]->d, qkv[i]->ne1, 0, rows[i], outs[i], nullptr, b, rows[i]};
-      ++i;
+  if (part != 1) {
+    // 1. attention RMSNorm, Q/K/V (+ bias), consecutive projections of one type per launch
+    if (!normed)
+      RF_LAUNCH(launch_rmsnorm_rows(m->p_h, static_cast<const float*>(L.attn_norm.d), d, nt, d, eps, m->p_xn, st),
+                "prefill attn norm");
+    const DevTensor* qkv[3] = {&L.q, &L.k, &L.v};
+    const DevTensor* bias[3] = {&L.bq, &L.bk, &L.bv};
+    float* outs[3] = {m->p_q, m->p_k, m->p_v};
+    const uint64_t rows[3] = {qd, kvd, kvd};
+    for (int i = 0; i < 3;) {
+      MmSegDesc segs[3];
+      int n = 0;
+      const uint32_t t = qkv[i]->type;
+      while (i < 3 && qkv[i]->type == t) {
+        const float* b = bias[i]->present() ? static_cast<const float*>(bias[i]->d) : nullptr;
+        segs[n++] = MmSegDesc{qkv[i]->d, qkv[i]->ne1, 0, rows[i], outs[i], nullptr, b, rows[i]};
+        ++i;
+      }
+      RF_LAUNCH(mm(segs, n, t, m->p_xn, d, EPI_STORE), "prefill qkv");
     }
-    RF_LAUNCH(mm(segs, n, t, m->p_xn, d, EPI_STORE), "prefill qkv");
+    // 2. RoPE of q and k, K/V cache rows pos0 .. pos0 + nt - 1
+    float* kc = m->k_cache + li * m->kv_cap * kvd;
+    float* vc = m->v_cache + li * m->kv_cap * kvd;
+    RF_LAUNCH(launch_rope_kv_rows(m->p_q, m->p_k, m->p_v, m->rope, pos0, nt, (uint32_t)c.head_count,
+                                  (uint32_t)c.head_count_kv, (uint32_t)hd, m->p_qr, kc, vc, st),
+              "prefill rope");
+    // 3. attention of every token over positions 0 .. its own
+    AttnArgs a{};
+    a.q = m->p_qr; a.k_hist = kc; a.v_hist = vc; a.out = m->p_a; a.ws = m->p_att;
+    a.hist = (uint32_t)pos0; a.ntok = (uint32_t)nt;
+    a.qh = (uint32_t)c.head_count; a.kvh = (uint32_t)c.head_count_kv; a.hd = (uint32_t)hd;
+    // The matrix-core kernel: 16-token tiles x KV heads x position splits.
+    // Otherwise the decode split kernel with a token dimension: nt x kvh
+    // workgroups, one per KV head (its query heads share each K/V row read)
+    // and chunks of up to ATT_MAX_CHUNK positions, so up to 1024 positions
+    // need no merge.
+    a.per_q = 0;
+    a.nsplit = prefill_attention_mfma_supported(a.qh, a.kvh, a.hd, pos0 + nt)
+                   ? prefill_attention_mfma_splits(pos0 + nt, nt, a.kvh)
+                   : prefill_attn_splits(pos0 + nt);
+    a.waves = attention_waves(att_chunk_positions(pos0 + nt, a.nsplit), 0);
+    a.denom = sqrtf((float)hd);
+    RF_LAUNCH(launch_attention(a, st), "prefill attention");
+    // 4. o-proj + residual, with the ffn RMSNorm
+    MmSegDesc so{L.o.d, L.o.ne1, 0, d, m->p_h, m->p_h, nullptr, d};
+    RF_LAUNCH(mm(&so, 1, L.o.type, m->p_a, qd, EPI_RESIDUAL, static_cast<const float*>(L.ffn_norm.d)),
+              "prefill o-proj + ffn norm");
   }
-  // 2. RoPE of q and k, K/V cache rows pos0 .. pos0 + nt - 1
-  float* kc = m->k_cache + li * m->kv_cap * kvd;
-  float* vc = m->v_cache + li * m->kv_cap * kvd;
-  RF_LAUNCH(launch_rope_kv_rows(m->p_q, m->p_k, m->p_v, m->rope, pos0, nt, (uint32_t)c.head_count,
-                                (uint32_t)c.head_count_kv, (uint32_t)hd, m->p_qr, kc, vc, st),
-            "prefill rope");
-  // 3. attention of every token over positions 0 .. its own
-  AttnArgs a{};
-  a.q = m->p_qr; a.k_hist = kc; a.v_hist = vc; a.out = m->p_a; a.ws = m->p_att;
-  a.hist = (uint32_t)pos0; a.ntok = (uint32_t)nt;
-  a.qh = (uint32_t)c.head_count; a.kvh = (uint32_t)c.head_count_kv; a.hd = (uint32_t)hd;
-  // The matrix-core kernel: 16-token tiles x KV heads x position splits.
-  // Otherwise the decode split kernel with a token dimension: nt x kvh
-  // workgroups, one per KV head (its query heads share each K/V row read)
-  // and chunks of up to ATT_MAX_CHUNK positions, so up to 1024 positions
-  // need no merge.
-  a.per_q = 0;
-  a.nsplit = prefill_attention_mfma_supported(a.qh, a.kvh, a.hd, pos0 + nt)
-                 ? prefill_attention_mfma_splits(pos0 + nt, nt, a.kvh)
-                 : prefill_attn_splits(pos0 + nt);
-  a.waves = attention_waves(att_chunk_positions(pos0 + nt, a.nsplit), 0);
-  a.denom = sqrtf((float)hd);
-  RF_LAUNCH(launch_attention(a, st), "prefill attention");
-  // 4. o-proj + residual, with the ffn RMSNorm
-  MmSegDesc so{L.o.d, L.o.ne1, 0, d, m->p_h, m->p_h, nullptr, d};
-  RF_LAUNCH(mm(&so, 1, L.o.type, m->p_a, qd, EPI_RESIDUAL, static_cast<const float*>(L.ffn_norm.d)),
-            "prefill o-proj + ffn norm");
-  // 5. gate/up, SiLU(gate) * up
-  MmSegDesc sg[2] = {MmSegDesc{L.gate.d, L.gate.ne1, 0, f, m->p_act, nullptr, nullptr, f},
-                     MmSegDesc{L.up.d, L.up.ne1, 0, f, m->p_up, nullptr, nullptr, f}};
-  if (L.gate.type == L.up.type) {
-    RF_LAUNCH(mm(sg, 2, L.gate.type, m->p_xn, d, EPI_SWIGLU), "prefill gate/up");
-  } else {
-    RF_LAUNCH(mm(&sg[0], 1, L.gate.type, m->p_xn, d, EPI_STORE), "prefill gate");
-    RF_LAUNCH(mm(&sg[1], 1, L.up.type, m->p_xn, d, EPI_STORE), "prefill up");
-    RF_LAUNCH(launch_binary(BIN_SWIGLU, m->p_act, m->p_up, nt * f, m->p_act, st), "prefill swiglu");
+  if (part != 0) {
+    // 5. gate/up, SiLU(gate) * up
+    MmSegDesc sg[2] = {MmSegDesc{L.gate.d, L.gate.ne1, 0, f, m->p_act, nullptr, nullptr, f},
+                       MmSegDesc{L.up.d, L.up.ne1, 0, f, m->p_up, nullptr, nullptr, f}};
+    if (L.gate.type == L.up.type) {
+      RF_LAUNCH(mm(sg, 2, L.gate.type, m->p_xn, d, EPI_SWIGLU), "prefill gate/up");
+    } else {
+      RF_LAUNCH(mm(&sg[0], 1, L.gate.type, m->p_xn, d, EPI_STORE), "prefill gate");
+      RF_LAUNCH(mm(&sg[1], 1, L.up.type, m->p_xn, d, EPI_STORE), "prefill up");
+      RF_LAUNCH(launch_binary(BIN_SWIGLU, m->p_act, m->p_up, nt * f, m->p_act, st), "prefill swiglu");
+    }
+    // 6. down + residual (with the next layer's attention RMSNorm)
+    MmSegDesc sd{L.down.d, L.down.ne1, 0, d, m->p_h, m->p_h, nullptr, d};
+    RF_LAUNCH(mm(&sd, 1, L.down.type, m->p_act, f, EPI_RESIDUAL, next_norm), "prefill down");
   }
-  // 6. down + residual (with the next layer's attention RMSNorm)
-  MmSegDesc sd{L.down.d, L.down.ne1, 0, d, m->p_h, m->p_h, nullptr, d};
-  RF_LAUNCH(mm(&sd, 1, L.down.type, m->p_act, f, EPI_RESIDUAL, next_norm), "prefill down");
   return RF_OK;
 }
 
@@ -1795,6 +1898,12 @@ int32_t prefill_tokens(rf_model* m, const uint32_t* tokens, uint64_t n) {
     RF_LAUNCH(launch_dequant_rows(m->token_embd.type, m->token_embd.d, d, nt, m->p_h, m->p_tok, c.vocab_size, st),
               "prefill embedding");
     for (uint32_t li = 0; li < nl; ++li) {
+      if (m->streaming && m->half_units) {
+        rc = forward_layer_halves(
+            m, li, [&](int part) { return enqueue_prefill_layer(m, li, pos0, nt, false, nullptr, part); });
+        if (rc) return rc;
+        continue;
+      }
       m->cur_layer = li;
       if (m->streaming) {  // as enqueue_forward: this layer resident, the next one's upload started
         if ((rc = acquire_layer(m, li, false))) return abort_pass(m, rc);
@@ -1944,14 +2053,16 @@ void rf_model_destroy(rf_model* m) {
   hipStreamSynchronize(m->ctx->compute);
   hipStreamSynchronize(m->ctx->copy);
   hipStreamSynchronize(m->ctx->copy2);
-  for (uint32_t li = 0; li < m->res.size(); ++li) {
-    layer_free(m, li);
+  for (uint32_t u = 0; u < m->res.size(); ++u) {
+    layer_free(m, u);
+    if (m->res[u].uploaded) hipEventDestroy(m->res[u].uploaded);
+    if (m->res[u].used) hipEventDestroy(m->res[u].used);
+  }
+  for (Layer& L : m->layers) {
     DevTensor* t[12];
-    layer_slots(m->layers[li], t);
+    layer_slots(L, t);
     for (DevTensor* x : t)
       if (x->host) hipHostFree(x->host);
-    if (m->res[li].uploaded) hipEventDestroy(m->res[li].uploaded);
-    if (m->res[li].used) hipEventDestroy(m->res[li].used);
   }
   if (m->up2) hipEventDestroy(m->up2);
   for (auto it = m->charges.rbegin(); it != m->charges.rend(); ++it) vram_release(m->ctx, *it);
@@ -2273,7 +2384,7 @@ int32_t rf_model_enable_streaming(rf_model* m, uint64_t layer_cache_bytes) {
     for (DevTensor* x : t)
       if (x->present()) return set_error(RF_ERR_INVALID, "layer streaming must be enabled before block tensors load");
   }
-  m->res.resize(m->layers.size());
+  m->res.resize(unit_count(m));
   for (LayerRes& R : m->res) {
     hipError_t e = hipEventCreateWithFlags(&R.uploaded, hipEventDisableTiming);
     if (e == hipSuccess) e = hipEventCreateWithFlags(&R.used, hipEventDisableTiming);
@@ -2454,6 +2565,43 @@ int32_t rf_model_set_cache_policy(rf_model* m, int32_t policy) {
   if (!m) return set_error(RF_ERR_INVALID, "null model");
   if (policy != 0 && policy != 1) return set_error(RF_ERR_INVALID, "unknown layer cache policy %d", policy);
   m->cache_policy = policy;
+  return RF_OK;
+}
+
+int32_t rf_model_set_stream_units(rf_model* m, int32_t half) {
+  if (!m) return set_error(RF_ERR_INVALID, "null model");
+  if (half != 0 && half != 1) return set_error(RF_ERR_INVALID, "unknown streaming unit %d", half);
+  if (!m->streaming) return set_error(RF_ERR_INVALID, "streaming units need layer streaming (rf_model_enable_streaming)");
+  if ((half != 0) == m->half_units) return RF_OK;
+  // every resident unit is released (waiting for its kernels), then the
+  // residency records are rebuilt for the new units
+  ra_stop(m);
+  const hipError_t se = hipStreamSynchronize(m->ctx->compute);
+  if (se != hipSuccess) return hip_error(se, "hipStreamSynchronize");
+  for (uint32_t u = 0; u < m->res.size(); ++u) {
+    const int32_t rc = layer_free(m, u);
+    if (rc) return rc;
+  }
+  const size_t n = m->layers.size() * (half ? 2 : 1);
+  while (m->res.size() > n) {
+    LayerRes& R = m->res.back();
+    if (R.uploaded) hipEventDestroy(R.uploaded);
+    if (R.used) hipEventDestroy(R.used);
+    m->res.pop_back();
+  }
+  while (m->res.size() < n) {
+    m->res.emplace_back();
+    LayerRes& R = m->res.back();
+    hipError_t e = hipEventCreateWithFlags(&R.uploaded, hipEventDisableTiming);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&R.used, hipEventDisableTiming);
+    if (e != hipSuccess) return hip_error(e, "hipEventCreate");
+  }
+  for (LayerRes& R : m->res) R.state = LAYER_HOST;
+  m->lru.clear();
+  m->cache_used = 0;
+  m->half_units = half != 0;
+  m->cur_layer = 0;
+  for (uint32_t li = 0; li < m->layers.size(); ++li) update_layer_bytes(m, li);
   return RF_OK;
 }
 

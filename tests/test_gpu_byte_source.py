@@ -158,6 +158,47 @@ def _layer_bytes(T, i):
     return sum(np.asarray(a).nbytes for n, (_, _, _, a) in T.items() if n.startswith(f"blk.{i}."))
 
 
+@pytest.mark.parametrize("read_ahead", [True, False])
+def test_half_units_from_file_source(ctx, tmp_path, read_ahead):
+    """Half units (attention tensors with the norms; gate, up, down) read
+    from the library's file source, with and without read-ahead, through a
+    cache of one and a half layers: hidden state and greedy tokens equal the
+    pinned tier's with whole layers bit for bit, with fewer bytes uploaded."""
+    rf = _rf()
+    cfg = STREAM_CFG
+    T = _tiny_tensors(np.random.default_rng(1460), cfg, STREAM_TYPES, bias=True)
+    blob, spans = _layout(T)
+    path = tmp_path / "model.bin"
+    blob.tofile(path)
+    cache = _layer_bytes(T, 0) * 3 // 2
+    prompt = [5, 60, 2, 41]
+    src = rf.FileSource(str(path), threads=2)
+    src.spans = spans
+    m = _sourced_model(ctx, cfg, T, src, 1 << 20, cache_bytes=cache)
+    try:
+        m.set_cache_policy(1)
+        m.set_stream_units(True)
+        m.set_read_ahead(read_ahead)
+        h = m.forward(prompt[0], 0, want_hidden=True)
+        m.reset()
+        toks = m.generate(prompt, 12)
+        up_half = m.residency_stats()["uploaded_bytes"]
+    finally:
+        m.close()
+        src.close()
+    pm = _pinned_model(cfg, T, cache_bytes=cache)
+    pm.set_cache_policy(1)
+    hp = pm.forward(prompt[0], 0, want_hidden=True)
+    pm.reset()
+    tp = pm.generate(prompt, 12)
+    up_whole = pm.residency_stats()["uploaded_bytes"]
+    pm.close()
+    pm.ctx.close()
+    assert np.array_equal(h, hp)
+    assert toks == tp
+    assert up_half < up_whole, (up_half, up_whole)
+
+
 @pytest.mark.parametrize("kind", ["file_source", "python_source"])
 @pytest.mark.parametrize("cached_layers", [0, 2])
 def test_read_ahead_matches_pinned_streaming(ctx, tmp_path, kind, cached_layers):

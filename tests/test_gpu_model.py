@@ -543,6 +543,108 @@ def test_next_use_policy_keeps_what_fits(ctx):
     sctx.close()
 
 
+def test_half_units_match_resident_model(ctx):
+    """Layers streamed in halves (attention tensors with both norms; gate,
+    up, down) through an LRU cache of one and a half layers under a VRAM
+    budget: bit-identical logits per forward and the same greedy tokens as
+    the resident model; the batched prefill equals the whole-layer streamed
+    one bit for bit; charges keep their per-tensor names; the ledger stays
+    within the budget and returns to the model's own buffers."""
+    rng = np.random.default_rng(1240)
+    T = _tiny_tensors(rng, STREAM_CFG, STREAM_TYPES, bias=True)
+    prompt = [3, 14, 15, 92]
+    ref_logits, ref_toks = _resident_reference(ctx, STREAM_CFG, T, prompt, 10)
+    lb = max(_layer_bytes(T, i) for i in range(4))
+    probe_ctx, probe = _streaming_model(STREAM_CFG, T, 0, 0)
+    base = probe_ctx.vram_used
+    probe.close()
+    probe_ctx.close()
+    budget = base + 2 * lb + 4096
+    sctx, sm = _streaming_model(STREAM_CFG, T, budget, lb + lb // 2)
+    sm.set_stream_units(True)
+    names = ("attn_q.weight", "ffn_gate.weight")
+    for p, tok in enumerate(prompt):
+        sm.forward(tok, p)
+        got = sm.logits()
+        assert np.array_equal(got.view(np.uint32), ref_logits[p].view(np.uint32)), p
+        active = [(i, n) for i in range(4) for n in names if sctx.charge(f"layer:{i}:{n}") is not None]
+        assert not active, active
+    cached = [(i, n) for i in range(4) for n in names if sctx.charge(f"cache:layer:{i}:{n}") is not None]
+    assert cached, "nothing cached"
+    sm.reset()
+    assert sm.generate(prompt, 10) == ref_toks
+    st = sm.residency_stats()
+    passes = len(prompt) + len(prompt) + 9
+    assert st["hits"] + st["misses"] == 8 * passes  # two units per layer and pass
+    assert sctx.vram_peak <= budget
+    sm.close()
+    assert sctx.vram_used == sctx.base_used
+    sctx.close()
+    # batched prefill (its workspace needs more than that budget): the same
+    # hidden state and logits as with whole layers
+    sctx, sm = _streaming_model(STREAM_CFG, T, 0, lb + lb // 2)
+    sm.set_stream_units(True)
+    h_half = sm.prefill(prompt, want_hidden=True)
+    l_half = sm.logits()
+    sm.set_stream_units(False)  # releases every resident unit
+    assert not [(i, n) for i in range(4) for n in names
+                if sctx.charge(f"cache:layer:{i}:{n}") is not None or sctx.charge(f"layer:{i}:{n}") is not None]
+    sm.reset()
+    h_whole = sm.prefill(prompt, want_hidden=True)
+    assert np.array_equal(h_half.view(np.uint32), h_whole.view(np.uint32))
+    assert np.array_equal(l_half.view(np.uint32), sm.logits().view(np.uint32))
+    sm.close()
+    sctx.close()
+
+
+def test_half_units_next_use_streams_fewer_bytes(ctx):
+    """Next-use policy with a cache of two and a half layers: with whole
+    layers two layers stream every pass; with half units the cache also keeps
+    part of a third layer, so fewer bytes are uploaded, with the resident
+    model's tokens either way."""
+    rng = np.random.default_rng(1241)
+    T = _tiny_tensors(rng, STREAM_CFG, STREAM_TYPES)
+    prompt = [9, 8, 7]
+    _, ref_toks = _resident_reference(ctx, STREAM_CFG, T, prompt, 8)
+    lb = max(_layer_bytes(T, i) for i in range(4))
+    st = {}
+    for half in (False, True):
+        sctx, sm = _streaming_model(STREAM_CFG, T, 0, lb * 5 // 2)
+        sm.set_cache_policy(1)
+        sm.set_stream_units(half)
+        assert sm.generate(prompt, 8) == ref_toks, half
+        st[half] = sm.residency_stats()
+        sm.close()
+        sctx.close()
+    print(f"  whole layers {st[False]}; half units {st[True]}", flush=True)
+    assert st[False]["cached_layers"] == 2
+    assert st[True]["cached_bytes"] > st[False]["cached_bytes"]
+    assert st[True]["uploaded_bytes"] < st[False]["uploaded_bytes"]
+
+
+def test_stream_units_validation(ctx):
+    rf = _rf()
+    rng = np.random.default_rng(1242)
+    T = _tiny_tensors(rng, STREAM_CFG, STREAM_TYPES)
+    gm = _load_gpu(ctx, STREAM_CFG, T, 40)
+    with pytest.raises(rf.RamforgeError, match="layer streaming"):
+        gm.set_stream_units(True)
+    gm.close()
+    sctx, sm = _streaming_model(STREAM_CFG, T, 0, 1 << 30)
+    with pytest.raises(rf.RamforgeError, match="unknown streaming unit"):
+        rf._lib.check(sctx.lib.rf_model_set_stream_units(sm.handle, 2))
+    sm.forward(5, 0)
+    assert all(sctx.charge(f"cache:layer:{i}:attn_q.weight") is not None for i in range(4))
+    sm.set_stream_units(True)  # releases every resident layer
+    for i in range(4):
+        assert sctx.charge(f"cache:layer:{i}:attn_q.weight") is None
+    sm.forward(6, 1)
+    assert sm.residency_stats()["cached_layers"] == 8  # units
+    sm.close()
+    assert sctx.vram_used == sctx.base_used
+    sctx.close()
+
+
 def test_streaming_without_cache_releases_every_layer(ctx):
     rng = np.random.default_rng(1235)
     T = _tiny_tensors(rng, STREAM_CFG, STREAM_TYPES)
