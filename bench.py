@@ -433,7 +433,7 @@ def pinned_h2d_gbs(ctx, nbytes: int = 256 << 20, reps: int = 8) -> float:
 
 
 def config5_bench(rf, syn, tokens: int, prompt_len: int, policy: int, persistent: int = 0,
-                  model_file=None, half_units: bool = False) -> dict:
+                  model_file=None, units: int = 1) -> dict:
     """8B shape, Q4_K body + Q6_K output, VRAM budget 4 GiB:
     the layers that do not fit stream from pinned host memory each token
     (layer cache on the device with LRU or next-use eviction, uploads on the
@@ -445,9 +445,10 @@ def config5_bench(rf, syn, tokens: int, prompt_len: int, policy: int, persistent
     layer load through the library's pread reader instead of kept in pinned
     host memory; the model's worker thread reads the next layer to load into
     one of two pinned layer buffers while the pass runs (read-ahead, on by
-    default for that reader).  half_units: the cache's unit is half a layer
-    (attention tensors with the norms; gate, up, down), so the budget also
-    keeps part of a layer (rf_model_set_stream_units)."""
+    default for that reader).  units: streaming units per layer (2:
+    attention tensors with the norms | gate, up, down; 3: attention | gate,
+    up | down), so the budget also keeps part of a layer
+    (rf_model_set_stream_units)."""
     import numpy as np
 
     cfg = syn.CONFIG_8B
@@ -465,8 +466,8 @@ def config5_bench(rf, syn, tokens: int, prompt_len: int, policy: int, persistent
     else:
         m = syn.build_file_model(ctx, cfg, specs, model_file[0], model_file[1], cfg["context_length"], budget,
                                  cache_policy=policy, kv_initial=prompt_len, persistent_policy=persistent)
-    if half_units:
-        m.set_stream_units(True)
+    if units > 1:
+        m.set_stream_units(units)
     fixed = ctx.vram_used
     layer = syn.weight_bytes([s for s in specs if s.name.startswith("blk.0.")])
     log(f"config 5: built in {time.perf_counter() - t0:.1f} s; fixed VRAM {fixed / 1e9:.2f} GB, "
@@ -490,7 +491,7 @@ def config5_bench(rf, syn, tokens: int, prompt_len: int, policy: int, persistent
                        f"{where}, KV cache grown in 256-position chunks",
            "pinned_host_bytes": m.host_bytes(),
            "cache_policy": ["lru", "next-use"][policy],
-           "stream_unit": "half layer" if half_units else "layer",
+           "stream_units_per_layer": units,
            "persistent": {0: "embedding and output resident (25% rule)",
                           3: "embedding in mapped host memory, output resident"}[persistent],
            "tokens": tokens, "tok_s": round(tokens / wall, 3),
@@ -663,8 +664,8 @@ def main() -> int:
     if args.matvec_probe:
         return matvec_probe(rf, args.matvec_probe)
     if args.config5:
-        res = [config5_bench(rf, syn, args.config5, args.prompt, policy, persistent, half_units=half)
-               for policy, persistent, half in ((1, 3, True), (1, 3, False), (1, 0, False), (0, 0, False))]
+        res = [config5_bench(rf, syn, args.config5, args.prompt, policy, persistent, units=k)
+               for policy, persistent, k in ((1, 3, 2), (1, 3, 1), (1, 0, 1), (0, 0, 1))]
         # the same model with its block tensors read from a model file
         import shutil
         import tempfile
@@ -680,9 +681,9 @@ def main() -> int:
                     spans = syn.write_model_file(wctx, specs5, path)
                 log(f"config 5: wrote {need / 1e9:.2f} GB of block tensors to {path} in "
                     f"{time.perf_counter() - t0:.1f} s")
-                for half in (True, False):
+                for k in (2, 1):
                     res.append(config5_bench(rf, syn, args.config5, args.prompt, 1, 3, model_file=(path, spans),
-                                             half_units=half))
+                                             units=k))
             else:
                 log("config 5: not enough free disk for the model file; file-read row skipped")
         finally:

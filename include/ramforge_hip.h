@@ -437,16 +437,16 @@ int32_t rf_model_enable_streaming(rf_model *model, uint64_t layer_cache_bytes);
  * needed later than every cached one is released instead of cached).  No
  * counterpart in the reference for policy 1. */
 int32_t rf_model_set_cache_policy(rf_model *model, int32_t policy);
-/* Unit of layer streaming: 0 = a whole layer (the reference's LayerCache
- * entry, the default); 1 = half a layer: layer i's attention tensors with
- * both norms, and its feed-forward matrices (gate, up, down), each loaded,
- * cached and evicted on its own, so a budget that holds part of a layer keeps
- * that part; the pass acquires the feed-forward half while the attention
- * half's kernels run.  Charges keep their names ("layer:{i}:{tensor}",
- * "cache:layer:{i}:{tensor}"); residency stats and the cache count units.
- * Needs layer streaming; releases every resident unit.  No counterpart in the
- * reference. */
-int32_t rf_model_set_stream_units(rf_model *model, int32_t half);
+/* Units of layer streaming per layer: 1 = the whole layer (the reference's
+ * LayerCache entry, the default); 2 = the attention tensors with both norms,
+ * then the feed-forward matrices (gate, up, down); 3 = the attention part,
+ * then gate and up, then down.  Each unit is loaded, cached and evicted on
+ * its own, so a budget that holds part of a layer keeps that part; the pass
+ * acquires each unit while the previous one's kernels run.  Charges keep
+ * their names ("layer:{i}:{tensor}", "cache:layer:{i}:{tensor}"); residency
+ * stats and the cache count units.  Needs layer streaming; releases every
+ * resident unit.  No counterpart in the reference. */
+int32_t rf_model_set_stream_units(rf_model *model, int32_t per_layer);
 /* out[6]: cache hits, misses (layer uploads), evictions, bytes uploaded,
  * bytes and layers currently cached. */
 int32_t rf_model_residency_stats(rf_model *model, uint64_t *out);

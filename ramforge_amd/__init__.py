@@ -641,11 +641,12 @@ class GpuLlamaModel:
         """0: least recently used (reference LayerCache); 1: next use in the layer cycle."""
         _lib.check(self.ctx.lib.rf_model_set_cache_policy(self.handle, policy))
 
-    def set_stream_units(self, half: bool) -> None:
-        """Streaming unit: False a whole layer (default); True half a layer
-        (attention tensors with the norms, and the feed-forward matrices),
-        loaded, cached and evicted separately (rf_model_set_stream_units)."""
-        _lib.check(self.ctx.lib.rf_model_set_stream_units(self.handle, 1 if half else 0))
+    def set_stream_units(self, per_layer: int) -> None:
+        """Streaming units per layer (rf_model_set_stream_units): 1 the whole
+        layer (default); 2 attention tensors with the norms | gate, up,
+        down; 3 attention | gate, up | down.  Units are loaded, cached and
+        evicted separately."""
+        _lib.check(self.ctx.lib.rf_model_set_stream_units(self.handle, int(per_layer)))
 
     def set_reader(self, source: "ByteSource", staging_bytes: int = 64 << 20) -> None:
         """Streamed layers read their declared tensors from `source`

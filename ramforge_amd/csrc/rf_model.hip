@@ -140,10 +140,10 @@ struct rf_model {
   std::list<uint32_t> lru;  // cached layers, most recently used first
   uint64_t st_hits = 0, st_misses = 0, st_evictions = 0, st_uploaded = 0;
   int cache_policy = 0;    // 0: LRU (LayerCache); 1: next use within the layer cycle
-  // Streaming unit (rf_model_set_stream_units): false, a whole layer (the
-  // reference's LayerCache entry); true, half a layer (unit_slots).  res,
-  // lru and cur_layer then count units.
-  bool half_units = false;
+  // Streaming units per layer (rf_model_set_stream_units): 1, the whole
+  // layer (the reference's LayerCache entry); 2 or 3, parts of it
+  // (unit_slots).  res, lru and cur_layer count units.
+  uint32_t upl = 1;
   uint32_t cur_layer = 0;  // streaming unit the forward pass is at (policy 1)
   // Byte source of streamed layers (rf_model_set_reader): ranges are read into
   // two pinned staging buffers of stage_bytes each and converted on the device
@@ -280,28 +280,30 @@ const char* slot_name(int i) {
   return n[i];
 }
 
-// Streaming units.  Whole layers: unit i = layer i.  Half units: unit 2i
-// holds layer i's attention tensors and both norms (the prefill's o-projection
-// applies the feed-forward norm), unit 2i + 1 its feed-forward matrices
-// (gate, up, down); the pass acquires the second while the first one's
-// kernels run.
-bool slot_in_ffn_unit(int i) { return i == 6 || i == 7 || i == 8; }
-
-uint32_t unit_count(const rf_model* m) {
-  return (uint32_t)m->layers.size() * (m->half_units ? 2u : 1u);
+// Streaming units.  With upl units per layer, unit upl i + p is part p of
+// layer i: upl 1, the whole layer; upl 2, the attention tensors with both
+// norms (the prefill's o-projection applies the feed-forward norm), then
+// the feed-forward matrices (gate, up, down); upl 3, the attention part,
+// then gate and up, then down.  The pass acquires each part while the
+// previous part's kernels run.
+uint32_t slot_part(uint32_t upl, int i) {
+  if (upl == 1 || i < 6 || i > 8) return 0;  // norms, attention, biases
+  return upl == 2 ? 1 : (i == 8 ? 2 : 1);     // gate, up | down
 }
 
-uint32_t unit_layer(const rf_model* m, uint32_t u) { return m->half_units ? u >> 1 : u; }
+uint32_t unit_count(const rf_model* m) { return (uint32_t)m->layers.size() * m->upl; }
 
-// The 12 tensor slots of unit u; with half units the other half's slots are
-// an empty tensor (not streamed, no buffer), which every streaming loop skips.
+uint32_t unit_layer(const rf_model* m, uint32_t u) { return u / m->upl; }
+
+// The 12 tensor slots of unit u; the slots of the layer's other parts are an
+// empty tensor (not streamed, no buffer), which every streaming loop skips.
 void unit_slots(rf_model* m, uint32_t u, DevTensor* out[12]) {
   layer_slots(m->layers[unit_layer(m, u)], out);
-  if (!m->half_units) return;
+  if (m->upl == 1) return;
   static DevTensor none;
-  const bool ffn = (u & 1u) != 0;
+  const uint32_t part = u % m->upl;
   for (int i = 0; i < 12; ++i)
-    if (slot_in_ffn_unit(i) != ffn) out[i] = &none;
+    if (slot_part(m->upl, i) != part) out[i] = &none;
 }
 
 // Charge of slot i of unit u while the unit is active ("layer:{layer}:{tensor}").
@@ -327,7 +329,7 @@ int32_t rename_unit(rf_model* m, uint32_t u, const std::string& from, const std:
 
 // Device bytes of each streaming unit of layer li.
 void update_layer_bytes(rf_model* m, uint32_t li) {
-  const uint32_t per = m->half_units ? 2u : 1u;
+  const uint32_t per = m->upl;
   for (uint32_t u = li * per; u < (li + 1) * per && u < m->res.size(); ++u) {
     DevTensor* t[12];
     unit_slots(m, u, t);
@@ -1507,22 +1509,33 @@ int32_t prof_group(rf_model* m, int kind, F&& body) {
   return RF_OK;
 }
 
-// Part 0: Q/K/V, attention, o-projection; part 1: gate/up, down.
-int32_t enqueue_layer_part(rf_model* m, size_t li, int part, int32_t* advance = nullptr) {
+// The launch groups of part p of a layer split into upl streaming units
+// (slot_part): group 0 Q/K/V, attention, o-projection; 1 gate/up; 2 down.
+void part_groups(uint32_t upl, uint32_t p, int* g0, int* g1) {
+  if (upl == 1) { *g0 = 0; *g1 = 2; }
+  else if (upl == 2) { *g0 = p == 0 ? 0 : 1; *g1 = p == 0 ? 0 : 2; }
+  else { *g0 = *g1 = (int)p; }
+}
+
+int32_t enqueue_layer_groups(rf_model* m, size_t li, int g0, int g1, int32_t* advance = nullptr) {
   int32_t rc;
-  if (part == 0) {
-    m->oproj_merge = false;
-    if ((rc = prof_group(m, 0, [&] { return enqueue_qkv(m, li); }))) return rc;
-    if ((rc = prof_group(m, 1, [&] { return enqueue_attention(m, li); }))) return rc;
-    return prof_group(m, 2, [&] { return enqueue_oproj(m, li); });
+  for (int g = g0; g <= g1; ++g) {
+    if (g == 0) {
+      m->oproj_merge = false;
+      if ((rc = prof_group(m, 0, [&] { return enqueue_qkv(m, li); }))) return rc;
+      if ((rc = prof_group(m, 1, [&] { return enqueue_attention(m, li); }))) return rc;
+      if ((rc = prof_group(m, 2, [&] { return enqueue_oproj(m, li); }))) return rc;
+    } else if (g == 1) {
+      if ((rc = prof_group(m, 3, [&] { return enqueue_gateup(m, li); }))) return rc;
+    } else {
+      if ((rc = prof_group(m, 4, [&] { return enqueue_down(m, li, advance); }))) return rc;
+    }
   }
-  if ((rc = prof_group(m, 3, [&] { return enqueue_gateup(m, li); }))) return rc;
-  return prof_group(m, 4, [&] { return enqueue_down(m, li, advance); });
+  return RF_OK;
 }
 
 int32_t enqueue_layer(rf_model* m, size_t li, int32_t* advance = nullptr) {
-  const int32_t rc = enqueue_layer_part(m, li, 0);
-  return rc ? rc : enqueue_layer_part(m, li, 1, advance);
+  return enqueue_layer_groups(m, li, 0, 2, advance);
 }
 
 // Algorithmic HBM bytes of one launch group of layer li (weights + vectors read
@@ -1546,35 +1559,34 @@ uint64_t part_bytes(rf_model* m, int kind, size_t li, uint64_t hist) {
   }
 }
 
-// Layer li of a streamed pass with half units (unit a = 2 li: attention,
-// unit f = a + 1: feed-forward).  Unit a is acquired, unit f's upload
-// started, and part 0's kernels wait for unit a only; unit f is then acquired
-// and the next layer's unit a requested before part 1's kernels wait for
-// unit f.  Both units are settled after part 1 (part 1 reads the
-// feed-forward norm of unit a).  With a byte source, reads run on this thread
-// between the parts, and the worker reads the next host-only unit meanwhile.
-// `part(p)` enqueues part p's kernels.
+// Layer li of a streamed pass split into upl units (unit upl li + p is part
+// p).  Each unit is acquired (a hit, or loaded if its upload was not started
+// yet), the next unit's upload started, and part p's kernels wait for unit p
+// only.  All the layer's units are settled after its last part (the
+// feed-forward kernels read the feed-forward norm, which the first unit
+// holds).  With a byte source, reads run on this thread between the parts,
+// and the worker reads the next host-only unit meanwhile.  `part(p)` enqueues
+// part p's kernels.
 template <class Part>
-int32_t forward_layer_halves(rf_model* m, uint32_t li, Part part) {
+int32_t forward_layer_units(rf_model* m, uint32_t li, Part part) {
   hipStream_t st = m->ctx->compute;
-  const uint32_t a = 2 * li, f = a + 1, nu = unit_count(m);
+  const uint32_t k = m->upl, first = k * li, nu = unit_count(m);
   const bool read_after = m->reader != nullptr;
   int32_t rc;
-  m->cur_layer = a;
-  if ((rc = acquire_layer(m, a, false))) return abort_pass(m, rc);
-  if (!read_after && (rc = acquire_layer(m, f, true))) return abort_pass(m, rc);
-  RF_LAUNCH(hipStreamWaitEvent(st, m->res[a].uploaded, 0), "wait for layer upload");
-  if ((rc = part(0))) return abort_pass(m, rc);
-  m->cur_layer = f;
-  if ((rc = acquire_layer(m, f, false))) return abort_pass(m, rc);
-  if (!read_after && f + 1 < nu && (rc = acquire_layer(m, f + 1, true))) return abort_pass(m, rc);
-  RF_LAUNCH(hipStreamWaitEvent(st, m->res[f].uploaded, 0), "wait for layer upload");
-  if ((rc = part(1))) return abort_pass(m, rc);
-  if ((rc = settle_layer(m, a))) return abort_pass(m, rc);
-  if ((rc = settle_layer(m, f))) return abort_pass(m, rc);
-  if (read_after && f + 1 < nu && (rc = acquire_layer(m, f + 1, true))) return abort_pass(m, rc);
+  for (uint32_t p = 0; p < k; ++p) {
+    const uint32_t u = first + p;
+    m->cur_layer = u;
+    if ((rc = acquire_layer(m, u, false))) return abort_pass(m, rc);
+    if (!read_after && u + 1 < nu && (rc = acquire_layer(m, u + 1, true))) return abort_pass(m, rc);
+    RF_LAUNCH(hipStreamWaitEvent(st, m->res[u].uploaded, 0), "wait for layer upload");
+    if ((rc = part(p))) return abort_pass(m, rc);
+  }
+  for (uint32_t p = 0; p < k; ++p)
+    if ((rc = settle_layer(m, first + p))) return abort_pass(m, rc);
+  const uint32_t next = first + k;
+  if (read_after && next < nu && (rc = acquire_layer(m, next, true))) return abort_pass(m, rc);
   if (read_after && m->ra.on) {
-    const int64_t nx = next_read_layer(m, f + 2);
+    const int64_t nx = next_read_layer(m, next + 1);
     if (nx >= 0) ra_post(m, (uint32_t)nx);
   }
   return RF_OK;
@@ -1591,10 +1603,12 @@ int32_t enqueue_forward(rf_model* m, bool embed = true) {
                                   c.vocab_size, st),
               "embedding");
   const uint32_t nl = (uint32_t)m->layers.size();
-  if (m->streaming && m->half_units) {
+  if (m->streaming && m->upl > 1) {
     for (uint32_t li = 0; li < nl; ++li) {
-      const int32_t rc = forward_layer_halves(m, li, [&](int part) {
-        return enqueue_layer_part(m, li, part, part == 1 && li + 1 == nl ? m->d_pos : nullptr);
+      const int32_t rc = forward_layer_units(m, li, [&](uint32_t p) {
+        int g0, g1;
+        part_groups(m->upl, p, &g0, &g1);
+        return enqueue_layer_groups(m, li, g0, g1, g1 == 2 && li + 1 == nl ? m->d_pos : nullptr);
       });
       if (rc) return rc;
     }
@@ -1789,10 +1803,10 @@ int32_t release_prefill_ws(rf_model* m) {
 // attention norm weights, produced with this layer's down projection (null
 // for the last layer, and when streaming: the next layer may still be
 // uploading).
-// Part 0: norm, Q/K/V, RoPE and K/V rows, attention, o-projection (with the
-// feed-forward norm); part 1: gate/up, down; -1: both.
+// Launch groups g0..g1: 0 norm, Q/K/V, RoPE and K/V rows, attention,
+// o-projection (with the feed-forward norm); 1 gate/up; 2 down.
 int32_t enqueue_prefill_layer(rf_model* m, size_t li, uint64_t pos0, uint64_t nt, bool normed,
-                              const float* next_norm, int part = -1) {
+                              const float* next_norm, int g0 = 0, int g1 = 2) {
   const rf_model_config& c = m->cfg;
   Layer& L = m->layers[li];
   hipStream_t st = m->ctx->compute;
@@ -1804,7 +1818,7 @@ int32_t enqueue_prefill_layer(rf_model* m, size_t li, uint64_t pos0, uint64_t nt
     return launch_matmul_packed(t, segs, n, x, in, nt, in, epi, m->p_part, m->p_part_floats, st, norm_w, eps,
                                 norm_w ? m->p_xn : nullptr);
   };
-  if (part != 1) {
+  if (g0 <= 0) {
     // 1. attention RMSNorm, Q/K/V (+ bias), consecutive projections of one type per launch
     if (!normed)
       RF_LAUNCH(launch_rmsnorm_rows(m->p_h, static_cast<const float*>(L.attn_norm.d), d, nt, d, eps, m->p_xn, st),
@@ -1852,7 +1866,7 @@ int32_t enqueue_prefill_layer(rf_model* m, size_t li, uint64_t pos0, uint64_t nt
     RF_LAUNCH(mm(&so, 1, L.o.type, m->p_a, qd, EPI_RESIDUAL, static_cast<const float*>(L.ffn_norm.d)),
               "prefill o-proj + ffn norm");
   }
-  if (part != 0) {
+  if (g0 <= 1 && g1 >= 1) {
     // 5. gate/up, SiLU(gate) * up
     MmSegDesc sg[2] = {MmSegDesc{L.gate.d, L.gate.ne1, 0, f, m->p_act, nullptr, nullptr, f},
                        MmSegDesc{L.up.d, L.up.ne1, 0, f, m->p_up, nullptr, nullptr, f}};
@@ -1863,6 +1877,8 @@ int32_t enqueue_prefill_layer(rf_model* m, size_t li, uint64_t pos0, uint64_t nt
       RF_LAUNCH(mm(&sg[1], 1, L.up.type, m->p_xn, d, EPI_STORE), "prefill up");
       RF_LAUNCH(launch_binary(BIN_SWIGLU, m->p_act, m->p_up, nt * f, m->p_act, st), "prefill swiglu");
     }
+  }
+  if (g1 >= 2) {
     // 6. down + residual (with the next layer's attention RMSNorm)
     MmSegDesc sd{L.down.d, L.down.ne1, 0, d, m->p_h, m->p_h, nullptr, d};
     RF_LAUNCH(mm(&sd, 1, L.down.type, m->p_act, f, EPI_RESIDUAL, next_norm), "prefill down");
@@ -1898,9 +1914,12 @@ int32_t prefill_tokens(rf_model* m, const uint32_t* tokens, uint64_t n) {
     RF_LAUNCH(launch_dequant_rows(m->token_embd.type, m->token_embd.d, d, nt, m->p_h, m->p_tok, c.vocab_size, st),
               "prefill embedding");
     for (uint32_t li = 0; li < nl; ++li) {
-      if (m->streaming && m->half_units) {
-        rc = forward_layer_halves(
-            m, li, [&](int part) { return enqueue_prefill_layer(m, li, pos0, nt, false, nullptr, part); });
+      if (m->streaming && m->upl > 1) {
+        rc = forward_layer_units(m, li, [&](uint32_t p) {
+          int g0, g1;
+          part_groups(m->upl, p, &g0, &g1);
+          return enqueue_prefill_layer(m, li, pos0, nt, false, nullptr, g0, g1);
+        });
         if (rc) return rc;
         continue;
       }
@@ -2568,11 +2587,12 @@ int32_t rf_model_set_cache_policy(rf_model* m, int32_t policy) {
   return RF_OK;
 }
 
-int32_t rf_model_set_stream_units(rf_model* m, int32_t half) {
+int32_t rf_model_set_stream_units(rf_model* m, int32_t per_layer) {
   if (!m) return set_error(RF_ERR_INVALID, "null model");
-  if (half != 0 && half != 1) return set_error(RF_ERR_INVALID, "unknown streaming unit %d", half);
+  if (per_layer < 1 || per_layer > 3)
+    return set_error(RF_ERR_INVALID, "streaming units per layer must be 1, 2 or 3, got %d", per_layer);
   if (!m->streaming) return set_error(RF_ERR_INVALID, "streaming units need layer streaming (rf_model_enable_streaming)");
-  if ((half != 0) == m->half_units) return RF_OK;
+  if ((uint32_t)per_layer == m->upl) return RF_OK;
   // every resident unit is released (waiting for its kernels), then the
   // residency records are rebuilt for the new units
   ra_stop(m);
@@ -2582,7 +2602,7 @@ int32_t rf_model_set_stream_units(rf_model* m, int32_t half) {
     const int32_t rc = layer_free(m, u);
     if (rc) return rc;
   }
-  const size_t n = m->layers.size() * (half ? 2 : 1);
+  const size_t n = m->layers.size() * (size_t)per_layer;
   while (m->res.size() > n) {
     LayerRes& R = m->res.back();
     if (R.uploaded) hipEventDestroy(R.uploaded);
@@ -2599,7 +2619,7 @@ int32_t rf_model_set_stream_units(rf_model* m, int32_t half) {
   for (LayerRes& R : m->res) R.state = LAYER_HOST;
   m->lru.clear();
   m->cache_used = 0;
-  m->half_units = half != 0;
+  m->upl = (uint32_t)per_layer;
   m->cur_layer = 0;
   for (uint32_t li = 0; li < m->layers.size(); ++li) update_layer_bytes(m, li);
   return RF_OK;

@@ -158,12 +158,14 @@ def _layer_bytes(T, i):
     return sum(np.asarray(a).nbytes for n, (_, _, _, a) in T.items() if n.startswith(f"blk.{i}."))
 
 
+@pytest.mark.parametrize("per_layer", [2, 3])
 @pytest.mark.parametrize("read_ahead", [True, False])
-def test_half_units_from_file_source(ctx, tmp_path, read_ahead):
-    """Half units (attention tensors with the norms; gate, up, down) read
-    from the library's file source, with and without read-ahead, through a
-    cache of one and a half layers: hidden state and greedy tokens equal the
-    pinned tier's with whole layers bit for bit, with fewer bytes uploaded."""
+def test_stream_units_from_file_source(ctx, tmp_path, read_ahead, per_layer):
+    """Layer parts as streaming units (2: attention tensors with the norms |
+    gate, up, down; 3: attention | gate, up | down) read from the library's
+    file source, with and without read-ahead, through a cache of one and a
+    half layers: hidden state and greedy tokens equal the pinned tier's with
+    whole layers bit for bit, with fewer bytes uploaded."""
     rf = _rf()
     cfg = STREAM_CFG
     T = _tiny_tensors(np.random.default_rng(1460), cfg, STREAM_TYPES, bias=True)
@@ -177,7 +179,7 @@ def test_half_units_from_file_source(ctx, tmp_path, read_ahead):
     m = _sourced_model(ctx, cfg, T, src, 1 << 20, cache_bytes=cache)
     try:
         m.set_cache_policy(1)
-        m.set_stream_units(True)
+        m.set_stream_units(per_layer)
         m.set_read_ahead(read_ahead)
         h = m.forward(prompt[0], 0, want_hidden=True)
         m.reset()

@@ -543,13 +543,15 @@ def test_next_use_policy_keeps_what_fits(ctx):
     sctx.close()
 
 
-def test_half_units_match_resident_model(ctx):
-    """Layers streamed in halves (attention tensors with both norms; gate,
-    up, down) through an LRU cache of one and a half layers under a VRAM
-    budget: bit-identical logits per forward and the same greedy tokens as
-    the resident model; the batched prefill equals the whole-layer streamed
-    one bit for bit; charges keep their per-tensor names; the ledger stays
-    within the budget and returns to the model's own buffers."""
+@pytest.mark.parametrize("per_layer", [2, 3])
+def test_stream_units_match_resident_model(ctx, per_layer):
+    """Layers streamed in parts (2: attention tensors with both norms | gate,
+    up, down; 3: attention | gate, up | down) through an LRU cache of one and
+    a half layers under a VRAM budget: bit-identical logits per forward and
+    the same greedy tokens as the resident model; the batched prefill equals
+    the whole-layer streamed one bit for bit; charges keep their per-tensor
+    names; the ledger stays within the budget and returns to the model's own
+    buffers."""
     rng = np.random.default_rng(1240)
     T = _tiny_tensors(rng, STREAM_CFG, STREAM_TYPES, bias=True)
     prompt = [3, 14, 15, 92]
@@ -561,8 +563,8 @@ def test_half_units_match_resident_model(ctx):
     probe_ctx.close()
     budget = base + 2 * lb + 4096
     sctx, sm = _streaming_model(STREAM_CFG, T, budget, lb + lb // 2)
-    sm.set_stream_units(True)
-    names = ("attn_q.weight", "ffn_gate.weight")
+    sm.set_stream_units(per_layer)
+    names = ("attn_q.weight", "ffn_gate.weight", "ffn_down.weight")
     for p, tok in enumerate(prompt):
         sm.forward(tok, p)
         got = sm.logits()
@@ -575,7 +577,7 @@ def test_half_units_match_resident_model(ctx):
     assert sm.generate(prompt, 10) == ref_toks
     st = sm.residency_stats()
     passes = len(prompt) + len(prompt) + 9
-    assert st["hits"] + st["misses"] == 8 * passes  # two units per layer and pass
+    assert st["hits"] + st["misses"] == 4 * per_layer * passes  # units per layer and pass
     assert sctx.vram_peak <= budget
     sm.close()
     assert sctx.vram_used == sctx.base_used
@@ -583,10 +585,10 @@ def test_half_units_match_resident_model(ctx):
     # batched prefill (its workspace needs more than that budget): the same
     # hidden state and logits as with whole layers
     sctx, sm = _streaming_model(STREAM_CFG, T, 0, lb + lb // 2)
-    sm.set_stream_units(True)
+    sm.set_stream_units(per_layer)
     h_half = sm.prefill(prompt, want_hidden=True)
     l_half = sm.logits()
-    sm.set_stream_units(False)  # releases every resident unit
+    sm.set_stream_units(1)  # releases every resident unit
     assert not [(i, n) for i in range(4) for n in names
                 if sctx.charge(f"cache:layer:{i}:{n}") is not None or sctx.charge(f"layer:{i}:{n}") is not None]
     sm.reset()
@@ -597,29 +599,30 @@ def test_half_units_match_resident_model(ctx):
     sctx.close()
 
 
-def test_half_units_next_use_streams_fewer_bytes(ctx):
+def test_stream_units_next_use_stream_fewer_bytes(ctx):
     """Next-use policy with a cache of two and a half layers: with whole
-    layers two layers stream every pass; with half units the cache also keeps
-    part of a third layer, so fewer bytes are uploaded, with the resident
-    model's tokens either way."""
+    layers two layers stream every pass; with two or three units per layer
+    the cache also keeps part of a third layer, so fewer bytes are uploaded,
+    with the resident model's tokens either way."""
     rng = np.random.default_rng(1241)
     T = _tiny_tensors(rng, STREAM_CFG, STREAM_TYPES)
     prompt = [9, 8, 7]
     _, ref_toks = _resident_reference(ctx, STREAM_CFG, T, prompt, 8)
     lb = max(_layer_bytes(T, i) for i in range(4))
     st = {}
-    for half in (False, True):
+    for k in (1, 2, 3):
         sctx, sm = _streaming_model(STREAM_CFG, T, 0, lb * 5 // 2)
         sm.set_cache_policy(1)
-        sm.set_stream_units(half)
-        assert sm.generate(prompt, 8) == ref_toks, half
-        st[half] = sm.residency_stats()
+        sm.set_stream_units(k)
+        assert sm.generate(prompt, 8) == ref_toks, k
+        st[k] = sm.residency_stats()
         sm.close()
         sctx.close()
-    print(f"  whole layers {st[False]}; half units {st[True]}", flush=True)
-    assert st[False]["cached_layers"] == 2
-    assert st[True]["cached_bytes"] > st[False]["cached_bytes"]
-    assert st[True]["uploaded_bytes"] < st[False]["uploaded_bytes"]
+        print(f"  {k} units per layer: {st[k]}", flush=True)
+    assert st[1]["cached_layers"] == 2
+    for k in (2, 3):
+        assert st[k]["cached_bytes"] > st[1]["cached_bytes"], k
+        assert st[k]["uploaded_bytes"] < st[1]["uploaded_bytes"], k
 
 
 def test_stream_units_validation(ctx):
@@ -628,18 +631,19 @@ def test_stream_units_validation(ctx):
     T = _tiny_tensors(rng, STREAM_CFG, STREAM_TYPES)
     gm = _load_gpu(ctx, STREAM_CFG, T, 40)
     with pytest.raises(rf.RamforgeError, match="layer streaming"):
-        gm.set_stream_units(True)
+        gm.set_stream_units(2)
     gm.close()
     sctx, sm = _streaming_model(STREAM_CFG, T, 0, 1 << 30)
-    with pytest.raises(rf.RamforgeError, match="unknown streaming unit"):
-        rf._lib.check(sctx.lib.rf_model_set_stream_units(sm.handle, 2))
+    for bad in (0, 4):
+        with pytest.raises(rf.RamforgeError, match="must be 1, 2 or 3"):
+            sm.set_stream_units(bad)
     sm.forward(5, 0)
     assert all(sctx.charge(f"cache:layer:{i}:attn_q.weight") is not None for i in range(4))
-    sm.set_stream_units(True)  # releases every resident layer
+    sm.set_stream_units(3)  # releases every resident layer
     for i in range(4):
         assert sctx.charge(f"cache:layer:{i}:attn_q.weight") is None
     sm.forward(6, 1)
-    assert sm.residency_stats()["cached_layers"] == 8  # units
+    assert sm.residency_stats()["cached_layers"] == 12  # units
     sm.close()
     assert sctx.vram_used == sctx.base_used
     sctx.close()
