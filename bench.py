@@ -586,12 +586,20 @@ def config4_bench(rf, syn, tokens: int = 128, prompt_len: int = 32) -> dict:
     ctx.synchronize()
     wall = time.perf_counter() - t0
     gen = m.read_tokens(tokens)
+    # per launch group: HIP events around back-to-back eager launches at the
+    # position the decode ended
+    m.use_graph(False)
+    groups = {}
+    for kind in ("qkv", "attention", "oproj", "gateup", "down", "logits"):
+        ms, b, _ = m.time_kernel(kind, 4)
+        groups[kind] = {"us_per_launch": round(ms * 1e3, 2), "bytes_per_launch": b,
+                        "kernel": m.kernel_name(kind) if kind != "attention" else ""}
     out = {"workload": "config 4: 16 layers, d 2048, 32/8 heads, FFN 8192, vocab 32000, Q8_0, resident",
            "prompt_tokens": prompt_len, "prompt_token_by_token_ms": round(tbt * 1e3, 2),
            "prompt_batched_ms": round(batched * 1e3, 2), "tokens": tokens, "tok_s": round(tokens / wall, 1),
            "ms_per_token": round(wall * 1e3 / tokens, 4), "weights_bytes_per_token": wbytes,
            "roofline_tok_s_at_peak": round(PEAK_HBM_GBS * 1e9 / wbytes, 1),
-           "tokens_head": gen[:8]}
+           "tokens_head": gen[:8], "per_group": groups}
     log(f"config 4: prompt {tbt * 1e3:.1f} ms token by token, {batched * 1e3:.1f} ms batched; "
         f"{out['tok_s']} tok/s decode ({out['ms_per_token']} ms/token; roofline {out['roofline_tok_s_at_peak']})")
     m.close()

@@ -374,7 +374,7 @@ struct PkStep {
 // is saved): per head, M = max of the chunks' m, factors f_c = exp(m_c - M),
 // L = sum of l_c f_c and x = (sum of f_c o_c) / L, taken as a product with
 // 1 / L.  Each thread merges half a unit (8 elements) over all chunks; the
-// launch sees to 2 nunit = NT and at most 8 chunks.
+// launch sees to 2 nunit <= NT and at most 8 chunks.
 template <uint32_t T, int EPI, bool NORM, int U, int LPW, int NB, int NT, bool IX, bool ALLF = false,
           bool MRG = false>
 __global__ __launch_bounds__(NT) void matvec_packed(PkArgs a) {
@@ -1224,7 +1224,7 @@ static hipError_t launch_pk_all(const PkArgs& a, uint32_t lds, hipStream_t st, b
 }
 
 // The single-step launch above with x merged from attention chunk records
-// (matvec_packed<..., MRG>): Q8_0 rows of 4 chunks, Q4_0 / Q4_K rows of 2,
+// (matvec_packed<..., MRG>): Q8_0 rows of 2 or 4 chunks, Q4_0 / Q4_K rows of 1 or 2,
 // with the MRG kernel's own occupancy and LDS (x, its unit sums, then the
 // records' factors and the heads' 1 / L).
 // hipErrorNotSupported when the shape does not take it;
@@ -1236,10 +1236,11 @@ static bool pk_merge_shape(uint32_t t, uint64_t in_dim, uint32_t nsplit, uint32_
     if (g_digits == 2) return false;  // digit planes everywhere: no float-x launch
   }
   const uint64_t nchunk = pk_nchunk(t, in_dim);
-  if (!((t == T_Q8_0 && nchunk == 4) || ((t == T_Q4_0 || t == T_Q4_K) && nchunk == 2))) return false;
+  if (!((t == T_Q8_0 && (nchunk == 2 || nchunk == 4)) || ((t == T_Q4_0 || t == T_Q4_K) && nchunk <= 2)))
+    return false;
   if (hd < 16 || (hd & (hd - 1)) != 0 || (uint64_t)qh * hd != in_dim) return false;
   if (nsplit < 1 || nsplit > 8 || qh > 64) return false;  // 8 lanes per head's chunk records
-  if (2 * nchunk * 64 * pk_epb(t) != 512) return false;  // two threads per unit of 16 elements
+  if (2 * nchunk * 64 * pk_epb(t) > 512) return false;  // two threads per unit of 16 elements
   const uint64_t l = p.lds_bytes + (uint64_t)nsplit * qh * 4 + (uint64_t)qh * 4;  // factors, 1 / L
   if (l + PK_STATIC_LDS > pk_lds_limit()) return false;
   *lds = (uint32_t)l;
@@ -1261,11 +1262,17 @@ static hipError_t launch_pk_merge(const PkArgs& a, uint32_t lds, bool launch, hi
   return hipGetLastError();
 }
 
+// LPW = the row's chunks (one step per row): Q8_0 rows of 2048 or 4096
+// inputs, Q4_0 / Q4_K rows of up to 4096.
 static hipError_t launch_pk_merge_t(uint32_t t, const PkArgs& a, uint32_t lds, bool launch, hipStream_t st) {
+  const uint64_t nchunk = pk_nchunk(t, a.in_dim);
   switch (t) {
-    case T_Q8_0: return launch_pk_merge<T_Q8_0, 4>(a, lds, launch, st);
-    case T_Q4_0: return launch_pk_merge<T_Q4_0, 2>(a, lds, launch, st);
-    case T_Q4_K: return launch_pk_merge<T_Q4_K, 2>(a, lds, launch, st);
+    case T_Q8_0:
+      return nchunk == 4 ? launch_pk_merge<T_Q8_0, 4>(a, lds, launch, st) : launch_pk_merge<T_Q8_0, 2>(a, lds, launch, st);
+    case T_Q4_0:
+      return nchunk == 2 ? launch_pk_merge<T_Q4_0, 2>(a, lds, launch, st) : launch_pk_merge<T_Q4_0, 1>(a, lds, launch, st);
+    case T_Q4_K:
+      return nchunk == 2 ? launch_pk_merge<T_Q4_K, 2>(a, lds, launch, st) : launch_pk_merge<T_Q4_K, 1>(a, lds, launch, st);
     default: return hipErrorNotSupported;
   }
 }
@@ -1277,6 +1284,7 @@ hipError_t pk_merge_supported(uint32_t t, uint64_t in_dim, uint64_t rows, uint32
     return hipErrorNotSupported;
   PkArgs a{};
   a.rows_total = (uint32_t)rows;
+  a.in_dim = (uint32_t)in_dim;
   return launch_pk_merge_t(t, a, lds, false, st);
 }
 

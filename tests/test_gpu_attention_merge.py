@@ -4,9 +4,11 @@
 o-projection, model_executor.rs:102-236).
 
 The models have 32 query heads of 128 dims (q_heads * head_dim = 4096, as
-the 8B shape) or 64 of 64, so the packed Q8_0 / Q4_0 / Q4_K o-projection
-takes the merged-x launch at every context the attention splits per query
-head (65 to 1024 positions here: 2 to 8 chunks, or to 4 with 64 heads).  The two modes differ in the merge's
+the 8B shape), 64 of 64, or 32 of 64 (2048 inputs, as BASELINE config 4:
+Q8_0 rows of two 1024-element chunks, Q4_0 / Q4_K rows of one), so the
+packed Q8_0 / Q4_0 / Q4_K o-projection takes the merged-x launch at every
+context the attention splits per query head (65 to 1024 positions here: 2 to
+8 chunks, or to 4 with 64 heads).  The two modes differ in the merge's
 rounding only: hidden states within 1e-5 of each other, both within 2e-4 of
 the oracle, and identical greedy tokens, eager and replayed from the decode
 graphs, across the launch regimes."""
@@ -22,6 +24,8 @@ CFG = dict(vocab_size=192, context_length=1100, embedding_length=256, block_coun
            head_count=32, head_count_kv=8, head_dim=128, rms_eps=1e-5, rope_freq_base=10000.0)
 # 64 heads of 64 dims: at most 4 chunks per query head (256 / 64), records of 68 floats
 CFG64 = dict(CFG, head_count=64, head_count_kv=16, head_dim=64)
+# 32 heads of 64 dims: a 2048-wide o-projection
+CFG2K = dict(CFG, head_count=32, head_count_kv=8, head_dim=64)
 CAP = 1100
 
 
@@ -39,8 +43,9 @@ def merge_mode():
 
 
 @pytest.mark.timeout(600)
-@pytest.mark.parametrize("o,cfg", [(Q8_0, CFG), (Q4_0, CFG), (Q4_K, CFG), (Q8_0, CFG64)],
-                         ids=["q8_0", "q4_0", "q4_k", "q8_0-hd64"])
+@pytest.mark.parametrize("o,cfg", [(Q8_0, CFG), (Q4_0, CFG), (Q4_K, CFG), (Q8_0, CFG64), (Q8_0, CFG2K),
+                                   (Q4_0, CFG2K), (Q4_K, CFG2K)],
+                         ids=["q8_0", "q4_0", "q4_k", "q8_0-hd64", "q8_0-2048", "q4_0-2048", "q4_k-2048"])
 def test_merged_oproj_matches_merge_kernel(ctx, orc, merge_mode, o, cfg):
     T = _tiny_tensors(np.random.default_rng(2400 + o), cfg, _types(o))
     import ramforge_amd as rf

@@ -529,10 +529,11 @@ def inflight_mode(request):
 
 @pytest.mark.parametrize("inflight_mode", [1, 0], indirect=True, ids=["inflight", "ring"])
 @pytest.mark.parametrize("t", PACKED)
-@pytest.mark.parametrize("out_dim,in_dim", [(4096, 4096), (1000, 4096), (2048, 4096)])
+@pytest.mark.parametrize("out_dim,in_dim", [(4096, 4096), (1000, 4096), (2048, 4096), (2048, 2048), (3072, 2048)])
 def test_matvec_packed_inflight_shapes(ctx, orc, inflight_mode, t, out_dim, in_dim):
     """in_dim 4096 launches with one row per wavefront (all requested before
-    the x prologue) and with the ring, against the oracle."""
+    the x prologue) and with the ring, against the oracle; rows of 2048
+    inputs (config 4's widths) take the ring in both modes."""
     _check_matvec_packed(ctx, orc, t, out_dim, in_dim, 2300 + t + out_dim)
     _check_matvec_packed(ctx, orc, t, out_dim, in_dim, 2310 + t + out_dim, row_start=7, row_count=out_dim - 20)
 
