@@ -144,21 +144,38 @@ __host__ __device__ inline uint64_t mm_row_bytes(uint32_t t, int k, uint64_t K) 
 // past the split) loads nothing.
 template <uint32_t T> struct MmW;
 
+// Q8_0: two steps per 16-byte load.  For steps 2p and 2p + 1 of a slice the
+// lanes of groups 0-1 load codes 16 (g & 1) .. + 15 of block 2p and groups 2-3
+// the same codes of block 2p + 1: 64 contiguous bytes of each of 16 rows per
+// instruction, half the load instructions of one 8-byte load per step.
+// prep(p) swaps the upper 32 lanes' first half with the lower 32 lanes'
+// second half (v_permlane32_swap), after which .xy is step 2p's operand and
+// .zw step 2p + 1's; lane group g then holds codes 8 mm_kperm(g) .. + 7 of
+// its block, and the x operand is read in the same K order.
+__device__ __forceinline__ uint32_t mm_kperm(uint32_t g) { return ((g & 1u) << 1) | (g >> 1); }
+
 template <> struct MmW<T_Q8_0> {
   static constexpr uint32_t NREG = 2;
-  uint2 c[MM_ST];
+  uint4 c[MM_ST / 2];
   uint2 sc;
   template <bool SC8>
   __device__ void load(const MmRsrc* rs, uint32_t row, uint32_t sl, uint32_t g, uint32_t nst, uint32_t K) {
-    const uint32_t cb = row * K + sl * MM_KS + 8u * g;
+    const uint32_t cb = row * K + sl * MM_KS + 32u * (g >> 1) + 16u * (g & 1u);
 #pragma unroll
-    for (uint32_t j = 0; j < MM_ST; ++j) c[j] = mm_ld8(rs[0], j < nst ? cb + 32u * j : MM_OOR);
+    for (uint32_t p = 0; p < MM_ST / 2; ++p) c[p] = mm_ld16(rs[0], 2u * p + (g >> 1) < nst ? cb + 64u * p : MM_OOR);
     mm_load_scales<SC8>(rs[1], (row * (K / 32u) + sl * MM_ST) * 2u, nst, sc);
   }
+  __device__ void prep(int p) {
+    const auto s0 = __builtin_amdgcn_permlane32_swap(c[p].x, c[p].z, false, false);
+    const auto s1 = __builtin_amdgcn_permlane32_swap(c[p].y, c[p].w, false, false);
+    c[p] = make_uint4(s0[0], s1[0], s0[1], s1[1]);
+  }
   __device__ void step(int j, uint32_t, bf16x8& b, float& d) const {
+    const uint4 w = c[j >> 1];
+    const uint2 q = (j & 1) ? make_uint2(w.z, w.w) : make_uint2(w.x, w.y);
     float v[8];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) v[k] = (float)(int)(int8_t)mm_byte(c[j], k);
+    for (int k = 0; k < 8; ++k) v[k] = (float)(int)(int8_t)mm_byte(q, k);
     b = mm_codes(v);
     d = rf_half_to_float_fast(mm_scale(sc, j));
   }
@@ -307,6 +324,7 @@ __global__ __launch_bounds__(64 * NW) void mm_packed(MmArgs a) {
   constexpr uint32_t BUF = 3 * PLANE + (T == T_Q4_K ? MM_ST * NT * 2 : 0);  // bf16 elements per buffer
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
   const uint32_t r16 = lane & 15u, g = lane >> 4;
+  const uint32_t gx = T == T_Q8_0 ? mm_kperm(g) : g;  // K order of the weight operand's lane groups
   MmSeg s = a.seg[0];
   if (a.nseg > 1 && blockIdx.x >= a.seg[1].group_begin) s = a.seg[1];
   if (a.nseg > 2 && blockIdx.x >= a.seg[2].group_begin) s = a.seg[2];
@@ -381,7 +399,7 @@ __global__ __launch_bounds__(64 * NW) void mm_packed(MmArgs a) {
   float4 xv[4];
   // Slice sl with weights w: the next slice's x and the weights of slice
   // sl + DEPTH - 1 (into the buffer slice sl - 1 used) are requested first.
-  auto run_slice = [&](uint32_t sl, const Wt& w, Wt& refill) {
+  auto run_slice = [&](uint32_t sl, Wt& w, Wt& refill) {
     const uint32_t cb = (sl - sl0) & 1u, nst = nsteps(sl);
     const bool more = sl + 1 < sl1;
     fetch_x(sl + 1, xv);
@@ -395,6 +413,9 @@ __global__ __launch_bounds__(64 * NW) void mm_packed(MmArgs a) {
       float d[2], e[2];
 #pragma unroll
       for (int rt = 0; rt < 2; ++rt) {
+        if constexpr (T == T_Q8_0) {
+          if ((j & 1) == 0) w[rt].prep(j >> 1);
+        }
         if constexpr (T == T_Q4_K) w[rt].step(j, g, b[rt], d[rt], e[rt]);
         else if constexpr (T == T_Q6_K) w[rt].step(j, g, b[rt], b2[rt], d[rt], e[rt]);
         else w[rt].step(j, g, b[rt], d[rt]);
@@ -406,7 +427,7 @@ __global__ __launch_bounds__(64 * NW) void mm_packed(MmArgs a) {
       bf16x8 ax[3][NTT];
 #pragma unroll
       for (int nt = 0; nt < NTT; ++nt) {
-        const __bf16* ap = xb + (nt * 16u + r16) * MM_XB + 32u * j + 8u * g;
+        const __bf16* ap = xb + (nt * 16u + r16) * MM_XB + 32u * j + 8u * gx;
 #pragma unroll
         for (int p = 0; p < 3; ++p) ax[p][nt] = *reinterpret_cast<const bf16x8*>(ap + p * PLANE);
       }
