@@ -259,10 +259,22 @@ uint64_t mm_part_floats_at(const uint64_t* rows, int nseg, uint64_t in_dim, uint
 // norm_w (EPI_RESIDUAL, one segment): also xn = RMSNorm(y) * norm_w per token
 // row (stride ld), the norm that follows a residual projection; fused into
 // the split-K reduce where the rows allow it, else a separate launch.
+// RoPE epilogue of a Q/K/V launch (EPI_STORE, segments q, k, v of qh hd,
+// kvh hd and kvh hd rows): the split-K reduce rotates q into qr[token] and k
+// into K cache row pos0 + token and copies v into V cache row pos0 + token,
+// with rope_kv_rows_kernel's arithmetic (the segments' own outputs are not
+// written).  rope = the [position][hd / 2][cos, sin] table.
+struct MmRope {
+  const float* rope;
+  uint32_t pos0, qh, kvh, hd;
+  float* qr;
+  float* kc;
+  float* vc;
+};
 hipError_t launch_matmul_packed(uint32_t t, const MmSegDesc* segs, int nseg, const float* x, uint64_t ldx,
                                 uint64_t n, uint64_t in_dim, int epi, float* part, uint64_t part_floats,
                                 hipStream_t st, const float* norm_w = nullptr, float eps = 0.f,
-                                float* xn = nullptr);
+                                float* xn = nullptr, const MmRope* rope = nullptr);
 hipError_t launch_rmsnorm_rows(const float* x, const float* w, uint64_t n, uint64_t rows, uint64_t ld, float eps,
                                float* y, hipStream_t st);
 hipError_t launch_rope_kv_rows(const float* q, const float* k, const float* v, const float* rope, uint64_t pos0,

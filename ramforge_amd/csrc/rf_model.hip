@@ -1814,9 +1814,9 @@ int32_t enqueue_prefill_layer(rf_model* m, size_t li, uint64_t pos0, uint64_t nt
   const uint64_t f = c.feed_forward_length;
   const float eps = c.rms_eps;
   auto mm = [&](const MmSegDesc* segs, int n, uint32_t t, const float* x, uint64_t in, int epi,
-                const float* norm_w = nullptr) {
+                const float* norm_w = nullptr, const MmRope* rope = nullptr) {
     return launch_matmul_packed(t, segs, n, x, in, nt, in, epi, m->p_part, m->p_part_floats, st, norm_w, eps,
-                                norm_w ? m->p_xn : nullptr);
+                                norm_w ? m->p_xn : nullptr, rope);
   };
   if (g0 <= 0) {
     // 1. attention RMSNorm, Q/K/V (+ bias), consecutive projections of one type per launch
@@ -1827,6 +1827,14 @@ int32_t enqueue_prefill_layer(rf_model* m, size_t li, uint64_t pos0, uint64_t nt
     const DevTensor* bias[3] = {&L.bq, &L.bk, &L.bv};
     float* outs[3] = {m->p_q, m->p_k, m->p_v};
     const uint64_t rows[3] = {qd, kvd, kvd};
+    float* kc = m->k_cache + li * m->kv_cap * kvd;
+    float* vc = m->v_cache + li * m->kv_cap * kvd;
+    // 2. RoPE of q and k, K/V cache rows pos0 .. pos0 + nt - 1: in the split-K
+    // reduce when Q, K and V are one launch (one weight type), else a launch
+    // of its own
+    const MmRope rope{m->rope, (uint32_t)pos0, (uint32_t)c.head_count, (uint32_t)c.head_count_kv, (uint32_t)hd,
+                      m->p_qr, kc, vc};
+    const bool fused = L.q.type == L.k.type && L.k.type == L.v.type && hd % 8 == 0;
     for (int i = 0; i < 3;) {
       MmSegDesc segs[3];
       int n = 0;
@@ -1836,14 +1844,12 @@ int32_t enqueue_prefill_layer(rf_model* m, size_t li, uint64_t pos0, uint64_t nt
         segs[n++] = MmSegDesc{qkv[i]->d, qkv[i]->ne1, 0, rows[i], outs[i], nullptr, b, rows[i]};
         ++i;
       }
-      RF_LAUNCH(mm(segs, n, t, m->p_xn, d, EPI_STORE), "prefill qkv");
+      RF_LAUNCH(mm(segs, n, t, m->p_xn, d, EPI_STORE, nullptr, fused ? &rope : nullptr), "prefill qkv");
     }
-    // 2. RoPE of q and k, K/V cache rows pos0 .. pos0 + nt - 1
-    float* kc = m->k_cache + li * m->kv_cap * kvd;
-    float* vc = m->v_cache + li * m->kv_cap * kvd;
-    RF_LAUNCH(launch_rope_kv_rows(m->p_q, m->p_k, m->p_v, m->rope, pos0, nt, (uint32_t)c.head_count,
-                                  (uint32_t)c.head_count_kv, (uint32_t)hd, m->p_qr, kc, vc, st),
-              "prefill rope");
+    if (!fused)
+      RF_LAUNCH(launch_rope_kv_rows(m->p_q, m->p_k, m->p_v, m->rope, pos0, nt, (uint32_t)c.head_count,
+                                    (uint32_t)c.head_count_kv, (uint32_t)hd, m->p_qr, kc, vc, st),
+                "prefill rope");
     // 3. attention of every token over positions 0 .. its own
     AttnArgs a{};
     a.q = m->p_qr; a.k_hist = kc; a.v_hist = vc; a.out = m->p_a; a.ws = m->p_att;

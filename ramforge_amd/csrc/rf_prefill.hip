@@ -670,6 +670,64 @@ __global__ __launch_bounds__(1024) void mm_reduce_norm(MmRedArgs a, const float*
   }
 }
 
+// mm_reduce4 for a Q/K/V launch with its RoPE epilogue (MmRope): item j of
+// token t is either four rotation pairs (i0 .. i0 + 3, i0 + hd/2 .. + 3) of a
+// q or k head, summed in split order with the bias added as mm_reduce4 does,
+// rotated as rope_kv_rows_kernel rotates them and stored into qr or the K
+// cache row, or four v columns stored into the V cache row.  The same bits as
+// the two launches it replaces.
+__global__ __launch_bounds__(256) void mm_reduce_rope(MmRedArgs a, MmRope p) {
+  const uint32_t half = p.hd >> 1, g4 = half / 4u;
+  const uint32_t nrot = (p.qh + p.kvh) * g4, per = nrot + p.kvh * p.hd / 4u;
+  const uint64_t e = (uint64_t)blockIdx.x * 256u + threadIdx.x;
+  if (e >= (uint64_t)a.n * per) return;
+  const uint32_t t = (uint32_t)(e / per), j = (uint32_t)(e % per);
+  const size_t stride = (size_t)a.n * a.mtot / 4;  // float4 units (mtot % 4 == 0)
+  const float* row = a.part + (size_t)t * a.mtot;
+  const uint32_t qd = p.qh * p.hd, kvd = p.kvh * p.hd, pos = p.pos0 + t;
+  if (j >= nrot) {  // four v columns
+    const uint32_t r = 4u * (j - nrot);
+    const float4* pv[1] = {reinterpret_cast<const float4*>(row + a.seg[2].col + r)};
+    float4 v[1];
+    mm_split_sums<1>(pv, stride, a.nsplit, v);
+    float4 o = v[0];
+    if (a.seg[2].bias) {
+      const float4 b = *reinterpret_cast<const float4*>(a.seg[2].bias + r);
+      o = make_float4(v[0].x + b.x, v[0].y + b.y, v[0].z + b.z, v[0].w + b.w);
+    }
+    *reinterpret_cast<float4*>(p.vc + (size_t)pos * kvd + r) = o;
+    return;
+  }
+  const uint32_t hr = j / g4, i0 = 4u * (j % g4);  // head row (q heads, then k heads), first pair
+  const bool isq = hr < p.qh;
+  const uint32_t col = isq ? a.seg[0].col : a.seg[1].col;
+  const float* bias = isq ? a.seg[0].bias : a.seg[1].bias;
+  const uint32_t r0 = (isq ? hr : hr - p.qh) * p.hd + i0;  // row of the segment; its partner r0 + half
+  const float4* pv[2] = {reinterpret_cast<const float4*>(row + col + r0),
+                         reinterpret_cast<const float4*>(row + col + r0 + half)};
+  float4 v[2];
+  mm_split_sums<2>(pv, stride, a.nsplit, v);
+  if (bias) {
+    const float4 b0 = *reinterpret_cast<const float4*>(bias + r0), b1 = *reinterpret_cast<const float4*>(bias + r0 + half);
+    v[0] = make_float4(v[0].x + b0.x, v[0].y + b0.y, v[0].z + b0.z, v[0].w + b0.w);
+    v[1] = make_float4(v[1].x + b1.x, v[1].y + b1.y, v[1].z + b1.z, v[1].w + b1.w);
+  }
+  // cos, sin of pairs i0 .. i0 + 3
+  const float4 ca = *reinterpret_cast<const float4*>(p.rope + (size_t)pos * p.hd + 2u * i0);
+  const float4 cb = *reinterpret_cast<const float4*>(p.rope + (size_t)pos * p.hd + 2u * i0 + 4u);
+  const float x0[4] = {v[0].x, v[0].y, v[0].z, v[0].w}, x1[4] = {v[1].x, v[1].y, v[1].z, v[1].w};
+  const float c[4] = {ca.x, ca.z, cb.x, cb.z}, sn[4] = {ca.y, ca.w, cb.y, cb.w};
+  float lo[4], hi[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    lo[k] = x0[k] * c[k] - x1[k] * sn[k];
+    hi[k] = x0[k] * sn[k] + x1[k] * c[k];
+  }
+  float* dst = isq ? p.qr + (size_t)t * qd + hr * p.hd : p.kc + (size_t)pos * kvd + (hr - p.qh) * p.hd;
+  *reinterpret_cast<float4*>(dst + i0) = make_float4(lo[0], lo[1], lo[2], lo[3]);
+  *reinterpret_cast<float4*>(dst + i0 + half) = make_float4(hi[0], hi[1], hi[2], hi[3]);
+}
+
 static bool mm_reduce_vec4(const MmRedArgs& r) {
   auto al = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
   if (r.mcols % 4 || r.mtot % 4 || !al(r.part)) return false;
@@ -836,8 +894,17 @@ static bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) 
 
 hipError_t launch_matmul_packed(uint32_t t, const MmSegDesc* segs, int nseg, const float* x, uint64_t ldx,
                                 uint64_t n, uint64_t in_dim, int epi, float* part, uint64_t part_floats,
-                                hipStream_t st, const float* norm_w, float eps, float* xn) {
+                                hipStream_t st, const float* norm_w, float eps, float* xn, const MmRope* rope) {
   if (norm_w && (epi != EPI_RESIDUAL || nseg != 1 || !xn)) return hipErrorInvalidValue;
+  if (rope) {  // q, k, v segments of one launch, 16-byte rows and tables
+    const uint64_t hd = rope->hd;
+    const uintptr_t al = reinterpret_cast<uintptr_t>(rope->rope) | reinterpret_cast<uintptr_t>(rope->qr) |
+                         reinterpret_cast<uintptr_t>(rope->kc) | reinterpret_cast<uintptr_t>(rope->vc);
+    if (epi != EPI_STORE || norm_w || nseg != 3 || hd == 0 || hd % 8 != 0 || (al & 15u) != 0 ||
+        segs[0].rows != (uint64_t)rope->qh * hd || segs[1].rows != (uint64_t)rope->kvh * hd ||
+        segs[2].rows != (uint64_t)rope->kvh * hd)
+      return hipErrorInvalidValue;
+  }
   if (!mm_supported(t, in_dim) || nseg < 1 || nseg > 3 || n == 0 || n > MM_MAX_TOKENS) return hipErrorInvalidValue;
   if (!al16(x) || ldx % 4 != 0 || ldx < in_dim || !part) return hipErrorInvalidValue;
   if (epi == EPI_SWIGLU && (nseg != 2 || segs[0].rows != segs[1].rows)) return hipErrorInvalidValue;
@@ -892,6 +959,14 @@ hipError_t launch_matmul_packed(uint32_t t, const MmSegDesc* segs, int nseg, con
   a.spp = spp;
   const dim3 grid((uint32_t)groups, nsplit);
   const int ntt = mm_ntt(n);
+  r.nseg = (uint32_t)nseg;
+  r.nsplit = nsplit;
+  r.n = (uint32_t)n;
+  r.mtot = (uint32_t)mtot;
+  r.mcols = epi == EPI_SWIGLU ? (uint32_t)segs[0].rows : (uint32_t)mtot;
+  r.epi = epi;
+  r.part = part;
+  if (rope && !mm_reduce_vec4(r)) return hipErrorInvalidValue;  // before any launch
   hipError_t e;
   switch (t) {
     case T_Q8_0: e = mm_launch_shape<T_Q8_0>(a, grid, ntt, wide, sc8, st); break;
@@ -900,18 +975,16 @@ hipError_t launch_matmul_packed(uint32_t t, const MmSegDesc* segs, int nseg, con
     default: e = mm_launch_shape<T_Q6_K>(a, grid, ntt, wide, false, st); break;
   }
   if (e != hipSuccess) return e;
-  r.nseg = (uint32_t)nseg;
-  r.nsplit = nsplit;
-  r.n = (uint32_t)n;
-  r.mtot = (uint32_t)mtot;
-  r.mcols = epi == EPI_SWIGLU ? (uint32_t)segs[0].rows : (uint32_t)mtot;
-  r.epi = epi;
-  r.part = part;
   const uint64_t total = (uint64_t)n * r.mcols;
   const bool al = ((reinterpret_cast<uintptr_t>(norm_w) | reinterpret_cast<uintptr_t>(xn)) & 15u) == 0;
   if (norm_w && al && mm_reduce_vec4(r) && r.mcols <= 8192) {
     if (r.mcols <= 4096) RF_KLAUNCH(mm_reduce_norm<1>, dim3((uint32_t)n), dim3(1024), 0, st, r, norm_w, eps, xn);
     else RF_KLAUNCH(mm_reduce_norm<2>, dim3((uint32_t)n), dim3(1024), 0, st, r, norm_w, eps, xn);
+    return hipGetLastError();
+  }
+  if (rope) {
+    const uint64_t items = n * ((uint64_t)(rope->qh + rope->kvh) * rope->hd / 8 + (uint64_t)rope->kvh * rope->hd / 4);
+    RF_KLAUNCH(mm_reduce_rope, dim3((uint32_t)((items + 255) / 256)), dim3(256), 0, st, r, *rope);
     return hipGetLastError();
   }
   if (mm_reduce_vec4(r))
