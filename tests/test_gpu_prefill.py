@@ -116,7 +116,7 @@ ALL_KQ = dict(embd=Q4_K, out=Q6_K, q=Q4_K, k=Q4_K, v=Q6_K, o=Q4_K, gate=Q4_K, up
 
 @pytest.mark.parametrize("kind,history,plen", [("q8", 0, 1), ("q8", 0, 37), ("q8", 3, 64), ("q8", 0, 150),
                                                ("q4", 0, 70), ("mixed", 0, 40), ("kq", 2, 90), ("kq_bias", 0, 20),
-                                               ("q8_attn0", 3, 150), ("kq_attn0", 0, 90)])
+                                               ("q8_bias", 2, 90), ("q8_attn0", 3, 150), ("kq_attn0", 0, 90)])
 def test_prefill_matches_token_by_token(ctx, orc, kind, history, plen):
     """Prompt of plen tokens after `history` single-token forwards: hidden
     state and logits of the last token against the oracle, then greedy
@@ -124,7 +124,9 @@ def test_prefill_matches_token_by_token(ctx, orc, kind, history, plen):
     tokens at history 3 crosses the 64-position attention regime inside a
     chunk.  The matrix-core prefill attention runs every chunk (these
     contexts are below its default threshold); *_attn0: the decode split
-    kernel with a token dimension instead."""
+    kernel with a token dimension instead.  Q, K and V of one weight type
+    take RoPE and the K/V rows in their split-K reduce (q8, q4, q8_bias with
+    Q/K/V biases); mixed types (kq, kq_bias) a launch of its own."""
     import ramforge_amd as rf
 
     old_attn = rf.tune_prefill_attention(0 if kind.endswith("_attn0") else 2)
@@ -136,10 +138,10 @@ def test_prefill_matches_token_by_token(ctx, orc, kind, history, plen):
 
 
 def _prefill_case(ctx, orc, kind, history, plen):
-    types = {"q8": ALL_Q8, "q4": ALL_Q4, "mixed": MIXED, "kq": ALL_KQ, "kq_bias": ALL_KQ}[kind]
-    cfg = dict(PF_CFG) if kind in ("q8", "q4") else dict(KQ_CFG)
+    types = {"q8": ALL_Q8, "q4": ALL_Q4, "mixed": MIXED, "kq": ALL_KQ, "kq_bias": ALL_KQ, "q8_bias": ALL_Q8}[kind]
+    cfg = dict(PF_CFG) if kind in ("q8", "q4", "q8_bias") else dict(KQ_CFG)
     rng = np.random.default_rng(3300 + plen + history)
-    T = _tiny_tensors(rng, cfg, types, bias=kind == "kq_bias")
+    T = _tiny_tensors(rng, cfg, types, bias=kind.endswith("_bias"))
     cap = history + plen + 24
     gm = _load_gpu(ctx, cfg, T, cap)
     om = orc.Model(cfg, T, kv_capacity=cap, threads=8)
