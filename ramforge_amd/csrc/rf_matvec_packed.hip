@@ -1205,10 +1205,10 @@ static hipError_t launch_pk_all_nb(const PkArgs& a, uint32_t lds, uint64_t grid,
 // workgroups 8.73 against 8.44 us for the ring's 3 rows in 256; with 1.5
 // rows per wavefront 8.33 against 8.21; the 14336-wide down projection 15.5
 // against 13.7 us, its x staged in twice as many workgroups, so neither
-// takes this shape; nor do rows of 2048 inputs, Q8_0 rows of two chunks (the
-// d-2048 model's Q/K/V and o-proj: 4.19 / 3.51 against 4.18 / 3.52 us), or of
-// 8192, eight chunks (its down projection: 6.3 against 5.9 us)).  *done
-// stays false otherwise.
+// takes this shape; nor do Q8_0 rows of 2048 inputs, two chunks (the d-2048
+// model's Q/K/V 4.19 / 4.25 against 4.07 / 4.08 us, decode 2,175 against
+// 2,181 tok/s), or of 8192, eight chunks (its down projection: 6.3 against
+// 5.9 us)).  *done stays false otherwise.
 template <uint32_t T, int EPI, bool NORM, int LPW>
 static hipError_t launch_pk_all(const PkArgs& a, uint32_t lds, hipStream_t st, bool* done) {
   *done = false;
