@@ -1132,11 +1132,13 @@ static uint64_t pk_digit_lds(uint32_t t, uint64_t in_dim) {
 // 9.3 us (Q8_0), 6.3 vs 7.1 us (Q4_0); Q4_0 gate/up 15.8 vs 16.8 us; the
 // other shapes within 0.2 us.
 // Workgroups: whole rounds of one per CU, enough for about `per` tasks per
-// wavefront, at most the kernel's occupancy.  Gate/up launches and rows of up
-// to 2048 inputs aim at 2 (8B gate/up: 768 workgroups, its occupancy, instead
-// of 512, 21.5 against 21.9 us back to back, decode 545 against 540 tok/s;
-// the d-2048 model's gate/up 8.57 against 8.69 us); the 8B's other launches
-// keep 4 (with 2: Q/K/V 7.75 against 7.30 us).
+// wavefront, at most the kernel's occupancy.  Q8_0 gate/up launches and rows
+// of up to 2048 inputs aim at 2 (8B gate/up: 768 workgroups, its occupancy,
+// instead of 512, 21.5 against 21.9 us back to back, decode 545 against 540
+// tok/s; the d-2048 model's gate/up 8.57 against 8.69 us); the 8B's other
+// launches keep 4 (with 2: Q/K/V 7.75 against 7.30 us), and so do the other
+// formats' gate/up (with 2: Q4_K 17.26 / Q4_0 16.15 against 17.30 / 16.17 us,
+// Q6_K 20.72 against 20.61).
 static uint64_t pk_grid(uint64_t tasks, uint64_t nw, int occ, int epi, uint64_t per = 4) {
   const uint64_t cus = (uint64_t)pk_cu_count();
   const uint64_t want = (tasks + nw - 1) / nw;
@@ -1160,7 +1162,7 @@ static hipError_t launch_pk(const PkArgs& a, uint32_t lds, hipStream_t st) {
   if (occ < 0) return hipErrorStreamCaptureUnsupported;
   if (occ < 1) return hipErrorInvalidConfiguration;
   const uint64_t tasks = (a.rows_total + U - 1) / U, nw = NT / 64;
-  uint64_t grid = pk_grid(tasks, nw, occ, EPI, (EPI == EPI_SWIGLU || a.in_dim <= 2048) ? 2 : 4);
+  uint64_t grid = pk_grid(tasks, nw, occ, EPI, ((EPI == EPI_SWIGLU && T == T_Q8_0) || a.in_dim <= 2048) ? 2 : 4);
   // Q8_0 / Q4_0 take the int8 digit planes of x when a wavefront's rows hold
   // at least 24 KiB of codes: their split costs each workgroup a longer
   // prologue, which the cheaper decode repays only over that many bytes
