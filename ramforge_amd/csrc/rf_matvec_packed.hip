@@ -1235,7 +1235,7 @@ static hipError_t launch_pk_all(const PkArgs& a, uint32_t lds, hipStream_t st, b
 }
 
 // The single-step launch above with x merged from attention chunk records
-// (matvec_packed<..., MRG>): Q8_0 rows of 2 or 4 chunks, Q4_0 / Q4_K rows of 1 or 2,
+// (matvec_packed<..., MRG>): Q8_0 rows of 2 or 4 chunks, Q4_0 / Q4_K / Q6_K rows of 1 or 2,
 // with the MRG kernel's own occupancy and LDS (x, its unit sums, then the
 // records' factors and the heads' 1 / L).
 // hipErrorNotSupported when the shape does not take it;
@@ -1247,7 +1247,7 @@ static bool pk_merge_shape(uint32_t t, uint64_t in_dim, uint32_t nsplit, uint32_
     if (g_digits == 2) return false;  // digit planes everywhere: no float-x launch
   }
   const uint64_t nchunk = pk_nchunk(t, in_dim);
-  if (!((t == T_Q8_0 && (nchunk == 2 || nchunk == 4)) || ((t == T_Q4_0 || t == T_Q4_K) && nchunk <= 2)))
+  if (!((t == T_Q8_0 && (nchunk == 2 || nchunk == 4)) || ((t == T_Q4_0 || t == T_Q4_K || t == T_Q6_K) && nchunk <= 2)))
     return false;
   if (hd < 16 || (hd & (hd - 1)) != 0 || (uint64_t)qh * hd != in_dim) return false;
   if (nsplit < 1 || nsplit > 8 || qh > 64) return false;  // 8 lanes per head's chunk records
@@ -1274,7 +1274,8 @@ static hipError_t launch_pk_merge(const PkArgs& a, uint32_t lds, bool launch, hi
 }
 
 // LPW = the row's chunks (one step per row): Q8_0 rows of 2048 or 4096
-// inputs, Q4_0 / Q4_K rows of up to 4096.
+// inputs, Q4_0 / Q4_K / Q6_K rows of up to 4096 (Q6_K: 110 VGPRs; an
+// all-Q6_K 8B model decodes at 534 against 517 tok/s with the merge kernel).
 static hipError_t launch_pk_merge_t(uint32_t t, const PkArgs& a, uint32_t lds, bool launch, hipStream_t st) {
   const uint64_t nchunk = pk_nchunk(t, a.in_dim);
   switch (t) {
@@ -1284,6 +1285,8 @@ static hipError_t launch_pk_merge_t(uint32_t t, const PkArgs& a, uint32_t lds, b
       return nchunk == 2 ? launch_pk_merge<T_Q4_0, 2>(a, lds, launch, st) : launch_pk_merge<T_Q4_0, 1>(a, lds, launch, st);
     case T_Q4_K:
       return nchunk == 2 ? launch_pk_merge<T_Q4_K, 2>(a, lds, launch, st) : launch_pk_merge<T_Q4_K, 1>(a, lds, launch, st);
+    case T_Q6_K:
+      return nchunk == 2 ? launch_pk_merge<T_Q6_K, 2>(a, lds, launch, st) : launch_pk_merge<T_Q6_K, 1>(a, lds, launch, st);
     default: return hipErrorNotSupported;
   }
 }

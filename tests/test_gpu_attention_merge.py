@@ -5,8 +5,8 @@ o-projection, model_executor.rs:102-236).
 
 The models have 32 query heads of 128 dims (q_heads * head_dim = 4096, as
 the 8B shape), 64 of 64, or 32 of 64 (2048 inputs, as BASELINE config 4:
-Q8_0 rows of two 1024-element chunks, Q4_0 / Q4_K rows of one), so the
-packed Q8_0 / Q4_0 / Q4_K o-projection takes the merged-x launch at every
+Q8_0 rows of two 1024-element chunks, the 4-bit and 6-bit formats' rows of one), so the
+packed Q8_0 / Q4_0 / Q4_K / Q6_K o-projection takes the merged-x launch at every
 context the attention splits per query head (65 to 1024 positions here: 2 to
 8 chunks, or to 4 with 64 heads).  The two modes differ in the merge's
 rounding only: hidden states within 1e-5 of each other, both within 2e-4 of
@@ -15,7 +15,7 @@ graphs, across the launch regimes."""
 import numpy as np
 import pytest
 
-from helpers import Q4_0, Q4_K, Q8_0
+from helpers import Q4_0, Q4_K, Q6_K, Q8_0
 from test_gpu_model import _load_gpu, _tiny_tensors
 
 pytestmark = pytest.mark.gpu
@@ -43,9 +43,10 @@ def merge_mode():
 
 
 @pytest.mark.timeout(600)
-@pytest.mark.parametrize("o,cfg", [(Q8_0, CFG), (Q4_0, CFG), (Q4_K, CFG), (Q8_0, CFG64), (Q8_0, CFG2K),
-                                   (Q4_0, CFG2K), (Q4_K, CFG2K)],
-                         ids=["q8_0", "q4_0", "q4_k", "q8_0-hd64", "q8_0-2048", "q4_0-2048", "q4_k-2048"])
+@pytest.mark.parametrize("o,cfg", [(Q8_0, CFG), (Q4_0, CFG), (Q4_K, CFG), (Q6_K, CFG), (Q8_0, CFG64),
+                                   (Q8_0, CFG2K), (Q4_0, CFG2K), (Q4_K, CFG2K), (Q6_K, CFG2K)],
+                         ids=["q8_0", "q4_0", "q4_k", "q6_k", "q8_0-hd64", "q8_0-2048", "q4_0-2048", "q4_k-2048",
+                              "q6_k-2048"])
 def test_merged_oproj_matches_merge_kernel(ctx, orc, merge_mode, o, cfg):
     T = _tiny_tensors(np.random.default_rng(2400 + o), cfg, _types(o))
     import ramforge_amd as rf
